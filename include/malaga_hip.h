@@ -1,0 +1,177 @@
+/*
+ * malaga_hip.h -- C ABI of libmalaga_hip.so, the MI355X (gfx950) backend for
+ * malaga's NLLB/M2M100 GGUF decode path.
+ *
+ * Plain C types only (no torch, no HIP types): a Rust FFI crate, ctypes or any
+ * C caller binds it directly.  Each entry point cites the reference interface it
+ * replaces (paths relative to rzafiamy/malaga, crates/malaga-core/).
+ *
+ * Conventions
+ *   - Every int-returning function returns MLG_OK (0) or an MLG_ERR_* status;
+ *     mlg_last_error() then holds a thread-local message.  Out-of-memory
+ *     messages contain "OUT_OF_MEMORY", the substring the reference's retry
+ *     logic matches (src/graph.rs:215, src/translator.rs:338-340).
+ *   - Host buffers are caller-owned; the library copies in and out.  All device
+ *     memory of contexts, models, batches and graph states is library-owned.
+ *   - A context (and the models loaded on it) is used by one thread at a time;
+ *     calls take the context's mutex (src/graph.rs:152-155).
+ *   - Kernel-level entry points take device pointers and a hipStream_t passed
+ *     as void* (NULL = the context-independent default stream).
+ */
+#ifndef MALAGA_HIP_H
+#define MALAGA_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum {
+    MLG_OK = 0,
+    MLG_ERR_INVALID = 1,
+    MLG_ERR_OOM = 2,
+    MLG_ERR_HIP = 3,
+    MLG_ERR_IO = 4,
+    MLG_ERR_FORMAT = 5,
+    MLG_ERR_UNSUPPORTED = 6,
+    MLG_ERR_NO_DEVICE = 7
+};
+
+/* ggml type ids (GGUF spec) accepted by the codecs and kernels */
+enum { MLG_F32 = 0, MLG_F16 = 1, MLG_Q8_0 = 8, MLG_Q4_K = 12, MLG_Q5_K = 13, MLG_Q6_K = 14, MLG_BF16 = 30 };
+
+/* src/convert.rs:151-212 presets */
+enum { MLG_PRESET_F32 = 0, MLG_PRESET_F16, MLG_PRESET_Q8_0, MLG_PRESET_Q6K, MLG_PRESET_Q5KM, MLG_PRESET_Q4KM };
+
+/* synthetic checkpoints (tests / benchmarks) */
+enum { MLG_INIT_TESTUTIL = 0, MLG_INIT_NORMAL = 1, MLG_INIT_NORMAL_RICH = 2 };
+
+/* generation flags */
+enum {
+    MLG_FLAG_EOS_MASK = 1, /* benchmark-only: EOS logit = -inf, fixed output lengths (no reference counterpart) */
+    MLG_FLAG_NO_GRAPH = 2  /* run the static step eagerly (MALAGA_NO_HIP_GRAPH for one call) */
+};
+
+typedef struct mlg_ctx mlg_ctx;
+typedef struct mlg_model mlg_model;
+typedef struct mlg_batch mlg_batch;
+typedef struct mlg_matrix mlg_matrix;
+
+/* Hyper-parameters: src/config.rs:14-39 (field for field). */
+typedef struct {
+    int vocab_size, d_model, encoder_layers, decoder_layers, encoder_heads, decoder_heads;
+    int encoder_ffn, decoder_ffn, max_position_embeddings, max_length, scale_embedding;
+    int bos_token_id, pad_token_id, eos_token_id, decoder_start_token_id;
+} mlg_config;
+
+/* src/translator.rs:15-53 GenOptions (shortlist is not offered by this backend). */
+typedef struct {
+    int beam_size;        /* 1 = greedy */
+    int max_new_tokens;   /* 0 = None: 2 * src_len + 16, capped by max_length */
+    float length_penalty;
+    int sync_every;
+    int max_batch;
+    int fused;            /* 1 = static step replayed as a hipGraph; 0 = same step, eager */
+    uint32_t flags;       /* MLG_FLAG_* */
+} mlg_gen_options;
+
+const char *mlg_last_error(void);
+const char *mlg_version(void);
+
+/* ---- block codecs (candle-core 0.11 QTensor quantize/dequantize, src/convert.rs:249-256) ---- */
+int mlg_type_info(uint32_t type, int *block_elems, int *block_bytes);
+int64_t mlg_type_bytes(uint32_t type, int64_t n);
+int mlg_quantize(uint32_t type, const float *x, int64_t n, void *out);
+int mlg_dequantize(uint32_t type, const void *in, int64_t n, float *out);
+
+/* ---- conversion (src/convert.rs:317-440) ---- */
+int mlg_preset_from_name(const char *name, int *preset);
+/* Supplies the f32 data of a Hugging Face tensor; return 0 on success. */
+typedef int (*mlg_tensor_fn)(void *user, const char *hf_name, int64_t numel, float *out);
+int mlg_convert(const char *out_path, const mlg_config *cfg, int preset, const char *model_name,
+                const char *tokenizer_json, mlg_tensor_fn fn, void *user);
+/* Synthetic checkpoint converted like mlg_convert (MLG_INIT_TESTUTIL restates src/testutil.rs:16-101). */
+int mlg_write_synthetic(const char *out_path, const mlg_config *cfg, int preset, int init, uint64_t seed,
+                        float std_dev, const char *model_name);
+/* The tiny test model of src/testutil.rs:18-30. */
+void mlg_tiny_config(mlg_config *out);
+
+/* ---- device context and model (src/translator.rs:62-73, src/model.rs:343-433) ---- */
+int mlg_device_count(int *n);
+int mlg_ctx_create(int device, mlg_ctx **out);
+void mlg_ctx_destroy(mlg_ctx *ctx);
+int mlg_model_load(mlg_ctx *ctx, const char *gguf_path, mlg_model **out);
+void mlg_model_free(mlg_model *m);
+int mlg_model_config(const mlg_model *m, mlg_config *out);
+int64_t mlg_model_weight_bytes(const mlg_model *m);
+
+/* ---- translation on token ids ---- */
+void mlg_gen_options_default(mlg_gen_options *o);
+/* Translator::translate_batch (src/translator.rs:136-167) + generate_to (175-207) on
+ * already-tokenized sources: n rows, row i = ids[off_i .. off_i + lens[i]).  out is
+ * [n][out_cap]; out_len[i] receives the length of row i (without specials). */
+int mlg_generate(mlg_model *m, const uint32_t *ids, const uint32_t *lens, int n, uint32_t tgt_lang,
+                 const mlg_gen_options *o, uint32_t *out, int out_cap, int *out_len);
+
+/* GraphCache boundary (src/graph.rs:182-223): encode once, then decode. */
+/* Nllb::encode_cross (src/model.rs:463-477). */
+int mlg_encode(mlg_model *m, const uint32_t *ids, const uint32_t *lens, int n, mlg_batch **out);
+void mlg_batch_free(mlg_batch *b);
+/* GraphCache::greedy (src/graph.rs:204-223); rows stripped at EOS. */
+int mlg_greedy(mlg_model *m, const mlg_batch *b, uint32_t tgt_lang, int max_new, int sync_every, uint32_t flags,
+               uint32_t *out, int out_cap, int *out_len);
+/* Translator::beam_search (src/translator.rs:250-335). */
+int mlg_beam(mlg_model *m, const mlg_batch *b, uint32_t tgt_lang, int max_new, int beam_size, float length_penalty,
+             uint32_t flags, uint32_t *out, int out_cap, int *out_len);
+/* GraphCache::clear (src/graph.rs:192-200). */
+void mlg_clear_graphs(mlg_model *m);
+int mlg_graph_stats(const mlg_model *m, int *entries, int *graphs, int *capture_enabled);
+/* Test hook: the n-th following device allocation fails with MLG_ERR_OOM (n < 0: off). */
+void mlg_debug_fail_alloc_after(long n);
+
+/* ---- kernel-level entry points (microbenchmarks and tests; device pointers) ---- */
+/* A GGUF matrix [N][K] of `type` (raw GGUF row bytes from the host) uploaded in the device layout. */
+int mlg_matrix_upload(mlg_ctx *ctx, uint32_t type, int N, int K, const void *gguf_rows, mlg_matrix **out);
+void mlg_matrix_free(mlg_matrix *w);
+int64_t mlg_matrix_bytes(const mlg_matrix *w);
+/* QMatMul::forward (src/model.rs:571-607): y[b][N] = x[b][K] W^T (+ bias) (relu). */
+int mlg_gemv(const mlg_matrix *w, const float *x, int b, float *y, const float *bias, int relu, void *stream);
+int mlg_gemv_max_batch(const mlg_matrix *w);
+int mlg_gemm(const mlg_matrix *w, const float *x, int M, float *y, const float *bias, int relu, void *stream);
+/* LM head + first argmax pass (kernels/malaga.cu:247-280 fused into the GEMV). */
+int mlg_gemv_argmax_parts(const mlg_matrix *w, int b);
+int mlg_gemv_argmax(const mlg_matrix *w, const float *x, int b, int mask_id, float *pv, uint32_t *pi, void *stream);
+/* bias_residual_ln (kernels/malaga.cu:89-105) with the bias already in y. */
+int mlg_residual_ln(float *x, const float *y, int rows, int d, const float *gamma, const float *beta, float eps,
+                    float *ln_out, void *stream);
+int mlg_layernorm(const float *x, int rows, int d, const float *gamma, const float *beta, float eps, float *out,
+                  void *stream);
+/* attn_decode (kernels/malaga.cu:165-227). K, V: f16 [b][H][L][hd]. */
+int mlg_attn_decode(const float *q, const void *K, const void *V, int b, int H, int hd, int L, const uint32_t *lens,
+                    const uint32_t *step, float *out, void *stream);
+/* argmax_partial (kernels/malaga.cu:247-280): pv/pi [b][parts]. */
+int mlg_argmax_partial(const float *logits, int b, int V, int mask_id, float *pv, uint32_t *pi, int parts,
+                       void *stream);
+/* greedy_finalize (kernels/malaga.cu:290-326). */
+int mlg_greedy_finalize(const float *pv, const uint32_t *pi, int parts, int b, uint8_t *finished, uint32_t *ids,
+                        uint32_t *out, int m, uint32_t *step, uint32_t eos, uint32_t pad, void *stream);
+/* log_softmax + topk (src/translator.rs:272, 343-358); scratch of mlg_logsoftmax_topk_scratch bytes. */
+size_t mlg_logsoftmax_topk_scratch(int rows, int k);
+int mlg_logsoftmax_topk(const float *logits, int rows, int V, int k, int mask_id, void *scratch, float *vals,
+                        uint32_t *idx, void *stream);
+/* Logits after feeding tgt[i][t] at decoder position t (t < T), eagerly: out is [n][T][vocab].
+ * Parity hook for Nllb::decode (src/model.rs:514-540); no counterpart in the reference. */
+int mlg_teacher_forced_logits(mlg_model *m, const uint32_t *ids, const uint32_t *lens, int n, const uint32_t *tgt, int T,
+                              float *logits);
+/* src/graph.rs:138-140 */
+int mlg_bucket(int n, int min, int max);
+/* per-sentence output budget, src/translator.rs:181-182 */
+int mlg_budget(const mlg_model *m, int len, int max_new_tokens);
+int mlg_synchronize(void);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,569 @@
+// Row-wise and attention kernels of the decoder step and the encoder:
+// LayerNorm (+ residual, + embedding/positions), q/k/v split into the f16 KV
+// cache, single-query and prefill attention, argmax + greedy bookkeeping,
+// log-softmax top-k for beam search, and small copy/gather helpers.
+#include "dequant.hpp"
+#include "kernels.hpp"
+
+namespace mlg {
+
+namespace {
+
+constexpr int kLnThreads = 256;
+constexpr int kLnMaxPerThread = 16;  // d <= 4096
+
+// LayerNorm of v[] (thread's elements i = tid + k * 256) with biased variance,
+// two passes in registers (kernels/malaga.cu:66-86 semantics).
+__device__ __forceinline__ void ln_rows(const float (&v)[kLnMaxPerThread], int d, const float *g, const float *b,
+                                        float eps, float *out, float *sh) {
+    float s = 0.f;
+#pragma unroll
+    for (int k = 0; k < kLnMaxPerThread; ++k) s += v[k];
+    const float mean = block_sum(s, sh) / float(d);
+    float s2 = 0.f;
+#pragma unroll
+    for (int k = 0; k < kLnMaxPerThread; ++k) {
+        const int i = threadIdx.x + k * kLnThreads;
+        const float c = i < d ? v[k] - mean : 0.f;
+        s2 += c * c;
+    }
+    __syncthreads();  // sh is reused
+    const float rstd = rsqrtf(block_sum(s2, sh) / float(d) + eps);
+#pragma unroll
+    for (int k = 0; k < kLnMaxPerThread; ++k) {
+        const int i = threadIdx.x + k * kLnThreads;
+        if (i < d) out[i] = (v[k] - mean) * rstd * g[i] + b[i];
+    }
+}
+
+__global__ __launch_bounds__(kLnThreads) void k_layernorm(const float *x, int d, const float *g, const float *b,
+                                                          float eps, float *out) {
+    __shared__ float sh[16];
+    const size_t off = size_t(blockIdx.x) * d;
+    float v[kLnMaxPerThread];
+#pragma unroll
+    for (int k = 0; k < kLnMaxPerThread; ++k) {
+        const int i = threadIdx.x + k * kLnThreads;
+        v[k] = i < d ? x[off + i] : 0.f;
+    }
+    ln_rows(v, d, g, b, eps, out + off, sh);
+}
+
+__global__ __launch_bounds__(kLnThreads) void k_residual_ln(float *x, const float *y, int d, const float *g,
+                                                            const float *b, float eps, float *h) {
+    __shared__ float sh[16];
+    const size_t off = size_t(blockIdx.x) * d;
+    float v[kLnMaxPerThread];
+#pragma unroll
+    for (int k = 0; k < kLnMaxPerThread; ++k) {
+        const int i = threadIdx.x + k * kLnThreads;
+        v[k] = 0.f;
+        if (i < d) {
+            v[k] = x[off + i] + y[off + i];
+            x[off + i] = v[k];
+        }
+    }
+    ln_rows(v, d, g, b, eps, h + off, sh);
+}
+
+// Dequantizes embedding row `tok` into LDS e[0..d)
+template <int T>
+__device__ __forceinline__ void embed_row(const uint8_t *q, const uint8_t *s, const uint8_t *dp, int d, uint32_t tok,
+                                          float *e) {
+    for (int k0 = threadIdx.x * 16; k0 < d; k0 += blockDim.x * 16) {
+        float w[16];
+        dequant16<T>(q, s, dp, d, int(tok), k0, w);
+#pragma unroll
+        for (int i = 0; i < 16; ++i) e[k0 + i] = w[i];
+    }
+    __syncthreads();
+}
+
+template <int T>
+__global__ __launch_bounds__(kLnThreads) void k_embed_pos_ln(const uint8_t *q, const uint8_t *s, const uint8_t *dp,
+                                                             const uint32_t *ids, const float *pos,
+                                                             const uint32_t *step, uint32_t base, float scale, int d,
+                                                             const float *g, const float *b, float eps, float *x,
+                                                             float *h) {
+    extern __shared__ float e[];
+    __shared__ float sh[16];
+    const int row = blockIdx.x;
+    embed_row<T>(q, s, dp, d, ids[row], e);
+    const float *pr = pos + size_t(*step + base) * d;
+    const size_t off = size_t(row) * d;
+    float v[kLnMaxPerThread];
+#pragma unroll
+    for (int k = 0; k < kLnMaxPerThread; ++k) {
+        const int i = threadIdx.x + k * kLnThreads;
+        v[k] = 0.f;
+        if (i < d) {
+            v[k] = e[i] * scale + pr[i];
+            x[off + i] = v[k];
+        }
+    }
+    ln_rows(v, d, g, b, eps, h + off, sh);
+}
+
+template <int T>
+__global__ __launch_bounds__(kLnThreads) void k_embed_pos_rows(const uint8_t *q, const uint8_t *s, const uint8_t *dp,
+                                                               const uint32_t *ids, const uint32_t *pidx,
+                                                               const float *pos, float scale, int d, float *x) {
+    extern __shared__ float e[];
+    const int row = blockIdx.x;
+    embed_row<T>(q, s, dp, d, ids[row], e);
+    const float *pr = pos + size_t(pidx[row]) * d;
+    for (int i = threadIdx.x; i < d; i += blockDim.x) x[size_t(row) * d + i] = e[i] * scale + pr[i];
+}
+
+__global__ void k_qkv_split(const float *qkv, int H, int hd, int m, const uint32_t *step, float *q, __half *kc,
+                            __half *vc) {
+    const int bh = blockIdx.x, bi = bh / H, hh = bh % H, d = H * hd;
+    const float *r = qkv + size_t(bi) * 3 * d;
+    const size_t slot = (size_t(bh) * m + *step) * hd;
+    for (int t = threadIdx.x; t < hd; t += blockDim.x) {
+        const int c = hh * hd + t;
+        q[size_t(bh) * hd + t] = r[c];
+        kc[slot + t] = __float2half(r[d + c]);
+        vc[slot + t] = __float2half(r[2 * d + c]);
+    }
+}
+
+// One workgroup per (row, head).  Thread j scores key j (16-byte f16 loads), block
+// max / exp / sum, then hd-wide thread groups split the keys for P.V.
+__global__ __launch_bounds__(256) void k_attn_decode(const float *q, const __half *K, const __half *V, int H, int hd,
+                                                     int L, const uint32_t *lens, const uint32_t *step, float *out) {
+    extern __shared__ float sm[];
+    __shared__ float red[16];
+    const int bh = blockIdx.x, bi = bh / H, hh = bh % H;
+    const int n = lens ? int(lens[bi]) : int(*step) + 1;
+    const int groups = max(1, int(blockDim.x) / hd);
+    float *qs = sm, *sc = sm + hd, *part = sc + L;
+    for (int t = threadIdx.x; t < hd; t += blockDim.x) qs[t] = q[size_t(bh) * hd + t];
+    __syncthreads();
+    const __half *Kb = K + size_t(bh) * L * hd, *Vb = V + size_t(bh) * L * hd;
+    float mx = -INFINITY;
+    for (int j = threadIdx.x; j < n; j += blockDim.x) {
+        const uint4 *k8 = reinterpret_cast<const uint4 *>(Kb + size_t(j) * hd);
+        float acc = 0.f;
+        for (int t = 0; t < hd / 8; ++t) {
+            const uint4 raw = k8[t];
+            const uint32_t w[4] = {raw.x, raw.y, raw.z, raw.w};
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                acc = fmaf(h2f(w[u]), qs[8 * t + 2 * u], acc);
+                acc = fmaf(h2f(w[u] >> 16), qs[8 * t + 2 * u + 1], acc);
+            }
+        }
+        sc[j] = acc;
+        mx = fmaxf(mx, acc);
+    }
+    mx = block_max(mx, red);
+    float sum = 0.f;
+    for (int j = threadIdx.x; j < n; j += blockDim.x) {
+        const float e = expf(sc[j] - mx);
+        sc[j] = e;
+        sum += e;
+    }
+    __syncthreads();
+    sum = block_sum(sum, red);
+    const float inv = 1.f / sum;
+    const int g = threadIdx.x / hd, t = threadIdx.x % hd;
+    if (g < groups) {
+        float a = 0.f;
+        for (int j = g; j < n; j += groups) a = fmaf(sc[j], __half2float(Vb[size_t(j) * hd + t]), a);
+        part[g * hd + t] = a;
+    }
+    __syncthreads();
+    for (int c = threadIdx.x; c < hd; c += blockDim.x) {
+        float o = 0.f;
+        for (int k = 0; k < groups; ++k) o += part[k * hd + c];
+        out[size_t(bi) * H * hd + hh * hd + c] = o * inv;
+    }
+}
+
+// Encoder attention: one wave per (sentence i, query t, head h).
+__global__ __launch_bounds__(64) void k_attn_prefill(const float *qkv, int s, int H, int hd, const uint32_t *lens,
+                                                     float *out) {
+    extern __shared__ float sc[];
+    const int id = blockIdx.x, hh = id % H, t = (id / H) % s, i = id / (H * s);
+    const int d = H * hd, n = int(lens[i]);
+    const float *qr = qkv + (size_t(i) * s + t) * 3 * d + hh * hd;
+    float mx = -INFINITY;
+    for (int j = threadIdx.x; j < n; j += 64) {
+        const float *kr = qkv + (size_t(i) * s + j) * 3 * d + d + hh * hd;
+        float acc = 0.f;
+        for (int e = 0; e < hd; e += 4) {
+            const float4 a = *reinterpret_cast<const float4 *>(qr + e), b = *reinterpret_cast<const float4 *>(kr + e);
+            acc = fmaf(a.x, b.x, acc);
+            acc = fmaf(a.y, b.y, acc);
+            acc = fmaf(a.z, b.z, acc);
+            acc = fmaf(a.w, b.w, acc);
+        }
+        sc[j] = acc;
+        mx = fmaxf(mx, acc);
+    }
+    mx = wave_max(mx);
+    float sum = 0.f;
+    for (int j = threadIdx.x; j < n; j += 64) {
+        const float e = expf(sc[j] - mx);
+        sc[j] = e;
+        sum += e;
+    }
+    sum = wave_sum(sum);
+    __syncthreads();
+    const float inv = 1.f / sum;
+    for (int e = threadIdx.x; e < hd; e += 64) {
+        float a = 0.f;
+        for (int j = 0; j < n; ++j) a = fmaf(sc[j], qkv[(size_t(i) * s + j) * 3 * d + 2 * d + hh * hd + e], a);
+        out[(size_t(i) * s + t) * d + hh * hd + e] = a * inv;
+    }
+}
+
+__global__ void k_split_cross_kv(const float *kv, int b, int s, int H, int hd, __half *K, __half *V) {
+    const int d = H * hd;
+    const size_t total = size_t(b) * s * d;
+    for (size_t idx = blockIdx.x * size_t(blockDim.x) + threadIdx.x; idx < total; idx += size_t(gridDim.x) * blockDim.x) {
+        const int c = int(idx % d);
+        const size_t tok = idx / d;
+        const int j = int(tok % s), i = int(tok / s), hh = c / hd, e = c % hd;
+        const size_t dst = ((size_t(i) * H + hh) * s + j) * hd + e;
+        K[dst] = __float2half(kv[tok * 2 * d + c]);
+        V[dst] = __float2half(kv[tok * 2 * d + d + c]);
+    }
+}
+
+// dst row r (< n_dst) <- src row map[r] (or r when map is null)
+__global__ void k_copy_cross(const __half *src, const uint32_t *map, int n_dst, int H, int s, int hd, __half *dst,
+                             int S) {
+    const size_t per_row = size_t(H) * s * hd, total = size_t(n_dst) * per_row;
+    for (size_t idx = blockIdx.x * size_t(blockDim.x) + threadIdx.x; idx < total; idx += size_t(gridDim.x) * blockDim.x) {
+        const size_t r = idx / per_row, rem = idx % per_row;
+        const int e = int(rem % hd);
+        const size_t hj = rem / hd;
+        const int j = int(hj % s), hh = int(hj / s);
+        const size_t sr = map ? map[r] : r;
+        dst[((r * H + hh) * S + j) * hd + e] = src[sr * per_row + rem];
+    }
+}
+
+__global__ __launch_bounds__(256) void k_argmax_partial(const float *logits, int V, int ldl, int chunk, int mask_id,
+                                                        float *pv, uint32_t *pi) {
+    __shared__ float sv[4];
+    __shared__ uint32_t si[4];
+    const int row = blockIdx.y, p = blockIdx.x, P = gridDim.x;
+    const int start = p * chunk, end = min(start + chunk, V);
+    const float *r = logits + size_t(row) * ldl;
+    float best = -INFINITY;
+    uint32_t bi = 0xffffffffu;
+    for (int i = start + threadIdx.x; i < end; i += blockDim.x)
+        if (i != mask_id) argmax_merge(best, bi, r[i], uint32_t(i));
+    wave_argmax(best, bi);
+    const int w = threadIdx.x >> 6;
+    if ((threadIdx.x & 63) == 0) {
+        sv[w] = best;
+        si[w] = bi;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        best = sv[0];
+        bi = si[0];
+        for (int k = 1; k < 4; ++k) argmax_merge(best, bi, sv[k], si[k]);
+        pv[size_t(row) * P + p] = best;
+        pi[size_t(row) * P + p] = bi;
+    }
+}
+
+// kernels/malaga.cu:290-326 semantics, without the shortlist mapping.
+__global__ __launch_bounds__(256) void k_greedy_finalize(const float *pv, const uint32_t *pi, int P, int b,
+                                                         uint8_t *finished, uint32_t *ids, uint32_t *out, int m,
+                                                         uint32_t *step, uint32_t eos, uint32_t pad) {
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, nw = blockDim.x >> 6;
+    const uint32_t s = *step;
+    for (int row = w; row < b; row += nw) {
+        float best = -INFINITY;
+        uint32_t bi = 0xffffffffu;
+        for (int p = lane; p < P; p += 64) argmax_merge(best, bi, pv[size_t(row) * P + p], pi[size_t(row) * P + p]);
+        wave_argmax(best, bi);
+        if (lane == 0) {
+            uint32_t tok = bi;
+            if (finished[row]) tok = pad;
+            if (tok == eos) finished[row] = 1;
+            ids[row] = tok;
+            out[size_t(row) * m + s] = tok;
+        }
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) *step = s + 1;
+}
+
+// ---- log-softmax + top-k (beam search) ------------------------------------
+constexpr int kTopMax = 8;
+constexpr int kTopParts = 64;
+
+struct TopK {
+    float v[kTopMax];
+    uint32_t i[kTopMax];
+};
+
+__device__ __forceinline__ bool better(float av, uint32_t ai, float bv, uint32_t bi) {
+    return av > bv || (av == bv && ai < bi);
+}
+
+__device__ __forceinline__ void topk_insert(TopK &t, int k, float v, uint32_t i) {
+    if (!better(v, i, t.v[k - 1], t.i[k - 1])) return;
+    int p = k - 1;
+    while (p > 0 && better(v, i, t.v[p - 1], t.i[p - 1])) {
+        t.v[p] = t.v[p - 1];
+        t.i[p] = t.i[p - 1];
+        --p;
+    }
+    t.v[p] = v;
+    t.i[p] = i;
+}
+
+// Pass 1: per (part, row): chunk max M, sum exp(x - M), chunk top-k.
+// scratch layout per (row, part): [M, S, v0..v7, i0..i7] (18 floats)
+__global__ __launch_bounds__(256) void k_lsm_topk_partial(const float *logits, int V, int k, int mask_id,
+                                                          float *scratch) {
+    __shared__ float red[16];
+    __shared__ float lv[256 * kTopMax];
+    __shared__ uint32_t li[256 * kTopMax];
+    const int row = blockIdx.y, p = blockIdx.x, P = gridDim.x;
+    const int chunk = (V + P - 1) / P, start = p * chunk, end = min(start + chunk, V);
+    const float *r = logits + size_t(row) * V;
+    TopK t;
+    for (int j = 0; j < kTopMax; ++j) {
+        t.v[j] = -INFINITY;
+        t.i[j] = 0xffffffffu;
+    }
+    float mx = -INFINITY;
+    for (int i = start + threadIdx.x; i < end; i += blockDim.x) {
+        if (i == mask_id) continue;
+        const float v = r[i];
+        mx = fmaxf(mx, v);
+        topk_insert(t, k, v, uint32_t(i));
+    }
+    mx = block_max(mx, red);
+    float s = 0.f;
+    for (int i = start + threadIdx.x; i < end; i += blockDim.x)
+        if (i != mask_id && mx > -INFINITY) s += expf(r[i] - mx);
+    __syncthreads();
+    s = block_sum(s, red);
+    for (int j = 0; j < k; ++j) {
+        lv[threadIdx.x * kTopMax + j] = t.v[j];
+        li[threadIdx.x * kTopMax + j] = t.i[j];
+    }
+    __syncthreads();
+    for (int stride = 128; stride > 0; stride >>= 1) {
+        if (int(threadIdx.x) < stride) {
+            const int o = threadIdx.x + stride;
+            for (int j = 0; j < k; ++j) topk_insert(t, k, lv[o * kTopMax + j], li[o * kTopMax + j]);
+            for (int j = 0; j < k; ++j) {
+                lv[threadIdx.x * kTopMax + j] = t.v[j];
+                li[threadIdx.x * kTopMax + j] = t.i[j];
+            }
+        }
+        __syncthreads();
+    }
+    if (threadIdx.x == 0) {
+        float *o = scratch + (size_t(row) * P + p) * (2 + 2 * kTopMax);
+        o[0] = mx;
+        o[1] = s;
+        for (int j = 0; j < kTopMax; ++j) {
+            o[2 + j] = j < k ? t.v[j] : -INFINITY;
+            o[2 + kTopMax + j] = __uint_as_float(j < k ? t.i[j] : 0xffffffffu);
+        }
+    }
+}
+
+// Pass 2: one thread per row merges the parts: vals = (x - max) - ln(sum exp(x - max)).
+__global__ void k_lsm_topk_final(const float *scratch, int rows, int P, int k, float *vals, uint32_t *idx) {
+    const int row = blockIdx.x * blockDim.x + threadIdx.x;
+    if (row >= rows) return;
+    const float *base = scratch + size_t(row) * P * (2 + 2 * kTopMax);
+    float M = -INFINITY;
+    for (int p = 0; p < P; ++p) M = fmaxf(M, base[p * (2 + 2 * kTopMax)]);
+    double S = 0.0;
+    TopK t;
+    for (int j = 0; j < kTopMax; ++j) {
+        t.v[j] = -INFINITY;
+        t.i[j] = 0xffffffffu;
+    }
+    for (int p = 0; p < P; ++p) {
+        const float *o = base + p * (2 + 2 * kTopMax);
+        if (o[0] > -INFINITY) S += double(o[1]) * exp(double(o[0]) - double(M));
+        for (int j = 0; j < k; ++j) topk_insert(t, k, o[2 + j], __float_as_uint(o[2 + kTopMax + j]));
+    }
+    const float ls = float(log(S));
+    for (int j = 0; j < k; ++j) {
+        vals[size_t(row) * k + j] = (t.v[j] - M) - ls;
+        idx[size_t(row) * k + j] = t.i[j];
+    }
+}
+
+__global__ void k_gather_rows_u32(const uint32_t *src, uint32_t *dst, const uint32_t *idx, int n, size_t row_words) {
+    const size_t total = size_t(n) * row_words;
+    for (size_t t = blockIdx.x * size_t(blockDim.x) + threadIdx.x; t < total; t += size_t(gridDim.x) * blockDim.x) {
+        const size_t r = t / row_words, c = t % row_words;
+        dst[t] = src[size_t(idx[r]) * row_words + c];
+    }
+}
+
+__global__ void k_gather_rows_u8(const uint8_t *src, uint8_t *dst, const uint32_t *idx, int n, size_t row_bytes) {
+    const size_t total = size_t(n) * row_bytes;
+    for (size_t t = blockIdx.x * size_t(blockDim.x) + threadIdx.x; t < total; t += size_t(gridDim.x) * blockDim.x) {
+        const size_t r = t / row_bytes, c = t % row_bytes;
+        dst[t] = src[size_t(idx[r]) * row_bytes + c];
+    }
+}
+
+__global__ void k_inc_u32(uint32_t *p) {
+    if (threadIdx.x == 0) *p += 1;
+}
+
+__global__ void k_fill_u32(uint32_t *p, uint32_t v, size_t n) {
+    for (size_t t = blockIdx.x * size_t(blockDim.x) + threadIdx.x; t < n; t += size_t(gridDim.x) * blockDim.x) p[t] = v;
+}
+
+int grid_1d(size_t n, int block) {
+    const size_t g = (n + block - 1) / block;
+    return int(g < 1 ? 1 : (g > 65536 ? 65536 : g));
+}
+
+template <int T>
+hipError_t launch_embed_pos_ln(const DevMatrix &E, const uint32_t *ids, int rows, const float *pos,
+                               const uint32_t *step, uint32_t base, float scale, const float *g, const float *b,
+                               float eps, float *x, float *h, hipStream_t st) {
+    hipLaunchKernelGGL(k_embed_pos_ln<T>, dim3(rows), dim3(kLnThreads), E.K * sizeof(float), st, E.q, E.s, E.d, ids,
+                       pos, step, base, scale, E.K, g, b, eps, x, h);
+    return hipGetLastError();
+}
+
+template <int T>
+hipError_t launch_embed_pos_rows(const DevMatrix &E, const uint32_t *ids, const uint32_t *pidx, int rows,
+                                 const float *pos, float scale, float *x, hipStream_t st) {
+    hipLaunchKernelGGL(k_embed_pos_rows<T>, dim3(rows), dim3(kLnThreads), E.K * sizeof(float), st, E.q, E.s, E.d,
+                       ids, pidx, pos, scale, E.K, x);
+    return hipGetLastError();
+}
+
+}  // namespace
+
+hipError_t layernorm(const float *x, int rows, int d, const float *g, const float *b, float eps, float *out,
+                     hipStream_t st) {
+    if (d > kLnThreads * kLnMaxPerThread) return hipErrorInvalidValue;
+    if (rows <= 0) return hipSuccess;
+    hipLaunchKernelGGL(k_layernorm, dim3(rows), dim3(kLnThreads), 0, st, x, d, g, b, eps, out);
+    return hipGetLastError();
+}
+
+hipError_t residual_ln(float *x, const float *y, int rows, int d, const float *g, const float *b, float eps, float *h,
+                       hipStream_t st) {
+    if (d > kLnThreads * kLnMaxPerThread) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(k_residual_ln, dim3(rows), dim3(kLnThreads), 0, st, x, y, d, g, b, eps, h);
+    return hipGetLastError();
+}
+
+hipError_t embed_pos_ln(const DevMatrix &E, const uint32_t *ids, int rows, const float *pos, const uint32_t *step,
+                        uint32_t base, float scale, const float *g, const float *b, float eps, float *x, float *h,
+                        hipStream_t st) {
+    if (E.K > kLnThreads * kLnMaxPerThread || E.K % 16) return hipErrorInvalidValue;
+    MLG_DISPATCH_TYPE(E.type, launch_embed_pos_ln, E, ids, rows, pos, step, base, scale, g, b, eps, x, h, st)
+}
+
+hipError_t embed_pos_rows(const DevMatrix &E, const uint32_t *ids, const uint32_t *pidx, int rows, const float *pos,
+                          float scale, float *x, hipStream_t st) {
+    if (E.K % 16) return hipErrorInvalidValue;
+    if (rows <= 0) return hipSuccess;
+    MLG_DISPATCH_TYPE(E.type, launch_embed_pos_rows, E, ids, pidx, rows, pos, scale, x, st)
+}
+
+hipError_t qkv_split(const float *qkv, int b, int H, int hd, int m, const uint32_t *step, float *q, __half *kc,
+                     __half *vc, hipStream_t st) {
+    hipLaunchKernelGGL(k_qkv_split, dim3(b * H), dim3(((hd + 63) / 64) * 64), 0, st, qkv, H, hd, m, step, q, kc, vc);
+    return hipGetLastError();
+}
+
+hipError_t attn_decode(const float *q, const __half *K, const __half *V, int b, int H, int hd, int L,
+                       const uint32_t *lens, const uint32_t *step, float *out, hipStream_t st) {
+    if (hd % 8 || hd > 256) return hipErrorInvalidValue;
+    const int block = 256, groups = block / hd > 0 ? block / hd : 1;
+    const size_t shared = sizeof(float) * (hd + L + groups * hd);
+    hipLaunchKernelGGL(k_attn_decode, dim3(b * H), dim3(block), shared, st, q, K, V, H, hd, L, lens, step, out);
+    return hipGetLastError();
+}
+
+hipError_t attn_prefill(const float *qkv, int b, int s, int H, int hd, const uint32_t *lens, float *out,
+                        hipStream_t st) {
+    if (hd % 4) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(k_attn_prefill, dim3(b * s * H), dim3(64), sizeof(float) * s, st, qkv, s, H, hd, lens, out);
+    return hipGetLastError();
+}
+
+hipError_t split_cross_kv(const float *kv, int b, int s, int H, int hd, __half *K, __half *V, hipStream_t st) {
+    const size_t n = size_t(b) * s * H * hd;
+    hipLaunchKernelGGL(k_split_cross_kv, dim3(grid_1d(n, 256)), dim3(256), 0, st, kv, b, s, H, hd, K, V);
+    return hipGetLastError();
+}
+
+hipError_t copy_cross(const __half *src, const uint32_t *map, int n_dst, int H, int s, int hd, __half *dst, int S,
+                      hipStream_t st) {
+    const size_t total = size_t(n_dst) * H * s * hd;
+    if (!total) return hipSuccess;
+    hipLaunchKernelGGL(k_copy_cross, dim3(grid_1d(total, 256)), dim3(256), 0, st, src, map, n_dst, H, s, hd, dst, S);
+    return hipGetLastError();
+}
+
+hipError_t argmax_partial(const float *logits, int b, int V, int ldl, int mask_id, float *pv, uint32_t *pi, int parts,
+                          hipStream_t st) {
+    const int chunk = (V + parts - 1) / parts;
+    hipLaunchKernelGGL(k_argmax_partial, dim3(parts, b), dim3(256), 0, st, logits, V, ldl, chunk, mask_id, pv, pi);
+    return hipGetLastError();
+}
+
+hipError_t greedy_finalize(const float *pv, const uint32_t *pi, int parts, int b, uint8_t *finished, uint32_t *ids,
+                           uint32_t *out, int m, uint32_t *step, uint32_t eos, uint32_t pad, hipStream_t st) {
+    hipLaunchKernelGGL(k_greedy_finalize, dim3(1), dim3(256), 0, st, pv, pi, parts, b, finished, ids, out, m, step,
+                       eos, pad);
+    return hipGetLastError();
+}
+
+size_t logsoftmax_topk_scratch(int rows, int k) {
+    (void)k;
+    return size_t(rows) * kTopParts * (2 + 2 * kTopMax) * sizeof(float);
+}
+
+hipError_t logsoftmax_topk(const float *logits, int rows, int V, int k, int mask_id, float *scratch, float *vals,
+                           uint32_t *idx, hipStream_t st) {
+    if (k < 1 || k > kTopMax) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(k_lsm_topk_partial, dim3(kTopParts, rows), dim3(256), 0, st, logits, V, k, mask_id, scratch);
+    hipLaunchKernelGGL(k_lsm_topk_final, dim3((rows + 63) / 64), dim3(64), 0, st, scratch, rows, kTopParts, k, vals,
+                       idx);
+    return hipGetLastError();
+}
+
+hipError_t gather_rows(const void *src, void *dst, const uint32_t *idx, int n, size_t row_bytes, hipStream_t st) {
+    if (!n || !row_bytes) return hipSuccess;
+    if (row_bytes % 4 == 0) {
+        const size_t words = row_bytes / 4;
+        hipLaunchKernelGGL(k_gather_rows_u32, dim3(grid_1d(n * words, 256)), dim3(256), 0, st,
+                           static_cast<const uint32_t *>(src), static_cast<uint32_t *>(dst), idx, n, words);
+    } else {
+        hipLaunchKernelGGL(k_gather_rows_u8, dim3(grid_1d(n * row_bytes, 256)), dim3(256), 0, st,
+                           static_cast<const uint8_t *>(src), static_cast<uint8_t *>(dst), idx, n, row_bytes);
+    }
+    return hipGetLastError();
+}
+
+hipError_t inc_u32(uint32_t *p, hipStream_t st) {
+    hipLaunchKernelGGL(k_inc_u32, dim3(1), dim3(64), 0, st, p);
+    return hipGetLastError();
+}
+
+hipError_t fill_u32(uint32_t *p, uint32_t v, size_t n, hipStream_t st) {
+    if (!n) return hipSuccess;
+    hipLaunchKernelGGL(k_fill_u32, dim3(grid_1d(n, 256)), dim3(256), 0, st, p, v, n);
+    return hipGetLastError();
+}
+
+}  // namespace mlg

@@ -1,0 +1,95 @@
+// Host-side launchers of the HIP kernels.  All pointers are device pointers;
+// every launcher is asynchronous on `st` and returns hipSuccess or the launch error.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace mlg {
+
+// A weight matrix W [N, K] resident in HBM.  Q4_K / Q5_K / F16 / F32 keep the
+// GGUF bytes as they are; Q6_K and Q8_0 are split into planes at upload so that
+// every plane is 16-byte aligned (same bytes in total, bit-identical dequant):
+//   Q6_K: q = [N][nb][192] (ql | qh), s = [N][nb][16] int8 scales, d = [N][nb] f16
+//   Q8_0: q = [N][K] int8,            d = [N][K/32] f16
+struct DevMatrix {
+    uint32_t type = 0;
+    int N = 0, K = 0;
+    uint8_t *q = nullptr, *s = nullptr, *d = nullptr;
+    size_t bytes = 0;  // total bytes of the planes (= GGUF bytes)
+};
+
+// Splits/copies GGUF rows [N][K] of `type` into the device layout (host side).
+// Fills `host_planes` with q | s | d concatenated and the plane offsets.
+bool layout_planes(uint32_t type, int N, int K, const uint8_t *gguf, uint8_t *out, size_t *off_s, size_t *off_d,
+                   size_t *total);
+size_t planes_bytes(uint32_t type, int N, int K);
+
+// Largest batch the register-resident GEMV handles for this matrix (0 if none).
+int gemv_max_batch(const DevMatrix &w);
+
+// y[b][n] = sum_k x[b][k] W[n][k] (+ bias[n]) (relu if set).  b <= gemv_max_batch(w).
+hipError_t gemv(const DevMatrix &w, const float *x, int ldx, int b, float *y, int ldy, const float *bias, bool relu,
+                hipStream_t st);
+// Same product, but each workgroup writes the argmax (ties -> lowest index) of its
+// rows to pv/pi [b][parts]; logits are not stored.  Index `mask_id` (>= 0) is skipped.
+hipError_t gemv_argmax(const DevMatrix &w, const float *x, int ldx, int b, int mask_id, float *pv, uint32_t *pi,
+                       int *parts, hipStream_t st);
+// Number of partial results gemv_argmax writes per batch row.
+int gemv_argmax_parts(const DevMatrix &w, int b);
+
+// Y[m][n] = sum_k X[m][k] W[n][k] + bias[n] (+ R[m][n]) (relu if set); any M.
+hipError_t gemm(const DevMatrix &w, const float *X, int ldx, int M, float *Y, int ldy, const float *bias, bool relu,
+                const float *R, int ldr, hipStream_t st);
+
+// Row LayerNorm (biased variance): out = (x - mean) * rsqrt(var + eps) * g + b.
+hipError_t layernorm(const float *x, int rows, int d, const float *g, const float *b, float eps, float *out,
+                     hipStream_t st);
+// x = x + y ; h = LayerNorm(x).  (bias already added to y by the producer)
+hipError_t residual_ln(float *x, const float *y, int rows, int d, const float *g, const float *b, float eps, float *h,
+                       hipStream_t st);
+// Decoder input: x = dequant(E[ids[r]]) * scale + pos[*step + base]; h = LayerNorm(x).
+hipError_t embed_pos_ln(const DevMatrix &E, const uint32_t *ids, int rows, const float *pos, const uint32_t *step,
+                        uint32_t base, float scale, const float *g, const float *b, float eps, float *x, float *h,
+                        hipStream_t st);
+// Encoder input rows: x[r] = dequant(E[ids[r]]) * scale + pos[pidx[r]].
+hipError_t embed_pos_rows(const DevMatrix &E, const uint32_t *ids, const uint32_t *pidx, int rows, const float *pos,
+                          float scale, float *x, hipStream_t st);
+// Splits qkv [b][3d] (bias included): q -> [b][H][hd] f32, k/v -> f16 caches
+// [b][H][m][hd] at slot *step.
+hipError_t qkv_split(const float *qkv, int b, int H, int hd, int m, const uint32_t *step, float *q, __half *kc,
+                     __half *vc, hipStream_t st);
+// Single-query attention per (row, head) over f16 K/V [b][H][L][hd]: n = lens[row]
+// if lens, else *step + 1.  out [b][H*hd].
+hipError_t attn_decode(const float *q, const __half *K, const __half *V, int b, int H, int hd, int L,
+                       const uint32_t *lens, const uint32_t *step, float *out, hipStream_t st);
+// Encoder self-attention over f32 qkv [b*s][3d] (rows of sentence i are i*s..),
+// key j of row i valid iff j < lens[i].  out [b*s][d].
+hipError_t attn_prefill(const float *qkv, int b, int s, int H, int hd, const uint32_t *lens, float *out,
+                        hipStream_t st);
+// kv [b*s][2d] f32 (k | v) -> f16 K, V [b][H][s][hd]
+hipError_t split_cross_kv(const float *kv, int b, int s, int H, int hd, __half *K, __half *V, hipStream_t st);
+// dst [.][H][S][hd] row r (< n_dst) <- src [.][H][s][hd] row map[r] (row r if map is
+// null), S >= s.  map is a device array.
+hipError_t copy_cross(const __half *src, const uint32_t *map, int n_dst, int H, int s, int hd, __half *dst, int S,
+                      hipStream_t st);
+// Argmax over logits [b][V] (row stride ldl) into pv/pi [b][parts].
+hipError_t argmax_partial(const float *logits, int b, int V, int ldl, int mask_id, float *pv, uint32_t *pi,
+                          int parts, hipStream_t st);
+// Second argmax pass + greedy bookkeeping (kernels/malaga.cu:290-326 semantics):
+// tok = finished ? pad : argmax ; finished |= tok == eos ; ids = tok ;
+// out[row][*step] = tok ; ++*step.
+hipError_t greedy_finalize(const float *pv, const uint32_t *pi, int parts, int b, uint8_t *finished, uint32_t *ids,
+                           uint32_t *out, int m, uint32_t *step, uint32_t eos, uint32_t pad, hipStream_t st);
+// Beam: per row log-softmax of logits [rows][V] and its top-k (k <= 8, ties -> lowest
+// index): vals/idx [rows][k].  mask_id (>= 0) is treated as -inf.
+hipError_t logsoftmax_topk(const float *logits, int rows, int V, int k, int mask_id, float *scratch, float *vals,
+                           uint32_t *idx, hipStream_t st);
+size_t logsoftmax_topk_scratch(int rows, int k);
+// dst[i] = src[idx[i]] for rows of `row_bytes` bytes (i < n).
+hipError_t gather_rows(const void *src, void *dst, const uint32_t *idx, int n, size_t row_bytes, hipStream_t st);
+// *p += 1 on the device.
+hipError_t inc_u32(uint32_t *p, hipStream_t st);
+// Fill n uint32 values (graph-safe replacement for hipMemsetAsync).
+hipError_t fill_u32(uint32_t *p, uint32_t v, size_t n, hipStream_t st);
+
+}  // namespace mlg

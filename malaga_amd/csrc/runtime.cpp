@@ -1,0 +1,765 @@
+#include "runtime.hpp"
+
+#include <algorithm>
+#include <atomic>
+#include <cmath>
+#include <cstdlib>
+#include <cstring>
+#include <numeric>
+
+#include "gguf.hpp"
+#include "quant.hpp"
+
+namespace mlg {
+
+namespace {
+
+constexpr float kLnEps = 1e-5f;          // src/config.rs:58
+constexpr size_t kGraphBytes = 32u << 20;  // accounting per captured graph (src/graph.rs:149-150)
+
+std::atomic<long> g_fail_after{-1};
+
+[[noreturn]] void fail(int code, const std::string &msg) { throw Failure{code, msg}; }
+
+uint32_t next_pow2(uint32_t n) {
+    uint32_t p = 1;
+    while (p < n) p <<= 1;
+    return p;
+}
+
+template <typename T>
+void h2d(T *dst, const std::vector<T> &src, hipStream_t st) {
+    if (src.empty()) return;
+    check_hip(hipMemcpyAsync(dst, src.data(), src.size() * sizeof(T), hipMemcpyHostToDevice, st), "H2D copy");
+    check_hip(hipStreamSynchronize(st), "H2D sync");
+}
+
+// Device buffers freed at scope exit.
+struct DevTemp {
+    std::vector<void *> p;
+    ~DevTemp() {
+        for (auto q : p) dev_free(q);
+    }
+    template <typename T>
+    T *get(size_t n, const char *what) {
+        p.push_back(dev_alloc(n * sizeof(T), what));
+        return static_cast<T *>(p.back());
+    }
+};
+
+}  // namespace
+
+void check_hip(hipError_t e, const char *what) {
+    if (e == hipSuccess) return;
+    if (e == hipErrorOutOfMemory) fail(ERR_OOM, std::string("OUT_OF_MEMORY: ") + what);
+    fail(ERR_HIP, std::string(what) + ": " + hipGetErrorString(e));
+}
+
+void set_fail_alloc_after(long n) { g_fail_after.store(n); }
+
+void *dev_alloc(size_t bytes, const char *what) {
+    const long n = g_fail_after.load();
+    if (n >= 0) {  // one-shot test hook
+        g_fail_after.store(n - 1);
+        if (n == 0) fail(ERR_OOM, std::string("OUT_OF_MEMORY: injected allocation failure (") + what + ")");
+    }
+    void *p = nullptr;
+    const hipError_t e = hipMalloc(&p, bytes ? bytes : 16);
+    if (e == hipErrorOutOfMemory) {
+        (void)hipGetLastError();
+        fail(ERR_OOM, std::string("OUT_OF_MEMORY: allocating ") + std::to_string(bytes) + " bytes for " + what);
+    }
+    check_hip(e, what);
+    return p;
+}
+
+void dev_free(void *p) {
+    if (p) (void)hipFree(p);
+}
+
+int bucket(int n, int min, int max) {
+    return std::max(std::min(int(next_pow2(uint32_t(std::max(n, min)))), max), n);
+}
+
+int budget(const ModelConfig &c, int len, int max_new_tokens) {
+    const int cap = std::min(c.max_length, c.max_position_embeddings - 2);
+    const int v = max_new_tokens > 0 ? max_new_tokens : 2 * len + 16;
+    return std::max(1, std::min(v, cap));
+}
+
+// ------------------------------------------------------------------ layout
+
+size_t planes_bytes(uint32_t type, int N, int K) { return size_t(type_bytes(type, K)) * size_t(N); }
+
+bool layout_planes(uint32_t type, int N, int K, const uint8_t *src, uint8_t *out, size_t *off_s, size_t *off_d,
+                   size_t *total) {
+    TypeInfo ti;
+    if (!type_info(type, &ti) || K % ti.block_elems) return false;
+    const size_t nblk = size_t(N) * (K / ti.block_elems);
+    *total = nblk * ti.block_bytes;
+    if (type == GGML_Q6_K) {
+        *off_s = nblk * 192;
+        *off_d = *off_s + nblk * 16;
+        for (int64_t i = 0; i < int64_t(nblk); ++i) {
+            const uint8_t *b = src + i * 210;
+            std::memcpy(out + i * 192, b, 192);
+            std::memcpy(out + *off_s + i * 16, b + 192, 16);
+            std::memcpy(out + *off_d + i * 2, b + 208, 2);
+        }
+    } else if (type == GGML_Q8_0) {
+        *off_s = nblk * 32;
+        *off_d = nblk * 32;
+        for (int64_t i = 0; i < int64_t(nblk); ++i) {
+            const uint8_t *b = src + i * 34;
+            std::memcpy(out + i * 32, b + 2, 32);
+            std::memcpy(out + *off_d + i * 2, b, 2);
+        }
+    } else {
+        std::memcpy(out, src, *total);
+        *off_s = *off_d = *total;
+    }
+    return true;
+}
+
+// ------------------------------------------------------------------- model
+
+Batch::~Batch() {
+    for (auto p : ck) dev_free(p);
+    for (auto p : cv) dev_free(p);
+}
+
+StaticState::~StaticState() {
+    for (auto p : owned) dev_free(p);
+}
+
+Model::~Model() {
+    graphs.clear();
+    for (auto p : owned_) dev_free(p);
+}
+
+float *Model::upload_f32(GgufFile &g, const std::string &name, int64_t n) {
+    const GgufTensorInfo *t = g.tensor(name);
+    if (!t) fail(ERR_FORMAT, "missing tensor " + name);
+    if (t->numel() != n) fail(ERR_FORMAT, "tensor " + name + " has " + std::to_string(t->numel()) + " values");
+    std::vector<float> host(static_cast<size_t>(n));
+    if (!dequantize(t->type, g.tensor_data(*t), n, host.data()))
+        fail(ERR_UNSUPPORTED, "tensor " + name + ": unsupported type " + std::to_string(t->type));
+    float *d = static_cast<float *>(dev_alloc(size_t(n) * 4, name.c_str()));
+    owned_.push_back(d);
+    check_hip(hipMemcpy(d, host.data(), size_t(n) * 4, hipMemcpyHostToDevice), "upload");
+    weight_bytes += size_t(n) * 4;
+    return d;
+}
+
+DevMatrix Model::upload_matrix(GgufFile &g, const std::string &name, int n, int k) {
+    const GgufTensorInfo *t = g.tensor(name);
+    if (!t) fail(ERR_FORMAT, "missing tensor " + name);
+    if (t->ne.size() != 2 || int64_t(t->ne[0]) != k || int64_t(t->ne[1]) != n)
+        fail(ERR_FORMAT, "tensor " + name + " has an unexpected shape");
+    TypeInfo ti;
+    if (!type_info(t->type, &ti) || t->type == GGML_BF16)
+        fail(ERR_UNSUPPORTED, "tensor " + name + ": unsupported type " + std::to_string(t->type));
+    DevMatrix m;
+    m.type = t->type;
+    m.N = n;
+    m.K = k;
+    size_t off_s, off_d, total;
+    std::vector<uint8_t> host(planes_bytes(t->type, n, k));
+    if (!layout_planes(t->type, n, k, g.tensor_data(*t), host.data(), &off_s, &off_d, &total))
+        fail(ERR_FORMAT, "tensor " + name + ": row length not a whole number of blocks");
+    uint8_t *d = static_cast<uint8_t *>(dev_alloc(total, name.c_str()));
+    owned_.push_back(d);
+    check_hip(hipMemcpy(d, host.data(), total, hipMemcpyHostToDevice), "upload");
+    m.q = d;
+    m.s = d + off_s;
+    m.d = d + off_d;
+    m.bytes = total;
+    weight_bytes += total;
+    return m;
+}
+
+Linear Model::load_linear(GgufFile &g, const std::string &name, int n, int k) {
+    Linear l;
+    l.w = upload_matrix(g, name + ".weight", n, k);
+    l.b = upload_f32(g, name + ".bias", n);
+    return l;
+}
+
+LNorm Model::load_ln(GgufFile &g, const std::string &name, int d) {
+    LNorm l;
+    l.g = upload_f32(g, name + ".weight", d);
+    l.b = upload_f32(g, name + ".bias", d);
+    return l;
+}
+
+// src/config.rs:93-116 and src/model.rs:343-433
+void Model::load(const std::string &path) {
+    GgufFile g;
+    const std::string err = g.open(path);
+    if (!err.empty()) fail(ERR_IO, err);
+    const GgufValue *arch = g.get("general.architecture");
+    if (!arch || arch->type != GV_STRING || arch->s != "nllb")
+        fail(ERR_FORMAT, "unsupported architecture, expected 'nllb'");
+    auto u = [&](const char *key) -> int {
+        const GgufValue *v = g.get(key);
+        if (!v || !v->is_int()) fail(ERR_FORMAT, std::string("missing GGUF metadata key '") + key + "'");
+        return int(v->u);
+    };
+    cfg.vocab_size = u("nllb.vocab_size");
+    cfg.d_model = u("nllb.embedding_length");
+    cfg.encoder_layers = u("nllb.encoder.block_count");
+    cfg.decoder_layers = u("nllb.decoder.block_count");
+    cfg.encoder_heads = u("nllb.encoder.attention.head_count");
+    cfg.decoder_heads = u("nllb.decoder.attention.head_count");
+    cfg.encoder_ffn = u("nllb.encoder.feed_forward_length");
+    cfg.decoder_ffn = u("nllb.decoder.feed_forward_length");
+    cfg.max_position_embeddings = u("nllb.context_length");
+    cfg.scale_embedding = u("nllb.scale_embedding");
+    cfg.max_length = u("nllb.max_length");
+    cfg.bos_token_id = u("tokenizer.ggml.bos_token_id");
+    cfg.pad_token_id = u("tokenizer.ggml.padding_token_id");
+    cfg.eos_token_id = u("tokenizer.ggml.eos_token_id");
+    cfg.decoder_start_token_id = u("tokenizer.ggml.decoder_start_token_id");
+    const int d = cfg.d_model;
+    if (d <= 0 || d % cfg.decoder_heads || d % cfg.encoder_heads || d > 4096 || d % 16)
+        fail(ERR_UNSUPPORTED, "unsupported d_model " + std::to_string(d));
+    if ((d / cfg.decoder_heads) % 8 || (d / cfg.encoder_heads) % 8)
+        fail(ERR_UNSUPPORTED, "head dimension must be a multiple of 8");
+
+    embed = upload_matrix(g, "token_embd.weight", cfg.vocab_size, d);
+    // src/model.rs:324-340: [sin | cos] in f64, row pad zeroed
+    n_pos = cfg.max_position_embeddings + cfg.pad_token_id + 1;
+    std::vector<float> table(static_cast<size_t>(n_pos) * d, 0.f);
+    const int half = d / 2;
+    const double step = std::log(10000.0) / (double(half) - 1.0);
+    for (int p = 0; p < n_pos; ++p) {
+        if (p == cfg.pad_token_id) continue;
+        for (int i = 0; i < half; ++i) {
+            const double a = double(p) * std::exp(-double(i) * step);
+            table[size_t(p) * d + i] = float(std::sin(a));
+            table[size_t(p) * d + half + i] = float(std::cos(a));
+        }
+    }
+    pos = static_cast<float *>(dev_alloc(table.size() * 4, "position table"));
+    owned_.push_back(pos);
+    check_hip(hipMemcpy(pos, table.data(), table.size() * 4, hipMemcpyHostToDevice), "upload");
+    embed_scale = cfg.scale_embedding ? float(std::sqrt(double(d))) : 1.f;
+
+    for (int i = 0; i < cfg.encoder_layers; ++i) {
+        const std::string p = "enc.blk." + std::to_string(i);
+        EncLayer l;
+        l.attn_norm = load_ln(g, p + ".attn_norm", d);
+        l.qkv = load_linear(g, p + ".attn_qkv", 3 * d, d);
+        l.out = load_linear(g, p + ".attn_out", d, d);
+        l.ffn_norm = load_ln(g, p + ".ffn_norm", d);
+        l.up = load_linear(g, p + ".ffn_up", cfg.encoder_ffn, d);
+        l.down = load_linear(g, p + ".ffn_down", d, cfg.encoder_ffn);
+        enc.push_back(l);
+    }
+    for (int i = 0; i < cfg.decoder_layers; ++i) {
+        const std::string p = "dec.blk." + std::to_string(i);
+        DecLayer l;
+        l.attn_norm = load_ln(g, p + ".attn_norm", d);
+        l.qkv = load_linear(g, p + ".attn_qkv", 3 * d, d);
+        l.out = load_linear(g, p + ".attn_out", d, d);
+        l.cross_norm = load_ln(g, p + ".cross_attn_norm", d);
+        l.cross_q = load_linear(g, p + ".cross_attn_q", d, d);
+        l.cross_kv = load_linear(g, p + ".cross_attn_kv", 2 * d, d);
+        l.cross_out = load_linear(g, p + ".cross_attn_out", d, d);
+        l.ffn_norm = load_ln(g, p + ".ffn_norm", d);
+        l.up = load_linear(g, p + ".ffn_up", cfg.decoder_ffn, d);
+        l.down = load_linear(g, p + ".ffn_down", d, cfg.decoder_ffn);
+        dec.push_back(l);
+    }
+    enc_norm = load_ln(g, "enc.output_norm", d);
+    dec_norm = load_ln(g, "dec.output_norm", d);
+    check_hip(hipDeviceSynchronize(), "model upload");
+}
+
+void Model::matmul(const Linear &l, const float *x, int rows, float *y, bool relu, const float *resid) {
+    hipStream_t st = ctx->stream;
+    if (!resid && rows <= gemv_max_batch(l.w)) {
+        check_hip(gemv(l.w, x, l.w.K, rows, y, l.w.N, l.b, relu, st), "gemv");
+    } else {
+        check_hip(gemm(l.w, x, l.w.K, rows, y, l.w.N, l.b, relu, resid, l.w.N, st), "gemm");
+    }
+}
+
+// src/model.rs:463-500: right-padded ids, embedding * scale + positions (j + pad + 1),
+// encoder layers, enc_norm, then the cross K/V of every decoder layer.
+std::unique_ptr<Batch> Model::encode(const std::vector<std::vector<uint32_t>> &src) {
+    hipStream_t st = ctx->stream;
+    auto out = std::make_unique<Batch>();
+    const int b = int(src.size());
+    int s = 0;
+    for (auto &r : src) s = std::max(s, int(r.size()));
+    if (b == 0 || s == 0) fail(ERR_INVALID, "empty batch");
+    if (s > cfg.max_position_embeddings) fail(ERR_INVALID, "source longer than the position table");
+    const int d = cfg.d_model, M = b * s, H = cfg.encoder_heads, hd = d / H, f = cfg.encoder_ffn;
+    const uint32_t pad = uint32_t(cfg.pad_token_id);
+    std::vector<uint32_t> ids(static_cast<size_t>(M), pad), pidx(size_t(M), pad);
+    out->b = b;
+    out->s = s;
+    for (int i = 0; i < b; ++i) {
+        out->lens.push_back(uint32_t(src[i].size()));
+        for (int j = 0; j < int(src[i].size()); ++j) {
+            if (src[i][j] >= uint32_t(cfg.vocab_size)) fail(ERR_INVALID, "token id out of range");
+            ids[size_t(i) * s + j] = src[i][j];
+            pidx[size_t(i) * s + j] = uint32_t(j) + pad + 1;
+        }
+    }
+    DevTemp tmp;
+    uint32_t *d_ids = tmp.get<uint32_t>(M, "encoder ids"), *d_pidx = tmp.get<uint32_t>(M, "encoder positions");
+    uint32_t *d_lens = tmp.get<uint32_t>(b, "encoder lens");
+    float *x = tmp.get<float>(size_t(M) * d, "encoder x"), *h = tmp.get<float>(size_t(M) * d, "encoder h");
+    float *qkv = tmp.get<float>(size_t(M) * std::max(3 * d, f), "encoder qkv");
+    float *att = tmp.get<float>(size_t(M) * d, "encoder att");
+    h2d(d_ids, ids, st);
+    h2d(d_pidx, pidx, st);
+    h2d(d_lens, out->lens, st);
+    check_hip(embed_pos_rows(embed, d_ids, d_pidx, M, pos, embed_scale, x, st), "embed");
+    for (auto &l : enc) {
+        check_hip(layernorm(x, M, d, l.attn_norm.g, l.attn_norm.b, kLnEps, h, st), "layernorm");
+        matmul(l.qkv, h, M, qkv, false, nullptr);
+        check_hip(attn_prefill(qkv, b, s, H, hd, d_lens, att, st), "attn_prefill");
+        matmul(l.out, att, M, x, false, x);
+        check_hip(layernorm(x, M, d, l.ffn_norm.g, l.ffn_norm.b, kLnEps, h, st), "layernorm");
+        matmul(l.up, h, M, qkv, true, nullptr);
+        matmul(l.down, qkv, M, x, false, x);
+    }
+    check_hip(layernorm(x, M, d, enc_norm.g, enc_norm.b, kLnEps, h, st), "layernorm");
+    const int Hd = cfg.decoder_heads, hdd = d / Hd;
+    float *kv = tmp.get<float>(size_t(M) * 2 * d, "cross kv");
+    for (auto &l : dec) {
+        __half *K = static_cast<__half *>(dev_alloc(size_t(M) * d * 2, "cross K"));
+        out->ck.push_back(K);
+        __half *V = static_cast<__half *>(dev_alloc(size_t(M) * d * 2, "cross V"));
+        out->cv.push_back(V);
+        matmul(l.cross_kv, h, M, kv, false, nullptr);
+        check_hip(split_cross_kv(kv, b, s, Hd, hdd, K, V, st), "split_cross_kv");
+    }
+    check_hip(hipStreamSynchronize(st), "encode");
+    return out;
+}
+
+std::unique_ptr<StaticState> Model::new_state(int b, int s, int m, bool beam) {
+    auto st = std::make_unique<StaticState>();
+    st->b = b;
+    st->s = s;
+    st->m = m;
+    const int d = cfg.d_model, H = cfg.decoder_heads, hd = d / H, L = cfg.decoder_layers, V = cfg.vocab_size;
+    auto get = [&](size_t bytes, const char *what) {
+        void *p = dev_alloc(bytes, what);
+        st->owned.push_back(p);
+        st->bytes += bytes;
+        return p;
+    };
+    st->ids = static_cast<uint32_t *>(get(size_t(b) * 4, "ids"));
+    st->step = static_cast<uint32_t *>(get(4, "step"));
+    st->lens = static_cast<uint32_t *>(get(size_t(b) * 4, "lens"));
+    st->out = static_cast<uint32_t *>(get(size_t(b) * m * 4, "out"));
+    st->finished = static_cast<uint8_t *>(get(size_t(b), "finished"));
+    for (int i = 0; i < L; ++i) {
+        st->kc.push_back(static_cast<__half *>(get(size_t(b) * H * m * hd * 2, "self K")));
+        st->vc.push_back(static_cast<__half *>(get(size_t(b) * H * m * hd * 2, "self V")));
+        st->ck.push_back(static_cast<__half *>(get(size_t(b) * H * s * hd * 2, "cross K")));
+        st->cv.push_back(static_cast<__half *>(get(size_t(b) * H * s * hd * 2, "cross V")));
+        check_hip(hipMemsetAsync(st->ck.back(), 0, size_t(b) * H * s * hd * 2, ctx->stream), "memset");
+        check_hip(hipMemsetAsync(st->cv.back(), 0, size_t(b) * H * s * hd * 2, ctx->stream), "memset");
+    }
+    st->x = static_cast<float *>(get(size_t(b) * d * 4, "x"));
+    st->h = static_cast<float *>(get(size_t(b) * d * 4, "h"));
+    st->y = static_cast<float *>(get(size_t(b) * d * 4, "y"));
+    st->att = static_cast<float *>(get(size_t(b) * d * 4, "att"));
+    st->q = static_cast<float *>(get(size_t(b) * d * 4, "q"));
+    st->qkv = static_cast<float *>(get(size_t(b) * 3 * d * 4, "qkv"));
+    st->u = static_cast<float *>(get(size_t(b) * cfg.decoder_ffn * 4, "ffn"));
+    if (beam || b > gemv_max_batch(embed)) st->logits = static_cast<float *>(get(size_t(b) * V * 4, "logits"));
+    st->parts = std::max(gemv_argmax_parts(embed, b), 64);
+    st->pv = static_cast<float *>(get(size_t(b) * st->parts * 4, "argmax partials"));
+    st->pi = static_cast<uint32_t *>(get(size_t(b) * st->parts * 4, "argmax partials"));
+    check_hip(hipStreamSynchronize(ctx->stream), "state");
+    return st;
+}
+
+// src/graph.rs:91-118: cross K/V and lens of the batch, start token, step 0.
+// Row r of the state takes source row row_of[r]; rows past row_of.size() are idle.
+void Model::reset_state(StaticState &st, const Batch &src, const std::vector<uint32_t> &row_of, uint32_t start) {
+    hipStream_t s = ctx->stream;
+    const int H = cfg.decoder_heads, hd = cfg.d_model / H, n = int(row_of.size());
+    uint32_t *d_map = static_cast<uint32_t *>(dev_alloc(size_t(std::max(n, 1)) * 4, "row map"));
+    struct Guard { void *p; ~Guard() { dev_free(p); } } guard{d_map};
+    h2d(d_map, row_of, s);
+    for (size_t l = 0; l < st.ck.size(); ++l) {
+        check_hip(copy_cross(src.ck[l], d_map, n, H, src.s, hd, st.ck[l], st.s, s), "copy_cross");
+        check_hip(copy_cross(src.cv[l], d_map, n, H, src.s, hd, st.cv[l], st.s, s), "copy_cross");
+    }
+    std::vector<uint32_t> lens(static_cast<size_t>(st.b), 1u);
+    for (int r = 0; r < n; ++r) lens[r] = src.lens[row_of[r]];
+    h2d(st.lens, lens, s);
+    check_hip(fill_u32(st.ids, start, size_t(st.b), s), "fill");
+    check_hip(fill_u32(st.step, 0, 1, s), "fill");
+    std::vector<uint8_t> fin(static_cast<size_t>(st.b));
+    for (int r = 0; r < st.b; ++r) fin[r] = r >= n;
+    h2d(st.finished, fin, s);
+}
+
+void Model::step(StaticState &st, bool greedy_mode, int mask_id) {
+    hipStream_t s = ctx->stream;
+    const int B = st.b, d = cfg.d_model, H = cfg.decoder_heads, hd = d / H, V = cfg.vocab_size;
+    check_hip(embed_pos_ln(embed, st.ids, B, pos, st.step, uint32_t(cfg.pad_token_id + 1), embed_scale,
+                           dec[0].attn_norm.g, dec[0].attn_norm.b, kLnEps, st.x, st.h, s),
+              "embed_pos_ln");
+    for (size_t i = 0; i < dec.size(); ++i) {
+        const DecLayer &l = dec[i];
+        matmul(l.qkv, st.h, B, st.qkv, false, nullptr);
+        check_hip(qkv_split(st.qkv, B, H, hd, st.m, st.step, st.q, st.kc[i], st.vc[i], s), "qkv_split");
+        check_hip(attn_decode(st.q, st.kc[i], st.vc[i], B, H, hd, st.m, nullptr, st.step, st.att, s), "attn");
+        matmul(l.out, st.att, B, st.y, false, nullptr);
+        check_hip(residual_ln(st.x, st.y, B, d, l.cross_norm.g, l.cross_norm.b, kLnEps, st.h, s), "residual_ln");
+        matmul(l.cross_q, st.h, B, st.q, false, nullptr);
+        check_hip(attn_decode(st.q, st.ck[i], st.cv[i], B, H, hd, st.s, st.lens, nullptr, st.att, s), "attn");
+        matmul(l.cross_out, st.att, B, st.y, false, nullptr);
+        check_hip(residual_ln(st.x, st.y, B, d, l.ffn_norm.g, l.ffn_norm.b, kLnEps, st.h, s), "residual_ln");
+        matmul(l.up, st.h, B, st.u, true, nullptr);
+        matmul(l.down, st.u, B, st.y, false, nullptr);
+        const LNorm &next = i + 1 < dec.size() ? dec[i + 1].attn_norm : dec_norm;
+        check_hip(residual_ln(st.x, st.y, B, d, next.g, next.b, kLnEps, st.h, s), "residual_ln");
+    }
+    // st.h is dec_norm(x): tied LM head
+    if (greedy_mode) {
+        int parts = 64;
+        if (B <= gemv_max_batch(embed)) {
+            check_hip(gemv_argmax(embed, st.h, d, B, mask_id, st.pv, st.pi, &parts, s), "lm_head");
+        } else {
+            check_hip(gemm(embed, st.h, d, B, st.logits, V, nullptr, false, nullptr, 0, s), "lm_head");
+            check_hip(argmax_partial(st.logits, B, V, V, mask_id, st.pv, st.pi, parts, s), "argmax");
+        }
+        check_hip(greedy_finalize(st.pv, st.pi, parts, B, st.finished, st.ids, st.out, st.m, st.step,
+                                  uint32_t(cfg.eos_token_id), uint32_t(cfg.pad_token_id), s),
+                  "greedy_finalize");
+    } else {
+        if (B <= gemv_max_batch(embed))
+            check_hip(gemv(embed, st.h, d, B, st.logits, V, nullptr, false, s), "lm_head");
+        else
+            check_hip(gemm(embed, st.h, d, B, st.logits, V, nullptr, false, nullptr, 0, s), "lm_head");
+        check_hip(inc_u32(st.step, s), "step");
+    }
+}
+
+// ------------------------------------------------------------ graph cache
+
+GraphCache::GraphCache(Model *m) : model_(m) {
+    const char *mb = std::getenv("MALAGA_GRAPH_CACHE_MB");
+    long v = mb ? std::atol(mb) : 512;
+    max_bytes_ = size_t(v > 0 ? v : 512) << 20;
+    const char *no = std::getenv("MALAGA_NO_HIP_GRAPH");
+    capture_ = !no || !*no || std::string(no) == "0";
+}
+
+GraphCache::~GraphCache() { clear(); }
+
+size_t GraphCache::Entry::bytes() const { return st->bytes + (exec ? kGraphBytes : 0); }
+
+size_t GraphCache::graphs() const {
+    size_t n = 0;
+    for (auto &e : entries_) n += e.exec != nullptr;
+    return n;
+}
+
+void GraphCache::clear() {
+    for (auto &e : entries_)
+        if (e.exec) (void)hipGraphExecDestroy(e.exec);
+    entries_.clear();
+}
+
+void GraphCache::evict(const Entry *keep) {
+    for (;;) {
+        size_t total = kGraphBytes;
+        for (auto &e : entries_) total += e.bytes();
+        if (total <= max_bytes_ || entries_.size() <= 1) return;
+        auto victim = entries_.end();
+        for (auto it = entries_.begin(); it != entries_.end(); ++it)
+            if (&*it != keep && (victim == entries_.end() || it->last_used < victim->last_used)) victim = it;
+        if (victim == entries_.end()) return;
+        if (victim->exec) (void)hipGraphExecDestroy(victim->exec);
+        entries_.erase(victim);
+    }
+}
+
+std::vector<std::vector<uint32_t>> GraphCache::greedy(const Batch &src, uint32_t tgt_lang, int max_new,
+                                                      int sync_every, bool eos_mask, bool use_graph) {
+    try {
+        return run(src, tgt_lang, max_new, sync_every, eos_mask, use_graph);
+    } catch (const Failure &f) {
+        // src/graph.rs:214-222: out of memory -> drop graphs for good, decode eagerly
+        if (f.code != ERR_OOM || !capture_) throw;
+        capture_ = false;
+        clear();
+        return run(src, tgt_lang, max_new, sync_every, eos_mask, use_graph);
+    }
+}
+
+std::vector<std::vector<uint32_t>> GraphCache::run(const Batch &src, uint32_t tgt_lang, int max_new, int sync_every,
+                                                   bool eos_mask, bool use_graph) {
+    Model &m = *model_;
+    hipStream_t s = m.ctx->stream;
+    const ModelConfig &c = m.cfg;
+    const bool capture = capture_ && use_graph;
+    const int n = src.b, max_m = c.max_position_embeddings;
+    const int b = capture ? int(next_pow2(uint32_t(n))) : n;
+    const int kb = b, ks = bucket(src.s, 16, max_m), km = bucket(max_new + 2, 32, max_m);
+    ++clock_;
+    Entry *e = nullptr;
+    for (auto &it : entries_)
+        if (it.b == kb && it.s == ks && it.m == km) e = &it;
+    if (!e) {
+        Entry ne;
+        ne.b = kb;
+        ne.s = ks;
+        ne.m = km;
+        ne.st = m.new_state(kb, ks, km, false);
+        entries_.push_back(std::move(ne));
+        e = &entries_.back();
+        evict(e);
+    }
+    e->last_used = clock_;
+    StaticState &st = *e->st;
+    const int mask_id = eos_mask ? c.eos_token_id : -1;
+
+    std::vector<uint32_t> rows(static_cast<size_t>(n));
+    std::iota(rows.begin(), rows.end(), 0u);
+    // step 0 consumes decoder_start; its token is replaced by the forced target language
+    m.reset_state(st, src, rows, uint32_t(c.decoder_start_token_id));
+    m.step(st, true, mask_id);
+    check_hip(fill_u32(st.ids, tgt_lang, size_t(st.b), s), "fill");
+    std::vector<uint8_t> fin(static_cast<size_t>(st.b));
+    for (int r = 0; r < st.b; ++r) fin[r] = r >= n;
+    h2d(st.finished, fin, s);
+    m.step(st, true, mask_id);
+    int steps = 2;
+    const int max_steps = std::min(max_new + 1, st.m);
+
+    if (capture && !e->exec && steps < max_steps) {
+        check_hip(hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal), "begin capture");
+        hipGraph_t graph = nullptr;
+        try {
+            m.step(st, true, mask_id);
+        } catch (...) {
+            (void)hipStreamEndCapture(s, &graph);
+            if (graph) (void)hipGraphDestroy(graph);
+            throw;
+        }
+        check_hip(hipStreamEndCapture(s, &graph), "end capture");
+        hipGraphExec_t exec = nullptr;
+        const hipError_t ie = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0);
+        (void)hipGraphDestroy(graph);
+        check_hip(ie, "graph instantiate");
+        e->exec = exec;
+        evict(e);
+    }
+    std::vector<uint8_t> done(static_cast<size_t>(st.b));
+    while (steps < max_steps) {
+        if (steps % sync_every == 0) {
+            check_hip(hipMemcpyAsync(done.data(), st.finished, done.size(), hipMemcpyDeviceToHost, s), "D2H");
+            check_hip(hipStreamSynchronize(s), "sync");
+            if (std::all_of(done.begin(), done.end(), [](uint8_t v) { return v != 0; })) break;
+        }
+        if (capture && e->exec) check_hip(hipGraphLaunch(e->exec, s), "graph launch");
+        else m.step(st, true, mask_id);
+        ++steps;
+    }
+    std::vector<uint32_t> out(static_cast<size_t>(st.b) * st.m);
+    check_hip(hipMemcpyAsync(out.data(), st.out, out.size() * 4, hipMemcpyDeviceToHost, s), "D2H");
+    check_hip(hipStreamSynchronize(s), "sync");
+    std::vector<std::vector<uint32_t>> res(static_cast<size_t>(n));
+    for (int r = 0; r < n; ++r)
+        for (int j = 1; j < steps; ++j) {
+            const uint32_t t = out[size_t(r) * st.m + j];
+            if (t == uint32_t(c.eos_token_id)) break;
+            res[r].push_back(t);
+        }
+    return res;
+}
+
+// ------------------------------------------------------------------- beam
+
+std::vector<std::vector<uint32_t>> Model::beam(const Batch &src, uint32_t tgt_lang, int max_new, int k, float lp,
+                                               bool eos_mask) {
+    hipStream_t s = ctx->stream;
+    const int b = src.b, bk = b * k, V = cfg.vocab_size, H = cfg.decoder_heads, hd = cfg.d_model / H;
+    const uint32_t eos = uint32_t(cfg.eos_token_id);
+    const int mask_id = eos_mask ? cfg.eos_token_id : -1;
+    auto st = new_state(bk, src.s, std::min(max_new + 2, cfg.max_position_embeddings), true);
+    std::vector<uint32_t> expand(static_cast<size_t>(bk));
+    for (int i = 0; i < bk; ++i) expand[i] = uint32_t(i / k);
+    reset_state(*st, src, expand, uint32_t(cfg.decoder_start_token_id));
+    DevTemp tmp;
+    float *scratch = tmp.get<float>(logsoftmax_topk_scratch(bk, k) / 4, "topk scratch");
+    float *d_vals = tmp.get<float>(size_t(bk) * k, "topk vals");
+    uint32_t *d_idx = tmp.get<uint32_t>(size_t(bk) * k, "topk idx");
+    uint32_t *d_reorder = tmp.get<uint32_t>(size_t(bk), "reorder");
+    const size_t self_row = size_t(H) * st->m * hd * 2;
+    uint8_t *swap = tmp.get<uint8_t>(self_row * bk, "reorder scratch");
+
+    // [start, tgt_lang] fed one position at a time (equal to the t = 2 causal pass)
+    step(*st, false, mask_id);
+    check_hip(fill_u32(st->ids, tgt_lang, size_t(bk), s), "fill");
+    step(*st, false, mask_id);
+
+    struct Hyp {
+        float score;
+        std::vector<uint32_t> toks;
+    };
+    std::vector<std::vector<Hyp>> alive(static_cast<size_t>(b), std::vector<Hyp>{Hyp{0.f, {}}});
+    std::vector<std::vector<Hyp>> done(static_cast<size_t>(b));
+    std::vector<uint8_t> is_done(static_cast<size_t>(b), 0);
+    auto penalty = [&](size_t len) { return std::pow(float(std::max<size_t>(len, 1)), lp); };
+    std::vector<float> vals(static_cast<size_t>(bk) * k);
+    std::vector<uint32_t> idx(static_cast<size_t>(bk) * k);
+    for (int stp = 1; stp <= max_new; ++stp) {
+        check_hip(logsoftmax_topk(st->logits, bk, V, k, mask_id, scratch, d_vals, d_idx, s), "topk");
+        check_hip(hipMemcpyAsync(vals.data(), d_vals, vals.size() * 4, hipMemcpyDeviceToHost, s), "D2H");
+        check_hip(hipMemcpyAsync(idx.data(), d_idx, idx.size() * 4, hipMemcpyDeviceToHost, s), "D2H");
+        check_hip(hipStreamSynchronize(s), "sync");
+        std::vector<uint32_t> reorder, next;
+        for (int sn = 0; sn < b; ++sn) {
+            struct Cand {
+                float score;
+                int bi;
+                uint32_t tok;
+            };
+            std::vector<Cand> cands;
+            for (int bi = 0; bi < int(alive[sn].size()); ++bi) {
+                const int row = sn * k + bi;
+                for (int j = 0; j < k; ++j)
+                    cands.push_back({alive[sn][bi].score + vals[size_t(row) * k + j], bi, idx[size_t(row) * k + j]});
+            }
+            std::stable_sort(cands.begin(), cands.end(), [](const Cand &a, const Cand &c) { return a.score > c.score; });
+            std::vector<Hyp> new_alive;
+            for (auto &cd : cands) {
+                if (int(new_alive.size()) == k) break;
+                std::vector<uint32_t> toks = alive[sn][cd.bi].toks;
+                if (cd.tok == eos || stp == max_new) {
+                    if (cd.tok != eos) toks.push_back(cd.tok);
+                    const size_t len = toks.size() + 1;
+                    if (!is_done[sn]) done[sn].push_back({cd.score / penalty(len), toks});
+                    continue;
+                }
+                toks.push_back(cd.tok);
+                reorder.push_back(uint32_t(sn * k + cd.bi));
+                next.push_back(cd.tok);
+                new_alive.push_back({cd.score, std::move(toks)});
+            }
+            float best_done = -INFINITY;
+            for (auto &h : done[sn]) best_done = std::max(best_done, h.score);
+            const float best_alive = new_alive.empty() ? -INFINITY : new_alive[0].score / penalty(size_t(stp) + 1);
+            if (int(done[sn].size()) >= k && best_done >= best_alive) is_done[sn] = 1;
+            while (int(new_alive.size()) < k) {
+                reorder.push_back(uint32_t(sn * k));
+                next.push_back(eos);
+                new_alive.push_back({-INFINITY, {}});
+            }
+            alive[sn] = std::move(new_alive);
+        }
+        if (stp == max_new || std::all_of(is_done.begin(), is_done.end(), [](uint8_t v) { return v != 0; })) break;
+        // src/model.rs:209-226: gather the self-attention caches by beam.  Cross K/V and
+        // lens are identical within a sentence's beams, and reorder never leaves a sentence.
+        h2d(d_reorder, reorder, s);
+        for (size_t l = 0; l < st->kc.size(); ++l) {
+            for (__half *buf : {st->kc[l], st->vc[l]}) {
+                check_hip(gather_rows(buf, swap, d_reorder, bk, self_row, s), "reorder");
+                check_hip(hipMemcpyAsync(buf, swap, self_row * bk, hipMemcpyDeviceToDevice, s), "reorder");
+            }
+        }
+        h2d(st->ids, next, s);
+        step(*st, false, mask_id);
+    }
+    std::vector<std::vector<uint32_t>> res(static_cast<size_t>(b));
+    for (int sn = 0; sn < b; ++sn) {
+        const auto &list = done[sn].empty() ? alive[sn] : done[sn];
+        int best = -1;
+        for (int i = 0; i < int(list.size()); ++i)  // Iterator::max_by keeps the last maximum
+            if (best < 0 || !(list[i].score < list[best].score)) best = i;
+        if (best >= 0) res[sn] = list[best].toks;
+    }
+    return res;
+}
+
+std::vector<float> Model::teacher_forced(const Batch &src, const std::vector<uint32_t> &tgt, int T) {
+    hipStream_t s = ctx->stream;
+    const int b = src.b, V = cfg.vocab_size;
+    if (T < 1 || int(tgt.size()) != b * T) fail(ERR_INVALID, "teacher_forced: bad target shape");
+    if (T + cfg.pad_token_id + 1 >= n_pos) fail(ERR_INVALID, "teacher_forced: sequence longer than the position table");
+    for (uint32_t t : tgt)
+        if (t >= uint32_t(V)) fail(ERR_INVALID, "token id out of range");
+    auto st = new_state(b, src.s, T, true);
+    std::vector<uint32_t> rows(static_cast<size_t>(b));
+    std::iota(rows.begin(), rows.end(), 0u);
+    reset_state(*st, src, rows, tgt[0]);
+    std::vector<float> out(size_t(b) * T * V);
+    std::vector<uint32_t> ids(static_cast<size_t>(b));
+    for (int t = 0; t < T; ++t) {
+        for (int i = 0; i < b; ++i) ids[i] = tgt[size_t(i) * T + t];
+        h2d(st->ids, ids, s);
+        step(*st, false, -1);
+        for (int i = 0; i < b; ++i)
+            check_hip(hipMemcpyAsync(out.data() + (size_t(i) * T + t) * V, st->logits + size_t(i) * V, size_t(V) * 4,
+                                     hipMemcpyDeviceToHost, s),
+                      "D2H");
+        check_hip(hipStreamSynchronize(s), "sync");
+    }
+    return out;
+}
+
+// -------------------------------------------------------------- translator
+
+std::vector<std::vector<uint32_t>> generate_to(Model &m, const std::vector<std::vector<uint32_t>> &src,
+                                               uint32_t tgt_lang, const GenOptions &o) {
+    if (src.empty()) return {};
+    int max_new = 1;
+    for (auto &r : src) max_new = std::max(max_new, budget(m.cfg, int(r.size()), o.max_new_tokens));
+    auto batch = m.encode(src);
+    std::vector<std::vector<uint32_t>> out;
+    if (o.beam_size <= 1)
+        out = m.graphs.greedy(*batch, tgt_lang, max_new, std::max(1, o.sync_every), o.eos_mask, o.fused);
+    else
+        out = m.beam(*batch, tgt_lang, max_new, o.beam_size, o.length_penalty, o.eos_mask);
+    for (size_t i = 0; i < src.size(); ++i) {
+        const size_t bud = size_t(budget(m.cfg, int(src[i].size()), o.max_new_tokens));
+        if (out[i].size() > bud) out[i].resize(bud);
+    }
+    return out;
+}
+
+std::vector<std::vector<uint32_t>> generate(Model &m, const std::vector<std::vector<uint32_t>> &src, uint32_t tgt_lang,
+                                            const GenOptions &o) {
+    std::vector<size_t> order(src.size());
+    std::iota(order.begin(), order.end(), size_t(0));
+    std::stable_sort(order.begin(), order.end(), [&](size_t a, size_t b) { return src[a].size() > src[b].size(); });
+    std::vector<std::vector<uint32_t>> out(src.size());
+    int max_batch = std::max(1, o.max_batch);
+    size_t done = 0;
+    while (done < order.size()) {
+        const size_t end = std::min(order.size(), done + size_t(max_batch));
+        std::vector<std::vector<uint32_t>> batch;
+        for (size_t i = done; i < end; ++i) batch.push_back(src[order[i]]);
+        std::vector<std::vector<uint32_t>> ids;
+        try {
+            ids = generate_to(m, batch, tgt_lang, o);
+        } catch (const Failure &f) {
+            // src/translator.rs:150-158: free cached buffers, retry with smaller batches
+            if (f.code == ERR_OOM && max_batch > 1) {
+                max_batch /= 2;
+                m.graphs.clear();
+                continue;
+            }
+            throw;
+        }
+        for (size_t i = done; i < end; ++i) out[order[i]] = std::move(ids[i - done]);
+        done = end;
+    }
+    return out;
+}
+
+}  // namespace mlg

@@ -1,0 +1,178 @@
+// Decode runtime on one MI355X: weights in HBM, the encoder, the fixed-shape
+// decoder state replayed as a hipGraph (src/graph.rs), greedy and beam drivers
+// (src/translator.rs), and the translate_batch batching policy.
+#pragma once
+#include <hip/hip_fp16.h>
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+#include <list>
+#include <memory>
+#include <mutex>
+#include <string>
+#include <vector>
+
+#include "convert.hpp"
+#include "kernels.hpp"
+
+namespace mlg {
+
+// Status codes of the C ABI (include/malaga_hip.h).
+enum Status : int { OK = 0, ERR_INVALID = 1, ERR_OOM = 2, ERR_HIP = 3, ERR_IO = 4, ERR_FORMAT = 5,
+                    ERR_UNSUPPORTED = 6, ERR_NO_DEVICE = 7 };
+
+struct Failure {
+    int code;
+    std::string msg;
+};
+
+// Device allocation with out-of-memory reporting ("OUT_OF_MEMORY" in the message,
+// which is what src/graph.rs:215 and src/translator.rs:338-340 match on) and a
+// test hook that makes the n-th allocation fail.
+void *dev_alloc(size_t bytes, const char *what);
+void dev_free(void *p);
+void set_fail_alloc_after(long n);  // < 0 disables
+
+struct Context {
+    int device = 0;
+    hipStream_t stream = nullptr;
+    std::mutex mu;  // one caller at a time per context (src/graph.rs:152-155)
+};
+
+struct Linear {
+    DevMatrix w;
+    float *b = nullptr;
+};
+struct LNorm {
+    float *g = nullptr, *b = nullptr;
+};
+struct EncLayer {
+    LNorm attn_norm, ffn_norm;
+    Linear qkv, out, up, down;
+};
+struct DecLayer {
+    LNorm attn_norm, cross_norm, ffn_norm;
+    Linear qkv, out, cross_q, cross_kv, cross_out, up, down;
+};
+
+// Encoded sources: per decoder layer cross K/V [b][H][s][hd] f16 (src/model.rs:463-477).
+struct Batch {
+    int b = 0, s = 0;
+    std::vector<uint32_t> lens;
+    std::vector<__half *> ck, cv;
+    ~Batch();
+};
+
+// src/graph.rs:23-49
+struct StaticState {
+    int b = 0, s = 0, m = 0;
+    uint32_t *ids = nullptr, *step = nullptr, *lens = nullptr, *out = nullptr;
+    uint8_t *finished = nullptr;
+    std::vector<__half *> kc, vc, ck, cv;
+    // workspace (nothing is allocated inside a step)
+    float *x = nullptr, *h = nullptr, *y = nullptr, *att = nullptr, *q = nullptr, *qkv = nullptr, *u = nullptr;
+    float *logits = nullptr, *pv = nullptr;
+    uint32_t *pi = nullptr;
+    int parts = 0;
+    size_t bytes = 0;
+    std::vector<void *> owned;
+    ~StaticState();
+};
+
+class Model;
+
+// src/graph.rs:149-335: bucketed static states + captured step graphs, LRU by bytes.
+class GraphCache {
+  public:
+    explicit GraphCache(Model *m);
+    ~GraphCache();
+    bool capture_enabled() const { return capture_; }
+    void clear();
+    // Greedy decoding of an encoded batch; rows stripped at EOS (src/graph.rs:204-298).
+    std::vector<std::vector<uint32_t>> greedy(const Batch &src, uint32_t tgt_lang, int max_new, int sync_every,
+                                              bool eos_mask, bool use_graph);
+    size_t entries() const { return entries_.size(); }
+    size_t graphs() const;
+
+  private:
+    struct Entry {
+        int b, s, m;
+        std::unique_ptr<StaticState> st;
+        hipGraphExec_t exec = nullptr;
+        uint64_t last_used = 0;
+        size_t bytes() const;
+    };
+    std::vector<std::vector<uint32_t>> run(const Batch &src, uint32_t tgt_lang, int max_new, int sync_every,
+                                           bool eos_mask, bool use_graph);
+    void evict(const Entry *keep);
+    Model *model_;
+    std::list<Entry> entries_;
+    uint64_t clock_ = 0;
+    size_t max_bytes_;
+    bool capture_;
+};
+
+class Model {
+  public:
+    Model(Context *ctx) : ctx(ctx), graphs(this) {}
+    ~Model();
+    void load(const std::string &path);  // throws Failure
+
+    Context *ctx;
+    ModelConfig cfg;
+    DevMatrix embed;  // token_embd, also the tied LM head
+    float *pos = nullptr;
+    int n_pos = 0;
+    float embed_scale = 1.f;
+    std::vector<EncLayer> enc;
+    std::vector<DecLayer> dec;
+    LNorm enc_norm, dec_norm;
+    size_t weight_bytes = 0;
+    GraphCache graphs;
+
+    // src/model.rs:463-500 (encoder + cross K/V of every decoder layer)
+    std::unique_ptr<Batch> encode(const std::vector<std::vector<uint32_t>> &src);
+    std::unique_ptr<StaticState> new_state(int b, int s, int m, bool beam);
+    // src/model.rs:552-612: one decoder step on fixed buffers.  greedy: argmax +
+    // bookkeeping, else logits into st.logits and ++step.
+    void step(StaticState &st, bool greedy, int mask_id);
+    void reset_state(StaticState &st, const Batch &src, const std::vector<uint32_t> &row_of, uint32_t start);
+    // src/translator.rs:250-335
+    std::vector<std::vector<uint32_t>> beam(const Batch &src, uint32_t tgt_lang, int max_new, int k, float lp,
+                                            bool eos_mask);
+    // Logits after feeding tgt[:, t] at position t, for t < T: [b][T][V] (parity tests).
+    std::vector<float> teacher_forced(const Batch &src, const std::vector<uint32_t> &tgt, int T);
+
+  private:
+    std::vector<void *> owned_;
+    Linear load_linear(class GgufFile &g, const std::string &name, int n, int k);
+    LNorm load_ln(class GgufFile &g, const std::string &name, int d);
+    float *upload_f32(class GgufFile &g, const std::string &name, int64_t n);
+    DevMatrix upload_matrix(class GgufFile &g, const std::string &name, int n, int k);
+    void matmul(const Linear &l, const float *x, int rows, float *y, bool relu, const float *resid);
+};
+
+void check_hip(hipError_t e, const char *what);  // throws Failure
+
+struct GenOptions {
+    int beam_size = 1;
+    int max_new_tokens = 0;  // 0 = 2*len + 16
+    float length_penalty = 1.f;
+    int sync_every = 4;
+    int max_batch = 32;
+    bool fused = true;
+    bool eos_mask = false;  // benchmark-only: fixed output lengths
+};
+
+// src/translator.rs:136-207 on token ids: sort by length, batch, per-row budget,
+// OOM batch halving.  Output order matches input order.
+std::vector<std::vector<uint32_t>> generate(Model &m, const std::vector<std::vector<uint32_t>> &src, uint32_t tgt_lang,
+                                            const GenOptions &o);
+// One batch (src/translator.rs:175-207).
+std::vector<std::vector<uint32_t>> generate_to(Model &m, const std::vector<std::vector<uint32_t>> &src,
+                                               uint32_t tgt_lang, const GenOptions &o);
+int budget(const ModelConfig &c, int len, int max_new_tokens);
+// src/graph.rs:138-140
+int bucket(int n, int min, int max);
+
+}  // namespace mlg

@@ -1,0 +1,206 @@
+"""Kernel-level parity through the C ABI (device buffers from torch, plain pointers in)."""
+import ctypes as C
+
+import numpy as np
+import pytest
+import torch
+
+import malaga_amd as M
+import oracle as O
+from malaga_amd import _lib
+
+pytestmark = pytest.mark.gpu
+F32, F16, Q8_0, Q4_K, Q5_K, Q6_K = 0, 1, 8, 12, 13, 14
+
+
+@pytest.fixture(scope="module")
+def ctx():
+    return M._Ctx(0)
+
+
+def dev(a):
+    return torch.from_numpy(np.ascontiguousarray(a)).cuda()
+
+
+def ptr(t):
+    return C.c_void_p(t.data_ptr())
+
+
+def upload(ctx, t, blocks, N, K):
+    h = C.c_void_p()
+    _lib.check(ctx.lib.mlg_matrix_upload(ctx.h, t, N, K, blocks.ctypes.data, C.byref(h)))
+    return h
+
+
+def bound(x, w):
+    """|y| error scale: sum_k |x_k| |w_nk| (float64)."""
+    return np.abs(x.astype(np.float64)) @ np.abs(w.astype(np.float64)).T
+
+
+CASES = [(t, N, K) for t in (Q4_K, Q5_K, Q6_K, Q8_0) for (N, K) in ((3072, 1024), (1024, 4096), (517, 256))] + \
+        [(F16, 192, 64), (F32, 192, 64), (F16, 130, 128), (F32, 128, 128)]
+
+
+@pytest.mark.parametrize("t,N,K", CASES)
+def test_gemv_matches_dequantized_dot(ctx, t, N, K):
+    rng = np.random.default_rng(N + K + t)
+    wf = rng.normal(0, 0.02, (N, K)).astype(np.float32)
+    blocks = M.quantize(t, wf)
+    w = upload(ctx, t, blocks, N, K)
+    try:
+        wd = O.dequant(t, blocks, N * K).reshape(N, K)
+        maxb = ctx.lib.mlg_gemv_max_batch(w)
+        assert maxb >= 1
+        for b in sorted({1, maxb}):
+            x = rng.normal(0, 1, (b, K)).astype(np.float32)
+            bias = rng.normal(0, 0.1, N).astype(np.float32)
+            xd, yd, bd = dev(x), torch.zeros((b, N), device="cuda"), dev(bias)
+            _lib.check(ctx.lib.mlg_gemv(w, ptr(xd), b, ptr(yd), ptr(bd), 0, None))
+            torch.cuda.synchronize()
+            ref = O.gemv(t, blocks, N, K, x) + bias
+            err = np.abs(yd.cpu().numpy() - ref)
+            assert (err <= 2e-6 * bound(x, wd) + 1e-6).all(), (b, err.max())
+            # relu epilogue
+            _lib.check(ctx.lib.mlg_gemv(w, ptr(xd), b, ptr(yd), ptr(bd), 1, None))
+            torch.cuda.synchronize()
+            assert (yd.cpu().numpy() >= 0).all()
+    finally:
+        ctx.lib.mlg_matrix_free(w)
+
+
+@pytest.mark.parametrize("t,N,K", [(Q4_K, 1000, 1024), (Q6_K, 300, 512), (Q8_0, 256, 1024), (F32, 96, 64)])
+def test_gemm_matches_dequantized_dot(ctx, t, N, K):
+    rng = np.random.default_rng(7 + t)
+    wf = rng.normal(0, 0.02, (N, K)).astype(np.float32)
+    blocks = M.quantize(t, wf)
+    w = upload(ctx, t, blocks, N, K)
+    try:
+        wd = O.dequant(t, blocks, N * K).reshape(N, K)
+        for M_ in (1, 37, 70):
+            x = rng.normal(0, 1, (M_, K)).astype(np.float32)
+            xd, yd = dev(x), torch.zeros((M_, N), device="cuda")
+            _lib.check(ctx.lib.mlg_gemm(w, ptr(xd), M_, ptr(yd), None, 0, None))
+            torch.cuda.synchronize()
+            ref = O.gemv(t, blocks, N, K, x)
+            assert (np.abs(yd.cpu().numpy() - ref) <= 2e-6 * bound(x, wd) + 1e-6).all()
+    finally:
+        ctx.lib.mlg_matrix_free(w)
+
+
+@pytest.mark.parametrize("t", [Q6_K, Q4_K, Q8_0])
+def test_gemv_argmax_lowest_index_on_ties(ctx, t):
+    rng = np.random.default_rng(99)
+    N, K = 20000, 1024
+    wf = rng.normal(0, 0.02, (N, K)).astype(np.float32)
+    wf[7777] = wf[12345] = wf[19999] = wf[3] * 0 + rng.normal(0, 0.5, K).astype(np.float32)  # dominant, tied rows
+    blocks = M.quantize(t, wf)
+    w = upload(ctx, t, blocks, N, K)
+    try:
+        b = ctx.lib.mlg_gemv_max_batch(w)
+        x = np.tile(np.abs(rng.normal(0, 1, K)).astype(np.float32) * np.sign(wf[7777]), (b, 1))
+        parts = ctx.lib.mlg_gemv_argmax_parts(w, b)
+        xd = dev(x)
+        pv = torch.zeros((b, parts), device="cuda")
+        pi = torch.zeros((b, parts), dtype=torch.int32, device="cuda")
+        _lib.check(ctx.lib.mlg_gemv_argmax(w, ptr(xd), b, -1, ptr(pv), ptr(pi), None))
+        torch.cuda.synchronize()
+        v, i = pv.cpu().numpy(), pi.cpu().numpy().view(np.uint32)
+        for r in range(b):
+            k = np.argmax(v[r])  # first max over parts; parts cover increasing row ranges
+            best = v[r].max()
+            assert i[r][v[r] == best].min() == 7777
+        # mask the winner's index: the next tied row wins
+        _lib.check(ctx.lib.mlg_gemv_argmax(w, ptr(xd), b, 7777, ptr(pv), ptr(pi), None))
+        torch.cuda.synchronize()
+        v, i = pv.cpu().numpy(), pi.cpu().numpy().view(np.uint32)
+        assert i[0][v[0] == v[0].max()].min() == 12345
+    finally:
+        ctx.lib.mlg_matrix_free(w)
+
+
+def test_residual_layernorm(ctx):
+    rng = np.random.default_rng(1)
+    for rows, d in ((1, 1024), (5, 2048), (3, 64)):
+        x = rng.normal(0, 3, (rows, d)).astype(np.float32)
+        y = rng.normal(0, 1, (rows, d)).astype(np.float32)
+        g = rng.normal(1, 0.1, d).astype(np.float32)
+        b = rng.normal(0, 0.1, d).astype(np.float32)
+        xd, yd, gd, bd, hd = dev(x), dev(y), dev(g), dev(b), torch.zeros((rows, d), device="cuda")
+        _lib.check(ctx.lib.mlg_residual_ln(ptr(xd), ptr(yd), rows, d, ptr(gd), ptr(bd), C.c_float(1e-5), ptr(hd), None))
+        torch.cuda.synchronize()
+        s = x.astype(np.float64) + y
+        np.testing.assert_allclose(xd.cpu().numpy(), (x + y), rtol=0, atol=0)
+        mu, var = s.mean(1, keepdims=True), s.var(1, keepdims=True)
+        ref = (s - mu) / np.sqrt(var + 1e-5) * g + b
+        np.testing.assert_allclose(hd.cpu().numpy(), ref, atol=2e-5, rtol=0)
+
+
+def test_attention_decode(ctx):
+    rng = np.random.default_rng(2)
+    b, H, hd, L = 3, 16, 64, 100
+    q = rng.normal(0, 1, (b, H, hd)).astype(np.float32)
+    K = rng.normal(0, 1, (b, H, L, hd)).astype(np.float16)
+    V = rng.normal(0, 1, (b, H, L, hd)).astype(np.float16)
+    lens = np.array([1, 37, 100], dtype=np.uint32)
+    qd, kd, vd, ld, od = dev(q), dev(K), dev(V), dev(lens.view(np.int32)), torch.zeros((b, H * hd), device="cuda")
+    _lib.check(ctx.lib.mlg_attn_decode(ptr(qd), ptr(kd), ptr(vd), b, H, hd, L, ptr(ld), None, ptr(od), None))
+    torch.cuda.synchronize()
+    out = od.cpu().numpy().reshape(b, H, hd)
+    for i in range(b):
+        n = lens[i]
+        s = np.einsum("hd,hld->hl", q[i].astype(np.float64), K[i, :, :n].astype(np.float64))
+        p = np.exp(s - s.max(1, keepdims=True))
+        p /= p.sum(1, keepdims=True)
+        ref = np.einsum("hl,hld->hd", p, V[i, :, :n].astype(np.float64))
+        np.testing.assert_allclose(out[i], ref, atol=2e-5, rtol=0)
+    # self-attention length from the device step counter: n = step + 1
+    step = dev(np.array([36], dtype=np.int32))
+    _lib.check(ctx.lib.mlg_attn_decode(ptr(qd), ptr(kd), ptr(vd), b, H, hd, L, None, ptr(step), ptr(od), None))
+    torch.cuda.synchronize()
+    np.testing.assert_allclose(od.cpu().numpy().reshape(b, H, hd)[1], out[1], atol=1e-6)
+
+
+def test_logsoftmax_topk(ctx):
+    rng = np.random.default_rng(3)
+    rows, V, k = 6, 256206, 4
+    x = rng.normal(0, 1, (rows, V)).astype(np.float32)
+    x[2, 100] = x[2, 50] = x[2, 7000] = 9.0  # ties -> lowest index first
+    xd = dev(x)
+    scratch = torch.zeros(ctx.lib.mlg_logsoftmax_topk_scratch(rows, k) // 4 + 1, device="cuda")
+    vals = torch.zeros((rows, k), device="cuda")
+    idx = torch.zeros((rows, k), dtype=torch.int32, device="cuda")
+    for mask in (-1, 2):
+        _lib.check(ctx.lib.mlg_logsoftmax_topk(ptr(xd), rows, V, k, mask, ptr(scratch), ptr(vals), ptr(idx), None))
+        torch.cuda.synchronize()
+        xx = x.astype(np.float64).copy()
+        if mask >= 0:
+            xx[:, mask] = -np.inf
+        lse = np.log(np.exp(xx - xx.max(1, keepdims=True)).sum(1)) + xx.max(1)
+        order = np.lexsort((np.tile(np.arange(V), (rows, 1)), -xx), axis=1)[:, :k]
+        np.testing.assert_array_equal(idx.cpu().numpy(), order)
+        np.testing.assert_allclose(vals.cpu().numpy(), np.take_along_axis(xx, order, 1) - lse[:, None], atol=2e-5)
+    assert idx.cpu().numpy()[2, :3].tolist() == [50, 100, 7000]
+
+
+def test_greedy_finalize_bookkeeping(ctx):
+    """kernels/malaga.cu:290-326: tok = finished ? pad : argmax; finished |= tok == eos; out[:, step]; ++step."""
+    b, P, m = 4, 8, 10
+    pv = np.full((b, P), -1.0, np.float32)
+    pi = np.zeros((b, P), np.uint32)
+    pv[0, 3], pi[0, 3] = 5.0, 42
+    pv[1, 2], pi[1, 2] = 5.0, 2      # eos
+    pv[2, 1], pi[2, 1] = 7.0, 9
+    pv[2, 5], pi[2, 5] = 7.0, 8      # tie -> lower index 8
+    pv[3, 0], pi[3, 0] = 1.0, 77     # already finished -> pad
+    fin = np.array([0, 0, 0, 1], np.uint8)
+    pvd, pid, find = dev(pv), dev(pi.view(np.int32)), dev(fin)
+    ids = torch.zeros(b, dtype=torch.int32, device="cuda")
+    out = torch.zeros((b, m), dtype=torch.int32, device="cuda")
+    step = dev(np.array([3], np.int32))
+    _lib.check(ctx.lib.mlg_greedy_finalize(ptr(pvd), ptr(pid), P, b, ptr(find), ptr(ids), ptr(out), m, ptr(step),
+                                           2, 1, None))
+    torch.cuda.synchronize()
+    assert ids.cpu().tolist() == [42, 2, 8, 1]
+    assert out.cpu().numpy()[:, 3].tolist() == [42, 2, 8, 1]
+    assert find.cpu().tolist() == [0, 1, 0, 1]
+    assert step.cpu().tolist() == [4]
