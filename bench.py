@@ -1,0 +1,357 @@
+#!/usr/bin/env python3
+"""Benchmark of the MI355X decode path on BASELINE.json's configurations.
+
+Headline (``value``): config 3 -- NLLB-600M q4_k_m (random init, seed 0), batch 1,
+32 random source ids, 48 greedy tokens with EOS masked, p50 ms per sentence
+(encode + 49 decoder steps replayed as a hipGraph).  One "step" is one sentence.
+
+Also reported on the same JSON line:
+  * p99, encoder ms, decoder ms/token, and the reference's own bench shape
+    (21 source ids -> 18 tokens, crates/malaga/src/main.rs:409-436);
+  * config 4: greedy batch 32 (lognormal lengths, length-sorted) and beam 4 at
+    batch 8, sentences/s;
+  * config 2: dequant-GEMV GB/s (q4_K, q8_0; four shapes) over rotating weight
+    copies (> 2x the 256 MB Infinity Cache), LayerNorm and argmax latency;
+  * ``roofline`` of the dominant kernel (the fused LM-head GEMV + argmax, q6_K
+    256206 x 1024, 66% of the step's bytes), timed with HIP events on the stream
+    it runs on;
+  * ``cpu_baseline``: the C restatement of the reference path (oracle/) on the
+    host cores, config 1 (600M q8_0, 32 ids, 32 greedy steps).
+
+Usage: python bench.py [--gpus 1] [--steps 200] [--warmup 3]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+import numpy as np
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+PEAK_HBM_GBS = 8000.0
+TGT_LANG = 256100  # any id < vocab: the forced target-language token
+
+
+def log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def model_path(preset: str) -> Path:
+    import malaga_amd as M
+
+    d = Path(os.environ.get("MALAGA_MODEL_DIR", "/tmp/malaga_bench_models"))
+    d.mkdir(parents=True, exist_ok=True)
+    p = d / f"nllb600m-random-s0-{preset}.gguf"
+    if not p.exists():
+        t = time.time()
+        M.write_synthetic(p, M.nllb_600m_config(), preset, M.INIT_NORMAL, seed=0, std=0.02,
+                          name="nllb-200-distilled-600M (random init, seed 0)")
+        log(f"wrote {p.name} ({p.stat().st_size / 1e6:.0f} MB) in {time.time() - t:.1f} s")
+    return p
+
+
+def sources(n: int, length: int, seed: int) -> list[list[int]]:
+    """Seeded random source ids U[4, 256206) (raw ids, no language/eos framing)."""
+    return [np.random.default_rng(seed + i).integers(4, 256206, length).tolist() for i in range(n)]
+
+
+def lognormal_lengths(n: int, mean: float, lo: int, hi: int, seed: int) -> list[int]:
+    sigma = 0.5
+    mu = np.log(mean) - sigma ** 2 / 2
+    v = np.random.default_rng(seed).lognormal(mu, sigma, n)
+    return np.clip(np.rint(v), lo, hi).astype(int).tolist()
+
+
+def bench_bs1(T, steps: int, warmup: int):
+    import torch
+    import malaga_amd as M
+
+    opts = M.GenOptions(max_new_tokens=48, eos_mask=True)
+    src = sources(steps + warmup, 32, seed=1000)
+    for s in src[:warmup]:
+        T.generate([s], TGT_LANG, opts)
+    torch.cuda.synchronize()
+    lat = []
+    t0 = time.perf_counter()
+    for s in src[warmup:]:
+        a = time.perf_counter()
+        out = T.generate([s], TGT_LANG, opts)
+        lat.append((time.perf_counter() - a) * 1e3)
+        assert len(out[0]) == 48
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    # encoder alone (src/model.rs:463-477), as main.rs:426-433 measures it
+    enc = []
+    for s in src[warmup: warmup + 50]:
+        a = time.perf_counter()
+        b = T.encode_cross([s])
+        torch.cuda.synchronize()
+        enc.append((time.perf_counter() - a) * 1e3)
+        del b
+    lat = np.array(lat)
+    p50, p99 = float(np.percentile(lat, 50)), float(np.percentile(lat, 99))
+    enc_ms = float(np.median(enc))
+    # the reference's bench shape: 21 source ids -> 18 target tokens
+    ref_opts = M.GenOptions(max_new_tokens=18, eos_mask=True)
+    ref_src = sources(50, 21, seed=5000)
+    ref_lat = []
+    for s in ref_src:
+        a = time.perf_counter()
+        T.generate([s], TGT_LANG, ref_opts)
+        ref_lat.append((time.perf_counter() - a) * 1e3)
+    ref_p50 = float(np.median(ref_lat))
+    return dict(p50=p50, p99=p99, mean=float(lat.mean()), wall_s=wall, encoder_ms=enc_ms,
+                ms_per_token=(p50 - enc_ms) / 49.0, ref_p50=ref_p50, ref_ms_per_token=(ref_p50 - enc_ms) / 19.0)
+
+
+def bench_batched(T):
+    import torch
+    import malaga_amd as M
+
+    lens = lognormal_lengths(32, 28, 4, 128, seed=0)
+    rng = np.random.default_rng(77)
+    src = [rng.integers(4, 256206, n).tolist() for n in lens]
+    res = {}
+    for name, batch, opts in (("greedy_bs32", src, M.GenOptions(eos_mask=True, max_batch=32)),
+                              ("beam4_bs8", src[:8], M.GenOptions(beam_size=4, eos_mask=True, max_batch=8))):
+        T.generate(batch, TGT_LANG, opts)  # warm-up (graph capture, buffers)
+        torch.cuda.synchronize()
+        times = []
+        for _ in range(3):
+            a = time.perf_counter()
+            out = T.generate(batch, TGT_LANG, opts)
+            torch.cuda.synchronize()
+            times.append(time.perf_counter() - a)
+        dt = float(np.median(times))
+        toks = sum(len(r) for r in out)
+        res[name] = dict(sentences_per_s=len(batch) / dt, ms_per_batch=dt * 1e3, tokens=toks,
+                         max_src_len=max(len(s) for s in batch), tokens_per_s=toks / dt)
+    return res
+
+
+class GemvBench:
+    """Times one kernel-level entry point over rotating device copies of a weight matrix."""
+
+    def __init__(self, ctx):
+        import torch
+
+        self.ctx, self.lib = ctx, ctx.lib
+        self.stream = torch.cuda.Stream()
+
+    def run(self, gguf_type: int, blocks: np.ndarray, N: int, K: int, launches: int = 60, argmax: bool = False):
+        import ctypes as C
+        import torch
+        from malaga_amd import _lib
+
+        nbytes = blocks.nbytes
+        copies = max(2, int(np.ceil(1.1e9 / nbytes)))  # > 4x the 256 MB Infinity Cache
+        mats = []
+        for _ in range(copies):
+            h = C.c_void_p()
+            _lib.check(self.lib.mlg_matrix_upload(self.ctx.h, gguf_type, N, K, blocks.ctypes.data, C.byref(h)))
+            mats.append(h)
+        x = torch.randn(1, K, device="cuda")
+        y = torch.zeros(1, N, device="cuda")
+        parts = self.lib.mlg_gemv_argmax_parts(mats[0], 1)
+        pv = torch.zeros(parts, device="cuda")
+        pi = torch.zeros(parts, dtype=torch.int32, device="cuda")
+        sp = C.c_void_p(self.stream.cuda_stream)
+        xp, yp = C.c_void_p(x.data_ptr()), C.c_void_p(y.data_ptr())
+
+        def launch(m):
+            if argmax:
+                return self.lib.mlg_gemv_argmax(m, xp, 1, -1, C.c_void_p(pv.data_ptr()), C.c_void_p(pi.data_ptr()), sp)
+            return self.lib.mlg_gemv(m, xp, 1, yp, None, 0, sp)
+
+        torch.cuda.synchronize()
+        with torch.cuda.stream(self.stream):
+            for i in range(2 * copies):
+                _lib.check(launch(mats[i % copies]))
+            start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            start.record(self.stream)
+            for i in range(launches):
+                _lib.check(launch(mats[i % copies]))
+            end.record(self.stream)
+        end.synchronize()
+        us = start.elapsed_time(end) * 1e3 / launches
+        for m in mats:
+            self.lib.mlg_matrix_free(m)
+        out_bytes = parts * 8 if argmax else N * 4
+        alg = nbytes + K * 4 + out_bytes
+        return dict(us=us, bytes=alg, GBps=alg / us / 1e3, copies=copies)
+
+
+def bench_kernels(T, lm_blocks: np.ndarray):
+    import ctypes as C
+    import torch
+    import malaga_amd as M
+    from malaga_amd import _lib
+
+    gb = GemvBench(T._ctx)
+    rng = np.random.default_rng(0)
+    shapes = [("qkv", 3072, 1024), ("ffn_up", 4096, 1024), ("ffn_down", 1024, 4096), ("lm_head", 256206, 1024)]
+    rows = []
+    for tname, t in (("q4_K", 12), ("q8_0", 8)):
+        for sname, N, K in shapes:
+            w = rng.normal(0, 0.02, (N, K)).astype(np.float32)
+            blocks = M.quantize(t, w)
+            del w
+            r = gb.run(t, blocks, N, K, launches=60 if N < 100000 else 30)
+            r.update(type=tname, shape=f"{N}x{K}", name=sname)
+            rows.append(r)
+            log(f"gemv {tname} {sname} {N}x{K}: {r['us']:.2f} us {r['GBps']:.0f} GB/s")
+    # the LM head the q4_k_m model actually runs: q6_K, fused argmax epilogue
+    lm = gb.run(14, lm_blocks, 256206, 1024, launches=40, argmax=True)
+    lm.update(type="q6_K", shape="256206x1024", name="lm_head_argmax")
+    rows.append(lm)
+    log(f"gemv_argmax q6_K lm_head: {lm['us']:.2f} us {lm['GBps']:.0f} GB/s")
+    # residual + LayerNorm on one 1024-d row, argmax over 256206 logits
+    lib = T.lib
+    d = 1024
+    x, y = torch.randn(1, d, device="cuda"), torch.randn(1, d, device="cuda")
+    g, b, h = torch.ones(d, device="cuda"), torch.zeros(d, device="cuda"), torch.zeros(1, d, device="cuda")
+    logits = torch.randn(1, 256206, device="cuda")
+    pv, pi = torch.zeros(64, device="cuda"), torch.zeros(64, dtype=torch.int32, device="cuda")
+    P = lambda t: C.c_void_p(t.data_ptr())  # noqa: E731
+    s = gb.stream
+    sp = C.c_void_p(s.cuda_stream)
+
+    def timed(fn, n=200):
+        with torch.cuda.stream(s):
+            for _ in range(10):
+                fn()
+            st, en = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            st.record(s)
+            for _ in range(n):
+                fn()
+            en.record(s)
+        en.synchronize()
+        return st.elapsed_time(en) * 1e3 / n
+
+    ln_us = timed(lambda: _lib.check(lib.mlg_residual_ln(P(x), P(y), 1, d, P(g), P(b), C.c_float(1e-5), P(h), sp)))
+
+    argmax_us = timed(lambda: _lib.check(lib.mlg_argmax_partial(P(logits), 1, 256206, -1, P(pv), P(pi), 64, sp)))
+    return rows, dict(residual_ln_1x1024_us=ln_us, argmax_partial_256206_us=argmax_us)
+
+
+def cpu_baseline():
+    """oracle/ (C restatement of the reference's generic path) on the host cores, config 1."""
+    import oracle as O
+
+    path = model_path("q8_0")
+    a = time.perf_counter()
+    m = O.Model(path)
+    load_s = time.perf_counter() - a
+    src = sources(1, 32, seed=9000)
+    a = time.perf_counter()
+    rows, _ = m.generate(src, TGT_LANG, max_new_tokens=32, eos_mask=True, kv_f16=False)
+    dt = time.perf_counter() - a
+    assert len(rows[0]) == 32
+    threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
+    return dict(value=dt * 1e3, unit="ms/sentence", cores=threads, kind="port",
+                ms_per_token=dt * 1e3 / 33, load_s=load_s,
+                sample="config 1: NLLB-600M q8_0 random init, 1 sentence x 32 source ids, 32 greedy steps "
+                       "(33 decoder passes, EOS masked); oracle/oracle.c, f64-accumulated, OpenMP"), path, src
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--skip-cpu", action="store_true")
+    ap.add_argument("--roofline-only", action="store_true", help="only the LM-head roofline leg (for rocprof)")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build targets one GPU: the decode path has no multi-GPU mode "
+                                   "(sentences shard across GPUs with zero exchange; see DESIGN.md)",
+                          "n_gpus": args.gpus}))
+        sys.exit(2)
+
+    import torch
+    import malaga_amd as M
+    from malaga_amd.gguf import tensor_bytes
+
+    q4 = model_path("q4_k_m")
+    lm_blocks, info = tensor_bytes(q4, "token_embd.weight")
+    assert info["type"] == 14
+    lm_blocks = np.ascontiguousarray(lm_blocks)
+    if args.roofline_only:
+        ctx = M._Ctx(0)
+        r = GemvBench(ctx).run(14, lm_blocks, 256206, 1024, launches=200, argmax=True)
+        print(json.dumps({"kernel": "lm_head gemv_argmax q6_K 256206x1024", **r}))
+        return
+
+    log("loading the model")
+    T = M.Translator.load(q4)
+    log(f"weights in HBM: {T.weight_bytes / 1e6:.1f} MB")
+    torch.cuda.synchronize()
+    b1 = bench_bs1(T, args.steps, args.warmup)
+    log(f"bs1: p50 {b1['p50']:.2f} ms p99 {b1['p99']:.2f} ms enc {b1['encoder_ms']:.2f} ms "
+        f"{b1['ms_per_token']:.3f} ms/token; ref shape {b1['ref_p50']:.2f} ms")
+    batched = bench_batched(T)
+    for k, v in batched.items():
+        log(f"{k}: {v['sentences_per_s']:.1f} sentences/s ({v['ms_per_batch']:.1f} ms/batch)")
+    gemv_rows, small = bench_kernels(T, lm_blocks)
+    lm = gemv_rows[-1]
+    roofline = dict(bound="hbm", achieved=round(lm["GBps"], 1), peak=PEAK_HBM_GBS, unit="GB/s",
+                    frac=round(lm["GBps"] / PEAK_HBM_GBS, 4), traffic=None,
+                    kernel="k_gemv<q6_K,B=1,argmax> (LM head 256206x1024 + fused argmax partials)",
+                    bytes_per_launch=lm["bytes"], us_per_launch=round(lm["us"], 3))
+    q4_lm = next(r for r in gemv_rows if r["type"] == "q4_K" and r["name"] == "lm_head")
+    cpu = None
+    if not args.skip_cpu:
+        log("cpu baseline (oracle, config 1)")
+        cpu, q8path, csrc = cpu_baseline()
+        T8 = M.Translator.load(q8path)
+        opts = M.GenOptions(max_new_tokens=32, eos_mask=True)
+        T8.generate(csrc, TGT_LANG, opts)
+        a = time.perf_counter()
+        for _ in range(20):
+            T8.generate(csrc, TGT_LANG, opts)
+        torch.cuda.synchronize()
+        cpu["gpu_same_workload_ms"] = (time.perf_counter() - a) * 1e3 / 20
+        log(f"cpu {cpu['value']:.0f} ms/sentence on {cpu['cores']} threads; gpu same workload "
+            f"{cpu['gpu_same_workload_ms']:.2f} ms")
+        T8.close()
+    line = {
+        "metric": "p50 ms/sentence 600M q4_k_m bs1",
+        "value": round(b1["p50"], 4),
+        "unit": "ms/sentence",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(b1["mean"], 4),
+        "higher_is_better": False,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic: random-init N(0,0.02) weights (seed 0) quantized to q4_k_m, seeded random token ids",
+        "config": {"workload": "config 3: NLLB-200-distilled-600M architecture, q4_k_m GGUF, batch 1, 32 source "
+                               "ids, 48 greedy tokens with EOS masked (49 hipGraph decoder steps)",
+                   "global_batch": 1, "seq_len": 32, "new_tokens": 48, "kv_cache": "f16"},
+        "p99_ms": round(b1["p99"], 4),
+        "encoder_ms": round(b1["encoder_ms"], 4),
+        "decoder_ms_per_token": round(b1["ms_per_token"], 4),
+        "reference_shape": {"src_ids": 21, "tokens": 18, "p50_ms": round(b1["ref_p50"], 4),
+                            "ms_per_token": round(b1["ref_ms_per_token"], 4),
+                            "published_rtx4090_ms": 16.4, "published_rtx4090_ms_per_token": 0.78},
+        "sentences_per_s_bs32": round(batched["greedy_bs32"]["sentences_per_s"], 2),
+        "batched": batched,
+        "gemv_HBM_GBps_q4K_lm_head": round(q4_lm["GBps"], 1),
+        "gemv": [{k: (round(v, 3) if isinstance(v, float) else v) for k, v in r.items()} for r in gemv_rows],
+        "small_kernels_us": {k: round(v, 3) for k, v in small.items()},
+        "roofline": roofline,
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,6 +1,9 @@
-"""Minimal GGUF v3 reader used by the tests (independent of the C++ reader)."""
+"""Minimal pure-Python GGUF v3 reader (metadata, tensor infos, raw tensor bytes).
+
+Independent of the C++ reader in csrc/gguf.cpp; used by tests and benchmarks."""
 from __future__ import annotations
 
+import mmap
 import struct
 from pathlib import Path
 
@@ -8,7 +11,8 @@ SCALAR = {0: "<B", 1: "<b", 2: "<H", 3: "<h", 4: "<I", 5: "<i", 6: "<f", 7: "<?"
 
 
 def read_gguf(path: str | Path):
-    data = Path(path).read_bytes()
+    with open(path, "rb") as f:
+        data = mmap.mmap(f.fileno(), 0, access=mmap.ACCESS_READ)
     pos = 0
 
     def take(fmt):
@@ -50,3 +54,18 @@ def read_gguf(path: str | Path):
     for t in tensors.values():
         t["data_start"] = start + t["offset"]
     return version, meta, tensors, data
+
+
+def tensor_bytes(path: str | Path, name: str) -> tuple[bytes, dict]:
+    """Raw GGUF bytes of one tensor and its info (ne, type)."""
+    import numpy as np
+
+    _, _, tensors, data = read_gguf(path)
+    t = tensors[name]
+    n = 1
+    for d in t["ne"]:
+        n *= d
+    from . import type_bytes
+
+    nb = type_bytes(t["type"], n)
+    return np.frombuffer(data, dtype=np.uint8, count=nb, offset=t["data_start"]), t

@@ -4,7 +4,7 @@ import pytest
 
 import malaga_amd as M
 from tests.conftest import KQ_CONFIG
-from tests.gguf_reader import read_gguf
+from malaga_amd.gguf import read_gguf
 
 F32, F16, Q8_0, Q4_K, Q5_K, Q6_K = 0, 1, 8, 12, 13, 14
 

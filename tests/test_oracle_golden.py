@@ -46,7 +46,7 @@ def test_f16_kv_rounding_changes_little(tiny_gguf):
 
 def test_xorshift_stream_matches_the_python_restatement(tiny_gguf):
     """First embedding values of the C++ testutil generator (F32 preset keeps them exact)."""
-    from tests.gguf_reader import read_gguf
+    from malaga_amd.gguf import read_gguf
 
     g, _ = golden_sources()
     _, meta, tensors, data = read_gguf(tiny_gguf("f32"))
