@@ -266,6 +266,8 @@ def main():
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--skip-cpu", action="store_true")
+    ap.add_argument("--legs", default="bs1,batched,kernels,cpu",
+                    help="comma-separated subset of bs1,batched,kernels,cpu (profiling runs)")
     ap.add_argument("--roofline-only", action="store_true", help="only the LM-head roofline leg (for rocprof)")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -288,6 +290,9 @@ def main():
         print(json.dumps({"kernel": "lm_head gemv_argmax q6_K 256206x1024", **r}))
         return
 
+    legs = set(args.legs.split(","))
+    if args.skip_cpu:
+        legs.discard("cpu")
     log("loading the model")
     T = M.Translator.load(q4)
     log(f"weights in HBM: {T.weight_bytes / 1e6:.1f} MB")
@@ -295,9 +300,15 @@ def main():
     b1 = bench_bs1(T, args.steps, args.warmup)
     log(f"bs1: p50 {b1['p50']:.2f} ms p99 {b1['p99']:.2f} ms enc {b1['encoder_ms']:.2f} ms "
         f"{b1['ms_per_token']:.3f} ms/token; ref shape {b1['ref_p50']:.2f} ms")
-    batched = bench_batched(T)
+    if "bs1" in legs and len(legs) == 1:
+        print(json.dumps({"p50_ms": b1["p50"], "encoder_ms": b1["encoder_ms"], "ms_per_token": b1["ms_per_token"]}))
+        return
+    batched = bench_batched(T) if "batched" in legs else {"greedy_bs32": {"sentences_per_s": float("nan")}}
     for k, v in batched.items():
-        log(f"{k}: {v['sentences_per_s']:.1f} sentences/s ({v['ms_per_batch']:.1f} ms/batch)")
+        log(f"{k}: {v['sentences_per_s']:.1f} sentences/s ({v.get('ms_per_batch', 0):.1f} ms/batch)")
+    if "kernels" not in legs:
+        print(json.dumps({"p50_ms": b1["p50"], "batched": batched}))
+        return
     gemv_rows, small = bench_kernels(T, lm_blocks)
     lm = gemv_rows[-1]
     roofline = dict(bound="hbm", achieved=round(lm["GBps"], 1), peak=PEAK_HBM_GBS, unit="GB/s",
@@ -306,7 +317,7 @@ def main():
                     bytes_per_launch=lm["bytes"], us_per_launch=round(lm["us"], 3))
     q4_lm = next(r for r in gemv_rows if r["type"] == "q4_K" and r["name"] == "lm_head")
     cpu = None
-    if not args.skip_cpu:
+    if "cpu" in legs:
         log("cpu baseline (oracle, config 1)")
         cpu, q8path, csrc = cpu_baseline()
         T8 = M.Translator.load(q8path)

@@ -12,11 +12,27 @@ __device__ __forceinline__ float h2f(uint32_t bits16) {
     return __half2float(__ushort_as_half(static_cast<unsigned short>(bits16 & 0xffffu)));
 }
 
-// byte b (0..3) of a dword as float; the backend selects v_cvt_f32_ubyteN for these
-__device__ __forceinline__ float ub0(uint32_t v) { return float(v & 0xffu); }
-__device__ __forceinline__ float ub1(uint32_t v) { return float((v >> 8) & 0xffu); }
-__device__ __forceinline__ float ub2(uint32_t v) { return float((v >> 16) & 0xffu); }
-__device__ __forceinline__ float ub3(uint32_t v) { return float(v >> 24); }
+// byte b (0..3) of a dword as float: one v_cvt_f32_ubyteN each
+__device__ __forceinline__ float ub0(uint32_t v) {
+    float r;
+    asm("v_cvt_f32_ubyte0 %0, %1" : "=v"(r) : "v"(v));
+    return r;
+}
+__device__ __forceinline__ float ub1(uint32_t v) {
+    float r;
+    asm("v_cvt_f32_ubyte1 %0, %1" : "=v"(r) : "v"(v));
+    return r;
+}
+__device__ __forceinline__ float ub2(uint32_t v) {
+    float r;
+    asm("v_cvt_f32_ubyte2 %0, %1" : "=v"(r) : "v"(v));
+    return r;
+}
+__device__ __forceinline__ float ub3(uint32_t v) {
+    float r;
+    asm("v_cvt_f32_ubyte3 %0, %1" : "=v"(r) : "v"(v));
+    return r;
+}
 
 // 4 products of the bytes of v with x[0..3], accumulated into acc
 __device__ __forceinline__ float dot4u8(uint32_t v, const float *x, float acc) {
@@ -25,6 +41,15 @@ __device__ __forceinline__ float dot4u8(uint32_t v, const float *x, float acc) {
     acc = fmaf(ub2(v), x[2], acc);
     acc = fmaf(ub3(v), x[3], acc);
     return acc;
+}
+
+// Workgroup barrier that waits only for this wave's LDS traffic (lgkmcnt(0)), not
+// for outstanding global loads, so prefetched weights stay in flight across it.
+__device__ __forceinline__ void lds_barrier() {
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    __builtin_amdgcn_s_waitcnt(0xc07f);  // vmcnt: no wait, expcnt: no wait, lgkmcnt(0)
+    __builtin_amdgcn_s_barrier();
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
 }
 
 template <int W>

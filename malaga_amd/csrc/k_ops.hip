@@ -273,26 +273,48 @@ __global__ __launch_bounds__(256) void k_argmax_partial(const float *logits, int
     }
 }
 
-// kernels/malaga.cu:290-326 semantics, without the shortlist mapping.
+// kernels/malaga.cu:290-326 semantics, without the shortlist mapping.  Each row's
+// partials are reduced by the whole workgroup (8 independent loads per thread).
 __global__ __launch_bounds__(256) void k_greedy_finalize(const float *pv, const uint32_t *pi, int P, int b,
                                                          uint8_t *finished, uint32_t *ids, uint32_t *out, int m,
                                                          uint32_t *step, uint32_t eos, uint32_t pad) {
-    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, nw = blockDim.x >> 6;
+    __shared__ float sv[4];
+    __shared__ uint32_t si[4];
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
     const uint32_t s = *step;
-    for (int row = w; row < b; row += nw) {
+    for (int row = 0; row < b; ++row) {
         float best = -INFINITY;
         uint32_t bi = 0xffffffffu;
-        for (int p = lane; p < P; p += 64) argmax_merge(best, bi, pv[size_t(row) * P + p], pi[size_t(row) * P + p]);
+        for (int p0 = threadIdx.x; p0 < P; p0 += 256 * 8) {
+            float v[8];
+            uint32_t ix[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+                const int p = p0 + u * 256;
+                v[u] = p < P ? pv[size_t(row) * P + p] : -INFINITY;
+                ix[u] = p < P ? pi[size_t(row) * P + p] : 0xffffffffu;
+            }
+#pragma unroll
+            for (int u = 0; u < 8; ++u) argmax_merge(best, bi, v[u], ix[u]);
+        }
         wave_argmax(best, bi);
         if (lane == 0) {
+            sv[w] = best;
+            si[w] = bi;
+        }
+        __syncthreads();
+        if (threadIdx.x == 0) {
+            best = sv[0];
+            bi = si[0];
+            for (int k = 1; k < 4; ++k) argmax_merge(best, bi, sv[k], si[k]);
             uint32_t tok = bi;
             if (finished[row]) tok = pad;
             if (tok == eos) finished[row] = 1;
             ids[row] = tok;
             out[size_t(row) * m + s] = tok;
         }
+        __syncthreads();
     }
-    __syncthreads();
     if (threadIdx.x == 0) *step = s + 1;
 }
 

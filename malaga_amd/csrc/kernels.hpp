@@ -1,6 +1,7 @@
 // Host-side launchers of the HIP kernels.  All pointers are device pointers;
 // every launcher is asynchronous on `st` and returns hipSuccess or the launch error.
 #pragma once
+#include <hip/hip_fp16.h>
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -26,6 +27,8 @@ size_t planes_bytes(uint32_t type, int N, int K);
 
 // Largest batch the register-resident GEMV handles for this matrix (0 if none).
 int gemv_max_batch(const DevMatrix &w);
+// Workgroups of a GEMV launch over w.
+int gemv_grid(const DevMatrix &w);
 
 // y[b][n] = sum_k x[b][k] W[n][k] (+ bias[n]) (relu if set).  b <= gemv_max_batch(w).
 hipError_t gemv(const DevMatrix &w, const float *x, int ldx, int b, float *y, int ldy, const float *bias, bool relu,
@@ -87,6 +90,30 @@ hipError_t logsoftmax_topk(const float *logits, int rows, int V, int k, int mask
 size_t logsoftmax_topk_scratch(int rows, int k);
 // dst[i] = src[idx[i]] for rows of `row_bytes` bytes (i < n).
 hipError_t gather_rows(const void *src, void *dst, const uint32_t *idx, int n, size_t row_bytes, hipStream_t st);
+// ---- fused decoder-step kernels (batch <= 4), k_step.hip ----
+// True when the fused kernels handle matrix w at batch nb (attention over L keys).
+bool step_fusable(const DevMatrix &w, int nb, int d, int H, int hd, int L);
+size_t step_attn_lds(int nb, int d, int H, int L);
+// True when step_qkv has an embedding prologue for (projection type, embedding type).
+bool step_embed_supported(uint32_t proj_type, uint32_t emb_type);
+// qkv projection; prologue = embedding rows (emb != null: x = E[ids] * scale +
+// pos[*step + base]) or residual (x = x_in + y_in); x_out <- x (workgroup 0);
+// h = LayerNorm(x); epilogue: q (rows < d), f16 K / V at cache slot *step.
+hipError_t step_qkv(const DevMatrix &w, const float *bias, int nb, int d, const DevMatrix *emb, const uint32_t *ids,
+                    const float *pos, uint32_t pos_base, float emb_scale, const float *x_in, const float *y_in,
+                    float *x_out, const float *gamma, const float *beta, float eps, const uint32_t *step, float *q,
+                    __half *kc, __half *vc, int H, int hd, int m, hipStream_t st);
+// y = attention(q, K, V) W^T + bias (lens: cross lengths, or null for *step + 1 keys).
+hipError_t step_attn_proj(const DevMatrix &w, const float *bias, int nb, int d, const float *q, const __half *K,
+                          const __half *V, int H, int hd, int L, const uint32_t *lens, const uint32_t *step, float *y,
+                          hipStream_t st);
+// x = x_in + y_in ; x_out <- x ; y = LayerNorm(x) W^T + bias (relu).
+hipError_t step_resid_proj(const DevMatrix &w, const float *bias, bool relu, int nb, int d, const float *x_in,
+                           const float *y_in, float *x_out, const float *gamma, const float *beta, float eps, float *y,
+                           hipStream_t st);
+// y = x W^T + bias, x [nb][K] in global memory.
+hipError_t step_proj(const DevMatrix &w, const float *bias, int nb, const float *x, float *y, hipStream_t st);
+
 // *p += 1 on the device.
 hipError_t inc_u32(uint32_t *p, hipStream_t st);
 // Fill n uint32 values (graph-safe replacement for hipMemsetAsync).

@@ -220,6 +220,8 @@ void Model::load(const std::string &path) {
     cfg.pad_token_id = u("tokenizer.ggml.padding_token_id");
     cfg.eos_token_id = u("tokenizer.ggml.eos_token_id");
     cfg.decoder_start_token_id = u("tokenizer.ggml.decoder_start_token_id");
+    const char *nf = std::getenv("MALAGA_NO_FUSED_STEP");
+    no_fuse_ = nf && *nf && std::string(nf) != "0";
     const int d = cfg.d_model;
     if (d <= 0 || d % cfg.decoder_heads || d % cfg.encoder_heads || d > 4096 || d % 16)
         fail(ERR_UNSUPPORTED, "unsupported d_model " + std::to_string(d));
@@ -368,6 +370,9 @@ std::unique_ptr<StaticState> Model::new_state(int b, int s, int m, bool beam) {
         check_hip(hipMemsetAsync(st->cv.back(), 0, size_t(b) * H * s * hd * 2, ctx->stream), "memset");
     }
     st->x = static_cast<float *>(get(size_t(b) * d * 4, "x"));
+    st->xb = static_cast<float *>(get(size_t(b) * d * 4, "x (second buffer)"));
+    st->qc = static_cast<float *>(get(size_t(b) * d * 4, "cross q"));
+    st->fused = fusable(b, m, s);
     st->h = static_cast<float *>(get(size_t(b) * d * 4, "h"));
     st->y = static_cast<float *>(get(size_t(b) * d * 4, "y"));
     st->att = static_cast<float *>(get(size_t(b) * d * 4, "att"));
@@ -404,9 +409,86 @@ void Model::reset_state(StaticState &st, const Batch &src, const std::vector<uin
     h2d(st.finished, fin, s);
 }
 
-void Model::step(StaticState &st, bool greedy_mode, int mask_id) {
+bool Model::fusable(int b, int m, int s) const {
+    if (no_fuse_ || b > 4 || dec.empty()) return false;
+    const int d = cfg.d_model, H = cfg.decoder_heads, hd = d / H;
+    const int L = std::max(m, s);
+    if (!step_embed_supported(dec[0].qkv.w.type, embed.type)) return false;
+    for (const DecLayer &l : dec)
+        for (const Linear *lin : {&l.qkv, &l.out, &l.cross_q, &l.cross_out, &l.up, &l.down})
+            if (!step_fusable(lin->w, b, d, H, hd, L)) return false;
+    return true;
+}
+
+// src/model.rs:552-612 as six fused launches per layer (k_step.hip).
+void Model::step_fused(StaticState &st) {
     hipStream_t s = ctx->stream;
-    const int B = st.b, d = cfg.d_model, H = cfg.decoder_heads, hd = d / H, V = cfg.vocab_size;
+    const int B = st.b, d = cfg.d_model, H = cfg.decoder_heads, hd = d / H;
+    float *cur = st.x, *nxt = st.xb;
+    for (size_t i = 0; i < dec.size(); ++i) {
+        const DecLayer &l = dec[i];
+        if (i == 0) {
+            check_hip(step_qkv(l.qkv.w, l.qkv.b, B, d, &embed, st.ids, pos, uint32_t(cfg.pad_token_id + 1),
+                               embed_scale, nullptr, nullptr, cur, l.attn_norm.g, l.attn_norm.b, kLnEps, st.step,
+                               st.q, st.kc[i], st.vc[i], H, hd, st.m, s),
+                      "step_qkv");
+        } else {
+            check_hip(step_qkv(l.qkv.w, l.qkv.b, B, d, nullptr, st.ids, pos, 0, 1.f, cur, st.y, nxt, l.attn_norm.g,
+                               l.attn_norm.b, kLnEps, st.step, st.q, st.kc[i], st.vc[i], H, hd, st.m, s),
+                      "step_qkv");
+            std::swap(cur, nxt);
+        }
+        check_hip(step_attn_proj(l.out.w, l.out.b, B, d, st.q, st.kc[i], st.vc[i], H, hd, st.m, nullptr, st.step,
+                                 st.y, s),
+                  "step_attn_out");
+        check_hip(step_resid_proj(l.cross_q.w, l.cross_q.b, false, B, d, cur, st.y, nxt, l.cross_norm.g,
+                                  l.cross_norm.b, kLnEps, st.qc, s),
+                  "step_cross_q");
+        std::swap(cur, nxt);
+        check_hip(step_attn_proj(l.cross_out.w, l.cross_out.b, B, d, st.qc, st.ck[i], st.cv[i], H, hd, st.s, st.lens,
+                                 nullptr, st.y, s),
+                  "step_cross_out");
+        check_hip(step_resid_proj(l.up.w, l.up.b, true, B, d, cur, st.y, nxt, l.ffn_norm.g, l.ffn_norm.b, kLnEps,
+                                  st.u, s),
+                  "step_up");
+        std::swap(cur, nxt);
+        check_hip(step_proj(l.down.w, l.down.b, B, st.u, st.y, s), "step_down");
+    }
+    // h = dec_norm(x + y) for the LM head
+    check_hip(residual_ln(cur, st.y, B, d, dec_norm.g, dec_norm.b, kLnEps, st.h, s), "residual_ln");
+}
+
+void Model::lm_head(StaticState &st, bool greedy_mode, int mask_id) {
+    hipStream_t s = ctx->stream;
+    const int B = st.b, d = cfg.d_model, V = cfg.vocab_size;
+    if (greedy_mode) {
+        int parts = 64;
+        if (B <= gemv_max_batch(embed)) {
+            check_hip(gemv_argmax(embed, st.h, d, B, mask_id, st.pv, st.pi, &parts, s), "lm_head");
+        } else {
+            check_hip(gemm(embed, st.h, d, B, st.logits, V, nullptr, false, nullptr, 0, s), "lm_head");
+            check_hip(argmax_partial(st.logits, B, V, V, mask_id, st.pv, st.pi, parts, s), "argmax");
+        }
+        check_hip(greedy_finalize(st.pv, st.pi, parts, B, st.finished, st.ids, st.out, st.m, st.step,
+                                  uint32_t(cfg.eos_token_id), uint32_t(cfg.pad_token_id), s),
+                  "greedy_finalize");
+    } else {
+        if (B <= gemv_max_batch(embed))
+            check_hip(gemv(embed, st.h, d, B, st.logits, V, nullptr, false, s), "lm_head");
+        else
+            check_hip(gemm(embed, st.h, d, B, st.logits, V, nullptr, false, nullptr, 0, s), "lm_head");
+        check_hip(inc_u32(st.step, s), "step");
+    }
+}
+
+void Model::step(StaticState &st, bool greedy_mode, int mask_id) {
+    if (st.fused) {
+        step_fused(st);
+        lm_head(st, greedy_mode, mask_id);
+        return;
+    }
+    hipStream_t s = ctx->stream;
+    const int B = st.b, d = cfg.d_model, H = cfg.decoder_heads, hd = d / H;
     check_hip(embed_pos_ln(embed, st.ids, B, pos, st.step, uint32_t(cfg.pad_token_id + 1), embed_scale,
                            dec[0].attn_norm.g, dec[0].attn_norm.b, kLnEps, st.x, st.h, s),
               "embed_pos_ln");
@@ -427,24 +509,7 @@ void Model::step(StaticState &st, bool greedy_mode, int mask_id) {
         check_hip(residual_ln(st.x, st.y, B, d, next.g, next.b, kLnEps, st.h, s), "residual_ln");
     }
     // st.h is dec_norm(x): tied LM head
-    if (greedy_mode) {
-        int parts = 64;
-        if (B <= gemv_max_batch(embed)) {
-            check_hip(gemv_argmax(embed, st.h, d, B, mask_id, st.pv, st.pi, &parts, s), "lm_head");
-        } else {
-            check_hip(gemm(embed, st.h, d, B, st.logits, V, nullptr, false, nullptr, 0, s), "lm_head");
-            check_hip(argmax_partial(st.logits, B, V, V, mask_id, st.pv, st.pi, parts, s), "argmax");
-        }
-        check_hip(greedy_finalize(st.pv, st.pi, parts, B, st.finished, st.ids, st.out, st.m, st.step,
-                                  uint32_t(cfg.eos_token_id), uint32_t(cfg.pad_token_id), s),
-                  "greedy_finalize");
-    } else {
-        if (B <= gemv_max_batch(embed))
-            check_hip(gemv(embed, st.h, d, B, st.logits, V, nullptr, false, s), "lm_head");
-        else
-            check_hip(gemm(embed, st.h, d, B, st.logits, V, nullptr, false, nullptr, 0, s), "lm_head");
-        check_hip(inc_u32(st.step, s), "step");
-    }
+    lm_head(st, greedy_mode, mask_id);
 }
 
 // ------------------------------------------------------------ graph cache

@@ -71,6 +71,8 @@ struct StaticState {
     std::vector<__half *> kc, vc, ck, cv;
     // workspace (nothing is allocated inside a step)
     float *x = nullptr, *h = nullptr, *y = nullptr, *att = nullptr, *q = nullptr, *qkv = nullptr, *u = nullptr;
+    float *xb = nullptr, *qc = nullptr;  // second residual buffer and cross queries (fused step)
+    bool fused = false;                   // decoder step uses the fused kernels of k_step.hip
     float *logits = nullptr, *pv = nullptr;
     uint32_t *pi = nullptr;
     int parts = 0;
@@ -136,6 +138,8 @@ class Model {
     // src/model.rs:552-612: one decoder step on fixed buffers.  greedy: argmax +
     // bookkeeping, else logits into st.logits and ++step.
     void step(StaticState &st, bool greedy, int mask_id);
+    // Whether the fused step kernels cover a state of b rows with caches of m / s slots.
+    bool fusable(int b, int m, int s) const;
     void reset_state(StaticState &st, const Batch &src, const std::vector<uint32_t> &row_of, uint32_t start);
     // src/translator.rs:250-335
     std::vector<std::vector<uint32_t>> beam(const Batch &src, uint32_t tgt_lang, int max_new, int k, float lp,
@@ -150,6 +154,9 @@ class Model {
     float *upload_f32(class GgufFile &g, const std::string &name, int64_t n);
     DevMatrix upload_matrix(class GgufFile &g, const std::string &name, int n, int k);
     void matmul(const Linear &l, const float *x, int rows, float *y, bool relu, const float *resid);
+    void step_fused(StaticState &st);
+    void lm_head(StaticState &st, bool greedy_mode, int mask_id);
+    bool no_fuse_ = false;  // MALAGA_NO_FUSED_STEP=1 forces the unfused step
 };
 
 void check_hip(hipError_t e, const char *what);  // throws Failure

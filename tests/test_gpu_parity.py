@@ -118,3 +118,60 @@ def test_oom_falls_back_to_eager_and_keeps_tokens(tiny_gguf, models):
         _lib.load().mlg_debug_fail_alloc_after(-1)
     assert [r[: gpu.budget(len(s))] for r, s in zip(got, src)] == want
     assert gpu.graph_stats()["capture"] is False
+
+
+@pytest.fixture(scope="module")
+def unfused_models():
+    """Second Translator per file with the unfused step (MALAGA_NO_FUSED_STEP=1)."""
+    import os
+
+    cache = {}
+
+    def get(path):
+        key = str(path)
+        if key not in cache:
+            os.environ["MALAGA_NO_FUSED_STEP"] = "1"
+            try:
+                cache[key] = M.Translator.load(path)
+            finally:
+                del os.environ["MALAGA_NO_FUSED_STEP"]
+        return cache[key]
+
+    return get
+
+
+@pytest.mark.parametrize("preset", ["f32", "f16", "q8_0"])
+@pytest.mark.parametrize("nb", [1, 2, 4])
+def test_fused_step_small_batches_tiny(tiny_gguf, models, unfused_models, preset, nb):
+    """Batches of <= 4 rows run the fused step kernels (k_step.hip)."""
+    gpu, orc = models(tiny_gguf(preset))
+    src = pipeline_sentences()[:nb]
+    want, gap = orc.translate_batch(src, PLT, kv_f16=True)
+    assert gpu.generate(src, PLT) == want, f"min gap {gap}"
+    assert gpu.generate(src, PLT, M.GenOptions(fused=False)) == want
+    assert unfused_models(tiny_gguf(preset)).generate(src, PLT) == want
+    T = 9
+    rng = np.random.default_rng(nb)
+    tgt = np.zeros((nb, T), np.uint32)
+    tgt[:, 0], tgt[:, 1] = 2, PLT
+    tgt[:, 2:] = rng.integers(4, 254, (nb, T - 2))
+    lg = gpu.teacher_forced_logits(src, tgt)
+    assert np.abs(lg - orc.teacher_forced_logits(src, tgt, kv_f16=True)).max() < 2e-3
+    assert np.abs(lg - unfused_models(tiny_gguf(preset)).teacher_forced_logits(src, tgt)).max() < 1e-4
+
+
+@pytest.mark.parametrize("preset", ["q4_k_m", "q5_k_m", "q6_k", "q8_0"])
+@pytest.mark.parametrize("nb", [1, 2])
+def test_fused_step_small_batches_kquant(kq_gguf, models, unfused_models, preset, nb):
+    gpu, orc = models(kq_gguf(preset))
+    rng = np.random.default_rng(100 + nb)
+    src = [[997] + rng.integers(4, 990, n).tolist() + [2] for n in (25, 7)[:nb]]
+    want, gap = orc.translate_batch(src, 998, kv_f16=True)
+    assert gpu.generate(src, 998) == want, f"min gap {gap}"
+    assert unfused_models(kq_gguf(preset)).generate(src, 998) == want
+    T = 12
+    tgt = np.zeros((nb, T), np.uint32)
+    tgt[:, 0], tgt[:, 1] = 2, 998
+    tgt[:, 2:] = rng.integers(4, 990, (nb, T - 2))
+    lg = gpu.teacher_forced_logits(src, tgt)
+    assert np.abs(lg - orc.teacher_forced_logits(src, tgt, kv_f16=True)).max() < 2e-3
