@@ -52,21 +52,83 @@ __device__ __forceinline__ void lds_barrier() {
     __atomic_signal_fence(__ATOMIC_SEQ_CST);
 }
 
+// Cross-lane moves with DPP (no LDS round trip).  Every helper below must be
+// called with all 64 lanes active.
+template <int CTRL>
+__device__ __forceinline__ float dpp_mov(float v) {
+    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), CTRL, 0xf, 0xf, true));
+}
+template <int CTRL>
+__device__ __forceinline__ uint32_t dpp_mov(uint32_t v) {
+    return uint32_t(__builtin_amdgcn_mov_dpp(int(v), CTRL, 0xf, 0xf, true));
+}
+constexpr int kDppXor1 = 0xB1;         // quad_perm [1, 0, 3, 2]
+constexpr int kDppXor2 = 0x4E;         // quad_perm [2, 3, 0, 1]
+constexpr int kDppHalfMirror = 0x141;  // lane i <- lane 7 - i within 8
+constexpr int kDppMirror = 0x140;      // lane i <- lane 15 - i within 16
+
+__device__ __forceinline__ float lane_value(float v, int lane) {
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), lane));
+}
+
+// Reduction within aligned groups of 2^log2w lanes (log2w <= 6, wave-uniform);
+// every lane of a group receives the same, bitwise identical result.  Each step
+// combines the lane with one in the other half of its current group, so the
+// combining order does not depend on the lane.
+template <class Op>
+__device__ __forceinline__ float group_reduce(float v, int log2w, Op op) {
+    if (log2w >= 1) v = op(v, dpp_mov<kDppXor1>(v));
+    if (log2w >= 2) v = op(v, dpp_mov<kDppXor2>(v));
+    if (log2w >= 3) v = op(v, dpp_mov<kDppHalfMirror>(v));
+    if (log2w >= 4) v = op(v, dpp_mov<kDppMirror>(v));
+    if (log2w >= 5) {
+        const float r0 = lane_value(v, 0), r1 = lane_value(v, 16), r2 = lane_value(v, 32), r3 = lane_value(v, 48);
+        if (log2w == 5) v = (threadIdx.x & 32) ? op(r2, r3) : op(r0, r1);
+        else v = op(op(r0, r1), op(r2, r3));
+    }
+    return v;
+}
+
+// Sum over the wave in f64 (two 32-bit DPP moves per step); every lane receives
+// the same result.
+template <int CTRL>
+__device__ __forceinline__ double dpp_mov_f64(double v) {
+    const long long b = __double_as_longlong(v);
+    const int lo = __builtin_amdgcn_mov_dpp(int(b), CTRL, 0xf, 0xf, true);
+    const int hi = __builtin_amdgcn_mov_dpp(int(b >> 32), CTRL, 0xf, 0xf, true);
+    return __longlong_as_double((static_cast<long long>(hi) << 32) | static_cast<unsigned int>(lo));
+}
+__device__ __forceinline__ double lane_value_f64(double v, int lane) {
+    const long long b = __double_as_longlong(v);
+    const int lo = __builtin_amdgcn_readlane(int(b), lane), hi = __builtin_amdgcn_readlane(int(b >> 32), lane);
+    return __longlong_as_double((static_cast<long long>(hi) << 32) | static_cast<unsigned int>(lo));
+}
+__device__ __forceinline__ double wave_sum_f64(double v) {
+    v += dpp_mov_f64<kDppXor1>(v);
+    v += dpp_mov_f64<kDppXor2>(v);
+    v += dpp_mov_f64<kDppHalfMirror>(v);
+    v += dpp_mov_f64<kDppMirror>(v);
+    return (lane_value_f64(v, 0) + lane_value_f64(v, 16)) + (lane_value_f64(v, 32) + lane_value_f64(v, 48));
+}
+
+struct OpAdd {
+    __device__ float operator()(float a, float b) const { return a + b; }
+};
+struct OpMax {
+    __device__ float operator()(float a, float b) const { return fmaxf(a, b); }
+};
+
 template <int W>
 __device__ __forceinline__ float group_sum(float v) {
-    // sum within aligned groups of W lanes (W power of two, <= 64)
-#pragma unroll
-    for (int o = W / 2; o > 0; o >>= 1) v += __shfl_xor(v, o, kWave);
-    return v;
+    constexpr int l2 = W >= 64 ? 6 : W >= 32 ? 5 : W >= 16 ? 4 : W >= 8 ? 3 : W >= 4 ? 2 : W >= 2 ? 1 : 0;
+    return group_reduce(v, l2, OpAdd{});
 }
 
-__device__ __forceinline__ float wave_sum(float v) { return group_sum<kWave>(v); }
+__device__ __forceinline__ float group_sum_dyn(float v, int log2w) { return group_reduce(v, log2w, OpAdd{}); }
 
-__device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-    for (int o = kWave / 2; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, kWave));
-    return v;
-}
+__device__ __forceinline__ float wave_sum(float v) { return group_reduce(v, 6, OpAdd{}); }
+
+__device__ __forceinline__ float wave_max(float v) { return group_reduce(v, 6, OpMax{}); }
 
 // (value, index) argmax step: larger value wins, ties go to the lower index.
 __device__ __forceinline__ void argmax_merge(float &v, uint32_t &i, float ov, uint32_t oi) {
@@ -77,12 +139,22 @@ __device__ __forceinline__ void argmax_merge(float &v, uint32_t &i, float ov, ui
 }
 
 __device__ __forceinline__ void wave_argmax(float &v, uint32_t &i) {
+    auto step = [&](float ov, uint32_t oi) { argmax_merge(v, i, ov, oi); };
+    step(dpp_mov<kDppXor1>(v), dpp_mov<kDppXor1>(i));
+    step(dpp_mov<kDppXor2>(v), dpp_mov<kDppXor2>(i));
+    step(dpp_mov<kDppHalfMirror>(v), dpp_mov<kDppHalfMirror>(i));
+    step(dpp_mov<kDppMirror>(v), dpp_mov<kDppMirror>(i));
+    float rv[4];
+    uint32_t ri[4];
 #pragma unroll
-    for (int o = kWave / 2; o > 0; o >>= 1) {
-        const float ov = __shfl_xor(v, o, kWave);
-        const uint32_t oi = __shfl_xor(i, o, kWave);
-        argmax_merge(v, i, ov, oi);
+    for (int r = 0; r < 4; ++r) {
+        rv[r] = lane_value(v, 16 * r);
+        ri[r] = uint32_t(__builtin_amdgcn_readlane(int(i), 16 * r));
     }
+    v = rv[0];
+    i = ri[0];
+#pragma unroll
+    for (int r = 1; r < 4; ++r) argmax_merge(v, i, rv[r], ri[r]);
 }
 
 // Block-wide sum for blockDim.x a multiple of 64 (<= 1024).  `sh` holds >= 16 floats.

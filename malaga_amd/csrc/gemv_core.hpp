@@ -253,15 +253,21 @@ __device__ __forceinline__ void gemv_load_x(const float *x, int ldx, int nb, con
     }
 }
 
+struct NoPre {
+    __device__ void operator()() const {}
+};
+
 // Streams the rows of W; calls epi(row, bi, value) on the group-leader lane of each
-// row (value = dot product + bias[row], the bias fetched with the weights).  Waves gwave, gwave + nwaves, ... share the
-// rows.  The first step's weight loads are issued before `prologue()` runs, so
-// their latency overlaps whatever produces x (prologue fills xr/xs and may use
-// workgroup barriers: every thread of the workgroup must call this function).
-template <int T, int B, int CPL, class Pro, class Epi>
+// row (value = dot product + bias[row], the bias fetched with the weights).  Waves
+// gwave, gwave + nwaves, ... share the rows.  Order of issue: pre() (loads the
+// prologue needs, so that waiting for them does not wait for the weights: loads
+// complete in order), the first step's weights, then prologue(), which fills
+// xr/xs and may use workgroup barriers (every thread of the workgroup must call
+// this function).
+template <int T, int B, int CPL, class PreF, class Pro, class Epi>
 __device__ __forceinline__ void gemv_rows(const WPtr &w, const GemvGeom &g, float (&xr)[CPL][B][GTraits<T>::XW],
-                                          float (&xs)[CPL][B][GTraits<T>::NS], int gwave, int nwaves, Pro &&prologue,
-                                          Epi &epi, const float *bias = nullptr) {
+                                          float (&xs)[CPL][B][GTraits<T>::NS], int gwave, int nwaves, PreF &&pre,
+                                          Pro &&prologue, Epi &epi, const float *bias = nullptr) {
     const int lane = threadIdx.x & 63;
     const int lpr = 1 << g.lpr_log2, rpw = 64 >> g.lpr_log2;
     const int grp = lane >> g.lpr_log2, cl = lane & (lpr - 1);
@@ -288,7 +294,7 @@ __device__ __forceinline__ void gemv_rows(const WPtr &w, const GemvGeom &g, floa
             for (int t = 0; t < CPL; ++t) dot_chunk<T, B>(cidx[t], r[u][t], xr[t], xs[t], acc);
 #pragma unroll
             for (int bi = 0; bi < B; ++bi)
-                for (int o = lpr >> 1; o > 0; o >>= 1) acc[bi] += __shfl_xor(acc[bi], o, 64);
+                acc[bi] = group_sum_dyn(acc[bi], g.lpr_log2);
             const int row = (rg + u * nwaves) * rpw + grp;
             if (cl == 0 && row < w.N) {
 #pragma unroll
@@ -302,7 +308,10 @@ __device__ __forceinline__ void gemv_rows(const WPtr &w, const GemvGeom &g, floa
     const bool any = rg * rpw < w.N;  // wave-uniform
     Raw<T> A[2][CPL], Bf[2][CPL];
     float ba[2] = {0.f, 0.f}, bb[2] = {0.f, 0.f};
+    pre();
+    __builtin_amdgcn_sched_barrier(0);
     if (any) load_step(rg, A, ba);
+    __builtin_amdgcn_sched_barrier(0);
     prologue();
     if (!any) return;
     for (;;) {

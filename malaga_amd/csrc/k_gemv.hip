@@ -52,7 +52,7 @@ __global__ __launch_bounds__(256) void k_gemv(GemvArgs a) {
     const int gwave = blockIdx.x * 4 + (threadIdx.x >> 6), nwaves = gridDim.x * 4;
     if constexpr (MODE == 0) {
         StoreEpi<B> epi{a};
-        gemv_rows<T, B, CPL>(a.w, a.g, xr, xs, gwave, nwaves, load_x, epi, a.bias);
+        gemv_rows<T, B, CPL>(a.w, a.g, xr, xs, gwave, nwaves, NoPre{}, load_x, epi, a.bias);
     } else {
         ArgmaxEpi<B> epi{a, {}, {}};
 #pragma unroll
@@ -60,7 +60,7 @@ __global__ __launch_bounds__(256) void k_gemv(GemvArgs a) {
             epi.best[bi] = -INFINITY;
             epi.idx[bi] = 0xffffffffu;
         }
-        gemv_rows<T, B, CPL>(a.w, a.g, xr, xs, gwave, nwaves, load_x, epi, a.bias);
+        gemv_rows<T, B, CPL>(a.w, a.g, xr, xs, gwave, nwaves, NoPre{}, load_x, epi, a.bias);
         __shared__ float sv[4][B];
         __shared__ uint32_t si[4][B];
         const int wv = threadIdx.x >> 6;

@@ -1,18 +1,18 @@
-// Fused decoder-step kernels for batch <= 4 (src/model.rs:552-612 with the
+// Fused decoder-step kernels for batch <= 4 (src/model.rs:552-612, with the
 // fused kernels of kernels/malaga.cu folded into the projections).
 //
-// One layer is six launches instead of twelve:
-//   qkv       : [embedding +] residual + LayerNorm -> GEMV -> q | f16 K/V at slot *step
-//   attn_out  : self-attention over the f16 cache   -> GEMV (+bias)
-//   cross_q   : residual + LayerNorm                -> GEMV (+bias)
-//   cross_out : cross-attention over the encoder K/V -> GEMV (+bias)
-//   up        : residual + LayerNorm                -> GEMV (+bias, ReLU)
-//   down      : GEMV over the FFN activations (+bias)
-// Every workgroup computes its prologue (the LayerNorm or the attention of all
-// heads) redundantly in LDS: at decode sizes that costs a few KB of L2 reads and
-// saves a launch plus a round trip through HBM per fused op.  The first row
-// group's weights are requested before the prologue starts.  Workgroup 0 writes
-// the updated residual stream to the other half of a ping-pong pair.
+// One layer is six launches:
+//   qkv        : [embedding |] residual + LayerNorm -> GEMV -> q | f16 K/V at slot *step
+//   attn_head  : per group of heads: attention over the f16 cache, then the group's
+//                column slice of the out-projection -> one partial sum per group
+//   resid_proj : residual (x + partial sums + bias) + LayerNorm -> GEMV
+//                (cross_q; then, after the cross attn_head, ffn_up with ReLU)
+//   proj       : GEMV over the FFN activations (ffn_down)
+// The residual prologue keeps each thread's values in registers: residual,
+// partial sums, gamma and beta are requested together, after the first row
+// group's weights.  Workgroup 0 writes the updated residual stream to the other
+// half of a ping-pong pair.  Partial sums are added in a fixed order, so results
+// do not depend on scheduling.
 #include "dequant.hpp"
 #include "gemv_core.hpp"
 #include "kernels.hpp"
@@ -21,275 +21,216 @@ namespace mlg {
 
 namespace {
 
-enum Pro : int { PRO_EMBED = 0, PRO_RESID = 1, PRO_ATTN = 2, PRO_GLOBAL = 3 };
+enum Pro : int { PRO_EMBED = 0, PRO_RESID = 1, PRO_GLOBAL = 2, PRO_RESID_PRE = 3 };
 enum Epi : int { EPI_STORE = 0, EPI_QKV = 1 };
+
+constexpr int kMaxF4 = 4;  // float4 slots per thread and row in the residual prologue (d <= 4096)
 
 struct StepArgs {
     WPtr w;
     GemvGeom g;
     int nb;  // rows of the state
-    int d;   // model width (prologue vector length for EMBED / RESID / ATTN)
-    // prologue inputs
-    const float *x_in, *y_in;  // RESID: x = x_in + y_in
-    float *x_out;              // RESID / EMBED: new residual stream (written by workgroup 0)
+    int d;   // model width
+    // residual prologue: x = x_in + sum_{p < P} part[p] + pbias
+    const float *x_in;
+    const float *part;  // [P][nb][d]
+    int P;
+    const float *pbias;  // bias of the projection that produced the partials (or null)
+    float *x_out;        // new residual stream (workgroup 0 writes it)
     const float *gamma, *beta;
     float eps;
-    const uint8_t *eq, *es, *ed;  // EMBED: token embedding planes
+    // embedding prologue: x = E[ids[r]] * emb_scale + pos[*step + pos_base]
+    const uint8_t *eq, *es, *ed;
     const uint32_t *ids;
     const float *pos;
     uint32_t pos_base;
     float emb_scale;
-    const float *q;                 // ATTN: queries [nb][d]
-    const __half *K, *V;            // ATTN: [nb][H][L][hd]
-    int H, hd, L;
-    const uint32_t *lens;           // ATTN: cross lengths, or null -> *step + 1
     const uint32_t *step;
-    const float *xg;                // GLOBAL: x [nb][ldx]
+    // plain prologue: x [nb][ldx] in global memory
+    const float *xg;
     int ldx;
     // epilogue
     const float *bias;
     int relu;
-    float *y;  // EPI_STORE: [nb][N]
-    float *qo;                  // EPI_QKV: q [nb][d]
-    __half *kc, *vc;            // EPI_QKV: caches [nb][H][m][hd]
-    int m;
+    float *y;         // EPI_STORE: [nb][N]
+    float *qo;        // EPI_QKV: q [nb][d]
+    __half *kc, *vc;  // EPI_QKV: caches [nb][H][m][hd]
+    int H, hd, m;
 };
 
-__device__ __forceinline__ void block_sums(float (&v)[4], int n, float *red) {
-    // sums n (<= 4) values over the 256-thread workgroup; red holds >= 16 floats
-    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+constexpr int kPreParts = 8;  // partial sums a preloading residual prologue keeps in registers
+
+// Operands of the residual prologue, loaded before the weights when they fit
+// (rows <= 2, one float4 slot per row, P <= kPreParts).
+struct PreLoads {
+    float4 part[2][kPreParts], x[2], pb, gr, br;
+};
+
+__device__ __forceinline__ void add4(float4 &a, const float4 &b) {
+    a.x += b.x;
+    a.y += b.y;
+    a.z += b.z;
+    a.w += b.w;
+}
+
+__device__ __forceinline__ float4 ld4(const float *p, int f) { return reinterpret_cast<const float4 *>(p)[f]; }
+
+__device__ __forceinline__ void preload(const StepArgs &a, PreLoads &L) {
+    const int f = min(int(threadIdx.x), (a.d >> 2) - 1);
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
-        if (i < n) v[i] = wave_sum(v[i]);
-    if (lane == 0)
+    for (int bi = 0; bi < 2; ++bi) {
+        if (bi >= a.nb) break;
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
-            if (i < n) red[i * 4 + w] = v[i];
+        for (int p = 0; p < kPreParts; ++p)
+            if (p < a.P) L.part[bi][p] = ld4(a.part + (size_t(p) * a.nb + bi) * a.d, f);
+        L.x[bi] = ld4(a.x_in + size_t(bi) * a.d, f);
+    }
+    L.pb = a.pbias ? ld4(a.pbias, f) : make_float4(0.f, 0.f, 0.f, 0.f);
+    L.gr = ld4(a.gamma, f);
+    L.br = ld4(a.beta, f);
+}
+
+// LayerNorm of the rows held in registers (thread t owns float4 slots t, t + 256,
+// ... of each row), written to xs[nb][d] (LDS).  Mean and variance come from one
+// pass of f64 sums of x and x^2 (biased variance).
+__device__ __forceinline__ void ln_to_lds(const float4 (&v)[4][kMaxF4], const float4 (&gr)[kMaxF4],
+                                          const float4 (&br)[kMaxF4], int nb, int d, float eps, float *xs,
+                                          double *red) {
+    const int t = threadIdx.x, nf = d >> 2, lane = t & 63, w = t >> 6;
+    double s1[4] = {0.0, 0.0, 0.0, 0.0}, s2[4] = {0.0, 0.0, 0.0, 0.0};
+#pragma unroll
+    for (int bi = 0; bi < 4; ++bi)
+#pragma unroll
+        for (int c = 0; c < kMaxF4; ++c)
+            if (bi < nb && t + 256 * c < nf) {
+                const double x0 = v[bi][c].x, x1 = v[bi][c].y, x2 = v[bi][c].z, x3 = v[bi][c].w;
+                s1[bi] += (x0 + x1) + (x2 + x3);
+                s2[bi] += (x0 * x0 + x1 * x1) + (x2 * x2 + x3 * x3);
+            }
+#pragma unroll
+    for (int bi = 0; bi < 4; ++bi)
+        if (bi < nb) {
+            s1[bi] = wave_sum_f64(s1[bi]);
+            s2[bi] = wave_sum_f64(s2[bi]);
+            if (lane == 0) {
+                red[(2 * bi) * 4 + w] = s1[bi];
+                red[(2 * bi + 1) * 4 + w] = s2[bi];
+            }
+        }
     lds_barrier();
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
-        if (i < n) v[i] = red[i * 4] + red[i * 4 + 1] + red[i * 4 + 2] + red[i * 4 + 3];
+    for (int bi = 0; bi < 4; ++bi) {
+        if (bi >= nb) break;
+        const double *r1 = red + 2 * bi * 4, *r2 = r1 + 4;
+        const double mean = ((r1[0] + r1[1]) + (r1[2] + r1[3])) / d;
+        const double var = fmax(((r2[0] + r2[1]) + (r2[2] + r2[3])) / d - mean * mean, 0.0);
+        const float rstd = float(1.0 / sqrt(var + double(eps))), m = float(mean);
+#pragma unroll
+        for (int c = 0; c < kMaxF4; ++c)
+            if (t + 256 * c < nf)
+                reinterpret_cast<float4 *>(xs + bi * d)[t + 256 * c] =
+                    make_float4((v[bi][c].x - m) * rstd * gr[c].x + br[c].x, (v[bi][c].y - m) * rstd * gr[c].y + br[c].y,
+                                (v[bi][c].z - m) * rstd * gr[c].z + br[c].z, (v[bi][c].w - m) * rstd * gr[c].w + br[c].w);
+    }
     lds_barrier();
 }
 
-// LayerNorm of the nb rows of xs[nb][d] (LDS) in place, biased variance.  gamma and
-// beta (d <= 4096: 16 values per thread) are fetched before the reductions.
-__device__ __forceinline__ void ln_lds(float *xs, int nb, int d, const float *gamma, const float *beta, float eps,
-                                       float *red) {
-    float gr[16], br[16];
+// Builds the residual stream x (PRO_RESID / PRO_RESID_PRE) or the embedded tokens
+// (PRO_EMBED) in registers, writes it to x_out (workgroup 0) and leaves
+// LayerNorm(x) in xs[nb][d] (LDS).
+template <int PRO, int ET>
+__device__ __forceinline__ void resid_ln_prologue(const StepArgs &a, const PreLoads &L, float *xs, double *red) {
+    const int d = a.d, nb = a.nb, nf = d >> 2, nc = (nf + 255) >> 8;
+    const int t = threadIdx.x;
+    float4 v[4][kMaxF4], gr[kMaxF4], br[kMaxF4];
+    if constexpr (PRO == PRO_RESID_PRE) {
+        gr[0] = L.gr;
+        br[0] = L.br;
 #pragma unroll
-    for (int i = 0; i < 16; ++i) {
-        const int k = threadIdx.x + i * 256;
-        gr[i] = k < d ? gamma[k] : 0.f;
-        br[i] = k < d ? beta[k] : 0.f;
-    }
-    float s[4] = {0.f, 0.f, 0.f, 0.f};
-    for (int bi = 0; bi < nb; ++bi)
-        for (int k = threadIdx.x; k < d; k += 256) s[bi] += xs[bi * d + k];
-    block_sums(s, nb, red);
-    float mean[4], v2[4] = {0.f, 0.f, 0.f, 0.f};
-    for (int bi = 0; bi < nb; ++bi) {
-        mean[bi] = s[bi] / float(d);
-        for (int k = threadIdx.x; k < d; k += 256) {
-            const float c = xs[bi * d + k] - mean[bi];
-            v2[bi] += c * c;
+        for (int bi = 0; bi < 2; ++bi) {
+            if (bi >= nb) break;
+            float4 acc = L.part[bi][0];
+#pragma unroll
+            for (int p = 1; p < kPreParts; ++p)
+                if (p < a.P) add4(acc, L.part[bi][p]);
+            add4(acc, L.pb);
+            v[bi][0] = make_float4(L.x[bi].x + acc.x, L.x[bi].y + acc.y, L.x[bi].z + acc.z, L.x[bi].w + acc.w);
         }
-    }
-    block_sums(v2, nb, red);
-    for (int bi = 0; bi < nb; ++bi) {
-        const float rstd = rsqrtf(v2[bi] / float(d) + eps);
+    } else {
 #pragma unroll
-        for (int i = 0; i < 16; ++i) {
-            const int k = threadIdx.x + i * 256;
-            if (k < d) xs[bi * d + k] = (xs[bi * d + k] - mean[bi]) * rstd * gr[i] + br[i];
+        for (int c = 0; c < kMaxF4; ++c) {
+            if (c >= nc) break;
+            const int f = min(t + 256 * c, nf - 1);
+            gr[c] = ld4(a.gamma, f);
+            br[c] = ld4(a.beta, f);
         }
-    }
-    lds_barrier();
-}
-
-template <int ET>
-__device__ __forceinline__ void embed_rows(const StepArgs &a, float *xs) {
-    const uint32_t s = *a.step;
-    for (int bi = 0; bi < a.nb; ++bi) {
-        const uint32_t tok = a.ids[bi];
-        const float *pr = a.pos + size_t(s + a.pos_base) * a.d;
-        for (int k0 = threadIdx.x * 16; k0 < a.d; k0 += 256 * 16) {
-            float e[16];
-            dequant16<ET>(a.eq, a.es, a.ed, a.d, int(tok), k0, e);
+        if constexpr (PRO == PRO_EMBED) {
+            const uint32_t s = *a.step;
+            const float *pr = a.pos + size_t(s + a.pos_base) * d;
+            const int per_row = d >> 4;
+            for (int i = t; i < nb * per_row; i += 256) {
+                const int bi = i / per_row, k0 = (i % per_row) * 16;
+                float e[16];
+                dequant16<ET>(a.eq, a.es, a.ed, d, int(a.ids[bi]), k0, e);
 #pragma unroll
-            for (int i = 0; i < 16; ++i) xs[bi * a.d + k0 + i] = e[i] * a.emb_scale + pr[k0 + i];
-        }
-    }
-}
-
-// Attention of all (row, head) pairs into out[nb][H*HD] (LDS).  Scores live in
-// sc[nb*H][L], queries are staged in qs[nb][d], key-split partial sums in
-// part[2048] (all LDS).  nb * H must divide 256 and be >= 4.  Every phase spreads
-// (pair, key) work over the whole workgroup and issues several independent
-// 16-byte loads per thread before using them.
-template <int HD>
-__device__ __forceinline__ void attention_lds(const StepArgs &a, float *qs, float *sc, float *part, float *out,
-                                              float *red) {
-    const int H = a.H, d = a.d, L = a.L, nb = a.nb;
-    const int pairs = nb * H;
-    int nmax = 0;
-    const int n_self = a.lens ? 0 : int(*a.step) + 1;
-    for (int bi = 0; bi < nb; ++bi) nmax = max(nmax, a.lens ? int(a.lens[bi]) : n_self);
-    // phase 1: scores, item f -> (pair f / nmax, key f % nmax), 4 items per thread in
-    // flight; the first keys are requested before the queries are staged in LDS
-    constexpr int U = 4;
-    const int items = pairs * nmax;
-    bool staged = false;
-    for (int base = threadIdx.x; base < items || !staged; base += 256 * U) {
-        uint4 kr[U][HD / 8];
-        int fp[U], fj[U];
-        bool ok[U];
-#pragma unroll
-        for (int u = 0; u < U; ++u) {
-            const int f = base + u * 256;
-            fp[u] = f / nmax;
-            fj[u] = f % nmax;
-            const int bi = min(fp[u], pairs - 1) / H;
-            const int n = a.lens ? int(a.lens[bi]) : n_self;
-            ok[u] = f < items && fj[u] < n;
-            const int p = ok[u] ? fp[u] : 0, j = ok[u] ? fj[u] : 0;
-            const uint4 *k8 = reinterpret_cast<const uint4 *>(a.K + (size_t(p) * L + j) * HD);
-#pragma unroll
-            for (int t = 0; t < HD / 8; ++t) kr[u][t] = k8[t];
-        }
-        if (!staged) {  // uniform: the first trip of every thread
-            for (int i = threadIdx.x * 4; i < nb * d; i += 256 * 4)
-                *reinterpret_cast<float4 *>(qs + i) = *reinterpret_cast<const float4 *>(a.q + i);
+                for (int j = 0; j < 16; ++j) xs[bi * d + k0 + j] = e[j] * a.emb_scale + pr[k0 + j];
+            }
             lds_barrier();
-            staged = true;
-        }
 #pragma unroll
-        for (int u = 0; u < U; ++u) {
-            if (!ok[u]) continue;
-            const int bi = fp[u] / H, hh = fp[u] % H;
-            const float *qv = qs + bi * d + hh * HD;
-            float acc = 0.f;
+            for (int bi = 0; bi < 4; ++bi) {
+                if (bi >= nb) break;
 #pragma unroll
-            for (int t = 0; t < HD / 8; ++t) {
-                const uint32_t wv[4] = {kr[u][t].x, kr[u][t].y, kr[u][t].z, kr[u][t].w};
-#pragma unroll
-                for (int q2 = 0; q2 < 4; ++q2) {
-                    acc = fmaf(h2f(wv[q2]), qv[8 * t + 2 * q2], acc);
-                    acc = fmaf(h2f(wv[q2] >> 16), qv[8 * t + 2 * q2 + 1], acc);
-                }
+                for (int c = 0; c < kMaxF4; ++c)
+                    if (c < nc) v[bi][c] = ld4(xs + bi * d, min(t + 256 * c, nf - 1));
             }
-            sc[fp[u] * L + fj[u]] = acc;
-        }
-    }
-    lds_barrier();
-    // phase 2: softmax per pair, 256 / pairs threads per pair (a power of two <= 64)
-    const int tpp = 256 / pairs;
-    {
-        const int p = threadIdx.x / tpp, sub = threadIdx.x % tpp;
-        const int n = a.lens ? int(a.lens[p / H]) : n_self;
-        float mx = -INFINITY, sum = 0.f;
-        for (int j = sub; j < n; j += tpp) mx = fmaxf(mx, sc[p * L + j]);
-        for (int o = tpp >> 1; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
-        for (int j = sub; j < n; j += tpp) {
-            const float e = expf(sc[p * L + j] - mx);
-            sc[p * L + j] = e;
-            sum += e;
-        }
-        for (int o = tpp >> 1; o > 0; o >>= 1) sum += __shfl_xor(sum, o, 64);
-        if (sub == 0) red[16 + p] = 1.f / sum;
-    }
-    lds_barrier();
-    // phase 3: P.V, work item -> (pair, 8 consecutive dims, key split); 8 keys in flight
-    constexpr int G = HD / 8;
-    const int groups8 = pairs * G;
-    const int splits = max(1, 256 / groups8);
-    for (int it = threadIdx.x; it < groups8 * splits; it += 256) {
-        const int gi = it % groups8, sp = it / groups8;
-        const int p = gi / G, e0 = (gi % G) * 8;
-        const int bi = p / H;
-        const int n = a.lens ? int(a.lens[bi]) : n_self;
-        const __half *Vb = a.V + size_t(p) * L * HD + e0;
-        float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-        for (int j0 = sp; j0 < n; j0 += 8 * splits) {
-            uint4 raw[8];
-            float pj[8];
-#pragma unroll
-            for (int u = 0; u < 8; ++u) {
-                const int j = j0 + u * splits;
-                const int jj = j < n ? j : sp;
-                raw[u] = *reinterpret_cast<const uint4 *>(Vb + size_t(jj) * HD);
-                pj[u] = j < n ? sc[p * L + jj] : 0.f;
-            }
-#pragma unroll
-            for (int u = 0; u < 8; ++u) {
-                const uint32_t wv[4] = {raw[u].x, raw[u].y, raw[u].z, raw[u].w};
-#pragma unroll
-                for (int q2 = 0; q2 < 4; ++q2) {
-                    acc[2 * q2] = fmaf(pj[u], h2f(wv[q2]), acc[2 * q2]);
-                    acc[2 * q2 + 1] = fmaf(pj[u], h2f(wv[q2] >> 16), acc[2 * q2 + 1]);
-                }
-            }
-        }
-        if (splits == 1) {
-            const float inv = red[16 + p];
-            const int hh = p % H;
-#pragma unroll
-            for (int u = 0; u < 8; ++u) out[bi * d + hh * HD + e0 + u] = acc[u] * inv;
         } else {
 #pragma unroll
-            for (int u = 0; u < 8; ++u) part[(sp * groups8 + gi) * 8 + u] = acc[u];
+            for (int bi = 0; bi < 4; ++bi) {
+                if (bi >= nb) break;
+#pragma unroll
+                for (int c = 0; c < kMaxF4; ++c) {
+                    if (c >= nc) break;
+                    const int f = min(t + 256 * c, nf - 1);
+                    float4 acc = ld4(a.part + size_t(bi) * d, f);
+                    for (int p = 1; p < a.P; ++p) add4(acc, ld4(a.part + (size_t(p) * nb + bi) * d, f));
+                    if (a.pbias) add4(acc, ld4(a.pbias, f));
+                    const float4 x = ld4(a.x_in + size_t(bi) * d, f);
+                    v[bi][c] = make_float4(x.x + acc.x, x.y + acc.y, x.z + acc.z, x.w + acc.w);
+                }
+            }
         }
     }
-    lds_barrier();
-    if (splits > 1) {
-        for (int i = threadIdx.x; i < groups8 * 8; i += 256) {
-            const int g = i / 8, u = i % 8;
-            float o = 0.f;
-            for (int s2 = 0; s2 < splits; ++s2) o += part[(s2 * groups8 + g) * 8 + u];
-            const int pp = g / G, ee = (g % G) * 8 + u;
-            const int bi = pp / H, hh = pp % H;
-            out[bi * d + hh * HD + ee] = o * red[16 + pp];
-        }
-        lds_barrier();
+    if (blockIdx.x == 0) {
+#pragma unroll
+        for (int bi = 0; bi < 4; ++bi)
+#pragma unroll
+            for (int c = 0; c < kMaxF4; ++c)
+                if (bi < nb && t + 256 * c < nf)
+                    reinterpret_cast<float4 *>(a.x_out + size_t(bi) * d)[t + 256 * c] = v[bi][c];
     }
+    ln_to_lds(v, gr, br, nb, d, a.eps, xs, red);
 }
 
 template <int T, int B, int CPL, int PRO, int EPI, int ET>
 __global__ __launch_bounds__(256) void k_step(StepArgs a) {
     constexpr int XW = GTraits<T>::XW, NS = GTraits<T>::NS;
     extern __shared__ float lds[];
-    __shared__ float red[96];
+    __shared__ double red[32];
     const int lane = threadIdx.x & 63;
     const int cl = lane & ((1 << a.g.lpr_log2) - 1);
     const int gwave = blockIdx.x * 4 + (threadIdx.x >> 6), nwaves = gridDim.x * 4;
     float xr[CPL][B][XW], xs[CPL][B][NS];
+    PreLoads L;
 
+    auto pre = [&] {
+        if constexpr (PRO == PRO_RESID_PRE) preload(a, L);
+    };
     auto prologue = [&] {
         if constexpr (PRO == PRO_GLOBAL) {
             gemv_load_x<T, B, CPL>(a.xg, a.ldx, a.nb, a.g, cl, xr, xs);
-        } else if constexpr (PRO == PRO_ATTN) {
-            float *qs = lds, *out = lds + a.nb * a.d, *part = lds + 2 * a.nb * a.d, *sc = part + 2048;
-            if (a.hd == 64) attention_lds<64>(a, qs, sc, part, out, red);
-            else if (a.hd == 128) attention_lds<128>(a, qs, sc, part, out, red);
-            else attention_lds<16>(a, qs, sc, part, out, red);
-            gemv_load_x<T, B, CPL>(out, a.d, a.nb, a.g, cl, xr, xs);
         } else {
-            float *v = lds;
-            if constexpr (PRO == PRO_EMBED) {
-                embed_rows<ET>(a, v);
-            } else {
-                for (int i = threadIdx.x * 4; i < a.nb * a.d; i += 256 * 4) {
-                    const float4 xa = *reinterpret_cast<const float4 *>(a.x_in + i);
-                    const float4 ya = *reinterpret_cast<const float4 *>(a.y_in + i);
-                    *reinterpret_cast<float4 *>(v + i) = make_float4(xa.x + ya.x, xa.y + ya.y, xa.z + ya.z, xa.w + ya.w);
-                }
-            }
-            lds_barrier();
-            if (blockIdx.x == 0)
-                for (int i = threadIdx.x; i < a.nb * a.d; i += 256) a.x_out[i] = v[i];
-            lds_barrier();
-            ln_lds(v, a.nb, a.d, a.gamma, a.beta, a.eps, red);
-            gemv_load_x<T, B, CPL>(v, a.d, a.nb, a.g, cl, xr, xs);
+            resid_ln_prologue<PRO, ET>(a, L, lds, red);
+            gemv_load_x<T, B, CPL>(lds, a.d, a.nb, a.g, cl, xr, xs);
         }
     };
 
@@ -299,7 +240,7 @@ __global__ __launch_bounds__(256) void k_step(StepArgs a) {
             if (a.relu) v = fmaxf(v, 0.f);
             a.y[size_t(bi) * a.w.N + row] = v;
         };
-        gemv_rows<T, B, CPL>(a.w, a.g, xr, xs, gwave, nwaves, prologue, epi, a.bias);
+        gemv_rows<T, B, CPL>(a.w, a.g, xr, xs, gwave, nwaves, pre, prologue, epi, a.bias);
     } else {
         const uint32_t slot = *a.step;
         auto epi = [&](int row, int bi, float v) {
@@ -313,13 +254,182 @@ __global__ __launch_bounds__(256) void k_step(StepArgs a) {
                 (row < 2 * d ? a.kc : a.vc)[off] = __float2half(v);
             }
         };
-        gemv_rows<T, B, CPL>(a.w, a.g, xr, xs, gwave, nwaves, prologue, epi, a.bias);
+        gemv_rows<T, B, CPL>(a.w, a.g, xr, xs, gwave, nwaves, pre, prologue, epi, a.bias);
     }
 }
 
+// ------------------------------------------------------------------ attn_head
+
+struct HeadArgs {
+    WPtr w;          // out-projection [d][d]
+    int nb, d, H, L;
+    int HG;          // heads per workgroup (C = HG * HD columns of W)
+    int RW;          // rows of W per workgroup
+    const float *q;  // [nb][d]
+    const __half *K, *V;   // [nb][H][L][HD]
+    const uint32_t *lens;  // cross lengths, or null: *step + 1 keys
+    const uint32_t *step;
+    float *part;     // [H / HG][nb][d]
+};
+
+constexpr int kHeadCols = 256;  // max columns (HG * HD) per workgroup
+constexpr int kHeadParts = 8;   // head groups are sized so that P = H / HG <= this when possible
+
+// Workgroup (g, r): attention of heads [g HG, (g + 1) HG) for all nb rows, then
+// part[g][bi][row] = sum_{c < C} W[row][g C + c] * att[bi][g C + c] for the RW
+// rows [r RW, (r + 1) RW), one (row, chunk) item per thread.  Workgroups with the
+// same g repeat the attention (a few KB of K/V from L2) so that the projection
+// is spread over many CUs.
+//
+// Attention runs one (row, head) pair per wave with no workgroup barrier: lane
+// (split, sub) owns dimensions [8 sub, 8 sub + 8) of the keys j = k SPL + split,
+// so the score a lane computes (summed over the TPK lanes of its split) is the
+// weight it applies to its own values.  Keys are consumed in chunks of U SPL with
+// an online softmax (running max and sum), so any length fits in registers.
+template <int T, int HD>
+__global__ __launch_bounds__(256) void k_attn_head(HeadArgs a) {
+    constexpr int XW = GTraits<T>::XW, NS = GTraits<T>::NS;
+    constexpr int TPK = HD / 8;     // lanes per key: 8-wide dimension groups
+    constexpr int SPL = 64 / TPK;   // keys per pass of a wave
+    constexpr int U = 8;            // passes per chunk (loads in flight)
+    extern __shared__ float lds[];
+    const int t = threadIdx.x, lane = t & 63, w = t >> 6;
+    const int nb = a.nb, d = a.d, H = a.H, L = a.L, HG = a.HG, hg_log2 = __builtin_ctz(a.HG);
+    const int C = HG * HD, g = blockIdx.x, h0 = g * HG, col0 = g * C;
+    const int pairs = nb * HG;
+    float *outv = lds;                           // [pairs][HD] = [nb][C]
+    float *wsc = lds + 4 * kHeadCols + w * 512;  // this wave's [64][8] scratch
+    const int sub = lane % TPK, split = lane / TPK;
+
+    // Order of issue: the first chunk of this wave's first pair (addresses do not
+    // depend on the key counts; keys past a row's count are masked when used),
+    // the projection's weights, then the key counts.  Loads complete in order, so
+    // the attention never waits for the weights.
+    uint4 kr[U], vr[U];
+    float4 qa, qb;
+    auto load_chunk_kv = [&](int p, int j0) {
+        const int bi = p >> hg_log2, hh = h0 + (p & (HG - 1));
+        const size_t base = (size_t(bi) * H + hh) * L;
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int j = min(j0 + u * SPL + split, L - 1);
+            kr[u] = *reinterpret_cast<const uint4 *>(a.K + (base + j) * HD + sub * 8);
+            vr[u] = *reinterpret_cast<const uint4 *>(a.V + (base + j) * HD + sub * 8);
+        }
+        const float *qp = a.q + size_t(bi) * d + hh * HD + sub * 8;
+        qa = *reinterpret_cast<const float4 *>(qp);
+        qb = *reinterpret_cast<const float4 *>(qp + 4);
+    };
+    if (w < pairs) load_chunk_kv(w, 0);
+    __builtin_amdgcn_sched_barrier(0);
+
+    const int CPR = C / XW, cpr_log2 = __builtin_ctz(CPR), c0 = col0 / XW;
+    const int rl = t >> cpr_log2, wcc = t & (CPR - 1);
+    const int wrow = blockIdx.y * a.RW + rl;
+    const bool wok = rl < a.RW && wrow < d;
+    Raw<T> wr;
+    load_chunk<T>(a.w, wok ? wrow : blockIdx.y * a.RW, c0 + wcc, wr);
+    __builtin_amdgcn_sched_barrier(0);
+
+    // key counts per row: wave-uniform (scalar) loads
+    const int n_self = a.lens ? 0 : int(*a.step) + 1;
+    int nk[4];
+#pragma unroll
+    for (int bi = 0; bi < 4; ++bi) nk[bi] = bi < nb ? (a.lens ? int(a.lens[bi]) : n_self) : 0;
+
+    for (int p = w; p < pairs; p += 4) {  // wave-uniform
+        const int bi = p >> hg_log2;
+        const int n = bi == 0 ? nk[0] : bi == 1 ? nk[1] : bi == 2 ? nk[2] : nk[3];
+        float m = -INFINITY, l = 0.f;
+        float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+        for (int j0 = 0; j0 < n; j0 += U * SPL) {
+            if (p != w || j0 != 0) load_chunk_kv(p, j0);
+            float sc[U];
+            float cmax = -INFINITY;
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                float s = h2f(kr[u].x) * qa.x;
+                s = fmaf(h2f(kr[u].x >> 16), qa.y, s);
+                s = fmaf(h2f(kr[u].y), qa.z, s);
+                s = fmaf(h2f(kr[u].y >> 16), qa.w, s);
+                s = fmaf(h2f(kr[u].z), qb.x, s);
+                s = fmaf(h2f(kr[u].z >> 16), qb.y, s);
+                s = fmaf(h2f(kr[u].w), qb.z, s);
+                s = fmaf(h2f(kr[u].w >> 16), qb.w, s);
+                s = group_sum<TPK>(s);
+                sc[u] = j0 + u * SPL + split < n ? s : -INFINITY;
+                cmax = fmaxf(cmax, sc[u]);
+            }
+            const float mnew = fmaxf(m, wave_max(cmax));  // finite: key j0 is valid
+            const float r = expf(m - mnew);
+            l *= r;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) acc[e] *= r;
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                const bool in = j0 + u * SPL + split < n;
+                const float pj = in ? expf(sc[u] - mnew) : 0.f;
+                l += pj;
+                const uint32_t wv[4] = {in ? vr[u].x : 0u, in ? vr[u].y : 0u, in ? vr[u].z : 0u, in ? vr[u].w : 0u};
+#pragma unroll
+                for (int q2 = 0; q2 < 4; ++q2) {
+                    acc[2 * q2] = fmaf(pj, h2f(wv[q2]), acc[2 * q2]);
+                    acc[2 * q2 + 1] = fmaf(pj, h2f(wv[q2] >> 16), acc[2 * q2 + 1]);
+                }
+            }
+            m = mnew;
+        }
+        // every lane of a split holds that split's sum; count each split once
+        const float inv = 1.f / wave_sum(sub == 0 ? l : 0.f);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) wsc[lane * 8 + e] = acc[e];
+        __builtin_amdgcn_s_waitcnt(0xc07f);  // this wave's LDS writes are done
+        __builtin_amdgcn_wave_barrier();
+        for (int e = lane; e < HD; e += 64) {
+            float o = 0.f;
+#pragma unroll
+            for (int s2 = 0; s2 < SPL; ++s2) o += wsc[(s2 * TPK + e / 8) * 8 + e % 8];
+            outv[p * HD + e] = o * inv;
+        }
+        __builtin_amdgcn_s_waitcnt(0xc07f);
+        __builtin_amdgcn_wave_barrier();
+    }
+    lds_barrier();
+
+    // the group's slice of the out-projection
+    const int c = c0 + wcc;
+    float acc[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int bi = 0; bi < 4; ++bi) {
+        if (bi >= nb) break;
+        float xr[1][XW], xs[1][NS];
+#pragma unroll
+        for (int e = 0; e < XW; e += 4) {
+            const float4 x4 = *reinterpret_cast<const float4 *>(outv + bi * C + xpos<T>(c, e) - col0);
+            xr[0][e] = x4.x;
+            xr[0][e + 1] = x4.y;
+            xr[0][e + 2] = x4.z;
+            xr[0][e + 3] = x4.w;
+        }
+#pragma unroll
+        for (int s2 = 0; s2 < NS; ++s2) xs[0][s2] = 0.f;
+#pragma unroll
+        for (int e = 0; e < XW; ++e) xs[0][xslot<T>(e)] += xr[0][e];
+        float a1[1] = {0.f};
+        dot_chunk<T, 1>(c, wr, xr, xs, a1);
+        acc[bi] = a1[0];
+    }
+#pragma unroll
+    for (int bi = 0; bi < 4; ++bi) acc[bi] = group_sum_dyn(acc[bi], cpr_log2);
+    if (wcc == 0 && wok)
+        for (int bi = 0; bi < nb; ++bi) a.part[(size_t(g) * nb + bi) * d + wrow] = acc[bi];
+}
+
+// ---------------------------------------------------------------- dispatch
+
 template <int T, int B, int CPL, int PRO, int EPI, int ET>
 hipError_t launch_t(const StepArgs &a, int grid, size_t lds, hipStream_t st) {
-    if constexpr (GTraits<T>::XW * B * CPL > kGemvMaxXRegs) {
+    if constexpr (GTraits<T>::XW * B * CPL > kGemvMaxXRegs || (PRO == PRO_RESID_PRE && B > 2)) {
         return hipErrorInvalidValue;
     } else {
         hipLaunchKernelGGL((k_step<T, B, CPL, PRO, EPI, ET>), dim3(grid), dim3(256), lds, st, a);
@@ -349,6 +459,9 @@ hipError_t dispatch_t(uint32_t type, const StepArgs &a, int B, int cpl, int grid
     }
 }
 
+// The residual operands fit the registers of PreLoads.
+bool preloadable(const StepArgs &a) { return a.nb <= 2 && a.d <= 1024 && a.P <= kPreParts; }
+
 bool prepare(const DevMatrix &w, int nb, StepArgs &a, int *cpl) {
     if (nb < 1 || nb > 4 || nb > gemv_max_batch(w) || !gemv_geometry(w, &a.g, cpl)) return false;
     a.w = wptr_of(w);
@@ -356,33 +469,82 @@ bool prepare(const DevMatrix &w, int nb, StepArgs &a, int *cpl) {
     return true;
 }
 
-}  // namespace
+// columns of W one head group must cover: whole chunks, and for q6_K whole
+// 128-column halves of a block (a chunk interleaves 16-value runs of a half)
+int head_unit(uint32_t type) { return type == GGML_Q6_K ? 128 : gemv_xw(type); }
 
-size_t step_attn_lds(int nb, int d, int H, int L) {
-    return sizeof(float) * (size_t(2) * nb * d + 2048 + size_t(nb) * H * L);
+struct HeadGeom {
+    int HG, P, RW, R;
+    size_t lds;
+};
+
+bool head_geometry(const DevMatrix &w, int nb, int d, int H, int hd, int L, HeadGeom *hg) {
+    const int xw = gemv_xw(w.type), unit = head_unit(w.type);
+    if (!xw || nb < 1 || nb > 4 || H < 1 || hd * H != d || w.N != d || w.K != d || L < 1) return false;
+    if (hd != 16 && hd != 64 && hd != 128) return false;
+    int HG = unit > hd ? unit / hd : 1;
+    while (H / HG > kHeadParts && H % (2 * HG) == 0 && 2 * HG * hd <= kHeadCols) HG *= 2;
+    const int C = HG * hd;
+    if (C > kHeadCols || H % HG || C % xw || C % unit) return false;
+    const int CPR = C / xw;  // a power of two
+    if (CPR > 256) return false;
+    const int RW = 256 / CPR < d ? 256 / CPR : d;
+    hg->HG = HG;
+    hg->P = H / HG;
+    hg->RW = RW;
+    hg->R = (d + RW - 1) / RW;
+    hg->lds = sizeof(float) * (size_t(4) * kHeadCols + 4 * 512);
+    return true;
 }
 
-bool step_fusable(const DevMatrix &w, int nb, int d, int H, int hd, int L) {
+template <int T, int HD>
+hipError_t launch_head(const HeadArgs &a, int R, size_t lds, hipStream_t st) {
+    hipLaunchKernelGGL((k_attn_head<T, HD>), dim3(a.H / a.HG, R), dim3(256), lds, st, a);
+    return hipGetLastError();
+}
+
+template <int T>
+hipError_t launch_head_hd(const HeadArgs &a, int hd, int R, size_t lds, hipStream_t st) {
+    switch (hd) {
+    case 16: return launch_head<T, 16>(a, R, lds, st);
+    case 64: return launch_head<T, 64>(a, R, lds, st);
+    case 128: return launch_head<T, 128>(a, R, lds, st);
+    default: return hipErrorInvalidValue;
+    }
+}
+
+}  // namespace
+
+bool step_fusable(const DevMatrix &w, int nb, int d) {
     GemvGeom g;
     int cpl;
     if (nb < 1 || nb > 4 || nb > gemv_max_batch(w) || !gemv_geometry(w, &g, &cpl) || cpl > 2) return false;
     if (nb == 4 && cpl > 1) return false;
-    if ((hd != 16 && hd != 64 && hd != 128) || d % 16 || nb * H < 4 || nb * H > 64 || 256 % (nb * H)) return false;
-    // attention scores + staged queries + outputs must fit the LDS budget
-    // dynamic LDS (+ 384 B static) within the default 64 KB per workgroup
-    return step_attn_lds(nb, d, H, L) + 512 <= 64 * 1024 && size_t(nb) * d * 4 + 512 <= 64 * 1024;
+    // residual prologue: float4 slots, nb rows of d floats in LDS
+    return d % 16 == 0 && d <= 1024 * kMaxF4 && size_t(nb) * d * 4 + 256 <= 64 * 1024;
 }
 
-hipError_t step_qkv(const DevMatrix &w, const float *bias, int nb, int d, const DevMatrix *emb, const uint32_t *ids, const float *pos, uint32_t pos_base, float emb_scale,
-                    const float *x_in, const float *y_in, float *x_out, const float *gamma, const float *beta,
-                    float eps, const uint32_t *step, float *q, __half *kc, __half *vc, int H, int hd, int m,
-                    hipStream_t st) {
+int step_head_parts(const DevMatrix &w, int nb, int d, int H, int hd, int L) {
+    HeadGeom hg;
+    return head_geometry(w, nb, d, H, hd, L, &hg) ? hg.P : 0;
+}
+
+bool step_embed_supported(uint32_t t, uint32_t e) {
+    return (e == GGML_Q6_K && (t == GGML_Q4_K || t == GGML_Q5_K || t == GGML_Q6_K)) ||
+           (t == e && (t == GGML_Q8_0 || t == GGML_F16 || t == GGML_F32));
+}
+
+hipError_t step_qkv(const DevMatrix &w, const float *bias, int nb, int d, const DevMatrix *emb, const uint32_t *ids,
+                    const float *pos, uint32_t pos_base, float emb_scale, const float *x_in, const float *y_in,
+                    float *x_out, const float *gamma, const float *beta, float eps, const uint32_t *step, float *q,
+                    __half *kc, __half *vc, int H, int hd, int m, hipStream_t st) {
     StepArgs a{};
     int cpl;
-    if (!prepare(w, nb, a, &cpl)) return hipErrorInvalidValue;
+    if (!prepare(w, nb, a, &cpl) || !step_fusable(w, nb, d) || w.N != 3 * d) return hipErrorInvalidValue;
     a.d = d;
     a.x_in = x_in;
-    a.y_in = y_in;
+    a.part = y_in;
+    a.P = 1;
     a.x_out = x_out;
     a.gamma = gamma;
     a.beta = beta;
@@ -407,7 +569,9 @@ hipError_t step_qkv(const DevMatrix &w, const float *bias, int nb, int d, const 
     const size_t lds = sizeof(float) * size_t(nb) * d;
     const int grid = gemv_grid(w);
     const int B = gemv_round_b(nb);
-    if (!emb) return dispatch_t<PRO_RESID, EPI_QKV, GGML_F32>(w.type, a, B, cpl, grid, lds, st);
+    if (!emb)
+        return preloadable(a) ? dispatch_t<PRO_RESID_PRE, EPI_QKV, GGML_F32>(w.type, a, B, cpl, grid, lds, st)
+                              : dispatch_t<PRO_RESID, EPI_QKV, GGML_F32>(w.type, a, B, cpl, grid, lds, st);
     // (projection type, embedding type) pairs the presets produce (src/convert.rs:188-211)
     const uint32_t t = w.type, e = emb->type;
     if (t == GGML_Q4_K && e == GGML_Q6_K) return dispatch_bc<GGML_Q4_K, PRO_EMBED, EPI_QKV, GGML_Q6_K>(a, B, cpl, grid, lds, st);
@@ -419,41 +583,46 @@ hipError_t step_qkv(const DevMatrix &w, const float *bias, int nb, int d, const 
     return hipErrorInvalidValue;
 }
 
-bool step_embed_supported(uint32_t t, uint32_t e) {
-    return (e == GGML_Q6_K && (t == GGML_Q4_K || t == GGML_Q5_K || t == GGML_Q6_K)) ||
-           (t == e && (t == GGML_Q8_0 || t == GGML_F16 || t == GGML_F32));
-}
-
-hipError_t step_attn_proj(const DevMatrix &w, const float *bias, int nb, int d, const float *q, const __half *K,
-                          const __half *V, int H, int hd, int L, const uint32_t *lens, const uint32_t *step, float *y,
-                          hipStream_t st) {
-    StepArgs a{};
-    int cpl;
-    if (!prepare(w, nb, a, &cpl)) return hipErrorInvalidValue;
+hipError_t step_attn_head(const DevMatrix &w, int nb, int d, const float *q, const __half *K, const __half *V, int H,
+                          int hd, int L, const uint32_t *lens, const uint32_t *step, float *part, hipStream_t st) {
+    HeadGeom hg;
+    if (!head_geometry(w, nb, d, H, hd, L, &hg)) return hipErrorInvalidValue;
+    HeadArgs a{};
+    a.w = wptr_of(w);
+    a.nb = nb;
     a.d = d;
+    a.H = H;
+    a.L = L;
+    a.HG = hg.HG;
+    a.RW = hg.RW;
     a.q = q;
     a.K = K;
     a.V = V;
-    a.H = H;
-    a.hd = hd;
-    a.L = L;
     a.lens = lens;
     a.step = step;
-    a.bias = bias;
-    a.y = y;
-    return dispatch_t<PRO_ATTN, EPI_STORE, GGML_F32>(w.type, a, gemv_round_b(nb), cpl, gemv_grid(w),
-                                                       step_attn_lds(nb, d, H, L), st);
+    a.part = part;
+    switch (w.type) {
+    case GGML_Q4_K: return launch_head_hd<GGML_Q4_K>(a, hd, hg.R, hg.lds, st);
+    case GGML_Q5_K: return launch_head_hd<GGML_Q5_K>(a, hd, hg.R, hg.lds, st);
+    case GGML_Q6_K: return launch_head_hd<GGML_Q6_K>(a, hd, hg.R, hg.lds, st);
+    case GGML_Q8_0: return launch_head_hd<GGML_Q8_0>(a, hd, hg.R, hg.lds, st);
+    case GGML_F16: return launch_head_hd<GGML_F16>(a, hd, hg.R, hg.lds, st);
+    case GGML_F32: return launch_head_hd<GGML_F32>(a, hd, hg.R, hg.lds, st);
+    default: return hipErrorInvalidValue;
+    }
 }
 
 hipError_t step_resid_proj(const DevMatrix &w, const float *bias, bool relu, int nb, int d, const float *x_in,
-                           const float *y_in, float *x_out, const float *gamma, const float *beta, float eps, float *y,
-                           hipStream_t st) {
+                           const float *part, int P, const float *pbias, float *x_out, const float *gamma,
+                           const float *beta, float eps, float *y, hipStream_t st) {
     StepArgs a{};
     int cpl;
-    if (!prepare(w, nb, a, &cpl)) return hipErrorInvalidValue;
+    if (!prepare(w, nb, a, &cpl) || !step_fusable(w, nb, d) || P < 1 || w.K != d) return hipErrorInvalidValue;
     a.d = d;
     a.x_in = x_in;
-    a.y_in = y_in;
+    a.part = part;
+    a.P = P;
+    a.pbias = pbias;
     a.x_out = x_out;
     a.gamma = gamma;
     a.beta = beta;
@@ -461,14 +630,17 @@ hipError_t step_resid_proj(const DevMatrix &w, const float *bias, bool relu, int
     a.bias = bias;
     a.relu = relu ? 1 : 0;
     a.y = y;
-    return dispatch_t<PRO_RESID, EPI_STORE, GGML_F32>(w.type, a, gemv_round_b(nb), cpl, gemv_grid(w),
-                                                        sizeof(float) * size_t(nb) * d, st);
+    const size_t lds = sizeof(float) * size_t(nb) * d;
+    return preloadable(a) ? dispatch_t<PRO_RESID_PRE, EPI_STORE, GGML_F32>(w.type, a, gemv_round_b(nb), cpl,
+                                                                        gemv_grid(w), lds, st)
+                          : dispatch_t<PRO_RESID, EPI_STORE, GGML_F32>(w.type, a, gemv_round_b(nb), cpl, gemv_grid(w),
+                                                                    lds, st);
 }
 
 hipError_t step_proj(const DevMatrix &w, const float *bias, int nb, const float *x, float *y, hipStream_t st) {
     StepArgs a{};
     int cpl;
-    if (!prepare(w, nb, a, &cpl)) return hipErrorInvalidValue;
+    if (!prepare(w, nb, a, &cpl) || w.K % 4) return hipErrorInvalidValue;
     a.xg = x;
     a.ldx = w.K;
     a.bias = bias;

@@ -91,9 +91,11 @@ size_t logsoftmax_topk_scratch(int rows, int k);
 // dst[i] = src[idx[i]] for rows of `row_bytes` bytes (i < n).
 hipError_t gather_rows(const void *src, void *dst, const uint32_t *idx, int n, size_t row_bytes, hipStream_t st);
 // ---- fused decoder-step kernels (batch <= 4), k_step.hip ----
-// True when the fused kernels handle matrix w at batch nb (attention over L keys).
-bool step_fusable(const DevMatrix &w, int nb, int d, int H, int hd, int L);
-size_t step_attn_lds(int nb, int d, int H, int L);
+// True when the fused GEMV kernels (residual + LayerNorm prologue over d-wide rows)
+// handle matrix w at batch nb.
+bool step_fusable(const DevMatrix &w, int nb, int d);
+// Number of partial sums step_attn_head writes for out-projection w (0: unsupported).
+int step_head_parts(const DevMatrix &w, int nb, int d, int H, int hd, int L);
 // True when step_qkv has an embedding prologue for (projection type, embedding type).
 bool step_embed_supported(uint32_t proj_type, uint32_t emb_type);
 // qkv projection; prologue = embedding rows (emb != null: x = E[ids] * scale +
@@ -103,14 +105,15 @@ hipError_t step_qkv(const DevMatrix &w, const float *bias, int nb, int d, const 
                     const float *pos, uint32_t pos_base, float emb_scale, const float *x_in, const float *y_in,
                     float *x_out, const float *gamma, const float *beta, float eps, const uint32_t *step, float *q,
                     __half *kc, __half *vc, int H, int hd, int m, hipStream_t st);
-// y = attention(q, K, V) W^T + bias (lens: cross lengths, or null for *step + 1 keys).
-hipError_t step_attn_proj(const DevMatrix &w, const float *bias, int nb, int d, const float *q, const __half *K,
-                          const __half *V, int H, int hd, int L, const uint32_t *lens, const uint32_t *step, float *y,
-                          hipStream_t st);
-// x = x_in + y_in ; x_out <- x ; y = LayerNorm(x) W^T + bias (relu).
+// Attention of q over K/V [nb][H][L][hd] (lens: cross lengths, or null for *step + 1
+// keys), times the out-projection w, as step_head_parts(...) partial sums
+// part[p][nb][d] (bias not added): sum over p = attention . W^T.
+hipError_t step_attn_head(const DevMatrix &w, int nb, int d, const float *q, const __half *K, const __half *V, int H,
+                          int hd, int L, const uint32_t *lens, const uint32_t *step, float *part, hipStream_t st);
+// x = x_in + sum_{p < P} part[p] + pbias ; x_out <- x ; y = LayerNorm(x) W^T + bias (relu).
 hipError_t step_resid_proj(const DevMatrix &w, const float *bias, bool relu, int nb, int d, const float *x_in,
-                           const float *y_in, float *x_out, const float *gamma, const float *beta, float eps, float *y,
-                           hipStream_t st);
+                           const float *part, int P, const float *pbias, float *x_out, const float *gamma,
+                           const float *beta, float eps, float *y, hipStream_t st);
 // y = x W^T + bias, x [nb][K] in global memory.
 hipError_t step_proj(const DevMatrix &w, const float *bias, int nb, const float *x, float *y, hipStream_t st);
 

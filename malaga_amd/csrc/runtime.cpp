@@ -364,6 +364,9 @@ std::unique_ptr<StaticState> Model::new_state(int b, int s, int m, bool beam) {
     for (int i = 0; i < L; ++i) {
         st->kc.push_back(static_cast<__half *>(get(size_t(b) * H * m * hd * 2, "self K")));
         st->vc.push_back(static_cast<__half *>(get(size_t(b) * H * m * hd * 2, "self V")));
+        // slots past the step are read (and masked) by the fused attention: keep them finite
+        check_hip(hipMemsetAsync(st->kc.back(), 0, size_t(b) * H * m * hd * 2, ctx->stream), "memset");
+        check_hip(hipMemsetAsync(st->vc.back(), 0, size_t(b) * H * m * hd * 2, ctx->stream), "memset");
         st->ck.push_back(static_cast<__half *>(get(size_t(b) * H * s * hd * 2, "cross K")));
         st->cv.push_back(static_cast<__half *>(get(size_t(b) * H * s * hd * 2, "cross V")));
         check_hip(hipMemsetAsync(st->ck.back(), 0, size_t(b) * H * s * hd * 2, ctx->stream), "memset");
@@ -373,6 +376,7 @@ std::unique_ptr<StaticState> Model::new_state(int b, int s, int m, bool beam) {
     st->xb = static_cast<float *>(get(size_t(b) * d * 4, "x (second buffer)"));
     st->qc = static_cast<float *>(get(size_t(b) * d * 4, "cross q"));
     st->fused = fusable(b, m, s);
+    if (st->fused) st->part = static_cast<float *>(get(size_t(H) * b * d * 4, "attention partial sums"));
     st->h = static_cast<float *>(get(size_t(b) * d * 4, "h"));
     st->y = static_cast<float *>(get(size_t(b) * d * 4, "y"));
     st->att = static_cast<float *>(get(size_t(b) * d * 4, "att"));
@@ -412,11 +416,13 @@ void Model::reset_state(StaticState &st, const Batch &src, const std::vector<uin
 bool Model::fusable(int b, int m, int s) const {
     if (no_fuse_ || b > 4 || dec.empty()) return false;
     const int d = cfg.d_model, H = cfg.decoder_heads, hd = d / H;
-    const int L = std::max(m, s);
     if (!step_embed_supported(dec[0].qkv.w.type, embed.type)) return false;
-    for (const DecLayer &l : dec)
-        for (const Linear *lin : {&l.qkv, &l.out, &l.cross_q, &l.cross_out, &l.up, &l.down})
-            if (!step_fusable(lin->w, b, d, H, hd, L)) return false;
+    for (const DecLayer &l : dec) {
+        for (const Linear *lin : {&l.qkv, &l.cross_q, &l.up, &l.down})
+            if (!step_fusable(lin->w, b, d)) return false;
+        const int ps = step_head_parts(l.out.w, b, d, H, hd, m), pc = step_head_parts(l.cross_out.w, b, d, H, hd, s);
+        if (ps < 1 || ps > H || pc < 1 || pc > H) return false;
+    }
     return true;
 }
 
@@ -438,18 +444,19 @@ void Model::step_fused(StaticState &st) {
                       "step_qkv");
             std::swap(cur, nxt);
         }
-        check_hip(step_attn_proj(l.out.w, l.out.b, B, d, st.q, st.kc[i], st.vc[i], H, hd, st.m, nullptr, st.step,
-                                 st.y, s),
-                  "step_attn_out");
-        check_hip(step_resid_proj(l.cross_q.w, l.cross_q.b, false, B, d, cur, st.y, nxt, l.cross_norm.g,
-                                  l.cross_norm.b, kLnEps, st.qc, s),
+        const int ps = step_head_parts(l.out.w, B, d, H, hd, st.m);
+        check_hip(step_attn_head(l.out.w, B, d, st.q, st.kc[i], st.vc[i], H, hd, st.m, nullptr, st.step, st.part, s),
+                  "step_attn_head");
+        check_hip(step_resid_proj(l.cross_q.w, l.cross_q.b, false, B, d, cur, st.part, ps, l.out.b, nxt,
+                                  l.cross_norm.g, l.cross_norm.b, kLnEps, st.qc, s),
                   "step_cross_q");
         std::swap(cur, nxt);
-        check_hip(step_attn_proj(l.cross_out.w, l.cross_out.b, B, d, st.qc, st.ck[i], st.cv[i], H, hd, st.s, st.lens,
-                                 nullptr, st.y, s),
-                  "step_cross_out");
-        check_hip(step_resid_proj(l.up.w, l.up.b, true, B, d, cur, st.y, nxt, l.ffn_norm.g, l.ffn_norm.b, kLnEps,
-                                  st.u, s),
+        const int pc = step_head_parts(l.cross_out.w, B, d, H, hd, st.s);
+        check_hip(step_attn_head(l.cross_out.w, B, d, st.qc, st.ck[i], st.cv[i], H, hd, st.s, st.lens, nullptr,
+                                 st.part, s),
+                  "step_attn_head");
+        check_hip(step_resid_proj(l.up.w, l.up.b, true, B, d, cur, st.part, pc, l.cross_out.b, nxt, l.ffn_norm.g,
+                                  l.ffn_norm.b, kLnEps, st.u, s),
                   "step_up");
         std::swap(cur, nxt);
         check_hip(step_proj(l.down.w, l.down.b, B, st.u, st.y, s), "step_down");

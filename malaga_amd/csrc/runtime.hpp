@@ -72,6 +72,7 @@ struct StaticState {
     // workspace (nothing is allocated inside a step)
     float *x = nullptr, *h = nullptr, *y = nullptr, *att = nullptr, *q = nullptr, *qkv = nullptr, *u = nullptr;
     float *xb = nullptr, *qc = nullptr;  // second residual buffer and cross queries (fused step)
+    float *part = nullptr;                // attention partial sums [parts][b][d] (fused step)
     bool fused = false;                   // decoder step uses the fused kernels of k_step.hip
     float *logits = nullptr, *pv = nullptr;
     uint32_t *pi = nullptr;

@@ -157,7 +157,10 @@ def test_fused_step_small_batches_tiny(tiny_gguf, models, unfused_models, preset
     tgt[:, 2:] = rng.integers(4, 254, (nb, T - 2))
     lg = gpu.teacher_forced_logits(src, tgt)
     assert np.abs(lg - orc.teacher_forced_logits(src, tgt, kv_f16=True)).max() < 2e-3
-    assert np.abs(lg - unfused_models(tiny_gguf(preset)).teacher_forced_logits(src, tgt)).max() < 1e-4
+    # The two paths sum in different orders; an f32 difference of one rounding can
+    # move a K/V value across an f16 rounding boundary (5e-4 relative), so the
+    # paths agree to ~1e-4 rather than to f32 rounding.
+    assert np.abs(lg - unfused_models(tiny_gguf(preset)).teacher_forced_logits(src, tgt)).max() < 1e-3
 
 
 @pytest.mark.parametrize("preset", ["q4_k_m", "q5_k_m", "q6_k", "q8_0"])
