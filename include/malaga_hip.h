@@ -140,6 +140,11 @@ int64_t mlg_matrix_bytes(const mlg_matrix *w);
 int mlg_gemv(const mlg_matrix *w, const float *x, int b, float *y, const float *bias, int relu, void *stream);
 int mlg_gemv_max_batch(const mlg_matrix *w);
 int mlg_gemm(const mlg_matrix *w, const float *x, int M, float *y, const float *bias, int relu, void *stream);
+/* As mlg_gemm, plus a residual: y = x W^T + bias + r (r may be y itself), then relu.
+ * The residual adds of EncoderLayer::forward (src/model.rs:150-153) folded into the
+ * projections that precede them. */
+int mlg_gemm_resid(const mlg_matrix *w, const float *x, int M, float *y, const float *bias, int relu, const float *r,
+                   void *stream);
 /* LM head + first argmax pass (kernels/malaga.cu:247-280 fused into the GEMV). */
 int mlg_gemv_argmax_parts(const mlg_matrix *w, int b);
 int mlg_gemv_argmax(const mlg_matrix *w, const float *x, int b, int mask_id, float *pv, uint32_t *pi, void *stream);

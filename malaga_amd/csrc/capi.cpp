@@ -390,6 +390,12 @@ int mlg_gemm(const mlg_matrix *w, const float *x, int M, float *y, const float *
     return hip_status(mlg::gemm(w->w, x, w->w.K, M, y, w->w.N, bias, relu != 0, nullptr, 0, as_stream(stream)), "gemm");
 }
 
+int mlg_gemm_resid(const mlg_matrix *w, const float *x, int M, float *y, const float *bias, int relu, const float *r,
+                   void *stream) {
+    if (!w || !x || !y || M < 1) return set_err(MLG_ERR_INVALID, "bad argument");
+    return hip_status(mlg::gemm(w->w, x, w->w.K, M, y, w->w.N, bias, relu != 0, r, w->w.N, as_stream(stream)), "gemm");
+}
+
 int mlg_gemv_argmax_parts(const mlg_matrix *w, int b) { return w ? mlg::gemv_argmax_parts(w->w, b) : 0; }
 
 int mlg_gemv_argmax(const mlg_matrix *w, const float *x, int b, int mask_id, float *pv, uint32_t *pi, void *stream) {

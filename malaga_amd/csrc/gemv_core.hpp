@@ -63,42 +63,71 @@ struct Raw {
     uint32_t e0, e1;
 };
 
-template <int T>
+typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
+typedef unsigned int u32x2_t __attribute__((ext_vector_type(2)));
+
+// 16 / 8 / 2-byte loads; NT marks streaming data (read once per step, e.g. the
+// 215 MB LM head) as non-temporal so that it does not evict what is reused.
+template <bool NT>
+__device__ __forceinline__ uint4 ld_u4(const uint8_t *p) {
+    if constexpr (NT) {
+        const u32x4_t v = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t *>(p));
+        return make_uint4(v.x, v.y, v.z, v.w);
+    } else {
+        return *reinterpret_cast<const uint4 *>(p);
+    }
+}
+template <bool NT>
+__device__ __forceinline__ uint2 ld_u2(const uint8_t *p) {
+    if constexpr (NT) {
+        const u32x2_t v = __builtin_nontemporal_load(reinterpret_cast<const u32x2_t *>(p));
+        return make_uint2(v.x, v.y);
+    } else {
+        return *reinterpret_cast<const uint2 *>(p);
+    }
+}
+template <bool NT>
+__device__ __forceinline__ uint32_t ld_u16(const uint8_t *p) {
+    if constexpr (NT) return __builtin_nontemporal_load(reinterpret_cast<const unsigned short *>(p));
+    else return *reinterpret_cast<const unsigned short *>(p);
+}
+
+template <int T, bool NT = false>
 __device__ __forceinline__ void load_chunk(const WPtr &w, int row, int c, Raw<T> &r) {
     if constexpr (T == GGML_Q4_K) {
         const uint8_t *blk = w.q + (size_t(row) * w.nb + (c >> 2)) * 144;
         const int g = c & 3;
-        r.h = *reinterpret_cast<const uint4 *>(blk);
-        r.a = *reinterpret_cast<const uint4 *>(blk + 16 + 32 * g);
-        r.b = *reinterpret_cast<const uint4 *>(blk + 32 + 32 * g);
+        r.h = ld_u4<NT>(blk);
+        r.a = ld_u4<NT>(blk + 16 + 32 * g);
+        r.b = ld_u4<NT>(blk + 32 + 32 * g);
     } else if constexpr (T == GGML_Q5_K) {
         const uint8_t *blk = w.q + (size_t(row) * w.nb + (c >> 2)) * 176;
         const int g = c & 3;
-        r.h = *reinterpret_cast<const uint4 *>(blk);
-        r.c = *reinterpret_cast<const uint4 *>(blk + 16);  // qh[0..15]
-        r.e = *reinterpret_cast<const uint4 *>(blk + 32);  // qh[16..31]
-        r.a = *reinterpret_cast<const uint4 *>(blk + 48 + 32 * g);
-        r.b = *reinterpret_cast<const uint4 *>(blk + 64 + 32 * g);
+        r.h = ld_u4<NT>(blk);
+        r.c = ld_u4<NT>(blk + 16);  // qh[0..15]
+        r.e = ld_u4<NT>(blk + 32);  // qh[16..31]
+        r.a = ld_u4<NT>(blk + 48 + 32 * g);
+        r.b = ld_u4<NT>(blk + 64 + 32 * g);
     } else if constexpr (T == GGML_Q6_K) {
         const size_t blk = size_t(row) * w.nb + (c >> 2);
         const int h2 = (c >> 1) & 1, i = c & 1;
         const uint8_t *qp = w.q + blk * 192;
-        r.a = *reinterpret_cast<const uint4 *>(qp + 64 * h2 + 16 * i);
-        r.b = *reinterpret_cast<const uint4 *>(qp + 64 * h2 + 32 + 16 * i);
-        r.h = *reinterpret_cast<const uint4 *>(qp + 128 + 32 * h2 + 16 * i);
-        const uint2 sc = *reinterpret_cast<const uint2 *>(w.s + blk * 16 + 8 * h2);
+        r.a = ld_u4<NT>(qp + 64 * h2 + 16 * i);
+        r.b = ld_u4<NT>(qp + 64 * h2 + 32 + 16 * i);
+        r.h = ld_u4<NT>(qp + 128 + 32 * h2 + 16 * i);
+        const uint2 sc = ld_u2<NT>(w.s + blk * 16 + 8 * h2);
         r.e0 = sc.x;
         r.e1 = sc.y;
-        r.c.x = *reinterpret_cast<const unsigned short *>(w.d + blk * 2);
+        r.c.x = ld_u16<NT>(w.d + blk * 2);
     } else if constexpr (T == GGML_Q8_0) {
         const uint8_t *qp = w.q + size_t(row) * w.K + 32 * c;
-        r.a = *reinterpret_cast<const uint4 *>(qp);
-        r.b = *reinterpret_cast<const uint4 *>(qp + 16);
-        r.e0 = *reinterpret_cast<const unsigned short *>(w.d + (size_t(row) * (w.K >> 5) + c) * 2);
+        r.a = ld_u4<NT>(qp);
+        r.b = ld_u4<NT>(qp + 16);
+        r.e0 = ld_u16<NT>(w.d + (size_t(row) * (w.K >> 5) + c) * 2);
     } else if constexpr (T == GGML_F16) {
-        r.a = *reinterpret_cast<const uint4 *>(w.q + (size_t(row) * w.K + 8 * c) * 2);
+        r.a = ld_u4<NT>(w.q + (size_t(row) * w.K + 8 * c) * 2);
     } else {
-        r.a = *reinterpret_cast<const uint4 *>(w.q + (size_t(row) * w.K + 4 * c) * 4);
+        r.a = ld_u4<NT>(w.q + (size_t(row) * w.K + 4 * c) * 4);
     }
 }
 
@@ -264,7 +293,7 @@ struct NoPre {
 // complete in order), the first step's weights, then prologue(), which fills
 // xr/xs and may use workgroup barriers (every thread of the workgroup must call
 // this function).
-template <int T, int B, int CPL, class PreF, class Pro, class Epi>
+template <int T, int B, int CPL, bool NT = false, class PreF, class Pro, class Epi>
 __device__ __forceinline__ void gemv_rows(const WPtr &w, const GemvGeom &g, float (&xr)[CPL][B][GTraits<T>::XW],
                                           float (&xs)[CPL][B][GTraits<T>::NS], int gwave, int nwaves, PreF &&pre,
                                           Pro &&prologue, Epi &epi, const float *bias = nullptr) {
@@ -280,7 +309,7 @@ __device__ __forceinline__ void gemv_rows(const WPtr &w, const GemvGeom &g, floa
         for (int u = 0; u < 2; ++u) {
             const int row = min((rg + u * nwaves) * rpw + grp, w.N - 1);
 #pragma unroll
-            for (int t = 0; t < CPL; ++t) load_chunk<T>(w, row, cidx[t], r[u][t]);
+            for (int t = 0; t < CPL; ++t) load_chunk<T, NT>(w, row, cidx[t], r[u][t]);
             bv[u] = bias ? bias[row] : 0.f;
         }
     };

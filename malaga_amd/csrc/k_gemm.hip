@@ -88,11 +88,18 @@ hipError_t launch(const DevMatrix &w, const float *X, int ldx, int M, float *Y, 
 
 }  // namespace
 
-hipError_t gemm(const DevMatrix &w, const float *X, int ldx, int M, float *Y, int ldy, const float *bias, bool relu,
-                const float *R, int ldr, hipStream_t st) {
+hipError_t gemm_simt(const DevMatrix &w, const float *X, int ldx, int M, float *Y, int ldy, const float *bias,
+                     bool relu, const float *R, int ldr, hipStream_t st) {
     if (M <= 0) return hipSuccess;
     if (w.K % 16) return hipErrorInvalidValue;
     MLG_DISPATCH_TYPE(w.type, launch, w, X, ldx, M, Y, ldy, bias, relu, R, ldr, st)
+}
+
+hipError_t gemm(const DevMatrix &w, const float *X, int ldx, int M, float *Y, int ldy, const float *bias, bool relu,
+                const float *R, int ldr, hipStream_t st) {
+    if (gemm_mfma_supported(w) && ldx % 4 == 0 && reinterpret_cast<uintptr_t>(X) % 16 == 0)
+        return gemm_mfma(w, X, ldx, M, Y, ldy, bias, relu, R, ldr, st);
+    return gemm_simt(w, X, ldx, M, Y, ldy, bias, relu, R, ldr, st);
 }
 
 }  // namespace mlg

@@ -53,14 +53,14 @@ __global__ __launch_bounds__(256) void k_gemv(GemvArgs a) {
     if constexpr (MODE == 0) {
         StoreEpi<B> epi{a};
         gemv_rows<T, B, CPL>(a.w, a.g, xr, xs, gwave, nwaves, NoPre{}, load_x, epi, a.bias);
-    } else {
+    } else {  // the LM head: weights streamed once per step
         ArgmaxEpi<B> epi{a, {}, {}};
 #pragma unroll
         for (int bi = 0; bi < B; ++bi) {
             epi.best[bi] = -INFINITY;
             epi.idx[bi] = 0xffffffffu;
         }
-        gemv_rows<T, B, CPL>(a.w, a.g, xr, xs, gwave, nwaves, NoPre{}, load_x, epi, a.bias);
+        gemv_rows<T, B, CPL, true>(a.w, a.g, xr, xs, gwave, nwaves, NoPre{}, load_x, epi, a.bias);
         __shared__ float sv[4][B];
         __shared__ uint32_t si[4][B];
         const int wv = threadIdx.x >> 6;

@@ -87,6 +87,36 @@ def test_gemm_matches_dequantized_dot(ctx, t, N, K):
         ctx.lib.mlg_matrix_free(w)
 
 
+@pytest.mark.parametrize("t,N,K", [(Q4_K, 200, 1024), (Q5_K, 130, 512), (Q6_K, 70, 2048), (Q8_0, 64, 768),
+                                   (F16, 90, 256)])
+def test_gemm_mfma_tiles_bias_relu_residual(ctx, t, N, K):
+    """The MFMA GEMM (K % 256 == 0) over every X-tile size (16 / 32 / 64 rows), partial
+    tiles in M and N, with bias, ReLU and an in-place residual (R = Y)."""
+    rng = np.random.default_rng(31 + t)
+    wf = rng.normal(0, 0.02, (N, K)).astype(np.float32)
+    blocks = M.quantize(t, wf)
+    w = upload(ctx, t, blocks, N, K)
+    try:
+        wd = O.dequant(t, blocks, N * K).reshape(N, K)
+        bias = rng.normal(0, 0.1, N).astype(np.float32)
+        bd = dev(bias)
+        for M_ in (3, 16, 29, 32, 64, 100):
+            x = (rng.normal(0, 1, (M_, K)) * rng.uniform(0.01, 30, (M_, 1))).astype(np.float32)
+            r0 = rng.normal(0, 1, (M_, N)).astype(np.float32)
+            xd, yd = dev(x), dev(r0)
+            for relu in (0, 1):
+                yd.copy_(torch.from_numpy(r0))
+                _lib.check(ctx.lib.mlg_gemm_resid(w, ptr(xd), M_, ptr(yd), ptr(bd), relu, ptr(yd), None))
+                torch.cuda.synchronize()
+                ref = O.gemv(t, blocks, N, K, x) + bias + r0
+                if relu:
+                    ref = np.maximum(ref, 0)
+                tol = 2e-6 * (bound(x, wd) + np.abs(bias) + np.abs(r0)) + 1e-6
+                assert (np.abs(yd.cpu().numpy() - ref) <= tol).all(), (M_, relu)
+    finally:
+        ctx.lib.mlg_matrix_free(w)
+
+
 @pytest.mark.parametrize("t", [Q6_K, Q4_K, Q8_0])
 def test_gemv_argmax_lowest_index_on_ties(ctx, t):
     rng = np.random.default_rng(99)
