@@ -23,6 +23,7 @@ struct mlg_batch {
 struct mlg_matrix {
     mlg::DevMatrix w;
     void *mem = nullptr;
+    mlg_ctx *ctx = nullptr;
 };
 
 namespace {
@@ -357,6 +358,7 @@ int mlg_matrix_upload(mlg_ctx *ctx, uint32_t type, int N, int K, const void *ggu
             mlg::dev_free(w->mem);
             mlg::check_hip(e, "upload");
         }
+        w->ctx = ctx;
         w->w.type = type;
         w->w.N = N;
         w->w.K = K;
@@ -387,13 +389,23 @@ int mlg_gemv(const mlg_matrix *w, const float *x, int b, float *y, const float *
 
 int mlg_gemm(const mlg_matrix *w, const float *x, int M, float *y, const float *bias, int relu, void *stream) {
     if (!w || !x || !y || M < 1) return set_err(MLG_ERR_INVALID, "bad argument");
-    return hip_status(mlg::gemm(w->w, x, w->w.K, M, y, w->w.N, bias, relu != 0, nullptr, 0, as_stream(stream)), "gemm");
+    return guarded([&]() -> int {
+        float *ws = w->ctx->c.gemm_workspace();
+        return hip_status(mlg::gemm(w->w, x, w->w.K, M, y, w->w.N, bias, relu != 0, nullptr, 0, as_stream(stream), ws,
+                                    mlg::kGemmWorkspaceBytes),
+                          "gemm");
+    });
 }
 
 int mlg_gemm_resid(const mlg_matrix *w, const float *x, int M, float *y, const float *bias, int relu, const float *r,
                    void *stream) {
     if (!w || !x || !y || M < 1) return set_err(MLG_ERR_INVALID, "bad argument");
-    return hip_status(mlg::gemm(w->w, x, w->w.K, M, y, w->w.N, bias, relu != 0, r, w->w.N, as_stream(stream)), "gemm");
+    return guarded([&]() -> int {
+        float *ws = w->ctx->c.gemm_workspace();
+        return hip_status(mlg::gemm(w->w, x, w->w.K, M, y, w->w.N, bias, relu != 0, r, w->w.N, as_stream(stream), ws,
+                                    mlg::kGemmWorkspaceBytes),
+                          "gemm");
+    });
 }
 
 int mlg_gemv_argmax_parts(const mlg_matrix *w, int b) { return w ? mlg::gemv_argmax_parts(w->w, b) : 0; }

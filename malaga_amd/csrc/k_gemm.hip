@@ -96,9 +96,9 @@ hipError_t gemm_simt(const DevMatrix &w, const float *X, int ldx, int M, float *
 }
 
 hipError_t gemm(const DevMatrix &w, const float *X, int ldx, int M, float *Y, int ldy, const float *bias, bool relu,
-                const float *R, int ldr, hipStream_t st) {
+                const float *R, int ldr, hipStream_t st, float *ws, size_t ws_bytes) {
     if (gemm_mfma_supported(w) && ldx % 4 == 0 && reinterpret_cast<uintptr_t>(X) % 16 == 0)
-        return gemm_mfma(w, X, ldx, M, Y, ldy, bias, relu, R, ldr, st);
+        return gemm_mfma(w, X, ldx, M, Y, ldy, bias, relu, R, ldr, st, ws, ws_bytes);
     return gemm_simt(w, X, ldx, M, Y, ldy, bias, relu, R, ldr, st);
 }
 

@@ -19,6 +19,8 @@
 #include "gemv_core.hpp"
 #include "kernels.hpp"
 
+#include <algorithm>
+
 namespace mlg {
 
 namespace {
@@ -40,6 +42,7 @@ struct MfmaArgs {
     int ldy;
     const float *bias, *R;
     int ldr, relu;
+    float *part;  // split K: raw sums [gridDim.z][M][N], epilogue in k_splitk_reduce
 };
 
 // f16 pair (1024 + byte sel0, 1024 + byte sel1) of v, minus `off` (exact for bytes < 1024 - off range)
@@ -213,7 +216,9 @@ __global__ __launch_bounds__(256) void k_mfma(MfmaArgs a) {
     const int n0 = blockIdx.x * kTileN + 16 * w;
     const int row = min(n0 + ln, a.w.N - 1);
     const int m0 = blockIdx.y * BM;
-    const int nsteps = a.w.K / kStep;
+    // K steps [kb0, kb1) of this split
+    const int nsteps = a.w.K / kStep, ks = gridDim.z;
+    const int kb0 = int(blockIdx.z) * nsteps / ks, kb1 = (int(blockIdx.z) + 1) * nsteps / ks;
 
     // X staging: thread t owns row m0 + t / TPR, values [(t % TPR) FPT, +FPT) of the step
     const int xm = t / TPR, xk = (t % TPR) * FPT;
@@ -253,13 +258,13 @@ __global__ __launch_bounds__(256) void k_mfma(MfmaArgs a) {
     for (int mt = 0; mt < MT; ++mt) acc[mt] = f4_t{0.f, 0.f, 0.f, 0.f};
 
     typename W::Regs cur, nxt;
-    W::load(a.w, row, 0, kq, cur);
-    load_x(0);
-    for (int kb = 0; kb < nsteps; ++kb) {
-        if (kb) lds_barrier();  // the previous step's reads of xh / xl / xsum are done
+    W::load(a.w, row, kb0, kq, cur);
+    load_x(kb0);
+    for (int kb = kb0; kb < kb1; ++kb) {
+        if (kb != kb0) lds_barrier();  // the previous step's reads of xh / xl / xsum are done
         stage_x();
         lds_barrier();
-        if (kb + 1 < nsteps) {
+        if (kb + 1 < kb1) {
             W::load(a.w, row, kb + 1, kq, nxt);
             load_x(kb + 1);
         }
@@ -298,6 +303,17 @@ __global__ __launch_bounds__(256) void k_mfma(MfmaArgs a) {
     }
     const int n = n0 + ln;
     if (n >= a.w.N) return;
+    if (a.part) {
+        float *pp = a.part + size_t(blockIdx.z) * a.M * a.w.N;
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int m = m0 + mt * 16 + 4 * kq + r;
+                if (m < a.M) pp[size_t(m) * a.w.N + n] = acc[mt][r];
+            }
+        return;
+    }
     const float bv = a.bias ? a.bias[n] : 0.f;
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt)
@@ -312,17 +328,40 @@ __global__ __launch_bounds__(256) void k_mfma(MfmaArgs a) {
         }
 }
 
+// y[m][n] = sum_{z < ks} part[z][m][n] (in order) + bias[n] (+ R[m][n]) (relu)
+__global__ __launch_bounds__(256) void k_splitk_reduce(const float *part, int ks, int M, int N, const float *bias,
+                                                        const float *R, int ldr, int relu, float *y, int ldy) {
+    const size_t i = size_t(blockIdx.x) * 256 + threadIdx.x, mn = size_t(M) * N;
+    if (i >= mn) return;
+    const int m = int(i / N), n = int(i % N);
+    float v = part[i];
+    for (int z = 1; z < ks; ++z) v += part[size_t(z) * mn + i];
+    if (bias) v += bias[n];
+    if (R) v += R[size_t(m) * ldr + n];
+    if (relu) v = fmaxf(v, 0.f);
+    y[size_t(m) * ldy + n] = v;
+}
+
 template <int T>
-hipError_t launch(const MfmaArgs &a, int M, hipStream_t st) {
+hipError_t launch(const MfmaArgs &a, int M, int ks, hipStream_t st) {
     const int gx = (a.w.N + kTileN - 1) / kTileN;
     if (M <= 16) {
-        hipLaunchKernelGGL((k_mfma<T, 16>), dim3(gx, (M + 15) / 16), dim3(256), 0, st, a);
+        hipLaunchKernelGGL((k_mfma<T, 16>), dim3(gx, (M + 15) / 16, ks), dim3(256), 0, st, a);
     } else if (M <= 32) {
-        hipLaunchKernelGGL((k_mfma<T, 32>), dim3(gx, 1), dim3(256), 0, st, a);
+        hipLaunchKernelGGL((k_mfma<T, 32>), dim3(gx, 1, ks), dim3(256), 0, st, a);
     } else {
-        hipLaunchKernelGGL((k_mfma<T, 64>), dim3(gx, (M + 63) / 64), dim3(256), 0, st, a);
+        hipLaunchKernelGGL((k_mfma<T, 64>), dim3(gx, (M + 63) / 64, ks), dim3(256), 0, st, a);
     }
     return hipGetLastError();
+}
+
+// K splits that bring the grid to about one workgroup per CU, within the workspace
+int split_k(const DevMatrix &w, int M, size_t ws_bytes) {
+    const int gx = (w.N + kTileN - 1) / kTileN, bm = M <= 16 ? 16 : M <= 32 ? 32 : 64;
+    const int base = gx * ((M + bm - 1) / bm), nsteps = w.K / kStep;
+    int ks = base >= 256 ? 1 : std::min(nsteps, (256 + base - 1) / base);
+    while (ks > 1 && size_t(ks) * M * w.N * sizeof(float) > ws_bytes) --ks;
+    return ks;
 }
 
 }  // namespace
@@ -334,7 +373,7 @@ bool gemm_mfma_supported(const DevMatrix &w) {
 }
 
 hipError_t gemm_mfma(const DevMatrix &w, const float *X, int ldx, int M, float *Y, int ldy, const float *bias,
-                     bool relu, const float *R, int ldr, hipStream_t st) {
+                     bool relu, const float *R, int ldr, hipStream_t st, float *ws, size_t ws_bytes) {
     if (M <= 0) return hipSuccess;
     if (!gemm_mfma_supported(w) || ldx % 4 || reinterpret_cast<uintptr_t>(X) % 16) return hipErrorInvalidValue;
     MfmaArgs a{};
@@ -348,14 +387,22 @@ hipError_t gemm_mfma(const DevMatrix &w, const float *X, int ldx, int M, float *
     a.R = R;
     a.ldr = ldr;
     a.relu = relu ? 1 : 0;
+    const int ks = ws ? split_k(w, M, ws_bytes) : 1;
+    a.part = ks > 1 ? ws : nullptr;
+    hipError_t e;
     switch (w.type) {
-    case GGML_Q4_K: return launch<GGML_Q4_K>(a, M, st);
-    case GGML_Q5_K: return launch<GGML_Q5_K>(a, M, st);
-    case GGML_Q6_K: return launch<GGML_Q6_K>(a, M, st);
-    case GGML_Q8_0: return launch<GGML_Q8_0>(a, M, st);
-    case GGML_F16: return launch<GGML_F16>(a, M, st);
+    case GGML_Q4_K: e = launch<GGML_Q4_K>(a, M, ks, st); break;
+    case GGML_Q5_K: e = launch<GGML_Q5_K>(a, M, ks, st); break;
+    case GGML_Q6_K: e = launch<GGML_Q6_K>(a, M, ks, st); break;
+    case GGML_Q8_0: e = launch<GGML_Q8_0>(a, M, ks, st); break;
+    case GGML_F16: e = launch<GGML_F16>(a, M, ks, st); break;
     default: return hipErrorInvalidValue;
     }
+    if (e != hipSuccess || ks == 1) return e;
+    const size_t mn = size_t(M) * w.N;
+    hipLaunchKernelGGL(k_splitk_reduce, dim3(unsigned((mn + 255) / 256)), dim3(256), 0, st, ws, ks, M, w.N, bias, R,
+                       ldr, relu ? 1 : 0, Y, ldy);
+    return hipGetLastError();
 }
 
 }  // namespace mlg

@@ -43,14 +43,17 @@ int gemv_argmax_parts(const DevMatrix &w, int b);
 // Y[m][n] = sum_k X[m][k] W[n][k] + bias[n] (+ R[m][n]) (relu if set); any M.
 // Runs on the MFMA units when gemm_mfma_supported(w) (K % 256 == 0, quantized or
 // f16 weights), else on the SIMT kernel.
+// ws (optional, ws_bytes): workspace for split-K partial sums when M is small; the
+// partials are added in a fixed order.
 hipError_t gemm(const DevMatrix &w, const float *X, int ldx, int M, float *Y, int ldy, const float *bias, bool relu,
-                const float *R, int ldr, hipStream_t st);
+                const float *R, int ldr, hipStream_t st, float *ws = nullptr, size_t ws_bytes = 0);
 hipError_t gemm_simt(const DevMatrix &w, const float *X, int ldx, int M, float *Y, int ldy, const float *bias,
                      bool relu, const float *R, int ldr, hipStream_t st);
 bool gemm_mfma_supported(const DevMatrix &w);
 // X: ldx % 4 == 0, 16-byte aligned.
 hipError_t gemm_mfma(const DevMatrix &w, const float *X, int ldx, int M, float *Y, int ldy, const float *bias,
-                     bool relu, const float *R, int ldr, hipStream_t st);
+                     bool relu, const float *R, int ldr, hipStream_t st, float *ws = nullptr, size_t ws_bytes = 0);
+constexpr size_t kGemmWorkspaceBytes = size_t(16) << 20;  // split-K partial sums
 
 // Row LayerNorm (biased variance): out = (x - mean) * rsqrt(var + eps) * g + b.
 hipError_t layernorm(const float *x, int rows, int d, const float *g, const float *b, float eps, float *out,

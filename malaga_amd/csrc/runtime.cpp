@@ -121,6 +121,13 @@ bool layout_planes(uint32_t type, int N, int K, const uint8_t *src, uint8_t *out
     return true;
 }
 
+float *Context::gemm_workspace() {
+    if (!gemm_ws) gemm_ws = static_cast<float *>(dev_alloc(kGemmWorkspaceBytes, "GEMM workspace"));
+    return gemm_ws;
+}
+
+Context::~Context() { dev_free(gemm_ws); }
+
 // ------------------------------------------------------------------- model
 
 Batch::~Batch() {
@@ -283,7 +290,9 @@ void Model::matmul(const Linear &l, const float *x, int rows, float *y, bool rel
     if (!resid && rows <= gemv_max_batch(l.w)) {
         check_hip(gemv(l.w, x, l.w.K, rows, y, l.w.N, l.b, relu, st), "gemv");
     } else {
-        check_hip(gemm(l.w, x, l.w.K, rows, y, l.w.N, l.b, relu, resid, l.w.N, st), "gemm");
+        check_hip(gemm(l.w, x, l.w.K, rows, y, l.w.N, l.b, relu, resid, l.w.N, st, ctx->gemm_workspace(),
+                       kGemmWorkspaceBytes),
+                  "gemm");
     }
 }
 
@@ -473,7 +482,9 @@ void Model::lm_head(StaticState &st, bool greedy_mode, int mask_id) {
         if (B <= gemv_max_batch(embed)) {
             check_hip(gemv_argmax(embed, st.h, d, B, mask_id, st.pv, st.pi, &parts, s), "lm_head");
         } else {
-            check_hip(gemm(embed, st.h, d, B, st.logits, V, nullptr, false, nullptr, 0, s), "lm_head");
+            check_hip(gemm(embed, st.h, d, B, st.logits, V, nullptr, false, nullptr, 0, s, ctx->gemm_workspace(),
+                           kGemmWorkspaceBytes),
+                      "lm_head");
             check_hip(argmax_partial(st.logits, B, V, V, mask_id, st.pv, st.pi, parts, s), "argmax");
         }
         check_hip(greedy_finalize(st.pv, st.pi, parts, B, st.finished, st.ids, st.out, st.m, st.step,
@@ -483,7 +494,9 @@ void Model::lm_head(StaticState &st, bool greedy_mode, int mask_id) {
         if (B <= gemv_max_batch(embed))
             check_hip(gemv(embed, st.h, d, B, st.logits, V, nullptr, false, s), "lm_head");
         else
-            check_hip(gemm(embed, st.h, d, B, st.logits, V, nullptr, false, nullptr, 0, s), "lm_head");
+            check_hip(gemm(embed, st.h, d, B, st.logits, V, nullptr, false, nullptr, 0, s, ctx->gemm_workspace(),
+                           kGemmWorkspaceBytes),
+                      "lm_head");
         check_hip(inc_u32(st.step, s), "step");
     }
 }

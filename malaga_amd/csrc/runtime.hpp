@@ -37,6 +37,11 @@ struct Context {
     int device = 0;
     hipStream_t stream = nullptr;
     std::mutex mu;  // one caller at a time per context (src/graph.rs:152-155)
+    float *gemm_ws = nullptr;  // split-K workspace of the MFMA GEMM (kGemmWorkspaceBytes)
+    // Allocates the workspace on first use (never inside a graph capture: the first
+    // eager step or the encoder reaches it first).
+    float *gemm_workspace();
+    ~Context();
 };
 
 struct Linear {

@@ -88,10 +88,11 @@ def test_gemm_matches_dequantized_dot(ctx, t, N, K):
 
 
 @pytest.mark.parametrize("t,N,K", [(Q4_K, 200, 1024), (Q5_K, 130, 512), (Q6_K, 70, 2048), (Q8_0, 64, 768),
-                                   (F16, 90, 256)])
+                                   (F16, 90, 256), (Q4_K, 16400, 512)])
 def test_gemm_mfma_tiles_bias_relu_residual(ctx, t, N, K):
     """The MFMA GEMM (K % 256 == 0) over every X-tile size (16 / 32 / 64 rows), partial
-    tiles in M and N, with bias, ReLU and an in-place residual (R = Y)."""
+    tiles in M and N, with bias, ReLU and an in-place residual (R = Y); small grids
+    split K over workgroups (fixed-order reduction), N = 16400 runs unsplit."""
     rng = np.random.default_rng(31 + t)
     wf = rng.normal(0, 0.02, (N, K)).astype(np.float32)
     blocks = M.quantize(t, wf)
