@@ -288,12 +288,15 @@ struct NoPre {
 
 // Streams the rows of W; calls epi(row, bi, value) on the group-leader lane of each
 // row (value = dot product + bias[row], the bias fetched with the weights).  Waves
-// gwave, gwave + nwaves, ... share the rows.  Order of issue: pre() (loads the
+// gwave, gwave + nwaves, ... share the rows, G row groups per wave and step (two
+// steps in flight).  G = 1 halves the arithmetic on a wave's critical path (small
+// matrices, latency-bound); G = 2 keeps more bytes in flight (the LM head).
+// Order of issue: pre() (loads the
 // prologue needs, so that waiting for them does not wait for the weights: loads
 // complete in order), the first step's weights, then prologue(), which fills
 // xr/xs and may use workgroup barriers (every thread of the workgroup must call
 // this function).
-template <int T, int B, int CPL, bool NT = false, class PreF, class Pro, class Epi>
+template <int T, int B, int CPL, bool NT = false, int G = 2, class PreF, class Pro, class Epi>
 __device__ __forceinline__ void gemv_rows(const WPtr &w, const GemvGeom &g, float (&xr)[CPL][B][GTraits<T>::XW],
                                           float (&xs)[CPL][B][GTraits<T>::NS], int gwave, int nwaves, PreF &&pre,
                                           Pro &&prologue, Epi &epi, const float *bias = nullptr) {
@@ -304,18 +307,18 @@ __device__ __forceinline__ void gemv_rows(const WPtr &w, const GemvGeom &g, floa
 #pragma unroll
     for (int t = 0; t < CPL; ++t) cidx[t] = (cl + t * lpr < g.nchunks) ? cl + t * lpr : 0;
 
-    auto load_step = [&](int rg, Raw<T> (&r)[2][CPL], float (&bv)[2]) {
+    auto load_step = [&](int rg, Raw<T> (&r)[G][CPL], float (&bv)[G]) {
 #pragma unroll
-        for (int u = 0; u < 2; ++u) {
+        for (int u = 0; u < G; ++u) {
             const int row = min((rg + u * nwaves) * rpw + grp, w.N - 1);
 #pragma unroll
             for (int t = 0; t < CPL; ++t) load_chunk<T, NT>(w, row, cidx[t], r[u][t]);
             bv[u] = bias ? bias[row] : 0.f;
         }
     };
-    auto compute_step = [&](int rg, const Raw<T> (&r)[2][CPL], const float (&bv)[2]) {
+    auto compute_step = [&](int rg, const Raw<T> (&r)[G][CPL], const float (&bv)[G]) {
 #pragma unroll
-        for (int u = 0; u < 2; ++u) {
+        for (int u = 0; u < G; ++u) {
             float acc[B];
 #pragma unroll
             for (int bi = 0; bi < B; ++bi) acc[bi] = 0.f;
@@ -332,11 +335,13 @@ __device__ __forceinline__ void gemv_rows(const WPtr &w, const GemvGeom &g, floa
         }
     };
 
-    const int stride = 2 * nwaves;
+    const int stride = G * nwaves;
     int rg = gwave;
     const bool any = rg * rpw < w.N;  // wave-uniform
-    Raw<T> A[2][CPL], Bf[2][CPL];
-    float ba[2] = {0.f, 0.f}, bb[2] = {0.f, 0.f};
+    Raw<T> A[G][CPL], Bf[G][CPL];
+    float ba[G], bb[G];
+#pragma unroll
+    for (int u = 0; u < G; ++u) ba[u] = bb[u] = 0.f;
     pre();
     __builtin_amdgcn_sched_barrier(0);
     if (any) load_step(rg, A, ba);

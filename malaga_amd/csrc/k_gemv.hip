@@ -42,6 +42,8 @@ struct ArgmaxEpi {
     }
 };
 
+// MODE 0: store (G = 1: small, latency-bound matrices); MODE 2: store, G = 2 (large
+// matrices); MODE 1: LM head with argmax partials, G = 2, non-temporal weights.
 template <int T, int B, int CPL, int MODE>
 __global__ __launch_bounds__(256) void k_gemv(GemvArgs a) {
     constexpr int XW = GTraits<T>::XW, NS = GTraits<T>::NS;
@@ -52,7 +54,10 @@ __global__ __launch_bounds__(256) void k_gemv(GemvArgs a) {
     const int gwave = blockIdx.x * 4 + (threadIdx.x >> 6), nwaves = gridDim.x * 4;
     if constexpr (MODE == 0) {
         StoreEpi<B> epi{a};
-        gemv_rows<T, B, CPL>(a.w, a.g, xr, xs, gwave, nwaves, NoPre{}, load_x, epi, a.bias);
+        gemv_rows<T, B, CPL, false, 1>(a.w, a.g, xr, xs, gwave, nwaves, NoPre{}, load_x, epi, a.bias);
+    } else if constexpr (MODE == 2) {
+        StoreEpi<B> epi{a};
+        gemv_rows<T, B, CPL, false, 2>(a.w, a.g, xr, xs, gwave, nwaves, NoPre{}, load_x, epi, a.bias);
     } else {  // the LM head: weights streamed once per step
         ArgmaxEpi<B> epi{a, {}, {}};
 #pragma unroll
@@ -129,16 +134,18 @@ GemvArgs make_args(const DevMatrix &w, const GemvGeom &g, const float *x, int ld
     return a;
 }
 
+constexpr int kGemvSmallRows = 65536;
+
 }  // namespace
 
-int gemv_grid(const DevMatrix &w) {
+int gemv_grid(const DevMatrix &w, int G) {
     GemvGeom g;
     int cpl;
     if (!gemv_geometry(w, &g, &cpl)) return 0;
     const int rpw = 64 >> g.lpr_log2;
     const int groups = (w.N + rpw - 1) / rpw;
-    // two row groups per wave and step; a large matrix gets ~8 workgroups per CU
-    const int waves = (groups + 1) / 2;
+    // G row groups per wave and step; a large matrix gets ~8 workgroups per CU
+    const int waves = (groups + G - 1) / G;
     const int grid = (waves + 3) / 4;
     return grid < 1 ? 1 : (grid > 2048 ? 2048 : grid);
 }
@@ -166,7 +173,8 @@ hipError_t gemv(const DevMatrix &w, const float *x, int ldx, int b, float *y, in
     a.ldy = ldy;
     a.bias = bias;
     a.relu = relu ? 1 : 0;
-    return dispatch<0>(w.type, a, gemv_round_b(b), cpl, gemv_grid(w), st);
+    if (w.N <= kGemvSmallRows) return dispatch<0>(w.type, a, gemv_round_b(b), cpl, gemv_grid(w, 1), st);
+    return dispatch<2>(w.type, a, gemv_round_b(b), cpl, gemv_grid(w, 2), st);
 }
 
 int gemv_argmax_parts(const DevMatrix &w, int b) {

@@ -240,7 +240,7 @@ __global__ __launch_bounds__(256) void k_step(StepArgs a) {
             if (a.relu) v = fmaxf(v, 0.f);
             a.y[size_t(bi) * a.w.N + row] = v;
         };
-        gemv_rows<T, B, CPL>(a.w, a.g, xr, xs, gwave, nwaves, pre, prologue, epi, a.bias);
+        gemv_rows<T, B, CPL, false, 1>(a.w, a.g, xr, xs, gwave, nwaves, pre, prologue, epi, a.bias);
     } else {
         const uint32_t slot = *a.step;
         auto epi = [&](int row, int bi, float v) {
@@ -254,7 +254,7 @@ __global__ __launch_bounds__(256) void k_step(StepArgs a) {
                 (row < 2 * d ? a.kc : a.vc)[off] = __float2half(v);
             }
         };
-        gemv_rows<T, B, CPL>(a.w, a.g, xr, xs, gwave, nwaves, pre, prologue, epi, a.bias);
+        gemv_rows<T, B, CPL, false, 1>(a.w, a.g, xr, xs, gwave, nwaves, pre, prologue, epi, a.bias);
     }
 }
 
@@ -567,7 +567,7 @@ hipError_t step_qkv(const DevMatrix &w, const float *bias, int nb, int d, const 
     a.hd = hd;
     a.m = m;
     const size_t lds = sizeof(float) * size_t(nb) * d;
-    const int grid = gemv_grid(w);
+    const int grid = gemv_grid(w, 1);
     const int B = gemv_round_b(nb);
     if (!emb)
         return preloadable(a) ? dispatch_t<PRO_RESID_PRE, EPI_QKV, GGML_F32>(w.type, a, B, cpl, grid, lds, st)
@@ -632,8 +632,8 @@ hipError_t step_resid_proj(const DevMatrix &w, const float *bias, bool relu, int
     a.y = y;
     const size_t lds = sizeof(float) * size_t(nb) * d;
     return preloadable(a) ? dispatch_t<PRO_RESID_PRE, EPI_STORE, GGML_F32>(w.type, a, gemv_round_b(nb), cpl,
-                                                                        gemv_grid(w), lds, st)
-                          : dispatch_t<PRO_RESID, EPI_STORE, GGML_F32>(w.type, a, gemv_round_b(nb), cpl, gemv_grid(w),
+                                                                        gemv_grid(w, 1), lds, st)
+                          : dispatch_t<PRO_RESID, EPI_STORE, GGML_F32>(w.type, a, gemv_round_b(nb), cpl, gemv_grid(w, 1),
                                                                     lds, st);
 }
 
@@ -645,7 +645,7 @@ hipError_t step_proj(const DevMatrix &w, const float *bias, int nb, const float 
     a.ldx = w.K;
     a.bias = bias;
     a.y = y;
-    return dispatch_t<PRO_GLOBAL, EPI_STORE, GGML_F32>(w.type, a, gemv_round_b(nb), cpl, gemv_grid(w), 0, st);
+    return dispatch_t<PRO_GLOBAL, EPI_STORE, GGML_F32>(w.type, a, gemv_round_b(nb), cpl, gemv_grid(w, 1), 0, st);
 }
 
 }  // namespace mlg

@@ -28,7 +28,7 @@ size_t planes_bytes(uint32_t type, int N, int K);
 // Largest batch the register-resident GEMV handles for this matrix (0 if none).
 int gemv_max_batch(const DevMatrix &w);
 // Workgroups of a GEMV launch over w.
-int gemv_grid(const DevMatrix &w);
+int gemv_grid(const DevMatrix &w, int G = 2);  // G: row groups per wave and step
 
 // y[b][n] = sum_k x[b][k] W[n][k] (+ bias[n]) (relu if set).  b <= gemv_max_batch(w).
 hipError_t gemv(const DevMatrix &w, const float *x, int ldx, int b, float *y, int ldy, const float *bias, bool relu,

@@ -11,6 +11,9 @@ What it pins, independently of oracle/oracle.c:
     head): logits of Hugging Face transformers' M2M100ForConditionalGeneration
     (the model the reference validated against, spec/manual-tests.md MT-01) on
     the tiny test checkpoint, for teacher-forced target sequences.
+  * Greedy decoding (src/translator.rs:214-241): transformers' greedy search with
+    the target language forced as the first generated token, 20 tokens per source,
+    for target languages 255 and 256.
   * Q8_0: the same logits with every projection weight replaced by its Q8_0
     round trip (closed form: d = f16(amax / 127), q = round-half-away(x / d)),
     which pins the converter's Q8_0 quantizer and the oracle's Q8_0 dequantizer.
@@ -116,6 +119,41 @@ def hf_logits(weights: dict, src: list[list[int]], tgt: np.ndarray):
     return out.logits.float().numpy(), enc.float().numpy()
 
 
+def hf_greedy(weights: dict, src: list[list[int]], tgt_lang: int, max_new: int) -> np.ndarray:
+    """transformers' greedy search with the target language forced as the first token
+    (decoder_start = eos, src/translator.rs:214-241); no forced EOS, no length limits
+    other than max_new greedy tokens after the language token."""
+    from transformers import GenerationConfig, M2M100Config, M2M100ForConditionalGeneration
+
+    cfg = M2M100Config(vocab_size=V, d_model=D, encoder_layers=LAYERS, decoder_layers=LAYERS,
+                       encoder_attention_heads=H, decoder_attention_heads=H, encoder_ffn_dim=FFN,
+                       decoder_ffn_dim=FFN, max_position_embeddings=MAXPOS, scale_embedding=True,
+                       activation_function="relu", dropout=0.0, attention_dropout=0.0, activation_dropout=0.0,
+                       encoder_layerdrop=0.0, decoder_layerdrop=0.0, pad_token_id=1, bos_token_id=0,
+                       eos_token_id=2, decoder_start_token_id=2, tie_word_embeddings=True)
+    cfg._attn_implementation = "eager"
+    model = M2M100ForConditionalGeneration(cfg).eval()
+    sd = {k: torch.from_numpy(np.ascontiguousarray(v)) for k, v in weights.items()}
+    for k in ("model.encoder.embed_tokens.weight", "model.decoder.embed_tokens.weight", "lm_head.weight"):
+        sd[k] = sd["model.shared.weight"]
+    model.load_state_dict(sd, strict=False)
+    gen = GenerationConfig(decoder_start_token_id=2, forced_bos_token_id=tgt_lang, forced_eos_token_id=None,
+                           eos_token_id=2, pad_token_id=1, bos_token_id=0, num_beams=1, do_sample=False,
+                           max_new_tokens=max_new + 1, min_length=0)
+    out = np.full((len(src), max_new), -1, dtype=np.int64)
+    with torch.no_grad():
+        for i, r in enumerate(src):  # one sentence at a time: no padding involved
+            seq = model.generate(input_ids=torch.tensor([r]), generation_config=gen)[0].tolist()
+            assert seq[:2] == [2, tgt_lang], seq[:2]
+            toks = []
+            for t in seq[2:]:
+                if t == 2:
+                    break
+                toks.append(t)
+            out[i, : len(toks)] = toks
+    return out
+
+
 def main():
     rng = np.random.default_rng(1234)
     # [src_lang] tokens [eos] (src/translator.rs:90-98) with the tiny vocabulary:
@@ -135,7 +173,8 @@ def main():
     lens = np.array([len(r) for r in src], dtype=np.uint32)
     ids = np.array([t for r in src for t in r], dtype=np.uint32)
     np.savez_compressed(OUT, src_ids=ids, src_lens=lens, tgt=tgt.astype(np.uint32), logits_f32=logits,
-                        logits_q8_0=logits_q8, encoder_out=enc, xorshift_seed7_scale05=first)
+                        logits_q8_0=logits_q8, encoder_out=enc, xorshift_seed7_scale05=first,
+                        greedy_255_20=hf_greedy(w, src, 255, 20), greedy_256_20=hf_greedy(w, src, 256, 20))
     print(f"wrote {OUT} ({OUT.stat().st_size} bytes); logits {logits.shape}, |logits| max {np.abs(logits).max():.3f}")
 
 

@@ -3,6 +3,7 @@
 * Hugging Face transformers' M2M100 logits on the tiny test checkpoint
   (tests/golden/make_golden.py): pins the forward pass, the converter's layout
   (fused QKV, 1/sqrt(hd) pre-scale, tied embedding) and the Q8_0 codec.
+* transformers' greedy search on the same checkpoint: pins the greedy decode loop.
 * src/testutil.rs:57-69 xorshift stream (Python integer restatement).
 * src/model.rs:324-340 sinusoidal table against its closed form.
 """
@@ -23,6 +24,20 @@ def test_logits_match_transformers_m2m100(tiny_gguf, preset, key):
     assert np.abs(lg - ref).max() < 5e-5
     # the argmax at every position agrees (what greedy decoding consumes)
     assert (lg.argmax(-1) == ref.argmax(-1)).all()
+
+
+@pytest.mark.parametrize("tgt_lang", [255, 256])
+def test_greedy_matches_transformers_generate(tiny_gguf, tgt_lang):
+    """Greedy decoding with the target language forced after decoder_start
+    (src/translator.rs:214-241, src/graph.rs:255-297) against transformers' greedy
+    search on the same checkpoint (EOS masking off, 20 tokens, f32 caches)."""
+    g, src = golden_sources()
+    want = g[f"greedy_{tgt_lang}_20"]
+    m = O.Model(tiny_gguf("f32"))
+    for i, s in enumerate(src):
+        rows, _ = m.generate([s], tgt_lang, max_new_tokens=20, kv_f16=False)
+        ref = [int(t) for t in want[i] if t >= 0]
+        assert rows[0] == ref, (i, rows[0], ref)
 
 
 def test_encoder_output_matches_transformers(tiny_gguf):
