@@ -240,6 +240,18 @@ def bench_kernels(T, lm_blocks: np.ndarray):
     return rows, dict(residual_ln_1x1024_us=ln_us, argmax_partial_256206_us=argmax_us)
 
 
+def measured_traffic():
+    """HBM bytes per LM-head launch from the committed rocprofv3 counter summary
+    (FETCH_SIZE + WRITE_SIZE, calibrated on a copy kernel), or None."""
+    f = ROOT / "profiles" / "lm_head_q6k_traffic.txt"
+    if not f.exists():
+        return None
+    for line in f.read_text().splitlines():
+        if line.startswith("traffic_bytes_per_launch:"):
+            return int(line.split(":")[1])
+    return None
+
+
 def cpu_baseline():
     """oracle/ (C restatement of the reference's generic path) on the host cores, config 1."""
     import oracle as O
@@ -287,7 +299,15 @@ def main():
     if args.roofline_only:
         ctx = M._Ctx(0)
         r = GemvBench(ctx).run(14, lm_blocks, 256206, 1024, launches=200, argmax=True)
-        print(json.dumps({"kernel": "lm_head gemv_argmax q6_K 256206x1024", **r}))
+        # calibration for the HBM byte counters: a plain device copy of known size
+        n = 256 << 20
+        src_t, dst_t = torch.empty(n // 4, device="cuda"), torch.empty(n // 4, device="cuda")
+        src_t.fill_(1.0)
+        for _ in range(5):
+            dst_t.copy_(src_t)
+        torch.cuda.synchronize()
+        print(json.dumps({"kernel": "lm_head gemv_argmax q6_K 256206x1024", **r,
+                          "copy_calibration_bytes_read": n, "copy_calibration_bytes_written": n}))
         return
 
     legs = set(args.legs.split(","))
@@ -312,7 +332,7 @@ def main():
     gemv_rows, small = bench_kernels(T, lm_blocks)
     lm = gemv_rows[-1]
     roofline = dict(bound="hbm", achieved=round(lm["GBps"], 1), peak=PEAK_HBM_GBS, unit="GB/s",
-                    frac=round(lm["GBps"] / PEAK_HBM_GBS, 4), traffic=None,
+                    frac=round(lm["GBps"] / PEAK_HBM_GBS, 4), traffic=measured_traffic(),
                     kernel="k_gemv<q6_K,B=1,argmax> (LM head 256206x1024 + fused argmax partials)",
                     bytes_per_launch=lm["bytes"], us_per_launch=round(lm["us"], 3))
     q4_lm = next(r for r in gemv_rows if r["type"] == "q4_K" and r["name"] == "lm_head")
