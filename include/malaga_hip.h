@@ -145,6 +145,10 @@ int mlg_gemm(const mlg_matrix *w, const float *x, int M, float *y, const float *
  * projections that precede them. */
 int mlg_gemm_resid(const mlg_matrix *w, const float *x, int M, float *y, const float *bias, int relu, const float *r,
                    void *stream);
+/* The same for decode batches of up to 32 rows on the MFMA units (X resident in LDS):
+ * partials [M][mlg_gemm_argmax_parts(w, M)]. */
+int mlg_gemm_argmax_parts(const mlg_matrix *w, int M);
+int mlg_gemm_argmax(const mlg_matrix *w, const float *x, int M, int mask_id, float *pv, uint32_t *pi, void *stream);
 /* LM head + first argmax pass (kernels/malaga.cu:247-280 fused into the GEMV). */
 int mlg_gemv_argmax_parts(const mlg_matrix *w, int b);
 int mlg_gemv_argmax(const mlg_matrix *w, const float *x, int b, int mask_id, float *pv, uint32_t *pi, void *stream);

@@ -87,6 +87,8 @@ SIGNATURES = {
     "mlg_gemv_max_batch": (C.c_int, [_P]),
     "mlg_gemm": (C.c_int, [_P, _P, C.c_int, _P, _P, C.c_int, _P]),
     "mlg_gemm_resid": (C.c_int, [_P, _P, C.c_int, _P, _P, C.c_int, _P, _P]),
+    "mlg_gemm_argmax_parts": (C.c_int, [_P, C.c_int]),
+    "mlg_gemm_argmax": (C.c_int, [_P, _P, C.c_int, C.c_int, _P, _P, _P]),
     "mlg_gemv_argmax_parts": (C.c_int, [_P, C.c_int]),
     "mlg_gemv_argmax": (C.c_int, [_P, _P, C.c_int, C.c_int, _P, _P, _P]),
     "mlg_residual_ln": (C.c_int, [_P, _P, C.c_int, C.c_int, _P, _P, C.c_float, _P, _P]),

@@ -355,6 +355,63 @@ hipError_t launch(const MfmaArgs &a, int M, int ks, hipStream_t st) {
     return hipGetLastError();
 }
 
+// Split-K reduction fused with the decoder's residual add and the next LayerNorm
+// (src/model.rs:183-187): y = sum_z part[z][m] (in order) + bias; x[m] += y;
+// h[m] = LayerNorm(x[m]) with biased variance.  One workgroup per row, N <= 4096.
+__global__ __launch_bounds__(256) void k_splitk_residual_ln(const float *part, int ks, int M, int N,
+                                                             const float *bias, float *x, const float *g,
+                                                             const float *b, float eps, float *h) {
+    __shared__ float sh[16];
+    const int m = blockIdx.x, t = threadIdx.x;
+    const size_t mn = size_t(M) * N, off = size_t(m) * N;
+    float v[16];
+    float s1 = 0.f;
+#pragma unroll
+    for (int k = 0; k < 16; ++k) {
+        const int i = t + 256 * k;
+        v[k] = 0.f;
+        if (i < N) {
+            float y = part[off + i];
+            for (int z = 1; z < ks; ++z) y += part[size_t(z) * mn + off + i];
+            if (bias) y += bias[i];
+            v[k] = x[off + i] + y;
+            x[off + i] = v[k];
+            s1 += v[k];
+        }
+    }
+    const float mean = block_sum(s1, sh) / float(N);
+    float s2 = 0.f;
+#pragma unroll
+    for (int k = 0; k < 16; ++k)
+        if (t + 256 * k < N) s2 += (v[k] - mean) * (v[k] - mean);
+    const float rstd = rsqrtf(block_sum(s2, sh) / float(N) + eps);
+#pragma unroll
+    for (int k = 0; k < 16; ++k) {
+        const int i = t + 256 * k;
+        if (i < N) h[off + i] = (v[k] - mean) * rstd * g[i] + b[i];
+    }
+}
+
+// Split-K reduction of the fused QKV projection written straight into q [M][d] and
+// the f16 caches at slot *step (kernels/malaga.cu:142-154).
+__global__ __launch_bounds__(256) void k_splitk_qkv(const float *part, int ks, int M, int d, const float *bias, int H,
+                                                     int hd, int slots, const uint32_t *step, float *q, __half *kc,
+                                                     __half *vc) {
+    const size_t i = size_t(blockIdx.x) * 256 + threadIdx.x, N = size_t(3) * d, mn = size_t(M) * N;
+    if (i >= mn) return;
+    const int m = int(i / N), c = int(i % N);
+    float v = part[i];
+    for (int z = 1; z < ks; ++z) v += part[size_t(z) * mn + i];
+    if (bias) v += bias[c];
+    if (c < d) {
+        q[size_t(m) * d + c] = v;
+    } else {
+        const int cc = c < 2 * d ? c - d : c - 2 * d;
+        const size_t o = ((size_t(m) * H + cc / hd) * slots + *step) * hd + cc % hd;
+        (c < 2 * d ? kc : vc)[o] = __float2half(v);
+    }
+}
+
 // K splits that bring the grid to about one workgroup per CU, within the workspace
 int split_k(const DevMatrix &w, int M, size_t ws_bytes) {
     const int gx = (w.N + kTileN - 1) / kTileN, bm = M <= 16 ? 16 : M <= 32 ? 32 : 64;
@@ -362,6 +419,263 @@ int split_k(const DevMatrix &w, int M, size_t ws_bytes) {
     int ks = base >= 256 ? 1 : std::min(nsteps, (256 + base - 1) / base);
     while (ks > 1 && size_t(ks) * M * w.N * sizeof(float) > ws_bytes) --ks;
     return ks;
+}
+
+// ---------------------------------------------------------------- resident X
+//
+// Decode batches (M <= 32) with K small enough that all of X fits in LDS as hi/lo
+// f16 (BM * K * 4 bytes <= ~140 KB): one persistent workgroup of 8 waves per CU
+// stages X once, then every wave streams 16-row tiles of W (tile t, t + waves, ...)
+// with the next (tile, K-step) in flight in registers.  No split K, no reduction
+// kernel, and X is read from HBM/L2 once per workgroup instead of once per tile.
+// MODE 0 stores Y (bias, residual, ReLU); MODE 1 keeps a running argmax per X row
+// (the greedy LM head) and writes one partial per wave.
+
+constexpr int kRxWaves = 8;
+constexpr int kRxDepth = 2;  // (group, K-step) jobs of W in flight per wave
+// 16-row tiles of W per job (reuse of each X fragment), sized to the registers a
+// type's raw K step needs
+template <int T>
+constexpr int rx_nt() { return T == GGML_F16 ? 1 : T == GGML_Q8_0 ? 2 : 4; }
+constexpr size_t kRxMaxLds = 150 * 1024;
+
+struct RxArgs {
+    WPtr w;
+    const float *x;
+    int ldx, M;
+    float *y;
+    int ldy;
+    const float *bias, *R;
+    int ldr, relu;
+    int mask_id;      // MODE 1: row index never selected (-1: none)
+    float *pv;        // MODE 1: partials [M][parts]
+    uint32_t *pi;
+    int parts;
+};
+
+__host__ __device__ constexpr int rx_stride(int K) { return K + 8; }  // halves per staged X row
+
+size_t rx_lds_bytes(int BM, int K) {
+    return size_t(BM) * rx_stride(K) * 2 * sizeof(_Float16) + size_t(K / 16) * BM * sizeof(float);
+}
+
+template <int T, int BM, int MODE>
+__global__ __launch_bounds__(kRxWaves * 64) void k_mfma_rx(RxArgs a) {
+    using W = MW<T>;
+    constexpr int MT = BM / 16;
+    constexpr int kRxNT = rx_nt<T>();
+    extern __shared__ __align__(16) unsigned char rx_lds[];
+    const int K = a.w.K, XS = rx_stride(K);
+    _Float16 *xh = reinterpret_cast<_Float16 *>(rx_lds);
+    _Float16 *xl = xh + BM * XS;
+    float *xsum = reinterpret_cast<float *>(xl + BM * XS);  // [K / 16][BM]
+    const int t = threadIdx.x, lane = t & 63;
+    const int kq = lane >> 4, ln = lane & 15;
+    const int nsteps = K / kStep;
+    const int ngroups = (a.w.N + 16 * kRxNT - 1) / (16 * kRxNT);  // groups of kRxNT 16-row tiles
+    const int gw = blockIdx.x * kRxWaves + (t >> 6), nw = gridDim.x * kRxWaves;
+    const int njobs = gw < ngroups ? ((ngroups - 1 - gw) / nw + 1) * nsteps : 0;  // (group, step) pairs of this wave
+
+    // the first kRxDepth (group, K-step) jobs of W in flight before X is staged
+    typename W::Regs ring[kRxDepth][kRxNT];
+    auto job_base = [&](int j) { return (gw + (j / nsteps) * nw) * 16 * kRxNT; };
+    auto load_job = [&](int j, typename W::Regs (&r)[kRxNT]) {
+#pragma unroll
+        for (int nt = 0; nt < kRxNT; ++nt)
+            W::load(a.w, min(job_base(j) + nt * 16 + ln, a.w.N - 1), j % nsteps, kq, r[nt]);
+    };
+#pragma unroll
+    for (int u = 0; u < kRxDepth; ++u)
+        if (u < njobs) load_job(u, ring[u]);
+
+    // stage X: chunks of 16 values, up to 4 per thread in flight
+    {
+        const int cpr = K / 16, nch = BM * cpr;
+        for (int c0 = t; c0 < nch; c0 += kRxWaves * 64 * 4) {
+            float4 v[4][4];
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const int c = c0 + u * kRxWaves * 64;
+                const int m = c / cpr, k0 = (c % cpr) * 16;
+                const bool ok = c < nch && m < a.M;
+                const float *src = a.x + size_t(ok ? m : 0) * a.ldx + (ok ? k0 : 0);
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+                    v[u][i] = ok ? reinterpret_cast<const float4 *>(src)[i] : make_float4(0.f, 0.f, 0.f, 0.f);
+            }
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const int c = c0 + u * kRxWaves * 64;
+                if (c >= nch) break;
+                const int m = c / cpr, k0 = (c % cpr) * 16;
+                float sum = 0.f;
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const float e[4] = {v[u][i].x, v[u][i].y, v[u][i].z, v[u][i].w};
+                    _Float16 hv[4], lv[4];
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) {
+                        hv[q] = _Float16(e[q]);
+                        lv[q] = _Float16(e[q] - float(hv[q]));
+                    }
+                    *reinterpret_cast<h4_t *>(xh + m * XS + k0 + 4 * i) = h4_t{hv[0], hv[1], hv[2], hv[3]};
+                    *reinterpret_cast<h4_t *>(xl + m * XS + k0 + 4 * i) = h4_t{lv[0], lv[1], lv[2], lv[3]};
+                    sum += (e[0] + e[1]) + (e[2] + e[3]);
+                }
+                xsum[(k0 >> 4) * BM + m] = sum;
+            }
+        }
+    }
+    __syncthreads();
+
+    f4_t acc[MT][kRxNT];
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+        for (int nt = 0; nt < kRxNT; ++nt) acc[mt][nt] = f4_t{0.f, 0.f, 0.f, 0.f};
+    float best[MT][4];
+    uint32_t bidx[MT][4];
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            best[mt][r] = -INFINITY;
+            bidx[mt][r] = 0xffffffffu;
+        }
+
+    // job j uses ring slot j % kRxDepth, refilled with job j + kRxDepth once consumed;
+    // each X fragment read from LDS feeds kRxNT tiles of W
+    auto job = [&](int j, const typename W::Regs (&cur)[kRxNT]) {
+        const int kb = j % nsteps;
+#pragma unroll
+        for (int s = 0; s < W::SLICES; ++s) {
+            float sc[kRxNT], mn[kRxNT];
+            decltype(W::b(cur[0], s)) bop[kRxNT];
+#pragma unroll
+            for (int nt = 0; nt < kRxNT; ++nt) {
+                W::scale(cur[nt], s, sc[nt], mn[nt]);
+                bop[nt] = W::b(cur[nt], s);
+            }
+            const int kx = kb * kStep + s * W::SK;
+#pragma unroll
+            for (int mt = 0; mt < MT; ++mt) {
+                const int xo = (mt * 16 + ln) * XS + kx + kq * (W::SK / 4);
+                const float *xsp = xsum + (kx >> 4) * BM + mt * 16 + 4 * kq;
+                float4 xsv = *reinterpret_cast<const float4 *>(xsp);
+                if constexpr (W::SK == 32) {
+                    const float4 x2 = *reinterpret_cast<const float4 *>(xsp + BM);
+                    xsv = make_float4(xsv.x + x2.x, xsv.y + x2.y, xsv.z + x2.z, xsv.w + x2.w);
+                }
+                if constexpr (W::SK == 32) {
+                    const h8_t ah = *reinterpret_cast<const h8_t *>(xh + xo), al = *reinterpret_cast<const h8_t *>(xl + xo);
+#pragma unroll
+                    for (int nt = 0; nt < kRxNT; ++nt) {
+                        f4_t tmp = f4_t{0.f, 0.f, 0.f, 0.f};
+                        tmp = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bop[nt], tmp, 0, 0, 0);
+                        tmp = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, bop[nt], tmp, 0, 0, 0);
+#pragma unroll
+                        for (int r = 0; r < 4; ++r)
+                            acc[mt][nt][r] = fmaf(sc[nt], tmp[r], fmaf(-mn[nt], (&xsv.x)[r], acc[mt][nt][r]));
+                    }
+                } else {
+                    const h4_t ah = *reinterpret_cast<const h4_t *>(xh + xo), al = *reinterpret_cast<const h4_t *>(xl + xo);
+#pragma unroll
+                    for (int nt = 0; nt < kRxNT; ++nt) {
+                        f4_t tmp = f4_t{0.f, 0.f, 0.f, 0.f};
+                        tmp = __builtin_amdgcn_mfma_f32_16x16x16f16(ah, bop[nt], tmp, 0, 0, 0);
+                        tmp = __builtin_amdgcn_mfma_f32_16x16x16f16(al, bop[nt], tmp, 0, 0, 0);
+#pragma unroll
+                        for (int r = 0; r < 4; ++r)
+                            acc[mt][nt][r] = fmaf(sc[nt], tmp[r], fmaf(-mn[nt], (&xsv.x)[r], acc[mt][nt][r]));
+                    }
+                }
+            }
+        }
+        if (kb == nsteps - 1) {  // group done
+#pragma unroll
+            for (int nt = 0; nt < kRxNT; ++nt) {
+                const int n = job_base(j) + nt * 16 + ln;
+                if (n < a.w.N) {
+                    const float bv = a.bias ? a.bias[n] : 0.f;
+#pragma unroll
+                    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+                        for (int r = 0; r < 4; ++r) {
+                            const int m = mt * 16 + 4 * kq + r;
+                            float v = acc[mt][nt][r] + bv;
+                            if constexpr (MODE == 0) {
+                                if (m < a.M) {
+                                    if (a.R) v += a.R[size_t(m) * a.ldr + n];
+                                    if (a.relu) v = fmaxf(v, 0.f);
+                                    a.y[size_t(m) * a.ldy + n] = v;
+                                }
+                            } else {
+                                if (n != a.mask_id) argmax_merge(best[mt][r], bidx[mt][r], v, uint32_t(n));
+                            }
+                        }
+                }
+#pragma unroll
+                for (int mt = 0; mt < MT; ++mt) acc[mt][nt] = f4_t{0.f, 0.f, 0.f, 0.f};
+            }
+        }
+    };
+    for (int j0 = 0; j0 < njobs; j0 += kRxDepth) {
+#pragma unroll
+        for (int u = 0; u < kRxDepth; ++u) {
+            const int j = j0 + u;
+            if (j >= njobs) break;  // wave-uniform
+            job(j, ring[u]);
+            if (j + kRxDepth < njobs) load_job(j + kRxDepth, ring[u]);
+        }
+    }
+    if constexpr (MODE == 1) {
+        // lanes 16 kq .. 16 kq + 15 hold the same X rows: reduce within each 16-lane row
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                float v = best[mt][r];
+                uint32_t i = bidx[mt][r];
+                argmax_merge(v, i, dpp_mov<kDppXor1>(v), dpp_mov<kDppXor1>(i));
+                argmax_merge(v, i, dpp_mov<kDppXor2>(v), dpp_mov<kDppXor2>(i));
+                argmax_merge(v, i, dpp_mov<kDppHalfMirror>(v), dpp_mov<kDppHalfMirror>(i));
+                argmax_merge(v, i, dpp_mov<kDppMirror>(v), dpp_mov<kDppMirror>(i));
+                const int m = mt * 16 + 4 * kq + r;
+                if (ln == 0 && m < a.M) {
+                    a.pv[size_t(m) * a.parts + gw] = v;
+                    a.pi[size_t(m) * a.parts + gw] = i;
+                }
+            }
+    }
+}
+
+// Dynamic LDS beyond 64 KB needs the kernel attribute raised once.
+template <int T, int BM, int MODE>
+hipError_t launch_rx_bm(const RxArgs &a, int grid, hipStream_t st) {
+    static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void *>(&k_mfma_rx<T, BM, MODE>),
+                                                       hipFuncAttributeMaxDynamicSharedMemorySize, int(kRxMaxLds));
+    if (attr != hipSuccess) return attr;
+    hipLaunchKernelGGL((k_mfma_rx<T, BM, MODE>), dim3(grid), dim3(kRxWaves * 64), rx_lds_bytes(BM, a.w.K), st, a);
+    return hipGetLastError();
+}
+
+template <int T, int MODE>
+hipError_t launch_rx(const RxArgs &a, int M, int grid, hipStream_t st) {
+    return M <= 16 ? launch_rx_bm<T, 16, MODE>(a, grid, st) : launch_rx_bm<T, 32, MODE>(a, grid, st);
+}
+
+int rx_nt_of(uint32_t t) {
+    return t == GGML_F16 ? rx_nt<GGML_F16>() : t == GGML_Q8_0 ? rx_nt<GGML_Q8_0>() : rx_nt<GGML_Q4_K>();
+}
+
+int rx_grid(const DevMatrix &w, int M) {
+    const int bm = M <= 16 ? 16 : 32;
+    const size_t lds = rx_lds_bytes(bm, w.K);
+    const int per_cu = lds * 2 <= 160 * 1024 ? 2 : 1;
+    const int nt = rx_nt_of(w.type);
+    const int groups = (w.N + 16 * nt - 1) / (16 * nt);
+    const int waves = std::min(groups, 256 * per_cu * kRxWaves);
+    return (waves + kRxWaves - 1) / kRxWaves;
 }
 
 }  // namespace
@@ -372,10 +686,67 @@ bool gemm_mfma_supported(const DevMatrix &w) {
     return type_ok && w.K % kStep == 0 && w.N > 0;
 }
 
+bool gemm_rx_supported(const DevMatrix &w, int M) {
+    return gemm_mfma_supported(w) && M >= 1 && M <= 32 && rx_lds_bytes(M <= 16 ? 16 : 32, w.K) <= kRxMaxLds;
+}
+
+// Stored products take the resident-X kernel only when W is large enough to keep
+// every CU busy (staging X per workgroup is then amortised); smaller matrices use
+// the split-K tile kernel.
+constexpr int kRxMinRows = 65536;
+
+namespace {
+template <int MODE>
+hipError_t run_rx(const DevMatrix &w, RxArgs &a, int M, int grid, hipStream_t st) {
+    switch (w.type) {
+    case GGML_Q4_K: return launch_rx<GGML_Q4_K, MODE>(a, M, grid, st);
+    case GGML_Q5_K: return launch_rx<GGML_Q5_K, MODE>(a, M, grid, st);
+    case GGML_Q6_K: return launch_rx<GGML_Q6_K, MODE>(a, M, grid, st);
+    case GGML_Q8_0: return launch_rx<GGML_Q8_0, MODE>(a, M, grid, st);
+    case GGML_F16: return launch_rx<GGML_F16, MODE>(a, M, grid, st);
+    default: return hipErrorInvalidValue;
+    }
+}
+RxArgs rx_args(const DevMatrix &w, const float *X, int ldx, int M) {
+    RxArgs a{};
+    a.w = wptr_of(w);
+    a.x = X;
+    a.ldx = ldx;
+    a.M = M;
+    a.mask_id = -1;
+    return a;
+}
+}  // namespace
+
+int gemm_argmax_parts(const DevMatrix &w, int M) { return rx_grid(w, M) * kRxWaves; }
+
+hipError_t gemm_argmax(const DevMatrix &w, const float *X, int ldx, int M, int mask_id, float *pv, uint32_t *pi,
+                       int *parts, hipStream_t st) {
+    if (!gemm_rx_supported(w, M) || ldx % 4 || reinterpret_cast<uintptr_t>(X) % 16) return hipErrorInvalidValue;
+    RxArgs a = rx_args(w, X, ldx, M);
+    a.mask_id = mask_id;
+    a.pv = pv;
+    a.pi = pi;
+    const int grid = rx_grid(w, M);
+    a.parts = grid * kRxWaves;
+    *parts = a.parts;
+    return run_rx<1>(w, a, M, grid, st);
+}
+
 hipError_t gemm_mfma(const DevMatrix &w, const float *X, int ldx, int M, float *Y, int ldy, const float *bias,
                      bool relu, const float *R, int ldr, hipStream_t st, float *ws, size_t ws_bytes) {
     if (M <= 0) return hipSuccess;
     if (!gemm_mfma_supported(w) || ldx % 4 || reinterpret_cast<uintptr_t>(X) % 16) return hipErrorInvalidValue;
+    if (gemm_rx_supported(w, M) && w.N >= kRxMinRows) {
+        RxArgs r = rx_args(w, X, ldx, M);
+        r.y = Y;
+        r.ldy = ldy;
+        r.bias = bias;
+        r.R = R;
+        r.ldr = ldr;
+        r.relu = relu ? 1 : 0;
+        return run_rx<0>(w, r, M, rx_grid(w, M), st);
+    }
     MfmaArgs a{};
     a.w = wptr_of(w);
     a.x = X;
@@ -403,6 +774,73 @@ hipError_t gemm_mfma(const DevMatrix &w, const float *X, int ldx, int M, float *
     hipLaunchKernelGGL(k_splitk_reduce, dim3(unsigned((mn + 255) / 256)), dim3(256), 0, st, ws, ks, M, w.N, bias, R,
                        ldr, relu ? 1 : 0, Y, ldy);
     return hipGetLastError();
+}
+
+
+namespace {
+// Runs the tile kernel with K split over workgroups into ws; returns the split
+// count (1: not split, nothing launched).
+int launch_split(const DevMatrix &w, const float *X, int ldx, int M, hipStream_t st, float *ws, size_t ws_bytes,
+                 hipError_t *err) {
+    *err = hipSuccess;
+    if (!ws || !gemm_mfma_supported(w) || ldx % 4 || reinterpret_cast<uintptr_t>(X) % 16) return 1;
+    if (gemm_rx_supported(w, M) && w.N >= kRxMinRows) return 1;
+    const int ks = split_k(w, M, ws_bytes);
+    if (ks <= 1) return 1;
+    MfmaArgs a{};
+    a.w = wptr_of(w);
+    a.x = X;
+    a.ldx = ldx;
+    a.M = M;
+    a.part = ws;
+    switch (w.type) {
+    case GGML_Q4_K: *err = launch<GGML_Q4_K>(a, M, ks, st); break;
+    case GGML_Q5_K: *err = launch<GGML_Q5_K>(a, M, ks, st); break;
+    case GGML_Q6_K: *err = launch<GGML_Q6_K>(a, M, ks, st); break;
+    case GGML_Q8_0: *err = launch<GGML_Q8_0>(a, M, ks, st); break;
+    case GGML_F16: *err = launch<GGML_F16>(a, M, ks, st); break;
+    default: return 1;
+    }
+    return ks;
+}
+}  // namespace
+
+hipError_t gemm_residual_ln(const DevMatrix &w, const float *X, int ldx, int M, const float *bias, float *x,
+                            const float *g, const float *b, float eps, float *h, hipStream_t st, float *ws,
+                            size_t ws_bytes) {
+    if (M <= 0) return hipSuccess;
+    if (w.N > 4096) return hipErrorInvalidValue;
+    hipError_t e;
+    const int ks = launch_split(w, X, ldx, M, st, ws, ws_bytes, &e);
+    if (e != hipSuccess) return e;
+    if (ks > 1) {
+        hipLaunchKernelGGL(k_splitk_residual_ln, dim3(M), dim3(256), 0, st, ws, ks, M, w.N, bias, x, g, b, eps, h);
+        return hipGetLastError();
+    }
+    // x = x + X W^T + bias in place (R = Y = x), then the LayerNorm
+    e = gemm(w, X, ldx, M, x, w.N, bias, false, x, w.N, st, ws, ws_bytes);
+    if (e != hipSuccess) return e;
+    return layernorm(x, M, w.N, g, b, eps, h, st);
+}
+
+hipError_t gemm_qkv(const DevMatrix &w, const float *X, int ldx, int M, const float *bias, int H, int hd, int slots,
+                    const uint32_t *step, float *q, __half *kc, __half *vc, float *qkv_tmp, hipStream_t st, float *ws,
+                    size_t ws_bytes) {
+    if (M <= 0) return hipSuccess;
+    const int d = H * hd;
+    if (w.N != 3 * d) return hipErrorInvalidValue;
+    hipError_t e;
+    const int ks = launch_split(w, X, ldx, M, st, ws, ws_bytes, &e);
+    if (e != hipSuccess) return e;
+    if (ks > 1) {
+        const size_t n = size_t(M) * w.N;
+        hipLaunchKernelGGL(k_splitk_qkv, dim3(unsigned((n + 255) / 256)), dim3(256), 0, st, ws, ks, M, d, bias, H, hd,
+                           slots, step, q, kc, vc);
+        return hipGetLastError();
+    }
+    e = gemm(w, X, ldx, M, qkv_tmp, w.N, bias, false, nullptr, 0, st, ws, ws_bytes);
+    if (e != hipSuccess) return e;
+    return qkv_split(qkv_tmp, M, H, hd, slots, step, q, kc, vc, st);
 }
 
 }  // namespace mlg

@@ -273,11 +273,12 @@ __global__ __launch_bounds__(256) void k_argmax_partial(const float *logits, int
     }
 }
 
-// kernels/malaga.cu:290-326 semantics, without the shortlist mapping.  Each row's
-// partials are reduced by the whole workgroup (8 independent loads per thread).
-__global__ __launch_bounds__(256) void k_greedy_finalize(const float *pv, const uint32_t *pi, int P, int b,
-                                                         uint8_t *finished, uint32_t *ids, uint32_t *out, int m,
-                                                         uint32_t *step, uint32_t eos, uint32_t pad) {
+// kernels/malaga.cu:290-326 semantics, without the shortlist mapping.
+// Small batches: each row's partials are reduced by the whole workgroup (8
+// independent loads per thread).
+__global__ __launch_bounds__(256) void k_greedy_finalize_wg(const float *pv, const uint32_t *pi, int P, int b,
+                                                            uint8_t *finished, uint32_t *ids, uint32_t *out, int m,
+                                                            uint32_t *step, uint32_t eos, uint32_t pad) {
     __shared__ float sv[4];
     __shared__ uint32_t si[4];
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
@@ -315,6 +316,41 @@ __global__ __launch_bounds__(256) void k_greedy_finalize(const float *pv, const 
         }
         __syncthreads();
     }
+    if (threadIdx.x == 0) *step = s + 1;
+}
+
+// Larger batches: one wave per row (rows w, w + 16, ...), 8 independent loads per
+// lane in flight; the step counter is advanced after every wave has read it.
+__global__ __launch_bounds__(1024) void k_greedy_finalize(const float *pv, const uint32_t *pi, int P, int b,
+                                                          uint8_t *finished, uint32_t *ids, uint32_t *out, int m,
+                                                          uint32_t *step, uint32_t eos, uint32_t pad) {
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, nw = blockDim.x >> 6;
+    const uint32_t s = *step;
+    for (int row = w; row < b; row += nw) {  // wave-uniform
+        float best = -INFINITY;
+        uint32_t bi = 0xffffffffu;
+        for (int p0 = lane; p0 < P; p0 += 64 * 8) {
+            float v[8];
+            uint32_t ix[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+                const int p = p0 + u * 64;
+                v[u] = p < P ? pv[size_t(row) * P + p] : -INFINITY;
+                ix[u] = p < P ? pi[size_t(row) * P + p] : 0xffffffffu;
+            }
+#pragma unroll
+            for (int u = 0; u < 8; ++u) argmax_merge(best, bi, v[u], ix[u]);
+        }
+        wave_argmax(best, bi);
+        if (lane == 0) {
+            uint32_t tok = bi;
+            if (finished[row]) tok = pad;
+            if (tok == eos) finished[row] = 1;
+            ids[row] = tok;
+            out[size_t(row) * m + s] = tok;
+        }
+    }
+    __syncthreads();
     if (threadIdx.x == 0) *step = s + 1;
 }
 
@@ -545,8 +581,12 @@ hipError_t argmax_partial(const float *logits, int b, int V, int ldl, int mask_i
 
 hipError_t greedy_finalize(const float *pv, const uint32_t *pi, int parts, int b, uint8_t *finished, uint32_t *ids,
                            uint32_t *out, int m, uint32_t *step, uint32_t eos, uint32_t pad, hipStream_t st) {
-    hipLaunchKernelGGL(k_greedy_finalize, dim3(1), dim3(256), 0, st, pv, pi, parts, b, finished, ids, out, m, step,
-                       eos, pad);
+    if (b <= 4)
+        hipLaunchKernelGGL(k_greedy_finalize_wg, dim3(1), dim3(256), 0, st, pv, pi, parts, b, finished, ids, out, m,
+                           step, eos, pad);
+    else
+        hipLaunchKernelGGL(k_greedy_finalize, dim3(1), dim3(1024), 0, st, pv, pi, parts, b, finished, ids, out, m,
+                           step, eos, pad);
     return hipGetLastError();
 }
 

@@ -54,6 +54,23 @@ bool gemm_mfma_supported(const DevMatrix &w);
 hipError_t gemm_mfma(const DevMatrix &w, const float *X, int ldx, int M, float *Y, int ldy, const float *bias,
                      bool relu, const float *R, int ldr, hipStream_t st, float *ws = nullptr, size_t ws_bytes = 0);
 constexpr size_t kGemmWorkspaceBytes = size_t(16) << 20;  // split-K partial sums
+// Decoder-layer products of batches too large for the register GEMV: the split-K
+// reduction folds in the residual add and the next LayerNorm (x += X W^T + bias;
+// h = LayerNorm(x), N <= 4096), or the q / f16 K / V split of the fused QKV
+// projection (q [M][d], caches at slot *step; qkv_tmp [M][3d] when K is not split).
+hipError_t gemm_residual_ln(const DevMatrix &w, const float *X, int ldx, int M, const float *bias, float *x,
+                            const float *g, const float *b, float eps, float *h, hipStream_t st, float *ws,
+                            size_t ws_bytes);
+hipError_t gemm_qkv(const DevMatrix &w, const float *X, int ldx, int M, const float *bias, int H, int hd, int slots,
+                    const uint32_t *step, float *q, __half *kc, __half *vc, float *qkv_tmp, hipStream_t st, float *ws,
+                    size_t ws_bytes);
+// M <= 32 rows with X resident in LDS (K <= 1024 at M > 16, K <= 2048 at M <= 16).
+bool gemm_rx_supported(const DevMatrix &w, int M);
+// Greedy LM head for 4 < M <= 32: per-wave argmax partials pv/pi [M][parts] of
+// X W^T (mask_id skipped), without storing the logits.
+int gemm_argmax_parts(const DevMatrix &w, int M);
+hipError_t gemm_argmax(const DevMatrix &w, const float *X, int ldx, int M, int mask_id, float *pv, uint32_t *pi,
+                       int *parts, hipStream_t st);
 
 // Row LayerNorm (biased variance): out = (x - mean) * rsqrt(var + eps) * g + b.
 hipError_t layernorm(const float *x, int rows, int d, const float *g, const float *b, float eps, float *out,

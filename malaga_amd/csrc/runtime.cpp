@@ -394,6 +394,7 @@ std::unique_ptr<StaticState> Model::new_state(int b, int s, int m, bool beam) {
     st->u = static_cast<float *>(get(size_t(b) * cfg.decoder_ffn * 4, "ffn"));
     if (beam || b > gemv_max_batch(embed)) st->logits = static_cast<float *>(get(size_t(b) * V * 4, "logits"));
     st->parts = std::max(gemv_argmax_parts(embed, b), 64);
+    if (b > gemv_max_batch(embed) && gemm_rx_supported(embed, b)) st->parts = std::max(st->parts, gemm_argmax_parts(embed, b));
     st->pv = static_cast<float *>(get(size_t(b) * st->parts * 4, "argmax partials"));
     st->pi = static_cast<uint32_t *>(get(size_t(b) * st->parts * 4, "argmax partials"));
     check_hip(hipStreamSynchronize(ctx->stream), "state");
@@ -481,6 +482,8 @@ void Model::lm_head(StaticState &st, bool greedy_mode, int mask_id) {
         int parts = 64;
         if (B <= gemv_max_batch(embed)) {
             check_hip(gemv_argmax(embed, st.h, d, B, mask_id, st.pv, st.pi, &parts, s), "lm_head");
+        } else if (gemm_rx_supported(embed, B)) {
+            check_hip(gemm_argmax(embed, st.h, d, B, mask_id, st.pv, st.pi, &parts, s), "lm_head");
         } else {
             check_hip(gemm(embed, st.h, d, B, st.logits, V, nullptr, false, nullptr, 0, s, ctx->gemm_workspace(),
                            kGemmWorkspaceBytes),
@@ -512,21 +515,35 @@ void Model::step(StaticState &st, bool greedy_mode, int mask_id) {
     check_hip(embed_pos_ln(embed, st.ids, B, pos, st.step, uint32_t(cfg.pad_token_id + 1), embed_scale,
                            dec[0].attn_norm.g, dec[0].attn_norm.b, kLnEps, st.x, st.h, s),
               "embed_pos_ln");
+    // x += y W^T + b; h = LayerNorm(x): register GEMV + residual_ln for small
+    // batches, else the MFMA GEMM with the residual and LayerNorm in its reduction
+    auto project_residual_ln = [&](const Linear &l, const float *in, const LNorm &n) {
+        if (B <= gemv_max_batch(l.w)) {
+            matmul(l, in, B, st.y, false, nullptr);
+            check_hip(residual_ln(st.x, st.y, B, d, n.g, n.b, kLnEps, st.h, s), "residual_ln");
+        } else {
+            check_hip(gemm_residual_ln(l.w, in, l.w.K, B, l.b, st.x, n.g, n.b, kLnEps, st.h, s, ctx->gemm_workspace(),
+                                       kGemmWorkspaceBytes),
+                      "gemm_residual_ln");
+        }
+    };
     for (size_t i = 0; i < dec.size(); ++i) {
         const DecLayer &l = dec[i];
-        matmul(l.qkv, st.h, B, st.qkv, false, nullptr);
-        check_hip(qkv_split(st.qkv, B, H, hd, st.m, st.step, st.q, st.kc[i], st.vc[i], s), "qkv_split");
+        if (B <= gemv_max_batch(l.qkv.w)) {
+            matmul(l.qkv, st.h, B, st.qkv, false, nullptr);
+            check_hip(qkv_split(st.qkv, B, H, hd, st.m, st.step, st.q, st.kc[i], st.vc[i], s), "qkv_split");
+        } else {
+            check_hip(gemm_qkv(l.qkv.w, st.h, d, B, l.qkv.b, H, hd, st.m, st.step, st.q, st.kc[i], st.vc[i], st.qkv, s,
+                               ctx->gemm_workspace(), kGemmWorkspaceBytes),
+                      "gemm_qkv");
+        }
         check_hip(attn_decode(st.q, st.kc[i], st.vc[i], B, H, hd, st.m, nullptr, st.step, st.att, s), "attn");
-        matmul(l.out, st.att, B, st.y, false, nullptr);
-        check_hip(residual_ln(st.x, st.y, B, d, l.cross_norm.g, l.cross_norm.b, kLnEps, st.h, s), "residual_ln");
+        project_residual_ln(l.out, st.att, l.cross_norm);
         matmul(l.cross_q, st.h, B, st.q, false, nullptr);
         check_hip(attn_decode(st.q, st.ck[i], st.cv[i], B, H, hd, st.s, st.lens, nullptr, st.att, s), "attn");
-        matmul(l.cross_out, st.att, B, st.y, false, nullptr);
-        check_hip(residual_ln(st.x, st.y, B, d, l.ffn_norm.g, l.ffn_norm.b, kLnEps, st.h, s), "residual_ln");
+        project_residual_ln(l.cross_out, st.att, l.ffn_norm);
         matmul(l.up, st.h, B, st.u, true, nullptr);
-        matmul(l.down, st.u, B, st.y, false, nullptr);
-        const LNorm &next = i + 1 < dec.size() ? dec[i + 1].attn_norm : dec_norm;
-        check_hip(residual_ln(st.x, st.y, B, d, next.g, next.b, kLnEps, st.h, s), "residual_ln");
+        project_residual_ln(l.down, st.u, i + 1 < dec.size() ? dec[i + 1].attn_norm : dec_norm);
     }
     // st.h is dec_norm(x): tied LM head
     lm_head(st, greedy_mode, mask_id);

@@ -118,6 +118,49 @@ def test_gemm_mfma_tiles_bias_relu_residual(ctx, t, N, K):
         ctx.lib.mlg_matrix_free(w)
 
 
+@pytest.mark.parametrize("t,K", [(Q6_K, 1024), (Q4_K, 1024), (Q8_0, 512), (Q5_K, 2048)])
+def test_gemm_argmax_batched_lm_head(ctx, t, K):
+    """Batched LM head (5..32 rows): per-wave argmax partials merged on the host equal
+    the argmax of the oracle's logits; ties -> lowest index; mask_id is skipped."""
+    rng = np.random.default_rng(5 + t)
+    N = 20000
+    wf = rng.normal(0, 0.02, (N, K)).astype(np.float32)
+    wf[4321] = wf[15000] = rng.normal(0, 0.5, K).astype(np.float32)  # tied dominant rows
+    blocks = M.quantize(t, wf)
+    w = upload(ctx, t, blocks, N, K)
+    try:
+        for M_ in (5, 16, 17, 32):
+            if K > 1024 and M_ > 16:
+                continue
+            x = rng.normal(0, 1, (M_, K)).astype(np.float32)
+            x[0] = np.abs(x[0]) * np.sign(wf[4321])
+            parts = ctx.lib.mlg_gemm_argmax_parts(w, M_)
+            assert parts > 0
+            ref = O.gemv(t, blocks, N, K, x)
+            for mask in (-1, 4321):
+                pv = torch.zeros((M_, parts), device="cuda")
+                pi = torch.zeros((M_, parts), dtype=torch.int32, device="cuda")
+                _lib.check(ctx.lib.mlg_gemm_argmax(w, ptr(dev(x)), M_, mask, ptr(pv), ptr(pi), None))
+                torch.cuda.synchronize()
+                v, i = pv.cpu().numpy(), pi.cpu().numpy().view(np.uint32)
+                r = ref.copy()
+                if mask >= 0:
+                    r[:, mask] = -np.inf
+                for m in range(M_):
+                    best = v[m].max()
+                    got = int(i[m][v[m] == best].min())
+                    want = int(np.argmax(r[m]))
+                    # near-ties within f32 rounding may legitimately resolve either way
+                    assert got == want or abs(r[m][got] - r[m][want]) <= 2e-6 * bound(x[m:m + 1], O.dequant(
+                        t, blocks, N * K).reshape(N, K)[[got, want]]).max() + 1e-6, (M_, m, got, want)
+                if mask < 0:
+                    assert int(i[0][v[0] == v[0].max()].min()) == 4321  # tie between 4321 and 15000
+                else:
+                    assert int(i[0][v[0] == v[0].max()].min()) == 15000
+    finally:
+        ctx.lib.mlg_matrix_free(w)
+
+
 @pytest.mark.parametrize("t", [Q6_K, Q4_K, Q8_0])
 def test_gemv_argmax_lowest_index_on_ties(ctx, t):
     rng = np.random.default_rng(99)

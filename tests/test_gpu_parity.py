@@ -178,3 +178,44 @@ def test_fused_step_small_batches_kquant(kq_gguf, models, unfused_models, preset
     tgt[:, 2:] = rng.integers(4, 990, (nb, T - 2))
     lg = gpu.teacher_forced_logits(src, tgt)
     assert np.abs(lg - orc.teacher_forced_logits(src, tgt, kv_f16=True)).max() < 2e-3
+
+
+@pytest.mark.parametrize("preset", ["q4_k_m", "q5_k_m", "q6_k", "q8_0", "f16"])
+@pytest.mark.parametrize("nb", [7, 16, 33])
+def test_batched_decode_mfma_path(kq_gguf, models, preset, nb):
+    """Batches above the register GEMV (> 4 rows): MFMA GEMMs with split-K reductions
+    fused with the residual + LayerNorm and the QKV split, the batched LM head
+    (argmax partials on the MFMA units up to 32 rows, logits + argmax above)."""
+    gpu, orc = models(kq_gguf(preset))
+    rng = np.random.default_rng(200 + nb)
+    src = [[997] + rng.integers(4, 990, int(n)).tolist() + [2] for n in rng.integers(2, 40, nb)]
+    want, gap = orc.translate_batch(src, 998, max_batch=64, kv_f16=True, max_new_tokens=10)
+    got = gpu.generate(src, 998, M.GenOptions(max_new_tokens=10, max_batch=64))
+    assert got == want, f"min top-2 gap {gap}"
+    T = 8
+    tgt = np.zeros((nb, T), np.uint32)
+    tgt[:, 0], tgt[:, 1] = 2, 998
+    tgt[:, 2:] = rng.integers(4, 990, (nb, T - 2))
+    lg = gpu.teacher_forced_logits(src, tgt)
+    assert np.abs(lg - orc.teacher_forced_logits(src, tgt, kv_f16=True)).max() < 2e-3
+
+
+def test_config5_shapes_batch64(model_dir, models):
+    """BASELINE config 5 shapes (NLLB-3.3B: d_model 2048, 16 heads of 128, FFN 8192,
+    q4_k_m) at two layers and a 4096-token vocabulary so that the oracle finishes in
+    seconds; a dynamic batch of 40 sentences (state bucket 64), lognormal lengths."""
+    cfg = M.nllb_3b_config()
+    cfg.update(vocab_size=4096, encoder_layers=2, decoder_layers=2, max_position_embeddings=256, max_length=64)
+    path = model_dir / "c5-q4_k_m.gguf"
+    if not path.exists():
+        M.write_synthetic(path, cfg, "q4_k_m", M.INIT_NORMAL_RICH, seed=5, std=0.02, name="config5-shape")
+    gpu, orc = models(path)
+    rng = np.random.default_rng(55)
+    lens = np.clip(np.rint(rng.lognormal(np.log(12) - 0.125, 0.5, 40)), 3, 40).astype(int)
+    src = [[4000] + rng.integers(4, 3990, int(n)).tolist() + [2] for n in lens]
+    want, gap = orc.translate_batch(src, 4001, max_batch=64, kv_f16=True, max_new_tokens=6)
+    got = gpu.generate(src, 4001, M.GenOptions(max_new_tokens=6, max_batch=64))
+    assert got == want, f"min top-2 gap {gap}"
+    # batch of 3: the fused step at d = 2048 (hd = 128, head groups of 2)
+    want3, gap3 = orc.translate_batch(src[:3], 4001, kv_f16=True, max_new_tokens=6)
+    assert gpu.generate(src[:3], 4001, M.GenOptions(max_new_tokens=6)) == want3, f"min top-2 gap {gap3}"
