@@ -249,9 +249,15 @@ struct GemvGeom {
     int nchunks;   // chunks per row
 };
 
+// LDS rows of x staged for the GEMV carry 4 floats of padding after every 64, so
+// that the 16-byte reads of the lanes of a row group (one chunk each, 64 floats
+// apart) fall in different banks.
+__host__ __device__ constexpr int lds_pad(int i) { return i + ((i >> 6) << 2); }
+
 // Loads this lane's slice of x (rows [0, nb) of a [B][ldx] array; 16-byte aligned,
 // generic pointer: LDS or global) into registers; padding rows/chunks are zero.
-template <int T, int B, int CPL>
+// PAD: x is an LDS copy in the lds_pad layout.
+template <int T, int B, int CPL, bool PAD = false>
 __device__ __forceinline__ void gemv_load_x(const float *x, int ldx, int nb, const GemvGeom &g, int cl,
                                             float (&xr)[CPL][B][GTraits<T>::XW],
                                             float (&xs)[CPL][B][GTraits<T>::NS]) {
@@ -268,7 +274,8 @@ __device__ __forceinline__ void gemv_load_x(const float *x, int ldx, int nb, con
             const float *row = x + size_t(bi < nb ? bi : 0) * ldx;
 #pragma unroll
             for (int e = 0; e < XW; e += 4) {
-                const float4 q = *reinterpret_cast<const float4 *>(row + xpos<T>(cc, e));
+                const int o = PAD ? lds_pad(xpos<T>(cc, e)) : xpos<T>(cc, e);
+                const float4 q = *reinterpret_cast<const float4 *>(row + o);
                 xr[t][bi][e] = v ? q.x : 0.f;
                 xr[t][bi][e + 1] = v ? q.y : 0.f;
                 xr[t][bi][e + 2] = v ? q.z : 0.f;

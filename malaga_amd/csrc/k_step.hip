@@ -128,7 +128,7 @@ __device__ __forceinline__ void ln_to_lds(const float4 (&v)[4][kMaxF4], const fl
 #pragma unroll
         for (int c = 0; c < kMaxF4; ++c)
             if (t + 256 * c < nf)
-                reinterpret_cast<float4 *>(xs + bi * d)[t + 256 * c] =
+                *reinterpret_cast<float4 *>(xs + bi * lds_pad(d) + lds_pad(4 * (t + 256 * c))) =
                     make_float4((v[bi][c].x - m) * rstd * gr[c].x + br[c].x, (v[bi][c].y - m) * rstd * gr[c].y + br[c].y,
                                 (v[bi][c].z - m) * rstd * gr[c].z + br[c].z, (v[bi][c].w - m) * rstd * gr[c].w + br[c].w);
     }
@@ -173,7 +173,7 @@ __device__ __forceinline__ void resid_ln_prologue(const StepArgs &a, const PreLo
                 float e[16];
                 dequant16<ET>(a.eq, a.es, a.ed, d, int(a.ids[bi]), k0, e);
 #pragma unroll
-                for (int j = 0; j < 16; ++j) xs[bi * d + k0 + j] = e[j] * a.emb_scale + pr[k0 + j];
+                for (int j = 0; j < 16; ++j) xs[bi * lds_pad(d) + lds_pad(k0 + j)] = e[j] * a.emb_scale + pr[k0 + j];
             }
             lds_barrier();
 #pragma unroll
@@ -181,7 +181,9 @@ __device__ __forceinline__ void resid_ln_prologue(const StepArgs &a, const PreLo
                 if (bi >= nb) break;
 #pragma unroll
                 for (int c = 0; c < kMaxF4; ++c)
-                    if (c < nc) v[bi][c] = ld4(xs + bi * d, min(t + 256 * c, nf - 1));
+                    if (c < nc)
+                        v[bi][c] = *reinterpret_cast<const float4 *>(xs + bi * lds_pad(d) +
+                                                                     lds_pad(4 * min(t + 256 * c, nf - 1)));
             }
         } else {
 #pragma unroll
@@ -230,7 +232,7 @@ __global__ __launch_bounds__(256) void k_step(StepArgs a) {
             gemv_load_x<T, B, CPL>(a.xg, a.ldx, a.nb, a.g, cl, xr, xs);
         } else {
             resid_ln_prologue<PRO, ET>(a, L, lds, red);
-            gemv_load_x<T, B, CPL>(lds, a.d, a.nb, a.g, cl, xr, xs);
+            gemv_load_x<T, B, CPL, true>(lds, lds_pad(a.d), a.nb, a.g, cl, xr, xs);
         }
     };
 
@@ -521,7 +523,7 @@ bool step_fusable(const DevMatrix &w, int nb, int d) {
     if (nb < 1 || nb > 4 || nb > gemv_max_batch(w) || !gemv_geometry(w, &g, &cpl) || cpl > 2) return false;
     if (nb == 4 && cpl > 1) return false;
     // residual prologue: float4 slots, nb rows of d floats in LDS
-    return d % 16 == 0 && d <= 1024 * kMaxF4 && size_t(nb) * d * 4 + 256 <= 64 * 1024;
+    return d % 16 == 0 && d <= 1024 * kMaxF4 && size_t(nb) * lds_pad(d) * 4 + 512 <= 64 * 1024;
 }
 
 int step_head_parts(const DevMatrix &w, int nb, int d, int H, int hd, int L) {
@@ -566,7 +568,7 @@ hipError_t step_qkv(const DevMatrix &w, const float *bias, int nb, int d, const 
     a.H = H;
     a.hd = hd;
     a.m = m;
-    const size_t lds = sizeof(float) * size_t(nb) * d;
+    const size_t lds = sizeof(float) * size_t(nb) * lds_pad(d);
     const int grid = gemv_grid(w, 1);
     const int B = gemv_round_b(nb);
     if (!emb)
@@ -630,7 +632,7 @@ hipError_t step_resid_proj(const DevMatrix &w, const float *bias, bool relu, int
     a.bias = bias;
     a.relu = relu ? 1 : 0;
     a.y = y;
-    const size_t lds = sizeof(float) * size_t(nb) * d;
+    const size_t lds = sizeof(float) * size_t(nb) * lds_pad(d);
     return preloadable(a) ? dispatch_t<PRO_RESID_PRE, EPI_STORE, GGML_F32>(w.type, a, gemv_round_b(nb), cpl,
                                                                         gemv_grid(w, 1), lds, st)
                           : dispatch_t<PRO_RESID, EPI_STORE, GGML_F32>(w.type, a, gemv_round_b(nb), cpl, gemv_grid(w, 1),
