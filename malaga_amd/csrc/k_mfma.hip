@@ -334,8 +334,15 @@ __global__ __launch_bounds__(256) void k_splitk_reduce(const float *part, int ks
     const size_t i = size_t(blockIdx.x) * 256 + threadIdx.x, mn = size_t(M) * N;
     if (i >= mn) return;
     const int m = int(i / N), n = int(i % N);
-    float v = part[i];
-    for (int z = 1; z < ks; ++z) v += part[size_t(z) * mn + i];
+    float v = 0.f;
+    for (int z0 = 0; z0 < ks; z0 += 8) {
+        float p8[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) p8[u] = z0 + u < ks ? part[size_t(z0 + u) * mn + i] : 0.f;
+#pragma unroll
+        for (int u = 0; u < 8; ++u)
+            if (z0 + u < ks) v = (z0 + u == 0) ? p8[u] : v + p8[u];
+    }
     if (bias) v += bias[n];
     if (R) v += R[size_t(m) * ldr + n];
     if (relu) v = fmaxf(v, 0.f);
@@ -371,8 +378,16 @@ __global__ __launch_bounds__(256) void k_splitk_residual_ln(const float *part, i
         const int i = t + 256 * k;
         v[k] = 0.f;
         if (i < N) {
-            float y = part[off + i];
-            for (int z = 1; z < ks; ++z) y += part[size_t(z) * mn + off + i];
+            // partials requested 8 at a time, then added in z order
+            float y = 0.f;
+            for (int z0 = 0; z0 < ks; z0 += 8) {
+                float p8[8];
+#pragma unroll
+                for (int u = 0; u < 8; ++u) p8[u] = z0 + u < ks ? part[size_t(z0 + u) * mn + off + i] : 0.f;
+#pragma unroll
+                for (int u = 0; u < 8; ++u)
+                    if (z0 + u < ks) y = (z0 + u == 0) ? p8[u] : y + p8[u];
+            }
             if (bias) y += bias[i];
             v[k] = x[off + i] + y;
             x[off + i] = v[k];
@@ -400,8 +415,15 @@ __global__ __launch_bounds__(256) void k_splitk_qkv(const float *part, int ks, i
     const size_t i = size_t(blockIdx.x) * 256 + threadIdx.x, N = size_t(3) * d, mn = size_t(M) * N;
     if (i >= mn) return;
     const int m = int(i / N), c = int(i % N);
-    float v = part[i];
-    for (int z = 1; z < ks; ++z) v += part[size_t(z) * mn + i];
+    float v = 0.f;
+    for (int z0 = 0; z0 < ks; z0 += 8) {
+        float p8[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) p8[u] = z0 + u < ks ? part[size_t(z0 + u) * mn + i] : 0.f;
+#pragma unroll
+        for (int u = 0; u < 8; ++u)
+            if (z0 + u < ks) v = (z0 + u == 0) ? p8[u] : v + p8[u];
+    }
     if (bias) v += bias[c];
     if (c < d) {
         q[size_t(m) * d + c] = v;

@@ -131,7 +131,8 @@ __global__ void k_qkv_split(const float *qkv, int H, int hd, int m, const uint32
 // One workgroup per (row, head).  Thread j scores key j (16-byte f16 loads), block
 // max / exp / sum, then hd-wide thread groups split the keys for P.V.
 __global__ __launch_bounds__(256) void k_attn_decode(const float *q, const __half *K, const __half *V, int H, int hd,
-                                                     int L, const uint32_t *lens, const uint32_t *step, float *out) {
+                                                     int L, const uint32_t *lens, const uint32_t *step, float *out,
+                                                     const uint32_t *rows) {
     extern __shared__ float sm[];
     __shared__ float red[16];
     const int bh = blockIdx.x, bi = bh / H, hh = bh % H;
@@ -140,10 +141,14 @@ __global__ __launch_bounds__(256) void k_attn_decode(const float *q, const __hal
     float *qs = sm, *sc = sm + hd, *part = sc + L;
     for (int t = threadIdx.x; t < hd; t += blockDim.x) qs[t] = q[size_t(bh) * hd + t];
     __syncthreads();
-    const __half *Kb = K + size_t(bh) * L * hd, *Vb = V + size_t(bh) * L * hd;
+    // rows[bi][j]: the cache row that holds slot j of row bi (beam search), else bi
+    auto slot = [&](const __half *C, int j) {
+        const size_t r = rows ? rows[size_t(bi) * L + j] : size_t(bi);
+        return C + ((r * H + hh) * L + j) * hd;
+    };
     float mx = -INFINITY;
     for (int j = threadIdx.x; j < n; j += blockDim.x) {
-        const uint4 *k8 = reinterpret_cast<const uint4 *>(Kb + size_t(j) * hd);
+        const uint4 *k8 = reinterpret_cast<const uint4 *>(slot(K, j));
         float acc = 0.f;
         for (int t = 0; t < hd / 8; ++t) {
             const uint4 raw = k8[t];
@@ -170,7 +175,7 @@ __global__ __launch_bounds__(256) void k_attn_decode(const float *q, const __hal
     const int g = threadIdx.x / hd, t = threadIdx.x % hd;
     if (g < groups) {
         float a = 0.f;
-        for (int j = g; j < n; j += groups) a = fmaf(sc[j], __half2float(Vb[size_t(j) * hd + t]), a);
+        for (int j = g; j < n; j += groups) a = fmaf(sc[j], __half2float(slot(V, j)[t]), a);
         part[g * hd + t] = a;
     }
     __syncthreads();
@@ -358,7 +363,9 @@ __global__ __launch_bounds__(1024) void k_greedy_finalize(const float *pv, const
 constexpr int kTopMax = 8;
 constexpr int kTopParts = 64;
 
-struct TopK {
+// Top-8 of (value, index) pairs, best first; larger value wins, ties -> lower index.
+// Always 8 entries (k <= 8 reads the first k): fixed register slots, no indexing.
+struct Top8 {
     float v[kTopMax];
     uint32_t i[kTopMax];
 };
@@ -367,19 +374,32 @@ __device__ __forceinline__ bool better(float av, uint32_t ai, float bv, uint32_t
     return av > bv || (av == bv && ai < bi);
 }
 
-__device__ __forceinline__ void topk_insert(TopK &t, int k, float v, uint32_t i) {
-    if (!better(v, i, t.v[k - 1], t.i[k - 1])) return;
-    int p = k - 1;
-    while (p > 0 && better(v, i, t.v[p - 1], t.i[p - 1])) {
-        t.v[p] = t.v[p - 1];
-        t.i[p] = t.i[p - 1];
-        --p;
+__device__ __forceinline__ void top8_init(Top8 &t) {
+#pragma unroll
+    for (int j = 0; j < kTopMax; ++j) {
+        t.v[j] = -INFINITY;
+        t.i[j] = 0xffffffffu;
     }
-    t.v[p] = v;
-    t.i[p] = i;
 }
 
-// Pass 1: per (part, row): chunk max M, sum exp(x - M), chunk top-k.
+__device__ __forceinline__ void top8_insert(Top8 &t, float v, uint32_t i) {
+    if (!better(v, i, t.v[kTopMax - 1], t.i[kTopMax - 1])) return;
+    t.v[kTopMax - 1] = v;
+    t.i[kTopMax - 1] = i;
+#pragma unroll
+    for (int j = kTopMax - 1; j > 0; --j) {
+        if (better(t.v[j], t.i[j], t.v[j - 1], t.i[j - 1])) {
+            const float tv = t.v[j];
+            const uint32_t ti = t.i[j];
+            t.v[j] = t.v[j - 1];
+            t.i[j] = t.i[j - 1];
+            t.v[j - 1] = tv;
+            t.i[j - 1] = ti;
+        }
+    }
+}
+
+// Pass 1: per (part, row): chunk max M, sum exp(x - M), chunk top-8.
 // scratch layout per (row, part): [M, S, v0..v7, i0..i7] (18 floats)
 __global__ __launch_bounds__(256) void k_lsm_topk_partial(const float *logits, int V, int k, int mask_id,
                                                           float *scratch) {
@@ -389,17 +409,14 @@ __global__ __launch_bounds__(256) void k_lsm_topk_partial(const float *logits, i
     const int row = blockIdx.y, p = blockIdx.x, P = gridDim.x;
     const int chunk = (V + P - 1) / P, start = p * chunk, end = min(start + chunk, V);
     const float *r = logits + size_t(row) * V;
-    TopK t;
-    for (int j = 0; j < kTopMax; ++j) {
-        t.v[j] = -INFINITY;
-        t.i[j] = 0xffffffffu;
-    }
+    Top8 t;
+    top8_init(t);
     float mx = -INFINITY;
     for (int i = start + threadIdx.x; i < end; i += blockDim.x) {
         if (i == mask_id) continue;
         const float v = r[i];
         mx = fmaxf(mx, v);
-        topk_insert(t, k, v, uint32_t(i));
+        top8_insert(t, v, uint32_t(i));
     }
     mx = block_max(mx, red);
     float s = 0.f;
@@ -407,7 +424,8 @@ __global__ __launch_bounds__(256) void k_lsm_topk_partial(const float *logits, i
         if (i != mask_id && mx > -INFINITY) s += expf(r[i] - mx);
     __syncthreads();
     s = block_sum(s, red);
-    for (int j = 0; j < k; ++j) {
+#pragma unroll
+    for (int j = 0; j < kTopMax; ++j) {
         lv[threadIdx.x * kTopMax + j] = t.v[j];
         li[threadIdx.x * kTopMax + j] = t.i[j];
     }
@@ -415,8 +433,10 @@ __global__ __launch_bounds__(256) void k_lsm_topk_partial(const float *logits, i
     for (int stride = 128; stride > 0; stride >>= 1) {
         if (int(threadIdx.x) < stride) {
             const int o = threadIdx.x + stride;
-            for (int j = 0; j < k; ++j) topk_insert(t, k, lv[o * kTopMax + j], li[o * kTopMax + j]);
-            for (int j = 0; j < k; ++j) {
+#pragma unroll
+            for (int j = 0; j < kTopMax; ++j) top8_insert(t, lv[o * kTopMax + j], li[o * kTopMax + j]);
+#pragma unroll
+            for (int j = 0; j < kTopMax; ++j) {
                 lv[threadIdx.x * kTopMax + j] = t.v[j];
                 li[threadIdx.x * kTopMax + j] = t.i[j];
             }
@@ -427,35 +447,52 @@ __global__ __launch_bounds__(256) void k_lsm_topk_partial(const float *logits, i
         float *o = scratch + (size_t(row) * P + p) * (2 + 2 * kTopMax);
         o[0] = mx;
         o[1] = s;
+#pragma unroll
         for (int j = 0; j < kTopMax; ++j) {
-            o[2 + j] = j < k ? t.v[j] : -INFINITY;
-            o[2 + kTopMax + j] = __uint_as_float(j < k ? t.i[j] : 0xffffffffu);
+            o[2 + j] = t.v[j];
+            o[2 + kTopMax + j] = __uint_as_float(t.i[j]);
         }
     }
 }
 
-// Pass 2: one thread per row merges the parts: vals = (x - max) - ln(sum exp(x - max)).
-__global__ void k_lsm_topk_final(const float *scratch, int rows, int P, int k, float *vals, uint32_t *idx) {
-    const int row = blockIdx.x * blockDim.x + threadIdx.x;
+// Pass 2: one wave per row, lane p holds part p (P <= 64): vals = (x - max) - ln(sum
+// exp(x - max)) with the sum in f64 in a fixed lane order; top-k by k rounds of a
+// wave argmax over the lanes' best remaining candidates.
+__global__ __launch_bounds__(64) void k_lsm_topk_final(const float *scratch, int rows, int P, int k, float *vals,
+                                                       uint32_t *idx) {
+    const int row = blockIdx.x, lane = threadIdx.x;
     if (row >= rows) return;
-    const float *base = scratch + size_t(row) * P * (2 + 2 * kTopMax);
-    float M = -INFINITY;
-    for (int p = 0; p < P; ++p) M = fmaxf(M, base[p * (2 + 2 * kTopMax)]);
-    double S = 0.0;
-    TopK t;
-    for (int j = 0; j < kTopMax; ++j) {
-        t.v[j] = -INFINITY;
-        t.i[j] = 0xffffffffu;
-    }
-    for (int p = 0; p < P; ++p) {
-        const float *o = base + p * (2 + 2 * kTopMax);
-        if (o[0] > -INFINITY) S += double(o[1]) * exp(double(o[0]) - double(M));
-        for (int j = 0; j < k; ++j) topk_insert(t, k, o[2 + j], __float_as_uint(o[2 + kTopMax + j]));
-    }
+    const float *o = scratch + (size_t(row) * P + lane) * (2 + 2 * kTopMax);
+    const bool ok = lane < P;
+    const float Mp = ok ? o[0] : -INFINITY, Sp = ok ? o[1] : 0.f;
+    Top8 t;
+    top8_init(t);
+    if (ok)
+#pragma unroll
+        for (int j = 0; j < kTopMax; ++j) {
+            t.v[j] = o[2 + j];
+            t.i[j] = __float_as_uint(o[2 + kTopMax + j]);
+        }
+    const float M = wave_max(Mp);
+    const double S = wave_sum_f64(Mp > -INFINITY ? double(Sp) * exp(double(Mp) - double(M)) : 0.0);
     const float ls = float(log(S));
-    for (int j = 0; j < k; ++j) {
-        vals[size_t(row) * k + j] = (t.v[j] - M) - ls;
-        idx[size_t(row) * k + j] = t.i[j];
+    for (int j = 0; j < k; ++j) {  // uniform
+        float bv = t.v[0];
+        uint32_t bi = t.i[0];
+        wave_argmax(bv, bi);
+        if (lane == 0) {
+            vals[size_t(row) * k + j] = (bv - M) - ls;
+            idx[size_t(row) * k + j] = bi;
+        }
+        if (ok && t.i[0] == bi && t.v[0] == bv) {  // the winning lane drops its head
+#pragma unroll
+            for (int q = 0; q < kTopMax - 1; ++q) {
+                t.v[q] = t.v[q + 1];
+                t.i[q] = t.i[q + 1];
+            }
+            t.v[kTopMax - 1] = -INFINITY;
+            t.i[kTopMax - 1] = 0xffffffffu;
+        }
     }
 }
 
@@ -543,11 +580,11 @@ hipError_t qkv_split(const float *qkv, int b, int H, int hd, int m, const uint32
 }
 
 hipError_t attn_decode(const float *q, const __half *K, const __half *V, int b, int H, int hd, int L,
-                       const uint32_t *lens, const uint32_t *step, float *out, hipStream_t st) {
+                       const uint32_t *lens, const uint32_t *step, float *out, hipStream_t st, const uint32_t *rows) {
     if (hd % 8 || hd > 256) return hipErrorInvalidValue;
     const int block = 256, groups = block / hd > 0 ? block / hd : 1;
     const size_t shared = sizeof(float) * (hd + L + groups * hd);
-    hipLaunchKernelGGL(k_attn_decode, dim3(b * H), dim3(block), shared, st, q, K, V, H, hd, L, lens, step, out);
+    hipLaunchKernelGGL(k_attn_decode, dim3(b * H), dim3(block), shared, st, q, K, V, H, hd, L, lens, step, out, rows);
     return hipGetLastError();
 }
 
@@ -599,8 +636,7 @@ hipError_t logsoftmax_topk(const float *logits, int rows, int V, int k, int mask
                            uint32_t *idx, hipStream_t st) {
     if (k < 1 || k > kTopMax) return hipErrorInvalidValue;
     hipLaunchKernelGGL(k_lsm_topk_partial, dim3(kTopParts, rows), dim3(256), 0, st, logits, V, k, mask_id, scratch);
-    hipLaunchKernelGGL(k_lsm_topk_final, dim3((rows + 63) / 64), dim3(64), 0, st, scratch, rows, kTopParts, k, vals,
-                       idx);
+    hipLaunchKernelGGL(k_lsm_topk_final, dim3(rows), dim3(64), 0, st, scratch, rows, kTopParts, k, vals, idx);
     return hipGetLastError();
 }
 

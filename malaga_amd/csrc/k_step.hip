@@ -272,6 +272,7 @@ struct HeadArgs {
     const uint32_t *lens;  // cross lengths, or null: *step + 1 keys
     const uint32_t *step;
     float *part;     // [H / HG][nb][d]
+    const uint32_t *rows;  // optional [nb][L]: cache row holding slot j of row bi (beam search)
 };
 
 constexpr int kHeadCols = 256;  // max columns (HG * HD) per workgroup
@@ -311,12 +312,13 @@ __global__ __launch_bounds__(256) void k_attn_head(HeadArgs a) {
     float4 qa, qb;
     auto load_chunk_kv = [&](int p, int j0) {
         const int bi = p >> hg_log2, hh = h0 + (p & (HG - 1));
-        const size_t base = (size_t(bi) * H + hh) * L;
 #pragma unroll
         for (int u = 0; u < U; ++u) {
             const int j = min(j0 + u * SPL + split, L - 1);
-            kr[u] = *reinterpret_cast<const uint4 *>(a.K + (base + j) * HD + sub * 8);
-            vr[u] = *reinterpret_cast<const uint4 *>(a.V + (base + j) * HD + sub * 8);
+            const size_t r = a.rows ? a.rows[size_t(bi) * L + j] : size_t(bi);
+            const size_t o = ((r * H + hh) * L + j) * HD + sub * 8;
+            kr[u] = *reinterpret_cast<const uint4 *>(a.K + o);
+            vr[u] = *reinterpret_cast<const uint4 *>(a.V + o);
         }
         const float *qp = a.q + size_t(bi) * d + hh * HD + sub * 8;
         qa = *reinterpret_cast<const float4 *>(qp);
@@ -586,7 +588,8 @@ hipError_t step_qkv(const DevMatrix &w, const float *bias, int nb, int d, const 
 }
 
 hipError_t step_attn_head(const DevMatrix &w, int nb, int d, const float *q, const __half *K, const __half *V, int H,
-                          int hd, int L, const uint32_t *lens, const uint32_t *step, float *part, hipStream_t st) {
+                          int hd, int L, const uint32_t *lens, const uint32_t *step, float *part, hipStream_t st,
+                          const uint32_t *rows) {
     HeadGeom hg;
     if (!head_geometry(w, nb, d, H, hd, L, &hg)) return hipErrorInvalidValue;
     HeadArgs a{};
@@ -603,6 +606,7 @@ hipError_t step_attn_head(const DevMatrix &w, int nb, int d, const float *q, con
     a.lens = lens;
     a.step = step;
     a.part = part;
+    a.rows = rows;
     switch (w.type) {
     case GGML_Q4_K: return launch_head_hd<GGML_Q4_K>(a, hd, hg.R, hg.lds, st);
     case GGML_Q5_K: return launch_head_hd<GGML_Q5_K>(a, hd, hg.R, hg.lds, st);

@@ -92,7 +92,8 @@ hipError_t qkv_split(const float *qkv, int b, int H, int hd, int m, const uint32
 // Single-query attention per (row, head) over f16 K/V [b][H][L][hd]: n = lens[row]
 // if lens, else *step + 1.  out [b][H*hd].
 hipError_t attn_decode(const float *q, const __half *K, const __half *V, int b, int H, int hd, int L,
-                       const uint32_t *lens, const uint32_t *step, float *out, hipStream_t st);
+                       const uint32_t *lens, const uint32_t *step, float *out, hipStream_t st, const uint32_t *rows = nullptr);
+// rows (optional, [b][L]): cache row holding slot j of row b (beam reordering without copies).
 // Encoder self-attention over f32 qkv [b*s][3d] (rows of sentence i are i*s..),
 // key j of row i valid iff j < lens[i].  out [b*s][d].
 hipError_t attn_prefill(const float *qkv, int b, int s, int H, int hd, const uint32_t *lens, float *out,
@@ -137,7 +138,8 @@ hipError_t step_qkv(const DevMatrix &w, const float *bias, int nb, int d, const 
 // keys), times the out-projection w, as step_head_parts(...) partial sums
 // part[p][nb][d] (bias not added): sum over p = attention . W^T.
 hipError_t step_attn_head(const DevMatrix &w, int nb, int d, const float *q, const __half *K, const __half *V, int H,
-                          int hd, int L, const uint32_t *lens, const uint32_t *step, float *part, hipStream_t st);
+                          int hd, int L, const uint32_t *lens, const uint32_t *step, float *part, hipStream_t st,
+                          const uint32_t *rows = nullptr);
 // x = x_in + sum_{p < P} part[p] + pbias ; x_out <- x ; y = LayerNorm(x) W^T + bias (relu).
 hipError_t step_resid_proj(const DevMatrix &w, const float *bias, bool relu, int nb, int d, const float *x_in,
                            const float *part, int P, const float *pbias, float *x_out, const float *gamma,

@@ -353,7 +353,7 @@ std::unique_ptr<Batch> Model::encode(const std::vector<std::vector<uint32_t>> &s
     return out;
 }
 
-std::unique_ptr<StaticState> Model::new_state(int b, int s, int m, bool beam) {
+std::unique_ptr<StaticState> Model::new_state(int b, int s, int m, bool logits, bool row_map) {
     auto st = std::make_unique<StaticState>();
     st->b = b;
     st->s = s;
@@ -392,7 +392,14 @@ std::unique_ptr<StaticState> Model::new_state(int b, int s, int m, bool beam) {
     st->q = static_cast<float *>(get(size_t(b) * d * 4, "q"));
     st->qkv = static_cast<float *>(get(size_t(b) * 3 * d * 4, "qkv"));
     st->u = static_cast<float *>(get(size_t(b) * cfg.decoder_ffn * 4, "ffn"));
-    if (beam || b > gemv_max_batch(embed)) st->logits = static_cast<float *>(get(size_t(b) * V * 4, "logits"));
+    if (logits || b > gemv_max_batch(embed)) st->logits = static_cast<float *>(get(size_t(b) * V * 4, "logits"));
+    if (row_map) {  // identity until a beam reorder rewrites it
+        st->rows = static_cast<uint32_t *>(get(size_t(b) * m * 4, "beam cache rows"));
+        std::vector<uint32_t> id(size_t(b) * m);
+        for (int r = 0; r < b; ++r)
+            for (int j = 0; j < m; ++j) id[size_t(r) * m + j] = uint32_t(r);
+        h2d(st->rows, id, ctx->stream);
+    }
     st->parts = std::max(gemv_argmax_parts(embed, b), 64);
     if (b > gemv_max_batch(embed) && gemm_rx_supported(embed, b)) st->parts = std::max(st->parts, gemm_argmax_parts(embed, b));
     st->pv = static_cast<float *>(get(size_t(b) * st->parts * 4, "argmax partials"));
@@ -455,7 +462,8 @@ void Model::step_fused(StaticState &st) {
             std::swap(cur, nxt);
         }
         const int ps = step_head_parts(l.out.w, B, d, H, hd, st.m);
-        check_hip(step_attn_head(l.out.w, B, d, st.q, st.kc[i], st.vc[i], H, hd, st.m, nullptr, st.step, st.part, s),
+        check_hip(step_attn_head(l.out.w, B, d, st.q, st.kc[i], st.vc[i], H, hd, st.m, nullptr, st.step, st.part, s,
+                                 st.rows),
                   "step_attn_head");
         check_hip(step_resid_proj(l.cross_q.w, l.cross_q.b, false, B, d, cur, st.part, ps, l.out.b, nxt,
                                   l.cross_norm.g, l.cross_norm.b, kLnEps, st.qc, s),
@@ -537,7 +545,7 @@ void Model::step(StaticState &st, bool greedy_mode, int mask_id) {
                                ctx->gemm_workspace(), kGemmWorkspaceBytes),
                       "gemm_qkv");
         }
-        check_hip(attn_decode(st.q, st.kc[i], st.vc[i], B, H, hd, st.m, nullptr, st.step, st.att, s), "attn");
+        check_hip(attn_decode(st.q, st.kc[i], st.vc[i], B, H, hd, st.m, nullptr, st.step, st.att, s, st.rows), "attn");
         project_residual_ln(l.out, st.att, l.cross_norm);
         matmul(l.cross_q, st.h, B, st.q, false, nullptr);
         check_hip(attn_decode(st.q, st.ck[i], st.cv[i], B, H, hd, st.s, st.lens, nullptr, st.att, s), "attn");
@@ -689,20 +697,25 @@ std::vector<std::vector<uint32_t>> GraphCache::run(const Batch &src, uint32_t tg
 std::vector<std::vector<uint32_t>> Model::beam(const Batch &src, uint32_t tgt_lang, int max_new, int k, float lp,
                                                bool eos_mask) {
     hipStream_t s = ctx->stream;
-    const int b = src.b, bk = b * k, V = cfg.vocab_size, H = cfg.decoder_heads, hd = cfg.d_model / H;
+    const int b = src.b, bk = b * k, V = cfg.vocab_size;
     const uint32_t eos = uint32_t(cfg.eos_token_id);
     const int mask_id = eos_mask ? cfg.eos_token_id : -1;
-    auto st = new_state(bk, src.s, std::min(max_new + 2, cfg.max_position_embeddings), true);
+    auto st = new_state(bk, src.s, std::min(max_new + 2, cfg.max_position_embeddings), true, true);
     std::vector<uint32_t> expand(static_cast<size_t>(bk));
     for (int i = 0; i < bk; ++i) expand[i] = uint32_t(i / k);
     reset_state(*st, src, expand, uint32_t(cfg.decoder_start_token_id));
+    // src/model.rs:209-226 reorders every self-attention cache by beam each step.
+    // Here the caches stay in place: rows[r][j] names the cache row that holds slot j
+    // of beam row r.  Slot j of a cache row is written once (at step j, by that row)
+    // and never again, so a reorder only rewrites the map.
+    std::vector<uint32_t> rows_map(size_t(bk) * st->m), rows_next(rows_map.size());
+    for (int r = 0; r < bk; ++r)
+        for (int j = 0; j < st->m; ++j) rows_map[size_t(r) * st->m + j] = uint32_t(r);
+    h2d(st->rows, rows_map, s);
     DevTemp tmp;
     float *scratch = tmp.get<float>(logsoftmax_topk_scratch(bk, k) / 4, "topk scratch");
     float *d_vals = tmp.get<float>(size_t(bk) * k, "topk vals");
     uint32_t *d_idx = tmp.get<uint32_t>(size_t(bk) * k, "topk idx");
-    uint32_t *d_reorder = tmp.get<uint32_t>(size_t(bk), "reorder");
-    const size_t self_row = size_t(H) * st->m * hd * 2;
-    uint8_t *swap = tmp.get<uint8_t>(self_row * bk, "reorder scratch");
 
     // [start, tgt_lang] fed one position at a time (equal to the t = 2 causal pass)
     step(*st, false, mask_id);
@@ -767,13 +780,15 @@ std::vector<std::vector<uint32_t>> Model::beam(const Batch &src, uint32_t tgt_la
         if (stp == max_new || std::all_of(is_done.begin(), is_done.end(), [](uint8_t v) { return v != 0; })) break;
         // src/model.rs:209-226: gather the self-attention caches by beam.  Cross K/V and
         // lens are identical within a sentence's beams, and reorder never leaves a sentence.
-        h2d(d_reorder, reorder, s);
-        for (size_t l = 0; l < st->kc.size(); ++l) {
-            for (__half *buf : {st->kc[l], st->vc[l]}) {
-                check_hip(gather_rows(buf, swap, d_reorder, bk, self_row, s), "reorder");
-                check_hip(hipMemcpyAsync(buf, swap, self_row * bk, hipMemcpyDeviceToDevice, s), "reorder");
-            }
+        // slots 0 .. stp are written; the next step writes slot stp + 1 into row r itself
+        const int m = st->m;
+        for (int r = 0; r < bk; ++r) {
+            const uint32_t *par = rows_map.data() + size_t(reorder[r]) * m;
+            uint32_t *dst = rows_next.data() + size_t(r) * m;
+            for (int j = 0; j < m; ++j) dst[j] = j <= stp ? par[j] : uint32_t(r);
         }
+        rows_map.swap(rows_next);
+        h2d(st->rows, rows_map, s);
         h2d(st->ids, next, s);
         step(*st, false, mask_id);
     }

@@ -78,6 +78,7 @@ struct StaticState {
     float *x = nullptr, *h = nullptr, *y = nullptr, *att = nullptr, *q = nullptr, *qkv = nullptr, *u = nullptr;
     float *xb = nullptr, *qc = nullptr;  // second residual buffer and cross queries (fused step)
     float *part = nullptr;                // attention partial sums [parts][b][d] (fused step)
+    uint32_t *rows = nullptr;             // beam: [b][m] cache row holding slot j of row r (null: r)
     bool fused = false;                   // decoder step uses the fused kernels of k_step.hip
     float *logits = nullptr, *pv = nullptr;
     uint32_t *pi = nullptr;
@@ -140,7 +141,8 @@ class Model {
 
     // src/model.rs:463-500 (encoder + cross K/V of every decoder layer)
     std::unique_ptr<Batch> encode(const std::vector<std::vector<uint32_t>> &src);
-    std::unique_ptr<StaticState> new_state(int b, int s, int m, bool beam);
+    // logits: keep a [b][V] logits buffer; row_map: beam-search cache-row map (rows).
+    std::unique_ptr<StaticState> new_state(int b, int s, int m, bool logits, bool row_map = false);
     // src/model.rs:552-612: one decoder step on fixed buffers.  greedy: argmax +
     // bookkeeping, else logits into st.logits and ++step.
     void step(StaticState &st, bool greedy, int mask_id);
