@@ -364,18 +364,19 @@ hipError_t launch(const MfmaArgs &a, int M, int ks, hipStream_t st) {
 
 // Split-K reduction fused with the decoder's residual add and the next LayerNorm
 // (src/model.rs:183-187): y = sum_z part[z][m] (in order) + bias; x[m] += y;
-// h[m] = LayerNorm(x[m]) with biased variance.  One workgroup per row, N <= 4096.
-__global__ __launch_bounds__(256) void k_splitk_residual_ln(const float *part, int ks, int M, int N,
-                                                             const float *bias, float *x, const float *g,
-                                                             const float *b, float eps, float *h) {
+// h[m] = LayerNorm(x[m]) with biased variance.  One workgroup of 1024 threads per
+// row, N <= 4096.
+__global__ __launch_bounds__(1024) void k_splitk_residual_ln(const float *part, int ks, int M, int N,
+                                                              const float *bias, float *x, const float *g,
+                                                              const float *b, float eps, float *h) {
     __shared__ float sh[16];
     const int m = blockIdx.x, t = threadIdx.x;
     const size_t mn = size_t(M) * N, off = size_t(m) * N;
-    float v[16];
+    float v[4];
     float s1 = 0.f;
 #pragma unroll
-    for (int k = 0; k < 16; ++k) {
-        const int i = t + 256 * k;
+    for (int k = 0; k < 4; ++k) {
+        const int i = t + 1024 * k;
         v[k] = 0.f;
         if (i < N) {
             // partials requested 8 at a time, then added in z order
@@ -397,12 +398,12 @@ __global__ __launch_bounds__(256) void k_splitk_residual_ln(const float *part, i
     const float mean = block_sum(s1, sh) / float(N);
     float s2 = 0.f;
 #pragma unroll
-    for (int k = 0; k < 16; ++k)
-        if (t + 256 * k < N) s2 += (v[k] - mean) * (v[k] - mean);
+    for (int k = 0; k < 4; ++k)
+        if (t + 1024 * k < N) s2 += (v[k] - mean) * (v[k] - mean);
     const float rstd = rsqrtf(block_sum(s2, sh) / float(N) + eps);
 #pragma unroll
-    for (int k = 0; k < 16; ++k) {
-        const int i = t + 256 * k;
+    for (int k = 0; k < 4; ++k) {
+        const int i = t + 1024 * k;
         if (i < N) h[off + i] = (v[k] - mean) * rstd * g[i] + b[i];
     }
 }
@@ -836,7 +837,7 @@ hipError_t gemm_residual_ln(const DevMatrix &w, const float *X, int ldx, int M, 
     const int ks = launch_split(w, X, ldx, M, st, ws, ws_bytes, &e);
     if (e != hipSuccess) return e;
     if (ks > 1) {
-        hipLaunchKernelGGL(k_splitk_residual_ln, dim3(M), dim3(256), 0, st, ws, ks, M, w.N, bias, x, g, b, eps, h);
+        hipLaunchKernelGGL(k_splitk_residual_ln, dim3(M), dim3(1024), 0, st, ws, ks, M, w.N, bias, x, g, b, eps, h);
         return hipGetLastError();
     }
     // x = x + X W^T + bias in place (R = Y = x), then the LayerNorm

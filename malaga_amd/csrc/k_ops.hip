@@ -359,6 +359,85 @@ __global__ __launch_bounds__(1024) void k_greedy_finalize(const float *pv, const
     if (threadIdx.x == 0) *step = s + 1;
 }
 
+// Batched decode attention, one wave per (row, head) pair, no workgroup barrier:
+// lane (split, sub) owns dimensions [8 sub, 8 sub + 8) of keys j = k SPL + split; the
+// scores of a chunk of U SPL keys feed an online softmax (running max and sum), and
+// the splits are combined through the wave's LDS scratch at the end.
+template <int HD>
+__global__ __launch_bounds__(256) void k_attn_waves(const float *q, const __half *K, const __half *V, int b, int H,
+                                                    int L, const uint32_t *lens, const uint32_t *step, float *out,
+                                                    const uint32_t *rows) {
+    constexpr int TPK = HD / 8, SPL = 64 / TPK, U = 8;
+    __shared__ float wsc_all[4 * 512];
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    const int p = blockIdx.x * 4 + w;
+    if (p >= b * H) return;  // wave-uniform; no workgroup barrier below
+    float *wsc = wsc_all + w * 512;
+    const int bi = p / H, hh = p % H, d = H * HD;
+    const int sub = lane % TPK, split = lane / TPK;
+    const int n = lens ? int(lens[bi]) : int(*step) + 1;
+    const float *qp = q + size_t(bi) * d + hh * HD + sub * 8;
+    const float4 qa = *reinterpret_cast<const float4 *>(qp), qb = *reinterpret_cast<const float4 *>(qp + 4);
+    float m = -INFINITY, l = 0.f;
+    float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    for (int j0 = 0; j0 < n; j0 += U * SPL) {
+        uint4 kr[U], vr[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int j = min(j0 + u * SPL + split, L - 1);
+            const size_t r = rows ? rows[size_t(bi) * L + j] : size_t(bi);
+            const size_t o = ((r * H + hh) * L + j) * HD + sub * 8;
+            kr[u] = *reinterpret_cast<const uint4 *>(K + o);
+            vr[u] = *reinterpret_cast<const uint4 *>(V + o);
+        }
+        float sc[U];
+        float cmax = -INFINITY;
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            float sdot = h2f(kr[u].x) * qa.x;
+            sdot = fmaf(h2f(kr[u].x >> 16), qa.y, sdot);
+            sdot = fmaf(h2f(kr[u].y), qa.z, sdot);
+            sdot = fmaf(h2f(kr[u].y >> 16), qa.w, sdot);
+            sdot = fmaf(h2f(kr[u].z), qb.x, sdot);
+            sdot = fmaf(h2f(kr[u].z >> 16), qb.y, sdot);
+            sdot = fmaf(h2f(kr[u].w), qb.z, sdot);
+            sdot = fmaf(h2f(kr[u].w >> 16), qb.w, sdot);
+            sdot = group_sum<TPK>(sdot);
+            sc[u] = j0 + u * SPL + split < n ? sdot : -INFINITY;
+            cmax = fmaxf(cmax, sc[u]);
+        }
+        const float mnew = fmaxf(m, wave_max(cmax));  // finite: key j0 is valid
+        const float rs = expf(m - mnew);
+        l *= rs;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) acc[e] *= rs;
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const bool in = j0 + u * SPL + split < n;
+            const float pj = in ? expf(sc[u] - mnew) : 0.f;
+            l += pj;
+            const uint32_t wv[4] = {in ? vr[u].x : 0u, in ? vr[u].y : 0u, in ? vr[u].z : 0u, in ? vr[u].w : 0u};
+#pragma unroll
+            for (int q2 = 0; q2 < 4; ++q2) {
+                acc[2 * q2] = fmaf(pj, h2f(wv[q2]), acc[2 * q2]);
+                acc[2 * q2 + 1] = fmaf(pj, h2f(wv[q2] >> 16), acc[2 * q2 + 1]);
+            }
+        }
+        m = mnew;
+    }
+    const float inv = 1.f / wave_sum(sub == 0 ? l : 0.f);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) wsc[lane * 8 + e] = acc[e];
+    __builtin_amdgcn_s_waitcnt(0xc07f);
+    __builtin_amdgcn_wave_barrier();
+    for (int e = lane; e < HD; e += 64) {
+        float o = 0.f;
+#pragma unroll
+        for (int s2 = 0; s2 < SPL; ++s2) o += wsc[(s2 * TPK + e / 8) * 8 + e % 8];
+        out[size_t(bi) * d + hh * HD + e] = o * inv;
+    }
+}
+
 // ---- log-softmax + top-k (beam search) ------------------------------------
 constexpr int kTopMax = 8;
 constexpr int kTopParts = 64;
@@ -582,6 +661,19 @@ hipError_t qkv_split(const float *qkv, int b, int H, int hd, int m, const uint32
 hipError_t attn_decode(const float *q, const __half *K, const __half *V, int b, int H, int hd, int L,
                        const uint32_t *lens, const uint32_t *step, float *out, hipStream_t st, const uint32_t *rows) {
     if (hd % 8 || hd > 256) return hipErrorInvalidValue;
+    const dim3 wgrid(unsigned((b * H + 3) / 4));
+    switch (hd) {
+    case 16:
+        hipLaunchKernelGGL(k_attn_waves<16>, wgrid, dim3(256), 0, st, q, K, V, b, H, L, lens, step, out, rows);
+        return hipGetLastError();
+    case 64:
+        hipLaunchKernelGGL(k_attn_waves<64>, wgrid, dim3(256), 0, st, q, K, V, b, H, L, lens, step, out, rows);
+        return hipGetLastError();
+    case 128:
+        hipLaunchKernelGGL(k_attn_waves<128>, wgrid, dim3(256), 0, st, q, K, V, b, H, L, lens, step, out, rows);
+        return hipGetLastError();
+    default: break;
+    }
     const int block = 256, groups = block / hd > 0 ? block / hd : 1;
     const size_t shared = sizeof(float) * (hd + L + groups * hd);
     hipLaunchKernelGGL(k_attn_decode, dim3(b * H), dim3(block), shared, st, q, K, V, H, hd, L, lens, step, out, rows);
