@@ -319,7 +319,8 @@ int mlg_beam(mlg_model *m, const mlg_batch *b, uint32_t tgt_lang, int max_new, i
             return set_err(MLG_ERR_INVALID, "bad argument");
         std::lock_guard<std::mutex> lk(m->m->ctx->mu);
         mlg::check_hip(hipSetDevice(m->m->ctx->device), "hipSetDevice");
-        auto rows = m->m->beam(*b->b, tgt_lang, max_new, beam_size, length_penalty, (flags & MLG_FLAG_EOS_MASK) != 0);
+        auto rows = m->m->beam(*b->b, tgt_lang, max_new, beam_size, length_penalty, (flags & MLG_FLAG_EOS_MASK) != 0,
+                               !(flags & MLG_FLAG_NO_GRAPH));
         return write_rows(rows, out, out_cap, out_len);
     });
 }

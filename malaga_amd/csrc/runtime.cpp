@@ -695,7 +695,7 @@ std::vector<std::vector<uint32_t>> GraphCache::run(const Batch &src, uint32_t tg
 // ------------------------------------------------------------------- beam
 
 std::vector<std::vector<uint32_t>> Model::beam(const Batch &src, uint32_t tgt_lang, int max_new, int k, float lp,
-                                               bool eos_mask) {
+                                               bool eos_mask, bool use_graph) {
     hipStream_t s = ctx->stream;
     const int b = src.b, bk = b * k, V = cfg.vocab_size;
     const uint32_t eos = uint32_t(cfg.eos_token_id);
@@ -717,10 +717,49 @@ std::vector<std::vector<uint32_t>> Model::beam(const Batch &src, uint32_t tgt_la
     float *d_vals = tmp.get<float>(size_t(bk) * k, "topk vals");
     uint32_t *d_idx = tmp.get<uint32_t>(size_t(bk) * k, "topk idx");
 
+    auto topk = [&] {
+        check_hip(logsoftmax_topk(st->logits, bk, V, k, mask_id, scratch, d_vals, d_idx, s), "topk");
+    };
+    // Every beam step runs the same launches on the same buffers (ids, rows and the
+    // device step counter carry the changes), so one capture of step + top-k is
+    // replayed for all steps after the first two.
+    const bool capture = use_graph && graphs.capture_enabled();
+    struct ExecGuard {
+        hipGraphExec_t e = nullptr;
+        ~ExecGuard() {
+            if (e) (void)hipGraphExecDestroy(e);
+        }
+    } exec;
+    auto advance = [&] {
+        if (capture && !exec.e) {
+            check_hip(hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal), "begin capture");
+            hipGraph_t graph = nullptr;
+            try {
+                step(*st, false, mask_id);
+                topk();
+            } catch (...) {
+                (void)hipStreamEndCapture(s, &graph);
+                if (graph) (void)hipGraphDestroy(graph);
+                throw;
+            }
+            check_hip(hipStreamEndCapture(s, &graph), "end capture");
+            const hipError_t ie = hipGraphInstantiate(&exec.e, graph, nullptr, nullptr, 0);
+            (void)hipGraphDestroy(graph);
+            check_hip(ie, "graph instantiate");
+        }
+        if (exec.e) {
+            check_hip(hipGraphLaunch(exec.e, s), "graph launch");
+        } else {
+            step(*st, false, mask_id);
+            topk();
+        }
+    };
+
     // [start, tgt_lang] fed one position at a time (equal to the t = 2 causal pass)
     step(*st, false, mask_id);
     check_hip(fill_u32(st->ids, tgt_lang, size_t(bk), s), "fill");
     step(*st, false, mask_id);
+    topk();
 
     struct Hyp {
         float score;
@@ -733,7 +772,6 @@ std::vector<std::vector<uint32_t>> Model::beam(const Batch &src, uint32_t tgt_la
     std::vector<float> vals(static_cast<size_t>(bk) * k);
     std::vector<uint32_t> idx(static_cast<size_t>(bk) * k);
     for (int stp = 1; stp <= max_new; ++stp) {
-        check_hip(logsoftmax_topk(st->logits, bk, V, k, mask_id, scratch, d_vals, d_idx, s), "topk");
         check_hip(hipMemcpyAsync(vals.data(), d_vals, vals.size() * 4, hipMemcpyDeviceToHost, s), "D2H");
         check_hip(hipMemcpyAsync(idx.data(), d_idx, idx.size() * 4, hipMemcpyDeviceToHost, s), "D2H");
         check_hip(hipStreamSynchronize(s), "sync");
@@ -790,7 +828,7 @@ std::vector<std::vector<uint32_t>> Model::beam(const Batch &src, uint32_t tgt_la
         rows_map.swap(rows_next);
         h2d(st->rows, rows_map, s);
         h2d(st->ids, next, s);
-        step(*st, false, mask_id);
+        advance();
     }
     std::vector<std::vector<uint32_t>> res(static_cast<size_t>(b));
     for (int sn = 0; sn < b; ++sn) {
@@ -841,7 +879,7 @@ std::vector<std::vector<uint32_t>> generate_to(Model &m, const std::vector<std::
     if (o.beam_size <= 1)
         out = m.graphs.greedy(*batch, tgt_lang, max_new, std::max(1, o.sync_every), o.eos_mask, o.fused);
     else
-        out = m.beam(*batch, tgt_lang, max_new, o.beam_size, o.length_penalty, o.eos_mask);
+        out = m.beam(*batch, tgt_lang, max_new, o.beam_size, o.length_penalty, o.eos_mask, o.fused);
     for (size_t i = 0; i < src.size(); ++i) {
         const size_t bud = size_t(budget(m.cfg, int(src[i].size()), o.max_new_tokens));
         if (out[i].size() > bud) out[i].resize(bud);

@@ -149,9 +149,10 @@ class Model {
     // Whether the fused step kernels cover a state of b rows with caches of m / s slots.
     bool fusable(int b, int m, int s) const;
     void reset_state(StaticState &st, const Batch &src, const std::vector<uint32_t> &row_of, uint32_t start);
-    // src/translator.rs:250-335
+    // src/translator.rs:250-335.  use_graph: replay one captured step + top-k per
+    // beam step (off when capture is disabled for the cache).
     std::vector<std::vector<uint32_t>> beam(const Batch &src, uint32_t tgt_lang, int max_new, int k, float lp,
-                                            bool eos_mask);
+                                            bool eos_mask, bool use_graph = true);
     // Logits after feeding tgt[:, t] at position t, for t < T: [b][T][V] (parity tests).
     std::vector<float> teacher_forced(const Batch &src, const std::vector<uint32_t> &tgt, int T);
 

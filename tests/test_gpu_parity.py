@@ -85,6 +85,19 @@ def test_beam_matches_oracle(tiny_gguf, kq_gguf, models, k):
         assert got == gpu.generate(src, tgt)  # beam 1 == greedy (pipeline.rs:59-69)
 
 
+def test_beam_graph_replay_matches_eager(kq_gguf, models):
+    """The beam step is one captured step + top-k replayed every step; eager calls
+    between the graph calls check that every replay gives the eager tokens."""
+    gpu, _ = models(kq_gguf("q4_k_m"))
+    src = [[997, 5, 6, 7, 8, 2], [997, 40, 2], [997] + list(range(10, 30)) + [2]]
+    graph = M.GenOptions(beam_size=4, max_new_tokens=14)
+    eager = M.GenOptions(beam_size=4, max_new_tokens=14, fused=False)
+    want = gpu.generate(src, 998, eager)
+    for _ in range(3):
+        assert gpu.generate(src, 998, graph) == want
+        assert gpu.generate(src[:2], 998, eager) == want[:2]
+
+
 def test_batching_does_not_change_translations_gpu(tiny_gguf, models):
     gpu, _ = models(tiny_gguf("f32"))
     src = pipeline_sentences()
