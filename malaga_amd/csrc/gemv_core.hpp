@@ -293,6 +293,7 @@ struct NoPre {
     __device__ void operator()() const {}
 };
 
+// NT: rows >= nt_from are loaded non-temporally, the rows before with cached loads.
 // Streams the rows of W; calls epi(row, bi, value) on the group-leader lane of each
 // row (value = dot product + bias[row], the bias fetched with the weights).  Waves
 // gwave, gwave + nwaves, ... share the rows, G row groups per wave and step (two
@@ -306,7 +307,8 @@ struct NoPre {
 template <int T, int B, int CPL, bool NT = false, int G = 2, class PreF, class Pro, class Epi>
 __device__ __forceinline__ void gemv_rows(const WPtr &w, const GemvGeom &g, float (&xr)[CPL][B][GTraits<T>::XW],
                                           float (&xs)[CPL][B][GTraits<T>::NS], int gwave, int nwaves, PreF &&pre,
-                                          Pro &&prologue, Epi &epi, const float *bias = nullptr) {
+                                          Pro &&prologue, Epi &epi, const float *bias = nullptr,
+                                          int nt_from = 0) {
     const int lane = threadIdx.x & 63;
     const int lpr = 1 << g.lpr_log2, rpw = 64 >> g.lpr_log2;
     const int grp = lane >> g.lpr_log2, cl = lane & (lpr - 1);
@@ -318,8 +320,13 @@ __device__ __forceinline__ void gemv_rows(const WPtr &w, const GemvGeom &g, floa
 #pragma unroll
         for (int u = 0; u < G; ++u) {
             const int row = min((rg + u * nwaves) * rpw + grp, w.N - 1);
+            if (NT && (rg + u * nwaves) * rpw >= nt_from) {  // wave-uniform
 #pragma unroll
-            for (int t = 0; t < CPL; ++t) load_chunk<T, NT>(w, row, cidx[t], r[u][t]);
+                for (int t = 0; t < CPL; ++t) load_chunk<T, true>(w, row, cidx[t], r[u][t]);
+            } else {
+#pragma unroll
+                for (int t = 0; t < CPL; ++t) load_chunk<T, false>(w, row, cidx[t], r[u][t]);
+            }
             bv[u] = bias ? bias[row] : 0.f;
         }
     };

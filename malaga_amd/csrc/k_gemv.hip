@@ -20,6 +20,7 @@ struct GemvArgs {
     float *pv;  // argmax partials [nb][gridDim.x]
     uint32_t *pi;
     int mask_id;
+    int nt_from;  // LM head: first row loaded non-temporally
 };
 
 template <int B>
@@ -43,7 +44,8 @@ struct ArgmaxEpi {
 };
 
 // MODE 0: store (G = 1: small, latency-bound matrices); MODE 2: store, G = 2 (large
-// matrices); MODE 1: LM head with argmax partials, G = 2, non-temporal weights.
+// matrices); MODE 1: LM head with argmax partials, G = 1 (fewer registers, three
+// waves per SIMD), mostly non-temporal weights.
 template <int T, int B, int CPL, int MODE>
 __global__ __launch_bounds__(256) void k_gemv(GemvArgs a) {
     constexpr int XW = GTraits<T>::XW, NS = GTraits<T>::NS;
@@ -65,10 +67,10 @@ __global__ __launch_bounds__(256) void k_gemv(GemvArgs a) {
             epi.best[bi] = -INFINITY;
             epi.idx[bi] = 0xffffffffu;
         }
-        // non-temporal: the 215 MB stream then evicts less of the layer weights from the
-        // MALL between steps (measured: -20 us per 600M step, although the kernel alone
-        // is ~15% slower than with temporal loads)
-        gemv_rows<T, B, CPL, true>(a.w, a.g, xr, xs, gwave, nwaves, NoPre{}, load_x, epi, a.bias);
+        // rows >= nt_from non-temporal: the 215 MB stream then evicts less of the layer
+        // weights from the MALL between steps (measured: -20 us per 600M step, although
+        // the kernel alone is ~15% slower than with temporal loads)
+        gemv_rows<T, B, CPL, true, 1>(a.w, a.g, xr, xs, gwave, nwaves, NoPre{}, load_x, epi, a.bias, a.nt_from);
         __shared__ float sv[4][B];
         __shared__ uint32_t si[4][B];
         const int wv = threadIdx.x >> 6;
@@ -139,6 +141,12 @@ GemvArgs make_args(const DevMatrix &w, const GemvGeom &g, const float *x, int ld
 
 constexpr int kGemvSmallRows = 65536;
 
+// The LM head streams its first 30% of rows with cached loads and the rest
+// non-temporally: with the layer weights (112 MB for 600M q4_k_m) that part stays
+// in the 256 MB MALL from step to step, while an all-cached head would evict the
+// layers.  Measured on 600M q4_k_m batch-1 decode: 0.3 beats 0, 0.2, 0.45 and 1.
+constexpr double kLmHeadCachedFrac = 0.3;
+
 }  // namespace
 
 int gemv_grid(const DevMatrix &w, int G) {
@@ -182,7 +190,7 @@ hipError_t gemv(const DevMatrix &w, const float *x, int ldx, int b, float *y, in
 
 int gemv_argmax_parts(const DevMatrix &w, int b) {
     (void)b;
-    return gemv_grid(w);
+    return gemv_grid(w, 1);
 }
 
 hipError_t gemv_argmax(const DevMatrix &w, const float *x, int ldx, int b, int mask_id, float *pv, uint32_t *pi,
@@ -196,8 +204,9 @@ hipError_t gemv_argmax(const DevMatrix &w, const float *x, int ldx, int b, int m
     a.pv = pv;
     a.pi = pi;
     a.mask_id = mask_id;
-    const int grid = gemv_grid(w);
+    const int grid = gemv_grid(w, 1);
     *parts = grid;
+    a.nt_from = int(kLmHeadCachedFrac * w.N);
     return dispatch<1>(w.type, a, gemv_round_b(b), cpl, grid, st);
 }
 
