@@ -7,11 +7,23 @@
 // covers 64/LPR rows per row group and handles two row groups per step.  All
 // loads of a step are issued unconditionally (row and chunk indices clamped, x
 // zeroed for padding chunks), and the next step's loads are issued before the
-// current step is computed, so a wave keeps up to four rows in flight.  Integer
-// quants are widened with v_cvt_f32_ubyteN and accumulated in f32; block
-// offsets (q4_K/q5_K min, q6_K -32, q8_0 sign) are applied once per group from
-// per-lane sums of x.
+// current step is computed, so a wave keeps up to four rows in flight.
+//
+// Arithmetic.  In the large streaming GEMVs (the LM head) with integer formats
+// (q4_K, q5_K, q6_K, q8_0), x is held as three balanced signed 8-bit limbs per
+// value, x = s (c0 + 2^8 c1 + 2^16 c2), with one power-of-two scale s per group of
+// values (256 for the k-quants, 32 for q8_0) chosen so that |x / s| < 2^22.  The products of the integer quants with
+// the limbs are exact in int32 (v_dot4_i32_i8, four weights per instruction and
+// limb); the three limb sums of a sub-block are combined in f32 and scaled by
+// the block's scales.  This is the f32 dequantized product up to the 2^-23
+// relative rounding of x to its limbs, at about half the instructions per
+// weight of widening each quant to f32.  The small latency-bound GEMVs (and
+// F16/F32 weights) widen the quants with v_cvt_f32_ubyteN and use f32 FMAs on x:
+// there the conversion of x to limbs and its barrier would sit on the critical
+// path, which costs more than the arithmetic saves (measured on the fused step).
 #pragma once
+#include <type_traits>
+
 #include "device.hpp"
 #include "kernels.hpp"
 #include "quant.hpp"
@@ -62,6 +74,33 @@ struct Raw {
     uint4 a, b, c, h, e;
     uint32_t e0, e1;
 };
+
+// ---- x of one chunk (and batch rows 0..B-1) as the dot products read it ----
+
+template <int T>
+constexpr bool kLimbX = T == GGML_Q4_K || T == GGML_Q5_K || T == GGML_Q6_K || T == GGML_Q8_0;
+
+// f32 x: XW values and NS partial sums (F16/F32 weights; the attention-head projection)
+template <int T, int B>
+struct XF {
+    float x[B][GTraits<T>::XW];
+    float s[B][GTraits<T>::NS];
+};
+
+// limb x (integer formats): c[b][l][j] packs limb l of values 4j..4j+3 of the chunk
+template <int T, int B>
+struct XQ {
+    static constexpr int NW = GTraits<T>::XW / 4;
+    int c[B][3][NW];
+    float sc[B];         // scale s of the chunk's group
+    float ms[B][2];      // q4_K/q5_K: sum of x over each 32-value sub-block (min term)
+    int init[B][4][3];   // q6_K: -32 * (sum of limb l over 16-value group g)
+};
+
+// LIMB: the large streaming GEMVs (LM head) take limb x; small latency-bound ones
+// keep f32 x, whose staging adds nothing to the critical path
+template <int T, int B, bool LIMB>
+using XRep = std::conditional_t<LIMB && kLimbX<T>, XQ<T, B>, XF<T, B>>;
 
 typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
 typedef unsigned int u32x2_t __attribute__((ext_vector_type(2)));
@@ -132,8 +171,7 @@ __device__ __forceinline__ void load_chunk(const WPtr &w, int row, int c, Raw<T>
 }
 
 template <int T, int B>
-__device__ __forceinline__ void dot_chunk(int c, const Raw<T> &r, const float (&x)[B][GTraits<T>::XW],
-                                          const float (&xs)[B][GTraits<T>::NS], float (&acc)[B]) {
+__device__ __forceinline__ void dot_chunk(int c, const Raw<T> &r, const XF<T, B> &X, float (&acc)[B]) {
     if constexpr (T == GGML_Q4_K || T == GGML_Q5_K) {
         const int g = c & 3;
         // scale/min of sub-blocks 2g (low nibbles) and 2g+1 (high nibbles); the 6-bit
@@ -173,11 +211,11 @@ __device__ __forceinline__ void dot_chunk(int c, const Raw<T> &r, const float (&
             float al = 0.f, ah = 0.f;
 #pragma unroll
             for (int u = 0; u < 8; ++u) {
-                al = dot4u8(lo[u], &x[bi][4 * u], al);
-                ah = dot4u8(hi[u], &x[bi][32 + 4 * u], ah);
+                al = dot4u8(lo[u], &X.x[bi][4 * u], al);
+                ah = dot4u8(hi[u], &X.x[bi][32 + 4 * u], ah);
             }
             if constexpr (T == GGML_Q4_K) ah *= 0.0625f;
-            acc[bi] += d * (sc0 * al + sc1 * ah) - dmin * (m0 * xs[bi][0] + m1 * xs[bi][1]);
+            acc[bi] += d * (sc0 * al + sc1 * ah) - dmin * (m0 * X.s[bi][0] + m1 * X.s[bi][1]);
         }
     } else if constexpr (T == GGML_Q6_K) {
         const int i = c & 1;
@@ -199,13 +237,13 @@ __device__ __forceinline__ void dot_chunk(int c, const Raw<T> &r, const float (&
             float a0 = 0.f, a1 = 0.f, a2 = 0.f, a3 = 0.f;
 #pragma unroll
             for (int u = 0; u < 4; ++u) {
-                a0 = dot4u8(g0[u], &x[bi][4 * u], a0);
-                a1 = dot4u8(g1[u], &x[bi][16 + 4 * u], a1);
-                a2 = dot4u8(g2[u], &x[bi][32 + 4 * u], a2);
-                a3 = dot4u8(g3[u], &x[bi][48 + 4 * u], a3);
+                a0 = dot4u8(g0[u], &X.x[bi][4 * u], a0);
+                a1 = dot4u8(g1[u], &X.x[bi][16 + 4 * u], a1);
+                a2 = dot4u8(g2[u], &X.x[bi][32 + 4 * u], a2);
+                a3 = dot4u8(g3[u], &X.x[bi][48 + 4 * u], a3);
             }
-            acc[bi] += d * (sc[0] * (a0 - 32.f * xs[bi][0]) + sc[1] * (a1 - 32.f * xs[bi][1]) +
-                            sc[2] * (a2 - 32.f * xs[bi][2]) + sc[3] * (a3 - 32.f * xs[bi][3]));
+            acc[bi] += d * (sc[0] * (a0 - 32.f * X.s[bi][0]) + sc[1] * (a1 - 32.f * X.s[bi][1]) +
+                            sc[2] * (a2 - 32.f * X.s[bi][2]) + sc[3] * (a3 - 32.f * X.s[bi][3]));
         }
     } else if constexpr (T == GGML_Q8_0) {
         const float d = h2f(r.e0);
@@ -215,8 +253,8 @@ __device__ __forceinline__ void dot_chunk(int c, const Raw<T> &r, const float (&
         for (int bi = 0; bi < B; ++bi) {
             float a = 0.f;
 #pragma unroll
-            for (int u = 0; u < 8; ++u) a = dot4u8(w[u], &x[bi][4 * u], a);  // (q + 128) . x
-            acc[bi] += d * (a - 128.f * xs[bi][0]);
+            for (int u = 0; u < 8; ++u) a = dot4u8(w[u], &X.x[bi][4 * u], a);  // (q + 128) . x
+            acc[bi] += d * (a - 128.f * X.s[bi][0]);
         }
     } else if constexpr (T == GGML_F16) {
         const uint32_t w[4] = {r.a.x, r.a.y, r.a.z, r.a.w};
@@ -225,8 +263,8 @@ __device__ __forceinline__ void dot_chunk(int c, const Raw<T> &r, const float (&
             float a = acc[bi];
 #pragma unroll
             for (int u = 0; u < 4; ++u) {
-                a = fmaf(h2f(w[u]), x[bi][2 * u], a);
-                a = fmaf(h2f(w[u] >> 16), x[bi][2 * u + 1], a);
+                a = fmaf(h2f(w[u]), X.x[bi][2 * u], a);
+                a = fmaf(h2f(w[u] >> 16), X.x[bi][2 * u + 1], a);
             }
             acc[bi] = a;
         }
@@ -237,8 +275,107 @@ __device__ __forceinline__ void dot_chunk(int c, const Raw<T> &r, const float (&
         for (int bi = 0; bi < B; ++bi) {
             float a = acc[bi];
 #pragma unroll
-            for (int u = 0; u < 4; ++u) a = fmaf(w[u], x[bi][u], a);
+            for (int u = 0; u < 4; ++u) a = fmaf(w[u], X.x[bi][u], a);
             acc[bi] = a;
+        }
+    }
+}
+
+__device__ __forceinline__ int sdot4(uint32_t a, int b, int c) { return __builtin_amdgcn_sdot4(int(a), b, c, false); }
+
+// s0 + 2^8 s1 + 2^16 s2 of three limb sums, in f32
+__device__ __forceinline__ float limb_sum(int s0, int s1, int s2) { return float(s0 + (s1 << 8)) + 65536.f * float(s2); }
+
+template <int T, int B>
+__device__ __forceinline__ void dot_chunk(int c, const Raw<T> &r, const XQ<T, B> &X, float (&acc)[B]) {
+    if constexpr (T == GGML_Q4_K || T == GGML_Q5_K) {
+        const int g = c & 3;
+        const int sh0 = 8 * ((2 * g) & 3), sh1 = sh0 + 8;
+        const bool upper = g >= 2;
+        auto decode = [&](int sh, float &sc, float &mn) {
+            const uint32_t B0 = r.h.y >> sh, B1 = r.h.z >> sh, B2 = r.h.w >> sh;
+            const uint32_t a = upper ? ((B2 & 15u) | ((B0 >> 2) & 48u)) : (B0 & 63u);
+            const uint32_t bb = upper ? (((B2 >> 4) & 15u) | ((B1 >> 2) & 48u)) : (B1 & 63u);
+            sc = float(a);
+            mn = float(bb);
+        };
+        float sc0, m0, sc1, m1;
+        decode(sh0, sc0, m0);
+        decode(sh1, sc1, m1);
+        const float d = h2f(r.h.x), dmin = h2f(r.h.x >> 16);
+        const uint32_t w[8] = {r.a.x, r.a.y, r.a.z, r.a.w, r.b.x, r.b.y, r.b.z, r.b.w};
+        const uint32_t hb[8] = {r.c.x, r.c.y, r.c.z, r.c.w, r.e.x, r.e.y, r.e.z, r.e.w};  // q5_K fifth bits
+        uint32_t lo[8], hi[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            if constexpr (T == GGML_Q5_K) {
+                lo[u] = (w[u] & 0x0F0F0F0Fu) | (((hb[u] >> (2 * g)) & 0x01010101u) << 4);
+                hi[u] = ((w[u] >> 4) & 0x0F0F0F0Fu) | (((hb[u] >> (2 * g + 1)) & 0x01010101u) << 4);
+            } else {
+                lo[u] = w[u] & 0x0F0F0F0Fu;
+                hi[u] = (w[u] >> 4) & 0x0F0F0F0Fu;
+            }
+        }
+#pragma unroll
+        for (int bi = 0; bi < B; ++bi) {
+            int a0 = 0, a1 = 0, a2 = 0, b0 = 0, b1 = 0, b2 = 0;
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+                a0 = sdot4(lo[u], X.c[bi][0][u], a0);
+                a1 = sdot4(lo[u], X.c[bi][1][u], a1);
+                a2 = sdot4(lo[u], X.c[bi][2][u], a2);
+                b0 = sdot4(hi[u], X.c[bi][0][8 + u], b0);
+                b1 = sdot4(hi[u], X.c[bi][1][8 + u], b1);
+                b2 = sdot4(hi[u], X.c[bi][2][8 + u], b2);
+            }
+            acc[bi] += d * X.sc[bi] * (sc0 * limb_sum(a0, a1, a2) + sc1 * limb_sum(b0, b1, b2)) -
+                       dmin * (m0 * X.ms[bi][0] + m1 * X.ms[bi][1]);
+        }
+    } else if constexpr (T == GGML_Q6_K) {
+        const int i = c & 1;
+        const float d = h2f(r.c.x);
+        const float sc[4] = {float(int8_t(r.e0 >> (8 * i))), float(int8_t(r.e0 >> (8 * i + 16))),
+                             float(int8_t(r.e1 >> (8 * i))), float(int8_t(r.e1 >> (8 * i + 16)))};
+        const uint32_t A[4] = {r.a.x, r.a.y, r.a.z, r.a.w}, Bq[4] = {r.b.x, r.b.y, r.b.z, r.b.w},
+                       H[4] = {r.h.x, r.h.y, r.h.z, r.h.w};
+        uint32_t q6[4][4];  // 6-bit quants (0..63) of the four 16-value groups
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            q6[0][u] = (A[u] & 0x0F0F0F0Fu) | ((H[u] << 4) & 0x30303030u);
+            q6[1][u] = (Bq[u] & 0x0F0F0F0Fu) | ((H[u] << 2) & 0x30303030u);
+            q6[2][u] = ((A[u] >> 4) & 0x0F0F0F0Fu) | (H[u] & 0x30303030u);
+            q6[3][u] = ((Bq[u] >> 4) & 0x0F0F0F0Fu) | ((H[u] >> 2) & 0x30303030u);
+        }
+#pragma unroll
+        for (int bi = 0; bi < B; ++bi) {
+            float tot = 0.f;
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                // sum (q6 - 32) * limb: the -32 term is the accumulator's start value
+                int a0 = X.init[bi][q][0], a1 = X.init[bi][q][1], a2 = X.init[bi][q][2];
+#pragma unroll
+                for (int u = 0; u < 4; ++u) {
+                    a0 = sdot4(q6[q][u], X.c[bi][0][4 * q + u], a0);
+                    a1 = sdot4(q6[q][u], X.c[bi][1][4 * q + u], a1);
+                    a2 = sdot4(q6[q][u], X.c[bi][2][4 * q + u], a2);
+                }
+                tot = fmaf(sc[q], limb_sum(a0, a1, a2), tot);
+            }
+            acc[bi] += d * X.sc[bi] * tot;
+        }
+    } else {  // q8_0: signed 8-bit quants
+        const float d = h2f(r.e0);
+        const uint32_t w[8] = {r.a.x, r.a.y, r.a.z, r.a.w, r.b.x, r.b.y, r.b.z, r.b.w};
+#pragma unroll
+        for (int bi = 0; bi < B; ++bi) {
+            int a0 = 0, a1 = 0, a2 = 0;
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+                a0 = sdot4(w[u], X.c[bi][0][u], a0);
+                a1 = sdot4(w[u], X.c[bi][1][u], a1);
+                a2 = sdot4(w[u], X.c[bi][2][u], a2);
+            }
+            acc[bi] += d * X.sc[bi] * limb_sum(a0, a1, a2);
         }
     }
 }
@@ -259,8 +396,7 @@ __host__ __device__ constexpr int lds_pad(int i) { return i + ((i >> 6) << 2); }
 // PAD: x is an LDS copy in the lds_pad layout.
 template <int T, int B, int CPL, bool PAD = false>
 __device__ __forceinline__ void gemv_load_x(const float *x, int ldx, int nb, const GemvGeom &g, int cl,
-                                            float (&xr)[CPL][B][GTraits<T>::XW],
-                                            float (&xs)[CPL][B][GTraits<T>::NS]) {
+                                            XF<T, B> (&xr)[CPL]) {
     constexpr int XW = GTraits<T>::XW, NS = GTraits<T>::NS;
     const int lpr = 1 << g.lpr_log2;
 #pragma unroll
@@ -276,15 +412,151 @@ __device__ __forceinline__ void gemv_load_x(const float *x, int ldx, int nb, con
             for (int e = 0; e < XW; e += 4) {
                 const int o = PAD ? lds_pad(xpos<T>(cc, e)) : xpos<T>(cc, e);
                 const float4 q = *reinterpret_cast<const float4 *>(row + o);
-                xr[t][bi][e] = v ? q.x : 0.f;
-                xr[t][bi][e + 1] = v ? q.y : 0.f;
-                xr[t][bi][e + 2] = v ? q.z : 0.f;
-                xr[t][bi][e + 3] = v ? q.w : 0.f;
+                xr[t].x[bi][e] = v ? q.x : 0.f;
+                xr[t].x[bi][e + 1] = v ? q.y : 0.f;
+                xr[t].x[bi][e + 2] = v ? q.z : 0.f;
+                xr[t].x[bi][e + 3] = v ? q.w : 0.f;
             }
 #pragma unroll
-            for (int s = 0; s < NS; ++s) xs[t][bi][s] = 0.f;
+            for (int s = 0; s < NS; ++s) xr[t].s[bi][s] = 0.f;
 #pragma unroll
-            for (int e = 0; e < XW; ++e) xs[t][bi][xslot<T>(e)] += xr[t][bi][e];
+            for (int e = 0; e < XW; ++e) xr[t].s[bi][xslot<T>(e)] += xr[t].x[bi][e];
+        }
+    }
+}
+
+// ---- limb x in LDS ----
+//
+// Row b of a staged x occupies xq_row_words(K) words: limb l of value word j
+// (values 4j..4j+3) at l * xq_lw(K) + lq_pad(j), then one f32 scale per group of
+// kScaleWords words.  4 words of padding after every 16 spread the 16-byte reads
+// of a row group's lanes (16 words apart) over the banks.
+
+template <int T>
+constexpr int kScaleWords = T == GGML_Q8_0 ? 8 : 64;  // value words per scale: q8_0 block / k-quant super-block
+
+__host__ __device__ constexpr int lq_pad(int j) { return j + ((j >> 4) << 2); }
+__host__ __device__ constexpr int xq_lw(int K) { return lq_pad(K / 4 - 1) + 1; }
+template <int T>
+__host__ __device__ constexpr int xq_row_words(int K) {
+    return (3 * xq_lw(K) + K / (4 * kScaleWords<T>) + 3) & ~3;
+}
+template <int T>
+__host__ __device__ constexpr int xq_lds_bytes(int K, int nb) {
+    return 4 * nb * xq_row_words<T>(K);
+}
+
+// Limbs of four values of one scale group.  Every lane of the wave must call this
+// (group maximum over SW lanes); a group of SW lanes shares the scale.
+template <int SW>
+__device__ __forceinline__ void limbs4(const float4 v, uint32_t &w0, uint32_t &w1, uint32_t &w2, float &scale) {
+    float m = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
+    m = group_reduce(m, SW == 64 ? 6 : 3, OpMax{});
+    int E;
+    (void)frexpf(m, &E);  // m < 2^E
+    const int e = m > 0.f ? 22 - E : 0;
+    const float vv[4] = {v.x, v.y, v.z, v.w};
+    w0 = w1 = w2 = 0u;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int xi = int(rintf(ldexpf(vv[i], e)));  // |xi| <= 2^22
+        const int c0 = (xi << 24) >> 24;              // balanced digits: c0, c1 in [-128, 127]
+        const int r = (xi - c0) >> 8;
+        const int c1 = (r << 24) >> 24;
+        const int c2 = (r - c1) >> 8;                 // |c2| <= 64
+        w0 |= uint32_t(c0 & 255) << (8 * i);
+        w1 |= uint32_t(c1 & 255) << (8 * i);
+        w2 |= uint32_t(c2 & 255) << (8 * i);
+    }
+    scale = ldexpf(1.f, -e);
+}
+
+// Stores the limbs of value word j of row `row` (from limbs4).
+template <int T>
+__device__ __forceinline__ void store_limbs(uint32_t *row, int K, int j, uint32_t w0, uint32_t w1, uint32_t w2,
+                                            float scale) {
+    const int lw = xq_lw(K), pj = lq_pad(j);
+    row[pj] = w0;
+    row[lw + pj] = w1;
+    row[2 * lw + pj] = w2;
+    if (j % kScaleWords<T> == 0) reinterpret_cast<float *>(row)[3 * lw + j / kScaleWords<T>] = scale;
+}
+
+// Workgroup-cooperative: rows [0, nb) of x [nb][ldx] (global, 16-byte aligned) to
+// limbs in LDS.  Needs K % (4 kScaleWords) == 0; every thread must call it; the
+// caller puts a barrier before the limbs are read.
+template <int T>
+__device__ __forceinline__ void stage_limbs(const float *x, int ldx, int nb, int K, uint32_t *lds) {
+    const int nw = K >> 2, total = nb * nw, rw = xq_row_words<T>(K);
+    for (int base = 0; base < total; base += blockDim.x) {
+        // groups of kScaleWords lanes are all in or all out (total is a multiple)
+        const int idx = base + int(threadIdx.x);
+        const int jj = min(idx, total - 1);
+        const int bi = jj / nw, j = jj - bi * nw;
+        const float4 v = *reinterpret_cast<const float4 *>(x + size_t(bi) * ldx + 4 * j);
+        uint32_t w0, w1, w2;
+        float scale;
+        limbs4<kScaleWords<T>>(v, w0, w1, w2, scale);
+        if (idx < total) store_limbs<T>(lds + bi * rw, K, j, w0, w1, w2, scale);
+    }
+}
+
+// This lane's chunks of the staged limb rows [0, nb) into registers (padding rows
+// and chunks zero), with the per-chunk sums the dot products need.
+template <int T, int B, int CPL>
+__device__ __forceinline__ void gemv_load_xq(const uint32_t *lds, int K, int nb, const GemvGeom &g, int cl,
+                                             XQ<T, B> (&xr)[CPL]) {
+    constexpr int NW = XQ<T, B>::NW;
+    const int lpr = 1 << g.lpr_log2, lw = xq_lw(K), rw = xq_row_words<T>(K);
+#pragma unroll
+    for (int t = 0; t < CPL; ++t) {
+        const int c = cl + t * lpr;
+        const bool valid = c < g.nchunks;
+        const int cc = valid ? c : 0;
+        int run[NW / 4];  // value word of each 4-word run of the chunk
+#pragma unroll
+        for (int q = 0; q < NW / 4; ++q) {
+            if constexpr (T == GGML_Q6_K) run[q] = (cc >> 2) * 64 + ((cc >> 1) & 1) * 32 + (cc & 1) * 4 + 8 * q;
+            else if constexpr (T == GGML_Q8_0) run[q] = 8 * cc + 4 * q;
+            else run[q] = (cc >> 2) * 64 + (cc & 3) * 16 + 4 * q;
+        }
+        const int sg = T == GGML_Q8_0 ? cc : (cc >> 2);
+#pragma unroll
+        for (int bi = 0; bi < B; ++bi) {
+            const bool v = valid && bi < nb;
+            const uint32_t *row = lds + (bi < nb ? bi : 0) * rw;
+#pragma unroll
+            for (int l = 0; l < 3; ++l)
+#pragma unroll
+                for (int q = 0; q < NW / 4; ++q) {
+                    const uint4 u = *reinterpret_cast<const uint4 *>(row + l * lw + lq_pad(run[q]));
+                    xr[t].c[bi][l][4 * q] = v ? int(u.x) : 0;
+                    xr[t].c[bi][l][4 * q + 1] = v ? int(u.y) : 0;
+                    xr[t].c[bi][l][4 * q + 2] = v ? int(u.z) : 0;
+                    xr[t].c[bi][l][4 * q + 3] = v ? int(u.w) : 0;
+                }
+            xr[t].sc[bi] = v ? reinterpret_cast<const float *>(row)[3 * lw + sg] : 0.f;
+            if constexpr (T == GGML_Q4_K || T == GGML_Q5_K) {
+#pragma unroll
+                for (int h = 0; h < 2; ++h) {
+                    int s3[3] = {0, 0, 0};
+#pragma unroll
+                    for (int l = 0; l < 3; ++l)
+#pragma unroll
+                        for (int u = 0; u < 8; ++u) s3[l] = sdot4(0x01010101u, xr[t].c[bi][l][8 * h + u], s3[l]);
+                    xr[t].ms[bi][h] = xr[t].sc[bi] * limb_sum(s3[0], s3[1], s3[2]);
+                }
+            } else if constexpr (T == GGML_Q6_K) {
+#pragma unroll
+                for (int q = 0; q < 4; ++q)
+#pragma unroll
+                    for (int l = 0; l < 3; ++l) {
+                        int s1 = 0;
+#pragma unroll
+                        for (int u = 0; u < 4; ++u) s1 = sdot4(0x01010101u, xr[t].c[bi][l][4 * q + u], s1);
+                        xr[t].init[bi][q][l] = -32 * s1;
+                    }
+            }
         }
     }
 }
@@ -302,12 +574,11 @@ struct NoPre {
 // Order of issue: pre() (loads the
 // prologue needs, so that waiting for them does not wait for the weights: loads
 // complete in order), the first step's weights, then prologue(), which fills
-// xr/xs and may use workgroup barriers (every thread of the workgroup must call
+// xr and may use workgroup barriers (every thread of the workgroup must call
 // this function).
-template <int T, int B, int CPL, bool NT = false, int G = 2, class PreF, class Pro, class Epi>
-__device__ __forceinline__ void gemv_rows(const WPtr &w, const GemvGeom &g, float (&xr)[CPL][B][GTraits<T>::XW],
-                                          float (&xs)[CPL][B][GTraits<T>::NS], int gwave, int nwaves, PreF &&pre,
-                                          Pro &&prologue, Epi &epi, const float *bias = nullptr,
+template <int T, int B, int CPL, bool NT = false, int G = 2, class XR, class PreF, class Pro, class Epi>
+__device__ __forceinline__ void gemv_rows(const WPtr &w, const GemvGeom &g, XR (&xr)[CPL], int gwave, int nwaves,
+                                          PreF &&pre, Pro &&prologue, Epi &epi, const float *bias = nullptr,
                                           int nt_from = 0) {
     const int lane = threadIdx.x & 63;
     const int lpr = 1 << g.lpr_log2, rpw = 64 >> g.lpr_log2;
@@ -337,7 +608,7 @@ __device__ __forceinline__ void gemv_rows(const WPtr &w, const GemvGeom &g, floa
 #pragma unroll
             for (int bi = 0; bi < B; ++bi) acc[bi] = 0.f;
 #pragma unroll
-            for (int t = 0; t < CPL; ++t) dot_chunk<T, B>(cidx[t], r[u][t], xr[t], xs[t], acc);
+            for (int t = 0; t < CPL; ++t) dot_chunk<T, B>(cidx[t], r[u][t], xr[t], acc);
 #pragma unroll
             for (int bi = 0; bi < B; ++bi)
                 acc[bi] = group_sum_dyn(acc[bi], g.lpr_log2);
@@ -412,5 +683,16 @@ inline bool gemv_geometry(const DevMatrix &w, GemvGeom *g, int *cpl) {
 }
 
 inline int gemv_round_b(int b) { return b <= 1 ? 1 : (b <= 2 ? 2 : 4); }
+
+// LDS bytes of nb staged limb rows of K values (0 for the f32-x formats)
+inline size_t gemv_xq_lds(uint32_t t, int K, int nb) {
+    switch (t) {
+    case GGML_Q4_K: return xq_lds_bytes<GGML_Q4_K>(K, nb);
+    case GGML_Q5_K: return xq_lds_bytes<GGML_Q5_K>(K, nb);
+    case GGML_Q6_K: return xq_lds_bytes<GGML_Q6_K>(K, nb);
+    case GGML_Q8_0: return xq_lds_bytes<GGML_Q8_0>(K, nb);
+    default: return 0;
+    }
+}
 
 }  // namespace mlg

@@ -46,20 +46,31 @@ struct ArgmaxEpi {
 // MODE 0: store (G = 1: small, latency-bound matrices); MODE 2: store, G = 2 (large
 // matrices); MODE 1: LM head with argmax partials, G = 1 (fewer registers, three
 // waves per SIMD), mostly non-temporal weights.
+template <int T, int MODE>
+constexpr bool kGemvLimbs = MODE != 0 && kLimbX<T>;  // large matrices: limb x (gemv_core.hpp)
+
 template <int T, int B, int CPL, int MODE>
 __global__ __launch_bounds__(256) void k_gemv(GemvArgs a) {
-    constexpr int XW = GTraits<T>::XW, NS = GTraits<T>::NS;
+    extern __shared__ uint32_t xlds[];  // limbs of x
     const int lane = threadIdx.x & 63;
     const int cl = lane & ((1 << a.g.lpr_log2) - 1);
-    float xr[CPL][B][XW], xs[CPL][B][NS];
-    auto load_x = [&] { gemv_load_x<T, B, CPL>(a.x, a.ldx, a.nb, a.g, cl, xr, xs); };
+    XRep<T, B, kGemvLimbs<T, MODE>> xr[CPL];
+    auto load_x = [&] {
+        if constexpr (kGemvLimbs<T, MODE>) {
+            stage_limbs<T>(a.x, a.ldx, a.nb, a.w.K, xlds);
+            lds_barrier();
+            gemv_load_xq<T, B, CPL>(xlds, a.w.K, a.nb, a.g, cl, xr);
+        } else {
+            gemv_load_x<T, B, CPL>(a.x, a.ldx, a.nb, a.g, cl, xr);
+        }
+    };
     const int gwave = blockIdx.x * 4 + (threadIdx.x >> 6), nwaves = gridDim.x * 4;
     if constexpr (MODE == 0) {
         StoreEpi<B> epi{a};
-        gemv_rows<T, B, CPL, false, 1>(a.w, a.g, xr, xs, gwave, nwaves, NoPre{}, load_x, epi, a.bias);
+        gemv_rows<T, B, CPL, false, 1>(a.w, a.g, xr, gwave, nwaves, NoPre{}, load_x, epi, a.bias);
     } else if constexpr (MODE == 2) {
         StoreEpi<B> epi{a};
-        gemv_rows<T, B, CPL, false, 2>(a.w, a.g, xr, xs, gwave, nwaves, NoPre{}, load_x, epi, a.bias);
+        gemv_rows<T, B, CPL, false, 2>(a.w, a.g, xr, gwave, nwaves, NoPre{}, load_x, epi, a.bias);
     } else {  // the LM head: weights streamed once per step
         ArgmaxEpi<B> epi{a, {}, {}};
 #pragma unroll
@@ -70,7 +81,7 @@ __global__ __launch_bounds__(256) void k_gemv(GemvArgs a) {
         // rows >= nt_from non-temporal: the 215 MB stream then evicts less of the layer
         // weights from the MALL between steps (measured: -20 us per 600M step, although
         // the kernel alone is ~15% slower than with temporal loads)
-        gemv_rows<T, B, CPL, true, 1>(a.w, a.g, xr, xs, gwave, nwaves, NoPre{}, load_x, epi, a.bias, a.nt_from);
+        gemv_rows<T, B, CPL, true, 1>(a.w, a.g, xr, gwave, nwaves, NoPre{}, load_x, epi, a.bias, a.nt_from);
         __shared__ float sv[4][B];
         __shared__ uint32_t si[4][B];
         const int wv = threadIdx.x >> 6;
@@ -99,7 +110,9 @@ hipError_t launch_t(const GemvArgs &a, int grid, hipStream_t st) {
     if constexpr (GTraits<T>::XW * B * CPL > kGemvMaxXRegs) {
         return hipErrorInvalidValue;
     } else {
-        hipLaunchKernelGGL((k_gemv<T, B, CPL, MODE>), dim3(grid), dim3(256), 0, st, a);
+        const int lds = kGemvLimbs<T, MODE> ? xq_lds_bytes<T>(a.w.K, a.nb) : 0;
+        if (lds > 65536) return hipErrorInvalidValue;
+        hipLaunchKernelGGL((k_gemv<T, B, CPL, MODE>), dim3(grid), dim3(256), lds, st, a);
         return hipGetLastError();
     }
 }

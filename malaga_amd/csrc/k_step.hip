@@ -215,13 +215,14 @@ __device__ __forceinline__ void resid_ln_prologue(const StepArgs &a, const PreLo
 
 template <int T, int B, int CPL, int PRO, int EPI, int ET>
 __global__ __launch_bounds__(256) void k_step(StepArgs a) {
-    constexpr int XW = GTraits<T>::XW, NS = GTraits<T>::NS;
     extern __shared__ float lds[];
     __shared__ double red[32];
     const int lane = threadIdx.x & 63;
     const int cl = lane & ((1 << a.g.lpr_log2) - 1);
     const int gwave = blockIdx.x * 4 + (threadIdx.x >> 6), nwaves = gridDim.x * 4;
-    float xr[CPL][B][XW], xs[CPL][B][NS];
+    // f32 x: these kernels are latency-bound, and staging integer limbs of x would
+    // add a conversion and a barrier to the critical path (measured slower)
+    XF<T, B> xr[CPL];
     PreLoads L;
 
     auto pre = [&] {
@@ -229,10 +230,10 @@ __global__ __launch_bounds__(256) void k_step(StepArgs a) {
     };
     auto prologue = [&] {
         if constexpr (PRO == PRO_GLOBAL) {
-            gemv_load_x<T, B, CPL>(a.xg, a.ldx, a.nb, a.g, cl, xr, xs);
+            gemv_load_x<T, B, CPL>(a.xg, a.ldx, a.nb, a.g, cl, xr);
         } else {
             resid_ln_prologue<PRO, ET>(a, L, lds, red);
-            gemv_load_x<T, B, CPL, true>(lds, lds_pad(a.d), a.nb, a.g, cl, xr, xs);
+            gemv_load_x<T, B, CPL, true>(lds, lds_pad(a.d), a.nb, a.g, cl, xr);
         }
     };
 
@@ -242,7 +243,7 @@ __global__ __launch_bounds__(256) void k_step(StepArgs a) {
             if (a.relu) v = fmaxf(v, 0.f);
             a.y[size_t(bi) * a.w.N + row] = v;
         };
-        gemv_rows<T, B, CPL, false, 1>(a.w, a.g, xr, xs, gwave, nwaves, pre, prologue, epi, a.bias);
+        gemv_rows<T, B, CPL, false, 1>(a.w, a.g, xr, gwave, nwaves, pre, prologue, epi, a.bias);
     } else {
         const uint32_t slot = *a.step;
         auto epi = [&](int row, int bi, float v) {
@@ -256,7 +257,7 @@ __global__ __launch_bounds__(256) void k_step(StepArgs a) {
                 (row < 2 * d ? a.kc : a.vc)[off] = __float2half(v);
             }
         };
-        gemv_rows<T, B, CPL, false, 1>(a.w, a.g, xr, xs, gwave, nwaves, pre, prologue, epi, a.bias);
+        gemv_rows<T, B, CPL, false, 1>(a.w, a.g, xr, gwave, nwaves, pre, prologue, epi, a.bias);
     }
 }
 
@@ -406,21 +407,21 @@ __global__ __launch_bounds__(256) void k_attn_head(HeadArgs a) {
 #pragma unroll
     for (int bi = 0; bi < 4; ++bi) {
         if (bi >= nb) break;
-        float xr[1][XW], xs[1][NS];
+        XF<T, 1> X;
 #pragma unroll
         for (int e = 0; e < XW; e += 4) {
             const float4 x4 = *reinterpret_cast<const float4 *>(outv + bi * C + xpos<T>(c, e) - col0);
-            xr[0][e] = x4.x;
-            xr[0][e + 1] = x4.y;
-            xr[0][e + 2] = x4.z;
-            xr[0][e + 3] = x4.w;
+            X.x[0][e] = x4.x;
+            X.x[0][e + 1] = x4.y;
+            X.x[0][e + 2] = x4.z;
+            X.x[0][e + 3] = x4.w;
         }
 #pragma unroll
-        for (int s2 = 0; s2 < NS; ++s2) xs[0][s2] = 0.f;
+        for (int s2 = 0; s2 < NS; ++s2) X.s[0][s2] = 0.f;
 #pragma unroll
-        for (int e = 0; e < XW; ++e) xs[0][xslot<T>(e)] += xr[0][e];
+        for (int e = 0; e < XW; ++e) X.s[0][xslot<T>(e)] += X.x[0][e];
         float a1[1] = {0.f};
-        dot_chunk<T, 1>(c, wr, xr, xs, a1);
+        dot_chunk<T, 1>(c, wr, X, a1);
         acc[bi] = a1[0];
     }
 #pragma unroll

@@ -161,6 +161,46 @@ def test_gemm_argmax_batched_lm_head(ctx, t, K):
         ctx.lib.mlg_matrix_free(w)
 
 
+@pytest.mark.parametrize("t,K", [(Q4_K, 1024), (Q5_K, 512), (Q6_K, 1024), (Q8_0, 1024), (Q8_0, 96)])
+def test_large_gemv_integer_limbs(ctx, t, K):
+    """N > 65536: the streaming GEMVs hold x as 8-bit limbs with one power-of-two
+    scale per group (exact integer dot products).  Besides f32 rounding, each x_k
+    is rounded by at most 2^-23 of its group's max |x|; the store and the fused
+    argmax (LM head) both follow the dequantized f64 dot product."""
+    rng = np.random.default_rng(K + t)
+    N = 70001
+    wf = rng.normal(0, 0.02, (N, K)).astype(np.float32)
+    blocks = M.quantize(t, wf)
+    w = upload(ctx, t, blocks, N, K)
+    try:
+        wd = O.dequant(t, blocks, N * K).reshape(N, K)
+        absw = np.abs(wd.astype(np.float64)).sum(1)
+        for b in sorted({1, ctx.lib.mlg_gemv_max_batch(w)}):
+            x = rng.normal(0, 1, (b, K)).astype(np.float32)
+            x[:, 5] = 40.0  # a group whose scale is set by one large value
+            ref = O.gemv(t, blocks, N, K, x)
+            tol = 2e-6 * bound(x, wd) + 2.0 ** -22 * np.abs(x).max(1, keepdims=True) * absw + 1e-6
+            xd, yd = dev(x), torch.zeros((b, N), device="cuda")
+            _lib.check(ctx.lib.mlg_gemv(w, ptr(xd), b, ptr(yd), None, 0, None))
+            torch.cuda.synchronize()
+            err = np.abs(yd.cpu().numpy() - ref)
+            assert (err <= tol).all(), (b, err.max())
+            parts = ctx.lib.mlg_gemv_argmax_parts(w, b)
+            pv = torch.zeros((b, parts), device="cuda")
+            pi = torch.zeros((b, parts), dtype=torch.int32, device="cuda")
+            _lib.check(ctx.lib.mlg_gemv_argmax(w, ptr(xd), b, -1, ptr(pv), ptr(pi), None))
+            torch.cuda.synchronize()
+            v, i = pv.cpu().numpy(), pi.cpu().numpy().view(np.uint32)
+            for r in range(b):
+                top = np.argsort(ref[r])[::-1][:2]
+                k = int(np.argmax(v[r]))
+                assert abs(v[r][k] - ref[r][top[0]]) <= tol[r][top[0]]
+                if ref[r][top[0]] - ref[r][top[1]] > 2 * tol[r].max():
+                    assert i[r][k] == top[0]
+    finally:
+        ctx.lib.mlg_matrix_free(w)
+
+
 @pytest.mark.parametrize("t", [Q6_K, Q4_K, Q8_0])
 def test_gemv_argmax_lowest_index_on_ties(ctx, t):
     rng = np.random.default_rng(99)
