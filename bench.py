@@ -56,6 +56,51 @@ def model_path(preset: str) -> Path:
     return p
 
 
+def model_path_3b(preset: str) -> Path:
+    import malaga_amd as M
+
+    d = Path(os.environ.get("MALAGA_MODEL_DIR", "/tmp/malaga_bench_models"))
+    d.mkdir(parents=True, exist_ok=True)
+    p = d / f"nllb3b3-random-s0-{preset}.gguf"
+    if not p.exists():
+        t = time.time()
+        M.write_synthetic(p, M.nllb_3b_config(), preset, M.INIT_NORMAL, seed=0, std=0.02,
+                          name="nllb-200-3.3B (random init, seed 0)")
+        log(f"wrote {p.name} ({p.stat().st_size / 1e6:.0f} MB) in {time.time() - t:.1f} s")
+    return p
+
+
+def bench_config5():
+    """Config 5: NLLB-3.3B q4_k_m, 64 sentences (lognormal lengths, mean 28, max 256), greedy
+    64 steps with EOS masked, one batch of 64 (length-sorted as translate_batch does)."""
+    import torch
+    import malaga_amd as M
+
+    T = M.Translator.load(model_path_3b("q4_k_m"))
+    lens = lognormal_lengths(64, 28, 4, 256, seed=5)
+    rng = np.random.default_rng(55)
+    src = [rng.integers(4, 256206, n).tolist() for n in lens]
+    opts = M.GenOptions(eos_mask=True, max_batch=64, max_new_tokens=64)
+    T.generate(src, TGT_LANG, opts)
+    torch.cuda.synchronize()
+    times, enc = [], []
+    for _ in range(3):
+        a = time.perf_counter()
+        out = T.generate(src, TGT_LANG, opts)
+        torch.cuda.synchronize()
+        times.append(time.perf_counter() - a)
+        a = time.perf_counter()
+        T.encode_cross(src)
+        torch.cuda.synchronize()
+        enc.append(time.perf_counter() - a)
+    dt, de = float(np.median(times)), float(np.median(enc))
+    toks = sum(len(r) for r in out)
+    T.close()
+    return dict(sentences_per_s=len(src) / dt, ms_per_batch=dt * 1e3, encoder_ms=de * 1e3,
+                decoder_ms_per_step=(dt - de) * 1e3 / 65, tokens=toks, max_src_len=max(lens),
+                weights_mb=round(model_path_3b("q4_k_m").stat().st_size / 1e6))
+
+
 def sources(n: int, length: int, seed: int) -> list[list[int]]:
     """Seeded random source ids U[4, 256206) (raw ids, no language/eos framing)."""
     return [np.random.default_rng(seed + i).integers(4, 256206, length).tolist() for i in range(n)]
@@ -279,7 +324,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--skip-cpu", action="store_true")
     ap.add_argument("--legs", default="bs1,batched,kernels,cpu",
-                    help="comma-separated subset of bs1,batched,kernels,cpu (profiling runs)")
+                    help="comma-separated subset of bs1,batched,kernels,cpu (profiling runs); "
+                         "'config5' alone runs only the 3.3B batch-64 leg")
     ap.add_argument("--roofline-only", action="store_true", help="only the LM-head roofline leg (for rocprof)")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -311,6 +357,12 @@ def main():
         return
 
     legs = set(args.legs.split(","))
+    if legs == {"config5"}:
+        r = bench_config5()
+        log(f"config5: {r['sentences_per_s']:.1f} sentences/s ({r['ms_per_batch']:.1f} ms/batch, encoder "
+            f"{r['encoder_ms']:.1f} ms, {r['decoder_ms_per_step']:.2f} ms/step)")
+        print(json.dumps({"config5": r}))
+        return
     if args.skip_cpu:
         legs.discard("cpu")
     log("loading the model")

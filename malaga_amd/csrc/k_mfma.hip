@@ -63,6 +63,7 @@ struct MW;  // per-type W fetch for one 256-wide K step
 template <>
 struct MW<GGML_Q4_K> {
     static constexpr int SLICES = 8, SK = 32;
+    static constexpr bool MIN = true;  // w = sc q - mn: the x sums carry the min term
     struct Regs {
         uint4 hdr;
         uint2 q[4];
@@ -92,6 +93,7 @@ struct MW<GGML_Q4_K> {
 template <>
 struct MW<GGML_Q5_K> {
     static constexpr int SLICES = 8, SK = 32;
+    static constexpr bool MIN = true;
     struct Regs {
         uint4 hdr;
         uint2 q[4];
@@ -126,6 +128,7 @@ struct MW<GGML_Q5_K> {
 template <>
 struct MW<GGML_Q6_K> {
     static constexpr int SLICES = 16, SK = 16;
+    static constexpr bool MIN = false;
     struct Regs {
         uint32_t qa[4], qb[4], qh[4];  // [2 n + h]
         uint4 sc;
@@ -162,6 +165,7 @@ struct MW<GGML_Q6_K> {
 template <>
 struct MW<GGML_Q8_0> {
     static constexpr int SLICES = 8, SK = 32;
+    static constexpr bool MIN = false;
     struct Regs {
         uint2 q[8];
         uint4 d;  // 8 f16 scales
@@ -188,6 +192,7 @@ struct MW<GGML_Q8_0> {
 template <>
 struct MW<GGML_F16> {
     static constexpr int SLICES = 8, SK = 32;
+    static constexpr bool MIN = false;
     struct Regs {
         uint4 q[8];
     };
@@ -287,16 +292,21 @@ __global__ __launch_bounds__(256) void k_mfma(MfmaArgs a) {
                     tmp = __builtin_amdgcn_mfma_f32_16x16x16f16(al, bop, tmp, 0, 0, 0);
                 }
                 // output rows m = mt 16 + 4 kq + r of this lane; x sums of the slice
-                const float *xsp = xsum + (s * W::SK / 16) * BM + mt * 16 + 4 * kq;
-                float4 xsv = *reinterpret_cast<const float4 *>(xsp);
-                if constexpr (W::SK == 32) {
-                    const float4 x2 = *reinterpret_cast<const float4 *>(xsp + BM);
-                    xsv = make_float4(xsv.x + x2.x, xsv.y + x2.y, xsv.z + x2.z, xsv.w + x2.w);
+                if constexpr (W::MIN) {
+                    const float *xsp = xsum + (s * W::SK / 16) * BM + mt * 16 + 4 * kq;
+                    float4 xsv = *reinterpret_cast<const float4 *>(xsp);
+                    if constexpr (W::SK == 32) {
+                        const float4 x2 = *reinterpret_cast<const float4 *>(xsp + BM);
+                        xsv = make_float4(xsv.x + x2.x, xsv.y + x2.y, xsv.z + x2.z, xsv.w + x2.w);
+                    }
+                    acc[mt][0] = fmaf(sc, tmp[0], fmaf(-mn, xsv.x, acc[mt][0]));
+                    acc[mt][1] = fmaf(sc, tmp[1], fmaf(-mn, xsv.y, acc[mt][1]));
+                    acc[mt][2] = fmaf(sc, tmp[2], fmaf(-mn, xsv.z, acc[mt][2]));
+                    acc[mt][3] = fmaf(sc, tmp[3], fmaf(-mn, xsv.w, acc[mt][3]));
+                } else {
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) acc[mt][r] = fmaf(sc, tmp[r], acc[mt][r]);
                 }
-                acc[mt][0] = fmaf(sc, tmp[0], fmaf(-mn, xsv.x, acc[mt][0]));
-                acc[mt][1] = fmaf(sc, tmp[1], fmaf(-mn, xsv.y, acc[mt][1]));
-                acc[mt][2] = fmaf(sc, tmp[2], fmaf(-mn, xsv.z, acc[mt][2]));
-                acc[mt][3] = fmaf(sc, tmp[3], fmaf(-mn, xsv.w, acc[mt][3]));
             }
         }
         cur = nxt;
@@ -349,8 +359,201 @@ __global__ __launch_bounds__(256) void k_splitk_reduce(const float *part, int ks
     y[size_t(m) * ldy + n] = v;
 }
 
+// ------------------------------------------------------------- wide tiles
+//
+// For large N at M > 32 (the LM head and FFN of batched decode, encoder prefill):
+// 8 waves, each owning WT 16-row tiles of W, so a workgroup covers 128 WT rows of
+// W and one staging of X per K step (f32 -> f16 hi/lo in LDS, x sums) serves
+// 2 WT times more rows than in k_mfma.  A wave reads each X fragment from LDS once
+// per slice and uses it for its WT tiles.
+constexpr int kWWaves = 8;
+
+template <int BM>
+constexpr size_t mfma_w_lds() {
+    return size_t(2) * BM * kXS * sizeof(_Float16) + size_t(16) * BM * sizeof(float);
+}
+
+template <int T, int BM, int WT>
+__global__ __launch_bounds__(512) void k_mfma_w(MfmaArgs a) {
+    using W = MW<T>;
+    constexpr int MT = BM / 16;
+    constexpr int NTH = kWWaves * 64;
+    constexpr int FPT = BM * kStep / NTH;  // X values staged per thread and step
+    constexpr int TPR = NTH / BM;          // threads per X row
+    extern __shared__ __align__(16) unsigned char wlds[];
+    _Float16 *xh = reinterpret_cast<_Float16 *>(wlds);
+    _Float16 *xl = xh + BM * kXS;
+    float *xsum = reinterpret_cast<float *>(xl + BM * kXS);  // [16-slice][m]
+    const int t = threadIdx.x, lane = t & 63, w = t >> 6;
+    const int kq = lane >> 4, ln = lane & 15;
+    const int n0 = blockIdx.x * (kWWaves * 16 * WT) + w * 16 * WT;
+    const int m0 = blockIdx.y * BM;
+    const int nsteps = a.w.K / kStep, ks = gridDim.z;
+    const int kb0 = int(blockIdx.z) * nsteps / ks, kb1 = (int(blockIdx.z) + 1) * nsteps / ks;
+
+    const int xm = t / TPR, xk = (t % TPR) * FPT;
+    const bool xrow_ok = m0 + xm < a.M;
+    const float *xsrc = a.x + size_t(xrow_ok ? m0 + xm : 0) * a.ldx + xk;
+    float4 xr[FPT / 4];
+    auto load_x = [&](int kb) {
+#pragma unroll
+        for (int i = 0; i < FPT / 4; ++i)
+            xr[i] = xrow_ok ? *reinterpret_cast<const float4 *>(xsrc + size_t(kb) * kStep + 4 * i)
+                            : make_float4(0.f, 0.f, 0.f, 0.f);
+    };
+    auto stage_x = [&] {
+#pragma unroll
+        for (int i = 0; i < FPT / 4; ++i) {
+            const float v[4] = {xr[i].x, xr[i].y, xr[i].z, xr[i].w};
+            _Float16 hv[4], lv[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                hv[e] = _Float16(v[e]);
+                lv[e] = _Float16(v[e] - float(hv[e]));
+            }
+            *reinterpret_cast<h4_t *>(xh + xm * kXS + xk + 4 * i) = h4_t{hv[0], hv[1], hv[2], hv[3]};
+            *reinterpret_cast<h4_t *>(xl + xm * kXS + xk + 4 * i) = h4_t{lv[0], lv[1], lv[2], lv[3]};
+        }
+#pragma unroll
+        for (int j = 0; j < FPT / 16; ++j) {
+            float s = 0.f;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) s += (xr[4 * j + i].x + xr[4 * j + i].y) + (xr[4 * j + i].z + xr[4 * j + i].w);
+            xsum[((xk >> 4) + j) * BM + xm] = s;
+        }
+    };
+
+    f4_t acc[WT][MT];
+#pragma unroll
+    for (int j = 0; j < WT; ++j)
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) acc[j][mt] = f4_t{0.f, 0.f, 0.f, 0.f};
+
+    typename W::Regs cur[WT], nxt[WT];
+#pragma unroll
+    for (int j = 0; j < WT; ++j) W::load(a.w, min(n0 + 16 * j + ln, a.w.N - 1), kb0, kq, cur[j]);
+    load_x(kb0);
+    for (int kb = kb0; kb < kb1; ++kb) {
+        if (kb != kb0) lds_barrier();  // the previous step's reads of xh / xl / xsum are done
+        stage_x();
+        lds_barrier();
+        if (kb + 1 < kb1) {
+#pragma unroll
+            for (int j = 0; j < WT; ++j) W::load(a.w, min(n0 + 16 * j + ln, a.w.N - 1), kb + 1, kq, nxt[j]);
+            load_x(kb + 1);
+        }
+#pragma unroll
+        for (int s = 0; s < W::SLICES; ++s) {
+            float sc[WT], mn[WT];
+            decltype(W::b(cur[0], 0)) bop[WT];
+#pragma unroll
+            for (int j = 0; j < WT; ++j) {
+                W::scale(cur[j], s, sc[j], mn[j]);
+                bop[j] = W::b(cur[j], s);
+            }
+#pragma unroll
+            for (int mt = 0; mt < MT; ++mt) {
+                const int xo = (mt * 16 + ln) * kXS + s * W::SK + kq * (W::SK / 4);
+                float4 xsv = make_float4(0.f, 0.f, 0.f, 0.f);
+                if constexpr (W::MIN) {
+                    const float *xsp = xsum + (s * W::SK / 16) * BM + mt * 16 + 4 * kq;
+                    xsv = *reinterpret_cast<const float4 *>(xsp);
+                    if constexpr (W::SK == 32) {
+                        const float4 x2 = *reinterpret_cast<const float4 *>(xsp + BM);
+                        xsv = make_float4(xsv.x + x2.x, xsv.y + x2.y, xsv.z + x2.z, xsv.w + x2.w);
+                    }
+                }
+                // acc += sc tmp (- mn xsum for the formats with mins)
+                auto scale_add = [&](f4_t &a4, const f4_t &tmp, float scj, float mnj) {
+                    if constexpr (W::MIN) {
+                        a4[0] = fmaf(scj, tmp[0], fmaf(-mnj, xsv.x, a4[0]));
+                        a4[1] = fmaf(scj, tmp[1], fmaf(-mnj, xsv.y, a4[1]));
+                        a4[2] = fmaf(scj, tmp[2], fmaf(-mnj, xsv.z, a4[2]));
+                        a4[3] = fmaf(scj, tmp[3], fmaf(-mnj, xsv.w, a4[3]));
+                    } else {
+#pragma unroll
+                        for (int r = 0; r < 4; ++r) a4[r] = fmaf(scj, tmp[r], a4[r]);
+                    }
+                };
+                if constexpr (W::SK == 32) {
+                    const h8_t ah = *reinterpret_cast<const h8_t *>(xh + xo), al = *reinterpret_cast<const h8_t *>(xl + xo);
+#pragma unroll
+                    for (int j = 0; j < WT; ++j) {
+                        f4_t tmp = f4_t{0.f, 0.f, 0.f, 0.f};
+                        tmp = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bop[j], tmp, 0, 0, 0);
+                        tmp = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, bop[j], tmp, 0, 0, 0);
+                        scale_add(acc[j][mt], tmp, sc[j], mn[j]);
+                    }
+                } else {
+                    const h4_t ah = *reinterpret_cast<const h4_t *>(xh + xo), al = *reinterpret_cast<const h4_t *>(xl + xo);
+#pragma unroll
+                    for (int j = 0; j < WT; ++j) {
+                        f4_t tmp = f4_t{0.f, 0.f, 0.f, 0.f};
+                        tmp = __builtin_amdgcn_mfma_f32_16x16x16f16(ah, bop[j], tmp, 0, 0, 0);
+                        tmp = __builtin_amdgcn_mfma_f32_16x16x16f16(al, bop[j], tmp, 0, 0, 0);
+                        scale_add(acc[j][mt], tmp, sc[j], mn[j]);
+                    }
+                }
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < WT; ++j) cur[j] = nxt[j];
+    }
+#pragma unroll
+    for (int j = 0; j < WT; ++j) {
+        const int n = n0 + 16 * j + ln;
+        if (n >= a.w.N) continue;
+        if (a.part) {
+            float *pp = a.part + size_t(blockIdx.z) * a.M * a.w.N;
+#pragma unroll
+            for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const int m = m0 + mt * 16 + 4 * kq + r;
+                    if (m < a.M) pp[size_t(m) * a.w.N + n] = acc[j][mt][r];
+                }
+            continue;
+        }
+        const float bv = a.bias ? a.bias[n] : 0.f;
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int m = m0 + mt * 16 + 4 * kq + r;
+                if (m >= a.M) continue;
+                float v = acc[j][mt][r] + bv;
+                if (a.R) v += a.R[size_t(m) * a.ldr + n];
+                if (a.relu) v = fmaxf(v, 0.f);
+                a.y[size_t(m) * a.ldy + n] = v;
+            }
+    }
+}
+
+// W tiles per wave of the wide kernel for (N, M), 0: use k_mfma.  Wide tiles pay
+// off once X (M > 32 rows) is re-staged by many tiles and enough workgroups remain.
+int wide_wt(int N, int M) {
+    if (M <= 32) return 0;
+    const int gy = (M + 63) / 64;
+    // WT = 4 (512 rows) would need more than the 256 registers a wave of a
+    // 512-thread workgroup can hold (spills), so 2 (256 rows)
+    return size_t((N + 255) / 256) * gy >= 192 ? 2 : 0;
+}
+
+template <int T, int BM, int WT>
+hipError_t launch_w_t(const MfmaArgs &a, int M, int ks, hipStream_t st) {
+    static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void *>(&k_mfma_w<T, BM, WT>),
+                                                       hipFuncAttributeMaxDynamicSharedMemorySize,
+                                                       int(mfma_w_lds<BM>()));
+    if (attr != hipSuccess) return attr;
+    const int gx = (a.w.N + 128 * WT - 1) / (128 * WT);
+    hipLaunchKernelGGL((k_mfma_w<T, BM, WT>), dim3(gx, (M + BM - 1) / BM, ks), dim3(kWWaves * 64), mfma_w_lds<BM>(),
+                       st, a);
+    return hipGetLastError();
+}
+
 template <int T>
 hipError_t launch(const MfmaArgs &a, int M, int ks, hipStream_t st) {
+    if (wide_wt(a.w.N, M) == 2) return launch_w_t<T, 64, 2>(a, M, ks, st);
     const int gx = (a.w.N + kTileN - 1) / kTileN;
     if (M <= 16) {
         hipLaunchKernelGGL((k_mfma<T, 16>), dim3(gx, (M + 15) / 16, ks), dim3(256), 0, st, a);
@@ -437,7 +640,9 @@ __global__ __launch_bounds__(256) void k_splitk_qkv(const float *part, int ks, i
 
 // K splits that bring the grid to about one workgroup per CU, within the workspace
 int split_k(const DevMatrix &w, int M, size_t ws_bytes) {
-    const int gx = (w.N + kTileN - 1) / kTileN, bm = M <= 16 ? 16 : M <= 32 ? 32 : 64;
+    const int wt = wide_wt(w.N, M);
+    const int gx = wt ? (w.N + 128 * wt - 1) / (128 * wt) : (w.N + kTileN - 1) / kTileN;
+    const int bm = M <= 16 ? 16 : M <= 32 ? 32 : 64;
     const int base = gx * ((M + bm - 1) / bm), nsteps = w.K / kStep;
     int ks = base >= 256 ? 1 : std::min(nsteps, (256 + base - 1) / base);
     while (ks > 1 && size_t(ks) * M * w.N * sizeof(float) > ws_bytes) --ks;
@@ -584,10 +789,13 @@ __global__ __launch_bounds__(kRxWaves * 64) void k_mfma_rx(RxArgs a) {
             for (int mt = 0; mt < MT; ++mt) {
                 const int xo = (mt * 16 + ln) * XS + kx + kq * (W::SK / 4);
                 const float *xsp = xsum + (kx >> 4) * BM + mt * 16 + 4 * kq;
-                float4 xsv = *reinterpret_cast<const float4 *>(xsp);
-                if constexpr (W::SK == 32) {
-                    const float4 x2 = *reinterpret_cast<const float4 *>(xsp + BM);
-                    xsv = make_float4(xsv.x + x2.x, xsv.y + x2.y, xsv.z + x2.z, xsv.w + x2.w);
+                float4 xsv = make_float4(0.f, 0.f, 0.f, 0.f);
+                if constexpr (W::MIN) {
+                    xsv = *reinterpret_cast<const float4 *>(xsp);
+                    if constexpr (W::SK == 32) {
+                        const float4 x2 = *reinterpret_cast<const float4 *>(xsp + BM);
+                        xsv = make_float4(xsv.x + x2.x, xsv.y + x2.y, xsv.z + x2.z, xsv.w + x2.w);
+                    }
                 }
                 if constexpr (W::SK == 32) {
                     const h8_t ah = *reinterpret_cast<const h8_t *>(xh + xo), al = *reinterpret_cast<const h8_t *>(xl + xo);
@@ -598,7 +806,8 @@ __global__ __launch_bounds__(kRxWaves * 64) void k_mfma_rx(RxArgs a) {
                         tmp = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, bop[nt], tmp, 0, 0, 0);
 #pragma unroll
                         for (int r = 0; r < 4; ++r)
-                            acc[mt][nt][r] = fmaf(sc[nt], tmp[r], fmaf(-mn[nt], (&xsv.x)[r], acc[mt][nt][r]));
+                            acc[mt][nt][r] = W::MIN ? fmaf(sc[nt], tmp[r], fmaf(-mn[nt], (&xsv.x)[r], acc[mt][nt][r]))
+                                                    : fmaf(sc[nt], tmp[r], acc[mt][nt][r]);
                     }
                 } else {
                     const h4_t ah = *reinterpret_cast<const h4_t *>(xh + xo), al = *reinterpret_cast<const h4_t *>(xl + xo);
@@ -609,7 +818,8 @@ __global__ __launch_bounds__(kRxWaves * 64) void k_mfma_rx(RxArgs a) {
                         tmp = __builtin_amdgcn_mfma_f32_16x16x16f16(al, bop[nt], tmp, 0, 0, 0);
 #pragma unroll
                         for (int r = 0; r < 4; ++r)
-                            acc[mt][nt][r] = fmaf(sc[nt], tmp[r], fmaf(-mn[nt], (&xsv.x)[r], acc[mt][nt][r]));
+                            acc[mt][nt][r] = W::MIN ? fmaf(sc[nt], tmp[r], fmaf(-mn[nt], (&xsv.x)[r], acc[mt][nt][r]))
+                                                    : fmaf(sc[nt], tmp[r], acc[mt][nt][r]);
                     }
                 }
             }

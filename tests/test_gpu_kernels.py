@@ -118,6 +118,33 @@ def test_gemm_mfma_tiles_bias_relu_residual(ctx, t, N, K):
         ctx.lib.mlg_matrix_free(w)
 
 
+@pytest.mark.parametrize("t,N,K", [(Q4_K, 12300, 512), (Q5_K, 12300, 256), (Q6_K, 6150, 512), (Q8_0, 6144, 256),
+                                   (F16, 12290, 256)])
+def test_gemm_wide_tiles(ctx, t, N, K):
+    """M > 32 with many W rows runs the wide-tile kernel (8 waves x 32 rows of W per
+    workgroup) once ceil(N / 256) * ceil(M / 64) >= 192: partial tiles in M and N,
+    bias, ReLU, residual; q4_K at M = 200 also splits K (gemm + reduction)."""
+    rng = np.random.default_rng(43 + t)
+    wf = rng.normal(0, 0.02, (N, K)).astype(np.float32)
+    blocks = M.quantize(t, wf)
+    w = upload(ctx, t, blocks, N, K)
+    try:
+        wd = O.dequant(t, blocks, N * K).reshape(N, K)
+        bias = rng.normal(0, 0.1, N).astype(np.float32)
+        bd = dev(bias)
+        for M_ in (200, 2100 if N < 8000 else 1100):
+            x = (rng.normal(0, 1, (M_, K)) * rng.uniform(0.01, 30, (M_, 1))).astype(np.float32)
+            r0 = rng.normal(0, 1, (M_, N)).astype(np.float32)
+            xd, yd = dev(x), dev(r0)
+            _lib.check(ctx.lib.mlg_gemm_resid(w, ptr(xd), M_, ptr(yd), ptr(bd), 1, ptr(yd), None))
+            torch.cuda.synchronize()
+            ref = np.maximum(O.gemv(t, blocks, N, K, x) + bias + r0, 0)
+            tol = 2e-6 * (bound(x, wd) + np.abs(bias) + np.abs(r0)) + 1e-6
+            assert (np.abs(yd.cpu().numpy() - ref) <= tol).all(), M_
+    finally:
+        ctx.lib.mlg_matrix_free(w)
+
+
 @pytest.mark.parametrize("t,K", [(Q6_K, 1024), (Q4_K, 1024), (Q8_0, 512), (Q5_K, 2048)])
 def test_gemm_argmax_batched_lm_head(ctx, t, K):
     """Batched LM head (5..32 rows): per-wave argmax partials merged on the host equal
