@@ -101,6 +101,37 @@ def bench_config5():
                 weights_mb=round(model_path_3b("q4_k_m").stat().st_size / 1e6))
 
 
+def bench_mfma_profile():
+    """Short runs of the MFMA GEMM paths for counter collection (rocprofv3 --pmc):
+    config-4 encoder prefill (bs 32) x3 and 16 greedy steps at bs 32 (600M), then
+    6 greedy steps of config 5 (3.3B, bs 64)."""
+    import torch
+    import malaga_amd as M
+
+    res = {}
+    T = M.Translator.load(model_path("q4_k_m"))
+    lens = lognormal_lengths(32, 28, 4, 128, seed=0)
+    rng = np.random.default_rng(77)
+    src = [rng.integers(4, 256206, n).tolist() for n in lens]
+    a = time.perf_counter()
+    for _ in range(3):
+        T.encode_cross(src)
+    T.generate(src, TGT_LANG, M.GenOptions(eos_mask=True, max_batch=32, max_new_tokens=16))
+    torch.cuda.synchronize()
+    res["config4_s"] = time.perf_counter() - a
+    T.close()
+    T = M.Translator.load(model_path_3b("q4_k_m"))
+    lens = lognormal_lengths(64, 28, 4, 256, seed=5)
+    rng = np.random.default_rng(55)
+    src = [rng.integers(4, 256206, n).tolist() for n in lens]
+    a = time.perf_counter()
+    T.generate(src, TGT_LANG, M.GenOptions(eos_mask=True, max_batch=64, max_new_tokens=6))
+    torch.cuda.synchronize()
+    res["config5_s"] = time.perf_counter() - a
+    T.close()
+    return res
+
+
 def sources(n: int, length: int, seed: int) -> list[list[int]]:
     """Seeded random source ids U[4, 256206) (raw ids, no language/eos framing)."""
     return [np.random.default_rng(seed + i).integers(4, 256206, length).tolist() for i in range(n)]
@@ -325,7 +356,8 @@ def main():
     ap.add_argument("--skip-cpu", action="store_true")
     ap.add_argument("--legs", default="bs1,batched,kernels,cpu",
                     help="comma-separated subset of bs1,batched,kernels,cpu (profiling runs); "
-                         "'config5' alone runs only the 3.3B batch-64 leg")
+                         "'config5' alone runs only the 3.3B batch-64 leg, 'mfma' alone the short "
+                         "MFMA-GEMM runs used for counter collection")
     ap.add_argument("--roofline-only", action="store_true", help="only the LM-head roofline leg (for rocprof)")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -357,6 +389,9 @@ def main():
         return
 
     legs = set(args.legs.split(","))
+    if legs == {"mfma"}:
+        print(json.dumps({"mfma_profile": bench_mfma_profile()}))
+        return
     if legs == {"config5"}:
         r = bench_config5()
         log(f"config5: {r['sentences_per_s']:.1f} sentences/s ({r['ms_per_batch']:.1f} ms/batch, encoder "
