@@ -633,18 +633,25 @@ __device__ __forceinline__ void gemv_rows(const WPtr &w, const GemvGeom &g, XR (
     __builtin_amdgcn_sched_barrier(0);
     prologue();
     if (!any) return;
+    // The last step is peeled off, so that every compute in the main loop follows
+    // an issued prefetch: a conditional prefetch would merge two load states and
+    // the compiler would wait for all loads (the prefetch included) before computing.
     for (;;) {
         const int rb = rg + stride;
-        const bool more_b = rb * rpw < w.N;
-        if (more_b) load_step(rb, Bf, bb);
+        if (rb * rpw >= w.N) {  // wave-uniform
+            compute_step(rg, A, ba);
+            break;
+        }
+        load_step(rb, Bf, bb);
         compute_step(rg, A, ba);
-        if (!more_b) break;
         rg = rb;
         const int ra = rg + stride;
-        const bool more_a = ra * rpw < w.N;
-        if (more_a) load_step(ra, A, ba);
+        if (ra * rpw >= w.N) {
+            compute_step(rg, Bf, bb);
+            break;
+        }
+        load_step(ra, A, ba);
         compute_step(rg, Bf, bb);
-        if (!more_a) break;
         rg = ra;
     }
 }

@@ -662,9 +662,11 @@ int split_k(const DevMatrix &w, int M, size_t ws_bytes) {
 constexpr int kRxWaves = 8;
 constexpr int kRxDepth = 2;  // (group, K-step) jobs of W in flight per wave
 // 16-row tiles of W per job (reuse of each X fragment), sized to the registers a
-// type's raw K step needs
+// type's raw K step needs; q6_K issues 14 loads per tile and K step, and a wave
+// tracks at most 63 outstanding loads (kRxDepth x tiles x loads must stay below,
+// or every job waits for all loads in flight)
 template <int T>
-constexpr int rx_nt() { return T == GGML_F16 ? 1 : T == GGML_Q8_0 ? 2 : 4; }
+constexpr int rx_nt() { return T == GGML_F16 ? 1 : (T == GGML_Q8_0 || T == GGML_Q6_K) ? 2 : 4; }
 constexpr size_t kRxMaxLds = 150 * 1024;
 
 struct RxArgs {
@@ -829,7 +831,10 @@ __global__ __launch_bounds__(kRxWaves * 64) void k_mfma_rx(RxArgs a) {
             for (int nt = 0; nt < kRxNT; ++nt) {
                 const int n = job_base(j) + nt * 16 + ln;
                 if (n < a.w.N) {
-                    const float bv = a.bias ? a.bias[n] : 0.f;
+                    // MODE 1 (the tied LM head) has no bias: no global load in this
+                    // epilogue, which would make every later job wait for all loads
+                    float bv = 0.f;
+                    if constexpr (MODE == 0) bv = a.bias ? a.bias[n] : 0.f;
 #pragma unroll
                     for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
@@ -852,7 +857,19 @@ __global__ __launch_bounds__(kRxWaves * 64) void k_mfma_rx(RxArgs a) {
             }
         }
     };
-    for (int j0 = 0; j0 < njobs; j0 += kRxDepth) {
+    // Main loop: every job is followed by its slot's refill.  The last jobs run in a
+    // separate tail, so that no job in the main loop follows a skipped refill: the
+    // compiler would then merge the two load states and wait for every load in
+    // flight (the refills included) at the top of each job.
+    int j0 = 0;
+    for (; j0 + 2 * kRxDepth <= njobs; j0 += kRxDepth) {
+#pragma unroll
+        for (int u = 0; u < kRxDepth; ++u) {
+            job(j0 + u, ring[u]);
+            load_job(j0 + u + kRxDepth, ring[u]);
+        }
+    }
+    for (; j0 < njobs; j0 += kRxDepth) {
 #pragma unroll
         for (int u = 0; u < kRxDepth; ++u) {
             const int j = j0 + u;
@@ -898,7 +915,13 @@ hipError_t launch_rx(const RxArgs &a, int M, int grid, hipStream_t st) {
 }
 
 int rx_nt_of(uint32_t t) {
-    return t == GGML_F16 ? rx_nt<GGML_F16>() : t == GGML_Q8_0 ? rx_nt<GGML_Q8_0>() : rx_nt<GGML_Q4_K>();
+    switch (t) {
+    case GGML_F16: return rx_nt<GGML_F16>();
+    case GGML_Q8_0: return rx_nt<GGML_Q8_0>();
+    case GGML_Q6_K: return rx_nt<GGML_Q6_K>();
+    case GGML_Q5_K: return rx_nt<GGML_Q5_K>();
+    default: return rx_nt<GGML_Q4_K>();
+    }
 }
 
 int rx_grid(const DevMatrix &w, int M) {
