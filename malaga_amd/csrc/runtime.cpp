@@ -567,7 +567,11 @@ GraphCache::GraphCache(Model *m) : model_(m) {
     capture_ = !no || !*no || std::string(no) == "0";
 }
 
-GraphCache::~GraphCache() { clear(); }
+GraphCache::~GraphCache() {
+    clear();
+    if (fin_host_) (void)hipHostFree(fin_host_);
+    if (fin_ev_) (void)hipEventDestroy(fin_ev_);
+}
 
 size_t GraphCache::Entry::bytes() const { return st->bytes + (exec ? kGraphBytes : 0); }
 
@@ -668,12 +672,31 @@ std::vector<std::vector<uint32_t>> GraphCache::run(const Batch &src, uint32_t tg
         e->exec = exec;
         evict(e);
     }
-    std::vector<uint8_t> done(static_cast<size_t>(st.b));
+    if (fin_cap_ < size_t(st.b)) {
+        if (fin_host_) (void)hipHostFree(fin_host_);
+        fin_host_ = nullptr;
+        fin_cap_ = 0;
+        void *p = nullptr;
+        check_hip(hipHostMalloc(&p, size_t(st.b), hipHostMallocDefault), "pinned finished flags");
+        fin_host_ = static_cast<uint8_t *>(p);
+        fin_cap_ = size_t(st.b);
+    }
+    if (!fin_ev_) check_hip(hipEventCreateWithFlags(&fin_ev_, hipEventDisableTiming), "event");
+    // src/graph.rs:279-288 checks the finished flags every sync_every steps.  Here the
+    // flags copied at one check point are read at the next, so the stream keeps
+    // sync_every steps queued while the host waits instead of draining.  Steps run
+    // after every row has finished only append pad tokens, which the EOS cut below
+    // removes, so the output is the same.
+    bool pending = false;
     while (steps < max_steps) {
         if (steps % sync_every == 0) {
-            check_hip(hipMemcpyAsync(done.data(), st.finished, done.size(), hipMemcpyDeviceToHost, s), "D2H");
-            check_hip(hipStreamSynchronize(s), "sync");
-            if (std::all_of(done.begin(), done.end(), [](uint8_t v) { return v != 0; })) break;
+            if (pending) {
+                check_hip(hipEventSynchronize(fin_ev_), "sync");
+                if (std::all_of(fin_host_, fin_host_ + st.b, [](uint8_t v) { return v != 0; })) break;
+            }
+            check_hip(hipMemcpyAsync(fin_host_, st.finished, size_t(st.b), hipMemcpyDeviceToHost, s), "D2H");
+            check_hip(hipEventRecord(fin_ev_, s), "event");
+            pending = true;
         }
         if (capture && e->exec) check_hip(hipGraphLaunch(e->exec, s), "graph launch");
         else m.step(st, true, mask_id);

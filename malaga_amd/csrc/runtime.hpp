@@ -119,6 +119,9 @@ class GraphCache {
     uint64_t clock_ = 0;
     size_t max_bytes_;
     bool capture_;
+    uint8_t *fin_host_ = nullptr;  // pinned copy of the finished flags
+    size_t fin_cap_ = 0;
+    hipEvent_t fin_ev_ = nullptr;
 };
 
 class Model {
