@@ -122,7 +122,8 @@ void mlg_batch_free(mlg_batch *b);
 /* GraphCache::greedy (src/graph.rs:204-223); rows stripped at EOS. */
 int mlg_greedy(mlg_model *m, const mlg_batch *b, uint32_t tgt_lang, int max_new, int sync_every, uint32_t flags,
                uint32_t *out, int out_cap, int *out_len);
-/* Translator::beam_search (src/translator.rs:250-335). */
+/* Translator::beam_search (src/translator.rs:250-335).  One decoder step + top-k is captured
+   once and replayed per step (MLG_FLAG_NO_GRAPH: eager); MLG_FLAG_EOS_MASK as for mlg_greedy. */
 int mlg_beam(mlg_model *m, const mlg_batch *b, uint32_t tgt_lang, int max_new, int beam_size, float length_penalty,
              uint32_t flags, uint32_t *out, int out_cap, int *out_len);
 /* GraphCache::clear (src/graph.rs:192-200). */

@@ -1,7 +1,7 @@
 // Row-wise and attention kernels of the decoder step and the encoder:
 // LayerNorm (+ residual, + embedding/positions), q/k/v split into the f16 KV
 // cache, single-query and prefill attention, argmax + greedy bookkeeping,
-// log-softmax top-k for beam search, and small copy/gather helpers.
+// log-softmax top-k for beam search, and small copy helpers.
 #include "dequant.hpp"
 #include "kernels.hpp"
 
@@ -575,21 +575,6 @@ __global__ __launch_bounds__(64) void k_lsm_topk_final(const float *scratch, int
     }
 }
 
-__global__ void k_gather_rows_u32(const uint32_t *src, uint32_t *dst, const uint32_t *idx, int n, size_t row_words) {
-    const size_t total = size_t(n) * row_words;
-    for (size_t t = blockIdx.x * size_t(blockDim.x) + threadIdx.x; t < total; t += size_t(gridDim.x) * blockDim.x) {
-        const size_t r = t / row_words, c = t % row_words;
-        dst[t] = src[size_t(idx[r]) * row_words + c];
-    }
-}
-
-__global__ void k_gather_rows_u8(const uint8_t *src, uint8_t *dst, const uint32_t *idx, int n, size_t row_bytes) {
-    const size_t total = size_t(n) * row_bytes;
-    for (size_t t = blockIdx.x * size_t(blockDim.x) + threadIdx.x; t < total; t += size_t(gridDim.x) * blockDim.x) {
-        const size_t r = t / row_bytes, c = t % row_bytes;
-        dst[t] = src[size_t(idx[r]) * row_bytes + c];
-    }
-}
 
 __global__ void k_inc_u32(uint32_t *p) {
     if (threadIdx.x == 0) *p += 1;
@@ -732,18 +717,6 @@ hipError_t logsoftmax_topk(const float *logits, int rows, int V, int k, int mask
     return hipGetLastError();
 }
 
-hipError_t gather_rows(const void *src, void *dst, const uint32_t *idx, int n, size_t row_bytes, hipStream_t st) {
-    if (!n || !row_bytes) return hipSuccess;
-    if (row_bytes % 4 == 0) {
-        const size_t words = row_bytes / 4;
-        hipLaunchKernelGGL(k_gather_rows_u32, dim3(grid_1d(n * words, 256)), dim3(256), 0, st,
-                           static_cast<const uint32_t *>(src), static_cast<uint32_t *>(dst), idx, n, words);
-    } else {
-        hipLaunchKernelGGL(k_gather_rows_u8, dim3(grid_1d(n * row_bytes, 256)), dim3(256), 0, st,
-                           static_cast<const uint8_t *>(src), static_cast<uint8_t *>(dst), idx, n, row_bytes);
-    }
-    return hipGetLastError();
-}
 
 hipError_t inc_u32(uint32_t *p, hipStream_t st) {
     hipLaunchKernelGGL(k_inc_u32, dim3(1), dim3(64), 0, st, p);

@@ -118,7 +118,6 @@ hipError_t logsoftmax_topk(const float *logits, int rows, int V, int k, int mask
                            uint32_t *idx, hipStream_t st);
 size_t logsoftmax_topk_scratch(int rows, int k);
 // dst[i] = src[idx[i]] for rows of `row_bytes` bytes (i < n).
-hipError_t gather_rows(const void *src, void *dst, const uint32_t *idx, int n, size_t row_bytes, hipStream_t st);
 // ---- fused decoder-step kernels (batch <= 4), k_step.hip ----
 // True when the fused GEMV kernels (residual + LayerNorm prologue over d-wide rows)
 // handle matrix w at batch nb.

@@ -839,9 +839,10 @@ std::vector<std::vector<uint32_t>> Model::beam(const Batch &src, uint32_t tgt_la
             alive[sn] = std::move(new_alive);
         }
         if (stp == max_new || std::all_of(is_done.begin(), is_done.end(), [](uint8_t v) { return v != 0; })) break;
-        // src/model.rs:209-226: gather the self-attention caches by beam.  Cross K/V and
-        // lens are identical within a sentence's beams, and reorder never leaves a sentence.
-        // slots 0 .. stp are written; the next step writes slot stp + 1 into row r itself
+        // src/model.rs:209-226 gathers the self-attention caches by beam; here only the
+        // row map changes (cross K/V and lens are identical within a sentence's beams, and
+        // a reorder never leaves a sentence).  Slots 0 .. stp are written; the next step
+        // writes slot stp + 1 into row r itself.
         const int m = st->m;
         for (int r = 0; r < bk; ++r) {
             const uint32_t *par = rows_map.data() + size_t(reorder[r]) * m;
