@@ -130,10 +130,7 @@ Context::~Context() { dev_free(gemm_ws); }
 
 // ------------------------------------------------------------------- model
 
-Batch::~Batch() {
-    for (auto p : ck) dev_free(p);
-    for (auto p : cv) dev_free(p);
-}
+Batch::~Batch() { dev_free(block); }
 
 StaticState::~StaticState() {
     for (auto p : owned) dev_free(p);
@@ -142,6 +139,7 @@ StaticState::~StaticState() {
 Model::~Model() {
     graphs.clear();
     for (auto p : owned_) dev_free(p);
+    dev_free(enc_ws_);
 }
 
 float *Model::upload_f32(GgufFile &g, const std::string &name, int64_t n) {
@@ -319,12 +317,32 @@ std::unique_ptr<Batch> Model::encode(const std::vector<std::vector<uint32_t>> &s
             pidx[size_t(i) * s + j] = uint32_t(j) + pad + 1;
         }
     }
-    DevTemp tmp;
-    uint32_t *d_ids = tmp.get<uint32_t>(M, "encoder ids"), *d_pidx = tmp.get<uint32_t>(M, "encoder positions");
-    uint32_t *d_lens = tmp.get<uint32_t>(b, "encoder lens");
-    float *x = tmp.get<float>(size_t(M) * d, "encoder x"), *h = tmp.get<float>(size_t(M) * d, "encoder h");
-    float *qkv = tmp.get<float>(size_t(M) * std::max(3 * d, f), "encoder qkv");
-    float *att = tmp.get<float>(size_t(M) * d, "encoder att");
+    // scratch: carved from the model's grow-only encoder workspace (256-byte aligned)
+    const size_t n_ids = (size_t(M) * 4 + 255) & ~size_t(255), n_lens = (size_t(b) * 4 + 255) & ~size_t(255);
+    const size_t n_act = (size_t(M) * d * 4 + 255) & ~size_t(255);
+    const size_t n_qkv = (size_t(M) * std::max(3 * d, f) * 4 + 255) & ~size_t(255);
+    const size_t n_kv = (size_t(M) * 2 * d * 4 + 255) & ~size_t(255);
+    const size_t need = 2 * n_ids + n_lens + 3 * n_act + n_qkv + n_kv;
+    if (enc_ws_bytes_ < need) {
+        check_hip(hipStreamSynchronize(st), "encode");  // a previous call may still use it
+        dev_free(enc_ws_);
+        enc_ws_ = nullptr;
+        enc_ws_bytes_ = 0;
+        enc_ws_ = dev_alloc(need, "encoder workspace");
+        enc_ws_bytes_ = need;
+    }
+    uint8_t *wp = static_cast<uint8_t *>(enc_ws_);
+    auto carve = [&](size_t bytes) {
+        void *p = wp;
+        wp += bytes;
+        return p;
+    };
+    uint32_t *d_ids = static_cast<uint32_t *>(carve(n_ids)), *d_pidx = static_cast<uint32_t *>(carve(n_ids));
+    uint32_t *d_lens = static_cast<uint32_t *>(carve(n_lens));
+    float *x = static_cast<float *>(carve(n_act)), *h = static_cast<float *>(carve(n_act));
+    float *att = static_cast<float *>(carve(n_act));
+    float *qkv = static_cast<float *>(carve(n_qkv));
+    float *kv = static_cast<float *>(carve(n_kv));
     h2d(d_ids, ids, st);
     h2d(d_pidx, pidx, st);
     h2d(d_lens, out->lens, st);
@@ -340,11 +358,12 @@ std::unique_ptr<Batch> Model::encode(const std::vector<std::vector<uint32_t>> &s
     }
     check_hip(layernorm(x, M, d, enc_norm.g, enc_norm.b, kLnEps, h, st), "layernorm");
     const int Hd = cfg.decoder_heads, hdd = d / Hd;
-    float *kv = tmp.get<float>(size_t(M) * 2 * d, "cross kv");
-    for (auto &l : dec) {
-        __half *K = static_cast<__half *>(dev_alloc(size_t(M) * d * 2, "cross K"));
+    const size_t kv_elems = size_t(M) * d;
+    out->block = dev_alloc(std::max<size_t>(dec.size(), 1) * 2 * kv_elems * 2, "cross K/V");
+    for (size_t i = 0; i < dec.size(); ++i) {
+        const DecLayer &l = dec[i];
+        __half *K = static_cast<__half *>(out->block) + 2 * i * kv_elems, *V = K + kv_elems;
         out->ck.push_back(K);
-        __half *V = static_cast<__half *>(dev_alloc(size_t(M) * d * 2, "cross V"));
         out->cv.push_back(V);
         matmul(l.cross_kv, h, M, kv, false, nullptr);
         check_hip(split_cross_kv(kv, b, s, Hd, hdd, K, V, st), "split_cross_kv");
@@ -370,6 +389,7 @@ std::unique_ptr<StaticState> Model::new_state(int b, int s, int m, bool logits, 
     st->lens = static_cast<uint32_t *>(get(size_t(b) * 4, "lens"));
     st->out = static_cast<uint32_t *>(get(size_t(b) * m * 4, "out"));
     st->finished = static_cast<uint8_t *>(get(size_t(b), "finished"));
+    st->row_src = static_cast<uint32_t *>(get(size_t(b) * 4, "source rows"));
     for (int i = 0; i < L; ++i) {
         st->kc.push_back(static_cast<__half *>(get(size_t(b) * H * m * hd * 2, "self K")));
         st->vc.push_back(static_cast<__half *>(get(size_t(b) * H * m * hd * 2, "self V")));
@@ -413,8 +433,8 @@ std::unique_ptr<StaticState> Model::new_state(int b, int s, int m, bool logits, 
 void Model::reset_state(StaticState &st, const Batch &src, const std::vector<uint32_t> &row_of, uint32_t start) {
     hipStream_t s = ctx->stream;
     const int H = cfg.decoder_heads, hd = cfg.d_model / H, n = int(row_of.size());
-    uint32_t *d_map = static_cast<uint32_t *>(dev_alloc(size_t(std::max(n, 1)) * 4, "row map"));
-    struct Guard { void *p; ~Guard() { dev_free(p); } } guard{d_map};
+    if (n > st.b) fail(ERR_INVALID, "reset_state: more source rows than state rows");
+    uint32_t *d_map = st.row_src;
     h2d(d_map, row_of, s);
     for (size_t l = 0; l < st.ck.size(); ++l) {
         check_hip(copy_cross(src.ck[l], d_map, n, H, src.s, hd, st.ck[l], st.s, s), "copy_cross");

@@ -64,7 +64,8 @@ struct DecLayer {
 struct Batch {
     int b = 0, s = 0;
     std::vector<uint32_t> lens;
-    std::vector<__half *> ck, cv;
+    std::vector<__half *> ck, cv;  // per decoder layer, inside `block`
+    void *block = nullptr;         // one allocation for every layer's cross K/V
     ~Batch();
 };
 
@@ -79,6 +80,7 @@ struct StaticState {
     float *xb = nullptr, *qc = nullptr;  // second residual buffer and cross queries (fused step)
     float *part = nullptr;                // attention partial sums [parts][b][d] (fused step)
     uint32_t *rows = nullptr;             // beam: [b][m] cache row holding slot j of row r (null: r)
+    uint32_t *row_src = nullptr;          // [b] source row of each state row (reset_state)
     bool fused = false;                   // decoder step uses the fused kernels of k_step.hip
     float *logits = nullptr, *pv = nullptr;
     uint32_t *pi = nullptr;
@@ -161,6 +163,10 @@ class Model {
 
   private:
     std::vector<void *> owned_;
+    // Encoder scratch (ids, activations): grow-only, reused by every encode call, so a
+    // call allocates only the cross K/V it returns.
+    void *enc_ws_ = nullptr;
+    size_t enc_ws_bytes_ = 0;
     Linear load_linear(class GgufFile &g, const std::string &name, int n, int k);
     LNorm load_ln(class GgufFile &g, const std::string &name, int d);
     float *upload_f32(class GgufFile &g, const std::string &name, int64_t n);
