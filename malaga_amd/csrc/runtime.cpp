@@ -663,14 +663,21 @@ std::vector<std::vector<uint32_t>> GraphCache::run(const Batch &src, uint32_t tg
 
     std::vector<uint32_t> rows(static_cast<size_t>(n));
     std::iota(rows.begin(), rows.end(), 0u);
-    // step 0 consumes decoder_start; its token is replaced by the forced target language
+    // step 0 consumes decoder_start; its token is replaced by the forced target language.
+    // Once the bucket's graph exists these two steps replay it as well (the graph is the
+    // same step; the fill and the flag reset between them are ordinary stream work).
+    const bool replay = capture && e->exec;
+    auto one_step = [&] {
+        if (replay) check_hip(hipGraphLaunch(e->exec, s), "graph launch");
+        else m.step(st, true, mask_id);
+    };
     m.reset_state(st, src, rows, uint32_t(c.decoder_start_token_id));
-    m.step(st, true, mask_id);
+    one_step();
     check_hip(fill_u32(st.ids, tgt_lang, size_t(st.b), s), "fill");
     std::vector<uint8_t> fin(static_cast<size_t>(st.b));
     for (int r = 0; r < st.b; ++r) fin[r] = r >= n;
     h2d(st.finished, fin, s);
-    m.step(st, true, mask_id);
+    one_step();
     int steps = 2;
     const int max_steps = std::min(max_new + 1, st.m);
 
