@@ -95,6 +95,21 @@ int mlg_convert(const char *out_path, const mlg_config *cfg, int preset, const c
 /* Synthetic checkpoint converted like mlg_convert (MLG_INIT_TESTUTIL restates src/testutil.rs:16-101). */
 int mlg_write_synthetic(const char *out_path, const mlg_config *cfg, int preset, int init, uint64_t seed,
                         float std_dev, const char *model_name);
+/* Per-language shortlist (reduced LM head, src/convert.rs:176-233): the writer adds ids 0..3
+   and lang_id, sorts, and stores token_embd's rows for the ids as lm_head.{code}.weight and
+   the ids as nllb.shortlist.{code}.  The reference tokenizes a corpus for `ids`; here the
+   caller supplies them. */
+typedef struct {
+    const char *code;     /* language code, e.g. "fra_Latn" */
+    uint32_t lang_id;     /* the language token (kept: it is fed to the decoder) */
+    const uint32_t *ids;  /* vocabulary ids of the shortlist (any order, duplicates allowed) */
+    int n_ids;
+} mlg_shortlist_spec;
+/* mlg_convert / mlg_write_synthetic plus shortlists (src/convert.rs:218-233, 303). */
+int mlg_convert_sl(const char *out_path, const mlg_config *cfg, int preset, const char *model_name,
+                   const char *tokenizer_json, mlg_tensor_fn fn, void *user, const mlg_shortlist_spec *sl, int n_sl);
+int mlg_write_synthetic_sl(const char *out_path, const mlg_config *cfg, int preset, int init, uint64_t seed,
+                           float std_dev, const char *model_name, const mlg_shortlist_spec *sl, int n_sl);
 /* The tiny test model of src/testutil.rs:18-30. */
 void mlg_tiny_config(mlg_config *out);
 

@@ -219,18 +219,41 @@ def _cfg(d: dict) -> Config:
     return c
 
 
+def _shortlist_specs(shortlists: dict | None):
+    """{code: (lang_id, ids)} -> (ctypes array of ShortlistSpec, keep-alive list)."""
+    from ._lib import ShortlistSpec
+
+    items = list((shortlists or {}).items())
+    arr = (ShortlistSpec * max(1, len(items)))()
+    keep = []
+    for i, (code, (lang_id, ids)) in enumerate(items):
+        a = np.ascontiguousarray(np.asarray(ids, dtype=np.uint32))
+        keep.append(a)
+        arr[i].code = code.encode()
+        arr[i].lang_id = int(lang_id)
+        arr[i].ids = a.ctypes.data_as(C.POINTER(C.c_uint32))
+        arr[i].n_ids = int(a.size)
+    return arr, len(items), keep
+
+
 def write_synthetic(path: str | Path, cfg: dict, preset: str, init: int = INIT_NORMAL, seed: int = 0,
-                    std: float = 0.02, name: str = "synthetic") -> Path:
-    """Random-init checkpoint converted to GGUF with the reference layout."""
+                    std: float = 0.02, name: str = "synthetic", shortlists: dict | None = None) -> Path:
+    """Random-init checkpoint converted to GGUF with the reference layout.  ``shortlists``:
+    {language code: (language token id, vocabulary ids)} per-language reduced LM heads
+    (src/convert.rs:218-233)."""
     lib = load()
     c = _cfg(cfg)
-    check(lib.mlg_write_synthetic(str(path).encode(), C.byref(c), PRESETS[preset], init, seed, std, name.encode()))
+    arr, n, _keep = _shortlist_specs(shortlists)
+    check(lib.mlg_write_synthetic_sl(str(path).encode(), C.byref(c), PRESETS[preset], init, seed, std,
+                                     name.encode(), arr, n))
     return Path(path)
 
 
 def convert(out_path: str | Path, cfg: dict, preset: str, tensors: Callable[[str], np.ndarray] | dict,
-            model_name: str = "facebook/nllb-200-distilled-600M", tokenizer_json: str = "{}") -> Path:
-    """src/convert.rs:317-440 from Hugging Face tensors (a dict or a name -> array function)."""
+            model_name: str = "facebook/nllb-200-distilled-600M", tokenizer_json: str = "{}",
+            shortlists: dict | None = None) -> Path:
+    """src/convert.rs:317-440 from Hugging Face tensors (a dict or a name -> array function);
+    ``shortlists`` as for write_synthetic."""
     lib = load()
     get = tensors.get if isinstance(tensors, dict) else tensors
     err: list[BaseException] = []
@@ -251,8 +274,9 @@ def convert(out_path: str | Path, cfg: dict, preset: str, tensors: Callable[[str
             return 1
 
     c = _cfg(cfg)
-    st = lib.mlg_convert(str(out_path).encode(), C.byref(c), PRESETS[preset], model_name.encode(),
-                         tokenizer_json.encode(), fn, None)
+    arr, n, _keep = _shortlist_specs(shortlists)
+    st = lib.mlg_convert_sl(str(out_path).encode(), C.byref(c), PRESETS[preset], model_name.encode(),
+                            tokenizer_json.encode(), fn, None, arr, n)
     if err:
         raise err[0]
     check(st)

@@ -44,6 +44,10 @@ class CGenOptions(C.Structure):
                 ("sync_every", C.c_int), ("max_batch", C.c_int), ("fused", C.c_int), ("flags", C.c_uint32)]
 
 
+class ShortlistSpec(C.Structure):
+    _fields_ = [("code", C.c_char_p), ("lang_id", C.c_uint32), ("ids", C.POINTER(C.c_uint32)), ("n_ids", C.c_int)]
+
+
 TENSOR_FN = C.CFUNCTYPE(C.c_int, C.c_void_p, C.c_char_p, C.c_int64, C.POINTER(C.c_float))
 
 _P = C.c_void_p
@@ -63,6 +67,10 @@ SIGNATURES = {
     "mlg_convert": (C.c_int, [C.c_char_p, C.POINTER(Config), C.c_int, C.c_char_p, C.c_char_p, TENSOR_FN, _P]),
     "mlg_write_synthetic": (C.c_int, [C.c_char_p, C.POINTER(Config), C.c_int, C.c_int, C.c_uint64, C.c_float,
                                       C.c_char_p]),
+    "mlg_convert_sl": (C.c_int, [C.c_char_p, C.POINTER(Config), C.c_int, C.c_char_p, C.c_char_p, TENSOR_FN, _P,
+                                 C.POINTER(ShortlistSpec), C.c_int]),
+    "mlg_write_synthetic_sl": (C.c_int, [C.c_char_p, C.POINTER(Config), C.c_int, C.c_int, C.c_uint64, C.c_float,
+                                         C.c_char_p, C.POINTER(ShortlistSpec), C.c_int]),
     "mlg_tiny_config": (None, [C.POINTER(Config)]),
     "mlg_device_count": (C.c_int, [_intp]),
     "mlg_ctx_create": (C.c_int, [C.c_int, C.POINTER(_P)]),

@@ -150,30 +150,59 @@ int mlg_preset_from_name(const char *name, int *preset) {
     return MLG_OK;
 }
 
-int mlg_convert(const char *out_path, const mlg_config *cfg, int preset, const char *model_name,
-                const char *tokenizer_json, mlg_tensor_fn fn, void *user) {
+namespace {
+bool to_shortlists(const mlg_shortlist_spec *sl, int n, std::vector<mlg::ShortlistSpec> *out) {
+    if (n < 0 || (n > 0 && !sl)) return false;
+    for (int i = 0; i < n; ++i) {
+        if (!sl[i].code || sl[i].n_ids < 0 || (sl[i].n_ids > 0 && !sl[i].ids)) return false;
+        mlg::ShortlistSpec t;
+        t.code = sl[i].code;
+        t.lang_id = sl[i].lang_id;
+        t.ids.assign(sl[i].ids, sl[i].ids + sl[i].n_ids);
+        out->push_back(std::move(t));
+    }
+    return true;
+}
+}  // namespace
+
+int mlg_convert_sl(const char *out_path, const mlg_config *cfg, int preset, const char *model_name,
+                   const char *tokenizer_json, mlg_tensor_fn fn, void *user, const mlg_shortlist_spec *sl, int n_sl) {
     return guarded([&]() -> int {
         if (preset < 0 || preset > mlg::PRESET_Q4KM) return set_err(MLG_ERR_INVALID, "unknown preset");
+        std::vector<mlg::ShortlistSpec> lists;
+        if (!to_shortlists(sl, n_sl, &lists)) return set_err(MLG_ERR_INVALID, "bad shortlist");
         auto src = [&](const std::string &name, int64_t n, float *out) { return fn(user, name.c_str(), n, out) == 0; };
         const std::string e = mlg::convert_to_gguf(out_path, to_cfg(cfg), mlg::Preset(preset), model_name ? model_name : "",
-                                                   tokenizer_json ? tokenizer_json : "{}", src);
+                                                   tokenizer_json ? tokenizer_json : "{}", src, lists);
+        return e.empty() ? MLG_OK : set_err(MLG_ERR_IO, e);
+    });
+}
+
+int mlg_convert(const char *out_path, const mlg_config *cfg, int preset, const char *model_name,
+                const char *tokenizer_json, mlg_tensor_fn fn, void *user) {
+    return mlg_convert_sl(out_path, cfg, preset, model_name, tokenizer_json, fn, user, nullptr, 0);
+}
+
+int mlg_write_synthetic_sl(const char *out_path, const mlg_config *cfg, int preset, int init, uint64_t seed,
+                           float std_dev, const char *model_name, const mlg_shortlist_spec *sl, int n_sl) {
+    return guarded([&]() -> int {
+        if (preset < 0 || preset > mlg::PRESET_Q4KM) return set_err(MLG_ERR_INVALID, "unknown preset");
+        if (init < 0 || init > 2) return set_err(MLG_ERR_INVALID, "unknown init");
+        std::vector<mlg::ShortlistSpec> lists;
+        if (!to_shortlists(sl, n_sl, &lists)) return set_err(MLG_ERR_INVALID, "bad shortlist");
+        const mlg::ModelConfig c = to_cfg(cfg);
+        auto src = mlg::synthetic_provider(c, mlg::SynthInit(init), seed, std_dev);
+        const std::string tok = init == mlg::SYNTH_TESTUTIL ? mlg::tiny_tokenizer_json(c.vocab_size)
+                                                            : std::string("{\"synthetic\":true}");
+        const std::string e = mlg::convert_to_gguf(out_path, c, mlg::Preset(preset),
+                                                   model_name ? model_name : "synthetic", tok, src, lists);
         return e.empty() ? MLG_OK : set_err(MLG_ERR_IO, e);
     });
 }
 
 int mlg_write_synthetic(const char *out_path, const mlg_config *cfg, int preset, int init, uint64_t seed,
                         float std_dev, const char *model_name) {
-    return guarded([&]() -> int {
-        if (preset < 0 || preset > mlg::PRESET_Q4KM) return set_err(MLG_ERR_INVALID, "unknown preset");
-        if (init < 0 || init > 2) return set_err(MLG_ERR_INVALID, "unknown init");
-        const mlg::ModelConfig c = to_cfg(cfg);
-        auto src = mlg::synthetic_provider(c, mlg::SynthInit(init), seed, std_dev);
-        const std::string tok = init == mlg::SYNTH_TESTUTIL ? mlg::tiny_tokenizer_json(c.vocab_size)
-                                                            : std::string("{\"synthetic\":true}");
-        const std::string e =
-            mlg::convert_to_gguf(out_path, c, mlg::Preset(preset), model_name ? model_name : "synthetic", tok, src);
-        return e.empty() ? MLG_OK : set_err(MLG_ERR_IO, e);
-    });
+    return mlg_write_synthetic_sl(out_path, cfg, preset, init, seed, std_dev, model_name, nullptr, 0);
 }
 
 void mlg_tiny_config(mlg_config *out) {

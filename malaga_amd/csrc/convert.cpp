@@ -1,5 +1,7 @@
 #include "convert.hpp"
 
+#include <algorithm>
+
 #include <cmath>
 #include <cstring>
 #include <map>
@@ -83,7 +85,8 @@ struct Writer {
 }  // namespace
 
 std::string convert_to_gguf(const std::string &out_path, const ModelConfig &c, Preset preset,
-                            const std::string &model_name, const std::string &tokenizer_json, const HfProvider &src) {
+                            const std::string &model_name, const std::string &tokenizer_json, const HfProvider &src,
+                            const std::vector<ShortlistSpec> &shortlists) {
     if (c.d_model <= 0 || c.encoder_heads <= 0 || c.decoder_heads <= 0 || c.d_model % c.encoder_heads ||
         c.d_model % c.decoder_heads || c.vocab_size <= 0)
         return "invalid model config";
@@ -107,6 +110,31 @@ std::string convert_to_gguf(const std::string &out_path, const ModelConfig &c, P
 
     w.add("token_embd.weight", {c.vocab_size, d}, take("model.shared.weight", int64_t(c.vocab_size) * d),
           preset_embedding(preset));
+    // src/convert.rs:218-233: per-language shortlists.  Quantization is row-local, so the
+    // rows of the shared table quantized for lm_head.{code} are token_embd's own rows:
+    // they are copied.
+    std::vector<std::pair<std::string, GgufValue>> sl_meta;
+    for (const ShortlistSpec &sl : shortlists) {
+        if (!w.err.empty() || !missing.empty()) break;
+        if (sl.code.empty()) return "shortlist without a language code";
+        std::vector<uint32_t> ids = {0, 1, 2, 3, sl.lang_id};
+        for (uint32_t id : sl.ids)
+            if (id < uint32_t(c.vocab_size)) ids.push_back(id);
+        std::sort(ids.begin(), ids.end());
+        ids.erase(std::unique(ids.begin(), ids.end()), ids.end());
+        if (ids.back() >= uint32_t(c.vocab_size)) return "shortlist language id out of range";
+        const GgufOutTensor &emb = w.tensors.front();
+        const size_t rb = size_t(type_bytes(emb.type, d));
+        GgufOutTensor t;
+        t.name = "lm_head." + sl.code + ".weight";
+        t.ne = {uint64_t(d), uint64_t(ids.size())};
+        t.type = emb.type;
+        t.bytes.resize(rb * ids.size());
+        for (size_t r = 0; r < ids.size(); ++r)
+            std::memcpy(t.bytes.data() + r * rb, emb.bytes.data() + size_t(ids[r]) * rb, rb);
+        w.tensors.push_back(std::move(t));
+        sl_meta.push_back({"nllb.shortlist." + sl.code, GgufValue::ArrU32(ids)});
+    }
     const uint32_t lin = preset_linear(preset), down = preset_ffn_down(preset);
     for (int side = 0; side < 2; ++side) {
         const bool dec = side == 1;
@@ -179,6 +207,7 @@ std::string convert_to_gguf(const std::string &out_path, const ModelConfig &c, P
         {"tokenizer.ggml.eos_token_id", GgufValue::U32(uint32_t(c.eos_token_id))},
         {"tokenizer.ggml.decoder_start_token_id", GgufValue::U32(uint32_t(c.decoder_start_token_id))},
     };
+    kv.insert(kv.end(), sl_meta.begin(), sl_meta.end());
     return gguf_write(out_path, kv, w.tensors);
 }
 

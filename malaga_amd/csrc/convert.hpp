@@ -31,9 +31,21 @@ uint32_t fallback_dtype(uint32_t dtype, const std::vector<int64_t> &dims);
 // count is passed in; return false if the tensor is missing.
 using HfProvider = std::function<bool(const std::string &name, int64_t numel, float *out)>;
 
+// A reduced LM head for one target language (src/convert.rs:176-233): the vocabulary
+// ids a corpus of that language uses.  The writer adds <s> <pad> </s> <unk> (ids 0..3)
+// and the language token, sorts, and stores the rows of token_embd for those ids as
+// lm_head.{code}.weight plus the id list as nllb.shortlist.{code}.  (The reference
+// derives `ids` by tokenizing a corpus; here the caller passes them.)
+struct ShortlistSpec {
+    std::string code;
+    uint32_t lang_id = 0;
+    std::vector<uint32_t> ids;
+};
+
 // src/convert.rs:317-440.  Returns "" on success.
 std::string convert_to_gguf(const std::string &out_path, const ModelConfig &cfg, Preset preset,
-                            const std::string &model_name, const std::string &tokenizer_json, const HfProvider &src);
+                            const std::string &model_name, const std::string &tokenizer_json, const HfProvider &src,
+                            const std::vector<ShortlistSpec> &shortlists = {});
 
 // Synthetic checkpoints.
 enum SynthInit : int {

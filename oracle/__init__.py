@@ -62,6 +62,9 @@ def lib() -> C.CDLL:
         L.orc_decode.restype, L.orc_decode.argtypes = C.c_int, [P, P, P, C.c_int, P, P]
         L.orc_generate.restype = C.c_int
         L.orc_generate.argtypes = [P, P, P, C.c_int, C.c_uint32, C.POINTER(OrcGenOptions), C.c_int, P, C.c_int, P, P]
+        L.orc_generate_sl.restype = C.c_int
+        L.orc_generate_sl.argtypes = [P, P, P, C.c_int, C.c_uint32, C.POINTER(OrcGenOptions), C.c_int, P, C.c_int,
+                                      P, C.c_int, P, P]
         _lib = L
     return _lib
 
@@ -134,8 +137,11 @@ class Model:
 
     def generate(self, src: Sequence[Sequence[int]], tgt_lang: int, beam_size: int = 1,
                  max_new_tokens: int | None = None, length_penalty: float = 1.0, sync_every: int = 4,
-                 kv_f16: bool = True, eos_mask: bool = False) -> tuple[list[list[int]], float]:
-        """One batch of src/translator.rs:175-207.  Returns (rows, min top-1/top-2 logit gap)."""
+                 kv_f16: bool = True, eos_mask: bool = False,
+                 shortlist: Sequence[int] | None = None) -> tuple[list[list[int]], float]:
+        """One batch of src/translator.rs:175-207.  Returns (rows, min top-1/top-2 logit gap).
+        ``shortlist``: sorted vocabulary ids of the target language's reduced LM head (greedy
+        only); source tokens stay candidates (the fused shortlist step, src/model.rs:594-603)."""
         ids, lens = _flat(src)
         o = OrcGenOptions(beam_size, max_new_tokens or 0, length_penalty, sync_every)
         cap = max(self.budget(len(r), max_new_tokens) for r in src)
@@ -143,8 +149,15 @@ class Model:
         out_len = np.zeros(len(src), dtype=np.int32)
         gap = C.c_float(float("inf"))
         flags = (KV_F16 if kv_f16 else 0) | (EOS_MASK if eos_mask else 0)
-        if self.L.orc_generate(self.h, ids.ctypes.data, lens.ctypes.data, len(src), tgt_lang, C.byref(o), flags,
-                               out.ctypes.data, cap, out_len.ctypes.data, C.byref(gap)):
+        if shortlist is not None:
+            sl = np.ascontiguousarray(np.asarray(shortlist, dtype=np.uint32))
+            rc = self.L.orc_generate_sl(self.h, ids.ctypes.data, lens.ctypes.data, len(src), tgt_lang, C.byref(o),
+                                        flags, sl.ctypes.data, int(sl.size), out.ctypes.data, cap,
+                                        out_len.ctypes.data, C.byref(gap))
+        else:
+            rc = self.L.orc_generate(self.h, ids.ctypes.data, lens.ctypes.data, len(src), tgt_lang, C.byref(o),
+                                     flags, out.ctypes.data, cap, out_len.ctypes.data, C.byref(gap))
+        if rc:
             _err("generate")
         return [out[i, : out_len[i]].tolist() for i in range(len(src))], gap.value
 

@@ -822,9 +822,43 @@ static int budget(const orc_config *c, int len, int max_new_tokens) {
     return v;
 }
 
-/* src/translator.rs:214-241 */
+/* Shortlist decoding (src/model.rs:594-603, kernels/malaga.cu:229-243, 286-326): the
+ * candidates of row r are the shortlist rows, then the row's source tokens, in that
+ * order (argmax ties to the lowest position).  A shortlist row is token_embd's row for
+ * its id and a source candidate is the token's own embedding, so each candidate's
+ * logit is the full-vocabulary logit of its token.  Padding positions of the source
+ * add the pad token, which every shortlist holds (ids 0..3), so they are not listed. */
+typedef struct {
+    const uint32_t *ids;  /* sorted shortlist, n >= 1 */
+    int n;
+    const uint32_t *src;  /* flattened source ids of the batch */
+    const uint32_t *off;  /* [b + 1] row offsets into src */
+} orc_shortlist;
+
+static uint32_t argmax_shortlist(const float *x, const orc_shortlist *sl, int row, int mask_eos, uint32_t eos,
+                                 float *gap) {
+    float best = -INFINITY, second = -INFINITY;
+    uint32_t bt = 0;
+    int have = 0;
+    const int ns = (int)(sl->off[row + 1] - sl->off[row]);
+    for (int i = 0; i < sl->n + ns; ++i) {
+        const uint32_t t = i < sl->n ? sl->ids[i] : sl->src[sl->off[row] + (i - sl->n)];
+        float a = x[t];
+        if (mask_eos && t == eos) a = -INFINITY;
+        if (!have || a > best) {
+            if (have && bt != t) second = best > second ? best : second;
+            best = a; bt = t; have = 1;
+        } else if (t != bt && a > second) {
+            second = a;
+        }
+    }
+    if (gap) *gap = best - second;
+    return bt;
+}
+
+/* src/translator.rs:214-241 (sl: the shortlist path of the fused GraphCache step) */
 static int greedy(const orc_model *m, orc_state *st, int b, uint32_t tgt, int max_new, int sync_every, int flags,
-                  uint32_t *toks /* [b][max_new] */, int *ntok, float *min_gap) {
+                  uint32_t *toks /* [b][max_new] */, int *ntok, float *min_gap, const orc_shortlist *sl) {
     const orc_config *c = &m->cfg;
     const int V = c->vocab_size;
     float *logits = malloc((size_t)b * V * 4);
@@ -839,7 +873,9 @@ static int greedy(const orc_model *m, orc_state *st, int b, uint32_t tgt, int ma
         int all = 1;
         for (int i = 0; i < b; ++i) {
             float gap;
-            const uint32_t a = argmax_row(logits + (size_t)i * V, V, flags & ORC_EOS_MASK, (uint32_t)c->eos_token_id, &gap);
+            const uint32_t a = sl ? argmax_shortlist(logits + (size_t)i * V, sl, i, flags & ORC_EOS_MASK,
+                                                     (uint32_t)c->eos_token_id, &gap)
+                                  : argmax_row(logits + (size_t)i * V, V, flags & ORC_EOS_MASK, (uint32_t)c->eos_token_id, &gap);
             if (!fin[i] && min_gap && gap < *min_gap) *min_gap = gap;
             next[i] = fin[i] ? (uint32_t)c->pad_token_id : a;
             fin[i] |= next[i] == (uint32_t)c->eos_token_id;
@@ -1020,8 +1056,27 @@ static int beam_search(const orc_model *m, orc_state *st, int b, uint32_t tgt, i
 
 /* src/translator.rs:175-207 for one batch: encode, greedy or beam, truncate each
  * row to its own budget.  out is [b][out_cap]; out_len receives the lengths. */
+static int generate_impl(const orc_model *m, const uint32_t *ids, const uint32_t *lens, int b, uint32_t tgt_lang,
+                         const orc_gen_options *o, int flags, uint32_t *out, int out_cap, int *out_len,
+                         float *min_gap, const uint32_t *sl_ids, int n_sl);
+
 int orc_generate(const orc_model *m, const uint32_t *ids, const uint32_t *lens, int b, uint32_t tgt_lang,
                  const orc_gen_options *o, int flags, uint32_t *out, int out_cap, int *out_len, float *min_gap) {
+    return generate_impl(m, ids, lens, b, tgt_lang, o, flags, out, out_cap, out_len, min_gap, NULL, 0);
+}
+
+/* Greedy with a shortlist (sl_ids sorted, n_sl > 0): src/translator.rs:184-194 with
+ * opts.shortlist, GraphCache::greedy's shortlist branch. */
+int orc_generate_sl(const orc_model *m, const uint32_t *ids, const uint32_t *lens, int b, uint32_t tgt_lang,
+                    const orc_gen_options *o, int flags, const uint32_t *sl_ids, int n_sl, uint32_t *out, int out_cap,
+                    int *out_len, float *min_gap) {
+    if (n_sl <= 0 || !sl_ids || o->beam_size > 1) return -1;
+    return generate_impl(m, ids, lens, b, tgt_lang, o, flags, out, out_cap, out_len, min_gap, sl_ids, n_sl);
+}
+
+static int generate_impl(const orc_model *m, const uint32_t *ids, const uint32_t *lens, int b, uint32_t tgt_lang,
+                         const orc_gen_options *o, int flags, uint32_t *out, int out_cap, int *out_len,
+                         float *min_gap, const uint32_t *sl_ids, int n_sl) {
     const orc_config *c = &m->cfg;
     if (b <= 0) return 0;
     int max_new = 1;
@@ -1032,7 +1087,15 @@ int orc_generate(const orc_model *m, const uint32_t *ids, const uint32_t *lens, 
     int *nt = calloc((size_t)b, sizeof(int));
     int rc;
     const int sync = o->sync_every > 0 ? o->sync_every : 1;
-    if (o->beam_size <= 1) rc = greedy(m, st, b, tgt_lang, max_new, sync, flags, toks, nt, min_gap);
+    uint32_t *off = NULL;
+    orc_shortlist sl = {sl_ids, n_sl, ids, NULL};
+    if (n_sl > 0) {
+        off = malloc((size_t)(b + 1) * 4);
+        off[0] = 0;
+        for (int i = 0; i < b; ++i) off[i + 1] = off[i] + lens[i];
+        sl.off = off;
+    }
+    if (o->beam_size <= 1) rc = greedy(m, st, b, tgt_lang, max_new, sync, flags, toks, nt, min_gap, n_sl > 0 ? &sl : NULL);
     else rc = beam_search(m, st, b, tgt_lang, max_new, o->beam_size, o->length_penalty, flags, toks, nt);
     for (int i = 0; rc == 0 && i < b; ++i) {
         int n = nt[i];
@@ -1042,7 +1105,7 @@ int orc_generate(const orc_model *m, const uint32_t *ids, const uint32_t *lens, 
         memcpy(out + (size_t)i * out_cap, toks + (size_t)i * max_new, (size_t)n * 4);
         out_len[i] = n;
     }
-    free(toks); free(nt);
+    free(toks); free(nt); free(off);
     orc_state_free(st);
     return rc;
 }
