@@ -66,7 +66,7 @@ typedef struct {
     int bos_token_id, pad_token_id, eos_token_id, decoder_start_token_id;
 } mlg_config;
 
-/* src/translator.rs:15-53 GenOptions (shortlist is not offered by this backend). */
+/* src/translator.rs:15-53 GenOptions. */
 typedef struct {
     int beam_size;        /* 1 = greedy */
     int max_new_tokens;   /* 0 = None: 2 * src_len + 16, capped by max_length */
@@ -75,6 +75,9 @@ typedef struct {
     int max_batch;
     int fused;            /* 1 = static step replayed as a hipGraph; 0 = same step, eager */
     uint32_t flags;       /* MLG_FLAG_* */
+    const char *shortlist; /* GenOptions::shortlist (--fast-vocab): the target-language code whose
+                              shortlist greedy decoding uses when the model has one that holds
+                              decoder_start and tgt_lang (src/translator.rs:184-194); NULL = exact */
 } mlg_gen_options;
 
 const char *mlg_last_error(void);
@@ -121,6 +124,10 @@ int mlg_model_load(mlg_ctx *ctx, const char *gguf_path, mlg_model **out);
 void mlg_model_free(mlg_model *m);
 int mlg_model_config(const mlg_model *m, mlg_config *out);
 int64_t mlg_model_weight_bytes(const mlg_model *m);
+/* Nllb::shortlist_langs / shortlist (src/model.rs:439-447): number of shortlists, and the
+   language code and row count of shortlist i (code valid while the model lives). */
+int mlg_model_shortlist_count(const mlg_model *m);
+int mlg_model_shortlist_info(const mlg_model *m, int i, const char **code, int *rows);
 
 /* ---- translation on token ids ---- */
 void mlg_gen_options_default(mlg_gen_options *o);
@@ -137,6 +144,12 @@ void mlg_batch_free(mlg_batch *b);
 /* GraphCache::greedy (src/graph.rs:204-223); rows stripped at EOS. */
 int mlg_greedy(mlg_model *m, const mlg_batch *b, uint32_t tgt_lang, int max_new, int sync_every, uint32_t flags,
                uint32_t *out, int out_cap, int *out_len);
+/* GraphCache::greedy with Some(shortlist) (src/graph.rs:204-298, src/model.rs:597-606): the
+   candidates of each step are the shortlist rows of language `code` and the batch's source
+   tokens.  MLG_ERR_INVALID if the model has no such shortlist or it lacks decoder_start or
+   tgt_lang ("token missing from the shortlist", src/graph.rs:125). */
+int mlg_greedy_sl(mlg_model *m, const mlg_batch *b, uint32_t tgt_lang, const char *code, int max_new, int sync_every,
+                  uint32_t flags, uint32_t *out, int out_cap, int *out_len);
 /* Translator::beam_search (src/translator.rs:250-335).  One decoder step + top-k is captured
    once and replayed per step (MLG_FLAG_NO_GRAPH: eager); MLG_FLAG_EOS_MASK as for mlg_greedy. */
 int mlg_beam(mlg_model *m, const mlg_batch *b, uint32_t tgt_lang, int max_new, int beam_size, float length_penalty,

@@ -34,7 +34,9 @@ __all__ = ["GenOptions", "Translator", "Config", "MalagaError", "convert", "writ
 
 @dataclasses.dataclass
 class GenOptions:
-    """src/translator.rs:15-53 (``shortlist`` is not offered by this backend)."""
+    """src/translator.rs:15-53.  ``shortlist``: the target-language code whose vocabulary
+    shortlist greedy decoding uses (``--fast-vocab``; the reference's bool plus the code it
+    derives from the tokenizer), or None for exact decoding."""
 
     beam_size: int = 1
     max_new_tokens: int | None = None
@@ -43,6 +45,7 @@ class GenOptions:
     max_batch: int = 32
     fused: bool = True
     eos_mask: bool = False  # benchmark-only: EOS never chosen, so lengths are fixed
+    shortlist: str | None = None
 
     def _c(self) -> CGenOptions:
         o = CGenOptions()
@@ -53,6 +56,7 @@ class GenOptions:
         o.max_batch = self.max_batch
         o.fused = 1 if self.fused else 0
         o.flags = FLAG_EOS_MASK if self.eos_mask else 0
+        o.shortlist = self.shortlist.encode() if self.shortlist else None
         return o
 
 
@@ -151,14 +155,28 @@ class Translator:
         return EncodedBatch(self.lib, h, len(src))
 
     def greedy(self, batch: EncodedBatch, tgt_lang: int, max_new: int, sync_every: int = 4,
-               eos_mask: bool = False, graph: bool = True) -> list[list[int]]:
-        """GraphCache::greedy (src/graph.rs:204-223): rows stripped at EOS."""
+               eos_mask: bool = False, graph: bool = True, shortlist: str | None = None) -> list[list[int]]:
+        """GraphCache::greedy (src/graph.rs:204-223): rows stripped at EOS.  ``shortlist``:
+        decode over that language's shortlist plus the source tokens."""
         out = np.zeros((batch.n, max_new + 1), dtype=np.uint32)
         out_len = np.zeros(batch.n, dtype=np.int32)
         flags = (FLAG_EOS_MASK if eos_mask else 0) | (0 if graph else FLAG_NO_GRAPH)
-        check(self.lib.mlg_greedy(self.h, batch.h, tgt_lang, max_new, sync_every, flags, out.ctypes.data,
-                                  max_new + 1, out_len.ctypes.data))
+        if shortlist:
+            check(self.lib.mlg_greedy_sl(self.h, batch.h, tgt_lang, shortlist.encode(), max_new, sync_every, flags,
+                                         out.ctypes.data, max_new + 1, out_len.ctypes.data))
+        else:
+            check(self.lib.mlg_greedy(self.h, batch.h, tgt_lang, max_new, sync_every, flags, out.ctypes.data,
+                                      max_new + 1, out_len.ctypes.data))
         return _rows(out, out_len)
+
+    def shortlists(self) -> dict[str, int]:
+        """Languages with a vocabulary shortlist and their row counts (src/model.rs:439-447)."""
+        res = {}
+        for i in range(int(self.lib.mlg_model_shortlist_count(self.h))):
+            code, rows = C.c_char_p(), C.c_int()
+            check(self.lib.mlg_model_shortlist_info(self.h, i, C.byref(code), C.byref(rows)))
+            res[code.value.decode()] = rows.value
+        return res
 
     def beam(self, batch: EncodedBatch, tgt_lang: int, max_new: int, beam_size: int, length_penalty: float = 1.0,
              eos_mask: bool = False) -> list[list[int]]:

@@ -41,7 +41,8 @@ class Config(C.Structure):
 
 class CGenOptions(C.Structure):
     _fields_ = [("beam_size", C.c_int), ("max_new_tokens", C.c_int), ("length_penalty", C.c_float),
-                ("sync_every", C.c_int), ("max_batch", C.c_int), ("fused", C.c_int), ("flags", C.c_uint32)]
+                ("sync_every", C.c_int), ("max_batch", C.c_int), ("fused", C.c_int), ("flags", C.c_uint32),
+                ("shortlist", C.c_char_p)]
 
 
 class ShortlistSpec(C.Structure):
@@ -79,11 +80,14 @@ SIGNATURES = {
     "mlg_model_free": (None, [_P]),
     "mlg_model_config": (C.c_int, [_P, C.POINTER(Config)]),
     "mlg_model_weight_bytes": (C.c_int64, [_P]),
+    "mlg_model_shortlist_count": (C.c_int, [_P]),
+    "mlg_model_shortlist_info": (C.c_int, [_P, C.c_int, C.POINTER(C.c_char_p), _intp]),
     "mlg_gen_options_default": (None, [C.POINTER(CGenOptions)]),
     "mlg_generate": (C.c_int, [_P, _P, _P, C.c_int, C.c_uint32, C.POINTER(CGenOptions), _P, C.c_int, _P]),
     "mlg_encode": (C.c_int, [_P, _P, _P, C.c_int, C.POINTER(_P)]),
     "mlg_batch_free": (None, [_P]),
     "mlg_greedy": (C.c_int, [_P, _P, C.c_uint32, C.c_int, C.c_int, C.c_uint32, _P, C.c_int, _P]),
+    "mlg_greedy_sl": (C.c_int, [_P, _P, C.c_uint32, C.c_char_p, C.c_int, C.c_int, C.c_uint32, _P, C.c_int, _P]),
     "mlg_beam": (C.c_int, [_P, _P, C.c_uint32, C.c_int, C.c_int, C.c_float, C.c_uint32, _P, C.c_int, _P]),
     "mlg_clear_graphs": (None, [_P]),
     "mlg_graph_stats": (C.c_int, [_P, _intp, _intp, _intp]),

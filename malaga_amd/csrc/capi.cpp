@@ -282,6 +282,16 @@ int mlg_model_config(const mlg_model *m, mlg_config *out) {
 
 int64_t mlg_model_weight_bytes(const mlg_model *m) { return m ? int64_t(m->m->weight_bytes) : 0; }
 
+int mlg_model_shortlist_count(const mlg_model *m) { return m ? int(m->m->shortlists.size()) : 0; }
+
+int mlg_model_shortlist_info(const mlg_model *m, int i, const char **code, int *rows) {
+    if (!m || i < 0 || i >= int(m->m->shortlists.size())) return set_err(MLG_ERR_INVALID, "no such shortlist");
+    const mlg::Shortlist &sl = *m->m->shortlists[size_t(i)];
+    if (code) *code = sl.code.c_str();
+    if (rows) *rows = int(sl.ids.size());
+    return MLG_OK;
+}
+
 void mlg_gen_options_default(mlg_gen_options *o) {
     o->beam_size = 1;
     o->max_new_tokens = 0;
@@ -290,6 +300,7 @@ void mlg_gen_options_default(mlg_gen_options *o) {
     o->max_batch = 32;
     o->fused = 1;
     o->flags = 0;
+    o->shortlist = nullptr;
 }
 
 int mlg_generate(mlg_model *m, const uint32_t *ids, const uint32_t *lens, int n, uint32_t tgt_lang,
@@ -307,6 +318,7 @@ int mlg_generate(mlg_model *m, const uint32_t *ids, const uint32_t *lens, int n,
         g.max_batch = o->max_batch;
         g.fused = o->fused != 0 && !(o->flags & MLG_FLAG_NO_GRAPH);
         g.eos_mask = (o->flags & MLG_FLAG_EOS_MASK) != 0;
+        if (o->shortlist) g.shortlist = o->shortlist;
         if (g.beam_size > 8) return set_err(MLG_ERR_UNSUPPORTED, "beam_size > 8");
         auto src = rows_of(ids, lens, n);
         for (auto &r : src)
@@ -337,6 +349,20 @@ int mlg_greedy(mlg_model *m, const mlg_batch *b, uint32_t tgt_lang, int max_new,
         mlg::check_hip(hipSetDevice(m->m->ctx->device), "hipSetDevice");
         auto rows = m->m->graphs.greedy(*b->b, tgt_lang, max_new, sync_every > 0 ? sync_every : 1,
                                         (flags & MLG_FLAG_EOS_MASK) != 0, !(flags & MLG_FLAG_NO_GRAPH));
+        return write_rows(rows, out, out_cap, out_len);
+    });
+}
+
+int mlg_greedy_sl(mlg_model *m, const mlg_batch *b, uint32_t tgt_lang, const char *code, int max_new, int sync_every,
+                  uint32_t flags, uint32_t *out, int out_cap, int *out_len) {
+    return guarded([&]() -> int {
+        if (!m || !b || !code || max_new < 1 || !out || !out_len) return set_err(MLG_ERR_INVALID, "bad argument");
+        const mlg::Shortlist *sl = m->m->shortlist(code);
+        if (!sl) return set_err(MLG_ERR_INVALID, std::string("no shortlist for ") + code);
+        std::lock_guard<std::mutex> lk(m->m->ctx->mu);
+        mlg::check_hip(hipSetDevice(m->m->ctx->device), "hipSetDevice");
+        auto rows = m->m->graphs.greedy(*b->b, tgt_lang, max_new, sync_every > 0 ? sync_every : 1,
+                                        (flags & MLG_FLAG_EOS_MASK) != 0, !(flags & MLG_FLAG_NO_GRAPH), sl);
         return write_rows(rows, out, out_cap, out_len);
     });
 }

@@ -84,11 +84,18 @@ __global__ __launch_bounds__(kLnThreads) void k_embed_pos_ln(const uint8_t *q, c
                                                              const uint32_t *ids, const float *pos,
                                                              const uint32_t *step, uint32_t base, float scale, int d,
                                                              const float *g, const float *b, float eps, float *x,
-                                                             float *h) {
+                                                             float *h, SrcEmb src) {
     extern __shared__ float e[];
     __shared__ float sh[16];
     const int row = blockIdx.x;
-    embed_row<T>(q, s, dp, d, ids[row], e);
+    const uint32_t sr = src.row ? src.row[row] : kNoRow;  // workgroup-uniform
+    if (sr != kNoRow) {  // the previous token was a copy of source position sr
+        const float *er = src.emb + (size_t(row) * src.S + sr) * d;
+        for (int i = threadIdx.x; i < d; i += blockDim.x) e[i] = er[i];
+        __syncthreads();
+    } else {
+        embed_row<T>(q, s, dp, d, ids[row], e);
+    }
     const float *pr = pos + size_t(*step + base) * d;
     const size_t off = size_t(row) * d;
     float v[kLnMaxPerThread];
@@ -113,6 +120,39 @@ __global__ __launch_bounds__(kLnThreads) void k_embed_pos_rows(const uint8_t *q,
     embed_row<T>(q, s, dp, d, ids[row], e);
     const float *pr = pos + size_t(pidx[row]) * d;
     for (int i = threadIdx.x; i < d; i += blockDim.x) x[size_t(row) * d + i] = e[i] * scale + pr[i];
+}
+
+template <int T>
+__global__ __launch_bounds__(kLnThreads) void k_embed_rows(const uint8_t *q, const uint8_t *s, const uint8_t *dp,
+                                                           const uint32_t *ids, int d, float *out) {
+    const int row = blockIdx.x;
+    for (int k0 = threadIdx.x * 16; k0 < d; k0 += blockDim.x * 16) {
+        float w[16];
+        dequant16<T>(q, s, dp, d, int(ids[row]), k0, w);
+#pragma unroll
+        for (int i = 0; i < 16; ++i) out[size_t(row) * d + k0 + i] = w[i];
+    }
+}
+
+// kernels/malaga.cu:229-243 (row_dots): one wave per (row, source position).
+__global__ __launch_bounds__(256) void k_source_logits(const float *h, const float *emb, const uint32_t *src_ids,
+                                                       int b, int S, int d, int mask_id, int V1, float *spv,
+                                                       uint32_t *spi) {
+    const int p = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
+    if (p >= b * S) return;  // wave-uniform
+    const int r = p / S;
+    const float4 *x = reinterpret_cast<const float4 *>(h + size_t(r) * d);
+    const float4 *e = reinterpret_cast<const float4 *>(emb + size_t(p) * d);
+    float acc = 0.f;
+    for (int t = lane; t < d / 4; t += 64) {
+        const float4 a = x[t], c = e[t];
+        acc += a.x * c.x + a.y * c.y + a.z * c.z + a.w * c.w;
+    }
+    acc = wave_sum(acc);
+    if (lane == 0) {
+        spv[p] = (mask_id >= 0 && src_ids[p] == uint32_t(mask_id)) ? -INFINITY : acc;
+        spi[p] = uint32_t(V1 + p % S);
+    }
 }
 
 __global__ void k_qkv_split(const float *qkv, int H, int hd, int m, const uint32_t *step, float *q, __half *kc,
@@ -278,12 +318,23 @@ __global__ __launch_bounds__(256) void k_argmax_partial(const float *logits, int
     }
 }
 
-// kernels/malaga.cu:290-326 semantics, without the shortlist mapping.
+// kernels/malaga.cu:290-326 semantics (with sl.vocab_map: the shortlist mapping).
 // Small batches: each row's partials are reduced by the whole workgroup (8
 // independent loads per thread).
+// Token of candidate i (shortlist decoding): shortlist row or source position, and
+// where the next step finds its embedding (kernels/malaga.cu:309-319).
+__device__ __forceinline__ uint32_t sl_token(const SlFinalize &sl, int row, uint32_t i, bool done, uint32_t pad) {
+    const bool from_sl = i < uint32_t(sl.V1), from_src = !from_sl && i - uint32_t(sl.V1) < uint32_t(sl.S);
+    const uint32_t tok = from_sl ? sl.vocab_map[i] : from_src ? sl.src_ids[size_t(row) * sl.S + (i - sl.V1)] : pad;
+    sl.sl_row[row] = (!done && from_sl) ? i : 0u;
+    sl.src_row[row] = (!done && from_src) ? i - uint32_t(sl.V1) : kNoRow;
+    return tok;
+}
+
 __global__ __launch_bounds__(256) void k_greedy_finalize_wg(const float *pv, const uint32_t *pi, int P, int b,
                                                             uint8_t *finished, uint32_t *ids, uint32_t *out, int m,
-                                                            uint32_t *step, uint32_t eos, uint32_t pad) {
+                                                            uint32_t *step, uint32_t eos, uint32_t pad,
+                                                            SlFinalize sl) {
     __shared__ float sv[4];
     __shared__ uint32_t si[4];
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
@@ -303,6 +354,9 @@ __global__ __launch_bounds__(256) void k_greedy_finalize_wg(const float *pv, con
 #pragma unroll
             for (int u = 0; u < 8; ++u) argmax_merge(best, bi, v[u], ix[u]);
         }
+        if (sl.vocab_map)  // the source-token candidates
+            for (int p = threadIdx.x; p < sl.S; p += 256)
+                argmax_merge(best, bi, sl.spv[size_t(row) * sl.S + p], sl.spi[size_t(row) * sl.S + p]);
         wave_argmax(best, bi);
         if (lane == 0) {
             sv[w] = best;
@@ -313,7 +367,7 @@ __global__ __launch_bounds__(256) void k_greedy_finalize_wg(const float *pv, con
             best = sv[0];
             bi = si[0];
             for (int k = 1; k < 4; ++k) argmax_merge(best, bi, sv[k], si[k]);
-            uint32_t tok = bi;
+            uint32_t tok = sl.vocab_map ? sl_token(sl, row, bi, finished[row] != 0, pad) : bi;
             if (finished[row]) tok = pad;
             if (tok == eos) finished[row] = 1;
             ids[row] = tok;
@@ -328,7 +382,7 @@ __global__ __launch_bounds__(256) void k_greedy_finalize_wg(const float *pv, con
 // lane in flight; the step counter is advanced after every wave has read it.
 __global__ __launch_bounds__(1024) void k_greedy_finalize(const float *pv, const uint32_t *pi, int P, int b,
                                                           uint8_t *finished, uint32_t *ids, uint32_t *out, int m,
-                                                          uint32_t *step, uint32_t eos, uint32_t pad) {
+                                                          uint32_t *step, uint32_t eos, uint32_t pad, SlFinalize sl) {
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, nw = blockDim.x >> 6;
     const uint32_t s = *step;
     for (int row = w; row < b; row += nw) {  // wave-uniform
@@ -346,9 +400,12 @@ __global__ __launch_bounds__(1024) void k_greedy_finalize(const float *pv, const
 #pragma unroll
             for (int u = 0; u < 8; ++u) argmax_merge(best, bi, v[u], ix[u]);
         }
+        if (sl.vocab_map)  // the source-token candidates
+            for (int p = lane; p < sl.S; p += 64)
+                argmax_merge(best, bi, sl.spv[size_t(row) * sl.S + p], sl.spi[size_t(row) * sl.S + p]);
         wave_argmax(best, bi);
         if (lane == 0) {
-            uint32_t tok = bi;
+            uint32_t tok = sl.vocab_map ? sl_token(sl, row, bi, finished[row] != 0, pad) : bi;
             if (finished[row]) tok = pad;
             if (tok == eos) finished[row] = 1;
             ids[row] = tok;
@@ -592,9 +649,15 @@ int grid_1d(size_t n, int block) {
 template <int T>
 hipError_t launch_embed_pos_ln(const DevMatrix &E, const uint32_t *ids, int rows, const float *pos,
                                const uint32_t *step, uint32_t base, float scale, const float *g, const float *b,
-                               float eps, float *x, float *h, hipStream_t st) {
+                               float eps, float *x, float *h, hipStream_t st, const SrcEmb &src) {
     hipLaunchKernelGGL(k_embed_pos_ln<T>, dim3(rows), dim3(kLnThreads), E.K * sizeof(float), st, E.q, E.s, E.d, ids,
-                       pos, step, base, scale, E.K, g, b, eps, x, h);
+                       pos, step, base, scale, E.K, g, b, eps, x, h, src);
+    return hipGetLastError();
+}
+
+template <int T>
+hipError_t launch_embed_rows(const DevMatrix &E, const uint32_t *ids, int rows, float *out, hipStream_t st) {
+    hipLaunchKernelGGL(k_embed_rows<T>, dim3(rows), dim3(kLnThreads), 0, st, E.q, E.s, E.d, ids, E.K, out);
     return hipGetLastError();
 }
 
@@ -625,9 +688,24 @@ hipError_t residual_ln(float *x, const float *y, int rows, int d, const float *g
 
 hipError_t embed_pos_ln(const DevMatrix &E, const uint32_t *ids, int rows, const float *pos, const uint32_t *step,
                         uint32_t base, float scale, const float *g, const float *b, float eps, float *x, float *h,
-                        hipStream_t st) {
-    if (E.K > kLnThreads * kLnMaxPerThread || E.K % 16) return hipErrorInvalidValue;
-    MLG_DISPATCH_TYPE(E.type, launch_embed_pos_ln, E, ids, rows, pos, step, base, scale, g, b, eps, x, h, st)
+                        hipStream_t st, const SrcEmb &src) {
+    if (E.K > kLnThreads * kLnMaxPerThread || E.K % 16 || (src.row && (!src.emb || src.S < 1)))
+        return hipErrorInvalidValue;
+    MLG_DISPATCH_TYPE(E.type, launch_embed_pos_ln, E, ids, rows, pos, step, base, scale, g, b, eps, x, h, st, src)
+}
+
+hipError_t embed_rows(const DevMatrix &E, const uint32_t *ids, int rows, float *out, hipStream_t st) {
+    if (E.K % 16) return hipErrorInvalidValue;
+    if (rows <= 0) return hipSuccess;
+    MLG_DISPATCH_TYPE(E.type, launch_embed_rows, E, ids, rows, out, st)
+}
+
+hipError_t source_logits(const float *h, const float *emb, const uint32_t *src_ids, int b, int S, int d, int mask_id,
+                         int V1, float *spv, uint32_t *spi, hipStream_t st) {
+    if (d % 4 || S < 1 || b < 1) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(k_source_logits, dim3(unsigned((b * S + 3) / 4)), dim3(256), 0, st, h, emb, src_ids, b, S, d,
+                       mask_id, V1, spv, spi);
+    return hipGetLastError();
 }
 
 hipError_t embed_pos_rows(const DevMatrix &E, const uint32_t *ids, const uint32_t *pidx, int rows, const float *pos,
@@ -694,13 +772,16 @@ hipError_t argmax_partial(const float *logits, int b, int V, int ldl, int mask_i
 }
 
 hipError_t greedy_finalize(const float *pv, const uint32_t *pi, int parts, int b, uint8_t *finished, uint32_t *ids,
-                           uint32_t *out, int m, uint32_t *step, uint32_t eos, uint32_t pad, hipStream_t st) {
+                           uint32_t *out, int m, uint32_t *step, uint32_t eos, uint32_t pad, hipStream_t st,
+                           const SlFinalize &sl) {
+    if (sl.vocab_map && (!sl.spv || !sl.spi || !sl.src_ids || !sl.sl_row || !sl.src_row || sl.S < 1))
+        return hipErrorInvalidValue;
     if (b <= 4)
         hipLaunchKernelGGL(k_greedy_finalize_wg, dim3(1), dim3(256), 0, st, pv, pi, parts, b, finished, ids, out, m,
-                           step, eos, pad);
+                           step, eos, pad, sl);
     else
         hipLaunchKernelGGL(k_greedy_finalize, dim3(1), dim3(1024), 0, st, pv, pi, parts, b, finished, ids, out, m,
-                           step, eos, pad);
+                           step, eos, pad, sl);
     return hipGetLastError();
 }
 

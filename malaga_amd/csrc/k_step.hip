@@ -42,6 +42,10 @@ struct StepArgs {
     // embedding prologue: x = E[ids[r]] * emb_scale + pos[*step + pos_base]
     const uint8_t *eq, *es, *ed;
     const uint32_t *ids;
+    // ... or, where src_row[r] != kNoRow, x = src_emb[r][src_row[r]] * emb_scale + pos (a copied source token)
+    const float *src_emb;
+    const uint32_t *src_row;
+    int S;
     const float *pos;
     uint32_t pos_base;
     float emb_scale;
@@ -171,7 +175,14 @@ __device__ __forceinline__ void resid_ln_prologue(const StepArgs &a, const PreLo
             for (int i = t; i < nb * per_row; i += 256) {
                 const int bi = i / per_row, k0 = (i % per_row) * 16;
                 float e[16];
-                dequant16<ET>(a.eq, a.es, a.ed, d, int(a.ids[bi]), k0, e);
+                const uint32_t sr = a.src_row ? a.src_row[bi] : kNoRow;
+                if (sr != kNoRow) {
+                    const float *er = a.src_emb + (size_t(bi) * a.S + sr) * d + k0;
+#pragma unroll
+                    for (int j = 0; j < 16; ++j) e[j] = er[j];
+                } else {
+                    dequant16<ET>(a.eq, a.es, a.ed, d, int(a.ids[bi]), k0, e);
+                }
 #pragma unroll
                 for (int j = 0; j < 16; ++j) xs[bi * lds_pad(d) + lds_pad(k0 + j)] = e[j] * a.emb_scale + pr[k0 + j];
             }
@@ -542,10 +553,14 @@ bool step_embed_supported(uint32_t t, uint32_t e) {
 hipError_t step_qkv(const DevMatrix &w, const float *bias, int nb, int d, const DevMatrix *emb, const uint32_t *ids,
                     const float *pos, uint32_t pos_base, float emb_scale, const float *x_in, const float *y_in,
                     float *x_out, const float *gamma, const float *beta, float eps, const uint32_t *step, float *q,
-                    __half *kc, __half *vc, int H, int hd, int m, hipStream_t st) {
+                    __half *kc, __half *vc, int H, int hd, int m, hipStream_t st, const SrcEmb &src) {
     StepArgs a{};
     int cpl;
     if (!prepare(w, nb, a, &cpl) || !step_fusable(w, nb, d) || w.N != 3 * d) return hipErrorInvalidValue;
+    if (src.row && (!emb || !src.emb || src.S < 1)) return hipErrorInvalidValue;
+    a.src_emb = src.emb;
+    a.src_row = src.row;
+    a.S = src.S;
     a.d = d;
     a.x_in = x_in;
     a.part = y_in;

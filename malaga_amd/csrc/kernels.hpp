@@ -78,10 +78,40 @@ hipError_t layernorm(const float *x, int rows, int d, const float *g, const floa
 // x = x + y ; h = LayerNorm(x).  (bias already added to y by the producer)
 hipError_t residual_ln(float *x, const float *y, int rows, int d, const float *g, const float *b, float eps, float *h,
                        hipStream_t st);
+// ---- vocabulary shortlists (src/model.rs:555-603, kernels/malaga.cu:107-118, 229-326) ----
+constexpr uint32_t kNoRow = 0xffffffffu;
+// Decoder input copied from the source sentence: row r uses emb[r][row[r]] (f32) when
+// row[r] != kNoRow, else the embedding matrix.
+struct SrcEmb {
+    const float *emb = nullptr;     // [b][S][d]
+    const uint32_t *row = nullptr;  // [b]
+    int S = 0;
+};
+// Shortlist form of greedy_finalize: the candidates of a row are the shortlist rows
+// (partials pv/pi, indices < V1) then the source tokens (spv/spi [b][S], indices V1 + j).
+// The winner maps to vocab_map[i] or src_ids[r][i - V1]; sl_row / src_row receive where
+// the next input embedding is (shortlist row, or source position, else kNoRow).
+struct SlFinalize {
+    const uint32_t *vocab_map = nullptr;  // [V1]; null: no shortlist
+    int V1 = 0;
+    const float *spv = nullptr;
+    const uint32_t *spi = nullptr;
+    const uint32_t *src_ids = nullptr;    // [b][S]
+    int S = 0;
+    uint32_t *sl_row = nullptr, *src_row = nullptr;
+};
+// Logits of the source tokens (row_dots): spv[r][j] = h[r] . emb[r][j], spi = V1 + j;
+// -inf where src_ids[r][j] == mask_id (mask_id >= 0).
+hipError_t source_logits(const float *h, const float *emb, const uint32_t *src_ids, int b, int S, int d, int mask_id,
+                         int V1, float *spv, uint32_t *spi, hipStream_t st);
+// Rows of E as f32: out[r] = dequant(E[ids[r]]) (source-token embeddings).
+hipError_t embed_rows(const DevMatrix &E, const uint32_t *ids, int rows, float *out, hipStream_t st);
+
 // Decoder input: x = dequant(E[ids[r]]) * scale + pos[*step + base]; h = LayerNorm(x).
+// src: rows whose input is a source-token embedding.
 hipError_t embed_pos_ln(const DevMatrix &E, const uint32_t *ids, int rows, const float *pos, const uint32_t *step,
                         uint32_t base, float scale, const float *g, const float *b, float eps, float *x, float *h,
-                        hipStream_t st);
+                        hipStream_t st, const SrcEmb &src = SrcEmb{});
 // Encoder input rows: x[r] = dequant(E[ids[r]]) * scale + pos[pidx[r]].
 hipError_t embed_pos_rows(const DevMatrix &E, const uint32_t *ids, const uint32_t *pidx, int rows, const float *pos,
                           float scale, float *x, hipStream_t st);
@@ -111,13 +141,13 @@ hipError_t argmax_partial(const float *logits, int b, int V, int ldl, int mask_i
 // tok = finished ? pad : argmax ; finished |= tok == eos ; ids = tok ;
 // out[row][*step] = tok ; ++*step.
 hipError_t greedy_finalize(const float *pv, const uint32_t *pi, int parts, int b, uint8_t *finished, uint32_t *ids,
-                           uint32_t *out, int m, uint32_t *step, uint32_t eos, uint32_t pad, hipStream_t st);
+                           uint32_t *out, int m, uint32_t *step, uint32_t eos, uint32_t pad, hipStream_t st,
+                           const SlFinalize &sl = SlFinalize{});
 // Beam: per row log-softmax of logits [rows][V] and its top-k (k <= 8, ties -> lowest
 // index): vals/idx [rows][k].  mask_id (>= 0) is treated as -inf.
 hipError_t logsoftmax_topk(const float *logits, int rows, int V, int k, int mask_id, float *scratch, float *vals,
                            uint32_t *idx, hipStream_t st);
 size_t logsoftmax_topk_scratch(int rows, int k);
-// dst[i] = src[idx[i]] for rows of `row_bytes` bytes (i < n).
 // ---- fused decoder-step kernels (batch <= 4), k_step.hip ----
 // True when the fused GEMV kernels (residual + LayerNorm prologue over d-wide rows)
 // handle matrix w at batch nb.
@@ -132,7 +162,7 @@ bool step_embed_supported(uint32_t proj_type, uint32_t emb_type);
 hipError_t step_qkv(const DevMatrix &w, const float *bias, int nb, int d, const DevMatrix *emb, const uint32_t *ids,
                     const float *pos, uint32_t pos_base, float emb_scale, const float *x_in, const float *y_in,
                     float *x_out, const float *gamma, const float *beta, float eps, const uint32_t *step, float *q,
-                    __half *kc, __half *vc, int H, int hd, int m, hipStream_t st);
+                    __half *kc, __half *vc, int H, int hd, int m, hipStream_t st, const SrcEmb &src = SrcEmb{});
 // Attention of q over K/V [nb][H][L][hd] (lens: cross lengths, or null for *step + 1
 // keys), times the out-projection w, as step_head_parts(...) partial sums
 // part[p][nb][d] (bias not added): sum over p = attention . W^T.

@@ -280,7 +280,36 @@ void Model::load(const std::string &path) {
     }
     enc_norm = load_ln(g, "enc.output_norm", d);
     dec_norm = load_ln(g, "dec.output_norm", d);
+    // src/model.rs:403-412: nllb.shortlist.{code} = ids, lm_head.{code}.weight = their rows
+    const std::string prefix = "nllb.shortlist.";
+    for (const auto &kv : g.metadata()) {
+        if (kv.first.compare(0, prefix.size(), prefix) != 0) continue;
+        auto sl = std::make_unique<Shortlist>();
+        sl->code = kv.first.substr(prefix.size());
+        if (kv.second.type != GV_ARRAY || kv.second.arr.empty())
+            fail(ERR_FORMAT, "shortlist " + sl->code + ": expected a non-empty id array");
+        for (const GgufValue &v : kv.second.arr) {
+            if (!v.is_int() || v.u >= uint64_t(cfg.vocab_size))
+                fail(ERR_FORMAT, "shortlist " + sl->code + ": id out of range");
+            sl->ids.push_back(uint32_t(v.u));
+        }
+        // Shortlist::row is a binary search (src/model.rs:246-249): the ids must be sorted
+        if (!std::is_sorted(sl->ids.begin(), sl->ids.end()))
+            fail(ERR_FORMAT, "shortlist " + sl->code + ": ids not sorted");
+        const int n = int(sl->ids.size());
+        sl->head = upload_matrix(g, "lm_head." + sl->code + ".weight", n, d);
+        sl->d_ids = static_cast<uint32_t *>(dev_alloc(size_t(n) * 4, "shortlist ids"));
+        owned_.push_back(sl->d_ids);
+        check_hip(hipMemcpy(sl->d_ids, sl->ids.data(), size_t(n) * 4, hipMemcpyHostToDevice), "upload");
+        shortlists.push_back(std::move(sl));
+    }
     check_hip(hipDeviceSynchronize(), "model upload");
+}
+
+const Shortlist *Model::shortlist(const std::string &code) const {
+    for (const auto &sl : shortlists)
+        if (sl->code == code) return sl.get();
+    return nullptr;
 }
 
 void Model::matmul(const Linear &l, const float *x, int rows, float *y, bool relu, const float *resid) {
@@ -345,6 +374,7 @@ std::unique_ptr<Batch> Model::encode(const std::vector<std::vector<uint32_t>> &s
     float *kv = static_cast<float *>(carve(n_kv));
     h2d(d_ids, ids, st);
     h2d(d_pidx, pidx, st);
+    out->ids = ids;
     h2d(d_lens, out->lens, st);
     check_hip(embed_pos_rows(embed, d_ids, d_pidx, M, pos, embed_scale, x, st), "embed");
     for (auto &l : enc) {
@@ -372,11 +402,13 @@ std::unique_ptr<Batch> Model::encode(const std::vector<std::vector<uint32_t>> &s
     return out;
 }
 
-std::unique_ptr<StaticState> Model::new_state(int b, int s, int m, bool logits, bool row_map) {
+std::unique_ptr<StaticState> Model::new_state(int b, int s, int m, bool logits, bool row_map, const Shortlist *sl) {
     auto st = std::make_unique<StaticState>();
     st->b = b;
     st->s = s;
     st->m = m;
+    st->sl = sl;
+    const DevMatrix &head = sl ? sl->head : embed;
     const int d = cfg.d_model, H = cfg.decoder_heads, hd = d / H, L = cfg.decoder_layers, V = cfg.vocab_size;
     auto get = [&](size_t bytes, const char *what) {
         void *p = dev_alloc(bytes, what);
@@ -404,7 +436,7 @@ std::unique_ptr<StaticState> Model::new_state(int b, int s, int m, bool logits, 
     st->x = static_cast<float *>(get(size_t(b) * d * 4, "x"));
     st->xb = static_cast<float *>(get(size_t(b) * d * 4, "x (second buffer)"));
     st->qc = static_cast<float *>(get(size_t(b) * d * 4, "cross q"));
-    st->fused = fusable(b, m, s);
+    st->fused = fusable(b, m, s) && (!sl || step_embed_supported(dec[0].qkv.w.type, sl->head.type));
     if (st->fused) st->part = static_cast<float *>(get(size_t(H) * b * d * 4, "attention partial sums"));
     st->h = static_cast<float *>(get(size_t(b) * d * 4, "h"));
     st->y = static_cast<float *>(get(size_t(b) * d * 4, "y"));
@@ -412,7 +444,16 @@ std::unique_ptr<StaticState> Model::new_state(int b, int s, int m, bool logits, 
     st->q = static_cast<float *>(get(size_t(b) * d * 4, "q"));
     st->qkv = static_cast<float *>(get(size_t(b) * 3 * d * 4, "qkv"));
     st->u = static_cast<float *>(get(size_t(b) * cfg.decoder_ffn * 4, "ffn"));
-    if (logits || b > gemv_max_batch(embed)) st->logits = static_cast<float *>(get(size_t(b) * V * 4, "logits"));
+    if (logits || b > gemv_max_batch(head))
+        st->logits = static_cast<float *>(get(size_t(b) * (sl ? head.N : V) * 4, "logits"));
+    if (sl) {  // src/graph.rs:76-79
+        st->src_ids = static_cast<uint32_t *>(get(size_t(b) * s * 4, "source ids"));
+        st->src_emb = static_cast<float *>(get(size_t(b) * s * d * 4, "source embeddings"));
+        st->sl_row = static_cast<uint32_t *>(get(size_t(b) * 4, "shortlist rows"));
+        st->src_row = static_cast<uint32_t *>(get(size_t(b) * 4, "source positions"));
+        st->spv = static_cast<float *>(get(size_t(b) * s * 4, "source logits"));
+        st->spi = static_cast<uint32_t *>(get(size_t(b) * s * 4, "source logits"));
+    }
     if (row_map) {  // identity until a beam reorder rewrites it
         st->rows = static_cast<uint32_t *>(get(size_t(b) * m * 4, "beam cache rows"));
         std::vector<uint32_t> id(size_t(b) * m);
@@ -420,8 +461,8 @@ std::unique_ptr<StaticState> Model::new_state(int b, int s, int m, bool logits, 
             for (int j = 0; j < m; ++j) id[size_t(r) * m + j] = uint32_t(r);
         h2d(st->rows, id, ctx->stream);
     }
-    st->parts = std::max(gemv_argmax_parts(embed, b), 64);
-    if (b > gemv_max_batch(embed) && gemm_rx_supported(embed, b)) st->parts = std::max(st->parts, gemm_argmax_parts(embed, b));
+    st->parts = std::max(gemv_argmax_parts(head, b), 64);
+    if (b > gemv_max_batch(head) && gemm_rx_supported(head, b)) st->parts = std::max(st->parts, gemm_argmax_parts(head, b));
     st->pv = static_cast<float *>(get(size_t(b) * st->parts * 4, "argmax partials"));
     st->pi = static_cast<uint32_t *>(get(size_t(b) * st->parts * 4, "argmax partials"));
     check_hip(hipStreamSynchronize(ctx->stream), "state");
@@ -445,9 +486,29 @@ void Model::reset_state(StaticState &st, const Batch &src, const std::vector<uin
     h2d(st.lens, lens, s);
     check_hip(fill_u32(st.ids, start, size_t(st.b), s), "fill");
     check_hip(fill_u32(st.step, 0, 1, s), "fill");
+    if (st.sl) {
+        // src/graph.rs:98-108: source ids of every row (pad past the row's length, idle
+        // rows all pad) and their token_embd rows
+        if (src.s > st.s) fail(ERR_INVALID, "reset_state: source longer than the state");
+        const uint32_t pad = uint32_t(cfg.pad_token_id);
+        std::vector<uint32_t> ids(size_t(st.b) * st.s, pad);
+        for (int r = 0; r < n; ++r)
+            std::copy_n(src.ids.begin() + size_t(row_of[r]) * src.s, src.s, ids.begin() + size_t(r) * st.s);
+        h2d(st.src_ids, ids, s);
+        check_hip(embed_rows(embed, st.src_ids, st.b * st.s, st.src_emb, s), "embed_rows");
+        set_shortlist_input(st, start);
+    }
     std::vector<uint8_t> fin(static_cast<size_t>(st.b));
     for (int r = 0; r < st.b; ++r) fin[r] = r >= n;
     h2d(st.finished, fin, s);
+}
+
+// src/graph.rs:121-130 (set_ids): every row's next input is vocabulary id `id`.
+void Model::set_shortlist_input(StaticState &st, uint32_t id) {
+    const int row = st.sl->row(id);
+    if (row < 0) fail(ERR_INVALID, "token " + std::to_string(id) + " missing from the shortlist");
+    check_hip(fill_u32(st.sl_row, uint32_t(row), size_t(st.b), ctx->stream), "fill");
+    check_hip(fill_u32(st.src_row, kNoRow, size_t(st.b), ctx->stream), "fill");
 }
 
 bool Model::fusable(int b, int m, int s) const {
@@ -471,9 +532,12 @@ void Model::step_fused(StaticState &st) {
     for (size_t i = 0; i < dec.size(); ++i) {
         const DecLayer &l = dec[i];
         if (i == 0) {
-            check_hip(step_qkv(l.qkv.w, l.qkv.b, B, d, &embed, st.ids, pos, uint32_t(cfg.pad_token_id + 1),
-                               embed_scale, nullptr, nullptr, cur, l.attn_norm.g, l.attn_norm.b, kLnEps, st.step,
-                               st.q, st.kc[i], st.vc[i], H, hd, st.m, s),
+            // src/model.rs:558-562: with a shortlist the input is a shortlist row or a source token
+            const SrcEmb src = st.sl ? SrcEmb{st.src_emb, st.src_row, st.s} : SrcEmb{};
+            check_hip(step_qkv(l.qkv.w, l.qkv.b, B, d, st.sl ? &st.sl->head : &embed, st.sl ? st.sl_row : st.ids,
+                               pos, uint32_t(cfg.pad_token_id + 1), embed_scale, nullptr, nullptr, cur,
+                               l.attn_norm.g, l.attn_norm.b, kLnEps, st.step, st.q, st.kc[i], st.vc[i], H, hd, st.m,
+                               s, src),
                       "step_qkv");
         } else {
             check_hip(step_qkv(l.qkv.w, l.qkv.b, B, d, nullptr, st.ids, pos, 0, 1.f, cur, st.y, nxt, l.attn_norm.g,
@@ -505,23 +569,35 @@ void Model::step_fused(StaticState &st) {
 
 void Model::lm_head(StaticState &st, bool greedy_mode, int mask_id) {
     hipStream_t s = ctx->stream;
-    const int B = st.b, d = cfg.d_model, V = cfg.vocab_size;
+    const int B = st.b, d = cfg.d_model;
     if (greedy_mode) {
+        // src/model.rs:597-610: the shortlist head (its rows masked by their vocabulary
+        // id) or the tied full head
+        const DevMatrix &head = st.sl ? st.sl->head : embed;
+        const int V = head.N, hmask = st.sl && mask_id >= 0 ? st.sl->row(uint32_t(mask_id)) : mask_id;
         int parts = 64;
-        if (B <= gemv_max_batch(embed)) {
-            check_hip(gemv_argmax(embed, st.h, d, B, mask_id, st.pv, st.pi, &parts, s), "lm_head");
-        } else if (gemm_rx_supported(embed, B)) {
-            check_hip(gemm_argmax(embed, st.h, d, B, mask_id, st.pv, st.pi, &parts, s), "lm_head");
+        if (B <= gemv_max_batch(head)) {
+            check_hip(gemv_argmax(head, st.h, d, B, hmask, st.pv, st.pi, &parts, s), "lm_head");
+        } else if (gemm_rx_supported(head, B)) {
+            check_hip(gemm_argmax(head, st.h, d, B, hmask, st.pv, st.pi, &parts, s), "lm_head");
         } else {
-            check_hip(gemm(embed, st.h, d, B, st.logits, V, nullptr, false, nullptr, 0, s, ctx->gemm_workspace(),
+            check_hip(gemm(head, st.h, d, B, st.logits, V, nullptr, false, nullptr, 0, s, ctx->gemm_workspace(),
                            kGemmWorkspaceBytes),
                       "lm_head");
-            check_hip(argmax_partial(st.logits, B, V, V, mask_id, st.pv, st.pi, parts, s), "argmax");
+            check_hip(argmax_partial(st.logits, B, V, V, hmask, st.pv, st.pi, parts, s), "argmax");
+        }
+        SlFinalize sl;
+        if (st.sl) {  // the source tokens: logits at candidate indices V + j (kernels/malaga.cu:229-243)
+            check_hip(source_logits(st.h, st.src_emb, st.src_ids, B, st.s, d, mask_id, V, st.spv, st.spi, s),
+                      "source_logits");
+            sl = SlFinalize{st.sl->d_ids, V, st.spv, st.spi, st.src_ids, st.s, st.sl_row, st.src_row};
         }
         check_hip(greedy_finalize(st.pv, st.pi, parts, B, st.finished, st.ids, st.out, st.m, st.step,
-                                  uint32_t(cfg.eos_token_id), uint32_t(cfg.pad_token_id), s),
+                                  uint32_t(cfg.eos_token_id), uint32_t(cfg.pad_token_id), s, sl),
                   "greedy_finalize");
     } else {
+        const int V = cfg.vocab_size;
+        if (st.sl) fail(ERR_UNSUPPORTED, "shortlist decoding is greedy only");
         if (B <= gemv_max_batch(embed))
             check_hip(gemv(embed, st.h, d, B, st.logits, V, nullptr, false, s), "lm_head");
         else
@@ -540,8 +616,10 @@ void Model::step(StaticState &st, bool greedy_mode, int mask_id) {
     }
     hipStream_t s = ctx->stream;
     const int B = st.b, d = cfg.d_model, H = cfg.decoder_heads, hd = d / H;
-    check_hip(embed_pos_ln(embed, st.ids, B, pos, st.step, uint32_t(cfg.pad_token_id + 1), embed_scale,
-                           dec[0].attn_norm.g, dec[0].attn_norm.b, kLnEps, st.x, st.h, s),
+    const SrcEmb src = st.sl ? SrcEmb{st.src_emb, st.src_row, st.s} : SrcEmb{};
+    check_hip(embed_pos_ln(st.sl ? st.sl->head : embed, st.sl ? st.sl_row : st.ids, B, pos, st.step,
+                           uint32_t(cfg.pad_token_id + 1), embed_scale, dec[0].attn_norm.g, dec[0].attn_norm.b,
+                           kLnEps, st.x, st.h, s, src),
               "embed_pos_ln");
     // x += y W^T + b; h = LayerNorm(x): register GEMV + residual_ln for small
     // batches, else the MFMA GEMM with the residual and LayerNorm in its reduction
@@ -622,20 +700,21 @@ void GraphCache::evict(const Entry *keep) {
 }
 
 std::vector<std::vector<uint32_t>> GraphCache::greedy(const Batch &src, uint32_t tgt_lang, int max_new,
-                                                      int sync_every, bool eos_mask, bool use_graph) {
+                                                      int sync_every, bool eos_mask, bool use_graph,
+                                                      const Shortlist *sl) {
     try {
-        return run(src, tgt_lang, max_new, sync_every, eos_mask, use_graph);
+        return run(src, tgt_lang, max_new, sync_every, eos_mask, use_graph, sl);
     } catch (const Failure &f) {
         // src/graph.rs:214-222: out of memory -> drop graphs for good, decode eagerly
         if (f.code != ERR_OOM || !capture_) throw;
         capture_ = false;
         clear();
-        return run(src, tgt_lang, max_new, sync_every, eos_mask, use_graph);
+        return run(src, tgt_lang, max_new, sync_every, eos_mask, use_graph, sl);
     }
 }
 
 std::vector<std::vector<uint32_t>> GraphCache::run(const Batch &src, uint32_t tgt_lang, int max_new, int sync_every,
-                                                   bool eos_mask, bool use_graph) {
+                                                   bool eos_mask, bool use_graph, const Shortlist *sl) {
     Model &m = *model_;
     hipStream_t s = m.ctx->stream;
     const ModelConfig &c = m.cfg;
@@ -646,13 +725,14 @@ std::vector<std::vector<uint32_t>> GraphCache::run(const Batch &src, uint32_t tg
     ++clock_;
     Entry *e = nullptr;
     for (auto &it : entries_)
-        if (it.b == kb && it.s == ks && it.m == km) e = &it;
+        if (it.b == kb && it.s == ks && it.m == km && it.sl == sl) e = &it;
     if (!e) {
         Entry ne;
         ne.b = kb;
         ne.s = ks;
         ne.m = km;
-        ne.st = m.new_state(kb, ks, km, false);
+        ne.sl = sl;
+        ne.st = m.new_state(kb, ks, km, false, false, sl);
         entries_.push_back(std::move(ne));
         e = &entries_.back();
         evict(e);
@@ -674,6 +754,7 @@ std::vector<std::vector<uint32_t>> GraphCache::run(const Batch &src, uint32_t tg
     m.reset_state(st, src, rows, uint32_t(c.decoder_start_token_id));
     one_step();
     check_hip(fill_u32(st.ids, tgt_lang, size_t(st.b), s), "fill");
+    if (sl) m.set_shortlist_input(st, tgt_lang);
     std::vector<uint8_t> fin(static_cast<size_t>(st.b));
     for (int r = 0; r < st.b; ++r) fin[r] = r >= n;
     h2d(st.finished, fin, s);
@@ -925,10 +1006,14 @@ std::vector<std::vector<uint32_t>> generate_to(Model &m, const std::vector<std::
     if (src.empty()) return {};
     int max_new = 1;
     for (auto &r : src) max_new = std::max(max_new, budget(m.cfg, int(r.size()), o.max_new_tokens));
+    // src/translator.rs:184-194: the shortlist serves greedy graph decoding when it holds
+    // both forced start tokens
+    const Shortlist *sl = o.shortlist.empty() || o.beam_size > 1 || !o.fused ? nullptr : m.shortlist(o.shortlist);
+    if (sl && !(sl->contains(uint32_t(m.cfg.decoder_start_token_id)) && sl->contains(tgt_lang))) sl = nullptr;
     auto batch = m.encode(src);
     std::vector<std::vector<uint32_t>> out;
     if (o.beam_size <= 1)
-        out = m.graphs.greedy(*batch, tgt_lang, max_new, std::max(1, o.sync_every), o.eos_mask, o.fused);
+        out = m.graphs.greedy(*batch, tgt_lang, max_new, std::max(1, o.sync_every), o.eos_mask, o.fused, sl);
     else
         out = m.beam(*batch, tgt_lang, max_new, o.beam_size, o.length_penalty, o.eos_mask, o.fused);
     for (size_t i = 0; i < src.size(); ++i) {

@@ -5,6 +5,7 @@
 #include <hip/hip_fp16.h>
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cstdint>
 #include <list>
 #include <memory>
@@ -60,10 +61,26 @@ struct DecLayer {
     Linear qkv, out, cross_q, cross_kv, cross_out, up, down;
 };
 
+// Reduced LM head of one target language (src/model.rs:229-250): rows of token_embd
+// for the sorted vocabulary ids `ids`, stored as lm_head.{code}.weight.
+struct Shortlist {
+    std::string code;
+    DevMatrix head;
+    std::vector<uint32_t> ids;  // sorted
+    uint32_t *d_ids = nullptr;  // same ids on the device
+    // Row of `head` holding vocabulary id `id`, or -1.
+    int row(uint32_t id) const {
+        auto it = std::lower_bound(ids.begin(), ids.end(), id);
+        return it != ids.end() && *it == id ? int(it - ids.begin()) : -1;
+    }
+    bool contains(uint32_t id) const { return row(id) >= 0; }
+};
+
 // Encoded sources: per decoder layer cross K/V [b][H][s][hd] f16 (src/model.rs:463-477).
 struct Batch {
     int b = 0, s = 0;
     std::vector<uint32_t> lens;
+    std::vector<uint32_t> ids;     // [b][s] source ids, right-padded with pad
     std::vector<__half *> ck, cv;  // per decoder layer, inside `block`
     void *block = nullptr;         // one allocation for every layer's cross K/V
     ~Batch();
@@ -81,6 +98,15 @@ struct StaticState {
     float *part = nullptr;                // attention partial sums [parts][b][d] (fused step)
     uint32_t *rows = nullptr;             // beam: [b][m] cache row holding slot j of row r (null: r)
     uint32_t *row_src = nullptr;          // [b] source row of each state row (reset_state)
+    // shortlist decoding (src/graph.rs:40-48): candidates are the shortlist rows and the
+    // source tokens; the next input embedding is shortlist row sl_row[r] or, where
+    // src_row[r] != kNoRow, source position src_row[r] of src_emb.
+    const Shortlist *sl = nullptr;
+    uint32_t *src_ids = nullptr;          // [b][s] pad beyond each row's length
+    float *src_emb = nullptr;             // [b][s][d] token_embd rows of src_ids
+    uint32_t *sl_row = nullptr, *src_row = nullptr;
+    float *spv = nullptr;                 // [b][s] source-token logits
+    uint32_t *spi = nullptr;              // [b][s] their candidate indices
     bool fused = false;                   // decoder step uses the fused kernels of k_step.hip
     float *logits = nullptr, *pv = nullptr;
     uint32_t *pi = nullptr;
@@ -100,21 +126,23 @@ class GraphCache {
     bool capture_enabled() const { return capture_; }
     void clear();
     // Greedy decoding of an encoded batch; rows stripped at EOS (src/graph.rs:204-298).
+    // sl: decode over the shortlist + source tokens (src/graph.rs:204-298 with a shortlist).
     std::vector<std::vector<uint32_t>> greedy(const Batch &src, uint32_t tgt_lang, int max_new, int sync_every,
-                                              bool eos_mask, bool use_graph);
+                                              bool eos_mask, bool use_graph, const Shortlist *sl = nullptr);
     size_t entries() const { return entries_.size(); }
     size_t graphs() const;
 
   private:
     struct Entry {
         int b, s, m;
+        const Shortlist *sl = nullptr;  // part of the key (src/graph.rs:157)
         std::unique_ptr<StaticState> st;
         hipGraphExec_t exec = nullptr;
         uint64_t last_used = 0;
         size_t bytes() const;
     };
     std::vector<std::vector<uint32_t>> run(const Batch &src, uint32_t tgt_lang, int max_new, int sync_every,
-                                           bool eos_mask, bool use_graph);
+                                           bool eos_mask, bool use_graph, const Shortlist *sl);
     void evict(const Entry *keep);
     Model *model_;
     std::list<Entry> entries_;
@@ -141,19 +169,26 @@ class Model {
     std::vector<EncLayer> enc;
     std::vector<DecLayer> dec;
     LNorm enc_norm, dec_norm;
+    std::vector<std::unique_ptr<Shortlist>> shortlists;  // src/model.rs:403-412
     size_t weight_bytes = 0;
     GraphCache graphs;
 
     // src/model.rs:463-500 (encoder + cross K/V of every decoder layer)
     std::unique_ptr<Batch> encode(const std::vector<std::vector<uint32_t>> &src);
-    // logits: keep a [b][V] logits buffer; row_map: beam-search cache-row map (rows).
-    std::unique_ptr<StaticState> new_state(int b, int s, int m, bool logits, bool row_map = false);
+    // Shortlist of a target-language code, or null (src/model.rs:439-442).
+    const Shortlist *shortlist(const std::string &code) const;
+    // logits: keep a [b][V] logits buffer; row_map: beam-search cache-row map (rows);
+    // sl: buffers of shortlist decoding (greedy only).
+    std::unique_ptr<StaticState> new_state(int b, int s, int m, bool logits, bool row_map = false,
+                                           const Shortlist *sl = nullptr);
     // src/model.rs:552-612: one decoder step on fixed buffers.  greedy: argmax +
     // bookkeeping, else logits into st.logits and ++step.
     void step(StaticState &st, bool greedy, int mask_id);
     // Whether the fused step kernels cover a state of b rows with caches of m / s slots.
     bool fusable(int b, int m, int s) const;
     void reset_state(StaticState &st, const Batch &src, const std::vector<uint32_t> &row_of, uint32_t start);
+    // Shortlist state: every row's next input embedding is the shortlist row of `id`.
+    void set_shortlist_input(StaticState &st, uint32_t id);
     // src/translator.rs:250-335.  use_graph: replay one captured step + top-k per
     // beam step (off when capture is disabled for the cache).
     std::vector<std::vector<uint32_t>> beam(const Batch &src, uint32_t tgt_lang, int max_new, int k, float lp,
@@ -187,6 +222,7 @@ struct GenOptions {
     int max_batch = 32;
     bool fused = true;
     bool eos_mask = false;  // benchmark-only: fixed output lengths
+    std::string shortlist;  // target-language code whose shortlist greedy decoding uses ("" = off)
 };
 
 // src/translator.rs:136-207 on token ids: sort by length, batch, per-row budget,

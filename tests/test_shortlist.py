@@ -66,17 +66,20 @@ def _stepwise(m, src_row, tgt, shortlist, max_new, eos):
     return out[: out.index(eos)] if eos in out else out
 
 
+SL_IDS = sorted(set(np.random.default_rng(3).integers(4, 1000, 300).tolist()) - {76, 258, 607, 884, 738, 182, 267, 931})
+
+
 def shortlist_fixture(path, preset):
     """d = 256 model whose greedy output varies (unscaled embeddings, std 0.2), with a
     shortlist that leaves out the tokens the full model prefers: those can then only be
-    produced as copies of source tokens."""
+    produced as copies of source tokens.  A second shortlist, "eng_Latn" (language id
+    997), lacks token 998 and so cannot serve decoding into 998."""
     from conftest import KQ_CONFIG
 
-    rng = np.random.default_rng(3)
-    ids = sorted(set(rng.integers(4, 1000, 300).tolist()) - {76, 258, 607, 884, 738, 182, 267, 931})
     if not path.exists():
         M.write_synthetic(path, dict(KQ_CONFIG, scale_embedding=0), preset, M.INIT_NORMAL_RICH, seed=11, std=0.2,
-                          name="kq-sl", shortlists={"fra_Latn": (998, ids)})
+                          name="kq-sl", shortlists={"fra_Latn": (998, SL_IDS),
+                                                    "eng_Latn": (997, [t for t in SL_IDS if t != 998])})
     return path, read_gguf(path)[1]["nllb.shortlist.fra_Latn"]
 
 
