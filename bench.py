@@ -10,6 +10,9 @@ Also reported on the same JSON line:
     (21 source ids -> 18 tokens, crates/malaga/src/main.rs:409-436);
   * config 4: greedy batch 32 (lognormal lengths, length-sorted) and beam 4 at
     batch 8, sentences/s;
+  * ``fast_vocab``: shortlist (--fast-vocab) decoding beside exact decoding on the
+    reference's bench shapes (bs1 21 -> 18, and batch 16), with a seeded random
+    37k-id shortlist stored in the q4_k_m model;
   * config 2: dequant-GEMV GB/s (q4_K, q8_0; four shapes) over rotating weight
     copies (> 2x the 256 MB Infinity Cache), LayerNorm and argmax latency;
   * ``roofline`` of the dominant kernel (the fused LM-head GEMV + argmax, q6_K
@@ -36,6 +39,8 @@ sys.path.insert(0, str(ROOT))
 
 PEAK_HBM_GBS = 8000.0
 TGT_LANG = 256100  # any id < vocab: the forced target-language token
+SL_CODE = "plt_Latn"  # the q4_k_m bench model's shortlist (--fast-vocab), language id TGT_LANG
+SL_ROWS = 37000  # the reference's Malagasy shortlist keeps ~37k of 256k tokens
 
 
 def log(msg: str) -> None:
@@ -47,11 +52,15 @@ def model_path(preset: str) -> Path:
 
     d = Path(os.environ.get("MALAGA_MODEL_DIR", "/tmp/malaga_bench_models"))
     d.mkdir(parents=True, exist_ok=True)
-    p = d / f"nllb600m-random-s0-{preset}.gguf"
+    # q4_k_m also carries a seeded random shortlist of SL_ROWS ids (lm_head.plt_Latn): it
+    # is read only when a run asks for --fast-vocab decoding
+    sl = {SL_CODE: (TGT_LANG, np.random.default_rng(9).choice(np.arange(4, 256206), SL_ROWS, replace=False)
+                    .tolist())} if preset == "q4_k_m" else None
+    p = d / f"nllb600m-random-s0-{preset}{'-sl' if sl else ''}.gguf"
     if not p.exists():
         t = time.time()
         M.write_synthetic(p, M.nllb_600m_config(), preset, M.INIT_NORMAL, seed=0, std=0.02,
-                          name="nllb-200-distilled-600M (random init, seed 0)")
+                          name="nllb-200-distilled-600M (random init, seed 0)", shortlists=sl)
         log(f"wrote {p.name} ({p.stat().st_size / 1e6:.0f} MB) in {time.time() - t:.1f} s")
     return p
 
@@ -211,6 +220,40 @@ def bench_batched(T):
     return res
 
 
+def bench_fast_vocab(T):
+    """--fast-vocab (shortlist) decoding next to exact decoding on the reference's bench
+    shapes: one sentence of 21 ids -> 18 tokens, and 16 such sentences in one batch
+    (crates/malaga/src/main.rs:409-450), EOS masked so both modes emit the same counts."""
+    import torch
+    import malaga_amd as M
+
+    res = {}
+    one = sources(60, 21, seed=5000)
+    batch = sources(16, 21, seed=6000)
+    for mode, code in (("exact", None), ("fast_vocab", SL_CODE)):
+        opts = M.GenOptions(max_new_tokens=18, eos_mask=True, shortlist=code)
+        for s in one[:5]:
+            T.generate([s], TGT_LANG, opts)
+        lat = []
+        for s in one[10:]:
+            a = time.perf_counter()
+            T.generate([s], TGT_LANG, opts)
+            lat.append((time.perf_counter() - a) * 1e3)
+        T.generate(batch, TGT_LANG, opts)
+        torch.cuda.synchronize()
+        times = []
+        for _ in range(5):
+            a = time.perf_counter()
+            T.generate(batch, TGT_LANG, opts)
+            torch.cuda.synchronize()
+            times.append(time.perf_counter() - a)
+        res[mode] = dict(bs1_p50_ms=float(np.median(lat)), bs16_sentences_per_s=16 / float(np.median(times)))
+    res["shortlist_rows"] = T.shortlists().get(SL_CODE)
+    res["published_rtx4090"] = {"exact": {"bs1_p50_ms": 16.4, "bs16_sentences_per_s": 363},
+                                "fast_vocab": {"bs1_p50_ms": 12.5, "bs16_sentences_per_s": 433}}
+    return res
+
+
 class GemvBench:
     """Times one kernel-level entry point over rotating device copies of a weight matrix."""
 
@@ -354,8 +397,8 @@ def main():
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--skip-cpu", action="store_true")
-    ap.add_argument("--legs", default="bs1,batched,kernels,cpu",
-                    help="comma-separated subset of bs1,batched,kernels,cpu (profiling runs); "
+    ap.add_argument("--legs", default="bs1,batched,fastvocab,kernels,cpu",
+                    help="comma-separated subset of bs1,batched,fastvocab,kernels,cpu (profiling runs); "
                          "'config5' alone runs only the 3.3B batch-64 leg, 'mfma' alone the short "
                          "MFMA-GEMM runs used for counter collection")
     ap.add_argument("--roofline-only", action="store_true", help="only the LM-head roofline leg (for rocprof)")
@@ -413,6 +456,11 @@ def main():
     batched = bench_batched(T) if "batched" in legs else {"greedy_bs32": {"sentences_per_s": float("nan")}}
     for k, v in batched.items():
         log(f"{k}: {v['sentences_per_s']:.1f} sentences/s ({v.get('ms_per_batch', 0):.1f} ms/batch)")
+    fast = bench_fast_vocab(T) if "fastvocab" in legs else None
+    if fast:
+        for k in ("exact", "fast_vocab"):
+            log(f"{k} (21 ids -> 18 tokens): bs1 p50 {fast[k]['bs1_p50_ms']:.2f} ms, bs16 "
+                f"{fast[k]['bs16_sentences_per_s']:.1f} sentences/s")
     if "kernels" not in legs:
         print(json.dumps({"p50_ms": b1["p50"], "batched": batched}))
         return
@@ -462,6 +510,7 @@ def main():
                             "published_rtx4090_ms": 16.4, "published_rtx4090_ms_per_token": 0.78},
         "sentences_per_s_bs32": round(batched["greedy_bs32"]["sentences_per_s"], 2),
         "batched": batched,
+        "fast_vocab": fast,
         "gemv_HBM_GBps_q4K_lm_head": round(q4_lm["GBps"], 1),
         "gemv": [{k: (round(v, 3) if isinstance(v, float) else v) for k, v in r.items()} for r in gemv_rows],
         "small_kernels_us": {k: round(v, 3) for k, v in small.items()},
