@@ -154,11 +154,13 @@ GemvArgs make_args(const DevMatrix &w, const GemvGeom &g, const float *x, int ld
 
 constexpr int kGemvSmallRows = 65536;
 
-// The LM head streams its first 30% of rows with cached loads and the rest
-// non-temporally: with the layer weights (112 MB for 600M q4_k_m) that part stays
-// in the 256 MB MALL from step to step, while an all-cached head would evict the
-// layers.  Measured on 600M q4_k_m batch-1 decode: 0.3 beats 0, 0.2, 0.45 and 1.
-constexpr double kLmHeadCachedFrac = 0.3;
+// The LM head streams its first kLmHeadCachedBytes of rows with cached loads and the
+// rest non-temporally: with the layer weights (112 MB for 600M q4_k_m) that part
+// stays in the 256 MB MALL from step to step, while an all-cached 215 MB head would
+// evict the layers.  Measured on 600M q4_k_m batch-1 decode, as a fraction of that
+// head: 0.3 (64 MB) beats 0, 0.2, 0.45 and 1.  A smaller head (a 37k-row shortlist
+// is 31 MB) is cached whole.
+constexpr size_t kLmHeadCachedBytes = 64000000;
 
 }  // namespace
 
@@ -219,7 +221,8 @@ hipError_t gemv_argmax(const DevMatrix &w, const float *x, int ldx, int b, int m
     a.mask_id = mask_id;
     const int grid = gemv_grid(w, 1);
     *parts = grid;
-    a.nt_from = int(kLmHeadCachedFrac * w.N);
+    const size_t row_bytes = w.bytes / size_t(w.N);
+    a.nt_from = row_bytes ? int(std::min<size_t>(size_t(w.N), kLmHeadCachedBytes / row_bytes)) : w.N;
     return dispatch<1>(w.type, a, gemv_round_b(b), cpl, grid, st);
 }
 

@@ -156,7 +156,8 @@ float *Model::upload_f32(GgufFile &g, const std::string &name, int64_t n) {
     return d;
 }
 
-DevMatrix Model::upload_matrix(GgufFile &g, const std::string &name, int n, int k) {
+namespace {
+const GgufTensorInfo *matrix_info(GgufFile &g, const std::string &name, int n, int k) {
     const GgufTensorInfo *t = g.tensor(name);
     if (!t) fail(ERR_FORMAT, "missing tensor " + name);
     if (t->ne.size() != 2 || int64_t(t->ne[0]) != k || int64_t(t->ne[1]) != n)
@@ -164,6 +165,13 @@ DevMatrix Model::upload_matrix(GgufFile &g, const std::string &name, int n, int 
     TypeInfo ti;
     if (!type_info(t->type, &ti) || t->type == GGML_BF16)
         fail(ERR_UNSUPPORTED, "tensor " + name + ": unsupported type " + std::to_string(t->type));
+    if (k % ti.block_elems) fail(ERR_FORMAT, "tensor " + name + ": row length not a whole number of blocks");
+    return t;
+}
+}  // namespace
+
+DevMatrix Model::upload_matrix(GgufFile &g, const std::string &name, int n, int k) {
+    const GgufTensorInfo *t = matrix_info(g, name, n, k);
     DevMatrix m;
     m.type = t->type;
     m.N = n;
@@ -233,7 +241,20 @@ void Model::load(const std::string &path) {
     if ((d / cfg.decoder_heads) % 8 || (d / cfg.encoder_heads) % 8)
         fail(ERR_UNSUPPORTED, "head dimension must be a multiple of 8");
 
-    embed = upload_matrix(g, "token_embd.weight", cfg.vocab_size, d);
+    // src/model.rs:416-420: MALAGA_LAZY_EMBEDDINGS (set, any value) defers the full table
+    // when the file has a shortlist
+    bool has_sl = false;
+    for (const auto &kv : g.metadata()) has_sl |= kv.first.compare(0, 15, "nllb.shortlist.") == 0;
+    if (has_sl && std::getenv("MALAGA_LAZY_EMBEDDINGS")) {
+        const GgufTensorInfo *t = matrix_info(g, "token_embd.weight", cfg.vocab_size, d);
+        embed.type = t->type;
+        embed.N = cfg.vocab_size;
+        embed.K = d;
+        embed.bytes = planes_bytes(t->type, cfg.vocab_size, d);
+        embed_host_.assign(g.tensor_data(*t), g.tensor_data(*t) + embed.bytes);
+    } else {
+        embed = upload_matrix(g, "token_embd.weight", cfg.vocab_size, d);
+    }
     // src/model.rs:324-340: [sin | cos] in f64, row pad zeroed
     n_pos = cfg.max_position_embeddings + cfg.pad_token_id + 1;
     std::vector<float> table(static_cast<size_t>(n_pos) * d, 0.f);
@@ -306,6 +327,44 @@ void Model::load(const std::string &path) {
     check_hip(hipDeviceSynchronize(), "model upload");
 }
 
+void Model::ensure_embed() {
+    if (embed.q) return;
+    std::vector<uint8_t> host(embed.bytes);
+    size_t off_s, off_d, total;
+    if (!layout_planes(embed.type, embed.N, embed.K, embed_host_.data(), host.data(), &off_s, &off_d, &total))
+        fail(ERR_FORMAT, "token_embd.weight: bad layout");
+    // the OOM message carries src/model.rs:282-285's hint
+    uint8_t *d = static_cast<uint8_t *>(
+        dev_alloc(total, "full-vocabulary LM head (token_embd); free some VRAM or decode to a language with a "
+                         "shortlist"));
+    owned_.push_back(d);
+    check_hip(hipMemcpy(d, host.data(), total, hipMemcpyHostToDevice), "upload");
+    embed.q = d;
+    embed.s = d + off_s;
+    embed.d = d + off_d;
+    weight_bytes += total;
+    embed_host_.clear();
+    embed_host_.shrink_to_fit();
+}
+
+DevMatrix Model::gather_embed(const uint32_t *ids, int n, uint8_t *buf) {
+    const size_t rb = size_t(type_bytes(embed.type, embed.K));
+    std::vector<uint8_t> rows(rb * size_t(n)), planes(planes_bytes(embed.type, n, embed.K));
+    for (int i = 0; i < n; ++i) std::memcpy(rows.data() + rb * i, embed_host_.data() + rb * ids[i], rb);
+    DevMatrix m;
+    m.type = embed.type;
+    m.N = n;
+    m.K = embed.K;
+    size_t off_s, off_d;
+    if (!layout_planes(embed.type, n, embed.K, rows.data(), planes.data(), &off_s, &off_d, &m.bytes))
+        fail(ERR_FORMAT, "token_embd.weight: bad layout");
+    h2d(buf, planes, ctx->stream);
+    m.q = buf;
+    m.s = buf + off_s;
+    m.d = buf + off_d;
+    return m;
+}
+
 const Shortlist *Model::shortlist(const std::string &code) const {
     for (const auto &sl : shortlists)
         if (sl->code == code) return sl.get();
@@ -351,7 +410,9 @@ std::unique_ptr<Batch> Model::encode(const std::vector<std::vector<uint32_t>> &s
     const size_t n_act = (size_t(M) * d * 4 + 255) & ~size_t(255);
     const size_t n_qkv = (size_t(M) * std::max(3 * d, f) * 4 + 255) & ~size_t(255);
     const size_t n_kv = (size_t(M) * 2 * d * 4 + 255) & ~size_t(255);
-    const size_t need = 2 * n_ids + n_lens + 3 * n_act + n_qkv + n_kv;
+    // lazy embeddings: the batch's token_embd rows, gathered on the host (src/model.rs:269-273)
+    const size_t n_rows = embed.q ? 0 : (planes_bytes(embed.type, M, d) + 255) & ~size_t(255);
+    const size_t need = 2 * n_ids + n_lens + 3 * n_act + n_qkv + n_kv + n_rows;
     if (enc_ws_bytes_ < need) {
         check_hip(hipStreamSynchronize(st), "encode");  // a previous call may still use it
         dev_free(enc_ws_);
@@ -372,11 +433,19 @@ std::unique_ptr<Batch> Model::encode(const std::vector<std::vector<uint32_t>> &s
     float *att = static_cast<float *>(carve(n_act));
     float *qkv = static_cast<float *>(carve(n_qkv));
     float *kv = static_cast<float *>(carve(n_kv));
-    h2d(d_ids, ids, st);
     h2d(d_pidx, pidx, st);
     out->ids = ids;
     h2d(d_lens, out->lens, st);
-    check_hip(embed_pos_rows(embed, d_ids, d_pidx, M, pos, embed_scale, x, st), "embed");
+    if (embed.q) {
+        h2d(d_ids, ids, st);
+        check_hip(embed_pos_rows(embed, d_ids, d_pidx, M, pos, embed_scale, x, st), "embed");
+    } else {
+        const DevMatrix rows = gather_embed(ids.data(), M, static_cast<uint8_t *>(carve(n_rows)));
+        std::vector<uint32_t> iota(static_cast<size_t>(M));
+        std::iota(iota.begin(), iota.end(), 0u);
+        h2d(d_ids, iota, st);
+        check_hip(embed_pos_rows(rows, d_ids, d_pidx, M, pos, embed_scale, x, st), "embed");
+    }
     for (auto &l : enc) {
         check_hip(layernorm(x, M, d, l.attn_norm.g, l.attn_norm.b, kLnEps, h, st), "layernorm");
         matmul(l.qkv, h, M, qkv, false, nullptr);
@@ -453,6 +522,13 @@ std::unique_ptr<StaticState> Model::new_state(int b, int s, int m, bool logits, 
         st->src_row = static_cast<uint32_t *>(get(size_t(b) * 4, "source positions"));
         st->spv = static_cast<float *>(get(size_t(b) * s * 4, "source logits"));
         st->spi = static_cast<uint32_t *>(get(size_t(b) * s * 4, "source logits"));
+        if (!embed.q) {
+            st->src_q = static_cast<uint8_t *>(get(planes_bytes(embed.type, b * s, d), "source rows"));
+            st->src_iota = static_cast<uint32_t *>(get(size_t(b) * s * 4, "source rows"));
+            std::vector<uint32_t> iota(size_t(b) * s);
+            std::iota(iota.begin(), iota.end(), 0u);
+            h2d(st->src_iota, iota, ctx->stream);
+        }
     }
     if (row_map) {  // identity until a beam reorder rewrites it
         st->rows = static_cast<uint32_t *>(get(size_t(b) * m * 4, "beam cache rows"));
@@ -495,7 +571,13 @@ void Model::reset_state(StaticState &st, const Batch &src, const std::vector<uin
         for (int r = 0; r < n; ++r)
             std::copy_n(src.ids.begin() + size_t(row_of[r]) * src.s, src.s, ids.begin() + size_t(r) * st.s);
         h2d(st.src_ids, ids, s);
-        check_hip(embed_rows(embed, st.src_ids, st.b * st.s, st.src_emb, s), "embed_rows");
+        if (embed.q) {
+            check_hip(embed_rows(embed, st.src_ids, st.b * st.s, st.src_emb, s), "embed_rows");
+        } else {
+            if (!st.src_q) fail(ERR_INVALID, "reset_state: state without source row buffers");
+            const DevMatrix rows = gather_embed(ids.data(), st.b * st.s, st.src_q);
+            check_hip(embed_rows(rows, st.src_iota, st.b * st.s, st.src_emb, s), "embed_rows");
+        }
         set_shortlist_input(st, start);
     }
     std::vector<uint8_t> fin(static_cast<size_t>(st.b));
@@ -716,6 +798,7 @@ std::vector<std::vector<uint32_t>> GraphCache::greedy(const Batch &src, uint32_t
 std::vector<std::vector<uint32_t>> GraphCache::run(const Batch &src, uint32_t tgt_lang, int max_new, int sync_every,
                                                    bool eos_mask, bool use_graph, const Shortlist *sl) {
     Model &m = *model_;
+    if (!sl) m.ensure_embed();  // the full LM head and input embeddings
     hipStream_t s = m.ctx->stream;
     const ModelConfig &c = m.cfg;
     const bool capture = capture_ && use_graph;
@@ -827,6 +910,7 @@ std::vector<std::vector<uint32_t>> GraphCache::run(const Batch &src, uint32_t tg
 
 std::vector<std::vector<uint32_t>> Model::beam(const Batch &src, uint32_t tgt_lang, int max_new, int k, float lp,
                                                bool eos_mask, bool use_graph) {
+    ensure_embed();
     hipStream_t s = ctx->stream;
     const int b = src.b, bk = b * k, V = cfg.vocab_size;
     const uint32_t eos = uint32_t(cfg.eos_token_id);
@@ -974,6 +1058,7 @@ std::vector<std::vector<uint32_t>> Model::beam(const Batch &src, uint32_t tgt_la
 }
 
 std::vector<float> Model::teacher_forced(const Batch &src, const std::vector<uint32_t> &tgt, int T) {
+    ensure_embed();
     hipStream_t s = ctx->stream;
     const int b = src.b, V = cfg.vocab_size;
     if (T < 1 || int(tgt.size()) != b * T) fail(ERR_INVALID, "teacher_forced: bad target shape");

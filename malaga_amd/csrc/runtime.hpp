@@ -107,6 +107,8 @@ struct StaticState {
     uint32_t *sl_row = nullptr, *src_row = nullptr;
     float *spv = nullptr;                 // [b][s] source-token logits
     uint32_t *spi = nullptr;              // [b][s] their candidate indices
+    uint8_t *src_q = nullptr;             // lazy embeddings: token_embd rows of src_ids (device layout)
+    uint32_t *src_iota = nullptr;         // lazy embeddings: 0 .. b*s-1
     bool fused = false;                   // decoder step uses the fused kernels of k_step.hip
     float *logits = nullptr, *pv = nullptr;
     uint32_t *pi = nullptr;
@@ -162,7 +164,7 @@ class Model {
 
     Context *ctx;
     ModelConfig cfg;
-    DevMatrix embed;  // token_embd, also the tied LM head
+    DevMatrix embed;  // token_embd, also the tied LM head (q == nullptr: still on the host, see ensure_embed)
     float *pos = nullptr;
     int n_pos = 0;
     float embed_scale = 1.f;
@@ -177,6 +179,11 @@ class Model {
     std::unique_ptr<Batch> encode(const std::vector<std::vector<uint32_t>> &src);
     // Shortlist of a target-language code, or null (src/model.rs:439-442).
     const Shortlist *shortlist(const std::string &code) const;
+    // Embedding::on_device (src/model.rs:275-305): with MALAGA_LAZY_EMBEDDINGS set and a
+    // shortlist in the file, token_embd stays on the host until exact decoding needs the
+    // full LM head; this uploads it (once).  Never called inside a graph capture.
+    void ensure_embed();
+    bool embed_resident() const { return embed.q != nullptr; }
     // logits: keep a [b][V] logits buffer; row_map: beam-search cache-row map (rows);
     // sl: buffers of shortlist decoding (greedy only).
     std::unique_ptr<StaticState> new_state(int b, int s, int m, bool logits, bool row_map = false,
@@ -198,6 +205,9 @@ class Model {
 
   private:
     std::vector<void *> owned_;
+    std::vector<uint8_t> embed_host_;  // token_embd GGUF rows while not resident
+    // token_embd rows of host ids as an n-row device matrix in buf (planes_bytes(type, n, d))
+    DevMatrix gather_embed(const uint32_t *ids, int n, uint8_t *buf);
     // Encoder scratch (ids, activations): grow-only, reused by every encode call, so a
     // call allocates only the cross K/V it returns.
     void *enc_ws_ = nullptr;

@@ -96,3 +96,29 @@ def test_shortlist_selection_rules(sl_models):
         gpu.greedy(b, FRA, 4, shortlist="xxx_Latn")
     with pytest.raises(MalagaError):  # token 998 missing from the eng_Latn shortlist
         gpu.greedy(b, FRA, 4, shortlist="eng_Latn")
+
+
+def test_lazy_embeddings(sl_models, model_dir, monkeypatch):
+    """MALAGA_LAZY_EMBEDDINGS (src/model.rs:252-307, 416-420): token_embd stays on the host
+    while shortlist decoding runs (encoder and source rows gathered from the host copy)
+    and is uploaded once when exact decoding needs the full LM head."""
+    from malaga_amd.gguf import tensor_bytes
+
+    eager, orc, sl = sl_models("q4_k_m")
+    p = model_dir / "kq-sl-q4_k_m.gguf"
+    monkeypatch.setenv("MALAGA_LAZY_EMBEDDINGS", "1")
+    lazy = M.Translator.load(p)
+    monkeypatch.delenv("MALAGA_LAZY_EMBEDDINGS")
+    emb_bytes = tensor_bytes(p, "token_embd.weight")[0].size
+    assert lazy.weight_bytes == eager.weight_bytes - emb_bytes
+    for nb in (4, 7):
+        src = _sources(nb, 70 + nb)
+        want, _ = orc.translate_batch(src, FRA, kv_f16=True, max_new_tokens=10, shortlist=sl)
+        assert lazy.generate(src, FRA, M.GenOptions(max_new_tokens=10, shortlist="fra_Latn")) == want
+    assert lazy.weight_bytes == eager.weight_bytes - emb_bytes
+    exact, _ = orc.translate_batch(SL_SOURCES, FRA, kv_f16=True, max_new_tokens=10)
+    assert lazy.generate(SL_SOURCES, FRA, M.GenOptions(max_new_tokens=10)) == exact
+    assert lazy.weight_bytes == eager.weight_bytes
+    want, _ = orc.translate_batch(SL_SOURCES, FRA, kv_f16=True, max_new_tokens=10, shortlist=sl)
+    assert lazy.generate(SL_SOURCES, FRA, M.GenOptions(max_new_tokens=10, shortlist="fra_Latn")) == want
+    lazy.close()
