@@ -154,6 +154,32 @@ int mlg_greedy_sl(mlg_model *m, const mlg_batch *b, uint32_t tgt_lang, const cha
    once and replayed per step (MLG_FLAG_NO_GRAPH: eager); MLG_FLAG_EOS_MASK as for mlg_greedy. */
 int mlg_beam(mlg_model *m, const mlg_batch *b, uint32_t tgt_lang, int max_new, int beam_size, float length_penalty,
              uint32_t flags, uint32_t *out, int out_cap, int *out_len);
+/* ---- dynamic batching caller (crates/malaga/src/server.rs:74-112) ----
+   One inference thread per server owns the model.  Jobs submitted from any thread are
+   queued; the thread takes every queued job, groups those with the same (src_lang,
+   tgt_lang, beam_size, shortlist) in order of first arrival (server.rs:83-90) and decodes
+   each group as one mlg_generate call with the server's options (server.rs:93-112), so
+   requests that arrive while the GPU is busy share the next batch.  The model must
+   outlive the server; other calls on the same model wait for the running group. */
+typedef struct mlg_server mlg_server;
+typedef struct mlg_job mlg_job;
+int mlg_server_start(mlg_model *m, const mlg_gen_options *defaults, mlg_server **out);
+/* Finishes every queued job, then stops the thread. */
+void mlg_server_stop(mlg_server *s);
+/* n sentences (as mlg_generate); beam_size <= 0 = the server's, clamped to 1..8
+   (server.rs:64); shortlist: language code or NULL (GenOptions::shortlist).  Bad ids,
+   empty rows or a stopped server: MLG_ERR_INVALID at submission. */
+int mlg_server_submit(mlg_server *s, const uint32_t *ids, const uint32_t *lens, int n, uint32_t src_lang,
+                      uint32_t tgt_lang, int beam_size, const char *shortlist, mlg_job **out);
+/* *done = 1 once the job has its result; timeout_ms < 0 waits without limit. */
+int mlg_job_wait(mlg_job *j, int timeout_ms, int *done);
+/* Waits for the job, then returns its status (the group's error, if any, with its
+   message in mlg_last_error) and its rows as mlg_generate does. */
+int mlg_job_result(mlg_job *j, uint32_t *out, int out_cap, int *out_len);
+void mlg_job_free(mlg_job *j);
+/* Jobs and sentences decoded, groups run, largest group in sentences. */
+int mlg_server_stats(const mlg_server *s, int64_t *jobs, int64_t *groups, int64_t *sentences, int64_t *largest_group);
+
 /* GraphCache::clear (src/graph.rs:192-200). */
 void mlg_clear_graphs(mlg_model *m);
 int mlg_graph_stats(const mlg_model *m, int *entries, int *graphs, int *capture_enabled);

@@ -27,7 +27,7 @@ import numpy as np
 from ._lib import (FLAG_EOS_MASK, FLAG_NO_GRAPH, INIT_NORMAL, INIT_NORMAL_RICH, INIT_TESTUTIL, PRESETS, TENSOR_FN,
                    CGenOptions, Config, MalagaError, check, load)
 
-__all__ = ["GenOptions", "Translator", "Config", "MalagaError", "convert", "write_synthetic", "tiny_config",
+__all__ = ["GenOptions", "Translator", "Server", "Job", "Config", "MalagaError", "convert", "write_synthetic", "tiny_config",
            "nllb_600m_config", "nllb_3b_config", "quantize", "dequantize", "type_bytes", "bucket",
            "INIT_TESTUTIL", "INIT_NORMAL", "INIT_NORMAL_RICH", "PRESETS"]
 
@@ -208,6 +208,65 @@ class Translator:
 
 
 # ----------------------------------------------------------------- configs
+
+class Job:
+    """One request queued on a Server (crates/malaga/src/server.rs:33-39)."""
+
+    def __init__(self, server: "Server", h, n: int, cap: int):
+        self.lib, self.h, self.n, self.cap, self._server = server.lib, h, n, cap, server
+
+    def done(self, timeout_ms: int = 0) -> bool:
+        d = C.c_int()
+        check(self.lib.mlg_job_wait(self.h, timeout_ms, C.byref(d)))
+        return bool(d.value)
+
+    def result(self) -> list[list[int]]:
+        """Blocks until the job's group has run; raises MalagaError with the group's error."""
+        out = np.zeros((max(self.n, 1), self.cap), dtype=np.uint32)
+        out_len = np.zeros(max(self.n, 1), dtype=np.int32)
+        check(self.lib.mlg_job_result(self.h, out.ctypes.data, self.cap, out_len.ctypes.data))
+        return _rows(out, out_len)[: self.n]
+
+    def __del__(self):
+        if getattr(self, "h", None):
+            self.lib.mlg_job_free(self.h)
+            self.h = None
+
+
+class Server:
+    """Dynamic batching caller (crates/malaga/src/server.rs:74-112): a native inference
+    thread decodes every queued job, grouped by (source, target, beam, shortlist), as
+    one translate_batch call per group.  Submit from any number of threads."""
+
+    def __init__(self, translator: Translator, defaults: GenOptions | None = None):
+        self.t, self.lib = translator, translator.lib
+        self.defaults = defaults or GenOptions()
+        h = C.c_void_p()
+        co = self.defaults._c()
+        check(self.lib.mlg_server_start(translator.h, C.byref(co), C.byref(h)))
+        self.h = h
+
+    def submit(self, src: Sequence[Sequence[int]], tgt_lang: int, src_lang: int = 0, beam_size: int = 0,
+               shortlist: str | None = None) -> Job:
+        ids, lens = _flat(src)
+        h = C.c_void_p()
+        check(self.lib.mlg_server_submit(self.h, ids.ctypes.data, lens.ctypes.data, len(src), src_lang, tgt_lang,
+                                         beam_size, shortlist.encode() if shortlist else None, C.byref(h)))
+        return Job(self, h, len(src), max([self.t.budget(len(r), self.defaults.max_new_tokens) for r in src] + [1]))
+
+    def stats(self) -> dict:
+        v = [C.c_int64() for _ in range(4)]
+        check(self.lib.mlg_server_stats(self.h, *[C.byref(x) for x in v]))
+        return dict(zip(("jobs", "groups", "sentences", "largest_group"), (x.value for x in v)))
+
+    def stop(self):
+        if getattr(self, "h", None):
+            self.lib.mlg_server_stop(self.h)
+            self.h = None
+
+    def __del__(self):
+        self.stop()
+
 
 def tiny_config() -> dict:
     """src/testutil.rs:18-30 (vocab 257, d 64, 4 heads, ffn 128, 2 + 2 layers)."""

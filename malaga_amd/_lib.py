@@ -89,6 +89,15 @@ SIGNATURES = {
     "mlg_greedy": (C.c_int, [_P, _P, C.c_uint32, C.c_int, C.c_int, C.c_uint32, _P, C.c_int, _P]),
     "mlg_greedy_sl": (C.c_int, [_P, _P, C.c_uint32, C.c_char_p, C.c_int, C.c_int, C.c_uint32, _P, C.c_int, _P]),
     "mlg_beam": (C.c_int, [_P, _P, C.c_uint32, C.c_int, C.c_int, C.c_float, C.c_uint32, _P, C.c_int, _P]),
+    "mlg_server_start": (C.c_int, [_P, C.POINTER(CGenOptions), C.POINTER(_P)]),
+    "mlg_server_stop": (None, [_P]),
+    "mlg_server_submit": (C.c_int, [_P, _P, _P, C.c_int, C.c_uint32, C.c_uint32, C.c_int, C.c_char_p,
+                                    C.POINTER(_P)]),
+    "mlg_job_wait": (C.c_int, [_P, C.c_int, _intp]),
+    "mlg_job_result": (C.c_int, [_P, _P, C.c_int, _P]),
+    "mlg_job_free": (None, [_P]),
+    "mlg_server_stats": (C.c_int, [_P, C.POINTER(C.c_int64), C.POINTER(C.c_int64), C.POINTER(C.c_int64),
+                                   C.POINTER(C.c_int64)]),
     "mlg_clear_graphs": (None, [_P]),
     "mlg_graph_stats": (C.c_int, [_P, _intp, _intp, _intp]),
     "mlg_debug_fail_alloc_after": (None, [C.c_long]),

@@ -10,6 +10,7 @@
 #include "convert.hpp"
 #include "quant.hpp"
 #include "runtime.hpp"
+#include "server.hpp"
 
 struct mlg_ctx {
     mlg::Context c;
@@ -19,6 +20,12 @@ struct mlg_model {
 };
 struct mlg_batch {
     std::unique_ptr<mlg::Batch> b;
+};
+struct mlg_server {
+    std::unique_ptr<mlg::Server> s;
+};
+struct mlg_job {
+    std::shared_ptr<mlg::Job> j;
 };
 struct mlg_matrix {
     mlg::DevMatrix w;
@@ -303,6 +310,21 @@ void mlg_gen_options_default(mlg_gen_options *o) {
     o->shortlist = nullptr;
 }
 
+namespace {
+mlg::GenOptions gen_options(const mlg_gen_options *o) {
+    mlg::GenOptions g;
+    g.beam_size = o->beam_size;
+    g.max_new_tokens = o->max_new_tokens;
+    g.length_penalty = o->length_penalty;
+    g.sync_every = o->sync_every;
+    g.max_batch = o->max_batch;
+    g.fused = o->fused != 0 && !(o->flags & MLG_FLAG_NO_GRAPH);
+    g.eos_mask = (o->flags & MLG_FLAG_EOS_MASK) != 0;
+    if (o->shortlist) g.shortlist = o->shortlist;
+    return g;
+}
+}  // namespace
+
 int mlg_generate(mlg_model *m, const uint32_t *ids, const uint32_t *lens, int n, uint32_t tgt_lang,
                  const mlg_gen_options *o, uint32_t *out, int out_cap, int *out_len) {
     return guarded([&]() -> int {
@@ -310,15 +332,7 @@ int mlg_generate(mlg_model *m, const uint32_t *ids, const uint32_t *lens, int n,
         std::lock_guard<std::mutex> lk(m->m->ctx->mu);
         mlg::check_hip(hipSetDevice(m->m->ctx->device), "hipSetDevice");
         if (tgt_lang >= uint32_t(m->m->cfg.vocab_size)) return set_err(MLG_ERR_INVALID, "target language id out of range");
-        mlg::GenOptions g;
-        g.beam_size = o->beam_size;
-        g.max_new_tokens = o->max_new_tokens;
-        g.length_penalty = o->length_penalty;
-        g.sync_every = o->sync_every;
-        g.max_batch = o->max_batch;
-        g.fused = o->fused != 0 && !(o->flags & MLG_FLAG_NO_GRAPH);
-        g.eos_mask = (o->flags & MLG_FLAG_EOS_MASK) != 0;
-        if (o->shortlist) g.shortlist = o->shortlist;
+        const mlg::GenOptions g = gen_options(o);
         if (g.beam_size > 8) return set_err(MLG_ERR_UNSUPPORTED, "beam_size > 8");
         auto src = rows_of(ids, lens, n);
         for (auto &r : src)
@@ -378,6 +392,57 @@ int mlg_beam(mlg_model *m, const mlg_batch *b, uint32_t tgt_lang, int max_new, i
                                !(flags & MLG_FLAG_NO_GRAPH));
         return write_rows(rows, out, out_cap, out_len);
     });
+}
+
+int mlg_server_start(mlg_model *m, const mlg_gen_options *defaults, mlg_server **out) {
+    return guarded([&]() -> int {
+        if (!m || !defaults || !out) return set_err(MLG_ERR_INVALID, "null argument");
+        if (defaults->beam_size > 8) return set_err(MLG_ERR_UNSUPPORTED, "beam_size > 8");
+        auto s = std::make_unique<mlg_server>();
+        s->s = std::make_unique<mlg::Server>(*m->m, gen_options(defaults));
+        *out = s.release();
+        return MLG_OK;
+    });
+}
+
+void mlg_server_stop(mlg_server *s) { delete s; }
+
+int mlg_server_submit(mlg_server *s, const uint32_t *ids, const uint32_t *lens, int n, uint32_t src_lang,
+                      uint32_t tgt_lang, int beam_size, const char *shortlist, mlg_job **out) {
+    return guarded([&]() -> int {
+        if (!s || n < 0 || (n && (!ids || !lens)) || !out) return set_err(MLG_ERR_INVALID, "null argument");
+        auto j = std::make_unique<mlg_job>();
+        j->j = s->s->submit(rows_of(ids, lens, n), src_lang, tgt_lang, beam_size, shortlist ? shortlist : "");
+        *out = j.release();
+        return MLG_OK;
+    });
+}
+
+int mlg_job_wait(mlg_job *j, int timeout_ms, int *done) {
+    if (!j || !done) return set_err(MLG_ERR_INVALID, "null argument");
+    *done = j->j->wait(timeout_ms) ? 1 : 0;
+    return MLG_OK;
+}
+
+int mlg_job_result(mlg_job *j, uint32_t *out, int out_cap, int *out_len) {
+    return guarded([&]() -> int {
+        if (!j || (!j->j->src.empty() && (!out || !out_len))) return set_err(MLG_ERR_INVALID, "null argument");
+        j->j->wait(-1);
+        if (j->j->status != MLG_OK) return set_err(j->j->status, j->j->error);
+        return write_rows(j->j->out, out, out_cap, out_len);
+    });
+}
+
+void mlg_job_free(mlg_job *j) { delete j; }
+
+int mlg_server_stats(const mlg_server *s, int64_t *jobs, int64_t *groups, int64_t *sentences, int64_t *largest_group) {
+    if (!s) return set_err(MLG_ERR_INVALID, "null server");
+    const mlg::ServerStats st = s->s->stats();
+    if (jobs) *jobs = st.jobs;
+    if (groups) *groups = st.groups;
+    if (sentences) *sentences = st.sentences;
+    if (largest_group) *largest_group = st.largest_group;
+    return MLG_OK;
 }
 
 void mlg_clear_graphs(mlg_model *m) {
