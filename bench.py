@@ -10,6 +10,8 @@ Also reported on the same JSON line:
     (21 source ids -> 18 tokens, crates/malaga/src/main.rs:409-436);
   * config 4: greedy batch 32 (lognormal lengths, length-sorted) and beam 4 at
     batch 8, sentences/s;
+  * ``server``: the dynamic batching caller under a burst of 64 one-sentence
+    requests from 64 threads, and 16 threads x 8 back-to-back requests;
   * ``fast_vocab``: shortlist (--fast-vocab) decoding beside exact decoding on the
     reference's bench shapes (bs1 21 -> 18, and batch 16), with a seeded random
     37k-id shortlist stored in the q4_k_m model;
@@ -254,6 +256,65 @@ def bench_fast_vocab(T):
     return res
 
 
+def bench_server(T):
+    """The dynamic batching caller (crates/malaga/src/server.rs:74-112) under a burst:
+    64 clients (threads) each submit one sentence of 21 ids at once and wait for its 18
+    tokens (EOS masked); the first job runs alone, the others queue behind it and share
+    the next batches.  Also 16 clients issuing 8 requests each back to back."""
+    import threading
+    import torch
+    import malaga_amd as M
+
+    srv = M.Server(T, M.GenOptions(max_new_tokens=18, eos_mask=True))
+    one = sources(64, 21, seed=7000)
+
+    def burst():
+        lat = [0.0] * len(one)
+        go = threading.Barrier(len(one) + 1)
+
+        def client(i):
+            go.wait()
+            a = time.perf_counter()
+            srv.submit([one[i]], TGT_LANG).result()
+            lat[i] = (time.perf_counter() - a) * 1e3
+
+        th = [threading.Thread(target=client, args=(i,)) for i in range(len(one))]
+        for t in th:
+            t.start()
+        go.wait()
+        a = time.perf_counter()
+        for t in th:
+            t.join()
+        return time.perf_counter() - a, lat
+
+    burst()  # warm-up (buckets, graphs)
+    torch.cuda.synchronize()
+    g0 = srv.stats()["groups"]
+    runs = [burst() for _ in range(5)]
+    groups = (srv.stats()["groups"] - g0) / 5
+    wall = sorted(r[0] for r in runs)[2]
+    lat = np.concatenate([r[1] for r in runs])
+
+    def closed_loop(clients=16, each=8):
+        def client(c):
+            for k in range(each):
+                srv.submit([one[(c * each + k) % len(one)]], TGT_LANG).result()
+
+        th = [threading.Thread(target=client, args=(c,)) for c in range(clients)]
+        a = time.perf_counter()
+        for t in th:
+            t.start()
+        for t in th:
+            t.join()
+        return clients * each / (time.perf_counter() - a)
+
+    closed = closed_loop()
+    srv.stop()
+    return dict(burst_clients=len(one), burst_sentences_per_s=len(one) / wall, burst_ms=wall * 1e3,
+                burst_latency_p50_ms=float(np.percentile(lat, 50)), burst_latency_p99_ms=float(np.percentile(lat, 99)),
+                groups_per_burst=groups, closed_loop_16x8_sentences_per_s=closed)
+
+
 class GemvBench:
     """Times one kernel-level entry point over rotating device copies of a weight matrix."""
 
@@ -397,8 +458,8 @@ def main():
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--skip-cpu", action="store_true")
-    ap.add_argument("--legs", default="bs1,batched,fastvocab,kernels,cpu",
-                    help="comma-separated subset of bs1,batched,fastvocab,kernels,cpu (profiling runs); "
+    ap.add_argument("--legs", default="bs1,batched,fastvocab,server,kernels,cpu",
+                    help="comma-separated subset of bs1,batched,fastvocab,server,kernels,cpu (profiling runs); "
                          "'config5' alone runs only the 3.3B batch-64 leg, 'mfma' alone the short "
                          "MFMA-GEMM runs used for counter collection")
     ap.add_argument("--roofline-only", action="store_true", help="only the LM-head roofline leg (for rocprof)")
@@ -457,12 +518,17 @@ def main():
     for k, v in batched.items():
         log(f"{k}: {v['sentences_per_s']:.1f} sentences/s ({v.get('ms_per_batch', 0):.1f} ms/batch)")
     fast = bench_fast_vocab(T) if "fastvocab" in legs else None
+    server = bench_server(T) if "server" in legs else None
+    if server:
+        log(f"server burst of {server['burst_clients']}: {server['burst_sentences_per_s']:.1f} sentences/s "
+            f"(p50 {server['burst_latency_p50_ms']:.1f} ms, {server['groups_per_burst']:.1f} groups); closed loop "
+            f"16x8: {server['closed_loop_16x8_sentences_per_s']:.1f} sentences/s")
     if fast:
         for k in ("exact", "fast_vocab"):
             log(f"{k} (21 ids -> 18 tokens): bs1 p50 {fast[k]['bs1_p50_ms']:.2f} ms, bs16 "
                 f"{fast[k]['bs16_sentences_per_s']:.1f} sentences/s")
     if "kernels" not in legs:
-        print(json.dumps({"p50_ms": b1["p50"], "batched": batched}))
+        print(json.dumps({"p50_ms": b1["p50"], "batched": batched, "fast_vocab": fast, "server": server}))
         return
     gemv_rows, small = bench_kernels(T, lm_blocks)
     lm = gemv_rows[-1]
@@ -511,6 +577,7 @@ def main():
         "sentences_per_s_bs32": round(batched["greedy_bs32"]["sentences_per_s"], 2),
         "batched": batched,
         "fast_vocab": fast,
+        "server": server,
         "gemv_HBM_GBps_q4K_lm_head": round(q4_lm["GBps"], 1),
         "gemv": [{k: (round(v, 3) if isinstance(v, float) else v) for k, v in r.items()} for r in gemv_rows],
         "small_kernels_us": {k: round(v, 3) for k, v in small.items()},
