@@ -34,9 +34,9 @@ __all__ = ["GenOptions", "Translator", "Server", "Job", "Config", "MalagaError",
 
 @dataclasses.dataclass
 class GenOptions:
-    """src/translator.rs:15-53.  ``shortlist``: the target-language code whose vocabulary
-    shortlist greedy decoding uses (``--fast-vocab``; the reference's bool plus the code it
-    derives from the tokenizer), or None for exact decoding."""
+    """src/translator.rs:15-53.  ``shortlist`` (``--fast-vocab``): True uses the target
+    language's shortlist (its code comes from the tokenizer, as the reference derives
+    it); a string names the shortlist's language code directly; None decodes exactly."""
 
     beam_size: int = 1
     max_new_tokens: int | None = None
@@ -45,7 +45,7 @@ class GenOptions:
     max_batch: int = 32
     fused: bool = True
     eos_mask: bool = False  # benchmark-only: EOS never chosen, so lengths are fixed
-    shortlist: str | None = None
+    shortlist: str | bool | None = None
 
     def _c(self) -> CGenOptions:
         o = CGenOptions()
@@ -56,7 +56,7 @@ class GenOptions:
         o.max_batch = self.max_batch
         o.fused = 1 if self.fused else 0
         o.flags = FLAG_EOS_MASK if self.eos_mask else 0
-        o.shortlist = self.shortlist.encode() if self.shortlist else None
+        o.shortlist = self.shortlist.encode() if isinstance(self.shortlist, str) and self.shortlist else None
         return o
 
 
@@ -98,18 +98,58 @@ class EncodedBatch:
 class Translator:
     """A GGUF NLLB model resident on one GPU (src/translator.rs:55-73)."""
 
-    def __init__(self, ctx: _Ctx, handle):
-        self._ctx, self.lib, self.h = ctx, ctx.lib, handle
+    def __init__(self, ctx: _Ctx, handle, path: str | Path | None = None):
+        self._ctx, self.lib, self.h, self.path = ctx, ctx.lib, handle, path
         c = Config()
         check(self.lib.mlg_model_config(self.h, C.byref(c)))
         self.cfg = c.as_dict()
+        self._text = None
 
     @classmethod
     def load(cls, path: str | Path, device: int = 0) -> "Translator":
         ctx = _Ctx(device)
         h = C.c_void_p()
         check(ctx.lib.mlg_model_load(ctx.h, str(path).encode(), C.byref(h)))
-        return cls(ctx, h)
+        return cls(ctx, h, path)
+
+    @property
+    def text(self):
+        """The model's tokenizer and text helpers (malaga_amd.text.TextCodec), read from
+        the GGUF key tokenizer.huggingface.json on first use (src/translator.rs:66-68)."""
+        if self._text is None:
+            from .text import TextCodec
+
+            if self.path is None:
+                raise MalagaError(1, "model loaded without a path: no tokenizer")
+            self._text = TextCodec.from_gguf(self.path, self.cfg)
+        return self._text
+
+    def lang_id(self, lang: str) -> int:
+        """Token id of an NLLB code (``fra_Latn``) or alias (``fr``) (src/translator.rs:83-87)."""
+        try:
+            return self.text.lang_id(lang)
+        except KeyError as e:
+            raise MalagaError(1, str(e.args[0])) from None
+
+    def translate_batch(self, texts: Sequence[str], src: str, tgt: str,
+                        opts: GenOptions | None = None) -> list[str]:
+        """Independent sentences in, translations out (src/translator.rs:136-167)."""
+        opts = opts or GenOptions()
+        self.lang_id(src), self.lang_id(tgt)  # unknown languages are errors
+        return self.text.translate_batch(texts, src, tgt, lambda rows, tid, code: self.generate(
+            rows, tid, dataclasses.replace(opts, shortlist=code) if opts.shortlist is True else opts))
+
+    def translate_docs(self, docs: Sequence[str], src: str, tgt: str, opts: GenOptions | None = None) -> list[str]:
+        """Documents: sentences of all documents decoded together, layout kept
+        (src/translator.rs:108-133)."""
+        opts = opts or GenOptions()
+        self.lang_id(src), self.lang_id(tgt)
+        return self.text.translate_docs(docs, src, tgt, lambda rows, tid, code: self.generate(
+            rows, tid, dataclasses.replace(opts, shortlist=code) if opts.shortlist is True else opts))
+
+    def translate(self, text: str, src: str, tgt: str, opts: GenOptions | None = None) -> str:
+        """src/translator.rs:102-104."""
+        return self.translate_docs([text], src, tgt, opts)[0]
 
     def close(self):
         if getattr(self, "h", None):
@@ -136,6 +176,8 @@ class Translator:
         opts = opts or GenOptions()
         if not src:
             return []
+        if opts.shortlist is True:  # src/translator.rs:170-172: the code is the target token
+            opts = dataclasses.replace(opts, shortlist=self.text.tok.id_to_token(tgt_lang) or None)
         ids, lens = _flat(src)
         cap = self._out_cap(src, opts)
         out = np.zeros((len(src), cap), dtype=np.uint32)

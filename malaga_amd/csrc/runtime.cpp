@@ -1125,7 +1125,8 @@ std::vector<std::vector<uint32_t>> generate(Model &m, const std::vector<std::vec
             ids = generate_to(m, batch, tgt_lang, o);
         } catch (const Failure &f) {
             // src/translator.rs:150-158: free cached buffers, retry with smaller batches
-            if (f.code == ERR_OOM && max_batch > 1) {
+            // ... unless the full-vocabulary LM head itself does not fit (translator.rs:152)
+            if (f.code == ERR_OOM && max_batch > 1 && f.msg.find("full-vocabulary") == std::string::npos) {
                 max_batch /= 2;
                 m.graphs.clear();
                 continue;
