@@ -446,16 +446,23 @@ std::unique_ptr<Batch> Model::encode(const std::vector<std::vector<uint32_t>> &s
         h2d(d_ids, iota, st);
         check_hip(embed_pos_rows(rows, d_ids, d_pidx, M, pos, embed_scale, x, st), "embed");
     }
-    for (auto &l : enc) {
-        check_hip(layernorm(x, M, d, l.attn_norm.g, l.attn_norm.b, kLnEps, h, st), "layernorm");
+    // pre-LN layers; each residual projection also produces the next LayerNorm (in the
+    // split-K reduction when the GEMM splits K), the last one enc_norm
+    if (!enc.empty()) check_hip(layernorm(x, M, d, enc[0].attn_norm.g, enc[0].attn_norm.b, kLnEps, h, st), "layernorm");
+    else check_hip(layernorm(x, M, d, enc_norm.g, enc_norm.b, kLnEps, h, st), "layernorm");
+    for (size_t li = 0; li < enc.size(); ++li) {
+        const EncLayer &l = enc[li];
+        const LNorm &next = li + 1 < enc.size() ? enc[li + 1].attn_norm : enc_norm;
         matmul(l.qkv, h, M, qkv, false, nullptr);
         check_hip(attn_prefill(qkv, b, s, H, hd, d_lens, att, st), "attn_prefill");
-        matmul(l.out, att, M, x, false, x);
-        check_hip(layernorm(x, M, d, l.ffn_norm.g, l.ffn_norm.b, kLnEps, h, st), "layernorm");
+        check_hip(gemm_residual_ln(l.out.w, att, d, M, l.out.b, x, l.ffn_norm.g, l.ffn_norm.b, kLnEps, h, st,
+                                   ctx->gemm_workspace(), kGemmWorkspaceBytes),
+                  "gemm_residual_ln");
         matmul(l.up, h, M, qkv, true, nullptr);
-        matmul(l.down, qkv, M, x, false, x);
+        check_hip(gemm_residual_ln(l.down.w, qkv, f, M, l.down.b, x, next.g, next.b, kLnEps, h, st,
+                                   ctx->gemm_workspace(), kGemmWorkspaceBytes),
+                  "gemm_residual_ln");
     }
-    check_hip(layernorm(x, M, d, enc_norm.g, enc_norm.b, kLnEps, h, st), "layernorm");
     const int Hd = cfg.decoder_heads, hdd = d / Hd;
     const size_t kv_elems = size_t(M) * d;
     out->block = dev_alloc(std::max<size_t>(dec.size(), 1) * 2 * kv_elems * 2, "cross K/V");
