@@ -30,6 +30,11 @@ struct mlg_job {
 struct mlg_matrix {
     mlg::DevMatrix w;
     void *mem = nullptr;
+    void *mem_lm = nullptr;
+    ~mlg_matrix() {
+        mlg::dev_free(mem);
+        mlg::dev_free(mem_lm);
+    }
     mlg_ctx *ctx = nullptr;
 };
 
@@ -474,11 +479,7 @@ int mlg_matrix_upload(mlg_ctx *ctx, uint32_t type, int N, int K, const void *ggu
         mlg::layout_planes(type, N, K, static_cast<const uint8_t *>(gguf_rows), host.data(), &off_s, &off_d, &total);
         auto w = std::make_unique<mlg_matrix>();
         w->mem = mlg::dev_alloc(total, "matrix");
-        const hipError_t e = hipMemcpy(w->mem, host.data(), total, hipMemcpyHostToDevice);
-        if (e != hipSuccess) {
-            mlg::dev_free(w->mem);
-            mlg::check_hip(e, "upload");
-        }
+        mlg::check_hip(hipMemcpy(w->mem, host.data(), total, hipMemcpyHostToDevice), "upload");
         w->ctx = ctx;
         w->w.type = type;
         w->w.N = N;
@@ -487,16 +488,19 @@ int mlg_matrix_upload(mlg_ctx *ctx, uint32_t type, int N, int K, const void *ggu
         w->w.s = w->w.q + off_s;
         w->w.d = w->w.q + off_d;
         w->w.bytes = total;
+        if (const size_t lb = mlg::lane_major_bytes(type, N, K)) {  // as the model's LM heads carry
+            std::vector<uint8_t> lm(lb);
+            mlg::layout_lane_major(N, K, host.data(), lm.data());
+            w->mem_lm = mlg::dev_alloc(lb, "matrix (lane-major quants)");
+            w->w.lm = static_cast<uint8_t *>(w->mem_lm);
+            mlg::check_hip(hipMemcpy(w->mem_lm, lm.data(), lb, hipMemcpyHostToDevice), "upload");
+        }
         *out = w.release();
         return MLG_OK;
     });
 }
 
-void mlg_matrix_free(mlg_matrix *w) {
-    if (!w) return;
-    mlg::dev_free(w->mem);
-    delete w;
-}
+void mlg_matrix_free(mlg_matrix *w) { delete w; }
 
 int64_t mlg_matrix_bytes(const mlg_matrix *w) { return w ? int64_t(w->w.bytes) : 0; }
 

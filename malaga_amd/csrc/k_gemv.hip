@@ -49,7 +49,8 @@ struct ArgmaxEpi {
 template <int T, int MODE>
 constexpr bool kGemvLimbs = MODE != 0 && kLimbX<T>;  // large matrices: limb x (gemv_core.hpp)
 
-template <int T, int B, int CPL, int MODE>
+// LM: a.w.q is the lane-major quant copy of a q6_K head (DevMatrix::lm)
+template <int T, int B, int CPL, int MODE, bool LM>
 __global__ __launch_bounds__(256) void k_gemv(GemvArgs a) {
     extern __shared__ uint32_t xlds[];  // limbs of x
     const int lane = threadIdx.x & 63;
@@ -67,10 +68,10 @@ __global__ __launch_bounds__(256) void k_gemv(GemvArgs a) {
     const int gwave = blockIdx.x * 4 + (threadIdx.x >> 6), nwaves = gridDim.x * 4;
     if constexpr (MODE == 0) {
         StoreEpi<B> epi{a};
-        gemv_rows<T, B, CPL, false, 1>(a.w, a.g, xr, gwave, nwaves, NoPre{}, load_x, epi, a.bias);
+        gemv_rows<T, B, CPL, false, 1, LM>(a.w, a.g, xr, gwave, nwaves, NoPre{}, load_x, epi, a.bias);
     } else if constexpr (MODE == 2) {
         StoreEpi<B> epi{a};
-        gemv_rows<T, B, CPL, false, 2>(a.w, a.g, xr, gwave, nwaves, NoPre{}, load_x, epi, a.bias);
+        gemv_rows<T, B, CPL, false, 2, LM>(a.w, a.g, xr, gwave, nwaves, NoPre{}, load_x, epi, a.bias);
     } else {  // the LM head: weights streamed once per step
         ArgmaxEpi<B> epi{a, {}, {}};
 #pragma unroll
@@ -79,9 +80,8 @@ __global__ __launch_bounds__(256) void k_gemv(GemvArgs a) {
             epi.idx[bi] = 0xffffffffu;
         }
         // rows >= nt_from non-temporal: the 215 MB stream then evicts less of the layer
-        // weights from the MALL between steps (measured: -20 us per 600M step, although
-        // the kernel alone is ~15% slower than with temporal loads)
-        gemv_rows<T, B, CPL, true, 1>(a.w, a.g, xr, gwave, nwaves, NoPre{}, load_x, epi, a.bias, a.nt_from);
+        // weights from the MALL between steps (measured: -20 us per 600M step)
+        gemv_rows<T, B, CPL, true, 1, LM>(a.w, a.g, xr, gwave, nwaves, NoPre{}, load_x, epi, a.bias, a.nt_from);
         __shared__ float sv[4][B];
         __shared__ uint32_t si[4][B];
         const int wv = threadIdx.x >> 6;
@@ -105,22 +105,22 @@ __global__ __launch_bounds__(256) void k_gemv(GemvArgs a) {
     }
 }
 
-template <int T, int B, int CPL, int MODE>
+template <int T, int B, int CPL, int MODE, bool LM>
 hipError_t launch_t(const GemvArgs &a, int grid, hipStream_t st) {
     if constexpr (GTraits<T>::XW * B * CPL > kGemvMaxXRegs) {
         return hipErrorInvalidValue;
     } else {
         const int lds = kGemvLimbs<T, MODE> ? xq_lds_bytes<T>(a.w.K, a.nb) : 0;
         if (lds > 65536) return hipErrorInvalidValue;
-        hipLaunchKernelGGL((k_gemv<T, B, CPL, MODE>), dim3(grid), dim3(256), lds, st, a);
+        hipLaunchKernelGGL((k_gemv<T, B, CPL, MODE, LM>), dim3(grid), dim3(256), lds, st, a);
         return hipGetLastError();
     }
 }
 
-template <int T, int MODE>
+template <int T, int MODE, bool LM = false>
 hipError_t dispatch_bc(const GemvArgs &a, int B, int cpl, int grid, hipStream_t st) {
 #define MLG_CASE(BB, CC) \
-    if (B == BB && cpl == CC) return launch_t<T, BB, CC, MODE>(a, grid, st);
+    if (B == BB && cpl == CC) return launch_t<T, BB, CC, MODE, LM>(a, grid, st);
     MLG_CASE(1, 1) MLG_CASE(1, 2) MLG_CASE(1, 4)
     MLG_CASE(2, 1) MLG_CASE(2, 2) MLG_CASE(2, 4)
     MLG_CASE(4, 1) MLG_CASE(4, 2) MLG_CASE(4, 4)
@@ -128,12 +128,22 @@ hipError_t dispatch_bc(const GemvArgs &a, int B, int cpl, int grid, hipStream_t 
     return hipErrorInvalidValue;
 }
 
+// lm: lane-major quants of a q6_K head (the large-matrix modes only)
 template <int MODE>
-hipError_t dispatch(uint32_t type, const GemvArgs &a, int B, int cpl, int grid, hipStream_t st) {
+hipError_t dispatch(uint32_t type, const GemvArgs &a, int B, int cpl, int grid, hipStream_t st,
+                    const uint8_t *lm = nullptr) {
     switch (type) {
     case GGML_Q4_K: return dispatch_bc<GGML_Q4_K, MODE>(a, B, cpl, grid, st);
     case GGML_Q5_K: return dispatch_bc<GGML_Q5_K, MODE>(a, B, cpl, grid, st);
-    case GGML_Q6_K: return dispatch_bc<GGML_Q6_K, MODE>(a, B, cpl, grid, st);
+    case GGML_Q6_K:
+        if constexpr (MODE != 0) {
+            if (lm) {
+                GemvArgs b = a;
+                b.w.q = lm;
+                return dispatch_bc<GGML_Q6_K, MODE, true>(b, B, cpl, grid, st);
+            }
+        }
+        return dispatch_bc<GGML_Q6_K, MODE>(a, B, cpl, grid, st);
     case GGML_Q8_0: return dispatch_bc<GGML_Q8_0, MODE>(a, B, cpl, grid, st);
     case GGML_F16: return dispatch_bc<GGML_F16, MODE>(a, B, cpl, grid, st);
     case GGML_F32: return dispatch_bc<GGML_F32, MODE>(a, B, cpl, grid, st);
@@ -200,7 +210,7 @@ hipError_t gemv(const DevMatrix &w, const float *x, int ldx, int b, float *y, in
     a.bias = bias;
     a.relu = relu ? 1 : 0;
     if (w.N <= kGemvSmallRows) return dispatch<0>(w.type, a, gemv_round_b(b), cpl, gemv_grid(w, 1), st);
-    return dispatch<2>(w.type, a, gemv_round_b(b), cpl, gemv_grid(w, 2), st);
+    return dispatch<2>(w.type, a, gemv_round_b(b), cpl, gemv_grid(w, 2), st, w.lm);
 }
 
 int gemv_argmax_parts(const DevMatrix &w, int b) {
@@ -223,7 +233,7 @@ hipError_t gemv_argmax(const DevMatrix &w, const float *x, int ldx, int b, int m
     *parts = grid;
     const size_t row_bytes = w.bytes / size_t(w.N);
     a.nt_from = row_bytes ? int(std::min<size_t>(size_t(w.N), kLmHeadCachedBytes / row_bytes)) : w.N;
-    return dispatch<1>(w.type, a, gemv_round_b(b), cpl, grid, st);
+    return dispatch<1>(w.type, a, gemv_round_b(b), cpl, grid, st, w.lm);
 }
 
 }  // namespace mlg

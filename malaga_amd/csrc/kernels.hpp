@@ -17,6 +17,9 @@ struct DevMatrix {
     int N = 0, K = 0;
     uint8_t *q = nullptr, *s = nullptr, *d = nullptr;
     size_t bytes = 0;  // total bytes of the planes (= GGUF bytes)
+    // q6_K LM heads: a second copy of the quant plane in lane-major order, read by the
+    // large-matrix GEMVs (layout_lane_major); null elsewhere
+    uint8_t *lm = nullptr;
 };
 
 // Splits/copies GGUF rows [N][K] of `type` into the device layout (host side).
@@ -24,6 +27,12 @@ struct DevMatrix {
 bool layout_planes(uint32_t type, int N, int K, const uint8_t *gguf, uint8_t *out, size_t *off_s, size_t *off_d,
                    size_t *total);
 size_t planes_bytes(uint32_t type, int N, int K);
+// q6_K: the quant plane (block-major [N * K/256][192], as layout_planes writes it) in
+// lane-major order: piece k of 64-value chunk c of row r (k = 0, 1: the two 16-byte ql
+// pieces, 2: the 16-byte qh piece a GEMV lane reads) at k * N * (K/256) * 64 +
+// (r * (K/64) + c) * 16.  The lanes of a row group then read whole cache lines per load.
+size_t lane_major_bytes(uint32_t type, int N, int K);  // 0: no lane-major form
+void layout_lane_major(int N, int K, const uint8_t *q_plane, uint8_t *out);
 
 // Largest batch the register-resident GEMV handles for this matrix (0 if none).
 int gemv_max_batch(const DevMatrix &w);

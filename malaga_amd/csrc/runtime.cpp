@@ -121,6 +121,25 @@ bool layout_planes(uint32_t type, int N, int K, const uint8_t *src, uint8_t *out
     return true;
 }
 
+size_t lane_major_bytes(uint32_t type, int N, int K) {
+    return type == GGML_Q6_K && K % 256 == 0 ? size_t(N) * (K / 256) * 192 : 0;
+}
+
+void layout_lane_major(int N, int K, const uint8_t *q_plane, uint8_t *out) {
+    const int nb = K / 256, nch = 4 * nb;
+    const size_t P = size_t(N) * nb * 64;
+    for (int64_t r = 0; r < N; ++r)
+        for (int c = 0; c < nch; ++c) {
+            // the pieces load_chunk<GGML_Q6_K> reads for chunk c (gemv_core.hpp)
+            const uint8_t *qp = q_plane + (size_t(r) * nb + (c >> 2)) * 192;
+            const int h2 = (c >> 1) & 1, i = c & 1;
+            const size_t o = (size_t(r) * nch + c) * 16;
+            std::memcpy(out + o, qp + 64 * h2 + 16 * i, 16);
+            std::memcpy(out + P + o, qp + 64 * h2 + 32 + 16 * i, 16);
+            std::memcpy(out + 2 * P + o, qp + 128 + 32 * h2 + 16 * i, 16);
+        }
+}
+
 float *Context::gemm_workspace() {
     if (!gemm_ws) gemm_ws = static_cast<float *>(dev_alloc(kGemmWorkspaceBytes, "GEMM workspace"));
     return gemm_ws;
@@ -170,7 +189,7 @@ const GgufTensorInfo *matrix_info(GgufFile &g, const std::string &name, int n, i
 }
 }  // namespace
 
-DevMatrix Model::upload_matrix(GgufFile &g, const std::string &name, int n, int k) {
+DevMatrix Model::upload_matrix(GgufFile &g, const std::string &name, int n, int k, bool head) {
     const GgufTensorInfo *t = matrix_info(g, name, n, k);
     DevMatrix m;
     m.type = t->type;
@@ -188,7 +207,19 @@ DevMatrix Model::upload_matrix(GgufFile &g, const std::string &name, int n, int 
     m.d = d + off_d;
     m.bytes = total;
     weight_bytes += total;
+    if (head) upload_lane_major(m, host.data());
     return m;
+}
+
+void Model::upload_lane_major(DevMatrix &m, const uint8_t *q_plane) {
+    const size_t lb = lane_major_bytes(m.type, m.N, m.K);
+    if (!lb) return;
+    std::vector<uint8_t> lm(lb);
+    layout_lane_major(m.N, m.K, q_plane, lm.data());
+    m.lm = static_cast<uint8_t *>(dev_alloc(lb, "LM head (lane-major quants)"));
+    owned_.push_back(m.lm);
+    check_hip(hipMemcpy(m.lm, lm.data(), lb, hipMemcpyHostToDevice), "upload");
+    weight_bytes += lb;
 }
 
 Linear Model::load_linear(GgufFile &g, const std::string &name, int n, int k) {
@@ -253,7 +284,7 @@ void Model::load(const std::string &path) {
         embed.bytes = planes_bytes(t->type, cfg.vocab_size, d);
         embed_host_.assign(g.tensor_data(*t), g.tensor_data(*t) + embed.bytes);
     } else {
-        embed = upload_matrix(g, "token_embd.weight", cfg.vocab_size, d);
+        embed = upload_matrix(g, "token_embd.weight", cfg.vocab_size, d, true);
     }
     // src/model.rs:324-340: [sin | cos] in f64, row pad zeroed
     n_pos = cfg.max_position_embeddings + cfg.pad_token_id + 1;
@@ -318,7 +349,7 @@ void Model::load(const std::string &path) {
         if (!std::is_sorted(sl->ids.begin(), sl->ids.end()))
             fail(ERR_FORMAT, "shortlist " + sl->code + ": ids not sorted");
         const int n = int(sl->ids.size());
-        sl->head = upload_matrix(g, "lm_head." + sl->code + ".weight", n, d);
+        sl->head = upload_matrix(g, "lm_head." + sl->code + ".weight", n, d, true);
         sl->d_ids = static_cast<uint32_t *>(dev_alloc(size_t(n) * 4, "shortlist ids"));
         owned_.push_back(sl->d_ids);
         check_hip(hipMemcpy(sl->d_ids, sl->ids.data(), size_t(n) * 4, hipMemcpyHostToDevice), "upload");
@@ -343,6 +374,7 @@ void Model::ensure_embed() {
     embed.s = d + off_s;
     embed.d = d + off_d;
     weight_bytes += total;
+    upload_lane_major(embed, host.data());
     embed_host_.clear();
     embed_host_.shrink_to_fit();
 }

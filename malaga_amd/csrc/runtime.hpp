@@ -215,7 +215,9 @@ class Model {
     Linear load_linear(class GgufFile &g, const std::string &name, int n, int k);
     LNorm load_ln(class GgufFile &g, const std::string &name, int d);
     float *upload_f32(class GgufFile &g, const std::string &name, int64_t n);
-    DevMatrix upload_matrix(class GgufFile &g, const std::string &name, int n, int k);
+    // head: also the lane-major quant copy of a q6_K LM head (DevMatrix::lm)
+    DevMatrix upload_matrix(class GgufFile &g, const std::string &name, int n, int k, bool head = false);
+    void upload_lane_major(DevMatrix &m, const uint8_t *q_plane);
     void matmul(const Linear &l, const float *x, int rows, float *y, bool relu, const float *resid);
     void step_fused(StaticState &st);
     void lm_head(StaticState &st, bool greedy_mode, int mask_id);
