@@ -188,12 +188,14 @@ def test_gemm_argmax_batched_lm_head(ctx, t, K):
         ctx.lib.mlg_matrix_free(w)
 
 
-@pytest.mark.parametrize("t,K", [(Q4_K, 1024), (Q5_K, 512), (Q6_K, 1024), (Q8_0, 1024), (Q8_0, 96)])
+@pytest.mark.parametrize("t,K", [(Q4_K, 1024), (Q5_K, 512), (Q6_K, 1024), (Q6_K, 2048), (Q6_K, 256), (Q8_0, 1024),
+                                 (Q8_0, 96)])
 def test_large_gemv_integer_limbs(ctx, t, K):
     """N > 65536: the streaming GEMVs hold x as 8-bit limbs with one power-of-two
     scale per group (exact integer dot products).  Besides f32 rounding, each x_k
     is rounded by at most 2^-23 of its group's max |x|; the store and the fused
-    argmax (LM head) both follow the dequantized f64 dot product."""
+    argmax (LM head) both follow the dequantized f64 dot product.  q6_K matrices
+    read the lane-major copy of their quants (K = 2048: two chunks per lane)."""
     rng = np.random.default_rng(K + t)
     N = 70001
     wf = rng.normal(0, 0.02, (N, K)).astype(np.float32)
