@@ -264,16 +264,19 @@ __global__ __launch_bounds__(64) void k_attn_prefill(const float *qkv, int s, in
     }
 }
 
-__global__ void k_split_cross_kv(const float *kv, int b, int s, int H, int hd, __half *K, __half *V) {
+__global__ void k_split_cross_kv(const float *kv, int b, int s, int H, int hd, int L, __half *K0, size_t kv_elems) {
     const int d = H * hd;
-    const size_t total = size_t(b) * s * d;
+    const size_t total = size_t(b) * s * L * d;
     for (size_t idx = blockIdx.x * size_t(blockDim.x) + threadIdx.x; idx < total; idx += size_t(gridDim.x) * blockDim.x) {
         const int c = int(idx % d);
-        const size_t tok = idx / d;
+        const size_t rest = idx / d, tok = rest / L;
+        const int l = int(rest % L);
         const int j = int(tok % s), i = int(tok / s), hh = c / hd, e = c % hd;
         const size_t dst = ((size_t(i) * H + hh) * s + j) * hd + e;
-        K[dst] = __float2half(kv[tok * 2 * d + c]);
-        V[dst] = __float2half(kv[tok * 2 * d + d + c]);
+        __half *K = K0 + 2 * size_t(l) * kv_elems;
+        const float *src = kv + (tok * L + l) * 2 * d;
+        K[dst] = __float2half(src[c]);
+        K[kv_elems + dst] = __float2half(src[d + c]);
     }
 }
 
@@ -750,9 +753,11 @@ hipError_t attn_prefill(const float *qkv, int b, int s, int H, int hd, const uin
     return hipGetLastError();
 }
 
-hipError_t split_cross_kv(const float *kv, int b, int s, int H, int hd, __half *K, __half *V, hipStream_t st) {
-    const size_t n = size_t(b) * s * H * hd;
-    hipLaunchKernelGGL(k_split_cross_kv, dim3(grid_1d(n, 256)), dim3(256), 0, st, kv, b, s, H, hd, K, V);
+hipError_t split_cross_kv(const float *kv, int b, int s, int H, int hd, int L, __half *K0, size_t kv_elems,
+                          hipStream_t st) {
+    const size_t n = size_t(b) * s * H * hd * L;
+    if (!n) return hipSuccess;
+    hipLaunchKernelGGL(k_split_cross_kv, dim3(grid_1d(n, 256)), dim3(256), 0, st, kv, b, s, H, hd, L, K0, kv_elems);
     return hipGetLastError();
 }
 

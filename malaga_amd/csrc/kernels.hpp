@@ -138,7 +138,12 @@ hipError_t attn_decode(const float *q, const __half *K, const __half *V, int b, 
 hipError_t attn_prefill(const float *qkv, int b, int s, int H, int hd, const uint32_t *lens, float *out,
                         hipStream_t st);
 // kv [b*s][2d] f32 (k | v) -> f16 K, V [b][H][s][hd]
-hipError_t split_cross_kv(const float *kv, int b, int s, int H, int hd, __half *K, __half *V, hipStream_t st);
+// kv [b*s][L][2d] f32 (the stacked cross K/V projection of L layers) -> f16 [b][H][s][hd]:
+// layer l's K at K0 + 2 l kv_elems, its V at K + kv_elems (kv_elems = b*s*d)
+hipError_t split_cross_kv(const float *kv, int b, int s, int H, int hd, int L, __half *K0, size_t kv_elems,
+                          hipStream_t st);
+// rows [r0, r0 + n) of w as a matrix of their own (block-major planes; no lane-major copy)
+DevMatrix rows_view(const DevMatrix &w, int r0, int n);
 // dst [.][H][S][hd] row r (< n_dst) <- src [.][H][s][hd] row map[r] (row r if map is
 // null), S >= s.  map is a device array.
 hipError_t copy_cross(const __half *src, const uint32_t *map, int n_dst, int H, int s, int hd, __half *dst, int S,

@@ -229,6 +229,69 @@ Linear Model::load_linear(GgufFile &g, const std::string &name, int n, int k) {
     return l;
 }
 
+// dec.blk.{i}{suffix} for i < layers, rows stacked layer after layer (same GGUF type)
+Linear Model::load_stacked(GgufFile &g, const std::string &suffix, int layers, int n, int k) {
+    Linear l;
+    if (layers <= 0) return l;
+    std::vector<uint8_t> rows;
+    std::vector<float> bias(size_t(layers) * n);
+    uint32_t type = 0;
+    for (int i = 0; i < layers; ++i) {
+        const std::string p = "dec.blk." + std::to_string(i) + suffix;
+        const GgufTensorInfo *t = matrix_info(g, p + ".weight", n, k);
+        if (i == 0) type = t->type;
+        if (t->type != type) fail(ERR_FORMAT, p + ".weight: type differs from layer 0");
+        const size_t rb = size_t(type_bytes(type, int64_t(n) * k));
+        rows.insert(rows.end(), g.tensor_data(*t), g.tensor_data(*t) + rb);
+        const GgufTensorInfo *b = g.tensor(p + ".bias");
+        if (!b) fail(ERR_FORMAT, "missing tensor " + p + ".bias");
+        if (b->numel() != n || !dequantize(b->type, g.tensor_data(*b), n, bias.data() + size_t(i) * n))
+            fail(ERR_FORMAT, "tensor " + p + ".bias: bad shape or type");
+    }
+    const int N = layers * n;
+    std::vector<uint8_t> host(planes_bytes(type, N, k));
+    size_t off_s, off_d, total;
+    if (!layout_planes(type, N, k, rows.data(), host.data(), &off_s, &off_d, &total))
+        fail(ERR_FORMAT, "dec.blk.*" + suffix + ": row length not a whole number of blocks");
+    uint8_t *d = static_cast<uint8_t *>(dev_alloc(total, ("dec.blk.*" + suffix).c_str()));
+    owned_.push_back(d);
+    check_hip(hipMemcpy(d, host.data(), total, hipMemcpyHostToDevice), "upload");
+    l.w.type = type;
+    l.w.N = N;
+    l.w.K = k;
+    l.w.q = d;
+    l.w.s = d + off_s;
+    l.w.d = d + off_d;
+    l.w.bytes = total;
+    l.b = static_cast<float *>(dev_alloc(bias.size() * 4, ("dec.blk.*" + suffix + " bias").c_str()));
+    owned_.push_back(l.b);
+    check_hip(hipMemcpy(l.b, bias.data(), bias.size() * 4, hipMemcpyHostToDevice), "upload");
+    weight_bytes += total + bias.size() * 4;
+    return l;
+}
+
+DevMatrix rows_view(const DevMatrix &w, int r0, int n) {
+    TypeInfo ti;
+    type_info(w.type, &ti);
+    const size_t nb = size_t(w.K / ti.block_elems), b0 = size_t(r0) * nb;
+    DevMatrix v = w;
+    v.N = n;
+    v.lm = nullptr;
+    v.bytes = size_t(n) * nb * ti.block_bytes;
+    if (w.type == GGML_Q6_K) {  // planes: quants 192, scales 16, d 2 bytes per block
+        v.q = w.q + b0 * 192;
+        v.s = w.s + b0 * 16;
+        v.d = w.d + b0 * 2;
+    } else if (w.type == GGML_Q8_0) {  // quants 32, d 2 bytes per block
+        v.q = w.q + b0 * 32;
+        v.s = v.d = w.d + b0 * 2;
+    } else {
+        v.q = w.q + b0 * ti.block_bytes;
+        v.s = v.d = v.q + v.bytes;
+    }
+    return v;
+}
+
 LNorm Model::load_ln(GgufFile &g, const std::string &name, int d) {
     LNorm l;
     l.g = upload_f32(g, name + ".weight", d);
@@ -323,13 +386,13 @@ void Model::load(const std::string &path) {
         l.out = load_linear(g, p + ".attn_out", d, d);
         l.cross_norm = load_ln(g, p + ".cross_attn_norm", d);
         l.cross_q = load_linear(g, p + ".cross_attn_q", d, d);
-        l.cross_kv = load_linear(g, p + ".cross_attn_kv", 2 * d, d);
         l.cross_out = load_linear(g, p + ".cross_attn_out", d, d);
         l.ffn_norm = load_ln(g, p + ".ffn_norm", d);
         l.up = load_linear(g, p + ".ffn_up", cfg.decoder_ffn, d);
         l.down = load_linear(g, p + ".ffn_down", d, cfg.decoder_ffn);
         dec.push_back(l);
     }
+    cross_kv = load_stacked(g, ".cross_attn_kv", cfg.decoder_layers, 2 * d, d);
     enc_norm = load_ln(g, "enc.output_norm", d);
     dec_norm = load_ln(g, "dec.output_norm", d);
     // src/model.rs:403-412: nllb.shortlist.{code} = ids, lm_head.{code}.weight = their rows
@@ -441,7 +504,10 @@ std::unique_ptr<Batch> Model::encode(const std::vector<std::vector<uint32_t>> &s
     const size_t n_ids = (size_t(M) * 4 + 255) & ~size_t(255), n_lens = (size_t(b) * 4 + 255) & ~size_t(255);
     const size_t n_act = (size_t(M) * d * 4 + 255) & ~size_t(255);
     const size_t n_qkv = (size_t(M) * std::max(3 * d, f) * 4 + 255) & ~size_t(255);
-    const size_t n_kv = (size_t(M) * 2 * d * 4 + 255) & ~size_t(255);
+    // cross K/V of all decoder layers per GEMM while the f32 staging stays <= 128 MB
+    const int L = int(dec.size()), per_layer = int(std::min<size_t>(std::max<size_t>(size_t(L), 1),
+                                                    std::max<size_t>(1, (size_t(128) << 20) / (size_t(M) * 2 * d * 4))));
+    const size_t n_kv = (size_t(M) * 2 * d * 4 * per_layer + 255) & ~size_t(255);
     // lazy embeddings: the batch's token_embd rows, gathered on the host (src/model.rs:269-273)
     const size_t n_rows = embed.q ? 0 : (planes_bytes(embed.type, M, d) + 255) & ~size_t(255);
     const size_t need = 2 * n_ids + n_lens + 3 * n_act + n_qkv + n_kv + n_rows;
@@ -498,13 +564,17 @@ std::unique_ptr<Batch> Model::encode(const std::vector<std::vector<uint32_t>> &s
     const int Hd = cfg.decoder_heads, hdd = d / Hd;
     const size_t kv_elems = size_t(M) * d;
     out->block = dev_alloc(std::max<size_t>(dec.size(), 1) * 2 * kv_elems * 2, "cross K/V");
-    for (size_t i = 0; i < dec.size(); ++i) {
-        const DecLayer &l = dec[i];
-        __half *K = static_cast<__half *>(out->block) + 2 * i * kv_elems, *V = K + kv_elems;
-        out->ck.push_back(K);
-        out->cv.push_back(V);
-        matmul(l.cross_kv, h, M, kv, false, nullptr);
-        check_hip(split_cross_kv(kv, b, s, Hd, hdd, K, V, st), "split_cross_kv");
+    __half *K0 = static_cast<__half *>(out->block);
+    for (int i = 0; i < L; ++i) {
+        out->ck.push_back(K0 + 2 * size_t(i) * kv_elems);
+        out->cv.push_back(K0 + (2 * size_t(i) + 1) * kv_elems);
+    }
+    for (int l0 = 0; l0 < L; l0 += per_layer) {  // layers [l0, l0 + nl) in one GEMM
+        const int nl = std::min(per_layer, L - l0);
+        const Linear part{rows_view(cross_kv.w, l0 * 2 * d, nl * 2 * d), cross_kv.b + size_t(l0) * 2 * d};
+        matmul(part, h, M, kv, false, nullptr);
+        check_hip(split_cross_kv(kv, b, s, Hd, hdd, nl, K0 + 2 * size_t(l0) * kv_elems, kv_elems, st),
+                  "split_cross_kv");
     }
     check_hip(hipStreamSynchronize(st), "encode");
     return out;

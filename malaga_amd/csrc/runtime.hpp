@@ -58,7 +58,7 @@ struct EncLayer {
 };
 struct DecLayer {
     LNorm attn_norm, cross_norm, ffn_norm;
-    Linear qkv, out, cross_q, cross_kv, cross_out, up, down;
+    Linear qkv, out, cross_q, cross_out, up, down;  // cross_attn_kv: Model::cross_kv
 };
 
 // Reduced LM head of one target language (src/model.rs:229-250): rows of token_embd
@@ -171,6 +171,9 @@ class Model {
     std::vector<EncLayer> enc;
     std::vector<DecLayer> dec;
     LNorm enc_norm, dec_norm;
+    // every decoder layer's cross_attn_kv [2d, d] stacked layer after layer into one
+    // [L * 2d, d] matrix (and bias), so that the encoder computes all cross K/V at once
+    Linear cross_kv;
     std::vector<std::unique_ptr<Shortlist>> shortlists;  // src/model.rs:403-412
     size_t weight_bytes = 0;
     GraphCache graphs;
@@ -218,6 +221,7 @@ class Model {
     // head: also the lane-major quant copy of a q6_K LM head (DevMatrix::lm)
     DevMatrix upload_matrix(class GgufFile &g, const std::string &name, int n, int k, bool head = false);
     void upload_lane_major(DevMatrix &m, const uint8_t *q_plane);
+    Linear load_stacked(class GgufFile &g, const std::string &suffix, int layers, int n, int k);
     void matmul(const Linear &l, const float *x, int rows, float *y, bool relu, const float *resid);
     void step_fused(StaticState &st);
     void lm_head(StaticState &st, bool greedy_mode, int mask_id);
