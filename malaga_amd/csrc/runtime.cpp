@@ -1040,6 +1040,23 @@ std::vector<std::vector<uint32_t>> Model::beam(const Batch &src, uint32_t tgt_la
     float *scratch = tmp.get<float>(logsoftmax_topk_scratch(bk, k) / 4, "topk scratch");
     float *d_vals = tmp.get<float>(size_t(bk) * k, "topk vals");
     uint32_t *d_idx = tmp.get<uint32_t>(size_t(bk) * k, "topk idx");
+    // Pinned staging: the per-step copies are asynchronous, and the host waits once per
+    // step (for the top-k).  A buffer is rewritten only after that wait, which follows
+    // the previous step's copies out of it on the stream.
+    struct Pinned {
+        void *p = nullptr;
+        ~Pinned() {
+            if (p) (void)hipHostFree(p);
+        }
+    } pin_vals, pin_idx, pin_rows, pin_next;
+    auto pinned = [&](Pinned &b, size_t bytes) {
+        check_hip(hipHostMalloc(&b.p, bytes, hipHostMallocDefault), "pinned staging");
+        return b.p;
+    };
+    float *h_vals = static_cast<float *>(pinned(pin_vals, size_t(bk) * k * 4));
+    uint32_t *h_idx = static_cast<uint32_t *>(pinned(pin_idx, size_t(bk) * k * 4));
+    uint32_t *h_rows = static_cast<uint32_t *>(pinned(pin_rows, size_t(bk) * st->m * 4));
+    uint32_t *h_next = static_cast<uint32_t *>(pinned(pin_next, size_t(bk) * 4));
 
     auto topk = [&] {
         check_hip(logsoftmax_topk(st->logits, bk, V, k, mask_id, scratch, d_vals, d_idx, s), "topk");
@@ -1093,11 +1110,11 @@ std::vector<std::vector<uint32_t>> Model::beam(const Batch &src, uint32_t tgt_la
     std::vector<std::vector<Hyp>> done(static_cast<size_t>(b));
     std::vector<uint8_t> is_done(static_cast<size_t>(b), 0);
     auto penalty = [&](size_t len) { return std::pow(float(std::max<size_t>(len, 1)), lp); };
-    std::vector<float> vals(static_cast<size_t>(bk) * k);
-    std::vector<uint32_t> idx(static_cast<size_t>(bk) * k);
+    const float *vals = h_vals;
+    const uint32_t *idx = h_idx;
     for (int stp = 1; stp <= max_new; ++stp) {
-        check_hip(hipMemcpyAsync(vals.data(), d_vals, vals.size() * 4, hipMemcpyDeviceToHost, s), "D2H");
-        check_hip(hipMemcpyAsync(idx.data(), d_idx, idx.size() * 4, hipMemcpyDeviceToHost, s), "D2H");
+        check_hip(hipMemcpyAsync(h_vals, d_vals, size_t(bk) * k * 4, hipMemcpyDeviceToHost, s), "D2H");
+        check_hip(hipMemcpyAsync(h_idx, d_idx, size_t(bk) * k * 4, hipMemcpyDeviceToHost, s), "D2H");
         check_hip(hipStreamSynchronize(s), "sync");
         std::vector<uint32_t> reorder, next;
         for (int sn = 0; sn < b; ++sn) {
@@ -1151,8 +1168,10 @@ std::vector<std::vector<uint32_t>> Model::beam(const Batch &src, uint32_t tgt_la
             for (int j = 0; j < m; ++j) dst[j] = j <= stp ? par[j] : uint32_t(r);
         }
         rows_map.swap(rows_next);
-        h2d(st->rows, rows_map, s);
-        h2d(st->ids, next, s);
+        std::copy(rows_map.begin(), rows_map.end(), h_rows);
+        std::copy(next.begin(), next.end(), h_next);
+        check_hip(hipMemcpyAsync(st->rows, h_rows, rows_map.size() * 4, hipMemcpyHostToDevice, s), "H2D");
+        check_hip(hipMemcpyAsync(st->ids, h_next, next.size() * 4, hipMemcpyHostToDevice, s), "H2D");
         advance();
     }
     std::vector<std::vector<uint32_t>> res(static_cast<size_t>(b));
