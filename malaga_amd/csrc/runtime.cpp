@@ -34,6 +34,42 @@ void h2d(T *dst, const std::vector<T> &src, hipStream_t st) {
     check_hip(hipStreamSynchronize(st), "H2D sync");
 }
 
+}  // namespace
+
+Staging::~Staging() {
+    if (pending_) (void)hipEventSynchronize(ev_);
+    if (ev_) (void)hipEventDestroy(ev_);
+    if (buf_) (void)hipHostFree(buf_);
+}
+
+void Staging::upload(void *dst, const void *src, size_t n, hipStream_t st) {
+    if (!n) return;
+    const size_t need = (n + 255) & ~size_t(255);
+    if (off_ + need > cap_) {
+        if (pending_) check_hip(hipEventSynchronize(ev_), "staging wait");
+        pending_ = false;
+        off_ = 0;
+        if (need > cap_) {
+            if (buf_) (void)hipHostFree(buf_);
+            buf_ = nullptr;
+            cap_ = 0;
+            void *p = nullptr;
+            const size_t cap = std::max(need, size_t(1) << 20);
+            check_hip(hipHostMalloc(&p, cap, hipHostMallocDefault), "pinned staging");
+            buf_ = static_cast<uint8_t *>(p);
+            cap_ = cap;
+        }
+    }
+    if (!ev_) check_hip(hipEventCreateWithFlags(&ev_, hipEventDisableTiming), "event");
+    std::memcpy(buf_ + off_, src, n);
+    check_hip(hipMemcpyAsync(dst, buf_ + off_, n, hipMemcpyHostToDevice, st), "H2D");
+    off_ += need;
+    check_hip(hipEventRecord(ev_, st), "event");
+    pending_ = true;
+}
+
+namespace {
+
 // Device buffers freed at scope exit.
 struct DevTemp {
     std::vector<void *> p;
@@ -531,17 +567,18 @@ std::unique_ptr<Batch> Model::encode(const std::vector<std::vector<uint32_t>> &s
     float *att = static_cast<float *>(carve(n_act));
     float *qkv = static_cast<float *>(carve(n_qkv));
     float *kv = static_cast<float *>(carve(n_kv));
-    h2d(d_pidx, pidx, st);
+    Staging &up = ctx->staging;
+    up.upload(d_pidx, pidx.data(), pidx.size() * 4, st);
     out->ids = ids;
-    h2d(d_lens, out->lens, st);
+    up.upload(d_lens, out->lens.data(), out->lens.size() * 4, st);
     if (embed.q) {
-        h2d(d_ids, ids, st);
+        up.upload(d_ids, ids.data(), ids.size() * 4, st);
         check_hip(embed_pos_rows(embed, d_ids, d_pidx, M, pos, embed_scale, x, st), "embed");
     } else {
         const DevMatrix rows = gather_embed(ids.data(), M, static_cast<uint8_t *>(carve(n_rows)));
         std::vector<uint32_t> iota(static_cast<size_t>(M));
         std::iota(iota.begin(), iota.end(), 0u);
-        h2d(d_ids, iota, st);
+        up.upload(d_ids, iota.data(), iota.size() * 4, st);
         check_hip(embed_pos_rows(rows, d_ids, d_pidx, M, pos, embed_scale, x, st), "embed");
     }
     // pre-LN layers; each residual projection also produces the next LayerNorm (in the
@@ -576,7 +613,8 @@ std::unique_ptr<Batch> Model::encode(const std::vector<std::vector<uint32_t>> &s
         check_hip(split_cross_kv(kv, b, s, Hd, hdd, nl, K0 + 2 * size_t(l0) * kv_elems, kv_elems, st),
                   "split_cross_kv");
     }
-    check_hip(hipStreamSynchronize(st), "encode");
+    // no wait: the batch's users run on the same stream
+    check_hip(hipGetLastError(), "encode");
     return out;
 }
 
@@ -661,14 +699,15 @@ void Model::reset_state(StaticState &st, const Batch &src, const std::vector<uin
     const int H = cfg.decoder_heads, hd = cfg.d_model / H, n = int(row_of.size());
     if (n > st.b) fail(ERR_INVALID, "reset_state: more source rows than state rows");
     uint32_t *d_map = st.row_src;
-    h2d(d_map, row_of, s);
+    Staging &up = ctx->staging;
+    up.upload(d_map, row_of.data(), row_of.size() * 4, s);
     for (size_t l = 0; l < st.ck.size(); ++l) {
         check_hip(copy_cross(src.ck[l], d_map, n, H, src.s, hd, st.ck[l], st.s, s), "copy_cross");
         check_hip(copy_cross(src.cv[l], d_map, n, H, src.s, hd, st.cv[l], st.s, s), "copy_cross");
     }
     std::vector<uint32_t> lens(static_cast<size_t>(st.b), 1u);
     for (int r = 0; r < n; ++r) lens[r] = src.lens[row_of[r]];
-    h2d(st.lens, lens, s);
+    up.upload(st.lens, lens.data(), lens.size() * 4, s);
     check_hip(fill_u32(st.ids, start, size_t(st.b), s), "fill");
     check_hip(fill_u32(st.step, 0, 1, s), "fill");
     if (st.sl) {
@@ -679,7 +718,7 @@ void Model::reset_state(StaticState &st, const Batch &src, const std::vector<uin
         std::vector<uint32_t> ids(size_t(st.b) * st.s, pad);
         for (int r = 0; r < n; ++r)
             std::copy_n(src.ids.begin() + size_t(row_of[r]) * src.s, src.s, ids.begin() + size_t(r) * st.s);
-        h2d(st.src_ids, ids, s);
+        up.upload(st.src_ids, ids.data(), ids.size() * 4, s);
         if (embed.q) {
             check_hip(embed_rows(embed, st.src_ids, st.b * st.s, st.src_emb, s), "embed_rows");
         } else {
@@ -691,7 +730,7 @@ void Model::reset_state(StaticState &st, const Batch &src, const std::vector<uin
     }
     std::vector<uint8_t> fin(static_cast<size_t>(st.b));
     for (int r = 0; r < st.b; ++r) fin[r] = r >= n;
-    h2d(st.finished, fin, s);
+    up.upload(st.finished, fin.data(), fin.size(), s);
 }
 
 // src/graph.rs:121-130 (set_ids): every row's next input is vocabulary id `id`.
@@ -949,7 +988,7 @@ std::vector<std::vector<uint32_t>> GraphCache::run(const Batch &src, uint32_t tg
     if (sl) m.set_shortlist_input(st, tgt_lang);
     std::vector<uint8_t> fin(static_cast<size_t>(st.b));
     for (int r = 0; r < st.b; ++r) fin[r] = r >= n;
-    h2d(st.finished, fin, s);
+    m.ctx->staging.upload(st.finished, fin.data(), fin.size(), s);
     one_step();
     int steps = 2;
     const int max_steps = std::min(max_new + 1, st.m);

@@ -34,11 +34,28 @@ void *dev_alloc(size_t bytes, const char *what);
 void dev_free(void *p);
 void set_fail_alloc_after(long n);  // < 0 disables
 
+// Pinned staging for the small host-to-device uploads of a batch (ids, lengths, flags):
+// the copies are asynchronous, and a region of the buffer is rewritten only after the
+// event recorded behind every earlier copy out of it has completed.
+class Staging {
+  public:
+    ~Staging();
+    // Queues a copy of n bytes from host src to device dst on st (src may be reused at once).
+    void upload(void *dst, const void *src, size_t n, hipStream_t st);
+
+  private:
+    uint8_t *buf_ = nullptr;
+    size_t cap_ = 0, off_ = 0;
+    hipEvent_t ev_ = nullptr;
+    bool pending_ = false;
+};
+
 struct Context {
     int device = 0;
     hipStream_t stream = nullptr;
     std::mutex mu;  // one caller at a time per context (src/graph.rs:152-155)
     float *gemm_ws = nullptr;  // split-K workspace of the MFMA GEMM (kGemmWorkspaceBytes)
+    Staging staging;           // uploads on `stream`
     // Allocates the workspace on first use (never inside a graph capture: the first
     // eager step or the encoder reaches it first).
     float *gemm_workspace();
