@@ -281,16 +281,23 @@ __global__ void k_split_cross_kv(const float *kv, int b, int s, int H, int hd, i
 }
 
 // dst row r (< n_dst) <- src row map[r] (or r when map is null)
-__global__ void k_copy_cross(const __half *src, const uint32_t *map, int n_dst, int H, int s, int hd, __half *dst,
-                             int S) {
-    const size_t per_row = size_t(H) * s * hd, total = size_t(n_dst) * per_row;
+// Every layer's cross K and V in one launch, 16 bytes per thread: pair p of the source
+// [b][H][s][hd] at src0 + p * src_pair -> pair p of the state [n][H][S][hd] at
+// dst0 + p * dst_pair; state row r takes source row map[r] (or r).
+__global__ void k_copy_cross(const __half *src0, size_t src_pair, const uint32_t *map, int n_dst, int H, int s, int hd,
+                             __half *dst0, size_t dst_pair, int S, int pairs) {
+    const int hv = hd / 8;
+    const size_t per_row = size_t(H) * s * hv, per_pair = size_t(n_dst) * per_row, total = per_pair * pairs;
     for (size_t idx = blockIdx.x * size_t(blockDim.x) + threadIdx.x; idx < total; idx += size_t(gridDim.x) * blockDim.x) {
-        const size_t r = idx / per_row, rem = idx % per_row;
-        const int e = int(rem % hd);
-        const size_t hj = rem / hd;
+        const size_t p = idx / per_pair, rem0 = idx % per_pair;
+        const size_t r = rem0 / per_row, rem = rem0 % per_row;
+        const int ev = int(rem % hv);
+        const size_t hj = rem / hv;
         const int j = int(hj % s), hh = int(hj / s);
         const size_t sr = map ? map[r] : r;
-        dst[((r * H + hh) * S + j) * hd + e] = src[sr * per_row + rem];
+        const uint4 *sp = reinterpret_cast<const uint4 *>(src0 + p * src_pair) + sr * per_row + rem;
+        uint4 *dp = reinterpret_cast<uint4 *>(dst0 + p * dst_pair) + ((r * H + hh) * S + j) * hv + ev;
+        *dp = *sp;
     }
 }
 
@@ -761,11 +768,15 @@ hipError_t split_cross_kv(const float *kv, int b, int s, int H, int hd, int L, _
     return hipGetLastError();
 }
 
-hipError_t copy_cross(const __half *src, const uint32_t *map, int n_dst, int H, int s, int hd, __half *dst, int S,
-                      hipStream_t st) {
-    const size_t total = size_t(n_dst) * H * s * hd;
+hipError_t copy_cross(const __half *src0, size_t src_pair, const uint32_t *map, int n_dst, int H, int s, int hd,
+                      __half *dst0, size_t dst_pair, int S, int pairs, hipStream_t st) {
+    if (hd % 8 || src_pair % 8 || dst_pair % 8 || reinterpret_cast<uintptr_t>(src0) % 16 ||
+        reinterpret_cast<uintptr_t>(dst0) % 16 || s > S)
+        return hipErrorInvalidValue;
+    const size_t total = size_t(pairs) * n_dst * H * s * (hd / 8);
     if (!total) return hipSuccess;
-    hipLaunchKernelGGL(k_copy_cross, dim3(grid_1d(total, 256)), dim3(256), 0, st, src, map, n_dst, H, s, hd, dst, S);
+    hipLaunchKernelGGL(k_copy_cross, dim3(grid_1d(total, 256)), dim3(256), 0, st, src0, src_pair, map, n_dst, H, s, hd,
+                       dst0, dst_pair, S, pairs);
     return hipGetLastError();
 }
 

@@ -144,10 +144,12 @@ hipError_t split_cross_kv(const float *kv, int b, int s, int H, int hd, int L, _
                           hipStream_t st);
 // rows [r0, r0 + n) of w as a matrix of their own (block-major planes; no lane-major copy)
 DevMatrix rows_view(const DevMatrix &w, int r0, int n);
-// dst [.][H][S][hd] row r (< n_dst) <- src [.][H][s][hd] row map[r] (row r if map is
-// null), S >= s.  map is a device array.
-hipError_t copy_cross(const __half *src, const uint32_t *map, int n_dst, int H, int s, int hd, __half *dst, int S,
-                      hipStream_t st);
+// For each of `pairs` arrays (every layer's cross K and V): dst0 + p * dst_pair
+// [.][H][S][hd] row r (< n_dst) <- src0 + p * src_pair [.][H][s][hd] row map[r] (row r if
+// map is null), S >= s.  map is a device array; hd, the pair strides and the bases are
+// 16-byte multiples.
+hipError_t copy_cross(const __half *src0, size_t src_pair, const uint32_t *map, int n_dst, int H, int s, int hd,
+                      __half *dst0, size_t dst_pair, int S, int pairs, hipStream_t st);
 // Argmax over logits [b][V] (row stride ldl) into pv/pi [b][parts].
 hipError_t argmax_partial(const float *logits, int b, int V, int ldl, int mask_id, float *pv, uint32_t *pi,
                           int parts, hipStream_t st);

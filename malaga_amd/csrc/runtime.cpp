@@ -638,16 +638,18 @@ std::unique_ptr<StaticState> Model::new_state(int b, int s, int m, bool logits, 
     st->out = static_cast<uint32_t *>(get(size_t(b) * m * 4, "out"));
     st->finished = static_cast<uint8_t *>(get(size_t(b), "finished"));
     st->row_src = static_cast<uint32_t *>(get(size_t(b) * 4, "source rows"));
+    // one block each for the self and the cross K/V of every layer (layer l: K, then V);
+    // slots past the step are read (and masked) by the fused attention: keep them finite
+    const size_t self_pair = size_t(b) * H * m * hd, cross_pair = size_t(b) * H * s * hd;
+    __half *self_kv = static_cast<__half *>(get(std::max<size_t>(2 * L * self_pair, 1) * 2, "self K/V"));
+    __half *cross_kv = static_cast<__half *>(get(std::max<size_t>(2 * L * cross_pair, 1) * 2, "cross K/V"));
+    check_hip(hipMemsetAsync(self_kv, 0, 2 * L * self_pair * 2, ctx->stream), "memset");
+    check_hip(hipMemsetAsync(cross_kv, 0, 2 * L * cross_pair * 2, ctx->stream), "memset");
     for (int i = 0; i < L; ++i) {
-        st->kc.push_back(static_cast<__half *>(get(size_t(b) * H * m * hd * 2, "self K")));
-        st->vc.push_back(static_cast<__half *>(get(size_t(b) * H * m * hd * 2, "self V")));
-        // slots past the step are read (and masked) by the fused attention: keep them finite
-        check_hip(hipMemsetAsync(st->kc.back(), 0, size_t(b) * H * m * hd * 2, ctx->stream), "memset");
-        check_hip(hipMemsetAsync(st->vc.back(), 0, size_t(b) * H * m * hd * 2, ctx->stream), "memset");
-        st->ck.push_back(static_cast<__half *>(get(size_t(b) * H * s * hd * 2, "cross K")));
-        st->cv.push_back(static_cast<__half *>(get(size_t(b) * H * s * hd * 2, "cross V")));
-        check_hip(hipMemsetAsync(st->ck.back(), 0, size_t(b) * H * s * hd * 2, ctx->stream), "memset");
-        check_hip(hipMemsetAsync(st->cv.back(), 0, size_t(b) * H * s * hd * 2, ctx->stream), "memset");
+        st->kc.push_back(self_kv + 2 * i * self_pair);
+        st->vc.push_back(self_kv + (2 * i + 1) * self_pair);
+        st->ck.push_back(cross_kv + 2 * i * cross_pair);
+        st->cv.push_back(cross_kv + (2 * i + 1) * cross_pair);
     }
     st->x = static_cast<float *>(get(size_t(b) * d * 4, "x"));
     st->xb = static_cast<float *>(get(size_t(b) * d * 4, "x (second buffer)"));
@@ -701,10 +703,11 @@ void Model::reset_state(StaticState &st, const Batch &src, const std::vector<uin
     uint32_t *d_map = st.row_src;
     Staging &up = ctx->staging;
     up.upload(d_map, row_of.data(), row_of.size() * 4, s);
-    for (size_t l = 0; l < st.ck.size(); ++l) {
-        check_hip(copy_cross(src.ck[l], d_map, n, H, src.s, hd, st.ck[l], st.s, s), "copy_cross");
-        check_hip(copy_cross(src.cv[l], d_map, n, H, src.s, hd, st.cv[l], st.s, s), "copy_cross");
-    }
+    // every layer's K and V in one launch: both blocks hold layer l's K, then its V
+    if (!st.ck.empty())
+        check_hip(copy_cross(src.ck[0], size_t(src.b) * src.s * cfg.d_model, d_map, n, H, src.s, hd, st.ck[0],
+                             size_t(st.b) * H * st.s * hd, st.s, 2 * int(st.ck.size()), s),
+                  "copy_cross");
     std::vector<uint32_t> lens(static_cast<size_t>(st.b), 1u);
     for (int r = 0; r < n; ++r) lens[r] = src.lens[row_of[r]];
     up.upload(st.lens, lens.data(), lens.size() * 4, s);
