@@ -387,7 +387,7 @@ def bench_kernels(T, lm_blocks: np.ndarray):
             rows.append(r)
             log(f"gemv {tname} {sname} {N}x{K}: {r['us']:.2f} us {r['GBps']:.0f} GB/s")
     # the LM head the q4_k_m model actually runs: q6_K, fused argmax epilogue
-    lm = gb.run(14, lm_blocks, 256206, 1024, launches=40, argmax=True)
+    lm = gb.run(14, lm_blocks, 256206, 1024, launches=200, argmax=True)  # as --roofline-only
     lm.update(type="q6_K", shape="256206x1024", name="lm_head_argmax")
     rows.append(lm)
     log(f"gemv_argmax q6_K lm_head: {lm['us']:.2f} us {lm['GBps']:.0f} GB/s")
