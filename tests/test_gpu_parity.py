@@ -85,6 +85,25 @@ def test_beam_matches_oracle(tiny_gguf, kq_gguf, models, k):
         assert got == gpu.generate(src, tgt)  # beam 1 == greedy (pipeline.rs:59-69)
 
 
+@pytest.mark.parametrize("preset", ["f32", "q8_0"])
+def test_wide_beam_is_exhaustive_search(model_dir, models, preset):
+    """Beam 8 over a vocabulary of 8 for two steps prunes nothing, so the GPU's beam
+    search must return the best of all hypotheses (tests/test_oracle_beam.py), at
+    length penalties under which hypotheses of 0, 1 and 2 tokens win."""
+    from tests.test_oracle_beam import PENALTIES, WIDE_SOURCES, WIDE_TGT, exhaustive, wide_model
+
+    gpu, orc = models(wide_model(model_dir, preset))
+    for p in PENALTIES:
+        opts = M.GenOptions(beam_size=8, max_new_tokens=2, length_penalty=p)
+        for graph in (True, False):
+            opts.fused = graph
+            got = gpu.generate(WIDE_SOURCES, WIDE_TGT, opts)
+            for src, row in zip(WIDE_SOURCES, got):
+                want, gap = exhaustive(orc, src, WIDE_TGT, p)
+                assert gap > 1e-3
+                assert row == want, (src, p, graph)
+
+
 def test_beam_graph_replay_matches_eager(kq_gguf, models):
     """The beam step is one captured step + top-k replayed every step; eager calls
     between the graph calls check that every replay gives the eager tokens."""
