@@ -83,8 +83,8 @@ template <int T>
 __global__ __launch_bounds__(kLnThreads) void k_embed_pos_ln(const uint8_t *q, const uint8_t *s, const uint8_t *dp,
                                                              const uint32_t *ids, const float *pos,
                                                              const uint32_t *step, uint32_t base, float scale, int d,
-                                                             const float *g, const float *b, float eps, float *x,
-                                                             float *h, SrcEmb src) {
+                                                             uint32_t last, const float *g, const float *b, float eps,
+                                                             float *x, float *h, SrcEmb src) {
     extern __shared__ float e[];
     __shared__ float sh[16];
     const int row = blockIdx.x;
@@ -94,7 +94,9 @@ __global__ __launch_bounds__(kLnThreads) void k_embed_pos_ln(const uint8_t *q, c
         for (int i = threadIdx.x; i < d; i += blockDim.x) e[i] = er[i];
         __syncthreads();
     } else {
-        embed_row<T>(q, s, dp, d, ids[row], e);
+        // a token the device produced: clamped to the table (an all-NaN row of logits
+        // yields 0xffffffff, malaga.cu:257-258), so a bad model cannot read past it
+        embed_row<T>(q, s, dp, d, min(ids[row], last), e);
     }
     const float *pr = pos + size_t(*step + base) * d;
     const size_t off = size_t(row) * d;
@@ -661,7 +663,7 @@ hipError_t launch_embed_pos_ln(const DevMatrix &E, const uint32_t *ids, int rows
                                const uint32_t *step, uint32_t base, float scale, const float *g, const float *b,
                                float eps, float *x, float *h, hipStream_t st, const SrcEmb &src) {
     hipLaunchKernelGGL(k_embed_pos_ln<T>, dim3(rows), dim3(kLnThreads), E.K * sizeof(float), st, E.q, E.s, E.d, ids,
-                       pos, step, base, scale, E.K, g, b, eps, x, h, src);
+                       pos, step, base, scale, E.K, uint32_t(E.N - 1), g, b, eps, x, h, src);
     return hipGetLastError();
 }
 

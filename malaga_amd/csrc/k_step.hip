@@ -42,6 +42,7 @@ struct StepArgs {
     // embedding prologue: x = E[ids[r]] * emb_scale + pos[*step + pos_base]
     const uint8_t *eq, *es, *ed;
     const uint32_t *ids;
+    uint32_t elast;  // last row of the embedding: device-produced ids are clamped to it
     // ... or, where src_row[r] != kNoRow, x = src_emb[r][src_row[r]] * emb_scale + pos (a copied source token)
     const float *src_emb;
     const uint32_t *src_row;
@@ -181,7 +182,7 @@ __device__ __forceinline__ void resid_ln_prologue(const StepArgs &a, const PreLo
 #pragma unroll
                     for (int j = 0; j < 16; ++j) e[j] = er[j];
                 } else {
-                    dequant16<ET>(a.eq, a.es, a.ed, d, int(a.ids[bi]), k0, e);
+                    dequant16<ET>(a.eq, a.es, a.ed, d, int(min(a.ids[bi], a.elast)), k0, e);
                 }
 #pragma unroll
                 for (int j = 0; j < 16; ++j) xs[bi * lds_pad(d) + lds_pad(k0 + j)] = e[j] * a.emb_scale + pr[k0 + j];
@@ -573,6 +574,7 @@ hipError_t step_qkv(const DevMatrix &w, const float *bias, int nb, int d, const 
         a.eq = emb->q;
         a.es = emb->s;
         a.ed = emb->d;
+        a.elast = uint32_t(emb->N - 1);
     }
     a.ids = ids;
     a.pos = pos;
