@@ -67,9 +67,11 @@ constexpr int kPreParts = 8;  // partial sums a preloading residual prologue kee
 
 // Operands of the residual prologue, loaded before the weights when they fit
 // (rows <= 2, one float4 slot per row, P <= kPreParts).
-struct PreLoads {
-    float4 part[2][kPreParts], x[2], pb, gr, br;
+template <int R = 2>
+struct PreLoadsR {
+    float4 part[R][kPreParts], x[R], pb, gr, br;
 };
+using PreLoads = PreLoadsR<2>;
 
 __device__ __forceinline__ void add4(float4 &a, const float4 &b) {
     a.x += b.x;
@@ -80,10 +82,11 @@ __device__ __forceinline__ void add4(float4 &a, const float4 &b) {
 
 __device__ __forceinline__ float4 ld4(const float *p, int f) { return reinterpret_cast<const float4 *>(p)[f]; }
 
-__device__ __forceinline__ void preload(const StepArgs &a, PreLoads &L) {
+template <int R = 2>
+__device__ __forceinline__ void preload(const StepArgs &a, PreLoadsR<R> &L) {
     const int f = min(int(threadIdx.x), (a.d >> 2) - 1);
 #pragma unroll
-    for (int bi = 0; bi < 2; ++bi) {
+    for (int bi = 0; bi < R; ++bi) {
         if (bi >= a.nb) break;
 #pragma unroll
         for (int p = 0; p < kPreParts; ++p)
@@ -98,15 +101,18 @@ __device__ __forceinline__ void preload(const StepArgs &a, PreLoads &L) {
 // LayerNorm of the rows held in registers (thread t owns float4 slots t, t + 256,
 // ... of each row), written to xs[nb][d] (LDS).  Mean and variance come from one
 // pass of f64 sums of x and x^2 (biased variance).
-__device__ __forceinline__ void ln_to_lds(const float4 (&v)[4][kMaxF4], const float4 (&gr)[kMaxF4],
-                                          const float4 (&br)[kMaxF4], int nb, int d, float eps, float *xs,
-                                          double *red) {
+// NW: waves of the workgroup (red holds 2 * 4 * NW doubles); waves past the first
+// four hold no slots and add zeros.
+// MF: float4 slots per thread and row (d <= 1024 MF).
+template <int NW = 4, int MF = kMaxF4>
+__device__ __forceinline__ void ln_to_lds(const float4 (&v)[4][MF], const float4 (&gr)[MF], const float4 (&br)[MF],
+                                          int nb, int d, float eps, float *xs, double *red) {
     const int t = threadIdx.x, nf = d >> 2, lane = t & 63, w = t >> 6;
     double s1[4] = {0.0, 0.0, 0.0, 0.0}, s2[4] = {0.0, 0.0, 0.0, 0.0};
 #pragma unroll
     for (int bi = 0; bi < 4; ++bi)
 #pragma unroll
-        for (int c = 0; c < kMaxF4; ++c)
+        for (int c = 0; c < MF; ++c)
             if (bi < nb && t + 256 * c < nf) {
                 const double x0 = v[bi][c].x, x1 = v[bi][c].y, x2 = v[bi][c].z, x3 = v[bi][c].w;
                 s1[bi] += (x0 + x1) + (x2 + x3);
@@ -118,20 +124,27 @@ __device__ __forceinline__ void ln_to_lds(const float4 (&v)[4][kMaxF4], const fl
             s1[bi] = wave_sum_f64(s1[bi]);
             s2[bi] = wave_sum_f64(s2[bi]);
             if (lane == 0) {
-                red[(2 * bi) * 4 + w] = s1[bi];
-                red[(2 * bi + 1) * 4 + w] = s2[bi];
+                red[(2 * bi) * NW + w] = s1[bi];
+                red[(2 * bi + 1) * NW + w] = s2[bi];
             }
         }
     lds_barrier();
+    // fixed-order sums; the zeros of waves 4.. leave the 4-wave value unchanged
+    auto sum_nw = [](const double *r) {
+        double q = (r[0] + r[1]) + (r[2] + r[3]);
+#pragma unroll
+        for (int k = 4; k < NW; k += 4) q += (r[k] + r[k + 1]) + (r[k + 2] + r[k + 3]);
+        return q;
+    };
 #pragma unroll
     for (int bi = 0; bi < 4; ++bi) {
         if (bi >= nb) break;
-        const double *r1 = red + 2 * bi * 4, *r2 = r1 + 4;
-        const double mean = ((r1[0] + r1[1]) + (r1[2] + r1[3])) / d;
-        const double var = fmax(((r2[0] + r2[1]) + (r2[2] + r2[3])) / d - mean * mean, 0.0);
+        const double *r1 = red + 2 * bi * NW, *r2 = r1 + NW;
+        const double mean = sum_nw(r1) / d;
+        const double var = fmax(sum_nw(r2) / d - mean * mean, 0.0);
         const float rstd = float(1.0 / sqrt(var + double(eps))), m = float(mean);
 #pragma unroll
-        for (int c = 0; c < kMaxF4; ++c)
+        for (int c = 0; c < MF; ++c)
             if (t + 256 * c < nf)
                 *reinterpret_cast<float4 *>(xs + bi * lds_pad(d) + lds_pad(4 * (t + 256 * c))) =
                     make_float4((v[bi][c].x - m) * rstd * gr[c].x + br[c].x, (v[bi][c].y - m) * rstd * gr[c].y + br[c].y,
@@ -143,16 +156,17 @@ __device__ __forceinline__ void ln_to_lds(const float4 (&v)[4][kMaxF4], const fl
 // Builds the residual stream x (PRO_RESID / PRO_RESID_PRE) or the embedded tokens
 // (PRO_EMBED) in registers, writes it to x_out (workgroup 0) and leaves
 // LayerNorm(x) in xs[nb][d] (LDS).
-template <int PRO, int ET>
-__device__ __forceinline__ void resid_ln_prologue(const StepArgs &a, const PreLoads &L, float *xs, double *red) {
+template <int PRO, int ET, int NW = 4, int MF = kMaxF4, int PR = 2>
+__device__ __forceinline__ void resid_ln_prologue(const StepArgs &a, const PreLoadsR<PR> &L, float *xs,
+                                                  double *red) {
     const int d = a.d, nb = a.nb, nf = d >> 2, nc = (nf + 255) >> 8;
     const int t = threadIdx.x;
-    float4 v[4][kMaxF4], gr[kMaxF4], br[kMaxF4];
+    float4 v[4][MF], gr[MF], br[MF];
     if constexpr (PRO == PRO_RESID_PRE) {
         gr[0] = L.gr;
         br[0] = L.br;
 #pragma unroll
-        for (int bi = 0; bi < 2; ++bi) {
+        for (int bi = 0; bi < PR; ++bi) {
             if (bi >= nb) break;
             float4 acc = L.part[bi][0];
 #pragma unroll
@@ -163,7 +177,7 @@ __device__ __forceinline__ void resid_ln_prologue(const StepArgs &a, const PreLo
         }
     } else {
 #pragma unroll
-        for (int c = 0; c < kMaxF4; ++c) {
+        for (int c = 0; c < MF; ++c) {
             if (c >= nc) break;
             const int f = min(t + 256 * c, nf - 1);
             gr[c] = ld4(a.gamma, f);
@@ -192,7 +206,7 @@ __device__ __forceinline__ void resid_ln_prologue(const StepArgs &a, const PreLo
             for (int bi = 0; bi < 4; ++bi) {
                 if (bi >= nb) break;
 #pragma unroll
-                for (int c = 0; c < kMaxF4; ++c)
+                for (int c = 0; c < MF; ++c)
                     if (c < nc)
                         v[bi][c] = *reinterpret_cast<const float4 *>(xs + bi * lds_pad(d) +
                                                                      lds_pad(4 * min(t + 256 * c, nf - 1)));
@@ -202,7 +216,7 @@ __device__ __forceinline__ void resid_ln_prologue(const StepArgs &a, const PreLo
             for (int bi = 0; bi < 4; ++bi) {
                 if (bi >= nb) break;
 #pragma unroll
-                for (int c = 0; c < kMaxF4; ++c) {
+                for (int c = 0; c < MF; ++c) {
                     if (c >= nc) break;
                     const int f = min(t + 256 * c, nf - 1);
                     float4 acc = ld4(a.part + size_t(bi) * d, f);
@@ -214,15 +228,15 @@ __device__ __forceinline__ void resid_ln_prologue(const StepArgs &a, const PreLo
             }
         }
     }
-    if (blockIdx.x == 0) {
+    if (blockIdx.x == 0 && blockIdx.y == 0) {
 #pragma unroll
         for (int bi = 0; bi < 4; ++bi)
 #pragma unroll
-            for (int c = 0; c < kMaxF4; ++c)
+            for (int c = 0; c < MF; ++c)
                 if (bi < nb && t + 256 * c < nf)
                     reinterpret_cast<float4 *>(a.x_out + size_t(bi) * d)[t + 256 * c] = v[bi][c];
     }
-    ln_to_lds(v, gr, br, nb, d, a.eps, xs, red);
+    ln_to_lds<NW, MF>(v, gr, br, nb, d, a.eps, xs, red);
 }
 
 template <int T, int B, int CPL, int PRO, int EPI, int ET>
@@ -442,6 +456,299 @@ __global__ __launch_bounds__(256) void k_attn_head(HeadArgs a) {
         for (int bi = 0; bi < nb; ++bi) a.part[(size_t(g) * nb + bi) * d + wrow] = acc[bi];
 }
 
+// ------------------------------------------- cross attention with its q projection
+
+constexpr int kXThreads = 512;  // 8 waves
+constexpr int kXItems = 4;      // (row, chunk) items of the q projection per thread
+
+// dot4u8 as one asm block: each byte is converted where it is used, so a schedule
+// cannot convert every item's bytes ahead of their products (which overflows the
+// registers of a multi-item dot); same operations, same order
+__device__ __forceinline__ float dot4u8_chain(uint32_t v, const float (&x)[4], float acc) {
+    float t0, t1, t2, t3;
+    asm("v_cvt_f32_ubyte0 %1, %5\n\t"
+        "v_cvt_f32_ubyte1 %2, %5\n\t"
+        "v_fmac_f32 %0, %1, %6\n\t"
+        "v_cvt_f32_ubyte2 %3, %5\n\t"
+        "v_fmac_f32 %0, %2, %7\n\t"
+        "v_cvt_f32_ubyte3 %4, %5\n\t"
+        "v_fmac_f32 %0, %3, %8\n\t"
+        "v_fmac_f32 %0, %4, %9"
+        : "+v"(acc), "=&v"(t0), "=&v"(t1), "=&v"(t2), "=&v"(t3)
+        : "v"(v), "v"(x[0]), "v"(x[1]), "v"(x[2]), "v"(x[3]));
+    return acc;
+}
+
+// dot_chunk of KI q4_K / q5_K items that share chunk c, with x read from LDS (xc:
+// the chunk's 64 contiguous values) one float4 at a time and applied to every item,
+// so no item's values are expanded all at once.  Per item the operations and their
+// order are those of dot_chunk with f32 x (one row): the results are equal.
+template <int T, int KI>
+__device__ __forceinline__ void dot_items(int c, const Raw<T> (&r)[KI], const float *xc, float (&out)[KI]) {
+    static_assert(T == GGML_Q4_K || T == GGML_Q5_K, "q4_K / q5_K only");
+    const int g = c & 3;
+    float al[KI], ah[KI];
+#pragma unroll
+    for (int k = 0; k < KI; ++k) al[k] = ah[k] = 0.f;
+    float s0 = 0.f, s1 = 0.f;
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+        const float4 xl = *reinterpret_cast<const float4 *>(xc + 4 * u);
+        const float4 xh = *reinterpret_cast<const float4 *>(xc + 32 + 4 * u);
+        const float vl[4] = {xl.x, xl.y, xl.z, xl.w}, vh[4] = {xh.x, xh.y, xh.z, xh.w};
+#pragma unroll
+        for (int k = 0; k < KI; ++k) {
+            const uint32_t wu = u < 4 ? (&r[k].a.x)[u] : (&r[k].b.x)[u - 4];
+            uint32_t lo, hi;
+            if constexpr (T == GGML_Q5_K) {
+                const uint32_t hb = u < 4 ? (&r[k].c.x)[u] : (&r[k].e.x)[u - 4];
+                lo = (wu & 0x0F0F0F0Fu) | (((hb >> (2 * g)) & 0x01010101u) << 4);
+                hi = ((wu >> 4) & 0x0F0F0F0Fu) | (((hb >> (2 * g + 1)) & 0x01010101u) << 4);
+            } else {
+                lo = wu & 0x0F0F0F0Fu;
+                hi = wu & 0xF0F0F0F0u;  // 16 * nibble; scaled back below
+            }
+            al[k] = dot4u8_chain(lo, vl, al[k]);
+            ah[k] = dot4u8_chain(hi, vh, ah[k]);
+        }
+    }
+    // the sums of gemv_load_x (xslot: values 0..31 -> 0, 32..63 -> 1), in its order
+#pragma unroll
+    for (int e = 0; e < 32; ++e) s0 += xc[e];
+#pragma unroll
+    for (int e = 32; e < 64; ++e) s1 += xc[e];
+    const int sh0 = 8 * ((2 * g) & 3), sh1 = sh0 + 8;
+    const bool upper = g >= 2;
+#pragma unroll
+    for (int k = 0; k < KI; ++k) {
+        auto decode = [&](int sh, float &sc, float &mn) {
+            const uint32_t B0 = r[k].h.y >> sh, B1 = r[k].h.z >> sh, B2 = r[k].h.w >> sh;
+            const uint32_t a = upper ? ((B2 & 15u) | ((B0 >> 2) & 48u)) : (B0 & 63u);
+            const uint32_t bb = upper ? (((B2 >> 4) & 15u) | ((B1 >> 2) & 48u)) : (B1 & 63u);
+            sc = float(a);
+            mn = float(bb);
+        };
+        float sc0, m0, sc1, m1;
+        decode(sh0, sc0, m0);
+        decode(sh1, sc1, m1);
+        const float d = h2f(r[k].h.x), dmin = h2f(r[k].h.x >> 16);
+        float a0 = ah[k];
+        if constexpr (T == GGML_Q4_K) a0 *= 0.0625f;
+        float acc = 0.f;
+        acc += d * (sc0 * al[k] + sc1 * a0) - dmin * (m0 * s0 + m1 * s1);
+        out[k] = acc;
+    }
+}
+
+struct XAttnArgs {
+    StepArgs s;            // residual prologue: x_in + self-attention partials + b_out, cross_norm
+    WPtr wq;               // cross_q [d][d]
+    const float *bq;
+    WPtr wo;               // cross_out [d][d]
+    int H, L, HG, RW;
+    const __half *K, *V;   // cross K/V [nb][H][L][HD]
+    const uint32_t *lens;  // [nb]
+    float *part;           // out: [H / HG][nb][d] (another buffer than s.part)
+};
+
+// cross_q, the cross attention and its out-projection slice in one launch (PR = batch
+// rows <= 2, d <= 1024, at most kPreParts self-attention partials).  Workgroup (g, r) rebuilds x = x_in + sum of the self-attention
+// partials + b_out (workgroup (0, 0) stores it), applies cross_norm, computes q for
+// heads [g HG, (g + 1) HG) from the C rows of Wq it needs (at most kXItems (row, chunk)
+// items per thread, all issued at entry with the out-projection's weights), then
+// runs the attention and projection of k_attn_head.  The workgroups of one group
+// repeat those C rows (72 KB at 600M, from L2) instead of waiting for a separate
+// launch.  Every sum is in the order of the separate kernels, so the partials equal
+// theirs bit for bit.
+template <int T, int HD, int PR>
+__global__ __launch_bounds__(kXThreads) void k_xattn(XAttnArgs a) {
+    constexpr int XW = GTraits<T>::XW, NS = GTraits<T>::NS;
+    constexpr int TPK = HD / 8, SPL = 64 / TPK, U = 8, NW = kXThreads / 64;
+    extern __shared__ float lds[];
+    __shared__ double red[2 * 4 * NW];
+    const int t = threadIdx.x, lane = t & 63, w = t >> 6;
+    const int nb = a.s.nb, d = a.s.d, H = a.H, L = a.L, HG = a.HG, hg_log2 = __builtin_ctz(a.HG);
+    const int C = HG * HD, g = blockIdx.x, h0 = g * HG, col0 = g * C;
+    const int pairs = nb * HG;
+    const int ldx = lds_pad(d);
+    float *xs = lds;                // [nb][ldx]: cross_norm(x)
+    float *qs = xs + nb * ldx;      // [nb][C]
+    float *outv = qs + nb * C;      // [nb][C] = [pairs][HD]
+    float *wsc = outv + nb * C + w * 512;  // attention waves: [64][8] scratch
+
+    // Order of issue: residual operands (the prologue waits for them first), the q
+    // rows, the out-projection chunk, the first K/V chunk.  Loads complete in order,
+    // so each phase waits only for what it uses.
+    PreLoadsR<PR> PL;
+    if (t < 256) {  // wave-uniform: the threads that own the float4 slots
+        preload<PR>(a.s, PL);
+    } else {
+#pragma unroll
+        for (int bi = 0; bi < PR; ++bi) {
+#pragma unroll
+            for (int p = 0; p < kPreParts; ++p) PL.part[bi][p] = make_float4(0.f, 0.f, 0.f, 0.f);
+            PL.x[bi] = make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+        PL.pb = PL.gr = PL.br = make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    const int CQ = a.wq.K / XW, cq_log2 = __builtin_ctz(CQ), qc = t & (CQ - 1);
+    Raw<T> wq[kXItems];
+    float qbias[kXItems];
+#pragma unroll
+    for (int k = 0; k < kXItems; ++k) {
+        const int row = (t + k * kXThreads) >> cq_log2;
+        const int r = col0 + (row < C ? row : 0);
+        load_chunk<T>(a.wq, r, qc, wq[k]);
+        qbias[k] = a.bq[r];
+    }
+    const int CPR = C / XW, cpr_log2 = __builtin_ctz(CPR), c0 = col0 / XW;
+    const int rl = t >> cpr_log2, wcc = t & (CPR - 1);
+    const int wrow = blockIdx.y * a.RW + rl;
+    const bool wok = rl < a.RW && wrow < d;
+    Raw<T> wr;
+    load_chunk<T>(a.wo, wok ? wrow : 0, c0 + wcc, wr);
+    // batch 1: the first key chunk of this wave's first (row, head) pair (addresses
+    // do not depend on the key counts; keys past a row's count are masked when used)
+    const int sub = lane % TPK, split = lane / TPK;
+    uint4 kr[U], vr[U];
+    auto load_kv = [&](int p, int j0) {
+        const int bi = p >> hg_log2, hh = h0 + (p & (HG - 1));
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int j = min(j0 + u * SPL + split, L - 1);
+            const size_t o = ((size_t(bi) * H + hh) * L + j) * HD + sub * 8;
+            kr[u] = *reinterpret_cast<const uint4 *>(a.K + o);
+            vr[u] = *reinterpret_cast<const uint4 *>(a.V + o);
+        }
+    };
+    constexpr bool kEarlyKV = PR == 1;  // two rows' q would not fit the registers beside them
+    if (kEarlyKV && w < pairs) load_kv(w, 0);
+    __builtin_amdgcn_sched_barrier(0);
+    int nk[PR];
+#pragma unroll
+    for (int bi = 0; bi < PR; ++bi) nk[bi] = bi < nb ? int(a.lens[bi]) : 0;
+
+    resid_ln_prologue<PRO_RESID_PRE, GGML_F32, NW, 1, PR>(a.s, PL, xs, red);
+
+    // q = cross_norm(x) Wq^T + bq for this group's C rows, as k_step computes them
+    {
+        float acc[kXItems][PR];
+#pragma unroll
+        for (int bi = 0; bi < PR; ++bi) {
+#pragma unroll
+            for (int k = 0; k < kXItems; ++k) acc[k][bi] = 0.f;
+            if (bi >= nb) continue;
+            float o[kXItems];
+            dot_items<T, kXItems>(qc, wq, xs + bi * ldx + lds_pad(xpos<T>(qc, 0)), o);
+#pragma unroll
+            for (int k = 0; k < kXItems; ++k) acc[k][bi] = o[k];
+        }
+#pragma unroll
+        for (int k = 0; k < kXItems; ++k) {
+            const int row = (t + k * kXThreads) >> cq_log2;
+#pragma unroll
+            for (int bi = 0; bi < PR; ++bi) {
+                const float v = group_sum_dyn(acc[k][bi], cq_log2);
+                if (qc == 0 && row < C && bi < nb) qs[bi * C + row] = v + qbias[k];
+            }
+        }
+    }
+    lds_barrier();
+
+    // attention: one (row, head) pair per wave, as in k_attn_head
+    for (int p = w; p < pairs; p += NW) {  // wave-uniform
+        const int bi = p >> hg_log2, hl = p & (HG - 1);
+        const int n = PR == 1 || bi == 0 ? nk[0] : nk[PR - 1];
+        const float4 qa = *reinterpret_cast<const float4 *>(qs + bi * C + hl * HD + sub * 8);
+        const float4 qb = *reinterpret_cast<const float4 *>(qs + bi * C + hl * HD + sub * 8 + 4);
+        float m = -INFINITY, l = 0.f;
+        float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+        for (int j0 = 0; j0 < n; j0 += U * SPL) {
+            if (!kEarlyKV || p != w || j0 != 0) load_kv(p, j0);
+            float sc[U];
+            float cmax = -INFINITY;
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                float s = h2f(kr[u].x) * qa.x;
+                s = fmaf(h2f(kr[u].x >> 16), qa.y, s);
+                s = fmaf(h2f(kr[u].y), qa.z, s);
+                s = fmaf(h2f(kr[u].y >> 16), qa.w, s);
+                s = fmaf(h2f(kr[u].z), qb.x, s);
+                s = fmaf(h2f(kr[u].z >> 16), qb.y, s);
+                s = fmaf(h2f(kr[u].w), qb.z, s);
+                s = fmaf(h2f(kr[u].w >> 16), qb.w, s);
+                s = group_sum<TPK>(s);
+                sc[u] = j0 + u * SPL + split < n ? s : -INFINITY;
+                cmax = fmaxf(cmax, sc[u]);
+            }
+            const float mnew = fmaxf(m, wave_max(cmax));
+            const float r = expf(m - mnew);
+            l *= r;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) acc[e] *= r;
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                const bool in = j0 + u * SPL + split < n;
+                const float pj = in ? expf(sc[u] - mnew) : 0.f;
+                l += pj;
+                const uint32_t wv[4] = {in ? vr[u].x : 0u, in ? vr[u].y : 0u, in ? vr[u].z : 0u, in ? vr[u].w : 0u};
+#pragma unroll
+                for (int q2 = 0; q2 < 4; ++q2) {
+                    acc[2 * q2] = fmaf(pj, h2f(wv[q2]), acc[2 * q2]);
+                    acc[2 * q2 + 1] = fmaf(pj, h2f(wv[q2] >> 16), acc[2 * q2 + 1]);
+                }
+            }
+            m = mnew;
+        }
+        const float inv = 1.f / wave_sum(sub == 0 ? l : 0.f);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) wsc[lane * 8 + e] = acc[e];
+        __builtin_amdgcn_s_waitcnt(0xc07f);
+        __builtin_amdgcn_wave_barrier();
+        for (int e = lane; e < HD; e += 64) {
+            float o = 0.f;
+#pragma unroll
+            for (int s2 = 0; s2 < SPL; ++s2) o += wsc[(s2 * TPK + e / 8) * 8 + e % 8];
+            outv[p * HD + e] = o * inv;
+        }
+        __builtin_amdgcn_s_waitcnt(0xc07f);
+        __builtin_amdgcn_wave_barrier();
+    }
+    lds_barrier();
+
+    // the group's slice of the out-projection
+    const int c = c0 + wcc;
+    float acc[PR];
+#pragma unroll
+    for (int bi = 0; bi < PR; ++bi) {
+        acc[bi] = 0.f;
+        if (bi >= nb) break;
+        XF<T, 1> X;
+#pragma unroll
+        for (int e = 0; e < XW; e += 4) {
+            const float4 x4 = *reinterpret_cast<const float4 *>(outv + bi * C + xpos<T>(c, e) - col0);
+            X.x[0][e] = x4.x;
+            X.x[0][e + 1] = x4.y;
+            X.x[0][e + 2] = x4.z;
+            X.x[0][e + 3] = x4.w;
+        }
+#pragma unroll
+        for (int s2 = 0; s2 < NS; ++s2) X.s[0][s2] = 0.f;
+#pragma unroll
+        for (int e = 0; e < XW; ++e) X.s[0][xslot<T>(e)] += X.x[0][e];
+        float a1[1] = {0.f};
+        dot_chunk<T, 1>(c, wr, X, a1);
+        acc[bi] = a1[0];
+    }
+#pragma unroll
+    for (int bi = 0; bi < PR; ++bi) acc[bi] = group_sum_dyn(acc[bi], cpr_log2);
+    if (wcc == 0 && wok)
+#pragma unroll
+        for (int bi = 0; bi < PR; ++bi)
+            if (bi < nb) a.part[(size_t(g) * nb + bi) * d + wrow] = acc[bi];
+}
+
 // ---------------------------------------------------------------- dispatch
 
 template <int T, int B, int CPL, int PRO, int EPI, int ET>
@@ -632,6 +939,82 @@ hipError_t step_attn_head(const DevMatrix &w, int nb, int d, const float *q, con
     case GGML_Q8_0: return launch_head_hd<GGML_Q8_0>(a, hd, hg.R, hg.lds, st);
     case GGML_F16: return launch_head_hd<GGML_F16>(a, hd, hg.R, hg.lds, st);
     case GGML_F32: return launch_head_hd<GGML_F32>(a, hd, hg.R, hg.lds, st);
+    default: return hipErrorInvalidValue;
+    }
+}
+
+namespace {
+
+template <int T, int HD>
+hipError_t launch_xattn(const XAttnArgs &a, int R, size_t lds, hipStream_t st) {
+    if (a.s.nb == 1)
+        hipLaunchKernelGGL((k_xattn<T, HD, 1>), dim3(a.H / a.HG, R), dim3(kXThreads), lds, st, a);
+    else
+        hipLaunchKernelGGL((k_xattn<T, HD, 2>), dim3(a.H / a.HG, R), dim3(kXThreads), lds, st, a);
+    return hipGetLastError();
+}
+
+template <int T>
+hipError_t launch_xattn_hd(const XAttnArgs &a, int hd, int R, size_t lds, hipStream_t st) {
+    switch (hd) {
+    case 16: return launch_xattn<T, 16>(a, R, lds, st);
+    case 64: return launch_xattn<T, 64>(a, R, lds, st);
+    default: return hipErrorInvalidValue;
+    }
+}
+
+}  // namespace
+
+bool step_cross_fusable(const DevMatrix &wq, const DevMatrix &wo, int nb, int d, int H, int hd, int L, int P) {
+    HeadGeom hg;
+    if (P < 1 || P > kPreParts) return false;
+    if (wq.type != wo.type || wq.N != d || wq.K != d || d > 1024 || d % 16 || nb < 1 || nb > 2) return false;
+    if (hd != 16 && hd != 64) return false;
+    if (wq.type != GGML_Q4_K && wq.type != GGML_Q5_K) return false;
+    if (!head_geometry(wo, nb, d, H, hd, L, &hg)) return false;
+    const int CQ = d / gemv_xw(wq.type), C = hg.HG * hd;
+    // one lane group per q row (a power of two <= 64 lanes), at most kXItems items per thread
+    return CQ >= 1 && CQ <= 64 && (CQ & (CQ - 1)) == 0 && size_t(C) * CQ <= size_t(kXItems) * kXThreads;
+}
+
+hipError_t step_cross_attn(const DevMatrix &wq, const float *bq, const DevMatrix &wo, int nb, int d, const float *x_in,
+                           const float *part_in, int P, const float *pbias, float *x_out, const float *gamma,
+                           const float *beta, float eps, const __half *K, const __half *V, int H, int hd, int L,
+                           const uint32_t *lens, float *part_out, hipStream_t st) {
+    HeadGeom hg;
+    if (!step_cross_fusable(wq, wo, nb, d, H, hd, L, P) || part_in == part_out ||
+        !head_geometry(wo, nb, d, H, hd, L, &hg))
+        return hipErrorInvalidValue;
+    XAttnArgs a{};
+    a.s.nb = nb;
+    a.s.d = d;
+    a.s.x_in = x_in;
+    a.s.part = part_in;
+    a.s.P = P;
+    a.s.pbias = pbias;
+    a.s.x_out = x_out;
+    a.s.gamma = gamma;
+    a.s.beta = beta;
+    a.s.eps = eps;
+    a.wq = wptr_of(wq);
+    a.bq = bq;
+    a.wo = wptr_of(wo);
+    a.H = H;
+    a.L = L;
+    a.HG = hg.HG;
+    const int C = hg.HG * hd, CPR = C / gemv_xw(wo.type);
+    a.RW = kXThreads / CPR < d ? kXThreads / CPR : d;
+    const int R = (d + a.RW - 1) / a.RW;
+    a.K = K;
+    a.V = V;
+    a.lens = lens;
+    a.part = part_out;
+    const int pairs = nb * hg.HG;
+    const size_t lds = sizeof(float) * (size_t(nb) * lds_pad(d) + 2 * size_t(nb) * C +
+                                        size_t(pairs < kXThreads / 64 ? pairs : kXThreads / 64) * 512);
+    switch (wq.type) {
+    case GGML_Q4_K: return launch_xattn_hd<GGML_Q4_K>(a, hd, R, lds, st);
+    case GGML_Q5_K: return launch_xattn_hd<GGML_Q5_K>(a, hd, R, lds, st);
     default: return hipErrorInvalidValue;
     }
 }

@@ -189,6 +189,15 @@ hipError_t step_attn_head(const DevMatrix &w, int nb, int d, const float *q, con
 hipError_t step_resid_proj(const DevMatrix &w, const float *bias, bool relu, int nb, int d, const float *x_in,
                            const float *part, int P, const float *pbias, float *x_out, const float *gamma,
                            const float *beta, float eps, float *y, hipStream_t st);
+// step_resid_proj(cross_q) followed by step_attn_head(cross_out) in one launch:
+// x = x_in + sum_{p < P} part_in[p] + pbias ; x_out <- x ; q = LayerNorm(x) Wq^T + bq ;
+// part_out = the cross attention of q over K/V [nb][H][L][hd] (lens keys) times wo^T,
+// step_head_parts(wo, ...) partial sums.  part_out must not alias part_in; P <= 8.
+bool step_cross_fusable(const DevMatrix &wq, const DevMatrix &wo, int nb, int d, int H, int hd, int L, int P);
+hipError_t step_cross_attn(const DevMatrix &wq, const float *bq, const DevMatrix &wo, int nb, int d, const float *x_in,
+                           const float *part_in, int P, const float *pbias, float *x_out, const float *gamma,
+                           const float *beta, float eps, const __half *K, const __half *V, int H, int hd, int L,
+                           const uint32_t *lens, float *part_out, hipStream_t st);
 // y = x W^T + bias, x [nb][K] in global memory.
 hipError_t step_proj(const DevMatrix &w, const float *bias, int nb, const float *x, float *y, hipStream_t st);
 

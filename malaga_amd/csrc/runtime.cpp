@@ -655,7 +655,10 @@ std::unique_ptr<StaticState> Model::new_state(int b, int s, int m, bool logits, 
     st->xb = static_cast<float *>(get(size_t(b) * d * 4, "x (second buffer)"));
     st->qc = static_cast<float *>(get(size_t(b) * d * 4, "cross q"));
     st->fused = fusable(b, m, s) && (!sl || step_embed_supported(dec[0].qkv.w.type, sl->head.type));
-    if (st->fused) st->part = static_cast<float *>(get(size_t(H) * b * d * 4, "attention partial sums"));
+    if (st->fused) {
+        st->part = static_cast<float *>(get(size_t(H) * b * d * 4, "attention partial sums"));
+        st->part2 = static_cast<float *>(get(size_t(H) * b * d * 4, "cross attention partial sums"));
+    }
     st->h = static_cast<float *>(get(size_t(b) * d * 4, "h"));
     st->y = static_cast<float *>(get(size_t(b) * d * 4, "y"));
     st->att = static_cast<float *>(get(size_t(b) * d * 4, "att"));
@@ -782,15 +785,25 @@ void Model::step_fused(StaticState &st) {
         check_hip(step_attn_head(l.out.w, B, d, st.q, st.kc[i], st.vc[i], H, hd, st.m, nullptr, st.step, st.part, s,
                                  st.rows),
                   "step_attn_head");
-        check_hip(step_resid_proj(l.cross_q.w, l.cross_q.b, false, B, d, cur, st.part, ps, l.out.b, nxt,
-                                  l.cross_norm.g, l.cross_norm.b, kLnEps, st.qc, s),
-                  "step_cross_q");
-        std::swap(cur, nxt);
         const int pc = step_head_parts(l.cross_out.w, B, d, H, hd, st.s);
-        check_hip(step_attn_head(l.cross_out.w, B, d, st.qc, st.ck[i], st.cv[i], H, hd, st.s, st.lens, nullptr,
-                                 st.part, s),
-                  "step_attn_head");
-        check_hip(step_resid_proj(l.up.w, l.up.b, true, B, d, cur, st.part, pc, l.cross_out.b, nxt, l.ffn_norm.g,
+        const float *cpart = st.part;
+        if (step_cross_fusable(l.cross_q.w, l.cross_out.w, B, d, H, hd, st.s, ps)) {
+            // cross_q + cross attention + out-projection slice in one launch
+            check_hip(step_cross_attn(l.cross_q.w, l.cross_q.b, l.cross_out.w, B, d, cur, st.part, ps, l.out.b, nxt,
+                                      l.cross_norm.g, l.cross_norm.b, kLnEps, st.ck[i], st.cv[i], H, hd, st.s,
+                                      st.lens, st.part2, s),
+                      "step_cross_attn");
+            cpart = st.part2;
+        } else {
+            check_hip(step_resid_proj(l.cross_q.w, l.cross_q.b, false, B, d, cur, st.part, ps, l.out.b, nxt,
+                                      l.cross_norm.g, l.cross_norm.b, kLnEps, st.qc, s),
+                      "step_cross_q");
+            check_hip(step_attn_head(l.cross_out.w, B, d, st.qc, st.ck[i], st.cv[i], H, hd, st.s, st.lens, nullptr,
+                                     st.part, s),
+                      "step_attn_head");
+        }
+        std::swap(cur, nxt);
+        check_hip(step_resid_proj(l.up.w, l.up.b, true, B, d, cur, cpart, pc, l.cross_out.b, nxt, l.ffn_norm.g,
                                   l.ffn_norm.b, kLnEps, st.u, s),
                   "step_up");
         std::swap(cur, nxt);

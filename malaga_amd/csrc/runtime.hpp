@@ -113,6 +113,7 @@ struct StaticState {
     float *x = nullptr, *h = nullptr, *y = nullptr, *att = nullptr, *q = nullptr, *qkv = nullptr, *u = nullptr;
     float *xb = nullptr, *qc = nullptr;  // second residual buffer and cross queries (fused step)
     float *part = nullptr;                // attention partial sums [parts][b][d] (fused step)
+    float *part2 = nullptr;               // second partials buffer: the cross launch reads part, writes part2
     uint32_t *rows = nullptr;             // beam: [b][m] cache row holding slot j of row r (null: r)
     uint32_t *row_src = nullptr;          // [b] source row of each state row (reset_state)
     // shortlist decoding (src/graph.rs:40-48): candidates are the shortlist rows and the
