@@ -365,6 +365,8 @@ void Model::load(const std::string &path) {
     cfg.decoder_start_token_id = u("tokenizer.ggml.decoder_start_token_id");
     const char *nf = std::getenv("MALAGA_NO_FUSED_STEP");
     no_fuse_ = nf && *nf && std::string(nf) != "0";
+    const char *sc = std::getenv("MALAGA_SPLIT_CROSS_STEP");
+    split_cross_ = sc && *sc && std::string(sc) != "0";
     const int d = cfg.d_model;
     if (d <= 0 || d % cfg.decoder_heads || d % cfg.encoder_heads || d > 4096 || d % 16)
         fail(ERR_UNSUPPORTED, "unsupported d_model " + std::to_string(d));
@@ -787,7 +789,7 @@ void Model::step_fused(StaticState &st) {
                   "step_attn_head");
         const int pc = step_head_parts(l.cross_out.w, B, d, H, hd, st.s);
         const float *cpart = st.part;
-        if (step_cross_fusable(l.cross_q.w, l.cross_out.w, B, d, H, hd, st.s, ps)) {
+        if (!split_cross_ && step_cross_fusable(l.cross_q.w, l.cross_out.w, B, d, H, hd, st.s, ps)) {
             // cross_q + cross attention + out-projection slice in one launch
             check_hip(step_cross_attn(l.cross_q.w, l.cross_q.b, l.cross_out.w, B, d, cur, st.part, ps, l.out.b, nxt,
                                       l.cross_norm.g, l.cross_norm.b, kLnEps, st.ck[i], st.cv[i], H, hd, st.s,

@@ -244,6 +244,7 @@ class Model {
     void step_fused(StaticState &st);
     void lm_head(StaticState &st, bool greedy_mode, int mask_id);
     bool no_fuse_ = false;  // MALAGA_NO_FUSED_STEP=1 forces the unfused step
+    bool split_cross_ = false;  // MALAGA_SPLIT_CROSS_STEP=1: cross_q and cross attention as two launches
 };
 
 void check_hip(hipError_t e, const char *what);  // throws Failure

@@ -212,6 +212,33 @@ def test_fused_step_small_batches_kquant(kq_gguf, models, unfused_models, preset
     assert np.abs(lg - orc.teacher_forced_logits(src, tgt, kv_f16=True)).max() < 2e-3
 
 
+@pytest.mark.parametrize("preset", ["q4_k_m", "q5_k_m"])
+@pytest.mark.parametrize("nb", [1, 2])
+def test_fused_cross_attention_equals_split_kernels(kq_gguf, models, preset, nb):
+    """k_xattn (cross_q + cross attention + out-projection slice in one launch) against
+    the same step with the two launches (MALAGA_SPLIT_CROSS_STEP=1): every sum is in the
+    same order, so the logits are equal bit for bit."""
+    import os
+
+    gpu, _ = models(kq_gguf(preset))
+    os.environ["MALAGA_SPLIT_CROSS_STEP"] = "1"
+    try:
+        split = M.Translator.load(kq_gguf(preset))
+    finally:
+        del os.environ["MALAGA_SPLIT_CROSS_STEP"]
+    rng = np.random.default_rng(300 + nb)
+    src = [[997] + rng.integers(4, 990, n).tolist() + [2] for n in (19, 40)[:nb]]
+    T = 10
+    tgt = np.zeros((nb, T), np.uint32)
+    tgt[:, 0], tgt[:, 1] = 2, 998
+    tgt[:, 2:] = rng.integers(4, 990, (nb, T - 2))
+    try:
+        assert np.array_equal(gpu.teacher_forced_logits(src, tgt), split.teacher_forced_logits(src, tgt))
+        assert gpu.generate(src, 998) == split.generate(src, 998)
+    finally:
+        split.close()
+
+
 @pytest.mark.parametrize("preset", ["q4_k_m", "q5_k_m", "q6_k", "q8_0", "f16"])
 @pytest.mark.parametrize("nb", [7, 16, 33])
 def test_batched_decode_mfma_path(kq_gguf, models, preset, nb):
