@@ -204,7 +204,8 @@ int mlg_gemm_resid(const mlg_matrix *w, const float *x, int M, float *y, const f
  * partials [M][mlg_gemm_argmax_parts(w, M)]. */
 int mlg_gemm_argmax_parts(const mlg_matrix *w, int M);
 int mlg_gemm_argmax(const mlg_matrix *w, const float *x, int M, int mask_id, float *pv, uint32_t *pi, void *stream);
-/* LM head + first argmax pass (kernels/malaga.cu:247-280 fused into the GEMV). */
+/* LM head + first argmax pass (kernels/malaga.cu:247-280 fused into the GEMV):
+ * partials pv/pi [b][mlg_gemv_argmax_parts(w, b)] (one per workgroup launched). */
 int mlg_gemv_argmax_parts(const mlg_matrix *w, int b);
 int mlg_gemv_argmax(const mlg_matrix *w, const float *x, int b, int mask_id, float *pv, uint32_t *pi, void *stream);
 /* bias_residual_ln (kernels/malaga.cu:89-105) with the bias already in y. */

@@ -105,22 +105,46 @@ __global__ __launch_bounds__(256) void k_gemv(GemvArgs a) {
     }
 }
 
+// Workgroups of one launch that are resident on the device at once (CUs x blocks per
+// CU at this kernel's occupancy), or 0 if the runtime cannot say.
+inline int resident_grid(const void *kernel, int lds) {
+    int dev = 0, cus = 0, per_cu = 0;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, 256, size_t(lds)) != hipSuccess)
+        return 0;
+    return cus * per_cu;
+}
+
+// grid: in, the workgroups that cover the rows; out, the workgroups launched.  The
+// large-matrix modes launch at most one resident round (each wave then streams its
+// rows to the end): with more workgroups than fit at once, the last round runs part
+// empty (measured on the 600M LM head: 2048 workgroups 46.2 us, 1536 45.1 us, one
+// round of 768 42.5 us).
+// launch = false: only the grid is set (the partial count gemv_argmax_parts reports).
 template <int T, int B, int CPL, int MODE, bool LM>
-hipError_t launch_t(const GemvArgs &a, int grid, hipStream_t st) {
+hipError_t launch_t(const GemvArgs &a, int &grid, hipStream_t st, bool launch) {
     if constexpr (GTraits<T>::XW * B * CPL > kGemvMaxXRegs) {
         return hipErrorInvalidValue;
     } else {
         const int lds = kGemvLimbs<T, MODE> ? xq_lds_bytes<T>(a.w.K, a.nb) : 0;
         if (lds > 65536) return hipErrorInvalidValue;
+        if constexpr (MODE != 0) {
+            // per instantiation; the LDS bytes of one x row (nb = 1) set the occupancy
+            static const int resident = resident_grid(reinterpret_cast<const void *>(&k_gemv<T, B, CPL, MODE, LM>),
+                                                      kGemvLimbs<T, MODE> ? xq_lds_bytes<T>(a.w.K, B) : 0);
+            if (resident > 0 && grid > resident) grid = resident;
+        }
+        if (!launch) return hipSuccess;
         hipLaunchKernelGGL((k_gemv<T, B, CPL, MODE, LM>), dim3(grid), dim3(256), lds, st, a);
         return hipGetLastError();
     }
 }
 
 template <int T, int MODE, bool LM = false>
-hipError_t dispatch_bc(const GemvArgs &a, int B, int cpl, int grid, hipStream_t st) {
+hipError_t dispatch_bc(const GemvArgs &a, int B, int cpl, int &grid, hipStream_t st, bool launch) {
 #define MLG_CASE(BB, CC) \
-    if (B == BB && cpl == CC) return launch_t<T, BB, CC, MODE, LM>(a, grid, st);
+    if (B == BB && cpl == CC) return launch_t<T, BB, CC, MODE, LM>(a, grid, st, launch);
     MLG_CASE(1, 1) MLG_CASE(1, 2) MLG_CASE(1, 4)
     MLG_CASE(2, 1) MLG_CASE(2, 2) MLG_CASE(2, 4)
     MLG_CASE(4, 1) MLG_CASE(4, 2) MLG_CASE(4, 4)
@@ -130,23 +154,23 @@ hipError_t dispatch_bc(const GemvArgs &a, int B, int cpl, int grid, hipStream_t 
 
 // lm: lane-major quants of a q6_K head (the large-matrix modes only)
 template <int MODE>
-hipError_t dispatch(uint32_t type, const GemvArgs &a, int B, int cpl, int grid, hipStream_t st,
-                    const uint8_t *lm = nullptr) {
+hipError_t dispatch(uint32_t type, const GemvArgs &a, int B, int cpl, int &grid, hipStream_t st,
+                    const uint8_t *lm = nullptr, bool launch = true) {
     switch (type) {
-    case GGML_Q4_K: return dispatch_bc<GGML_Q4_K, MODE>(a, B, cpl, grid, st);
-    case GGML_Q5_K: return dispatch_bc<GGML_Q5_K, MODE>(a, B, cpl, grid, st);
+    case GGML_Q4_K: return dispatch_bc<GGML_Q4_K, MODE>(a, B, cpl, grid, st, launch);
+    case GGML_Q5_K: return dispatch_bc<GGML_Q5_K, MODE>(a, B, cpl, grid, st, launch);
     case GGML_Q6_K:
         if constexpr (MODE != 0) {
             if (lm) {
                 GemvArgs b = a;
                 b.w.q = lm;
-                return dispatch_bc<GGML_Q6_K, MODE, true>(b, B, cpl, grid, st);
+                return dispatch_bc<GGML_Q6_K, MODE, true>(b, B, cpl, grid, st, launch);
             }
         }
-        return dispatch_bc<GGML_Q6_K, MODE>(a, B, cpl, grid, st);
-    case GGML_Q8_0: return dispatch_bc<GGML_Q8_0, MODE>(a, B, cpl, grid, st);
-    case GGML_F16: return dispatch_bc<GGML_F16, MODE>(a, B, cpl, grid, st);
-    case GGML_F32: return dispatch_bc<GGML_F32, MODE>(a, B, cpl, grid, st);
+        return dispatch_bc<GGML_Q6_K, MODE>(a, B, cpl, grid, st, launch);
+    case GGML_Q8_0: return dispatch_bc<GGML_Q8_0, MODE>(a, B, cpl, grid, st, launch);
+    case GGML_F16: return dispatch_bc<GGML_F16, MODE>(a, B, cpl, grid, st, launch);
+    case GGML_F32: return dispatch_bc<GGML_F32, MODE>(a, B, cpl, grid, st, launch);
     default: return hipErrorInvalidValue;
     }
 }
@@ -209,13 +233,22 @@ hipError_t gemv(const DevMatrix &w, const float *x, int ldx, int b, float *y, in
     a.ldy = ldy;
     a.bias = bias;
     a.relu = relu ? 1 : 0;
-    if (w.N <= kGemvSmallRows) return dispatch<0>(w.type, a, gemv_round_b(b), cpl, gemv_grid(w, 1), st);
-    return dispatch<2>(w.type, a, gemv_round_b(b), cpl, gemv_grid(w, 2), st, w.lm);
+    if (w.N <= kGemvSmallRows) {
+        int grid = gemv_grid(w, 1);
+        return dispatch<0>(w.type, a, gemv_round_b(b), cpl, grid, st);
+    }
+    int grid = gemv_grid(w, 2);
+    return dispatch<2>(w.type, a, gemv_round_b(b), cpl, grid, st, w.lm);
 }
 
 int gemv_argmax_parts(const DevMatrix &w, int b) {
-    (void)b;
-    return gemv_grid(w, 1);
+    GemvGeom g;
+    int cpl;
+    if (b < 1 || b > gemv_max_batch(w) || !gemv_geometry(w, &g, &cpl)) return gemv_grid(w, 1);
+    GemvArgs a = make_args(w, g, nullptr, 0, b);
+    int grid = gemv_grid(w, 1);
+    dispatch<1>(w.type, a, gemv_round_b(b), cpl, grid, nullptr, w.lm, false);
+    return grid;
 }
 
 hipError_t gemv_argmax(const DevMatrix &w, const float *x, int ldx, int b, int mask_id, float *pv, uint32_t *pi,
@@ -229,11 +262,12 @@ hipError_t gemv_argmax(const DevMatrix &w, const float *x, int ldx, int b, int m
     a.pv = pv;
     a.pi = pi;
     a.mask_id = mask_id;
-    const int grid = gemv_grid(w, 1);
-    *parts = grid;
+    int grid = gemv_grid(w, 1);
     const size_t row_bytes = w.bytes / size_t(w.N);
     a.nt_from = row_bytes ? int(std::min<size_t>(size_t(w.N), kLmHeadCachedBytes / row_bytes)) : w.N;
-    return dispatch<1>(w.type, a, gemv_round_b(b), cpl, grid, st, w.lm);
+    const hipError_t e = dispatch<1>(w.type, a, gemv_round_b(b), cpl, grid, st, w.lm);
+    *parts = grid;  // the workgroups launched, = gemv_argmax_parts(w, b)
+    return e;
 }
 
 }  // namespace mlg
