@@ -587,14 +587,16 @@ struct NoPre {
 // complete in order), the first step's weights, then prologue(), which fills
 // xr and may use workgroup barriers (every thread of the workgroup must call
 // this function).
-template <int T, int B, int CPL, bool NT = false, int G = 2, bool LM = false, class XR, class PreF, class Pro,
-          class Epi>
+// L2 > 0: g.lpr_log2 known at compile time (static lane-group reductions).
+template <int T, int B, int CPL, bool NT = false, int G = 2, bool LM = false, int L2 = 0, class XR, class PreF,
+          class Pro, class Epi>
 __device__ __forceinline__ void gemv_rows(const WPtr &w, const GemvGeom &g, XR (&xr)[CPL], int gwave, int nwaves,
                                           PreF &&pre, Pro &&prologue, Epi &epi, const float *bias = nullptr,
                                           int nt_from = 0) {
     const int lane = threadIdx.x & 63;
-    const int lpr = 1 << g.lpr_log2, rpw = 64 >> g.lpr_log2;
-    const int grp = lane >> g.lpr_log2, cl = lane & (lpr - 1);
+    const int l2 = L2 > 0 ? L2 : g.lpr_log2;
+    const int lpr = 1 << l2, rpw = 64 >> l2;
+    const int grp = lane >> l2, cl = lane & (lpr - 1);
     int cidx[CPL];
 #pragma unroll
     for (int t = 0; t < CPL; ++t) cidx[t] = (cl + t * lpr < g.nchunks) ? cl + t * lpr : 0;
@@ -622,8 +624,10 @@ __device__ __forceinline__ void gemv_rows(const WPtr &w, const GemvGeom &g, XR (
 #pragma unroll
             for (int t = 0; t < CPL; ++t) dot_chunk<T, B>(cidx[t], r[u][t], xr[t], acc);
 #pragma unroll
-            for (int bi = 0; bi < B; ++bi)
-                acc[bi] = group_sum_dyn(acc[bi], g.lpr_log2);
+            for (int bi = 0; bi < B; ++bi) {
+                if constexpr (L2 > 0) acc[bi] = group_sum<1 << L2>(acc[bi]);
+                else acc[bi] = group_sum_dyn(acc[bi], g.lpr_log2);
+            }
             const int row = (rg + u * nwaves) * rpw + grp;
             if (cl == 0 && row < w.N) {
 #pragma unroll

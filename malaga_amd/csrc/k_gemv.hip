@@ -50,11 +50,12 @@ template <int T, int MODE>
 constexpr bool kGemvLimbs = MODE != 0 && kLimbX<T>;  // large matrices: limb x (gemv_core.hpp)
 
 // LM: a.w.q is the lane-major quant copy of a q6_K head (DevMatrix::lm)
-template <int T, int B, int CPL, int MODE, bool LM>
+// L2 > 0: lanes per row group = 2^L2 at compile time (a.g.lpr_log2 == L2)
+template <int T, int B, int CPL, int MODE, bool LM, int L2 = 0>
 __global__ __launch_bounds__(256) void k_gemv(GemvArgs a) {
     extern __shared__ uint32_t xlds[];  // limbs of x
     const int lane = threadIdx.x & 63;
-    const int cl = lane & ((1 << a.g.lpr_log2) - 1);
+    const int cl = lane & ((1 << (L2 > 0 ? L2 : a.g.lpr_log2)) - 1);
     XRep<T, B, kGemvLimbs<T, MODE>> xr[CPL];
     auto load_x = [&] {
         if constexpr (kGemvLimbs<T, MODE>) {
@@ -81,7 +82,8 @@ __global__ __launch_bounds__(256) void k_gemv(GemvArgs a) {
         }
         // rows >= nt_from non-temporal: the 215 MB stream then evicts less of the layer
         // weights from the MALL between steps (measured: -20 us per 600M step)
-        gemv_rows<T, B, CPL, true, 1, LM>(a.w, a.g, xr, gwave, nwaves, NoPre{}, load_x, epi, a.bias, a.nt_from);
+        gemv_rows<T, B, CPL, true, 1, LM, L2>(a.w, a.g, xr, gwave, nwaves, NoPre{}, load_x, epi, a.bias,
+                                              a.nt_from);
         __shared__ float sv[4][B];
         __shared__ uint32_t si[4][B];
         const int wv = threadIdx.x >> 6;
@@ -122,7 +124,7 @@ inline int resident_grid(const void *kernel, int lds) {
 // empty (measured on the 600M LM head: 2048 workgroups 46.2 us, 1536 45.1 us, one
 // round of 768 42.5 us).
 // launch = false: only the grid is set (the partial count gemv_argmax_parts reports).
-template <int T, int B, int CPL, int MODE, bool LM>
+template <int T, int B, int CPL, int MODE, bool LM, int L2 = 0>
 hipError_t launch_t(const GemvArgs &a, int &grid, hipStream_t st, bool launch) {
     if constexpr (GTraits<T>::XW * B * CPL > kGemvMaxXRegs) {
         return hipErrorInvalidValue;
@@ -131,18 +133,22 @@ hipError_t launch_t(const GemvArgs &a, int &grid, hipStream_t st, bool launch) {
         if (lds > 65536) return hipErrorInvalidValue;
         if constexpr (MODE != 0) {
             // per instantiation; the LDS bytes of one x row (nb = 1) set the occupancy
-            static const int resident = resident_grid(reinterpret_cast<const void *>(&k_gemv<T, B, CPL, MODE, LM>),
+            static const int resident = resident_grid(reinterpret_cast<const void *>(&k_gemv<T, B, CPL, MODE, LM, L2>),
                                                       kGemvLimbs<T, MODE> ? xq_lds_bytes<T>(a.w.K, B) : 0);
             if (resident > 0 && grid > resident) grid = resident;
         }
         if (!launch) return hipSuccess;
-        hipLaunchKernelGGL((k_gemv<T, B, CPL, MODE, LM>), dim3(grid), dim3(256), lds, st, a);
+        hipLaunchKernelGGL((k_gemv<T, B, CPL, MODE, LM, L2>), dim3(grid), dim3(256), lds, st, a);
         return hipGetLastError();
     }
 }
 
 template <int T, int MODE, bool LM = false>
 hipError_t dispatch_bc(const GemvArgs &a, int B, int cpl, int &grid, hipStream_t st, bool launch) {
+    if constexpr (MODE == 1) {  // batch-1 LM heads of K = 1024 (16 or 32 lanes per row) and 2048
+        if (B == 1 && cpl == 1 && a.g.lpr_log2 == 4) return launch_t<T, 1, 1, MODE, LM, 4>(a, grid, st, launch);
+        if (B == 1 && cpl == 1 && a.g.lpr_log2 == 5) return launch_t<T, 1, 1, MODE, LM, 5>(a, grid, st, launch);
+    }
 #define MLG_CASE(BB, CC) \
     if (B == BB && cpl == CC) return launch_t<T, BB, CC, MODE, LM>(a, grid, st, launch);
     MLG_CASE(1, 1) MLG_CASE(1, 2) MLG_CASE(1, 4)
