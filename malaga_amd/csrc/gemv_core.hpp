@@ -345,8 +345,8 @@ __device__ __forceinline__ void dot_chunk(int c, const Raw<T> &r, const XQ<T, B>
     } else if constexpr (T == GGML_Q6_K) {
         const int i = c & 1;
         const float d = h2f(r.c.x);
-        const float sc[4] = {float(int8_t(r.e0 >> (8 * i))), float(int8_t(r.e0 >> (8 * i + 16))),
-                             float(int8_t(r.e1 >> (8 * i))), float(int8_t(r.e1 >> (8 * i + 16)))};
+        const int sc[4] = {int(int8_t(r.e0 >> (8 * i))), int(int8_t(r.e0 >> (8 * i + 16))),
+                           int(int8_t(r.e1 >> (8 * i))), int(int8_t(r.e1 >> (8 * i + 16)))};
         const uint32_t A[4] = {r.a.x, r.a.y, r.a.z, r.a.w}, Bq[4] = {r.b.x, r.b.y, r.b.z, r.b.w},
                        H[4] = {r.h.x, r.h.y, r.h.z, r.h.w};
         uint32_t q6[4][4];  // 6-bit quants (0..63) of the four 16-value groups
@@ -359,7 +359,9 @@ __device__ __forceinline__ void dot_chunk(int c, const Raw<T> &r, const XQ<T, B>
         }
 #pragma unroll
         for (int bi = 0; bi < B; ++bi) {
-            float tot = 0.f;
+            // per limb, sum over groups of scale * (sum (q6 - 32) * limb) in int32:
+            // |group sum| <= 16 * 32 * 128 = 2^16, |scale| <= 128, four groups < 2^25
+            int t0 = 0, t1 = 0, t2 = 0;
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
                 // sum (q6 - 32) * limb: the -32 term is the accumulator's start value
@@ -370,9 +372,11 @@ __device__ __forceinline__ void dot_chunk(int c, const Raw<T> &r, const XQ<T, B>
                     a1 = sdot4(q6[q][u], X.c[bi][1][4 * q + u], a1);
                     a2 = sdot4(q6[q][u], X.c[bi][2][4 * q + u], a2);
                 }
-                tot = fmaf(sc[q], limb_sum(a0, a1, a2), tot);
+                t0 += __mul24(a0, sc[q]);
+                t1 += __mul24(a1, sc[q]);
+                t2 += __mul24(a2, sc[q]);
             }
-            acc[bi] += d * X.sc[bi] * tot;
+            acc[bi] += d * X.sc[bi] * fmaf(65536.f, float(t2), fmaf(256.f, float(t1), float(t0)));
         }
     } else {  // q8_0: signed 8-bit quants
         const float d = h2f(r.e0);
