@@ -584,8 +584,8 @@ struct NoPre {
 // Streams the rows of W; calls epi(row, bi, value) on the group-leader lane of each
 // row (value = dot product + bias[row], the bias fetched with the weights).  Waves
 // gwave, gwave + nwaves, ... share the rows, G row groups per wave and step (two
-// steps in flight).  G = 1 halves the arithmetic on a wave's critical path (small
-// matrices, latency-bound); G = 2 keeps more bytes in flight (the LM head).
+// steps in flight).  G = 1 halves the arithmetic on a wave's critical path and the
+// registers (every caller uses it); G = 2 keeps more bytes in flight per wave.
 // Order of issue: pre() (loads the
 // prologue needs, so that waiting for them does not wait for the weights: loads
 // complete in order), the first step's weights, then prologue(), which fills

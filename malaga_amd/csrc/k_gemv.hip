@@ -43,9 +43,10 @@ struct ArgmaxEpi {
     }
 };
 
-// MODE 0: store (G = 1: small, latency-bound matrices); MODE 2: store, G = 2 (large
-// matrices); MODE 1: LM head with argmax partials, G = 1 (fewer registers, three
-// waves per SIMD), mostly non-temporal weights.
+// MODE 0: store (small, latency-bound matrices, f32 x); MODE 2: store, large matrices
+// (limb x, one resident round of workgroups); MODE 1: LM head with argmax partials,
+// mostly non-temporal weights.  One row group per wave step (G = 1) in all three:
+// fewer registers, more waves per SIMD (measured faster than G = 2 for the large ones).
 template <int T, int MODE>
 constexpr bool kGemvLimbs = MODE != 0 && kLimbX<T>;  // large matrices: limb x (gemv_core.hpp)
 
@@ -72,7 +73,7 @@ __global__ __launch_bounds__(256) void k_gemv(GemvArgs a) {
         gemv_rows<T, B, CPL, false, 1, LM>(a.w, a.g, xr, gwave, nwaves, NoPre{}, load_x, epi, a.bias);
     } else if constexpr (MODE == 2) {
         StoreEpi<B> epi{a};
-        gemv_rows<T, B, CPL, false, 2, LM>(a.w, a.g, xr, gwave, nwaves, NoPre{}, load_x, epi, a.bias);
+        gemv_rows<T, B, CPL, false, 1, LM, L2>(a.w, a.g, xr, gwave, nwaves, NoPre{}, load_x, epi, a.bias);
     } else {  // the LM head: weights streamed once per step
         ArgmaxEpi<B> epi{a, {}, {}};
 #pragma unroll
@@ -145,7 +146,7 @@ hipError_t launch_t(const GemvArgs &a, int &grid, hipStream_t st, bool launch) {
 
 template <int T, int MODE, bool LM = false>
 hipError_t dispatch_bc(const GemvArgs &a, int B, int cpl, int &grid, hipStream_t st, bool launch) {
-    if constexpr (MODE == 1) {  // batch-1 LM heads of K = 1024 (16 or 32 lanes per row) and 2048
+    if constexpr (MODE != 0) {  // batch-1 large GEMVs of K = 1024 (16 or 32 lanes per row) and 2048
         if (B == 1 && cpl == 1 && a.g.lpr_log2 == 4) return launch_t<T, 1, 1, MODE, LM, 4>(a, grid, st, launch);
         if (B == 1 && cpl == 1 && a.g.lpr_log2 == 5) return launch_t<T, 1, 1, MODE, LM, 5>(a, grid, st, launch);
     }
@@ -243,7 +244,7 @@ hipError_t gemv(const DevMatrix &w, const float *x, int ldx, int b, float *y, in
         int grid = gemv_grid(w, 1);
         return dispatch<0>(w.type, a, gemv_round_b(b), cpl, grid, st);
     }
-    int grid = gemv_grid(w, 2);
+    int grid = gemv_grid(w, 1);
     return dispatch<2>(w.type, a, gemv_round_b(b), cpl, grid, st, w.lm);
 }
 
