@@ -211,7 +211,8 @@ int gemv_grid(const DevMatrix &w, int G) {
     if (!gemv_geometry(w, &g, &cpl)) return 0;
     const int rpw = 64 >> g.lpr_log2;
     const int groups = (w.N + rpw - 1) / rpw;
-    // G row groups per wave and step; a large matrix gets ~8 workgroups per CU
+    // G row groups per wave and step; capped at 2048 workgroups (the large-matrix modes
+    // then launch at most one resident round: launch_t)
     const int waves = (groups + G - 1) / G;
     const int grid = (waves + 3) / 4;
     return grid < 1 ? 1 : (grid > 2048 ? 2048 : grid);
