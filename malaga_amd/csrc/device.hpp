@@ -169,6 +169,33 @@ __device__ __forceinline__ float block_sum(float v, float *sh) {
     return t;
 }
 
+constexpr int kLnThreads = 256;
+constexpr int kLnMaxPerThread = 16;  // d <= 4096
+
+// LayerNorm of v[] (thread's elements i = tid + k * 256) with biased variance,
+// two passes in registers (kernels/malaga.cu:66-86 semantics).
+__device__ __forceinline__ void ln_rows(const float (&v)[kLnMaxPerThread], int d, const float *g, const float *b,
+                                        float eps, float *out, float *sh) {
+    float s = 0.f;
+#pragma unroll
+    for (int k = 0; k < kLnMaxPerThread; ++k) s += v[k];
+    const float mean = block_sum(s, sh) / float(d);
+    float s2 = 0.f;
+#pragma unroll
+    for (int k = 0; k < kLnMaxPerThread; ++k) {
+        const int i = threadIdx.x + k * kLnThreads;
+        const float c = i < d ? v[k] - mean : 0.f;
+        s2 += c * c;
+    }
+    __syncthreads();  // sh is reused
+    const float rstd = rsqrtf(block_sum(s2, sh) / float(d) + eps);
+#pragma unroll
+    for (int k = 0; k < kLnMaxPerThread; ++k) {
+        const int i = threadIdx.x + k * kLnThreads;
+        if (i < d) out[i] = (v[k] - mean) * rstd * g[i] + b[i];
+    }
+}
+
 __device__ __forceinline__ float block_max(float v, float *sh) {
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, nw = blockDim.x >> 6;
     v = wave_max(v);

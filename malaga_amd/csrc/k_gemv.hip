@@ -21,6 +21,11 @@ struct GemvArgs {
     uint32_t *pi;
     int mask_id;
     int nt_from;  // LM head: first row loaded non-temporally
+    // LM head: x = LayerNorm(ln_x + ln_y) (ln_g, ln_b, ln_eps) computed by every
+    // workgroup (workgroup 0 also stores it to ln_h); a.x is unused then
+    const float *ln_x, *ln_y, *ln_g, *ln_b;
+    float ln_eps;
+    float *ln_h;
 };
 
 template <int B>
@@ -60,7 +65,27 @@ __global__ __launch_bounds__(256) void k_gemv(GemvArgs a) {
     XRep<T, B, kGemvLimbs<T, MODE>> xr[CPL];
     auto load_x = [&] {
         if constexpr (kGemvLimbs<T, MODE>) {
-            stage_limbs<T>(a.x, a.ldx, a.nb, a.w.K, xlds);
+            if (MODE == 1 && a.ln_x) {
+                // k_residual_ln's arithmetic (ln_rows, 256 threads), rows kept in LDS
+                __shared__ float lnsh[16];
+                const int K = a.w.K;
+                float *hs = reinterpret_cast<float *>(xlds) + xq_lds_bytes<T>(K, a.nb) / 4;
+                for (int bi = 0; bi < a.nb; ++bi) {  // workgroup-uniform
+                    float v[kLnMaxPerThread];
+#pragma unroll
+                    for (int k = 0; k < kLnMaxPerThread; ++k) {
+                        const int i = int(threadIdx.x) + k * kLnThreads;
+                        v[k] = i < K ? a.ln_x[size_t(bi) * K + i] + a.ln_y[size_t(bi) * K + i] : 0.f;
+                    }
+                    ln_rows(v, K, a.ln_g, a.ln_b, a.ln_eps, hs + size_t(bi) * K, lnsh);
+                }
+                __syncthreads();
+                if (blockIdx.x == 0 && a.ln_h)
+                    for (int i = threadIdx.x; i < a.nb * K; i += blockDim.x) a.ln_h[i] = hs[i];
+                stage_limbs<T>(hs, K, a.nb, K, xlds);
+            } else {
+                stage_limbs<T>(a.x, a.ldx, a.nb, a.w.K, xlds);
+            }
             lds_barrier();
             gemv_load_xq<T, B, CPL>(xlds, a.w.K, a.nb, a.g, cl, xr);
         } else {
@@ -130,7 +155,8 @@ hipError_t launch_t(const GemvArgs &a, int &grid, hipStream_t st, bool launch) {
     if constexpr (GTraits<T>::XW * B * CPL > kGemvMaxXRegs) {
         return hipErrorInvalidValue;
     } else {
-        const int lds = kGemvLimbs<T, MODE> ? xq_lds_bytes<T>(a.w.K, a.nb) : 0;
+        const int lds = (kGemvLimbs<T, MODE> ? xq_lds_bytes<T>(a.w.K, a.nb) : 0) +
+                        (MODE == 1 && a.ln_x ? a.nb * a.w.K * int(sizeof(float)) : 0);
         if (lds > 65536) return hipErrorInvalidValue;
         if constexpr (MODE != 0) {
             // per instantiation; the LDS bytes of one x row (nb = 1) set the occupancy
@@ -260,7 +286,7 @@ int gemv_argmax_parts(const DevMatrix &w, int b) {
 }
 
 hipError_t gemv_argmax(const DevMatrix &w, const float *x, int ldx, int b, int mask_id, float *pv, uint32_t *pi,
-                       int *parts, hipStream_t st) {
+                       int *parts, hipStream_t st, const GemvLn *ln) {
     GemvGeom g;
     int cpl;
     if (b < 1 || b > gemv_max_batch(w) || !gemv_geometry(w, &g, &cpl) || ldx % 4 ||
@@ -270,6 +296,17 @@ hipError_t gemv_argmax(const DevMatrix &w, const float *x, int ldx, int b, int m
     a.pv = pv;
     a.pi = pi;
     a.mask_id = mask_id;
+    if (ln) {
+        if (!(w.type == GGML_Q4_K || w.type == GGML_Q5_K || w.type == GGML_Q6_K || w.type == GGML_Q8_0) ||
+            w.K > kLnThreads * kLnMaxPerThread)
+            return hipErrorInvalidValue;
+        a.ln_x = ln->x;
+        a.ln_y = ln->y;
+        a.ln_g = ln->g;
+        a.ln_b = ln->b;
+        a.ln_eps = ln->eps;
+        a.ln_h = ln->h;
+    }
     int grid = gemv_grid(w, 1);
     const size_t row_bytes = w.bytes / size_t(w.N);
     a.nt_from = row_bytes ? int(std::min<size_t>(size_t(w.N), kLmHeadCachedBytes / row_bytes)) : w.N;

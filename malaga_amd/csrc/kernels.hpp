@@ -44,8 +44,15 @@ hipError_t gemv(const DevMatrix &w, const float *x, int ldx, int b, float *y, in
                 hipStream_t st);
 // Same product, but each workgroup writes the argmax (ties -> lowest index) of its
 // rows to pv/pi [b][parts]; logits are not stored.  Index `mask_id` (>= 0) is skipped.
+// ln (optional, integer formats): the GEMV's x is LayerNorm(ln->x + ln->y) ([b][K] rows,
+// residual_ln's arithmetic) computed inside the launch; ln->h (if set) receives it.
+struct GemvLn {
+    const float *x, *y, *g, *b;
+    float eps;
+    float *h;
+};
 hipError_t gemv_argmax(const DevMatrix &w, const float *x, int ldx, int b, int mask_id, float *pv, uint32_t *pi,
-                       int *parts, hipStream_t st);
+                       int *parts, hipStream_t st, const GemvLn *ln = nullptr);
 // Number of partial results gemv_argmax writes per batch row.
 int gemv_argmax_parts(const DevMatrix &w, int b);
 

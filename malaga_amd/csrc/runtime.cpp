@@ -763,7 +763,7 @@ bool Model::fusable(int b, int m, int s) const {
 }
 
 // src/model.rs:552-612 as six fused launches per layer (k_step.hip).
-void Model::step_fused(StaticState &st) {
+float *Model::step_fused(StaticState &st, bool final_ln) {
     hipStream_t s = ctx->stream;
     const int B = st.b, d = cfg.d_model, H = cfg.decoder_heads, hd = d / H;
     float *cur = st.x, *nxt = st.xb;
@@ -812,10 +812,11 @@ void Model::step_fused(StaticState &st) {
         check_hip(step_proj(l.down.w, l.down.b, B, st.u, st.y, s), "step_down");
     }
     // h = dec_norm(x + y) for the LM head
-    check_hip(residual_ln(cur, st.y, B, d, dec_norm.g, dec_norm.b, kLnEps, st.h, s), "residual_ln");
+    if (final_ln) check_hip(residual_ln(cur, st.y, B, d, dec_norm.g, dec_norm.b, kLnEps, st.h, s), "residual_ln");
+    return cur;
 }
 
-void Model::lm_head(StaticState &st, bool greedy_mode, int mask_id) {
+void Model::lm_head(StaticState &st, bool greedy_mode, int mask_id, const float *ln_x) {
     hipStream_t s = ctx->stream;
     const int B = st.b, d = cfg.d_model;
     if (greedy_mode) {
@@ -825,7 +826,8 @@ void Model::lm_head(StaticState &st, bool greedy_mode, int mask_id) {
         const int V = head.N, hmask = st.sl && mask_id >= 0 ? st.sl->row(uint32_t(mask_id)) : mask_id;
         int parts = 64;
         if (B <= gemv_max_batch(head)) {
-            check_hip(gemv_argmax(head, st.h, d, B, hmask, st.pv, st.pi, &parts, s), "lm_head");
+            const GemvLn ln{ln_x, st.y, dec_norm.g, dec_norm.b, kLnEps, st.h};
+            check_hip(gemv_argmax(head, st.h, d, B, hmask, st.pv, st.pi, &parts, s, ln_x ? &ln : nullptr), "lm_head");
         } else if (gemm_rx_supported(head, B)) {
             check_hip(gemm_argmax(head, st.h, d, B, hmask, st.pv, st.pi, &parts, s), "lm_head");
         } else {
@@ -858,8 +860,12 @@ void Model::lm_head(StaticState &st, bool greedy_mode, int mask_id) {
 
 void Model::step(StaticState &st, bool greedy_mode, int mask_id) {
     if (st.fused) {
-        step_fused(st);
-        lm_head(st, greedy_mode, mask_id);
+        // greedy batches up to the register GEMV fold the final LayerNorm into the head
+        const DevMatrix &head = st.sl ? st.sl->head : embed;
+        const bool fold = greedy_mode && st.b <= gemv_max_batch(head) && (head.type == GGML_Q4_K || head.type == GGML_Q5_K || head.type == GGML_Q6_K ||
+                                                                      head.type == GGML_Q8_0);
+        float *x = step_fused(st, !fold);
+        lm_head(st, greedy_mode, mask_id, fold ? x : nullptr);
         return;
     }
     hipStream_t s = ctx->stream;

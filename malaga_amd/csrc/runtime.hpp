@@ -241,8 +241,11 @@ class Model {
     void upload_lane_major(DevMatrix &m, const uint8_t *q_plane);
     Linear load_stacked(class GgufFile &g, const std::string &suffix, int layers, int n, int k);
     void matmul(const Linear &l, const float *x, int rows, float *y, bool relu, const float *resid);
-    void step_fused(StaticState &st);
-    void lm_head(StaticState &st, bool greedy_mode, int mask_id);
+    // final_ln: end with h = dec_norm(x + y); otherwise return x for the LM head to
+    // fold that LayerNorm into its launch (the residual buffer holding x)
+    float *step_fused(StaticState &st, bool final_ln = true);
+    // ln_x: x of the final LayerNorm when the head computes it (step_fused(st, false))
+    void lm_head(StaticState &st, bool greedy_mode, int mask_id, const float *ln_x = nullptr);
     bool no_fuse_ = false;  // MALAGA_NO_FUSED_STEP=1 forces the unfused step
     bool split_cross_ = false;  // MALAGA_SPLIT_CROSS_STEP=1: cross_q and cross attention as two launches
 };
