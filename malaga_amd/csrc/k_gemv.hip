@@ -224,10 +224,11 @@ constexpr int kGemvSmallRows = 65536;
 // The LM head streams its first kLmHeadCachedBytes of rows with cached loads and the
 // rest non-temporally: with the layer weights (112 MB for 600M q4_k_m) that part
 // stays in the 256 MB MALL from step to step, while an all-cached 215 MB head would
-// evict the layers.  Measured on 600M q4_k_m batch-1 decode, as a fraction of that
-// head: 0.3 (64 MB) beats 0, 0.2, 0.45 and 1.  A smaller head (a 37k-row shortlist
-// is 31 MB) is cached whole.
-constexpr size_t kLmHeadCachedBytes = 64000000;
+// evict the layers.  Measured on 600M q4_k_m batch-1 decode with one resident round
+// of workgroups: 0, 16 and 32 MB within noise of each other, 64 MB 0.15 ms per
+// sentence slower, 128 MB 0.6 ms slower.  A smaller head (a 37k-row shortlist is
+// 31 MB) is cached whole.
+constexpr size_t kLmHeadCachedBytes = 32000000;
 
 }  // namespace
 
