@@ -10,6 +10,7 @@ Also reported on the same JSON line:
     (21 source ids -> 18 tokens, crates/malaga/src/main.rs:409-436);
   * config 4: greedy batch 32 (lognormal lengths, length-sorted) and beam 4 at
     batch 8, sentences/s;
+  * config 5: NLLB-3.3B q4_k_m, one dynamic batch of 64, 64 greedy steps, sentences/s;
   * ``server``: the dynamic batching caller under a burst of 64 one-sentence
     requests from 64 threads, and 16 threads x 8 back-to-back requests;
   * ``fast_vocab``: shortlist (--fast-vocab) decoding beside exact decoding on the
@@ -21,7 +22,8 @@ Also reported on the same JSON line:
     256206 x 1024, 66% of the step's bytes), timed with HIP events on the stream
     it runs on;
   * ``cpu_baseline``: the C restatement of the reference path (oracle/) on the
-    host cores, config 1 (600M q8_0, 32 ids, 32 greedy steps).
+    host cores, config 1 (600M q8_0, 32 ids, 32 greedy steps); the GPU's tokens for
+    the same sentence must equal the oracle's (the run fails otherwise).
 
 Usage: python bench.py [--gpus 1] [--steps 200] [--warmup 3]
 """
@@ -445,11 +447,25 @@ def cpu_baseline():
     rows, _ = m.generate(src, TGT_LANG, max_new_tokens=32, eos_mask=True, kv_f16=False)
     dt = time.perf_counter() - a
     assert len(rows[0]) == 32
+    # untimed: the same decode with the GPU's f16 K/V rounding, for the token check
+    rows16, gap = m.generate(src, TGT_LANG, max_new_tokens=32, eos_mask=True, kv_f16=True)
     threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
-    return dict(value=dt * 1e3, unit="ms/sentence", cores=threads, kind="port",
+    return dict(value=dt * 1e3, unit="ms/sentence", cores=threads, kind="port", cpu_model=cpu_model(),
                 ms_per_token=dt * 1e3 / 33, load_s=load_s,
                 sample="config 1: NLLB-600M q8_0 random init, 1 sentence x 32 source ids, 32 greedy steps "
-                       "(33 decoder passes, EOS masked); oracle/oracle.c, f64-accumulated, OpenMP"), path, src
+                       "(33 decoder passes, EOS masked); oracle/oracle.c, f64-accumulated, OpenMP"), path, src, \
+        (rows, rows16, gap)
+
+
+def cpu_model() -> str:
+    """The host CPU's model name (lscpu / /proc/cpuinfo)."""
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
 
 
 def main():
@@ -458,8 +474,8 @@ def main():
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--skip-cpu", action="store_true")
-    ap.add_argument("--legs", default="bs1,batched,fastvocab,server,kernels,cpu",
-                    help="comma-separated subset of bs1,batched,fastvocab,server,kernels,cpu (profiling runs); "
+    ap.add_argument("--legs", default="bs1,batched,config5,fastvocab,server,kernels,cpu",
+                    help="comma-separated subset of bs1,batched,config5,fastvocab,server,kernels,cpu (profiling runs); "
                          "'config5' alone runs only the 3.3B batch-64 leg, 'mfma' alone the short "
                          "MFMA-GEMM runs used for counter collection")
     ap.add_argument("--roofline-only", action="store_true", help="only the LM-head roofline leg (for rocprof)")
@@ -517,6 +533,11 @@ def main():
     batched = bench_batched(T) if "batched" in legs else {"greedy_bs32": {"sentences_per_s": float("nan")}}
     for k, v in batched.items():
         log(f"{k}: {v['sentences_per_s']:.1f} sentences/s ({v.get('ms_per_batch', 0):.1f} ms/batch)")
+    config5 = None
+    if "config5" in legs:
+        config5 = bench_config5()
+        log(f"config5: {config5['sentences_per_s']:.1f} sentences/s ({config5['ms_per_batch']:.1f} ms/batch, encoder "
+            f"{config5['encoder_ms']:.1f} ms, {config5['decoder_ms_per_step']:.2f} ms/step)")
     fast = bench_fast_vocab(T) if "fastvocab" in legs else None
     server = bench_server(T) if "server" in legs else None
     if server:
@@ -534,16 +555,24 @@ def main():
     lm = gemv_rows[-1]
     roofline = dict(bound="hbm", achieved=round(lm["GBps"], 1), peak=PEAK_HBM_GBS, unit="GB/s",
                     frac=round(lm["GBps"] / PEAK_HBM_GBS, 4), traffic=measured_traffic(),
+                    traffic_source="profile-derived, not measured in this run: profiles/lm_head_q6k_traffic.txt "
+                                   "(rocprofv3 --pmc FETCH_SIZE, WRITE_SIZE; copy-kernel calibrated)",
                     kernel="k_gemv<q6_K,B=1,argmax> (LM head 256206x1024 + fused argmax partials)",
                     bytes_per_launch=lm["bytes"], us_per_launch=round(lm["us"], 3))
     q4_lm = next(r for r in gemv_rows if r["type"] == "q4_K" and r["name"] == "lm_head")
     cpu = None
     if "cpu" in legs:
         log("cpu baseline (oracle, config 1)")
-        cpu, q8path, csrc = cpu_baseline()
+        cpu, q8path, csrc, (rows32, rows16, gap) = cpu_baseline()
         T8 = M.Translator.load(q8path)
         opts = M.GenOptions(max_new_tokens=32, eos_mask=True)
-        T8.generate(csrc, TGT_LANG, opts)
+        gpu_rows = T8.generate(csrc, TGT_LANG, opts)
+        # parity of the timed workload: the GPU's tokens are the oracle's (f16 K/V, as the
+        # GPU keeps them), and the reference's f32-K/V generic path gives the same tokens
+        assert gpu_rows == rows16, "config 1: GPU tokens differ from the oracle's"
+        cpu["gpu_tokens_equal_oracle"] = gpu_rows == rows16
+        cpu["gpu_tokens_equal_oracle_f32_kv"] = gpu_rows == rows32
+        cpu["oracle_min_top2_gap"] = round(float(gap), 5)
         a = time.perf_counter()
         for _ in range(20):
             T8.generate(csrc, TGT_LANG, opts)
@@ -576,6 +605,7 @@ def main():
                             "published_rtx4090_ms": 16.4, "published_rtx4090_ms_per_token": 0.78},
         "sentences_per_s_bs32": round(batched["greedy_bs32"]["sentences_per_s"], 2),
         "batched": batched,
+        "config5": config5,
         "fast_vocab": fast,
         "server": server,
         "gemv_HBM_GBps_q4K_lm_head": round(q4_lm["GBps"], 1),

@@ -536,18 +536,77 @@ void orc_get_config(const orc_model *m, orc_config *out) { *out = m->cfg; }
 
 /* ----------------------------------------------------------- primitives */
 
-/* y[r][n] = f32(sum_k x[r][k] w[n][k]) + b[n]   (QMatMul then broadcast_add, src/model.rs:80-84) */
-static void linear(const float *x, int rows, const lin *l, float *y) {
-    const int N = l->n, K = l->k;
-#pragma omp parallel for schedule(static) collapse(2)
-    for (int r = 0; r < rows; ++r)
-        for (int n = 0; n < N; ++n) {
-            const float *xr = x + (size_t)r * K, *wr = l->w + (size_t)n * K;
-            double acc = 0;
-            for (int k = 0; k < K; ++k) acc += (double)xr[k] * wr[k];
-            y[(size_t)r * N + n] = (float)acc + l->b[n];
-        }
+/* y[r][n] = f32(sum_k x[r][k] w[n][k]) (+ b[n]).  Every sum starts at 0 and adds the
+ * products in k order in f64; a product of two floats is exact in f64, so each step
+ * rounds once whether or not it is fused.  Layout for speed only: the input rows are
+ * interleaved in blocks of 8 (xt[blk][k][8]), so one weight load serves 8 independent
+ * sums held in two 4-wide f64 vectors, and weight rows are the outer loop, so a batch
+ * reads every weight once. */
+typedef double orc_v4d __attribute__((vector_size(32)));
+typedef float orc_v4f __attribute__((vector_size(16)));
+
+/* acc[i][j] = sum_k xt[k][j] w_i[k] for 4 weight rows w_0..w_3 (8 independent chains). */
+__attribute__((target_clones("avx512f", "avx2", "default")))
+static void dot4x8(const float *xt, const float *w0, const float *w1, const float *w2, const float *w3, int K,
+                   double *acc) {
+    orc_v4d a0 = {0, 0, 0, 0}, a1 = a0, a2 = a0, a3 = a0, a4 = a0, a5 = a0, a6 = a0, a7 = a0;
+    for (int k = 0; k < K; ++k) {
+        orc_v4f lo, hi;
+        memcpy(&lo, xt + (size_t)k * 8, 16);
+        memcpy(&hi, xt + (size_t)k * 8 + 4, 16);
+        const orc_v4d xl = __builtin_convertvector(lo, orc_v4d), xh = __builtin_convertvector(hi, orc_v4d);
+        const double q0 = w0[k], q1 = w1[k], q2 = w2[k], q3 = w3[k];
+        const orc_v4d v0 = {q0, q0, q0, q0}, v1 = {q1, q1, q1, q1}, v2 = {q2, q2, q2, q2}, v3 = {q3, q3, q3, q3};
+        a0 += xl * v0;
+        a1 += xh * v0;
+        a2 += xl * v1;
+        a3 += xh * v1;
+        a4 += xl * v2;
+        a5 += xh * v2;
+        a6 += xl * v3;
+        a7 += xh * v3;
+    }
+    memcpy(acc, &a0, 32);
+    memcpy(acc + 4, &a1, 32);
+    memcpy(acc + 8, &a2, 32);
+    memcpy(acc + 12, &a3, 32);
+    memcpy(acc + 16, &a4, 32);
+    memcpy(acc + 20, &a5, 32);
+    memcpy(acc + 24, &a6, 32);
+    memcpy(acc + 28, &a7, 32);
 }
+
+static void dot_rows(const float *x, int rows, const float *w, int N, int K, const float *bias, float *y) {
+    const int nblk = (rows + 7) / 8;
+    float *xt = calloc((size_t)nblk * K * 8, sizeof(float));
+    for (int r = 0; r < rows; ++r)
+        for (int k = 0; k < K; ++k) xt[((size_t)(r / 8) * K + k) * 8 + r % 8] = x[(size_t)r * K + k];
+    /* row blocks in chunks of ~256 KB of xt, so a chunk stays in cache while the
+     * weight rows stream past it */
+    int chunk = (int)(262144 / ((size_t)K * 32));
+    if (chunk < 1) chunk = 1;
+    for (int b0 = 0; b0 < nblk; b0 += chunk) {
+        const int b1 = b0 + chunk < nblk ? b0 + chunk : nblk;
+#pragma omp parallel for schedule(static)
+        for (int n0 = 0; n0 < N; n0 += 4) {
+            const float *wr[4];
+            for (int i = 0; i < 4; ++i) wr[i] = w + (size_t)(n0 + i < N ? n0 + i : n0) * K;
+            for (int blk = b0; blk < b1; ++blk) {
+                double acc[32];
+                dot4x8(xt + (size_t)blk * K * 8, wr[0], wr[1], wr[2], wr[3], K, acc);
+                for (int i = 0; i < 4 && n0 + i < N; ++i)
+                    for (int j = 0; j < 8 && blk * 8 + j < rows; ++j) {
+                        const float v = (float)acc[i * 8 + j];
+                        y[(size_t)(blk * 8 + j) * N + n0 + i] = bias ? v + bias[n0 + i] : v;
+                    }
+            }
+        }
+    }
+    free(xt);
+}
+
+/* QMatMul then broadcast_add (src/model.rs:80-84) */
+static void linear(const float *x, int rows, const lin *l, float *y) { dot_rows(x, rows, l->w, l->n, l->k, l->b, y); }
 
 /* candle_nn LayerNorm, eps = 1e-5 (src/config.rs:58): biased variance. */
 static void layer_norm(const float *x, int rows, int d, const lnorm *l, float *y) {
@@ -631,20 +690,20 @@ orc_state *orc_encode(const orc_model *m, const uint32_t *ids, const uint32_t *l
         const enc_layer *l = &m->enc[li];
         layer_norm(x, n, d, &l->attn_norm, h);
         linear(h, n, &l->qkv, qkv);
-#pragma omp parallel for collapse(3) schedule(static)
+#pragma omp parallel for collapse(2) schedule(static)
         for (int i = 0; i < b; ++i)
-            for (int hh = 0; hh < H; ++hh)
-                for (int t = 0; t < s; ++t) {
-                    float *K = malloc((size_t)s * hd * 4), *V = malloc((size_t)s * hd * 4);
-                    for (int j = 0; j < s; ++j)
-                        for (int e = 0; e < hd; ++e) {
-                            K[j * hd + e] = qkv[((size_t)i * s + j) * 3 * d + d + hh * hd + e];
-                            V[j * hd + e] = qkv[((size_t)i * s + j) * 3 * d + 2 * d + hh * hd + e];
-                        }
+            for (int hh = 0; hh < H; ++hh) {
+                float *K = malloc((size_t)s * hd * 4), *V = malloc((size_t)s * hd * 4);
+                for (int j = 0; j < s; ++j)
+                    for (int e = 0; e < hd; ++e) {
+                        K[j * hd + e] = qkv[((size_t)i * s + j) * 3 * d + d + hh * hd + e];
+                        V[j * hd + e] = qkv[((size_t)i * s + j) * 3 * d + 2 * d + hh * hd + e];
+                    }
+                for (int t = 0; t < s; ++t)
                     attend(qkv + ((size_t)i * s + t) * 3 * d + hh * hd, K, V, s, hd, (int)lens[i],
                            att + ((size_t)i * s + t) * d + hh * hd);
-                    free(K); free(V);
-                }
+                free(K); free(V);
+            }
         linear(att, n, &l->out, y);
         for (size_t k = 0; k < (size_t)n * d; ++k) x[k] = x[k] + y[k];
         layer_norm(x, n, d, &l->ffn_norm, h);
@@ -757,14 +816,7 @@ int orc_decode(const orc_model *m, orc_state *st, const uint32_t *ids, int t, fl
     for (int i = 0; i < b; ++i) memcpy(last + (size_t)i * d, x + ((size_t)i * t + t - 1) * d, (size_t)d * 4);
     layer_norm(last, b, d, &m->dec_norm, h);
     if (hidden) memcpy(hidden, h, (size_t)b * d * 4);
-#pragma omp parallel for collapse(2) schedule(static)
-    for (int i = 0; i < b; ++i)
-        for (int v = 0; v < V; ++v) {
-            const float *hr = h + (size_t)i * d, *er = m->embed + (size_t)v * d;
-            double a = 0;
-            for (int k = 0; k < d; ++k) a += (double)hr[k] * er[k];
-            logits[(size_t)i * V + v] = (float)a;
-        }
+    dot_rows(h, b, m->embed, V, d, NULL, logits);
     free(last); free(x); free(h); free(qkv); free(att); free(y); free(u);
     return 0;
 }
