@@ -154,6 +154,21 @@ int mlg_greedy_sl(mlg_model *m, const mlg_batch *b, uint32_t tgt_lang, const cha
    once and replayed per step (MLG_FLAG_NO_GRAPH: eager); MLG_FLAG_EOS_MASK as for mlg_greedy. */
 int mlg_beam(mlg_model *m, const mlg_batch *b, uint32_t tgt_lang, int max_new, int beam_size, float length_penalty,
              uint32_t flags, uint32_t *out, int out_cap, int *out_len);
+/* The host half of Translator::beam_search (src/translator.rs:250-335: candidate merge,
+   length penalty, early stop, padding, final pick) over a caller's decoder: for callers
+   that run the decoder step and top-k themselves, and for tests of the merge rules.
+   decode(user, step, rows, reorder, next, vals, idx) is called for step 1 with
+   reorder = next = NULL (the rows have just decoded [decoder_start, tgt_lang]); for
+   step s > 1 row r first continues row reorder[r] (st.reorder, translator.rs:323) and
+   is fed next[r] (translator.rs:324-325).  It writes the top-k log-probs and tokens of
+   every row, best first with ties to the lowest token (translator.rs:343-358), into
+   vals/idx [rows][k] (rows = b * k) and returns 0, or nonzero to stop with
+   MLG_ERR_INVALID.  No device is used.  out is [b][out_cap] as mlg_generate. */
+typedef int (*mlg_beam_decode_fn)(void *user, int step, int rows, const uint32_t *reorder, const uint32_t *next,
+                                  float *vals, uint32_t *idx);
+int mlg_beam_search_host(int b, int k, int max_new, float length_penalty, uint32_t eos, mlg_beam_decode_fn fn,
+                         void *user, uint32_t *out, int out_cap, int *out_len);
+
 /* ---- dynamic batching caller (crates/malaga/src/server.rs:74-112) ----
    One inference thread per server owns the model.  Jobs submitted from any thread are
    queued; the thread takes every queued job, groups those with the same (src_lang,
@@ -183,6 +198,11 @@ int mlg_server_stats(const mlg_server *s, int64_t *jobs, int64_t *groups, int64_
 /* GraphCache::clear (src/graph.rs:192-200). */
 void mlg_clear_graphs(mlg_model *m);
 int mlg_graph_stats(const mlg_model *m, int *entries, int *graphs, int *capture_enabled);
+/* The cache's entries, least recently used first (the eviction order of src/graph.rs:301-323):
+   up to cap rows of (batch bucket, source bucket, output bucket, has a graph) into keys
+   [cap][4]; returns the number of entries (or a negative status).  Introspection for
+   tests; no counterpart in the reference. */
+int mlg_graph_cache_keys(const mlg_model *m, int *keys, int cap);
 /* Test hook: the n-th following device allocation fails with MLG_ERR_OOM (n < 0: off). */
 void mlg_debug_fail_alloc_after(long n);
 

@@ -243,6 +243,15 @@ class Translator:
         """GraphCache::clear (src/graph.rs:192-200)."""
         self.lib.mlg_clear_graphs(self.h)
 
+    def graph_keys(self) -> list[tuple[int, int, int, bool]]:
+        """(batch, source, output) bucket and whether a graph is captured, for every cached
+        state, least recently used first (src/graph.rs:301-323 evicts from the front)."""
+        buf = np.zeros((64, 4), dtype=np.int32)
+        n = int(self.lib.mlg_graph_cache_keys(self.h, buf.ctypes.data, 64))
+        if n < 0:
+            check(-n)
+        return [(int(a), int(b), int(c), bool(d)) for a, b, c, d in buf[: min(n, 64)]]
+
     def graph_stats(self) -> dict:
         e, g, c = C.c_int(), C.c_int(), C.c_int()
         check(self.lib.mlg_graph_stats(self.h, C.byref(e), C.byref(g), C.byref(c)))

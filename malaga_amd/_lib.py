@@ -50,6 +50,9 @@ class ShortlistSpec(C.Structure):
 
 
 TENSOR_FN = C.CFUNCTYPE(C.c_int, C.c_void_p, C.c_char_p, C.c_int64, C.POINTER(C.c_float))
+# mlg_beam_decode_fn(user, step, rows, reorder, next, vals, idx)
+BEAM_DECODE_FN = C.CFUNCTYPE(C.c_int, C.c_void_p, C.c_int, C.c_int, C.POINTER(C.c_uint32), C.POINTER(C.c_uint32),
+                             C.POINTER(C.c_float), C.POINTER(C.c_uint32))
 
 _P = C.c_void_p
 _u32p = C.POINTER(C.c_uint32)
@@ -89,6 +92,8 @@ SIGNATURES = {
     "mlg_greedy": (C.c_int, [_P, _P, C.c_uint32, C.c_int, C.c_int, C.c_uint32, _P, C.c_int, _P]),
     "mlg_greedy_sl": (C.c_int, [_P, _P, C.c_uint32, C.c_char_p, C.c_int, C.c_int, C.c_uint32, _P, C.c_int, _P]),
     "mlg_beam": (C.c_int, [_P, _P, C.c_uint32, C.c_int, C.c_int, C.c_float, C.c_uint32, _P, C.c_int, _P]),
+    "mlg_beam_search_host": (C.c_int, [C.c_int, C.c_int, C.c_int, C.c_float, C.c_uint32, BEAM_DECODE_FN, _P, _P,
+                                       C.c_int, _P]),
     "mlg_server_start": (C.c_int, [_P, C.POINTER(CGenOptions), C.POINTER(_P)]),
     "mlg_server_stop": (None, [_P]),
     "mlg_server_submit": (C.c_int, [_P, _P, _P, C.c_int, C.c_uint32, C.c_uint32, C.c_int, C.c_char_p,
@@ -100,6 +105,7 @@ SIGNATURES = {
                                    C.POINTER(C.c_int64)]),
     "mlg_clear_graphs": (None, [_P]),
     "mlg_graph_stats": (C.c_int, [_P, _intp, _intp, _intp]),
+    "mlg_graph_cache_keys": (C.c_int, [_P, _P, C.c_int]),
     "mlg_debug_fail_alloc_after": (None, [C.c_long]),
     "mlg_matrix_upload": (C.c_int, [_P, C.c_uint32, C.c_int, C.c_int, _P, C.POINTER(_P)]),
     "mlg_matrix_free": (None, [_P]),

@@ -7,6 +7,7 @@
 #include <memory>
 #include <string>
 
+#include "beam.hpp"
 #include "convert.hpp"
 #include "quant.hpp"
 #include "runtime.hpp"
@@ -399,6 +400,25 @@ int mlg_beam(mlg_model *m, const mlg_batch *b, uint32_t tgt_lang, int max_new, i
     });
 }
 
+int mlg_beam_search_host(int b, int k, int max_new, float length_penalty, uint32_t eos, mlg_beam_decode_fn fn,
+                         void *user, uint32_t *out, int out_cap, int *out_len) {
+    return guarded([&]() -> int {
+        if (b < 1 || k < 1 || max_new < 0 || !fn || !out || !out_len) return set_err(MLG_ERR_INVALID, "bad argument");
+        const size_t rows = size_t(b) * k;
+        std::vector<float> vals(rows * k);
+        std::vector<uint32_t> idx(rows * k);
+        mlg::BeamMerge merge(b, k, max_new, length_penalty, eos);
+        if (fn(user, 1, int(rows), nullptr, nullptr, vals.data(), idx.data()))
+            return set_err(MLG_ERR_INVALID, "decode callback failed at step 1");
+        for (int step = 1; step <= max_new; ++step) {
+            if (merge.merge(step, vals.data(), idx.data())) break;
+            if (fn(user, step + 1, int(rows), merge.reorder().data(), merge.next().data(), vals.data(), idx.data()))
+                return set_err(MLG_ERR_INVALID, "decode callback failed at step " + std::to_string(step + 1));
+        }
+        return write_rows(merge.result(), out, out_cap, out_len);
+    });
+}
+
 int mlg_server_start(mlg_model *m, const mlg_gen_options *defaults, mlg_server **out) {
     return guarded([&]() -> int {
         if (!m || !defaults || !out) return set_err(MLG_ERR_INVALID, "null argument");
@@ -462,6 +482,19 @@ int mlg_graph_stats(const mlg_model *m, int *entries, int *graphs, int *capture_
     *graphs = int(m->m->graphs.graphs());
     *capture_enabled = m->m->graphs.capture_enabled() ? 1 : 0;
     return MLG_OK;
+}
+
+int mlg_graph_cache_keys(const mlg_model *m, int *keys, int cap) {
+    if (!m || cap < 0 || (cap && !keys)) return -set_err(MLG_ERR_INVALID, "bad argument");
+    std::lock_guard<std::mutex> lk(m->m->ctx->mu);
+    const auto k = m->m->graphs.keys();
+    for (size_t i = 0; i < k.size() && int(i) < cap; ++i) {
+        keys[4 * i] = k[i].b;
+        keys[4 * i + 1] = k[i].s;
+        keys[4 * i + 2] = k[i].m;
+        keys[4 * i + 3] = k[i].graph ? 1 : 0;
+    }
+    return int(k.size());
 }
 
 void mlg_debug_fail_alloc_after(long n) { mlg::set_fail_alloc_after(n); }

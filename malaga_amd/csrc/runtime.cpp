@@ -7,6 +7,7 @@
 #include <cstring>
 #include <numeric>
 
+#include "beam.hpp"
 #include "gguf.hpp"
 #include "quant.hpp"
 
@@ -911,12 +912,36 @@ void Model::step(StaticState &st, bool greedy_mode, int mask_id) {
 
 // ------------------------------------------------------------ graph cache
 
+namespace {
+// Rust's str::parse::<usize>: the whole string is decimal digits (an optional leading
+// '+'), else no value.
+bool parse_usize(const char *s, size_t *out) {
+    if (!s) return false;
+    if (*s == '+') ++s;
+    if (!*s) return false;
+    size_t v = 0;
+    for (; *s; ++s) {
+        if (*s < '0' || *s > '9') return false;
+        v = v * 10 + size_t(*s - '0');
+    }
+    *out = v;
+    return true;
+}
+
+// src/graph.rs:184: capture stays on when the variable is unset, empty or "0"
+bool graph_switch_on(const char *name) {
+    const char *v = std::getenv(name);
+    return !v || !*v || std::string(v) == "0";
+}
+}  // namespace
+
+// src/graph.rs:182-186.  MALAGA_NO_HIP_GRAPH is this backend's name for the reference's
+// MALAGA_NO_CUDA_GRAPH; either turns capture off.
 GraphCache::GraphCache(Model *m) : model_(m) {
-    const char *mb = std::getenv("MALAGA_GRAPH_CACHE_MB");
-    long v = mb ? std::atol(mb) : 512;
-    max_bytes_ = size_t(v > 0 ? v : 512) << 20;
-    const char *no = std::getenv("MALAGA_NO_HIP_GRAPH");
-    capture_ = !no || !*no || std::string(no) == "0";
+    size_t mb = 512;
+    if (!parse_usize(std::getenv("MALAGA_GRAPH_CACHE_MB"), &mb)) mb = 512;
+    max_bytes_ = mb << 20;
+    capture_ = graph_switch_on("MALAGA_NO_CUDA_GRAPH") && graph_switch_on("MALAGA_NO_HIP_GRAPH");
 }
 
 GraphCache::~GraphCache() {
@@ -933,24 +958,52 @@ size_t GraphCache::graphs() const {
     return n;
 }
 
+// src/graph.rs:193-200, 325-335: destroyed graphs' memory goes back to the driver
 void GraphCache::clear() {
+    bool had_graphs = false;
     for (auto &e : entries_)
-        if (e.exec) (void)hipGraphExecDestroy(e.exec);
+        if (e.exec) {
+            (void)hipGraphExecDestroy(e.exec);
+            had_graphs = true;
+        }
     entries_.clear();
+    if (had_graphs) trim_graph_memory();
 }
 
+void GraphCache::trim_graph_memory() {
+    int dev = 0;
+    if (hipGetDevice(&dev) == hipSuccess) (void)hipDeviceGraphMemTrim(dev);
+}
+
+// src/graph.rs:301-323: drop least recently used entries (never `keep`) while the
+// entries plus one graph's reserve exceed the budget
 void GraphCache::evict(const Entry *keep) {
+    bool dropped_graph = false;
     for (;;) {
         size_t total = kGraphBytes;
         for (auto &e : entries_) total += e.bytes();
-        if (total <= max_bytes_ || entries_.size() <= 1) return;
+        if (total <= max_bytes_ || entries_.size() <= 1) break;
         auto victim = entries_.end();
         for (auto it = entries_.begin(); it != entries_.end(); ++it)
             if (&*it != keep && (victim == entries_.end() || it->last_used < victim->last_used)) victim = it;
-        if (victim == entries_.end()) return;
-        if (victim->exec) (void)hipGraphExecDestroy(victim->exec);
+        if (victim == entries_.end()) break;
+        if (victim->exec) {
+            (void)hipGraphExecDestroy(victim->exec);
+            dropped_graph = true;
+        }
         entries_.erase(victim);
     }
+    if (dropped_graph) trim_graph_memory();
+}
+
+std::vector<GraphCache::Key> GraphCache::keys() const {
+    std::vector<const Entry *> order;
+    for (auto &e : entries_) order.push_back(&e);
+    std::stable_sort(order.begin(), order.end(),
+                     [](const Entry *a, const Entry *b) { return a->last_used < b->last_used; });
+    std::vector<Key> out;
+    for (const Entry *e : order) out.push_back(Key{e->b, e->s, e->m, e->exec != nullptr});
+    return out;
 }
 
 std::vector<std::vector<uint32_t>> GraphCache::greedy(const Batch &src, uint32_t tgt_lang, int max_new,
@@ -1033,7 +1086,6 @@ std::vector<std::vector<uint32_t>> GraphCache::run(const Batch &src, uint32_t tg
         (void)hipGraphDestroy(graph);
         check_hip(ie, "graph instantiate");
         e->exec = exec;
-        evict(e);
     }
     if (fin_cap_ < size_t(st.b)) {
         if (fin_host_) (void)hipHostFree(fin_host_);
@@ -1082,12 +1134,17 @@ std::vector<std::vector<uint32_t>> GraphCache::run(const Batch &src, uint32_t tg
 
 std::vector<std::vector<uint32_t>> Model::beam(const Batch &src, uint32_t tgt_lang, int max_new, int k, float lp,
                                                bool eos_mask, bool use_graph) {
+    // the step writes K/V slot max_new and reads position max_new + pad + 1: both exist
+    // only up to max_position_embeddings - 2, the cap translate_batch's budget applies
+    if (k < 1 || max_new < 0 || max_new > cfg.max_position_embeddings - 2)
+        fail(ERR_INVALID, "beam: max_new " + std::to_string(max_new) + " outside 0.." +
+                              std::to_string(cfg.max_position_embeddings - 2) + " or beam size < 1");
     ensure_embed();
     hipStream_t s = ctx->stream;
     const int b = src.b, bk = b * k, V = cfg.vocab_size;
     const uint32_t eos = uint32_t(cfg.eos_token_id);
     const int mask_id = eos_mask ? cfg.eos_token_id : -1;
-    auto st = new_state(bk, src.s, std::min(max_new + 2, cfg.max_position_embeddings), true, true);
+    auto st = new_state(bk, src.s, max_new + 2, true, true);
     std::vector<uint32_t> expand(static_cast<size_t>(bk));
     for (int i = 0; i < bk; ++i) expand[i] = uint32_t(i / k);
     reset_state(*st, src, expand, uint32_t(cfg.decoder_start_token_id));
@@ -1165,61 +1222,15 @@ std::vector<std::vector<uint32_t>> Model::beam(const Batch &src, uint32_t tgt_la
     step(*st, false, mask_id);
     topk();
 
-    struct Hyp {
-        float score;
-        std::vector<uint32_t> toks;
-    };
-    std::vector<std::vector<Hyp>> alive(static_cast<size_t>(b), std::vector<Hyp>{Hyp{0.f, {}}});
-    std::vector<std::vector<Hyp>> done(static_cast<size_t>(b));
-    std::vector<uint8_t> is_done(static_cast<size_t>(b), 0);
-    auto penalty = [&](size_t len) { return std::pow(float(std::max<size_t>(len, 1)), lp); };
+    BeamMerge merge(b, k, max_new, lp, eos);
     const float *vals = h_vals;
     const uint32_t *idx = h_idx;
     for (int stp = 1; stp <= max_new; ++stp) {
         check_hip(hipMemcpyAsync(h_vals, d_vals, size_t(bk) * k * 4, hipMemcpyDeviceToHost, s), "D2H");
         check_hip(hipMemcpyAsync(h_idx, d_idx, size_t(bk) * k * 4, hipMemcpyDeviceToHost, s), "D2H");
         check_hip(hipStreamSynchronize(s), "sync");
-        std::vector<uint32_t> reorder, next;
-        for (int sn = 0; sn < b; ++sn) {
-            struct Cand {
-                float score;
-                int bi;
-                uint32_t tok;
-            };
-            std::vector<Cand> cands;
-            for (int bi = 0; bi < int(alive[sn].size()); ++bi) {
-                const int row = sn * k + bi;
-                for (int j = 0; j < k; ++j)
-                    cands.push_back({alive[sn][bi].score + vals[size_t(row) * k + j], bi, idx[size_t(row) * k + j]});
-            }
-            std::stable_sort(cands.begin(), cands.end(), [](const Cand &a, const Cand &c) { return a.score > c.score; });
-            std::vector<Hyp> new_alive;
-            for (auto &cd : cands) {
-                if (int(new_alive.size()) == k) break;
-                std::vector<uint32_t> toks = alive[sn][cd.bi].toks;
-                if (cd.tok == eos || stp == max_new) {
-                    if (cd.tok != eos) toks.push_back(cd.tok);
-                    const size_t len = toks.size() + 1;
-                    if (!is_done[sn]) done[sn].push_back({cd.score / penalty(len), toks});
-                    continue;
-                }
-                toks.push_back(cd.tok);
-                reorder.push_back(uint32_t(sn * k + cd.bi));
-                next.push_back(cd.tok);
-                new_alive.push_back({cd.score, std::move(toks)});
-            }
-            float best_done = -INFINITY;
-            for (auto &h : done[sn]) best_done = std::max(best_done, h.score);
-            const float best_alive = new_alive.empty() ? -INFINITY : new_alive[0].score / penalty(size_t(stp) + 1);
-            if (int(done[sn].size()) >= k && best_done >= best_alive) is_done[sn] = 1;
-            while (int(new_alive.size()) < k) {
-                reorder.push_back(uint32_t(sn * k));
-                next.push_back(eos);
-                new_alive.push_back({-INFINITY, {}});
-            }
-            alive[sn] = std::move(new_alive);
-        }
-        if (stp == max_new || std::all_of(is_done.begin(), is_done.end(), [](uint8_t v) { return v != 0; })) break;
+        if (merge.merge(stp, vals, idx)) break;
+        const std::vector<uint32_t> &reorder = merge.reorder(), &next = merge.next();
         // src/model.rs:209-226 gathers the self-attention caches by beam; here only the
         // row map changes (cross K/V and lens are identical within a sentence's beams, and
         // a reorder never leaves a sentence).  Slots 0 .. stp are written; the next step
@@ -1237,15 +1248,7 @@ std::vector<std::vector<uint32_t>> Model::beam(const Batch &src, uint32_t tgt_la
         check_hip(hipMemcpyAsync(st->ids, h_next, next.size() * 4, hipMemcpyHostToDevice, s), "H2D");
         advance();
     }
-    std::vector<std::vector<uint32_t>> res(static_cast<size_t>(b));
-    for (int sn = 0; sn < b; ++sn) {
-        const auto &list = done[sn].empty() ? alive[sn] : done[sn];
-        int best = -1;
-        for (int i = 0; i < int(list.size()); ++i)  // Iterator::max_by keeps the last maximum
-            if (best < 0 || !(list[i].score < list[best].score)) best = i;
-        if (best >= 0) res[sn] = list[best].toks;
-    }
-    return res;
+    return merge.result();
 }
 
 std::vector<float> Model::teacher_forced(const Batch &src, const std::vector<uint32_t> &tgt, int T) {

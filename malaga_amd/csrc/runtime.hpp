@@ -151,6 +151,13 @@ class GraphCache {
                                               bool eos_mask, bool use_graph, const Shortlist *sl = nullptr);
     size_t entries() const { return entries_.size(); }
     size_t graphs() const;
+    // Bucket keys (b, s, m) of the cached states, least recently used first, and
+    // whether each holds a captured graph.
+    struct Key {
+        int b, s, m;
+        bool graph;
+    };
+    std::vector<Key> keys() const;
 
   private:
     struct Entry {
@@ -164,6 +171,7 @@ class GraphCache {
     std::vector<std::vector<uint32_t>> run(const Batch &src, uint32_t tgt_lang, int max_new, int sync_every,
                                            bool eos_mask, bool use_graph, const Shortlist *sl);
     void evict(const Entry *keep);
+    static void trim_graph_memory();
     Model *model_;
     std::list<Entry> entries_;
     uint64_t clock_ = 0;

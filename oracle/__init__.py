@@ -26,6 +26,10 @@ class OrcConfig(C.Structure):
         "bos_token_id", "pad_token_id", "eos_token_id", "decoder_start_token_id")]
 
 
+# orc_script_fn(user, step, rows, hist, hist_len, logprobs)
+SCRIPT_FN = C.CFUNCTYPE(C.c_int, C.c_void_p, C.c_int, C.c_int, C.POINTER(C.c_uint32), C.c_int, C.POINTER(C.c_float))
+
+
 class OrcGenOptions(C.Structure):
     _fields_ = [("beam_size", C.c_int), ("max_new_tokens", C.c_int), ("length_penalty", C.c_float),
                 ("sync_every", C.c_int)]
@@ -62,6 +66,9 @@ def lib() -> C.CDLL:
         L.orc_decode.restype, L.orc_decode.argtypes = C.c_int, [P, P, P, C.c_int, P, P]
         L.orc_generate.restype = C.c_int
         L.orc_generate.argtypes = [P, P, P, C.c_int, C.c_uint32, C.POINTER(OrcGenOptions), C.c_int, P, C.c_int, P, P]
+        L.orc_beam_scripted.restype = C.c_int
+        L.orc_beam_scripted.argtypes = [C.c_int, C.c_int, C.c_int, C.c_uint32, C.c_int, C.c_float, C.c_int, SCRIPT_FN,
+                                        P, C.c_int, P, P]
         L.orc_generate_sl.restype = C.c_int
         L.orc_generate_sl.argtypes = [P, P, P, C.c_int, C.c_uint32, C.POINTER(OrcGenOptions), C.c_int, P, C.c_int,
                                       P, C.c_int, P, P]

@@ -976,30 +976,56 @@ static void log_softmax_row(const float *x, int V, float *y) {
     for (int v = 0; v < V; ++v) y[v] = (x[v] - mx) - ls;
 }
 
-static int cand_cmp_desc(float a, float b) { return a > b ? -1 : (a < b ? 1 : 0); }
+/* f32::total_cmp's order as a signed integer key (negative values' magnitude bits flipped). */
+static int32_t total_key(float f) {
+    int32_t i;
+    memcpy(&i, &f, 4);
+    return i ^ (int32_t)((uint32_t)(i >> 31) >> 1);
+}
 
-/* src/translator.rs:250-335 */
-static int beam_search(const orc_model *m, orc_state *st, int b, uint32_t tgt, int max_new, int k, float lp, int flags,
-                       uint32_t *out /* [b][max_new] */, int *ntok) {
-    const orc_config *c = &m->cfg;
-    const int V = c->vocab_size;
-    const uint32_t eos = (uint32_t)c->eos_token_id;
-    uint32_t *expand = malloc((size_t)b * k * 4);
-    for (int i = 0; i < b * k; ++i) expand[i] = (uint32_t)(i / k);
-    state_reorder(st, expand, b * k);
-    free(expand);
+/* sort_by(|a, c| c.0.total_cmp(&a.0)): descending under the total order */
+static int cand_cmp_desc(float a, float b) {
+    const int32_t x = total_key(a), y = total_key(b);
+    return x > y ? -1 : (x < y ? 1 : 0);
+}
+
+/* The decoder seen by the beam merge: `first` decodes [start, tgt] on all b*k rows,
+ * `advance` makes row r continue row reorder[r] (src/model.rs:209-226) and feeds it
+ * next[r]; both write one row of `width` values per decoder row.  `normalize`: the
+ * values are logits (log_softmax applied here, src/model.rs:615-617), otherwise they
+ * are already log-probabilities (scripted tests). */
+typedef struct {
+    int (*first)(void *self, float *out);
+    int (*advance)(void *self, const uint32_t *reorder, const uint32_t *next, float *out);
+    void *self;
+    int width, normalize;
+} beam_decoder;
+
+/* Planted mistakes for the tests that check the known answers can tell them apart
+ * (0 = the reference's rules). */
+enum {
+    MUT_STOP_STRICT = 1,     /* best_done > best_alive instead of >= */
+    MUT_ALIVE_PEN_STEP = 2,  /* best_alive / penalty(step) instead of penalty(step + 1) */
+    MUT_PAD_TOKEN = 3,       /* padded rows fed token 1 (NLLB's pad id) instead of EOS */
+    MUT_DONE_LEN = 4,        /* done score / penalty(tokens) instead of penalty(tokens + 1) */
+    MUT_FIRST_MAX = 5,       /* final pick: first maximum instead of Iterator::max_by's last */
+    MUT_NO_COUNT = 6,        /* stop without done.len() >= k */
+    MUT_PAD_SCORE = 8,       /* padded hypotheses score 0 instead of -inf */
+    MUT_PUSH_AFTER_DONE = 9  /* finished sentences keep collecting done hypotheses */
+};
+
+/* src/translator.rs:250-335 over any decoder. */
+static int beam_core(int b, int k, int max_new, float lp, uint32_t eos, int mask_eos, const beam_decoder *dec,
+                     int mutant, uint32_t *out /* [b][max_new] */, int *ntok) {
+    const int W = dec->width;
     hyp *alive = calloc((size_t)b * k, sizeof(hyp));
     int *nalive = calloc((size_t)b, sizeof(int));
-    hyp *done = NULL;
     int *ndone = calloc((size_t)b, sizeof(int)), *capdone = calloc((size_t)b, sizeof(int));
     hyp **dl = calloc((size_t)b, sizeof(hyp *));
     uint8_t *is_done = calloc((size_t)b, 1);
     for (int s = 0; s < b; ++s) { nalive[s] = 1; alive[s * k].score = 0; alive[s * k].n = 0; alive[s * k].toks = NULL; }
-    float *logits = malloc((size_t)b * k * V * 4), *lsm = malloc((size_t)V * 4);
-    uint32_t *start = malloc((size_t)b * k * 2 * 4);
-    for (int i = 0; i < b * k; ++i) { start[2 * i] = (uint32_t)c->decoder_start_token_id; start[2 * i + 1] = tgt; }
-    int rc = orc_decode(m, st, start, 2, logits, NULL);
-    free(start);
+    float *logits = malloc((size_t)b * k * W * 4), *lsm = malloc((size_t)W * 4);
+    int rc = dec->first(dec->self, logits);
     float *vals = malloc((size_t)b * k * k * 4);
     uint32_t *idx = malloc((size_t)b * k * k * 4), *reorder = malloc((size_t)b * k * 4), *next = malloc((size_t)b * k * 4);
     typedef struct { float score; int bi; uint32_t tok; } cand;
@@ -1008,9 +1034,11 @@ static int beam_search(const orc_model *m, orc_state *st, int b, uint32_t tgt, i
 #define PEN(len) powf((float)((len) > 1 ? (len) : 1), lp)
     for (int step = 1; rc == 0 && step <= max_new; ++step) {
         for (int r = 0; r < b * k; ++r) {
-            if (flags & ORC_EOS_MASK) logits[(size_t)r * V + eos] = -INFINITY; /* benchmark-only fixed lengths */
-            log_softmax_row(logits + (size_t)r * V, V, lsm);
-            topk_row(lsm, V, k, vals + (size_t)r * k, idx + (size_t)r * k);
+            float *row = logits + (size_t)r * W;
+            if (mask_eos) row[eos] = -INFINITY; /* benchmark-only fixed lengths */
+            if (dec->normalize) log_softmax_row(row, W, lsm);
+            else memcpy(lsm, row, (size_t)W * 4);
+            topk_row(lsm, W, k, vals + (size_t)r * k, idx + (size_t)r * k);
         }
         int nr = 0;
         for (int s = 0; s < b; ++s) {
@@ -1036,7 +1064,7 @@ static int beam_search(const orc_model *m, orc_state *st, int b, uint32_t tgt, i
                 const uint32_t tok = cands[ci].tok;
                 if (tok == eos || step == max_new) {
                     const int n = src->n + (tok != eos);
-                    if (!is_done[s]) {
+                    if (!is_done[s] || mutant == MUT_PUSH_AFTER_DONE) {
                         if (ndone[s] == capdone[s]) {
                             capdone[s] = capdone[s] ? 2 * capdone[s] : 8;
                             dl[s] = realloc(dl[s], (size_t)capdone[s] * sizeof(hyp));
@@ -1046,7 +1074,7 @@ static int beam_search(const orc_model *m, orc_state *st, int b, uint32_t tgt, i
                         h->toks = malloc((size_t)(n ? n : 1) * 4);
                         if (src->n) memcpy(h->toks, src->toks, (size_t)src->n * 4);
                         if (tok != eos) h->toks[src->n] = tok;
-                        h->score = cands[ci].score / PEN(n + 1);
+                        h->score = cands[ci].score / PEN(mutant == MUT_DONE_LEN ? n : n + 1);
                     }
                     continue;
                 }
@@ -1061,12 +1089,15 @@ static int beam_search(const orc_model *m, orc_state *st, int b, uint32_t tgt, i
             }
             float best_done = -INFINITY;
             for (int i = 0; i < ndone[s]; ++i) best_done = fmaxf(best_done, dl[s][i].score);
-            const float best_alive = na > 0 ? new_alive[0].score / PEN(step + 1) : -INFINITY;
-            if (ndone[s] >= k && best_done >= best_alive) is_done[s] = 1;
+            const float best_alive =
+                na > 0 ? new_alive[0].score / PEN(mutant == MUT_ALIVE_PEN_STEP ? step : step + 1) : -INFINITY;
+            const int enough = ndone[s] >= k || mutant == MUT_NO_COUNT;
+            if (enough && (mutant == MUT_STOP_STRICT ? best_done > best_alive : best_done >= best_alive)) is_done[s] = 1;
+            /* keep the batch rectangular: copies of beam 0 fed EOS, scored -inf */
             while (na < k) {
                 reorder[nr] = (uint32_t)(s * k);
-                next[nr++] = eos;
-                new_alive[na].score = -INFINITY;
+                next[nr++] = mutant == MUT_PAD_TOKEN ? 1u : eos;
+                new_alive[na].score = mutant == MUT_PAD_SCORE ? 0.f : -INFINITY;
                 new_alive[na].n = 0;
                 new_alive[na].toks = NULL;
                 ++na;
@@ -1078,16 +1109,18 @@ static int beam_search(const orc_model *m, orc_state *st, int b, uint32_t tgt, i
         int all = 1;
         for (int s = 0; s < b; ++s) all &= is_done[s];
         if (step == max_new || all) break;
-        state_reorder(st, reorder, b * k);
-        rc = orc_decode(m, st, next, 1, logits, NULL);
+        rc = dec->advance(dec->self, reorder, next, logits);
     }
 #undef PEN
     for (int s = 0; s < b; ++s) {
         const hyp *list = ndone[s] ? dl[s] : &alive[s * k];
         const int n = ndone[s] ? ndone[s] : nalive[s];
         int best = -1;
-        for (int i = 0; i < n; ++i) /* Iterator::max_by: the last maximum wins */
-            if (best < 0 || !(list[i].score < list[best].score)) best = i;
+        for (int i = 0; i < n; ++i) { /* Iterator::max_by: the last maximum wins */
+            const int32_t ki = total_key(list[i].score), kb = total_key(list[best < 0 ? 0 : best].score);
+            const int better = mutant == MUT_FIRST_MAX ? ki > kb : ki >= kb;
+            if (best < 0 || better) best = i;
+        }
         ntok[s] = 0;
         if (best >= 0) {
             const int nn = list[best].n < max_new ? list[best].n : max_new;
@@ -1100,9 +1133,95 @@ static int beam_search(const orc_model *m, orc_state *st, int b, uint32_t tgt, i
         for (int i = 0; i < ndone[s]; ++i) free(dl[s][i].toks);
         free(dl[s]);
     }
-    (void)done;
     free(dl); free(ndone); free(capdone); free(alive); free(nalive); free(is_done); free(logits); free(lsm);
     free(vals); free(idx); free(reorder); free(next); free(cands); free(new_alive);
+    return rc;
+}
+
+/* The model as the beam's decoder: the cache of every row, reordered and fed by the merge. */
+typedef struct {
+    const orc_model *m;
+    orc_state *st;
+    uint32_t tgt;
+    int rows;
+} model_decoder;
+
+static int model_first(void *self, float *out) {
+    model_decoder *md = self;
+    uint32_t *start = malloc((size_t)md->rows * 2 * 4);
+    for (int i = 0; i < md->rows; ++i) {
+        start[2 * i] = (uint32_t)md->m->cfg.decoder_start_token_id;
+        start[2 * i + 1] = md->tgt;
+    }
+    const int rc = orc_decode(md->m, md->st, start, 2, out, NULL);
+    free(start);
+    return rc;
+}
+
+static int model_advance(void *self, const uint32_t *reorder, const uint32_t *next, float *out) {
+    model_decoder *md = self;
+    state_reorder(md->st, reorder, md->rows);
+    return orc_decode(md->m, md->st, next, 1, out, NULL);
+}
+
+/* src/translator.rs:250-335 */
+static int beam_search(const orc_model *m, orc_state *st, int b, uint32_t tgt, int max_new, int k, float lp, int flags,
+                       uint32_t *out /* [b][max_new] */, int *ntok) {
+    uint32_t *expand = malloc((size_t)b * k * 4);
+    for (int i = 0; i < b * k; ++i) expand[i] = (uint32_t)(i / k);
+    state_reorder(st, expand, b * k);
+    free(expand);
+    model_decoder md = {m, st, tgt, b * k};
+    const beam_decoder dec = {model_first, model_advance, &md, m->cfg.vocab_size, 1};
+    return beam_core(b, k, max_new, lp, (uint32_t)m->cfg.eos_token_id, (flags & ORC_EOS_MASK) != 0, &dec, 0, out,
+                     ntok);
+}
+
+/* A scripted decoder: each row's history (the tokens fed after [start, tgt], reordered
+ * with the row) goes to the caller, which returns that row's log-probabilities. */
+typedef struct {
+    orc_script_fn fn;
+    void *user;
+    int rows, len, cap, step;
+    uint32_t *hist, *tmp; /* [rows][cap] */
+} script_decoder;
+
+static int script_first(void *self, float *out) {
+    script_decoder *sd = self;
+    sd->step = 1;
+    return sd->fn(sd->user, 1, sd->rows, sd->hist, 0, out);
+}
+
+static int script_advance(void *self, const uint32_t *reorder, const uint32_t *next, float *out) {
+    script_decoder *sd = self;
+    if (sd->len + 1 > sd->cap) return -1;
+    for (int r = 0; r < sd->rows; ++r) {
+        memcpy(sd->tmp + (size_t)r * sd->cap, sd->hist + (size_t)reorder[r] * sd->cap, (size_t)sd->len * 4);
+        sd->tmp[(size_t)r * sd->cap + sd->len] = next[r];
+    }
+    uint32_t *t = sd->hist;
+    sd->hist = sd->tmp;
+    sd->tmp = t;
+    ++sd->len;
+    ++sd->step;
+    /* rows handed over packed: [rows][len] */
+    uint32_t *packed = malloc((size_t)sd->rows * sd->len * 4 + 4);
+    for (int r = 0; r < sd->rows; ++r) memcpy(packed + (size_t)r * sd->len, sd->hist + (size_t)r * sd->cap, (size_t)sd->len * 4);
+    const int rc = sd->fn(sd->user, sd->step, sd->rows, packed, sd->len, out);
+    free(packed);
+    return rc;
+}
+
+int orc_beam_scripted(int b, int k, int V, uint32_t eos, int max_new, float length_penalty, int flags,
+                      orc_script_fn fn, void *user, int mutant, uint32_t *out, int *ntok) {
+    if (b <= 0 || k <= 0 || k > V || max_new < 0 || eos >= (uint32_t)V || !fn) return -1;
+    script_decoder sd = {fn, user, b * k, 0, max_new + 1, 0, NULL, NULL};
+    sd.hist = calloc((size_t)sd.rows * sd.cap, 4);
+    sd.tmp = calloc((size_t)sd.rows * sd.cap, 4);
+    const beam_decoder dec = {script_first, script_advance, &sd, V, 0};
+    const int rc = beam_core(b, k, max_new, length_penalty, eos, (flags & ORC_EOS_MASK) != 0, &dec, mutant, out, ntok);
+    free(sd.hist);
+    free(sd.tmp);
     return rc;
 }
 

@@ -44,6 +44,14 @@ int orc_decode(const orc_model *m, orc_state *st, const uint32_t *ids, int t, fl
 int orc_generate(const orc_model *m, const uint32_t *ids, const uint32_t *lens, int b, uint32_t tgt_lang,
                  const orc_gen_options *o, int flags, uint32_t *out, int out_cap, int *out_len, float *min_gap);
 
+/* Beam search (src/translator.rs:250-335) over a scripted decoder: fn fills
+ * logprobs[rows][V] given each row's history hist[rows][hist_len] (the tokens fed after
+ * [decoder_start, tgt_lang], reordered with the row); step is 1-based.  mutant != 0
+ * plants one of the oracle's numbered mistakes (tests only).  out is [b][max_new]. */
+typedef int (*orc_script_fn)(void *user, int step, int rows, const uint32_t *hist, int hist_len, float *logprobs);
+int orc_beam_scripted(int b, int k, int V, uint32_t eos, int max_new, float length_penalty, int flags,
+                      orc_script_fn fn, void *user, int mutant, uint32_t *out, int *ntok);
+
 #ifdef __cplusplus
 }
 #endif
