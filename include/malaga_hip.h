@@ -228,12 +228,14 @@ int mlg_gemm_argmax(const mlg_matrix *w, const float *x, int M, int mask_id, flo
  * partials pv/pi [b][mlg_gemv_argmax_parts(w, b)] (one per workgroup launched). */
 int mlg_gemv_argmax_parts(const mlg_matrix *w, int b);
 int mlg_gemv_argmax(const mlg_matrix *w, const float *x, int b, int mask_id, float *pv, uint32_t *pi, void *stream);
-/* bias_residual_ln (kernels/malaga.cu:89-105) with the bias already in y. */
+/* bias_residual_ln (kernels/malaga.cu:89-105 semantics) with the bias already in y: x += y,
+   ln_out = LayerNorm(x) (biased variance); d % 4 == 0, d <= 4096. */
 int mlg_residual_ln(float *x, const float *y, int rows, int d, const float *gamma, const float *beta, float eps,
                     float *ln_out, void *stream);
 int mlg_layernorm(const float *x, int rows, int d, const float *gamma, const float *beta, float eps, float *out,
                   void *stream);
-/* attn_decode (kernels/malaga.cu:165-227). K, V: f16 [b][H][L][hd]. */
+/* attn_decode (kernels/malaga.cu:165-227 semantics). K, V: f16 [b][H][L][hd]; hd one of 8, 16,
+   32, 64, 128, 256 (else MLG_ERR_UNSUPPORTED); n = lens[row] keys, or *step + 1 without lens. */
 int mlg_attn_decode(const float *q, const void *K, const void *V, int b, int H, int hd, int L, const uint32_t *lens,
                     const uint32_t *step, float *out, void *stream);
 /* argmax_partial (kernels/malaga.cu:247-280): pv/pi [b][parts]. */

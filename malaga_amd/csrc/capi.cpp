@@ -4,6 +4,7 @@
 #include "../../include/malaga_hip.h"
 
 #include <cstring>
+#include <initializer_list>
 #include <memory>
 #include <string>
 
@@ -115,6 +116,12 @@ std::vector<std::vector<uint32_t>> rows_of(const uint32_t *ids, const uint32_t *
         off += lens[i];
     }
     return src;
+}
+
+bool aligned16(std::initializer_list<const void *> ptrs) {
+    for (const void *p : ptrs)
+        if (reinterpret_cast<uintptr_t>(p) % 16) return false;
+    return true;
 }
 
 int write_rows(const std::vector<std::vector<uint32_t>> &rows, uint32_t *out, int out_cap, int *out_len) {
@@ -588,19 +595,24 @@ int mlg_gemv_argmax(const mlg_matrix *w, const float *x, int b, int mask_id, flo
 int mlg_residual_ln(float *x, const float *y, int rows, int d, const float *gamma, const float *beta, float eps,
                     float *ln_out, void *stream) {
     if (!x || !y || !gamma || !beta || !ln_out || rows < 1 || d < 1) return set_err(MLG_ERR_INVALID, "bad argument");
+    if (d % 4 || d > 4096 || !aligned16({x, y, gamma, beta, ln_out}))
+        return set_err(MLG_ERR_INVALID, "residual_ln: d % 4 == 0, d <= 4096 and 16-byte aligned rows required");
     return hip_status(mlg::residual_ln(x, y, rows, d, gamma, beta, eps, ln_out, as_stream(stream)), "residual_ln");
 }
 
 int mlg_layernorm(const float *x, int rows, int d, const float *gamma, const float *beta, float eps, float *out,
                   void *stream) {
     if (!x || !gamma || !beta || !out || rows < 1 || d < 1) return set_err(MLG_ERR_INVALID, "bad argument");
+    if (d % 4 || d > 4096 || !aligned16({x, gamma, beta, out}))
+        return set_err(MLG_ERR_INVALID, "layernorm: d % 4 == 0, d <= 4096 and 16-byte aligned rows required");
     return hip_status(mlg::layernorm(x, rows, d, gamma, beta, eps, out, as_stream(stream)), "layernorm");
 }
 
 int mlg_attn_decode(const float *q, const void *K, const void *V, int b, int H, int hd, int L, const uint32_t *lens,
                     const uint32_t *step, float *out, void *stream) {
-    if (!q || !K || !V || !out || b < 1 || H < 1 || hd < 8 || L < 1 || (!lens && !step))
+    if (!q || !K || !V || !out || b < 1 || H < 1 || L < 1 || (!lens && !step))
         return set_err(MLG_ERR_INVALID, "bad argument");
+    if (!mlg::attn_head_size_supported(hd)) return set_err(MLG_ERR_UNSUPPORTED, "head size " + std::to_string(hd));
     return hip_status(mlg::attn_decode(q, static_cast<const __half *>(K), static_cast<const __half *>(V), b, H, hd, L,
                                        lens, lens ? nullptr : step, out, as_stream(stream)),
                       "attn_decode");

@@ -169,32 +169,111 @@ __device__ __forceinline__ float block_sum(float v, float *sh) {
     return t;
 }
 
-constexpr int kLnThreads = 256;
-constexpr int kLnMaxPerThread = 16;  // d <= 4096
+__device__ __forceinline__ void add4(float4 &a, const float4 &b) {
+    a.x += b.x;
+    a.y += b.y;
+    a.z += b.z;
+    a.w += b.w;
+}
 
-// LayerNorm of v[] (thread's elements i = tid + k * 256) with biased variance,
-// two passes in registers (kernels/malaga.cu:66-86 semantics).
-__device__ __forceinline__ void ln_rows(const float (&v)[kLnMaxPerThread], int d, const float *g, const float *b,
-                                        float eps, float *out, float *sh) {
-    float s = 0.f;
+__device__ __forceinline__ float4 ld4(const float *p, int f) { return reinterpret_cast<const float4 *>(p)[f]; }
+
+// ---- LayerNorm statistics in f64 (biased variance, eps inside the root) ----------
+// The f64 sums of a float4's values and squares, paired as the fused step's prologue.
+__device__ __forceinline__ void ln_acc(const float4 &v, double &s1, double &s2) {
+    const double x0 = v.x, x1 = v.y, x2 = v.z, x3 = v.w;
+    s1 += (x0 + x1) + (x2 + x3);
+    s2 += (x0 * x0 + x1 * x1) + (x2 * x2 + x3 * x3);
+}
+
+// Mean and 1 / sqrt(var + eps) of a row of d values from the wave's lanes' f64 sums of
+// x and x^2 (one pass); every lane receives them.
+__device__ __forceinline__ void wave_ln_stats(double s1, double s2, int d, float eps, float &mean, float &rstd) {
+    s1 = wave_sum_f64(s1);
+    s2 = wave_sum_f64(s2);
+    const double mu = s1 / d;
+    const double var = fmax(s2 / d - mu * mu, 0.0);
+    mean = float(mu);
+    rstd = float(1.0 / sqrt(var + double(eps)));
+}
+
+__device__ __forceinline__ float4 ln_apply(const float4 &v, float mean, float rstd, const float4 &g, const float4 &b) {
+    return make_float4((v.x - mean) * rstd * g.x + b.x, (v.y - mean) * rstd * g.y + b.y,
+                       (v.z - mean) * rstd * g.z + b.z, (v.w - mean) * rstd * g.w + b.w);
+}
+
+// Row LayerNorm by one wave, no LDS and no barrier: lane l holds the float4 slots
+// f = l + 64 j (j < NJ, so d <= 256 NJ, d % 4 == 0) of the row in registers between the
+// statistics and the normalization.  form(f) returns slot f of the input row; keep(f, v)
+// sees it first (a residual kernel stores it there).  out may point to global memory
+// or LDS.
+template <int NJ, class Form, class Keep>
+__device__ __forceinline__ void wave_row_layernorm(int d, Form form, Keep keep, const float *g, const float *b,
+                                                   float eps, float *out) {
+    const int lane = threadIdx.x & 63, nf = d >> 2;
+    float4 v[NJ];
+    double s1 = 0.0, s2 = 0.0;
 #pragma unroll
-    for (int k = 0; k < kLnMaxPerThread; ++k) s += v[k];
-    const float mean = block_sum(s, sh) / float(d);
-    float s2 = 0.f;
-#pragma unroll
-    for (int k = 0; k < kLnMaxPerThread; ++k) {
-        const int i = threadIdx.x + k * kLnThreads;
-        const float c = i < d ? v[k] - mean : 0.f;
-        s2 += c * c;
+    for (int j = 0; j < NJ; ++j) {
+        const int f = lane + 64 * j;
+        if (f < nf) {
+            v[j] = form(f);
+            keep(f, v[j]);
+            ln_acc(v[j], s1, s2);
+        }
     }
-    __syncthreads();  // sh is reused
-    const float rstd = rsqrtf(block_sum(s2, sh) / float(d) + eps);
+    float mean, rstd;
+    wave_ln_stats(s1, s2, d, eps, mean, rstd);
 #pragma unroll
-    for (int k = 0; k < kLnMaxPerThread; ++k) {
-        const int i = threadIdx.x + k * kLnThreads;
-        if (i < d) out[i] = (v[k] - mean) * rstd * g[i] + b[i];
+    for (int j = 0; j < NJ; ++j) {
+        const int f = lane + 64 * j;
+        if (f < nf) reinterpret_cast<float4 *>(out)[f] = ln_apply(v[j], mean, rstd, ld4(g, f), ld4(b, f));
     }
 }
+
+struct NoKeep {
+    __device__ void operator()(int, const float4 &) const {}
+};
+
+// Row LayerNorm by a workgroup of 256 threads: thread t holds the float4 slots
+// f = t + 256 c (c < NC, d <= 1024 NC) in registers; the f64 sums go across the wave
+// with DPP and across the four waves through red[8] (LDS, fixed order), as the fused
+// step's prologue does.  Every thread of the workgroup must call it (two barriers).
+template <int NC, class Form, class Keep>
+__device__ __forceinline__ void workgroup_row_layernorm(int d, Form form, Keep keep, const float *g, const float *b,
+                                                        float eps, float *out, double *red) {
+    const int t = threadIdx.x, nf = d >> 2, lane = t & 63, w = t >> 6;
+    float4 v[NC];
+    double s1 = 0.0, s2 = 0.0;
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+        const int f = t + 256 * c;
+        if (f < nf) {
+            v[c] = form(f);
+            keep(f, v[c]);
+            ln_acc(v[c], s1, s2);
+        }
+    }
+    s1 = wave_sum_f64(s1);
+    s2 = wave_sum_f64(s2);
+    if (lane == 0) {
+        red[w] = s1;
+        red[4 + w] = s2;
+    }
+    __syncthreads();
+    const double mu = ((red[0] + red[1]) + (red[2] + red[3])) / d;
+    const double var = fmax(((red[4] + red[5]) + (red[6] + red[7])) / d - mu * mu, 0.0);
+    __syncthreads();  // red is free for the next row
+    const float mean = float(mu), rstd = float(1.0 / sqrt(var + double(eps)));
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+        const int f = t + 256 * c;
+        if (f < nf) reinterpret_cast<float4 *>(out)[f] = ln_apply(v[c], mean, rstd, ld4(g, f), ld4(b, f));
+    }
+}
+
+// Largest row a wave normalizes (16 float4 slots per lane).
+constexpr int kWaveLnMaxD = 4096;
 
 __device__ __forceinline__ float block_max(float v, float *sh) {
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, nw = blockDim.x >> 6;

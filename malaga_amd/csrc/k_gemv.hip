@@ -1,6 +1,10 @@
 // Stand-alone dequant-GEMV kernels (batch 1..4): y = x W^T (+ bias) (relu), and
 // the LM-head variant whose epilogue keeps a per-workgroup argmax instead of
 // storing the logits.  The streaming core is gemv_core.hpp.
+#include <map>
+#include <mutex>
+#include <tuple>
+
 #include "gemv_core.hpp"
 #include "kernels.hpp"
 
@@ -66,18 +70,21 @@ __global__ __launch_bounds__(256) void k_gemv(GemvArgs a) {
     auto load_x = [&] {
         if constexpr (kGemvLimbs<T, MODE>) {
             if (MODE == 1 && a.ln_x) {
-                // k_residual_ln's arithmetic (ln_rows, 256 threads), rows kept in LDS
-                __shared__ float lnsh[16];
+                // h = LayerNorm(ln_x + ln_y) (biased variance, f64 statistics), each row
+                // spread over the workgroup's 256 threads, into LDS after the limbs
+                __shared__ double red[8];
                 const int K = a.w.K;
                 float *hs = reinterpret_cast<float *>(xlds) + xq_lds_bytes<T>(K, a.nb) / 4;
                 for (int bi = 0; bi < a.nb; ++bi) {  // workgroup-uniform
-                    float v[kLnMaxPerThread];
-#pragma unroll
-                    for (int k = 0; k < kLnMaxPerThread; ++k) {
-                        const int i = int(threadIdx.x) + k * kLnThreads;
-                        v[k] = i < K ? a.ln_x[size_t(bi) * K + i] + a.ln_y[size_t(bi) * K + i] : 0.f;
-                    }
-                    ln_rows(v, K, a.ln_g, a.ln_b, a.ln_eps, hs + size_t(bi) * K, lnsh);
+                    const float4 *xr = reinterpret_cast<const float4 *>(a.ln_x + size_t(bi) * K);
+                    const float4 *yr = reinterpret_cast<const float4 *>(a.ln_y + size_t(bi) * K);
+                    auto form = [&](int f) {
+                        float4 v = xr[f];
+                        add4(v, yr[f]);
+                        return v;
+                    };
+                    workgroup_row_layernorm<kWaveLnMaxD / 1024>(K, form, NoKeep{}, a.ln_g, a.ln_b, a.ln_eps,
+                                                                hs + size_t(bi) * K, red);
                 }
                 __syncthreads();
                 if (blockIdx.x == 0 && a.ln_h)
@@ -134,15 +141,27 @@ __global__ __launch_bounds__(256) void k_gemv(GemvArgs a) {
 }
 
 // Workgroups of one launch that are resident on the device at once (CUs x blocks per
-// CU at this kernel's occupancy), or 0 if the runtime cannot say.
+// CU at this kernel's occupancy with `lds` dynamic LDS bytes), or 0 if the runtime
+// cannot say.  Remembered per (kernel, device, LDS bytes).
 inline int resident_grid(const void *kernel, int lds) {
-    int dev = 0, cus = 0, per_cu = 0;
-    if (hipGetDevice(&dev) != hipSuccess ||
-        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+    static std::mutex mu;
+    static std::map<std::tuple<const void *, int, int>, int> known;
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return 0;
+    const auto key = std::make_tuple(kernel, dev, lds);
+    std::lock_guard<std::mutex> lk(mu);
+    auto it = known.find(key);
+    if (it != known.end()) return it->second;
+    int cus = 0, per_cu = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
         hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, 256, size_t(lds)) != hipSuccess)
         return 0;
-    return cus * per_cu;
+    return known[key] = cus * per_cu;
 }
+
+// Static LDS of k_gemv: the argmax epilogue's per-wave (value, index) pairs and the
+// folded LayerNorm's wave sums.
+constexpr int kGemvStaticLds = 4 * 4 * (sizeof(float) + sizeof(uint32_t)) + 8 * sizeof(double);
 
 // grid: in, the workgroups that cover the rows; out, the workgroups launched.  The
 // large-matrix modes launch at most one resident round (each wave then streams its
@@ -157,11 +176,11 @@ hipError_t launch_t(const GemvArgs &a, int &grid, hipStream_t st, bool launch) {
     } else {
         const int lds = (kGemvLimbs<T, MODE> ? xq_lds_bytes<T>(a.w.K, a.nb) : 0) +
                         (MODE == 1 && a.ln_x ? a.nb * a.w.K * int(sizeof(float)) : 0);
-        if (lds > 65536) return hipErrorInvalidValue;
+        if (lds + kGemvStaticLds > 65536) return hipErrorInvalidValue;
         if constexpr (MODE != 0) {
-            // per instantiation; the LDS bytes of one x row (nb = 1) set the occupancy
-            static const int resident = resident_grid(reinterpret_cast<const void *>(&k_gemv<T, B, CPL, MODE, LM, L2>),
-                                                      kGemvLimbs<T, MODE> ? xq_lds_bytes<T>(a.w.K, B) : 0);
+            // the occupancy of this launch's LDS bytes (limbs of nb rows, the folded
+            // LayerNorm's rows)
+            const int resident = resident_grid(reinterpret_cast<const void *>(&k_gemv<T, B, CPL, MODE, LM, L2>), lds);
             if (resident > 0 && grid > resident) grid = resident;
         }
         if (!launch) return hipSuccess;
@@ -299,7 +318,7 @@ hipError_t gemv_argmax(const DevMatrix &w, const float *x, int ldx, int b, int m
     a.mask_id = mask_id;
     if (ln) {
         if (!(w.type == GGML_Q4_K || w.type == GGML_Q5_K || w.type == GGML_Q6_K || w.type == GGML_Q8_0) ||
-            w.K > kLnThreads * kLnMaxPerThread)
+            w.K > kWaveLnMaxD || w.K % 4)
             return hipErrorInvalidValue;
         a.ln_x = ln->x;
         a.ln_y = ln->y;

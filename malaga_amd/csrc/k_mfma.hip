@@ -566,49 +566,37 @@ hipError_t launch(const MfmaArgs &a, int M, int ks, hipStream_t st) {
 }
 
 // Split-K reduction fused with the decoder's residual add and the next LayerNorm
-// (src/model.rs:183-187): y = sum_z part[z][m] (in order) + bias; x[m] += y;
-// h[m] = LayerNorm(x[m]) with biased variance.  One workgroup of 1024 threads per
-// row, N <= 4096.
-__global__ __launch_bounds__(1024) void k_splitk_residual_ln(const float *part, int ks, int M, int N,
-                                                              const float *bias, float *x, const float *g,
-                                                              const float *b, float eps, float *h) {
-    __shared__ float sh[16];
-    const int m = blockIdx.x, t = threadIdx.x;
+// (src/model.rs:183-187): y = sum_z part[z][m] (in z order) + bias; x[m] += y;
+// h[m] = LayerNorm(x[m]) with biased variance (f64 statistics).  One workgroup of 256
+// threads per row, each thread on float4 slots t + 256 c; N <= 4096, N % 4 == 0.
+__global__ __launch_bounds__(256) void k_splitk_residual_ln(const float *part, int ks, int M, int N,
+                                                             const float *bias, float *x, const float *g,
+                                                             const float *b, float eps, float *h) {
+    __shared__ double red[8];
+    const int m = blockIdx.x;
     const size_t mn = size_t(M) * N, off = size_t(m) * N;
-    float v[4];
-    float s1 = 0.f;
+    float4 *xr = reinterpret_cast<float4 *>(x + off);
+    auto form = [&](int f) {
+        // the partials requested eight at a time, then added in z order
+        float4 y = make_float4(0.f, 0.f, 0.f, 0.f);
+        for (int z0 = 0; z0 < ks; z0 += 8) {
+            float4 p8[8];
 #pragma unroll
-    for (int k = 0; k < 4; ++k) {
-        const int i = t + 1024 * k;
-        v[k] = 0.f;
-        if (i < N) {
-            // partials requested 8 at a time, then added in z order
-            float y = 0.f;
-            for (int z0 = 0; z0 < ks; z0 += 8) {
-                float p8[8];
+            for (int u = 0; u < 8; ++u)
+                p8[u] = z0 + u < ks ? ld4(part + size_t(z0 + u) * mn + off, f) : make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll
-                for (int u = 0; u < 8; ++u) p8[u] = z0 + u < ks ? part[size_t(z0 + u) * mn + off + i] : 0.f;
-#pragma unroll
-                for (int u = 0; u < 8; ++u)
-                    if (z0 + u < ks) y = (z0 + u == 0) ? p8[u] : y + p8[u];
-            }
-            if (bias) y += bias[i];
-            v[k] = x[off + i] + y;
-            x[off + i] = v[k];
-            s1 += v[k];
+            for (int u = 0; u < 8; ++u)
+                if (z0 + u < ks) {
+                    if (z0 + u == 0) y = p8[u];
+                    else add4(y, p8[u]);
+                }
         }
-    }
-    const float mean = block_sum(s1, sh) / float(N);
-    float s2 = 0.f;
-#pragma unroll
-    for (int k = 0; k < 4; ++k)
-        if (t + 1024 * k < N) s2 += (v[k] - mean) * (v[k] - mean);
-    const float rstd = rsqrtf(block_sum(s2, sh) / float(N) + eps);
-#pragma unroll
-    for (int k = 0; k < 4; ++k) {
-        const int i = t + 1024 * k;
-        if (i < N) h[off + i] = (v[k] - mean) * rstd * g[i] + b[i];
-    }
+        if (bias) add4(y, ld4(bias, f));
+        float4 v = xr[f];
+        add4(v, y);
+        return v;
+    };
+    workgroup_row_layernorm<4>(N, form, [&](int f, const float4 &v) { xr[f] = v; }, g, b, eps, h + off, red);
 }
 
 // Split-K reduction of the fused QKV projection written straight into q [M][d] and
@@ -1065,12 +1053,12 @@ hipError_t gemm_residual_ln(const DevMatrix &w, const float *X, int ldx, int M, 
                             const float *g, const float *b, float eps, float *h, hipStream_t st, float *ws,
                             size_t ws_bytes) {
     if (M <= 0) return hipSuccess;
-    if (w.N > 4096) return hipErrorInvalidValue;
+    if (w.N > 4096 || w.N % 4) return hipErrorInvalidValue;
     hipError_t e;
     const int ks = launch_split(w, X, ldx, M, st, ws, ws_bytes, &e);
     if (e != hipSuccess) return e;
     if (ks > 1) {
-        hipLaunchKernelGGL(k_splitk_residual_ln, dim3(M), dim3(1024), 0, st, ws, ks, M, w.N, bias, x, g, b, eps, h);
+        hipLaunchKernelGGL(k_splitk_residual_ln, dim3(M), dim3(256), 0, st, ws, ks, M, w.N, bias, x, g, b, eps, h);
         return hipGetLastError();
     }
     // x = x + X W^T + bias in place (R = Y = x), then the LayerNorm

@@ -9,103 +9,126 @@ namespace mlg {
 
 namespace {
 
-__global__ __launch_bounds__(kLnThreads) void k_layernorm(const float *x, int d, const float *g, const float *b,
-                                                          float eps, float *out) {
-    __shared__ float sh[16];
-    const size_t off = size_t(blockIdx.x) * d;
-    float v[kLnMaxPerThread];
-#pragma unroll
-    for (int k = 0; k < kLnMaxPerThread; ++k) {
-        const int i = threadIdx.x + k * kLnThreads;
-        v[k] = i < d ? x[off + i] : 0.f;
+// ---- rows: one wave per row, four rows per workgroup ----------------------------
+
+// LayerNorm of rows (RESID: x += y first, stored back; the normalized row goes to h).
+template <int NJ, bool RESID>
+__global__ __launch_bounds__(256) void k_rows_ln(float *x, const float *y, int rows, int d, const float *g,
+                                                 const float *b, float eps, float *h) {
+    const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (row >= rows) return;  // wave-uniform; nothing below synchronizes the workgroup
+    float4 *xr = reinterpret_cast<float4 *>(x + size_t(row) * d);
+    const float4 *yr = reinterpret_cast<const float4 *>(y + size_t(row) * d);
+    auto form = [&](int f) {
+        float4 v = xr[f];
+        if constexpr (RESID) add4(v, yr[f]);
+        return v;
+    };
+    if constexpr (RESID) {
+        wave_row_layernorm<NJ>(d, form, [&](int f, const float4 &v) { xr[f] = v; }, g, b, eps, h + size_t(row) * d);
+    } else {
+        wave_row_layernorm<NJ>(d, form, NoKeep{}, g, b, eps, h + size_t(row) * d);
     }
-    ln_rows(v, d, g, b, eps, out + off, sh);
 }
 
-__global__ __launch_bounds__(kLnThreads) void k_residual_ln(float *x, const float *y, int d, const float *g,
-                                                            const float *b, float eps, float *h) {
-    __shared__ float sh[16];
-    const size_t off = size_t(blockIdx.x) * d;
-    float v[kLnMaxPerThread];
+// Embedding rows, one wave per row: lane l owns the 16-value chunks c = l + 64 j
+// (j < NC, d <= 1024 NC, d % 16 == 0), each dequantized straight into registers.
+template <int T, int NC>
+__device__ __forceinline__ void embed_chunks(const uint8_t *q, const uint8_t *s, const uint8_t *dp, int d,
+                                             uint32_t tok, float (&w)[NC][16]) {
+    const int lane = threadIdx.x & 63;
 #pragma unroll
-    for (int k = 0; k < kLnMaxPerThread; ++k) {
-        const int i = threadIdx.x + k * kLnThreads;
-        v[k] = 0.f;
-        if (i < d) {
-            v[k] = x[off + i] + y[off + i];
-            x[off + i] = v[k];
-        }
-    }
-    ln_rows(v, d, g, b, eps, h + off, sh);
+    for (int j = 0; j < NC; ++j)
+        if (16 * (lane + 64 * j) < d) dequant16<T>(q, s, dp, d, int(tok), 16 * (lane + 64 * j), w[j]);
 }
 
-// Dequantizes embedding row `tok` into LDS e[0..d)
-template <int T>
-__device__ __forceinline__ void embed_row(const uint8_t *q, const uint8_t *s, const uint8_t *dp, int d, uint32_t tok,
-                                          float *e) {
-    for (int k0 = threadIdx.x * 16; k0 < d; k0 += blockDim.x * 16) {
-        float w[16];
-        dequant16<T>(q, s, dp, d, int(tok), k0, w);
-#pragma unroll
-        for (int i = 0; i < 16; ++i) e[k0 + i] = w[i];
-    }
-    __syncthreads();
-}
-
-template <int T>
-__global__ __launch_bounds__(kLnThreads) void k_embed_pos_ln(const uint8_t *q, const uint8_t *s, const uint8_t *dp,
-                                                             const uint32_t *ids, const float *pos,
-                                                             const uint32_t *step, uint32_t base, float scale, int d,
-                                                             uint32_t last, const float *g, const float *b, float eps,
-                                                             float *x, float *h, SrcEmb src) {
-    extern __shared__ float e[];
-    __shared__ float sh[16];
-    const int row = blockIdx.x;
-    const uint32_t sr = src.row ? src.row[row] : kNoRow;  // workgroup-uniform
+// src/model.rs:558-568: x = token_embd[id] * scale + pos[*step + base] (or, for a copied
+// source token, its row of src.emb), stored to x, and h = LayerNorm(x) (decoder layer
+// 0's attn_norm).  The row's values stay in registers: one pass of f64 statistics.
+template <int T, int NC>
+__global__ __launch_bounds__(256) void k_embed_pos_ln(const uint8_t *q, const uint8_t *s, const uint8_t *dp,
+                                                      const uint32_t *ids, int rows, const float *pos,
+                                                      const uint32_t *step, uint32_t base, float scale, int d,
+                                                      uint32_t last, const float *g, const float *b, float eps,
+                                                      float *x, float *h, SrcEmb src) {
+    const int row = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
+    if (row >= rows) return;  // wave-uniform
+    const uint32_t sr = src.row ? src.row[row] : kNoRow;  // wave-uniform
+    float w[NC][16];
     if (sr != kNoRow) {  // the previous token was a copy of source position sr
         const float *er = src.emb + (size_t(row) * src.S + sr) * d;
-        for (int i = threadIdx.x; i < d; i += blockDim.x) e[i] = er[i];
-        __syncthreads();
+#pragma unroll
+        for (int j = 0; j < NC; ++j) {
+            const int c = lane + 64 * j;
+            if (16 * c < d)
+#pragma unroll
+                for (int u = 0; u < 4; ++u) {
+                    const float4 v = ld4(er, 4 * c + u);
+                    w[j][4 * u] = v.x;
+                    w[j][4 * u + 1] = v.y;
+                    w[j][4 * u + 2] = v.z;
+                    w[j][4 * u + 3] = v.w;
+                }
+        }
     } else {
         // a token the device produced: clamped to the table (an all-NaN row of logits
         // yields 0xffffffff, malaga.cu:257-258), so a bad model cannot read past it
-        embed_row<T>(q, s, dp, d, min(ids[row], last), e);
+        embed_chunks<T, NC>(q, s, dp, d, min(ids[row], last), w);
     }
     const float *pr = pos + size_t(*step + base) * d;
-    const size_t off = size_t(row) * d;
-    float v[kLnMaxPerThread];
+    float4 *xr = reinterpret_cast<float4 *>(x + size_t(row) * d);
+    float4 v[NC][4];
+    double s1 = 0.0, s2 = 0.0;
 #pragma unroll
-    for (int k = 0; k < kLnMaxPerThread; ++k) {
-        const int i = threadIdx.x + k * kLnThreads;
-        v[k] = 0.f;
-        if (i < d) {
-            v[k] = e[i] * scale + pr[i];
-            x[off + i] = v[k];
+    for (int j = 0; j < NC; ++j) {
+        const int c = lane + 64 * j;
+        if (16 * c >= d) continue;
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const float4 p = ld4(pr, 4 * c + u);
+            v[j][u] = make_float4(w[j][4 * u] * scale + p.x, w[j][4 * u + 1] * scale + p.y,
+                                  w[j][4 * u + 2] * scale + p.z, w[j][4 * u + 3] * scale + p.w);
+            xr[4 * c + u] = v[j][u];
+            ln_acc(v[j][u], s1, s2);
         }
     }
-    ln_rows(v, d, g, b, eps, h + off, sh);
-}
-
-template <int T>
-__global__ __launch_bounds__(kLnThreads) void k_embed_pos_rows(const uint8_t *q, const uint8_t *s, const uint8_t *dp,
-                                                               const uint32_t *ids, const uint32_t *pidx,
-                                                               const float *pos, float scale, int d, float *x) {
-    extern __shared__ float e[];
-    const int row = blockIdx.x;
-    embed_row<T>(q, s, dp, d, ids[row], e);
-    const float *pr = pos + size_t(pidx[row]) * d;
-    for (int i = threadIdx.x; i < d; i += blockDim.x) x[size_t(row) * d + i] = e[i] * scale + pr[i];
-}
-
-template <int T>
-__global__ __launch_bounds__(kLnThreads) void k_embed_rows(const uint8_t *q, const uint8_t *s, const uint8_t *dp,
-                                                           const uint32_t *ids, int d, float *out) {
-    const int row = blockIdx.x;
-    for (int k0 = threadIdx.x * 16; k0 < d; k0 += blockDim.x * 16) {
-        float w[16];
-        dequant16<T>(q, s, dp, d, int(ids[row]), k0, w);
+    float mean, rstd;
+    wave_ln_stats(s1, s2, d, eps, mean, rstd);
+    float4 *hr = reinterpret_cast<float4 *>(h + size_t(row) * d);
 #pragma unroll
-        for (int i = 0; i < 16; ++i) out[size_t(row) * d + k0 + i] = w[i];
+    for (int j = 0; j < NC; ++j) {
+        const int c = lane + 64 * j;
+        if (16 * c >= d) continue;
+#pragma unroll
+        for (int u = 0; u < 4; ++u) hr[4 * c + u] = ln_apply(v[j][u], mean, rstd, ld4(g, 4 * c + u), ld4(b, 4 * c + u));
+    }
+}
+
+// Encoder input (src/model.rs:463-477): x = token_embd[ids[r]] * scale + pos[pidx[r]].
+// scale = 0: the embedding rows alone (token_embd gathers, shortlist source rows).
+template <int T, int NC>
+__global__ __launch_bounds__(256) void k_embed_pos_rows(const uint8_t *q, const uint8_t *s, const uint8_t *dp,
+                                                        const uint32_t *ids, const uint32_t *pidx, int rows,
+                                                        const float *pos, float scale, int d, float *x) {
+    const int row = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
+    if (row >= rows) return;
+    float w[NC][16];
+    embed_chunks<T, NC>(q, s, dp, d, ids[row], w);
+    const float *pr = pos ? pos + size_t(pidx[row]) * d : nullptr;
+    float4 *xr = reinterpret_cast<float4 *>(x + size_t(row) * d);
+#pragma unroll
+    for (int j = 0; j < NC; ++j) {
+        const int c = lane + 64 * j;
+        if (16 * c >= d) continue;
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            float4 v = make_float4(w[j][4 * u], w[j][4 * u + 1], w[j][4 * u + 2], w[j][4 * u + 3]);
+            if (pr) {
+                const float4 p = ld4(pr, 4 * c + u);
+                v = make_float4(v.x * scale + p.x, v.y * scale + p.y, v.z * scale + p.z, v.w * scale + p.w);
+            }
+            xr[4 * c + u] = v;
+        }
     }
 }
 
@@ -130,75 +153,31 @@ __global__ __launch_bounds__(256) void k_source_logits(const float *h, const flo
     }
 }
 
-__global__ void k_qkv_split(const float *qkv, int H, int hd, int m, const uint32_t *step, float *q, __half *kc,
-                            __half *vc) {
-    const int bh = blockIdx.x, bi = bh / H, hh = bh % H, d = H * hd;
-    const float *r = qkv + size_t(bi) * 3 * d;
-    const size_t slot = (size_t(bh) * m + *step) * hd;
-    for (int t = threadIdx.x; t < hd; t += blockDim.x) {
-        const int c = hh * hd + t;
-        q[size_t(bh) * hd + t] = r[c];
-        kc[slot + t] = __float2half(r[d + c]);
-        vc[slot + t] = __float2half(r[2 * d + c]);
-    }
-}
-
-// One workgroup per (row, head).  Thread j scores key j (16-byte f16 loads), block
-// max / exp / sum, then hd-wide thread groups split the keys for P.V.
-__global__ __launch_bounds__(256) void k_attn_decode(const float *q, const __half *K, const __half *V, int H, int hd,
-                                                     int L, const uint32_t *lens, const uint32_t *step, float *out,
-                                                     const uint32_t *rows) {
-    extern __shared__ float sm[];
-    __shared__ float red[16];
-    const int bh = blockIdx.x, bi = bh / H, hh = bh % H;
-    const int n = lens ? int(lens[bi]) : int(*step) + 1;
-    const int groups = max(1, int(blockDim.x) / hd);
-    float *qs = sm, *sc = sm + hd, *part = sc + L;
-    for (int t = threadIdx.x; t < hd; t += blockDim.x) qs[t] = q[size_t(bh) * hd + t];
-    __syncthreads();
-    // rows[bi][j]: the cache row that holds slot j of row bi (beam search), else bi
-    auto slot = [&](const __half *C, int j) {
-        const size_t r = rows ? rows[size_t(bi) * L + j] : size_t(bi);
-        return C + ((r * H + hh) * L + j) * hd;
+// The fused projection's rows [b][3d] (bias included) split into q (f32 [b][d]) and
+// the f16 K/V caches at slot *step ([b][H][m][hd]): one thread per 8 consecutive values
+// of the row's d columns, two 16-byte loads per part, one 16-byte store per f16 part.
+__global__ __launch_bounds__(256) void k_split_qkv8(const float *qkv, int b, int H, int hd, int m,
+                                                    const uint32_t *step, float *q, __half *kc, __half *vc) {
+    const int d = H * hd, per_row = d / 8;
+    const int t = blockIdx.x * 256 + threadIdx.x;
+    if (t >= b * per_row) return;
+    const int bi = t / per_row, c = (t - bi * per_row) * 8, hh = c / hd, e = c - hh * hd;
+    const float *r = qkv + size_t(bi) * 3 * d + c;
+    float4 *qd = reinterpret_cast<float4 *>(q + size_t(bi) * d + c);
+    qd[0] = ld4(r, 0);
+    qd[1] = ld4(r, 1);
+    const size_t slot = ((size_t(bi) * H + hh) * m + *step) * hd + e;
+    auto f16x8 = [](const float *p) {
+        const float4 a = ld4(p, 0), z = ld4(p, 1);
+        uint4 o;
+        o.x = uint32_t(__half_as_ushort(__float2half(a.x))) | uint32_t(__half_as_ushort(__float2half(a.y))) << 16;
+        o.y = uint32_t(__half_as_ushort(__float2half(a.z))) | uint32_t(__half_as_ushort(__float2half(a.w))) << 16;
+        o.z = uint32_t(__half_as_ushort(__float2half(z.x))) | uint32_t(__half_as_ushort(__float2half(z.y))) << 16;
+        o.w = uint32_t(__half_as_ushort(__float2half(z.z))) | uint32_t(__half_as_ushort(__float2half(z.w))) << 16;
+        return o;
     };
-    float mx = -INFINITY;
-    for (int j = threadIdx.x; j < n; j += blockDim.x) {
-        const uint4 *k8 = reinterpret_cast<const uint4 *>(slot(K, j));
-        float acc = 0.f;
-        for (int t = 0; t < hd / 8; ++t) {
-            const uint4 raw = k8[t];
-            const uint32_t w[4] = {raw.x, raw.y, raw.z, raw.w};
-#pragma unroll
-            for (int u = 0; u < 4; ++u) {
-                acc = fmaf(h2f(w[u]), qs[8 * t + 2 * u], acc);
-                acc = fmaf(h2f(w[u] >> 16), qs[8 * t + 2 * u + 1], acc);
-            }
-        }
-        sc[j] = acc;
-        mx = fmaxf(mx, acc);
-    }
-    mx = block_max(mx, red);
-    float sum = 0.f;
-    for (int j = threadIdx.x; j < n; j += blockDim.x) {
-        const float e = expf(sc[j] - mx);
-        sc[j] = e;
-        sum += e;
-    }
-    __syncthreads();
-    sum = block_sum(sum, red);
-    const float inv = 1.f / sum;
-    const int g = threadIdx.x / hd, t = threadIdx.x % hd;
-    if (g < groups) {
-        float a = 0.f;
-        for (int j = g; j < n; j += groups) a = fmaf(sc[j], __half2float(slot(V, j)[t]), a);
-        part[g * hd + t] = a;
-    }
-    __syncthreads();
-    for (int c = threadIdx.x; c < hd; c += blockDim.x) {
-        float o = 0.f;
-        for (int k = 0; k < groups; ++k) o += part[k * hd + c];
-        out[size_t(bi) * H * hd + hh * hd + c] = o * inv;
-    }
+    *reinterpret_cast<uint4 *>(kc + slot) = f16x8(r + d);
+    *reinterpret_cast<uint4 *>(vc + slot) = f16x8(r + 2 * d);
 }
 
 // Encoder attention: one wave per (sentence i, query t, head h).
@@ -631,26 +610,63 @@ int grid_1d(size_t n, int block) {
     return int(g < 1 ? 1 : (g > 65536 ? 65536 : g));
 }
 
+// chunks of 16 values per lane for a row of d (<= 4096) values: 1, 2 or 4
+inline int embed_nc(int d) { return d <= 1024 ? 1 : d <= 2048 ? 2 : 4; }
+
 template <int T>
 hipError_t launch_embed_pos_ln(const DevMatrix &E, const uint32_t *ids, int rows, const float *pos,
                                const uint32_t *step, uint32_t base, float scale, const float *g, const float *b,
                                float eps, float *x, float *h, hipStream_t st, const SrcEmb &src) {
-    hipLaunchKernelGGL(k_embed_pos_ln<T>, dim3(rows), dim3(kLnThreads), E.K * sizeof(float), st, E.q, E.s, E.d, ids,
-                       pos, step, base, scale, E.K, uint32_t(E.N - 1), g, b, eps, x, h, src);
-    return hipGetLastError();
-}
-
-template <int T>
-hipError_t launch_embed_rows(const DevMatrix &E, const uint32_t *ids, int rows, float *out, hipStream_t st) {
-    hipLaunchKernelGGL(k_embed_rows<T>, dim3(rows), dim3(kLnThreads), 0, st, E.q, E.s, E.d, ids, E.K, out);
+    const dim3 grid(unsigned((rows + 3) / 4));
+    const uint32_t last = uint32_t(E.N - 1);
+    switch (embed_nc(E.K)) {
+    case 1:
+        hipLaunchKernelGGL((k_embed_pos_ln<T, 1>), grid, dim3(256), 0, st, E.q, E.s, E.d, ids, rows, pos, step, base,
+                           scale, E.K, last, g, b, eps, x, h, src);
+        break;
+    case 2:
+        hipLaunchKernelGGL((k_embed_pos_ln<T, 2>), grid, dim3(256), 0, st, E.q, E.s, E.d, ids, rows, pos, step, base,
+                           scale, E.K, last, g, b, eps, x, h, src);
+        break;
+    default:
+        hipLaunchKernelGGL((k_embed_pos_ln<T, 4>), grid, dim3(256), 0, st, E.q, E.s, E.d, ids, rows, pos, step, base,
+                           scale, E.K, last, g, b, eps, x, h, src);
+    }
     return hipGetLastError();
 }
 
 template <int T>
 hipError_t launch_embed_pos_rows(const DevMatrix &E, const uint32_t *ids, const uint32_t *pidx, int rows,
                                  const float *pos, float scale, float *x, hipStream_t st) {
-    hipLaunchKernelGGL(k_embed_pos_rows<T>, dim3(rows), dim3(kLnThreads), E.K * sizeof(float), st, E.q, E.s, E.d,
-                       ids, pidx, pos, scale, E.K, x);
+    const dim3 grid(unsigned((rows + 3) / 4));
+    switch (embed_nc(E.K)) {
+    case 1:
+        hipLaunchKernelGGL((k_embed_pos_rows<T, 1>), grid, dim3(256), 0, st, E.q, E.s, E.d, ids, pidx, rows, pos,
+                           scale, E.K, x);
+        break;
+    case 2:
+        hipLaunchKernelGGL((k_embed_pos_rows<T, 2>), grid, dim3(256), 0, st, E.q, E.s, E.d, ids, pidx, rows, pos,
+                           scale, E.K, x);
+        break;
+    default:
+        hipLaunchKernelGGL((k_embed_pos_rows<T, 4>), grid, dim3(256), 0, st, E.q, E.s, E.d, ids, pidx, rows, pos,
+                           scale, E.K, x);
+    }
+    return hipGetLastError();
+}
+
+template <bool RESID>
+hipError_t launch_rows_ln(float *x, const float *y, int rows, int d, const float *g, const float *b, float eps,
+                          float *h, hipStream_t st) {
+    if (d % 4 || d > kWaveLnMaxD) return hipErrorInvalidValue;
+    if (rows <= 0) return hipSuccess;
+    const dim3 grid(unsigned((rows + 3) / 4));
+    const int nj = (d + 255) / 256;
+    if (nj <= 1) hipLaunchKernelGGL((k_rows_ln<1, RESID>), grid, dim3(256), 0, st, x, y, rows, d, g, b, eps, h);
+    else if (nj <= 2) hipLaunchKernelGGL((k_rows_ln<2, RESID>), grid, dim3(256), 0, st, x, y, rows, d, g, b, eps, h);
+    else if (nj <= 4) hipLaunchKernelGGL((k_rows_ln<4, RESID>), grid, dim3(256), 0, st, x, y, rows, d, g, b, eps, h);
+    else if (nj <= 8) hipLaunchKernelGGL((k_rows_ln<8, RESID>), grid, dim3(256), 0, st, x, y, rows, d, g, b, eps, h);
+    else hipLaunchKernelGGL((k_rows_ln<16, RESID>), grid, dim3(256), 0, st, x, y, rows, d, g, b, eps, h);
     return hipGetLastError();
 }
 
@@ -658,31 +674,26 @@ hipError_t launch_embed_pos_rows(const DevMatrix &E, const uint32_t *ids, const 
 
 hipError_t layernorm(const float *x, int rows, int d, const float *g, const float *b, float eps, float *out,
                      hipStream_t st) {
-    if (d > kLnThreads * kLnMaxPerThread) return hipErrorInvalidValue;
-    if (rows <= 0) return hipSuccess;
-    hipLaunchKernelGGL(k_layernorm, dim3(rows), dim3(kLnThreads), 0, st, x, d, g, b, eps, out);
-    return hipGetLastError();
+    return launch_rows_ln<false>(const_cast<float *>(x), nullptr, rows, d, g, b, eps, out, st);
 }
 
 hipError_t residual_ln(float *x, const float *y, int rows, int d, const float *g, const float *b, float eps, float *h,
                        hipStream_t st) {
-    if (d > kLnThreads * kLnMaxPerThread) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(k_residual_ln, dim3(rows), dim3(kLnThreads), 0, st, x, y, d, g, b, eps, h);
-    return hipGetLastError();
+    return launch_rows_ln<true>(x, y, rows, d, g, b, eps, h, st);
 }
 
 hipError_t embed_pos_ln(const DevMatrix &E, const uint32_t *ids, int rows, const float *pos, const uint32_t *step,
                         uint32_t base, float scale, const float *g, const float *b, float eps, float *x, float *h,
                         hipStream_t st, const SrcEmb &src) {
-    if (E.K > kLnThreads * kLnMaxPerThread || E.K % 16 || (src.row && (!src.emb || src.S < 1)))
-        return hipErrorInvalidValue;
+    if (E.K > kWaveLnMaxD || E.K % 16 || (src.row && (!src.emb || src.S < 1))) return hipErrorInvalidValue;
+    if (rows <= 0) return hipSuccess;
     MLG_DISPATCH_TYPE(E.type, launch_embed_pos_ln, E, ids, rows, pos, step, base, scale, g, b, eps, x, h, st, src)
 }
 
 hipError_t embed_rows(const DevMatrix &E, const uint32_t *ids, int rows, float *out, hipStream_t st) {
-    if (E.K % 16) return hipErrorInvalidValue;
+    if (E.K % 16 || E.K > kWaveLnMaxD) return hipErrorInvalidValue;
     if (rows <= 0) return hipSuccess;
-    MLG_DISPATCH_TYPE(E.type, launch_embed_rows, E, ids, rows, out, st)
+    MLG_DISPATCH_TYPE(E.type, launch_embed_pos_rows, E, ids, nullptr, rows, nullptr, 0.f, out, st)
 }
 
 hipError_t source_logits(const float *h, const float *emb, const uint32_t *src_ids, int b, int S, int d, int mask_id,
@@ -695,37 +706,42 @@ hipError_t source_logits(const float *h, const float *emb, const uint32_t *src_i
 
 hipError_t embed_pos_rows(const DevMatrix &E, const uint32_t *ids, const uint32_t *pidx, int rows, const float *pos,
                           float scale, float *x, hipStream_t st) {
-    if (E.K % 16) return hipErrorInvalidValue;
+    if (E.K % 16 || E.K > kWaveLnMaxD || !pos || !pidx) return hipErrorInvalidValue;
     if (rows <= 0) return hipSuccess;
     MLG_DISPATCH_TYPE(E.type, launch_embed_pos_rows, E, ids, pidx, rows, pos, scale, x, st)
 }
 
 hipError_t qkv_split(const float *qkv, int b, int H, int hd, int m, const uint32_t *step, float *q, __half *kc,
                      __half *vc, hipStream_t st) {
-    hipLaunchKernelGGL(k_qkv_split, dim3(b * H), dim3(((hd + 63) / 64) * 64), 0, st, qkv, H, hd, m, step, q, kc, vc);
+    if (hd % 8 || b <= 0) return b <= 0 ? hipSuccess : hipErrorInvalidValue;
+    const int n = b * H * hd / 8;
+    hipLaunchKernelGGL(k_split_qkv8, dim3(unsigned((n + 255) / 256)), dim3(256), 0, st, qkv, b, H, hd, m, step, q, kc,
+                       vc);
     return hipGetLastError();
+}
+
+bool attn_head_size_supported(int hd) {
+    return hd == 8 || hd == 16 || hd == 32 || hd == 64 || hd == 128 || hd == 256;
 }
 
 hipError_t attn_decode(const float *q, const __half *K, const __half *V, int b, int H, int hd, int L,
                        const uint32_t *lens, const uint32_t *step, float *out, hipStream_t st, const uint32_t *rows) {
-    if (hd % 8 || hd > 256) return hipErrorInvalidValue;
+    if (b * H <= 0) return hipSuccess;
     const dim3 wgrid(unsigned((b * H + 3) / 4));
     switch (hd) {
-    case 16:
-        hipLaunchKernelGGL(k_attn_waves<16>, wgrid, dim3(256), 0, st, q, K, V, b, H, L, lens, step, out, rows);
+#define MLG_ATTN_WAVES(HD)                                                                                          \
+    case HD:                                                                                                        \
+        hipLaunchKernelGGL(k_attn_waves<HD>, wgrid, dim3(256), 0, st, q, K, V, b, H, L, lens, step, out, rows);     \
         return hipGetLastError();
-    case 64:
-        hipLaunchKernelGGL(k_attn_waves<64>, wgrid, dim3(256), 0, st, q, K, V, b, H, L, lens, step, out, rows);
-        return hipGetLastError();
-    case 128:
-        hipLaunchKernelGGL(k_attn_waves<128>, wgrid, dim3(256), 0, st, q, K, V, b, H, L, lens, step, out, rows);
-        return hipGetLastError();
-    default: break;
+        MLG_ATTN_WAVES(8)
+        MLG_ATTN_WAVES(16)
+        MLG_ATTN_WAVES(32)
+        MLG_ATTN_WAVES(64)
+        MLG_ATTN_WAVES(128)
+        MLG_ATTN_WAVES(256)
+#undef MLG_ATTN_WAVES
+    default: return hipErrorInvalidValue;  // attn_head_size_supported is checked at model load
     }
-    const int block = 256, groups = block / hd > 0 ? block / hd : 1;
-    const size_t shared = sizeof(float) * (hd + L + groups * hd);
-    hipLaunchKernelGGL(k_attn_decode, dim3(b * H), dim3(block), shared, st, q, K, V, H, hd, L, lens, step, out, rows);
-    return hipGetLastError();
 }
 
 hipError_t attn_prefill(const float *qkv, int b, int s, int H, int hd, const uint32_t *lens, float *out,

@@ -73,15 +73,6 @@ struct PreLoadsR {
 };
 using PreLoads = PreLoadsR<2>;
 
-__device__ __forceinline__ void add4(float4 &a, const float4 &b) {
-    a.x += b.x;
-    a.y += b.y;
-    a.z += b.z;
-    a.w += b.w;
-}
-
-__device__ __forceinline__ float4 ld4(const float *p, int f) { return reinterpret_cast<const float4 *>(p)[f]; }
-
 template <int R = 2>
 __device__ __forceinline__ void preload(const StepArgs &a, PreLoadsR<R> &L) {
     const int f = min(int(threadIdx.x), (a.d >> 2) - 1);

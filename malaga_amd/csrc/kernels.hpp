@@ -136,7 +136,8 @@ hipError_t embed_pos_rows(const DevMatrix &E, const uint32_t *ids, const uint32_
 hipError_t qkv_split(const float *qkv, int b, int H, int hd, int m, const uint32_t *step, float *q, __half *kc,
                      __half *vc, hipStream_t st);
 // Single-query attention per (row, head) over f16 K/V [b][H][L][hd]: n = lens[row]
-// if lens, else *step + 1.  out [b][H*hd].
+// if lens, else *step + 1.  out [b][H*hd].  Head sizes: attn_head_size_supported.
+bool attn_head_size_supported(int hd);
 hipError_t attn_decode(const float *q, const __half *K, const __half *V, int b, int H, int hd, int L,
                        const uint32_t *lens, const uint32_t *step, float *out, hipStream_t st, const uint32_t *rows = nullptr);
 // rows (optional, [b][L]): cache row holding slot j of row b (beam reordering without copies).

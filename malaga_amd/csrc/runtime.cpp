@@ -373,6 +373,9 @@ void Model::load(const std::string &path) {
         fail(ERR_UNSUPPORTED, "unsupported d_model " + std::to_string(d));
     if ((d / cfg.decoder_heads) % 8 || (d / cfg.encoder_heads) % 8)
         fail(ERR_UNSUPPORTED, "head dimension must be a multiple of 8");
+    if (!attn_head_size_supported(d / cfg.decoder_heads))
+        fail(ERR_UNSUPPORTED, "decoder head size " + std::to_string(d / cfg.decoder_heads) +
+                                  " (supported: 8, 16, 32, 64, 128, 256)");
 
     // src/model.rs:416-420: MALAGA_LAZY_EMBEDDINGS (set, any value) defers the full table
     // when the file has a shortlist

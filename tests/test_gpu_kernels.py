@@ -262,8 +262,10 @@ def test_gemv_argmax_lowest_index_on_ties(ctx, t):
 
 
 def test_residual_layernorm(ctx):
+    """One wave per row (rows need not fill the four waves of a workgroup), rows up to
+    4096 wide; x += y is stored exactly, h follows the f64 LayerNorm."""
     rng = np.random.default_rng(1)
-    for rows, d in ((1, 1024), (5, 2048), (3, 64)):
+    for rows, d in ((1, 1024), (5, 2048), (3, 64), (7, 4096), (4, 256), (9, 1000)):
         x = rng.normal(0, 3, (rows, d)).astype(np.float32)
         y = rng.normal(0, 1, (rows, d)).astype(np.float32)
         g = rng.normal(1, 0.1, d).astype(np.float32)
@@ -276,12 +278,20 @@ def test_residual_layernorm(ctx):
         mu, var = s.mean(1, keepdims=True), s.var(1, keepdims=True)
         ref = (s - mu) / np.sqrt(var + 1e-5) * g + b
         np.testing.assert_allclose(hd.cpu().numpy(), ref, atol=2e-5, rtol=0)
+        # LayerNorm alone (encoder input, final norms)
+        od = torch.zeros((rows, d), device="cuda")
+        _lib.check(ctx.lib.mlg_layernorm(ptr(xd), rows, d, ptr(gd), ptr(bd), C.c_float(1e-5), ptr(od), None))
+        torch.cuda.synchronize()
+        np.testing.assert_allclose(od.cpu().numpy(), ref, atol=2e-5, rtol=0)
 
 
-def test_attention_decode(ctx):
-    rng = np.random.default_rng(2)
-    b, H, hd, L = 3, 16, 64, 100
-    q = rng.normal(0, 1, (b, H, hd)).astype(np.float32)
+@pytest.mark.parametrize("hd", [8, 16, 32, 64, 128, 256])
+def test_attention_decode(ctx, hd):
+    """One wave per (row, head) for every supported head size; keys split over lane
+    groups with an online softmax; cross lengths and the self-attention step counter."""
+    rng = np.random.default_rng(2 + hd)
+    b, H, L = 3, 1024 // hd if hd <= 64 else 8, 100
+    q = (rng.normal(0, 1, (b, H, hd)) / np.sqrt(hd)).astype(np.float32)  # pre-scaled, as W_q is
     K = rng.normal(0, 1, (b, H, L, hd)).astype(np.float16)
     V = rng.normal(0, 1, (b, H, L, hd)).astype(np.float16)
     lens = np.array([1, 37, 100], dtype=np.uint32)
@@ -323,6 +333,15 @@ def test_logsoftmax_topk(ctx):
         np.testing.assert_array_equal(idx.cpu().numpy(), order)
         np.testing.assert_allclose(vals.cpu().numpy(), np.take_along_axis(xx, order, 1) - lse[:, None], atol=2e-5)
     assert idx.cpu().numpy()[2, :3].tolist() == [50, 100, 7000]
+
+
+def test_attention_rejects_unsupported_head_size(ctx):
+    q = torch.zeros(1, 48, device="cuda")
+    kv = torch.zeros(1, 1, 4, 48, dtype=torch.float16, device="cuda")
+    o = torch.zeros(1, 48, device="cuda")
+    lens = dev(np.array([4], dtype=np.int32))
+    st = ctx.lib.mlg_attn_decode(ptr(q), ptr(kv), ptr(kv), 1, 1, 48, 4, ptr(lens), None, ptr(o), None)
+    assert st != 0
 
 
 def test_greedy_finalize_bookkeeping(ctx):
