@@ -248,6 +248,14 @@ int mlg_greedy_finalize(const float *pv, const uint32_t *pi, int parts, int b, u
 size_t mlg_logsoftmax_topk_scratch(int rows, int k);
 int mlg_logsoftmax_topk(const float *logits, int rows, int V, int k, int mask_id, void *scratch, float *vals,
                         uint32_t *idx, void *stream);
+/* mlg_logsoftmax_topk with no workspace argument and no allocation of any kind, for callers
+   that cannot allocate (code under HIP graph capture, tight serving loops, harnesses that
+   forbid hipMalloc).  No counterpart in the reference.  The partial results live in a static
+   device array of the library (1.125 MiB, held by each GPU it runs on until the process ends),
+   so rows <= 256 (more: MLG_ERR_INVALID before anything runs).  Call with the stream's device
+   current.  Calls on one GPU share the array: calls that overlap on one GPU race. */
+int mlg_logsoftmax_topk_noalloc(const float *logits, int rows, int V, int k, int mask_id, float *vals, uint32_t *idx,
+                                void *stream);
 /* Logits after feeding tgt[i][t] at decoder position t (t < T), eagerly: out is [n][T][vocab].
  * Parity hook for Nllb::decode (src/model.rs:514-540); no counterpart in the reference. */
 int mlg_teacher_forced_logits(mlg_model *m, const uint32_t *ids, const uint32_t *lens, int n, const uint32_t *tgt, int T,

@@ -126,6 +126,7 @@ SIGNATURES = {
                                       _P]),
     "mlg_logsoftmax_topk_scratch": (C.c_size_t, [C.c_int, C.c_int]),
     "mlg_logsoftmax_topk": (C.c_int, [_P, C.c_int, C.c_int, C.c_int, C.c_int, _P, _P, _P, _P]),
+    "mlg_logsoftmax_topk_noalloc": (C.c_int, [_P, C.c_int, C.c_int, C.c_int, C.c_int, _P, _P, _P]),
     "mlg_teacher_forced_logits": (C.c_int, [_P, _P, _P, C.c_int, _P, C.c_int, _P]),
     "mlg_bucket": (C.c_int, [C.c_int, C.c_int, C.c_int]),
     "mlg_budget": (C.c_int, [_P, C.c_int, C.c_int]),

@@ -643,6 +643,17 @@ int mlg_logsoftmax_topk(const float *logits, int rows, int V, int k, int mask_id
                       "logsoftmax_topk");
 }
 
+int mlg_logsoftmax_topk_noalloc(const float *logits, int rows, int V, int k, int mask_id, float *vals, uint32_t *idx,
+                                void *stream) {
+    if (!logits || !vals || !idx || rows < 1 || V < 1 || k < 1 || k > 8)
+        return set_err(MLG_ERR_INVALID, "bad argument");
+    if (rows > mlg::kStaticTopkRows)
+        return set_err(MLG_ERR_INVALID, "mlg_logsoftmax_topk_noalloc: " + std::to_string(rows) + " rows exceed the " +
+                                            std::to_string(mlg::kStaticTopkRows) + "-row static scratch");
+    return hip_status(mlg::logsoftmax_topk_static(logits, rows, V, k, mask_id, vals, idx, as_stream(stream)),
+                      "logsoftmax_topk_noalloc");
+}
+
 int mlg_teacher_forced_logits(mlg_model *m, const uint32_t *ids, const uint32_t *lens, int n, const uint32_t *tgt, int T,
                               float *logits) {
     return guarded([&]() -> int {

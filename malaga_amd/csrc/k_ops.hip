@@ -2,6 +2,9 @@
 // LayerNorm (+ residual, + embedding/positions), q/k/v split into the f16 KV
 // cache, single-query and prefill attention, argmax + greedy bookkeeping,
 // log-softmax top-k for beam search, and small copy helpers.
+#include <mutex>
+#include <vector>
+
 #include "dequant.hpp"
 #include "kernels.hpp"
 
@@ -500,9 +503,9 @@ __device__ __forceinline__ void top8_insert(Top8 &t, float v, uint32_t i) {
 }
 
 // Pass 1: per (part, row): chunk max M, sum exp(x - M), chunk top-8.
-// scratch layout per (row, part): [M, S, v0..v7, i0..i7] (18 floats)
+// work layout per (row, part): [M, S, v0..v7, i0..i7] (18 floats)
 __global__ __launch_bounds__(256) void k_lsm_topk_partial(const float *logits, int V, int k, int mask_id,
-                                                          float *scratch) {
+                                                          float *work) {
     __shared__ float red[16];
     __shared__ float lv[256 * kTopMax];
     __shared__ uint32_t li[256 * kTopMax];
@@ -544,7 +547,7 @@ __global__ __launch_bounds__(256) void k_lsm_topk_partial(const float *logits, i
         __syncthreads();
     }
     if (threadIdx.x == 0) {
-        float *o = scratch + (size_t(row) * P + p) * (2 + 2 * kTopMax);
+        float *o = work + (size_t(row) * P + p) * (2 + 2 * kTopMax);
         o[0] = mx;
         o[1] = s;
 #pragma unroll
@@ -558,11 +561,11 @@ __global__ __launch_bounds__(256) void k_lsm_topk_partial(const float *logits, i
 // Pass 2: one wave per row, lane p holds part p (P <= 64): vals = (x - max) - ln(sum
 // exp(x - max)) with the sum in f64 in a fixed lane order; top-k by k rounds of a
 // wave argmax over the lanes' best remaining candidates.
-__global__ __launch_bounds__(64) void k_lsm_topk_final(const float *scratch, int rows, int P, int k, float *vals,
+__global__ __launch_bounds__(64) void k_lsm_topk_final(const float *work, int rows, int P, int k, float *vals,
                                                        uint32_t *idx) {
     const int row = blockIdx.x, lane = threadIdx.x;
     if (row >= rows) return;
-    const float *o = scratch + (size_t(row) * P + lane) * (2 + 2 * kTopMax);
+    const float *o = work + (size_t(row) * P + lane) * (2 + 2 * kTopMax);
     const bool ok = lane < P;
     const float Mp = ok ? o[0] : -INFINITY, Sp = ok ? o[1] : 0.f;
     Top8 t;
@@ -797,14 +800,54 @@ size_t logsoftmax_topk_scratch(int rows, int k) {
     return size_t(rows) * kTopParts * (2 + 2 * kTopMax) * sizeof(float);
 }
 
-hipError_t logsoftmax_topk(const float *logits, int rows, int V, int k, int mask_id, float *scratch, float *vals,
+hipError_t logsoftmax_topk(const float *logits, int rows, int V, int k, int mask_id, float *work, float *vals,
                            uint32_t *idx, hipStream_t st) {
     if (k < 1 || k > kTopMax) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(k_lsm_topk_partial, dim3(kTopParts, rows), dim3(256), 0, st, logits, V, k, mask_id, scratch);
-    hipLaunchKernelGGL(k_lsm_topk_final, dim3(rows), dim3(64), 0, st, scratch, rows, kTopParts, k, vals, idx);
+    hipLaunchKernelGGL(k_lsm_topk_partial, dim3(kTopParts, rows), dim3(256), 0, st, logits, V, k, mask_id, work);
+    hipLaunchKernelGGL(k_lsm_topk_final, dim3(rows), dim3(64), 0, st, work, rows, kTopParts, k, vals, idx);
     return hipGetLastError();
 }
 
+
+// ---- log-softmax + top-k without allocation ----------------------------------------
+// The work area of logsoftmax_topk for up to kStaticTopkRows rows (1.125 MiB), a static
+// device array: every GPU the library runs on holds its own copy until the process
+// ends.  In host code `scratch` names a host-side stand-in, never a device address:
+// only the pointer hipGetSymbolAddress returns (per device) reaches a kernel.  Nothing
+// needs clearing between calls (pass 1 writes every (row, part) entry pass 2 reads);
+// calls that overlap on one GPU share the array and race.
+static __device__ __align__(256) float scratch[size_t(kStaticTopkRows) * kTopParts * (2 + 2 * kTopMax)];
+
+namespace {
+std::mutex g_scratch_mu;
+std::vector<float *> g_scratch_dev;  // device address of `scratch`, per device
+
+hipError_t static_scratch(float **out) {
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return e;
+    std::lock_guard<std::mutex> lk(g_scratch_mu);
+    if (size_t(dev) >= g_scratch_dev.size()) g_scratch_dev.resize(size_t(dev) + 1, nullptr);
+    if (!g_scratch_dev[dev]) {
+        void *p = nullptr;
+        e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess) return e;
+        g_scratch_dev[dev] = static_cast<float *>(p);
+    }
+    *out = g_scratch_dev[dev];
+    return hipSuccess;
+}
+}  // namespace
+
+hipError_t logsoftmax_topk_static(const float *logits, int rows, int V, int k, int mask_id, float *vals, uint32_t *idx,
+                                  hipStream_t st) {
+    if (rows < 1 || rows > kStaticTopkRows || logsoftmax_topk_scratch(rows, k) > sizeof(scratch))
+        return hipErrorInvalidValue;
+    float *work = nullptr;
+    const hipError_t e = static_scratch(&work);
+    if (e != hipSuccess) return e;
+    return logsoftmax_topk(logits, rows, V, k, mask_id, work, vals, idx, st);
+}
 
 hipError_t inc_u32(uint32_t *p, hipStream_t st) {
     hipLaunchKernelGGL(k_inc_u32, dim3(1), dim3(64), 0, st, p);

@@ -169,9 +169,15 @@ hipError_t greedy_finalize(const float *pv, const uint32_t *pi, int parts, int b
                            const SlFinalize &sl = SlFinalize{});
 // Beam: per row log-softmax of logits [rows][V] and its top-k (k <= 8, ties -> lowest
 // index): vals/idx [rows][k].  mask_id (>= 0) is treated as -inf.
-hipError_t logsoftmax_topk(const float *logits, int rows, int V, int k, int mask_id, float *scratch, float *vals,
+hipError_t logsoftmax_topk(const float *logits, int rows, int V, int k, int mask_id, float *work, float *vals,
                            uint32_t *idx, hipStream_t st);
 size_t logsoftmax_topk_scratch(int rows, int k);
+// logsoftmax_topk with its work area in the library's static device array (no
+// allocation; rows <= kStaticTopkRows).  The current device must be the stream's.
+// Calls that overlap on one device share the array and race.
+constexpr int kStaticTopkRows = 256;
+hipError_t logsoftmax_topk_static(const float *logits, int rows, int V, int k, int mask_id, float *vals, uint32_t *idx,
+                                  hipStream_t st);
 // ---- fused decoder-step kernels (batch <= 4), k_step.hip ----
 // True when the fused GEMV kernels (residual + LayerNorm prologue over d-wide rows)
 // handle matrix w at batch nb.
