@@ -42,7 +42,7 @@ enum {
 /* ggml type ids (GGUF spec) accepted by the codecs and kernels */
 enum { MLG_F32 = 0, MLG_F16 = 1, MLG_Q8_0 = 8, MLG_Q4_K = 12, MLG_Q5_K = 13, MLG_Q6_K = 14, MLG_BF16 = 30 };
 
-/* src/convert.rs:151-212 presets */
+/* src/convert.rs:25-91 presets (Preset and its linear / ffn_down / embedding types) */
 enum { MLG_PRESET_F32 = 0, MLG_PRESET_F16, MLG_PRESET_Q8_0, MLG_PRESET_Q6K, MLG_PRESET_Q5KM, MLG_PRESET_Q4KM };
 
 /* synthetic checkpoints (tests / benchmarks) */
@@ -83,13 +83,13 @@ typedef struct {
 const char *mlg_last_error(void);
 const char *mlg_version(void);
 
-/* ---- block codecs (candle-core 0.11 QTensor quantize/dequantize, src/convert.rs:249-256) ---- */
+/* ---- block codecs (candle-core 0.11 QTensor quantize/dequantize, src/convert.rs:128-136) ---- */
 int mlg_type_info(uint32_t type, int *block_elems, int *block_bytes);
 int64_t mlg_type_bytes(uint32_t type, int64_t n);
 int mlg_quantize(uint32_t type, const float *x, int64_t n, void *out);
 int mlg_dequantize(uint32_t type, const void *in, int64_t n, float *out);
 
-/* ---- conversion (src/convert.rs:317-440) ---- */
+/* ---- conversion (src/convert.rs:196-318) ---- */
 int mlg_preset_from_name(const char *name, int *preset);
 /* Supplies the f32 data of a Hugging Face tensor; return 0 on success. */
 typedef int (*mlg_tensor_fn)(void *user, const char *hf_name, int64_t numel, float *out);

@@ -8,7 +8,7 @@ Host-side mirror of the reference interface (rzafiamy/malaga, crates/malaga-core
   * ``Translator.translate_batch_ids`` <- src/translator.rs:136-167 (sort, batch, OOM halving)
   * ``Translator.encode_cross`` / ``greedy`` / ``beam`` <- src/model.rs:463-477,
     src/graph.rs:204-223, src/translator.rs:250-335
-  * ``convert`` / ``write_synthetic`` <- src/convert.rs:317-440, src/testutil.rs:16-101
+  * ``convert`` / ``write_synthetic`` <- src/convert.rs:196-318, src/testutil.rs:16-101
 
 Text tokenization and segmentation are outside this backend: callers pass
 token ids, as ``Translator::generate`` does.  Every call goes to the HIP
@@ -380,7 +380,7 @@ def write_synthetic(path: str | Path, cfg: dict, preset: str, init: int = INIT_N
 def convert(out_path: str | Path, cfg: dict, preset: str, tensors: Callable[[str], np.ndarray] | dict,
             model_name: str = "facebook/nllb-200-distilled-600M", tokenizer_json: str = "{}",
             shortlists: dict | None = None) -> Path:
-    """src/convert.rs:317-440 from Hugging Face tensors (a dict or a name -> array function);
+    """src/convert.rs:196-318 from Hugging Face tensors (a dict or a name -> array function);
     ``shortlists`` as for write_synthetic."""
     lib = load()
     get = tensors.get if isinstance(tensors, dict) else tensors

@@ -47,7 +47,7 @@ uint32_t preset_linear(Preset p) {
     return GGML_F32;
 }
 
-// The _m presets keep ffn_down and the embedding at Q6_K (src/convert.rs:199-211).
+// The _m presets keep ffn_down and the embedding at Q6_K (src/convert.rs:78-91).
 uint32_t preset_ffn_down(Preset p) { return (p == PRESET_Q5KM || p == PRESET_Q4KM) ? uint32_t(GGML_Q6_K) : preset_linear(p); }
 uint32_t preset_embedding(Preset p) { return preset_ffn_down(p); }
 
@@ -142,7 +142,7 @@ std::string convert_to_gguf(const std::string &out_path, const ModelConfig &c, P
         const int layers = dec ? c.decoder_layers : c.encoder_layers;
         const int64_t ffn = dec ? c.decoder_ffn : c.encoder_ffn;
         const int heads = dec ? c.decoder_heads : c.encoder_heads;
-        // 1/sqrt(head_dim) folded into the query weights and bias (src/convert.rs:332-333, 364-365)
+        // 1/sqrt(head_dim) folded into the query weights and bias (src/convert.rs:211-212, 243-244, 258-259)
         const float s = float(std::pow(double(d / heads), -0.5));
         for (int i = 0; i < layers; ++i) {
             const std::string p = "model." + sname + ".layers." + std::to_string(i), o = sh + ".blk." + std::to_string(i);
@@ -182,7 +182,7 @@ std::string convert_to_gguf(const std::string &out_path, const ModelConfig &c, P
     if (!missing.empty()) return "missing tensor " + missing;
     if (!w.err.empty()) return w.err;
 
-    // src/convert.rs:414-424 and src/config.rs:71-91
+    // src/convert.rs:293-303 and src/config.rs:71-91
     std::vector<std::pair<std::string, GgufValue>> kv = {
         {"general.architecture", GgufValue::Str("nllb")},
         {"general.name", GgufValue::Str(model_name)},

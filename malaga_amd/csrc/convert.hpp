@@ -16,14 +16,14 @@ struct ModelConfig {
     int bos_token_id = 0, pad_token_id = 1, eos_token_id = 2, decoder_start_token_id = 2;
 };
 
-// src/convert.rs:151-212
+// src/convert.rs:25-91
 enum Preset : int { PRESET_F32 = 0, PRESET_F16, PRESET_Q8_0, PRESET_Q6K, PRESET_Q5KM, PRESET_Q4KM };
 bool preset_from_name(const std::string &s, Preset *out);
 const char *preset_name(Preset p);
 uint32_t preset_linear(Preset p);
 uint32_t preset_ffn_down(Preset p);
 uint32_t preset_embedding(Preset p);
-// src/convert.rs:269-283: k-quants need rows % 256, legacy quants rows % 32.
+// src/convert.rs:148-162: k-quants need rows % 256, legacy quants rows % 32.
 uint32_t fallback_dtype(uint32_t dtype, const std::vector<int64_t> &dims);
 
 // Supplies the f32 data of a Hugging Face tensor by name ("model.shared.weight",
@@ -42,7 +42,7 @@ struct ShortlistSpec {
     std::vector<uint32_t> ids;
 };
 
-// src/convert.rs:317-440.  Returns "" on success.
+// src/convert.rs:196-318.  Returns "" on success.
 std::string convert_to_gguf(const std::string &out_path, const ModelConfig &cfg, Preset preset,
                             const std::string &model_name, const std::string &tokenizer_json, const HfProvider &src,
                             const std::vector<ShortlistSpec> &shortlists = {});

@@ -1,6 +1,6 @@
 // GGUF v3 container: reader (mmap) and writer.
 // Public GGUF layout; malaga's metadata keys and tensor names are those of
-// src/config.rs:71-116 and src/convert.rs:335-424.
+// src/config.rs:71-116 and src/convert.rs:293-318.
 #pragma once
 #include <cstdint>
 #include <map>

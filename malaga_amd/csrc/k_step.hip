@@ -892,7 +892,7 @@ hipError_t step_qkv(const DevMatrix &w, const float *bias, int nb, int d, const 
     if (!emb)
         return preloadable(a) ? dispatch_t<PRO_RESID_PRE, EPI_QKV, GGML_F32>(w.type, a, B, cpl, grid, lds, st)
                               : dispatch_t<PRO_RESID, EPI_QKV, GGML_F32>(w.type, a, B, cpl, grid, lds, st);
-    // (projection type, embedding type) pairs the presets produce (src/convert.rs:188-211)
+    // (projection type, embedding type) pairs the presets produce (src/convert.rs:67-91)
     const uint32_t t = w.type, e = emb->type;
     if (t == GGML_Q4_K && e == GGML_Q6_K) return dispatch_bc<GGML_Q4_K, PRO_EMBED, EPI_QKV, GGML_Q6_K>(a, B, cpl, grid, lds, st);
     if (t == GGML_Q5_K && e == GGML_Q6_K) return dispatch_bc<GGML_Q5_K, PRO_EMBED, EPI_QKV, GGML_Q6_K>(a, B, cpl, grid, lds, st);

@@ -1,7 +1,7 @@
 // Block quantizers and dequantizers for the GGUF formats malaga writes.
 //
 // The reference quantizes with candle-core 0.11 `QTensor::quantize`
-// (src/convert.rs:249-256), which is not vendored.  The quantizers here follow
+// (src/convert.rs:128-136), which is not vendored.  The quantizers here follow
 // ggml's published reference algorithms (quantize_row_q8_0 / q4_K / q5_K /
 // q6_K with make_qkx2_quants and make_qx_quants).  Parity of the decode path
 // is anchored on the GGUF bytes, not on the quantizer: the oracle and the GPU

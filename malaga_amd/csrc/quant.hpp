@@ -1,4 +1,4 @@
-// ggml block formats used by malaga's GGUF presets (src/convert.rs:146-212):
+// ggml block formats used by malaga's GGUF presets (src/convert.rs:25-91, 148-162):
 // F32, F16, Q8_0, Q4_K, Q5_K, Q6_K.  Byte layouts are the public GGUF/ggml ones.
 #pragma once
 #include <cstddef>

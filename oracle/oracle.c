@@ -8,7 +8,7 @@
  *
  * What it restates (reference = /root/reference/crates/malaga-core):
  *   - GGUF v3 container parsing (candle gguf_file; keys/names from
- *     src/config.rs:71-116 and src/convert.rs:335-411)
+ *     src/config.rs:71-116 and src/convert.rs:214-318)
  *   - ggml block dequantization: F32, F16, BF16, Q8_0, Q4_K, Q5_K, Q6_K
  *     (candle-core 0.11 k_quants, which follows ggml's public block formats;
  *     the crate is not vendored, see tests/test_oracle_blocks.py for the

@@ -1,4 +1,4 @@
-"""GGUF layout written by the converter (src/convert.rs:214-440, src/config.rs:71-91)."""
+"""GGUF layout written by the converter (src/convert.rs:196-318, src/config.rs:71-91)."""
 import numpy as np
 import pytest
 
@@ -51,7 +51,7 @@ def test_tensor_names_and_shapes(tiny_gguf):
 
 
 def test_tiny_q4_k_m_falls_back_to_q8_0(tiny_gguf):
-    """Rows of 64/128 values are not a multiple of 256: k-quants fall back (src/convert.rs:269-283)."""
+    """Rows of 64/128 values are not a multiple of 256: k-quants fall back (src/convert.rs:148-162)."""
     _, _, tensors, _ = read_gguf(tiny_gguf("q4_k_m"))
     assert tensors["dec.blk.0.attn_qkv.weight"]["type"] == Q8_0
     assert tensors["dec.blk.0.ffn_down.weight"]["type"] == Q8_0
@@ -64,7 +64,7 @@ def test_tiny_q4_k_m_falls_back_to_q8_0(tiny_gguf):
                                                  ("q6_k", Q6_K, Q6_K, Q6_K), ("q8_0", Q8_0, Q8_0, Q8_0),
                                                  ("f16", F16, F16, F16)])
 def test_preset_type_map(kq_gguf, preset, lin, down, emb):
-    """src/convert.rs:188-211: _m presets keep ffn_down and the embedding at Q6_K."""
+    """src/convert.rs:78-91: _m presets keep ffn_down and the embedding at Q6_K."""
     _, _, tensors, _ = read_gguf(kq_gguf(preset))
     for name in ("attn_qkv", "attn_out", "ffn_up", "cross_attn_q", "cross_attn_kv", "cross_attn_out"):
         assert tensors[f"dec.blk.1.{name}.weight"]["type"] == lin, name
@@ -74,7 +74,7 @@ def test_preset_type_map(kq_gguf, preset, lin, down, emb):
 
 
 def test_fused_qkv_order_and_query_prescale(tmp_path):
-    """attn_qkv = cat(q * hd^-0.5, k, v) (src/convert.rs:363-372); cross q pre-scaled, kv = cat(k, v)."""
+    """attn_qkv = cat(q * hd^-0.5, k, v) (src/convert.rs:242-251, 258-267); cross q pre-scaled, kv = cat(k, v)."""
     cfg = dict(M.tiny_config())
     rng = np.random.default_rng(0)
     d, f, V = cfg["d_model"], cfg["encoder_ffn"], cfg["vocab_size"]

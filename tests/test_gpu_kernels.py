@@ -37,7 +37,9 @@ def bound(x, w):
     return np.abs(x.astype(np.float64)) @ np.abs(w.astype(np.float64)).T
 
 
-CASES = [(t, N, K) for t in (Q4_K, Q5_K, Q6_K, Q8_0) for (N, K) in ((3072, 1024), (1024, 4096), (517, 256))] + \
+# BASELINE config 2 shapes at 600M: fused QKV 3072 x 1024, FFN-up 4096 x 1024, FFN-down 1024 x 4096
+CASES = [(t, N, K) for t in (Q4_K, Q5_K, Q6_K, Q8_0) for (N, K) in ((3072, 1024), (4096, 1024), (1024, 4096),
+                                                                  (517, 256))] + \
         [(F16, 192, 64), (F32, 192, 64), (F16, 130, 128), (F32, 128, 128)]
 
 
@@ -188,16 +190,19 @@ def test_gemm_argmax_batched_lm_head(ctx, t, K):
         ctx.lib.mlg_matrix_free(w)
 
 
-@pytest.mark.parametrize("t,K", [(Q4_K, 1024), (Q5_K, 512), (Q6_K, 1024), (Q6_K, 2048), (Q6_K, 256), (Q8_0, 1024),
-                                 (Q8_0, 96)])
-def test_large_gemv_integer_limbs(ctx, t, K):
+@pytest.mark.parametrize("t,K,N", [(Q4_K, 1024, 70001), (Q5_K, 512, 70001), (Q6_K, 1024, 70001), (Q6_K, 2048, 70001),
+                                   (Q6_K, 256, 70001), (Q8_0, 1024, 70001), (Q8_0, 96, 70001),
+                                   # the LM head at BASELINE config 2's full size: 256206 x 1024
+                                   (Q4_K, 1024, 256206), (Q8_0, 1024, 256206), (Q6_K, 1024, 256206)])
+def test_large_gemv_integer_limbs(ctx, t, K, N):
     """N > 65536: the streaming GEMVs hold x as 8-bit limbs with one power-of-two
     scale per group (exact integer dot products).  Besides f32 rounding, each x_k
     is rounded by at most 2^-23 of its group's max |x|; the store and the fused
     argmax (LM head) both follow the dequantized f64 dot product.  q6_K matrices
-    read the lane-major copy of their quants (K = 2048: two chunks per lane)."""
-    rng = np.random.default_rng(K + t)
-    N = 70001
+    read the lane-major copy of their quants (K = 2048: two chunks per lane).  At
+    N = 256206 the launch is one resident round of workgroups and the rows past the
+    first 32 MB are loaded non-temporally."""
+    rng = np.random.default_rng(K + t + N)
     wf = rng.normal(0, 0.02, (N, K)).astype(np.float32)
     blocks = M.quantize(t, wf)
     w = upload(ctx, t, blocks, N, K)
@@ -311,6 +316,35 @@ def test_attention_decode(ctx, hd):
     _lib.check(ctx.lib.mlg_attn_decode(ptr(qd), ptr(kd), ptr(vd), b, H, hd, L, None, ptr(step), ptr(od), None))
     torch.cuda.synchronize()
     np.testing.assert_allclose(od.cpu().numpy().reshape(b, H, hd)[1], out[1], atol=1e-6)
+
+
+def test_argmax_partial_full_vocabulary(ctx):
+    """BASELINE config 2's argmax over 256206 f32 logits (kernels/malaga.cu:247-280 then
+    the merge): the partial maxima merge to np.argmax's answer, ties go to the lowest
+    index, and the masked id is never chosen."""
+    rng = np.random.default_rng(4)
+    b, V = 4, 256206
+    x = rng.normal(0, 1, (b, V)).astype(np.float32)
+    x[1, 200000] = x[1, 9] = 11.0  # tie across partials: 9 wins
+    x[2, V - 1] = 12.0  # the last id
+    x[3, 2] = 50.0  # masked below: the runner-up wins
+    xd = dev(x)
+    for parts in (1, 64, 300):
+        pv = torch.zeros((b, parts), device="cuda")
+        pi = torch.zeros((b, parts), dtype=torch.int32, device="cuda")
+        for mask in (-1, 2):
+            _lib.check(ctx.lib.mlg_argmax_partial(ptr(xd), b, V, mask, ptr(pv), ptr(pi), parts, None))
+            torch.cuda.synchronize()
+            v, i = pv.cpu().numpy(), pi.cpu().numpy().view(np.uint32)
+            ref = x.copy()
+            if mask >= 0:
+                ref[:, mask] = -np.inf
+            for r in range(b):
+                best = v[r].max()
+                got = int(i[r][v[r] == best].min())
+                assert got == int(np.argmax(ref[r])), (parts, mask, r)
+                assert best == ref[r].max()
+            assert int(i[1][v[1] == v[1].max()].min()) == 9
 
 
 def test_logsoftmax_topk(ctx):
