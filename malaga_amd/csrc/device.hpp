@@ -1,5 +1,6 @@
 // Device-side helpers shared by the HIP kernels (gfx950, wave64).
 #pragma once
+#include <type_traits>
 #include <hip/hip_fp16.h>
 #include <hip/hip_runtime.h>
 #include <stdint.h>
@@ -111,6 +112,18 @@ __device__ __forceinline__ double wave_sum_f64(double v) {
     return (lane_value_f64(v, 0) + lane_value_f64(v, 16)) + (lane_value_f64(v, 32) + lane_value_f64(v, 48));
 }
 
+// Sum over aligned groups of W lanes (W = 1, 2, 4, 8, 16) in f64; every lane of a group
+// receives the same, bitwise identical result.
+template <int W>
+__device__ __forceinline__ double group_sum_f64(double v) {
+    if constexpr (W >= 2) v += dpp_mov_f64<kDppXor1>(v);
+    if constexpr (W >= 4) v += dpp_mov_f64<kDppXor2>(v);
+    if constexpr (W >= 8) v += dpp_mov_f64<kDppHalfMirror>(v);
+    if constexpr (W >= 16) v += dpp_mov_f64<kDppMirror>(v);
+    static_assert(W <= 16, "groups of at most 16 lanes");
+    return v;
+}
+
 struct OpAdd {
     __device__ float operator()(float a, float b) const { return a + b; }
 };
@@ -176,7 +189,21 @@ __device__ __forceinline__ void add4(float4 &a, const float4 &b) {
     a.w += b.w;
 }
 
+typedef _Float16 h2_t __attribute__((ext_vector_type(2)));
+typedef _Float16 h4_t __attribute__((ext_vector_type(4)));
+typedef _Float16 h8_t __attribute__((ext_vector_type(8)));
+typedef float f4_t __attribute__((ext_vector_type(4)));
 __device__ __forceinline__ float4 ld4(const float *p, int f) { return reinterpret_cast<const float4 *>(p)[f]; }
+
+// f(std::integral_constant<int, I>) for I = 0 .. N - 1: loop indices that are constants
+// from the start (register arrays indexed by them stay in registers)
+template <int I, int N, class F>
+__device__ __forceinline__ void static_for(F &&f) {
+    if constexpr (I < N) {
+        f(std::integral_constant<int, I>{});
+        static_for<I + 1, N>(f);
+    }
+}
 
 // ---- LayerNorm statistics in f64 (biased variance, eps inside the root) ----------
 // The f64 sums of a float4's values and squares, paired as the fused step's prologue.

@@ -1,0 +1,453 @@
+// Decode projections for batches of up to 64 rows (src/model.rs:552-612 at batch > 4):
+// one launch per projection on the MFMA units, no split K, no reduction kernel.
+//
+// A workgroup owns one 16 x 16 output tile (grid N / 16 x M / 16).  Its NW waves split K:
+// wave w takes the 256-wide K blocks w, w + NW, ..., so each X value is read by exactly
+// one wave, straight from global memory into the A-operand registers (split there into
+// f16 hi + lo), with no LDS staging.  The waves' partial tiles meet in LDS and are added
+// in a fixed order; the epilogue then runs once per output, one output per thread of the
+// first four waves.
+//
+// Loads complete in the order they are issued, and a wave that waits for one load waits
+// for every load before it.  So each thread first requests what is needed first or is
+// small (the LayerNorm operands, its epilogue operands), then the W quants of its first K
+// block, then the X fragments in the order the slices use them; every load is
+// unconditional (rows past M read row M - 1 and are never stored) and the wave index is a
+// scalar, so that slice s waits for its own fragment and nothing later.
+//
+// PRO_SPLIT: the input arrives split into f16 hi = f16(x) and lo = f16(x - hi), the form
+// the A operand needs, written that way by its producer (the FFN-up projection, the
+// attention), so no conversion is left here.  Each 4 values of a row are stored as
+// [hi0..hi3 | lo0..lo3] in the 16 bytes their f32 values would take, so the loads are
+// those of an f32 input; producers write each such group with one 16-byte store.
+//
+// PRO_LN: the input is LayerNorm(x) of the residual stream, normalized as the fragments
+// arrive.  The row statistics are not recomputed: the launch that last wrote x
+// (EPI_RESID) left the f64 sums of x and x^2 of every 16 columns beside it, and the
+// prologue adds those P = K / 16 partials per row in a fixed order.
+//
+// Epilogues: EPI_STORE y = x W^T + bias (ReLU), f32 or split into hi and lo planes; EPI_RESID x += x_in W^T + bias in place,
+// plus the statistics of the new x; EPI_QKV q (f32) and K/V (f16, cache slot *step).
+#include "kernels.hpp"
+#include "mfma_core.hpp"
+
+namespace mlg {
+
+namespace {
+
+struct DArgs {
+    WPtr w;
+    const float *x;  // [M][ldx] input rows (PRO_LN: the residual stream; PRO_SPLIT: split rows)
+    int ldx, M;
+    const double *stats;  // PRO_LN: [P][M][2] sums of x and x^2 per 16 columns
+    int P;
+    const float *gamma, *beta;
+    float eps;
+    const float *bias;
+    float *y;  // EPI_STORE [M][ldy] f32 (split rows if split_out)
+    int ldy, relu, split_out;
+    float *xres;        // EPI_RESID: the residual stream [M][N]
+    double *stats_out;  // EPI_RESID: [N / 16][M][2]
+    float *q;           // EPI_QKV: q [M][d], caches [M][H][slots][hd]
+    __half *kc, *vc;
+    int H, hd, slots;
+    const uint32_t *step;
+};
+
+enum DPro : int { PRO_RAW = 0, PRO_LN = 1, PRO_SPLIT = 2 };
+enum DEpi : int { EPI_STORE = 0, EPI_RESID = 1, EPI_QKV = 2 };
+
+constexpr int kDgMaxNW = 8;      // waves per workgroup at most (the K split)
+constexpr int kDgMaxBPW = 4;     // K blocks per wave at most: K <= 8192
+constexpr int kDgMaxLnK = 2048;  // LayerNorm projections: K = d_model <= 2048 (gamma, beta in LDS)
+constexpr int kLnTPR = 16;                          // threads per row adding the statistics
+constexpr int kLnQ = kDgMaxLnK / 16 / kLnTPR;       // partials per thread at most
+constexpr int kRS = 17;                             // LDS row stride of the partial tiles
+
+// BPW: K blocks per wave (compile time, it sizes the fragment ring); NT: 16-column tiles
+// per workgroup (1 or 2; with 2, each X fragment, once normalized and split, feeds two
+// tiles); the wave count NW (4 or 8) is blockDim.x / 64.
+template <int T, int BPW, int NT, int PRO, int EPI>
+__global__ __launch_bounds__(kDgMaxNW * 64) void k_dgemm(DArgs a) {
+    using W = MW<T>;
+    constexpr int SK = W::SK, XQ = SK / 16;  // float4s of X per lane and slice
+    constexpr int TN = 16 * NT, RS = TN + 1;  // columns of the tile; LDS row stride
+    __shared__ float red[kDgMaxNW * 16 * RS];
+    __shared__ float lnm[16], lnr[16];
+    __shared__ float gb[PRO == PRO_LN ? 2 * kDgMaxLnK : 1];  // PRO_LN: gamma | beta
+    const int NW = int(blockDim.x) >> 6;
+    const int t = threadIdx.x, lane = t & 63, ln = lane & 15, kq = lane >> 4;
+    const int wv = __builtin_amdgcn_readfirstlane(t >> 6);
+    const int K = a.w.K, nblk = K / kStep, n0 = blockIdx.x * TN, m0 = blockIdx.y * 16;
+    // K block j of this wave; every wave runs BPW blocks, and a block past the end (K not
+    // a multiple of NW x BPW blocks) is read at the last block and weighs 0
+    auto blk = [&](int j) { return min(wv + j * NW, nblk - 1); };
+
+    // PRO_LN operands: this thread's float4 of gamma and beta, and its share of the
+    // statistics of row m0 + t / 16 (partials p = t % 16 + 16 q)
+    float4 gv = make_float4(0.f, 0.f, 0.f, 0.f), bv = gv;
+    double2 sp[PRO == PRO_LN ? kLnQ : 1];
+    if constexpr (PRO == PRO_LN) {
+        const int gi = min(t, K / 4 - 1);
+        gv = ld4(a.gamma, gi);
+        bv = ld4(a.beta, gi);
+        // waves 4..7 take no share: they read one address (no branch, which would make
+        // the loads after it wait for these)
+        const int m = wv < 4 ? min(m0 + (t >> 4), a.M - 1) : 0;
+#pragma unroll
+        for (int q = 0; q < kLnQ; ++q) {
+            const int p = wv < 4 ? min((t & 15) + q * kLnTPR, a.P - 1) : 0;
+            sp[q] = *reinterpret_cast<const double2 *>(a.stats + (size_t(p) * a.M + m) * 2);
+        }
+    }
+    // epilogue operands of this thread's outputs o = t + 256 u: row m0 + o / TN, column
+    // n0 + o % TN
+    float bias_v[NT], xold[NT];
+#pragma unroll
+    for (int u = 0; u < NT; ++u) {
+        const int o = t + 256 * u, omc = min(m0 + o / TN, a.M - 1), onc = min(n0 + o % TN, a.w.N - 1);
+        bias_v[u] = a.bias ? a.bias[onc] : 0.f;
+        xold[u] = 0.f;
+        if constexpr (EPI == EPI_RESID) xold[u] = a.xres[size_t(omc) * a.w.N + onc];
+    }
+
+    using WR = typename W::Regs;
+    // W of the first K block, then the next block's when a block starts
+    WR wr[2][NT];
+    int wrow[NT];
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) {
+        wrow[nt] = min(n0 + nt * 16 + ln, a.w.N - 1);
+        W::load(a.w, wrow[nt], blk(0), kq, wr[0][nt]);
+    }
+
+    // X fragment of (block kb, slice s): row m0 + ln, columns kb 256 + s SK + kq SK / 4
+    // (PRO_SPLIT: the same bytes hold [hi0..hi3 | lo0..lo3] per 4 columns)
+    const float *xrow = a.x + size_t(min(m0 + ln, a.M - 1)) * a.ldx;
+    struct Frag {
+        float4 x[XQ];
+    };
+    auto load_x = [&](int kb, int s, Frag &f) {
+        const float4 *src = reinterpret_cast<const float4 *>(xrow + kb * kStep + s * SK + kq * (SK / 4));
+#pragma unroll
+        for (int i = 0; i < XQ; ++i) f.x[i] = src[i];
+    };
+    // The (block, slice) items of this wave in order, D fragments in flight: item i uses
+    // slot i % D, refilled with item i + D as soon as it is used.
+    constexpr int NI = W::SLICES * BPW, D = NI < 16 / XQ ? NI : 16 / XQ;
+    Frag buf[D];
+#pragma unroll
+    for (int i = 0; i < D; ++i) load_x(blk(i / W::SLICES), i % W::SLICES, buf[i]);
+    // all of the above is requested before any of it is used
+    __builtin_amdgcn_sched_barrier(0);
+
+    float mrow = 0.f, rrow = 0.f;  // PRO_LN: mean and 1 / sqrt(var + eps) of this lane's row
+    if constexpr (PRO == PRO_LN) {
+        if (t < K / 4) {
+            reinterpret_cast<float4 *>(gb)[t] = gv;
+            reinterpret_cast<float4 *>(gb + K)[t] = bv;
+        }
+        if (wv < 4) {
+            const int j = t & 15;
+            double s1 = 0.0, s2 = 0.0;
+#pragma unroll
+            for (int q = 0; q < kLnQ; ++q)
+                if (j + q * kLnTPR < a.P) {
+                    s1 += sp[q].x;
+                    s2 += sp[q].y;
+                }
+            s1 = group_sum_f64<kLnTPR>(s1);
+            s2 = group_sum_f64<kLnTPR>(s2);
+            if (j == 0) {
+                const int ml = t >> 4;
+                const double mu = s1 / K, var = fmax(s2 / K - mu * mu, 0.0);
+                lnm[ml] = m0 + ml < a.M ? float(mu) : 0.f;
+                lnr[ml] = m0 + ml < a.M ? float(1.0 / sqrt(var + double(a.eps))) : 0.f;
+            }
+        }
+        __syncthreads();
+        mrow = lnm[ln];
+        rrow = lnr[ln];
+    }
+
+    f4_t acc[NT];
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) acc[nt] = f4_t{0.f, 0.f, 0.f, 0.f};
+    // slice s of block kb with the W registers wrb and the fragment f
+    auto compute = [&](int kb, int s, const WR (&wrb)[NT], const Frag &f, bool live) {
+        float sc[NT], mn[NT];
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt) {
+            W::scale(wrb[nt], s, sc[nt], mn[nt]);
+            sc[nt] = live ? sc[nt] : 0.f;
+            mn[nt] = live ? mn[nt] : 0.f;
+        }
+        float v[SK / 4];
+#pragma unroll
+        for (int i = 0; i < (PRO == PRO_SPLIT ? 0 : XQ); ++i) {
+            float4 e = f.x[i];
+            if constexpr (PRO == PRO_LN) {
+                const int k = kb * kStep + s * SK + kq * (SK / 4) + 4 * i;
+                const float4 g = *reinterpret_cast<const float4 *>(gb + k), b = *reinterpret_cast<const float4 *>(gb + K + k);
+                e = make_float4((e.x - mrow) * rrow * g.x + b.x, (e.y - mrow) * rrow * g.y + b.y,
+                                (e.z - mrow) * rrow * g.z + b.z, (e.w - mrow) * rrow * g.w + b.w);
+            }
+            v[4 * i] = e.x;
+            v[4 * i + 1] = e.y;
+            v[4 * i + 2] = e.z;
+            v[4 * i + 3] = e.w;
+        }
+        if constexpr (SK == 32) {
+            h8_t ah, al;
+            if constexpr (PRO == PRO_SPLIT) {
+                // whole-vector shuffles (component access would keep the ring in memory)
+                const h8_t p0 = __builtin_bit_cast(h8_t, f.x[0]), p1 = __builtin_bit_cast(h8_t, f.x[1]);
+                ah = __builtin_shufflevector(p0, p1, 0, 1, 2, 3, 8, 9, 10, 11);
+                al = __builtin_shufflevector(p0, p1, 4, 5, 6, 7, 12, 13, 14, 15);
+            } else {
+#pragma unroll
+                for (int i = 0; i < 8; ++i) {
+                    ah[i] = _Float16(v[i]);
+                    al[i] = _Float16(v[i] - float(ah[i]));
+                }
+            }
+            f4_t xs = f4_t{0.f, 0.f, 0.f, 0.f};
+            if constexpr (W::MIN) {  // per-row sums of the 32 X values: B = ones
+                const h8_t ones = {_Float16(1), _Float16(1), _Float16(1), _Float16(1),
+                                   _Float16(1), _Float16(1), _Float16(1), _Float16(1)};
+                xs = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, ones, xs, 0, 0, 0);
+                xs = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, ones, xs, 0, 0, 0);
+            }
+#pragma unroll
+            for (int nt = 0; nt < NT; ++nt) {
+                const h8_t bop = W::b(wrb[nt], s);
+                f4_t tmp = f4_t{0.f, 0.f, 0.f, 0.f};
+                tmp = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bop, tmp, 0, 0, 0);
+                tmp = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, bop, tmp, 0, 0, 0);
+#pragma unroll
+                for (int r = 0; r < 4; ++r)
+                    acc[nt][r] = W::MIN ? fmaf(sc[nt], tmp[r], fmaf(-mn[nt], xs[r], acc[nt][r]))
+                                        : fmaf(sc[nt], tmp[r], acc[nt][r]);
+            }
+        } else {
+            h4_t ah, al;
+            if constexpr (PRO == PRO_SPLIT) {
+                const h8_t p0 = __builtin_bit_cast(h8_t, f.x[0]);
+                ah = __builtin_shufflevector(p0, p0, 0, 1, 2, 3);
+                al = __builtin_shufflevector(p0, p0, 4, 5, 6, 7);
+            } else {
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    ah[i] = _Float16(v[i]);
+                    al[i] = _Float16(v[i] - float(ah[i]));
+                }
+            }
+#pragma unroll
+            for (int nt = 0; nt < NT; ++nt) {
+                const h4_t bop = W::b(wrb[nt], s);
+                f4_t tmp = f4_t{0.f, 0.f, 0.f, 0.f};
+                tmp = __builtin_amdgcn_mfma_f32_16x16x16f16(ah, bop, tmp, 0, 0, 0);
+                tmp = __builtin_amdgcn_mfma_f32_16x16x16f16(al, bop, tmp, 0, 0, 0);
+#pragma unroll
+                for (int r = 0; r < 4; ++r) acc[nt][r] = fmaf(sc[nt], tmp[r], acc[nt][r]);
+            }
+        }
+    };
+    static_for<0, BPW>([&](auto jc) {
+        constexpr int j = decltype(jc)::value;
+        const int kb = blk(j);
+        const bool live = wv + j * NW < nblk;  // scalar
+        if constexpr (j + 1 < BPW)
+#pragma unroll
+            for (int nt = 0; nt < NT; ++nt) W::load(a.w, wrow[nt], blk(j + 1), kq, wr[(j + 1) & 1][nt]);
+        static_for<0, W::SLICES>([&](auto sc) {
+            constexpr int s = decltype(sc)::value, i = j * W::SLICES + s, r = i + D;
+            compute(kb, s, wr[j & 1], buf[i % D], live);
+            if constexpr (r < NI) {
+                // the refill stays behind the compute that frees its slot (hoisted,
+                // it would hold a second set of fragments in registers)
+                __builtin_amdgcn_sched_barrier(0);
+                load_x(blk(r / W::SLICES), r % W::SLICES, buf[i % D]);
+            }
+        });
+    });
+
+    // the waves' partial tiles (lane: column nt 16 + ln, rows 4 kq .. 4 kq + 3), added in
+    // wave order
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) red[(wv * 16 + 4 * kq + r) * RS + nt * 16 + ln] = acc[nt][r];
+    __syncthreads();
+    if (wv >= 4) return;  // scalar: 256 NT outputs, NT per thread of the first four waves
+    const uint32_t slot = EPI == EPI_QKV ? *a.step : 0u;
+#pragma unroll
+    for (int u = 0; u < NT; ++u) {
+        const int o = t + 256 * u, ml = o / TN, c = o % TN, om = m0 + ml, on = n0 + c;
+        const bool own = om < a.M && on < a.w.N;
+        float v = red[ml * RS + c];
+        for (int w = 1; w < NW; ++w) v += red[(w * 16 + ml) * RS + c];
+        v += bias_v[u];
+        if constexpr (EPI == EPI_STORE) {
+            const float r = a.relu ? fmaxf(v, 0.f) : v;
+            if (a.split_out) {  // kernel argument: every lane takes this branch
+                // lanes 4g .. 4g + 3 hold 4 consecutive columns of one row; the first
+                // writes their [hi0..hi3 | lo0..lo3] as one 16-byte store
+                h4_t hv, lv;
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const float rj = __shfl(r, j, 4);
+                    hv[j] = _Float16(rj);
+                    lv[j] = _Float16(rj - float(hv[j]));
+                }
+                if (own && (c & 3) == 0) {
+                    const uint2 hb = __builtin_bit_cast(uint2, hv), lb = __builtin_bit_cast(uint2, lv);
+                    *reinterpret_cast<uint4 *>(a.y + size_t(om) * a.ldy + on) = make_uint4(hb.x, hb.y, lb.x, lb.y);
+                }
+            } else if (own) {
+                a.y[size_t(om) * a.ldy + on] = r;
+            }
+        } else if constexpr (EPI == EPI_QKV) {
+            if (own) {
+                const int d = a.H * a.hd;
+                if (on < d) {
+                    a.q[size_t(om) * d + on] = v;
+                } else {
+                    const int cc = on < 2 * d ? on - d : on - 2 * d;
+                    const size_t off = ((size_t(om) * a.H + cc / a.hd) * a.slots + slot) * a.hd + cc % a.hd;
+                    (on < 2 * d ? a.kc : a.vc)[off] = __float2half(v);
+                }
+            }
+        } else {  // EPI_RESID: x += y, and the new x's sums per row and 16 columns (16 lanes)
+            const float xn = own ? xold[u] + v : 0.f;
+            if (own) a.xres[size_t(om) * a.w.N + on] = xn;
+            const double s1 = group_sum_f64<16>(double(xn)), s2 = group_sum_f64<16>(double(xn) * double(xn));
+            if (own && (c & 15) == 0) {
+                double *sp_out = a.stats_out + (size_t(on >> 4) * a.M + om) * 2;
+                sp_out[0] = s1;
+                sp_out[1] = s2;
+            }
+        }
+    }
+}
+
+// The K split: 4 waves up to four K blocks (K <= 1024), else 8 waves of 1, 2 or 4 blocks.
+inline int dg_waves(int nblk) { return nblk <= 4 ? 4 : kDgMaxNW; }
+inline int dg_bpw(int nblk) {
+    const int nw = dg_waves(nblk), per = (nblk + nw - 1) / nw;
+    return per <= 1 ? 1 : per <= 2 ? 2 : 4;
+}
+
+// Two column tiles per workgroup where one tile each would take more than two
+// workgroups per CU (K-split waves share the CU): the normalized, split X then feeds both.
+constexpr int kDgWideGrid = 512;
+
+template <int T, int BPW, int PRO, int EPI>
+hipError_t launch_dgemm(const DArgs &a, hipStream_t st) {
+    const unsigned gy = unsigned((a.M + 15) / 16), block = unsigned(dg_waves(a.w.K / kStep) * 64);
+    const unsigned tiles1 = unsigned((a.w.N + 15) / 16);
+    if constexpr (EPI != EPI_RESID) {  // the residual projections are N = d_model wide
+        if (tiles1 * gy >= unsigned(kDgWideGrid)) {
+            hipLaunchKernelGGL((k_dgemm<T, BPW, 2, PRO, EPI>), dim3((a.w.N + 31) / 32, gy), dim3(block), 0, st, a);
+            return hipGetLastError();
+        }
+    }
+    hipLaunchKernelGGL((k_dgemm<T, BPW, 1, PRO, EPI>), dim3(tiles1, gy), dim3(block), 0, st, a);
+    return hipGetLastError();
+}
+
+// only the residual projections (ffn_down: K = the FFN width) take more than one K
+// block per wave
+template <int T, int PRO, int EPI>
+hipError_t launch_dgemm_m(const DArgs &a, hipStream_t st) {
+    const int bpw = dg_bpw(a.w.K / kStep);
+    if constexpr (EPI == EPI_RESID) {
+        if (bpw == 4) return launch_dgemm<T, 4, PRO, EPI>(a, st);
+        if (bpw == 2) return launch_dgemm<T, 2, PRO, EPI>(a, st);
+    } else if (bpw != 1) {
+        return hipErrorInvalidValue;  // K > 2048 in a LayerNorm / QKV projection: not a decoder shape
+    }
+    return launch_dgemm<T, 1, PRO, EPI>(a, st);
+}
+
+template <int PRO, int EPI>
+hipError_t launch_dgemm_t(const DevMatrix &w, const DArgs &a, hipStream_t st) {
+    switch (w.type) {
+    case GGML_Q4_K: return launch_dgemm_m<GGML_Q4_K, PRO, EPI>(a, st);
+    case GGML_Q5_K: return launch_dgemm_m<GGML_Q5_K, PRO, EPI>(a, st);
+    case GGML_Q6_K: return launch_dgemm_m<GGML_Q6_K, PRO, EPI>(a, st);
+    case GGML_Q8_0: return launch_dgemm_m<GGML_Q8_0, PRO, EPI>(a, st);
+    case GGML_F16: return launch_dgemm_m<GGML_F16, PRO, EPI>(a, st);
+    default: return hipErrorInvalidValue;
+    }
+}
+
+DArgs dargs(const DevMatrix &w, const float *x, int ldx, int M, const DgemmLn *ln, const float *bias) {
+    DArgs a{};
+    a.w = wptr_of(w);
+    a.x = x;
+    a.ldx = ldx;
+    a.M = M;
+    a.bias = bias;
+    if (ln) {
+        a.stats = ln->stats;
+        a.P = w.K / 16;
+        a.gamma = ln->g;
+        a.beta = ln->b;
+        a.eps = ln->eps;
+    }
+    return a;
+}
+
+bool dgemm_args_ok(const DevMatrix &w, const float *x, int ldx, int M, const DgemmLn *ln) {
+    // ldx % 8: rows of the split planes start on 16 bytes too
+    return dgemm_supported(w, M) && x && ldx % 8 == 0 && ldx >= w.K && reinterpret_cast<uintptr_t>(x) % 16 == 0 &&
+           (!ln || (ln->stats && ln->g && ln->b && reinterpret_cast<uintptr_t>(ln->g) % 16 == 0 &&
+                    reinterpret_cast<uintptr_t>(ln->b) % 16 == 0));
+}
+
+}  // namespace
+
+bool dgemm_supported(const DevMatrix &w, int M) {
+    return gemm_mfma_supported(w) && M >= 1 && M <= kDgemmMaxRows && w.K / kStep <= kDgMaxBPW * kDgMaxNW;
+}
+
+hipError_t dgemm_store(const DevMatrix &w, const float *x, int ldx, int M, const DgemmLn *ln, const float *bias,
+                       bool relu, float *y, int ldy, hipStream_t st, bool y_split) {
+    if (!dgemm_args_ok(w, x, ldx, M, ln) || !y || ldy < w.N) return hipErrorInvalidValue;
+    // split rows are written 4 columns (16 bytes) at a time
+    if (y_split && (w.N % 4 || ldy % 4 || reinterpret_cast<uintptr_t>(y) % 16)) return hipErrorInvalidValue;
+    DArgs a = dargs(w, x, ldx, M, ln, bias);
+    a.y = y;
+    a.split_out = y_split ? 1 : 0;
+    a.ldy = ldy;
+    a.relu = relu ? 1 : 0;
+    return ln ? launch_dgemm_t<PRO_LN, EPI_STORE>(w, a, st) : launch_dgemm_t<PRO_RAW, EPI_STORE>(w, a, st);
+}
+
+hipError_t dgemm_resid(const DevMatrix &w, const float *x, int ldx, int M, const float *bias, float *xres,
+                       double *stats_out, hipStream_t st, bool x_split) {
+    if (!dgemm_args_ok(w, x, ldx, M, nullptr) || !xres || !stats_out || w.N % 16) return hipErrorInvalidValue;
+    DArgs a = dargs(w, x, ldx, M, nullptr, bias);
+    a.xres = xres;
+    a.stats_out = stats_out;
+    if (x_split) return launch_dgemm_t<PRO_SPLIT, EPI_RESID>(w, a, st);
+    return launch_dgemm_t<PRO_RAW, EPI_RESID>(w, a, st);
+}
+
+hipError_t dgemm_qkv(const DevMatrix &w, const float *x, int ldx, int M, const DgemmLn *ln, const float *bias, int H,
+                     int hd, int slots, const uint32_t *step, float *q, __half *kc, __half *vc, hipStream_t st) {
+    if (!dgemm_args_ok(w, x, ldx, M, ln) || w.N != 3 * H * hd || !q || !kc || !vc || !step)
+        return hipErrorInvalidValue;
+    DArgs a = dargs(w, x, ldx, M, ln, bias);
+    a.q = q;
+    a.kc = kc;
+    a.vc = vc;
+    a.H = H;
+    a.hd = hd;
+    a.slots = slots;
+    a.step = step;
+    return ln ? launch_dgemm_t<PRO_LN, EPI_QKV>(w, a, st) : launch_dgemm_t<PRO_RAW, EPI_QKV>(w, a, st);
+}
+
+}  // namespace mlg

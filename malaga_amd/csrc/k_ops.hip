@@ -390,7 +390,7 @@ __global__ __launch_bounds__(1024) void k_greedy_finalize(const float *pv, const
 template <int HD>
 __global__ __launch_bounds__(256) void k_attn_waves(const float *q, const __half *K, const __half *V, int b, int H,
                                                     int L, const uint32_t *lens, const uint32_t *step, float *out,
-                                                    const uint32_t *rows) {
+                                                    const uint32_t *rows, int out_split) {
     constexpr int TPK = HD / 8, SPL = 64 / TPK, U = 8;
     __shared__ float wsc_all[4 * 512];
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
@@ -454,6 +454,26 @@ __global__ __launch_bounds__(256) void k_attn_waves(const float *q, const __half
     for (int e = 0; e < 8; ++e) wsc[lane * 8 + e] = acc[e];
     __builtin_amdgcn_s_waitcnt(0xc07f);
     __builtin_amdgcn_wave_barrier();
+    if (out_split) {
+        // per 4 values f16 hi0..hi3, lo0..lo3 in the 16 bytes of their f32 values: one
+        // lane per 4 values, one whole store each
+        for (int e4 = lane; e4 < HD / 4; e4 += 64) {
+            h4_t hv, lv;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const int e = 4 * e4 + j;
+                float o = 0.f;
+#pragma unroll
+                for (int s2 = 0; s2 < SPL; ++s2) o += wsc[(s2 * TPK + e / 8) * 8 + e % 8];
+                o *= inv;
+                hv[j] = _Float16(o);
+                lv[j] = _Float16(o - float(hv[j]));
+            }
+            const uint2 hb = __builtin_bit_cast(uint2, hv), lb = __builtin_bit_cast(uint2, lv);
+            reinterpret_cast<uint4 *>(out + size_t(bi) * d + hh * HD)[e4] = make_uint4(hb.x, hb.y, lb.x, lb.y);
+        }
+        return;
+    }
     for (int e = lane; e < HD; e += 64) {
         float o = 0.f;
 #pragma unroll
@@ -728,13 +748,15 @@ bool attn_head_size_supported(int hd) {
 }
 
 hipError_t attn_decode(const float *q, const __half *K, const __half *V, int b, int H, int hd, int L,
-                       const uint32_t *lens, const uint32_t *step, float *out, hipStream_t st, const uint32_t *rows) {
+                       const uint32_t *lens, const uint32_t *step, float *out, hipStream_t st, const uint32_t *rows,
+                       bool out_split) {
     if (b * H <= 0) return hipSuccess;
     const dim3 wgrid(unsigned((b * H + 3) / 4));
     switch (hd) {
 #define MLG_ATTN_WAVES(HD)                                                                                          \
     case HD:                                                                                                        \
-        hipLaunchKernelGGL(k_attn_waves<HD>, wgrid, dim3(256), 0, st, q, K, V, b, H, L, lens, step, out, rows);     \
+        hipLaunchKernelGGL(k_attn_waves<HD>, wgrid, dim3(256), 0, st, q, K, V, b, H, L, lens, step, out, rows,      \
+                           out_split ? 1 : 0);                                                                      \
         return hipGetLastError();
         MLG_ATTN_WAVES(8)
         MLG_ATTN_WAVES(16)

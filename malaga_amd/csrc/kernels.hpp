@@ -80,6 +80,29 @@ hipError_t gemm_residual_ln(const DevMatrix &w, const float *X, int ldx, int M, 
 hipError_t gemm_qkv(const DevMatrix &w, const float *X, int ldx, int M, const float *bias, int H, int hd, int slots,
                     const uint32_t *step, float *q, __half *kc, __half *vc, float *qkv_tmp, hipStream_t st, float *ws,
                     size_t ws_bytes);
+// ---- decode projections for batches of up to 64 rows, one launch each (k_dgemm.hip) ----
+constexpr int kDgemmMaxRows = 64;
+// Input LayerNorm from the statistics the residual stream's last writer left:
+// stats [K / 16][M][2] (f64 sums of x and x^2 per 16 columns), gamma/beta [K].
+struct DgemmLn {
+    const double *stats;
+    const float *g, *b;
+    float eps;
+};
+bool dgemm_supported(const DevMatrix &w, int M);
+// y[m][n] = (LN(x) or x)[m] . W[n] + bias[n], ReLU optional.  y_split: y is written as
+// split rows in the same bytes: per 4 columns f16 hi0..hi3 = f16(y) then lo0..lo3 =
+// f16(y - hi), the A-operand form of the decode GEMMs.
+hipError_t dgemm_store(const DevMatrix &w, const float *x, int ldx, int M, const DgemmLn *ln, const float *bias,
+                       bool relu, float *y, int ldy, hipStream_t st, bool y_split = false);
+// xres[m][n] += x[m] . W[n] + bias[n] in place (xres [M][N]), and stats_out [N / 16][M][2]
+// of the new rows.  x_split: x holds split rows (as y_split above).
+hipError_t dgemm_resid(const DevMatrix &w, const float *x, int ldx, int M, const float *bias, float *xres,
+                       double *stats_out, hipStream_t st, bool x_split = false);
+// The fused QKV projection: q [M][d] f32, K/V f16 into the caches [M][H][slots][hd] at *step.
+hipError_t dgemm_qkv(const DevMatrix &w, const float *x, int ldx, int M, const DgemmLn *ln, const float *bias, int H,
+                     int hd, int slots, const uint32_t *step, float *q, __half *kc, __half *vc, hipStream_t st);
+
 // M <= 32 rows with X resident in LDS (K <= 1024 at M > 16, K <= 2048 at M <= 16).
 bool gemm_rx_supported(const DevMatrix &w, int M);
 // Greedy LM head for 4 < M <= 32: per-wave argmax partials pv/pi [M][parts] of
@@ -139,8 +162,11 @@ hipError_t qkv_split(const float *qkv, int b, int H, int hd, int m, const uint32
 // if lens, else *step + 1.  out [b][H*hd].  Head sizes: attn_head_size_supported.
 bool attn_head_size_supported(int hd);
 hipError_t attn_decode(const float *q, const __half *K, const __half *V, int b, int H, int hd, int L,
-                       const uint32_t *lens, const uint32_t *step, float *out, hipStream_t st, const uint32_t *rows = nullptr);
+                       const uint32_t *lens, const uint32_t *step, float *out, hipStream_t st, const uint32_t *rows = nullptr,
+                       bool out_split = false);
 // rows (optional, [b][L]): cache row holding slot j of row b (beam reordering without copies).
+// out_split: out is written as split rows (per 4 values f16 hi0..hi3, then lo0..lo3 =
+// f16(out - hi), in the bytes of the f32 row): the input form of the decode GEMMs' x_split.
 // Encoder self-attention over f32 qkv [b*s][3d] (rows of sentence i are i*s..),
 // key j of row i valid iff j < lens[i].  out [b*s][d].
 hipError_t attn_prefill(const float *qkv, int b, int s, int H, int hd, const uint32_t *lens, float *out,

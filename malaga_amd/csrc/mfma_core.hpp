@@ -1,0 +1,182 @@
+// MFMA operands from quantized weights (gfx950 f16 MFMA), shared by the GEMM kernels:
+// the integer quants (q4_K / q5_K nibbles, q6_K 6-bit values - 32, q8_0 int8) are exact
+// in f16, so they are the B operand as they are; block scales and k-quant mins are
+// applied per sub-block in f32 by the caller:
+//   sum_k w_k x_k = d sc * sum_k q_k x_k - dmin m * sum_k x_k.
+// B-operand layout (16x16x32 / 16x16x16 f16 MFMA): lane l holds W row l % 16 and the
+// k-group l / 16 of the sub-block.  Quant bytes become f16 with v_perm
+// (byte -> 0x64xx = 1024 + byte) and one packed f16 subtraction.
+#pragma once
+#include "device.hpp"
+#include "gemv_core.hpp"
+
+namespace mlg {
+
+
+constexpr int kStep = 256;  // K per W fetch (one k-quant super-block)
+
+
+// f16 pair (1024 + byte sel0, 1024 + byte sel1) of v, minus `off` (exact for bytes < 1024 - off range)
+__device__ __forceinline__ uint32_t bytes_to_h2(uint32_t v, uint32_t sel, h2_t off) {
+    const uint32_t p = __builtin_amdgcn_perm(0x64646464u, v, sel);
+    return __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2_t, p) - off);
+}
+// the 4 bytes of v as 4 f16 values (byte - (off - 1024)) in natural order
+__device__ __forceinline__ uint2 bytes_to_h4(uint32_t v, h2_t off) {
+    return make_uint2(bytes_to_h2(v, 0x04010400u, off), bytes_to_h2(v, 0x04030402u, off));
+}
+
+template <int T>
+struct MW;  // per-type W fetch for one 256-wide K step
+
+// q4_K: 8 sub-blocks of 32; lane k-group kq reads bytes qs[32 g + 8 kq, +8) of the
+// 4 byte groups g (low nibbles: sub-block 2g, high nibbles: 2g + 1).
+template <>
+struct MW<GGML_Q4_K> {
+    static constexpr int SLICES = 8, SK = 32;
+    static constexpr bool MIN = true;  // w = sc q - mn: the x sums carry the min term
+    struct Regs {
+        uint4 hdr;
+        uint2 q[4];
+    };
+    __device__ static void load(const WPtr &w, int row, int kb, int kq, Regs &r) {
+        const uint8_t *blk = w.q + (size_t(row) * w.nb + kb) * 144;
+        r.hdr = *reinterpret_cast<const uint4 *>(blk);
+#pragma unroll
+        for (int g = 0; g < 4; ++g) r.q[g] = *reinterpret_cast<const uint2 *>(blk + 16 + 32 * g + 8 * kq);
+    }
+    __device__ static h8_t b(const Regs &r, int s) {
+        const uint2 q = r.q[s >> 1];
+        const int sh = 4 * (s & 1);
+        const h2_t off = {_Float16(1024), _Float16(1024)};
+        const uint2 lo = bytes_to_h4((q.x >> sh) & 0x0F0F0F0Fu, off), hi = bytes_to_h4((q.y >> sh) & 0x0F0F0F0Fu, off);
+        return __builtin_bit_cast(h8_t, make_uint4(lo.x, lo.y, hi.x, hi.y));
+    }
+    __device__ static void scale(const Regs &r, int s, float &sc, float &mn) {
+        float a, m;
+        k4_scale_min(s, r.hdr.y, r.hdr.z, r.hdr.w, a, m);
+        sc = h2f(r.hdr.x) * a;
+        mn = h2f(r.hdr.x >> 16) * m;
+    }
+};
+
+// q5_K: as q4_K plus the fifth bit of sub-block s in bit s of qh[l] (l < 32).
+template <>
+struct MW<GGML_Q5_K> {
+    static constexpr int SLICES = 8, SK = 32;
+    static constexpr bool MIN = true;
+    struct Regs {
+        uint4 hdr;
+        uint2 q[4];
+        uint2 qh;
+    };
+    __device__ static void load(const WPtr &w, int row, int kb, int kq, Regs &r) {
+        const uint8_t *blk = w.q + (size_t(row) * w.nb + kb) * 176;
+        r.hdr = *reinterpret_cast<const uint4 *>(blk);
+        r.qh = *reinterpret_cast<const uint2 *>(blk + 16 + 8 * kq);
+#pragma unroll
+        for (int g = 0; g < 4; ++g) r.q[g] = *reinterpret_cast<const uint2 *>(blk + 48 + 32 * g + 8 * kq);
+    }
+    __device__ static h8_t b(const Regs &r, int s) {
+        const uint2 q = r.q[s >> 1];
+        const int sh = 4 * (s & 1);
+        const h2_t off = {_Float16(1024), _Float16(1024)};
+        const uint32_t v0 = ((q.x >> sh) & 0x0F0F0F0Fu) | (((r.qh.x >> s) & 0x01010101u) << 4);
+        const uint32_t v1 = ((q.y >> sh) & 0x0F0F0F0Fu) | (((r.qh.y >> s) & 0x01010101u) << 4);
+        const uint2 lo = bytes_to_h4(v0, off), hi = bytes_to_h4(v1, off);
+        return __builtin_bit_cast(h8_t, make_uint4(lo.x, lo.y, hi.x, hi.y));
+    }
+    __device__ static void scale(const Regs &r, int s, float &sc, float &mn) {
+        MW<GGML_Q4_K>::Regs t{r.hdr, {}};
+        MW<GGML_Q4_K>::scale(t, s, sc, mn);
+    }
+};
+
+// q6_K: 16 groups of 16 with an int8 scale each (one 16x16x16 MFMA per group).
+// Group G = 8 n + 2 t + h holds values 128 n + 32 t + 16 h + j (j < 16): low 4 bits
+// from ql[64 n + 32 (t & 1) + 16 h + j] (nibble t >> 1), high 2 bits from
+// qh[32 n + 16 h + j] bits 2t..2t+1.  Lane k-group kq takes j = 4 kq .. 4 kq + 3.
+template <>
+struct MW<GGML_Q6_K> {
+    static constexpr int SLICES = 16, SK = 16;
+    static constexpr bool MIN = false;
+    struct Regs {
+        uint32_t qa[4], qb[4], qh[4];  // [2 n + h]
+        uint4 sc;
+        uint32_t d;
+    };
+    __device__ static void load(const WPtr &w, int row, int kb, int kq, Regs &r) {
+        const size_t blk = size_t(row) * w.nb + kb;
+        const uint8_t *qp = w.q + blk * 192;
+#pragma unroll
+        for (int nh = 0; nh < 4; ++nh) {
+            const int n = nh >> 1, h = nh & 1;
+            r.qa[nh] = *reinterpret_cast<const uint32_t *>(qp + 64 * n + 16 * h + 4 * kq);
+            r.qb[nh] = *reinterpret_cast<const uint32_t *>(qp + 64 * n + 32 + 16 * h + 4 * kq);
+            r.qh[nh] = *reinterpret_cast<const uint32_t *>(qp + 128 + 32 * n + 16 * h + 4 * kq);
+        }
+        r.sc = *reinterpret_cast<const uint4 *>(w.s + blk * 16);
+        r.d = *reinterpret_cast<const unsigned short *>(w.d + blk * 2);
+    }
+    __device__ static h4_t b(const Regs &r, int G) {
+        const int n = G >> 3, t = (G >> 1) & 3, h = G & 1, nh = 2 * n + h;
+        const uint32_t ql = (t & 1) ? r.qb[nh] : r.qa[nh];
+        const uint32_t v = ((ql >> (4 * (t >> 1))) & 0x0F0F0F0Fu) | (((r.qh[nh] >> (2 * t)) & 0x03030303u) << 4);
+        const h2_t off = {_Float16(1056), _Float16(1056)};  // 1024 + 32
+        return __builtin_bit_cast(h4_t, bytes_to_h4(v, off));
+    }
+    __device__ static void scale(const Regs &r, int G, float &sc, float &mn) {
+        const uint32_t wv = G < 8 ? (G < 4 ? r.sc.x : r.sc.y) : (G < 12 ? r.sc.z : r.sc.w);
+        sc = h2f(r.d) * float(int8_t(wv >> (8 * (G & 3))));
+        mn = 0.f;
+    }
+};
+
+// q8_0: 8 blocks of 32 per step, int8 values (q ^ 0x80 = q + 128 as a byte).
+template <>
+struct MW<GGML_Q8_0> {
+    static constexpr int SLICES = 8, SK = 32;
+    static constexpr bool MIN = false;
+    struct Regs {
+        uint2 q[8];
+        uint4 d;  // 8 f16 scales
+    };
+    __device__ static void load(const WPtr &w, int row, int kb, int kq, Regs &r) {
+        const uint8_t *qp = w.q + size_t(row) * w.K + size_t(kb) * 256 + 8 * kq;
+#pragma unroll
+        for (int b = 0; b < 8; ++b) r.q[b] = *reinterpret_cast<const uint2 *>(qp + 32 * b);
+        r.d = *reinterpret_cast<const uint4 *>(w.d + (size_t(row) * (w.K >> 5) + size_t(kb) * 8) * 2);
+    }
+    __device__ static h8_t b(const Regs &r, int s) {
+        const h2_t off = {_Float16(1152), _Float16(1152)};  // 1024 + 128
+        const uint2 lo = bytes_to_h4(r.q[s].x ^ 0x80808080u, off), hi = bytes_to_h4(r.q[s].y ^ 0x80808080u, off);
+        return __builtin_bit_cast(h8_t, make_uint4(lo.x, lo.y, hi.x, hi.y));
+    }
+    __device__ static void scale(const Regs &r, int s, float &sc, float &mn) {
+        const uint32_t wv = s < 4 ? (s < 2 ? r.d.x : r.d.y) : (s < 6 ? r.d.z : r.d.w);
+        sc = h2f(wv >> (16 * (s & 1)));
+        mn = 0.f;
+    }
+};
+
+// f16 weights: used as they are.
+template <>
+struct MW<GGML_F16> {
+    static constexpr int SLICES = 8, SK = 32;
+    static constexpr bool MIN = false;
+    struct Regs {
+        uint4 q[8];
+    };
+    __device__ static void load(const WPtr &w, int row, int kb, int kq, Regs &r) {
+        const uint8_t *qp = w.q + (size_t(row) * w.K + size_t(kb) * 256 + 8 * kq) * 2;
+#pragma unroll
+        for (int s = 0; s < 8; ++s) r.q[s] = *reinterpret_cast<const uint4 *>(qp + 64 * s);
+    }
+    __device__ static h8_t b(const Regs &r, int s) { return __builtin_bit_cast(h8_t, r.q[s]); }
+    __device__ static void scale(const Regs &, int, float &sc, float &mn) {
+        sc = 1.f;
+        mn = 0.f;
+    }
+};
+
+}  // namespace mlg

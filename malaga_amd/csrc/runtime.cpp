@@ -368,6 +368,8 @@ void Model::load(const std::string &path) {
     no_fuse_ = nf && *nf && std::string(nf) != "0";
     const char *sc = std::getenv("MALAGA_SPLIT_CROSS_STEP");
     split_cross_ = sc && *sc && std::string(sc) != "0";
+    const char *sk = std::getenv("MALAGA_SPLIT_K_STEP");
+    split_k_step_ = sk && *sk && std::string(sk) != "0";
     const int d = cfg.d_model;
     if (d <= 0 || d % cfg.decoder_heads || d % cfg.encoder_heads || d > 4096 || d % 16)
         fail(ERR_UNSUPPORTED, "unsupported d_model " + std::to_string(d));
@@ -665,6 +667,8 @@ std::unique_ptr<StaticState> Model::new_state(int b, int s, int m, bool logits, 
         st->part = static_cast<float *>(get(size_t(H) * b * d * 4, "attention partial sums"));
         st->part2 = static_cast<float *>(get(size_t(H) * b * d * 4, "cross attention partial sums"));
     }
+    if (!st->fused && dgemm_step_ok(b))
+        st->lnstat = static_cast<double *>(get(size_t(d / 16) * b * 2 * sizeof(double), "LayerNorm statistics"));
     st->h = static_cast<float *>(get(size_t(b) * d * 4, "h"));
     st->y = static_cast<float *>(get(size_t(b) * d * 4, "y"));
     st->att = static_cast<float *>(get(size_t(b) * d * 4, "att"));
@@ -872,6 +876,10 @@ void Model::step(StaticState &st, bool greedy_mode, int mask_id) {
         lm_head(st, greedy_mode, mask_id, fold ? x : nullptr);
         return;
     }
+    if (st.lnstat) {
+        step_dgemm(st, greedy_mode, mask_id);
+        return;
+    }
     hipStream_t s = ctx->stream;
     const int B = st.b, d = cfg.d_model, H = cfg.decoder_heads, hd = d / H;
     const SrcEmb src = st.sl ? SrcEmb{st.src_emb, st.src_row, st.s} : SrcEmb{};
@@ -910,6 +918,53 @@ void Model::step(StaticState &st, bool greedy_mode, int mask_id) {
         project_residual_ln(l.down, st.u, i + 1 < dec.size() ? dec[i + 1].attn_norm : dec_norm);
     }
     // st.h is dec_norm(x): tied LM head
+    lm_head(st, greedy_mode, mask_id);
+}
+
+bool Model::dgemm_step_ok(int b) const {
+    // LayerNorm and QKV projections take K = d_model in one K block per wave: d <= 2048
+    if (split_k_step_ || dec.empty() || b > kDgemmMaxRows || cfg.d_model % 16 || cfg.d_model > 2048) return false;
+    for (const DecLayer &l : dec) {
+        if (b <= gemv_max_batch(l.qkv.w)) return false;  // the register GEMVs serve small batches
+        for (const Linear *lin : {&l.qkv, &l.out, &l.cross_q, &l.cross_out, &l.up, &l.down})
+            if (!dgemm_supported(lin->w, b)) return false;
+    }
+    return true;
+}
+
+// src/model.rs:552-612 for batches of 5..64 rows: eight launches per layer, six decode
+// GEMMs (k_dgemm.hip) and the two attentions.  The LayerNorms live in the GEMMs: each
+// projection that adds to the residual stream x also leaves the new rows' statistics in
+// st.lnstat, and the next projection that takes LayerNorm(x) normalizes x as it loads it.
+void Model::step_dgemm(StaticState &st, bool greedy_mode, int mask_id) {
+    hipStream_t s = ctx->stream;
+    const int B = st.b, d = cfg.d_model, H = cfg.decoder_heads, hd = d / H, f = cfg.decoder_ffn;
+    const SrcEmb src = st.sl ? SrcEmb{st.src_emb, st.src_row, st.s} : SrcEmb{};
+    // x = embedding + position, h = LayerNorm(x) with layer 0's attn_norm
+    check_hip(embed_pos_ln(st.sl ? st.sl->head : embed, st.sl ? st.sl_row : st.ids, B, pos, st.step,
+                           uint32_t(cfg.pad_token_id + 1), embed_scale, dec[0].attn_norm.g, dec[0].attn_norm.b,
+                           kLnEps, st.x, st.h, s, src),
+              "embed_pos_ln");
+    auto ln = [&](const LNorm &n) { return DgemmLn{st.lnstat, n.g, n.b, kLnEps}; };
+    for (size_t i = 0; i < dec.size(); ++i) {
+        const DecLayer &l = dec[i];
+        const DgemmLn ln_attn = ln(l.attn_norm), ln_cross = ln(l.cross_norm), ln_ffn = ln(l.ffn_norm);
+        check_hip(dgemm_qkv(l.qkv.w, i == 0 ? st.h : st.x, d, B, i == 0 ? nullptr : &ln_attn, l.qkv.b, H, hd, st.m,
+                            st.step, st.q, st.kc[i], st.vc[i], s),
+                  "dgemm_qkv");
+        // att and u travel as split f16 hi / lo planes (the A-operand form of the GEMMs)
+        check_hip(attn_decode(st.q, st.kc[i], st.vc[i], B, H, hd, st.m, nullptr, st.step, st.att, s, st.rows, true),
+                  "attn");
+        check_hip(dgemm_resid(l.out.w, st.att, d, B, l.out.b, st.x, st.lnstat, s, true), "dgemm_out");
+        check_hip(dgemm_store(l.cross_q.w, st.x, d, B, &ln_cross, l.cross_q.b, false, st.q, d, s), "dgemm_cross_q");
+        check_hip(attn_decode(st.q, st.ck[i], st.cv[i], B, H, hd, st.s, st.lens, nullptr, st.att, s, nullptr, true),
+                  "attn");
+        check_hip(dgemm_resid(l.cross_out.w, st.att, d, B, l.cross_out.b, st.x, st.lnstat, s, true), "dgemm_cross_out");
+        check_hip(dgemm_store(l.up.w, st.x, d, B, &ln_ffn, l.up.b, true, st.u, f, s, true), "dgemm_up");
+        check_hip(dgemm_resid(l.down.w, st.u, f, B, l.down.b, st.x, st.lnstat, s, true), "dgemm_down");
+    }
+    // st.h = dec_norm(x): tied LM head
+    check_hip(layernorm(st.x, B, d, dec_norm.g, dec_norm.b, kLnEps, st.h, s), "layernorm");
     lm_head(st, greedy_mode, mask_id);
 }
 

@@ -131,6 +131,10 @@ struct StaticState {
     float *logits = nullptr, *pv = nullptr;
     uint32_t *pi = nullptr;
     int parts = 0;
+    // decode-GEMM step (batches of 5..64 rows): [d / 16][b][2] f64 sums of the residual
+    // stream and its squares per 16 columns, written with x by every projection that adds
+    // to it and read by the next LayerNorm (null: the split-K step)
+    double *lnstat = nullptr;
     size_t bytes = 0;
     std::vector<void *> owned;
     ~StaticState();
@@ -254,6 +258,11 @@ class Model {
     float *step_fused(StaticState &st, bool final_ln = true);
     // ln_x: x of the final LayerNorm when the head computes it (step_fused(st, false))
     void lm_head(StaticState &st, bool greedy_mode, int mask_id, const float *ln_x = nullptr);
+    // batches of 5..64 rows: eight launches per layer (decode GEMMs with the LayerNorms
+    // folded in, k_dgemm.hip); false when a matrix or the batch does not fit them
+    bool dgemm_step_ok(int b) const;
+    void step_dgemm(StaticState &st, bool greedy_mode, int mask_id);
+    bool split_k_step_ = false;  // MALAGA_SPLIT_K_STEP=1: batches > 4 keep the split-K GEMMs
     bool no_fuse_ = false;  // MALAGA_NO_FUSED_STEP=1 forces the unfused step
     bool split_cross_ = false;  // MALAGA_SPLIT_CROSS_STEP=1: cross_q and cross attention as two launches
 };

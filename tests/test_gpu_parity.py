@@ -278,3 +278,34 @@ def test_config5_shapes_batch64(model_dir, models):
     # batch of 3: the fused step at d = 2048 (hd = 128, head groups of 2)
     want3, gap3 = orc.translate_batch(src[:3], 4001, kv_f16=True, max_new_tokens=6)
     assert gpu.generate(src[:3], 4001, M.GenOptions(max_new_tokens=6)) == want3, f"min top-2 gap {gap3}"
+
+
+@pytest.mark.parametrize("preset", ["q4_k_m", "q6_k", "q8_0"])
+def test_decode_gemm_step_equals_split_k_step(kq_gguf, models, preset):
+    """Batches of 5..64 rows run the decode GEMMs (k_dgemm.hip: LayerNorm statistics
+    carried with the residual stream, no split K); MALAGA_SPLIT_K_STEP=1 keeps the
+    split-K GEMMs with their reduction kernels.  Same tokens; logits within the f32
+    reordering of the sums (plus f16 K/V rounding flips, as for the fused step)."""
+    import os
+
+    gpu, orc = models(kq_gguf(preset))
+    os.environ["MALAGA_SPLIT_K_STEP"] = "1"
+    try:
+        split = M.Translator.load(kq_gguf(preset))
+    finally:
+        del os.environ["MALAGA_SPLIT_K_STEP"]
+    rng = np.random.default_rng(400)
+    try:
+        for nb in (5, 33, 64):
+            src = [[997] + rng.integers(4, 990, int(n)).tolist() + [2] for n in rng.integers(2, 40, nb)]
+            opts = M.GenOptions(max_new_tokens=8, max_batch=64)
+            assert gpu.generate(src, 998, opts) == split.generate(src, 998, opts)
+            T = 6
+            tgt = np.zeros((nb, T), np.uint32)
+            tgt[:, 0], tgt[:, 1] = 2, 998
+            tgt[:, 2:] = rng.integers(4, 990, (nb, T - 2))
+            a, b = gpu.teacher_forced_logits(src, tgt), split.teacher_forced_logits(src, tgt)
+            assert np.abs(a - b).max() < 1e-3
+            assert np.abs(a - orc.teacher_forced_logits(src, tgt, kv_f16=True)).max() < 2e-3
+    finally:
+        split.close()
