@@ -592,8 +592,10 @@ struct NoPre {
 // xr and may use workgroup barriers (every thread of the workgroup must call
 // this function).
 // L2 > 0: g.lpr_log2 known at compile time (static lane-group reductions).
-template <int T, int B, int CPL, bool NT = false, int G = 2, bool LM = false, int L2 = 0, class XR, class PreF,
-          class Pro, class Epi>
+// DEPTH: steps of weights a wave keeps requested (2, or 3 for the long LM-head stream:
+// more bytes in flight per wave at the same occupancy).
+template <int T, int B, int CPL, bool NT = false, int G = 2, bool LM = false, int L2 = 0, int DEPTH = 2, class XR,
+          class PreF, class Pro, class Epi>
 __device__ __forceinline__ void gemv_rows(const WPtr &w, const GemvGeom &g, XR (&xr)[CPL], int gwave, int nwaves,
                                           PreF &&pre, Pro &&prologue, Epi &epi, const float *bias = nullptr,
                                           int nt_from = 0) {
@@ -641,6 +643,66 @@ __device__ __forceinline__ void gemv_rows(const WPtr &w, const GemvGeom &g, XR (
     };
 
     const int stride = G * nwaves;
+    if constexpr (DEPTH > 2) {
+        // step k of this wave: row group gwave + k stride, for k < nst.  Ring of DEPTH
+        // buffers: the compute of step k is followed by the request of step k + DEPTH
+        // into its buffer; the last DEPTH steps request nothing.  With NT, one cache
+        // policy per wave (waves gwave < nt_from nwaves / N cached, the rest
+        // non-temporal: the same share of rows as a row threshold); that choice and
+        // whether there is a bias are made once, outside the loop, so that no load sits
+        // behind a branch and every compute waits for its own step only.
+        const int groups = (w.N + rpw - 1) / rpw;
+        const int nst = gwave < groups ? (groups - gwave + stride - 1) / stride : 0;  // wave-uniform
+        Raw<T> R[DEPTH][G][CPL];
+        float bv[DEPTH][G];
+        auto ring = [&](auto ntc, auto biasc) {
+            constexpr bool NTW = decltype(ntc)::value, BIAS = decltype(biasc)::value;
+            auto load = [&](int rg, Raw<T>(&r)[G][CPL], float(&b)[G]) {
+#pragma unroll
+                for (int u = 0; u < G; ++u) {
+                    const int row = min((rg + u * nwaves) * rpw + grp, w.N - 1);
+#pragma unroll
+                    for (int t = 0; t < CPL; ++t) load_chunk<T, NTW, LM>(w, row, cidx[t], r[u][t]);
+                    b[u] = BIAS ? bias[row] : 0.f;
+                }
+            };
+            pre();
+            __builtin_amdgcn_sched_barrier(0);
+            static_for<0, DEPTH>([&](auto jc) {
+                constexpr int j = decltype(jc)::value;
+                if (j < nst) load(gwave + j * stride, R[j], bv[j]);
+            });
+            __builtin_amdgcn_sched_barrier(0);
+            prologue();
+            if (nst == 0) return;
+            int k = 0;
+            for (; k + 2 * DEPTH <= nst; k += DEPTH)  // every request of this round exists
+                static_for<0, DEPTH>([&](auto jc) {
+                    constexpr int j = decltype(jc)::value;
+                    compute_step(gwave + (k + j) * stride, R[j], bv[j]);
+                    load(gwave + (k + j + DEPTH) * stride, R[j], bv[j]);
+                });
+            static_for<0, DEPTH>([&](auto jc) {  // fewer than 2 DEPTH steps left
+                constexpr int j = decltype(jc)::value;
+                if (k + j < nst) {
+                    compute_step(gwave + (k + j) * stride, R[j], bv[j]);
+                    if (k + j + DEPTH < nst) load(gwave + (k + j + DEPTH) * stride, R[j], bv[j]);
+                }
+            });
+            static_for<0, DEPTH>([&](auto jc) {
+                constexpr int j = decltype(jc)::value;
+                if (k + DEPTH + j < nst) compute_step(gwave + (k + DEPTH + j) * stride, R[j], bv[j]);
+            });
+        };
+        using yes = std::integral_constant<bool, true>;
+        using no = std::integral_constant<bool, false>;
+        const bool ntw = NT && int64_t(gwave) * w.N >= int64_t(nt_from) * nwaves;  // wave-uniform
+        if (ntw)
+            bias ? ring(yes{}, yes{}) : ring(yes{}, no{});
+        else
+            bias ? ring(no{}, yes{}) : ring(no{}, no{});
+        return;
+    }
     int rg = gwave;
     const bool any = rg * rpw < w.N;  // wave-uniform
     Raw<T> A[G][CPL], Bf[G][CPL];

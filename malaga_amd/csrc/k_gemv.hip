@@ -56,6 +56,9 @@ struct ArgmaxEpi {
 // (limb x, one resident round of workgroups); MODE 1: LM head with argmax partials,
 // mostly non-temporal weights.  One row group per wave step (G = 1) in all three:
 // fewer registers, more waves per SIMD (measured faster than G = 2 for the large ones).
+// LM head: three steps of weights requested per wave (two for the other GEMVs)
+constexpr int kLmHeadDepth = 3;
+
 template <int T, int MODE>
 constexpr bool kGemvLimbs = MODE != 0 && kLimbX<T>;  // large matrices: limb x (gemv_core.hpp)
 
@@ -99,7 +102,8 @@ __global__ __launch_bounds__(256) void k_gemv(GemvArgs a) {
             gemv_load_x<T, B, CPL>(a.x, a.ldx, a.nb, a.g, cl, xr);
         }
     };
-    const int gwave = blockIdx.x * 4 + (threadIdx.x >> 6), nwaves = gridDim.x * 4;
+    // a scalar: the per-step branches on it stay uniform (no divergent load paths)
+    const int gwave = __builtin_amdgcn_readfirstlane(blockIdx.x * 4 + (threadIdx.x >> 6)), nwaves = gridDim.x * 4;
     if constexpr (MODE == 0) {
         StoreEpi<B> epi{a};
         gemv_rows<T, B, CPL, false, 1, LM>(a.w, a.g, xr, gwave, nwaves, NoPre{}, load_x, epi, a.bias);
@@ -115,8 +119,8 @@ __global__ __launch_bounds__(256) void k_gemv(GemvArgs a) {
         }
         // rows >= nt_from non-temporal: the 215 MB stream then evicts less of the layer
         // weights from the MALL between steps (measured: -20 us per 600M step)
-        gemv_rows<T, B, CPL, true, 1, LM, L2>(a.w, a.g, xr, gwave, nwaves, NoPre{}, load_x, epi, a.bias,
-                                              a.nt_from);
+        gemv_rows<T, B, CPL, true, 1, LM, L2, kLmHeadDepth>(a.w, a.g, xr, gwave, nwaves, NoPre{}, load_x, epi,
+                                                            a.bias, a.nt_from);
         __shared__ float sv[4][B];
         __shared__ uint32_t si[4][B];
         const int wv = threadIdx.x >> 6;
