@@ -522,10 +522,10 @@ __global__ __launch_bounds__(kRxWaves * 64) void k_mfma_rx(RxArgs a) {
     const int kq = lane >> 4, ln = lane & 15;
     const int nsteps = K / kStep;
     const int ngroups = (a.w.N + 16 * kRxNT - 1) / (16 * kRxNT);  // groups of kRxNT 16-row tiles
-    const int gw = blockIdx.x * kRxWaves + (t >> 6), nw = gridDim.x * kRxWaves;
+    // a scalar: the job loop's bounds stay uniform (no divergent load paths)
+    const int gw = __builtin_amdgcn_readfirstlane(blockIdx.x * kRxWaves + (t >> 6)), nw = gridDim.x * kRxWaves;
     const int njobs = gw < ngroups ? ((ngroups - 1 - gw) / nw + 1) * nsteps : 0;  // (group, step) pairs of this wave
 
-    // the first kRxDepth (group, K-step) jobs of W in flight before X is staged
     typename W::Regs ring[kRxDepth][kRxNT];
     auto job_base = [&](int j) { return (gw + (j / nsteps) * nw) * 16 * kRxNT; };
     auto load_job = [&](int j, typename W::Regs (&r)[kRxNT]) {
@@ -533,9 +533,6 @@ __global__ __launch_bounds__(kRxWaves * 64) void k_mfma_rx(RxArgs a) {
         for (int nt = 0; nt < kRxNT; ++nt)
             W::load(a.w, min(job_base(j) + nt * 16 + ln, a.w.N - 1), j % nsteps, kq, r[nt]);
     };
-#pragma unroll
-    for (int u = 0; u < kRxDepth; ++u)
-        if (u < njobs) load_job(u, ring[u]);
 
     // stage X: chunks of 16 values, up to 4 per thread in flight
     {
@@ -576,6 +573,17 @@ __global__ __launch_bounds__(kRxWaves * 64) void k_mfma_rx(RxArgs a) {
         }
     }
     __syncthreads();
+    // the first kRxDepth (group, K-step) jobs of W: requested once X is staged, so that
+    // the job loop is entered with the same loads in flight as on every later trip
+    // (requested before the staging, they made the compiler wait for every load at the
+    // top of each job: 2 of the ring's jobs in flight became 0)
+    // (unconditional: a job past this wave's last reads a clamped row and is never used;
+    // a skipped request would leave the compiler unsure how many loads follow each one)
+#pragma unroll
+    for (int u = 0; u < kRxDepth; ++u) {
+        load_job(u, ring[u]);
+        __builtin_amdgcn_sched_barrier(0);  // jobs requested in order
+    }
 
     f4_t acc[MT][kRxNT];
 #pragma unroll
@@ -685,7 +693,9 @@ __global__ __launch_bounds__(kRxWaves * 64) void k_mfma_rx(RxArgs a) {
 #pragma unroll
         for (int u = 0; u < kRxDepth; ++u) {
             job(j0 + u, ring[u]);
+            __builtin_amdgcn_sched_barrier(0);
             load_job(j0 + u + kRxDepth, ring[u]);
+            __builtin_amdgcn_sched_barrier(0);
         }
     }
     for (; j0 < njobs; j0 += kRxDepth) {
