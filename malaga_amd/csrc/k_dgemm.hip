@@ -15,18 +15,19 @@
 // unconditional (rows past M read row M - 1 and are never stored) and the wave index is a
 // scalar, so that slice s waits for its own fragment and nothing later.
 //
+// Inputs are in fragment order (frag_index, device.hpp: whole cache lines per load),
+// except PRO_RAW (row-major, the first layer's LayerNorm output).
+//
 // PRO_SPLIT: the input arrives split into f16 hi = f16(x) and lo = f16(x - hi), the form
 // the A operand needs, written that way by its producer (the FFN-up projection, the
-// attention), so no conversion is left here.  Each 4 values of a row are stored as
-// [hi0..hi3 | lo0..lo3] in the 16 bytes their f32 values would take, so the loads are
-// those of an f32 input; producers write each such group with one 16-byte store.
+// attention), so no conversion is left here.
 //
-// PRO_LN: the input is LayerNorm(x) of the residual stream, normalized as the fragments
-// arrive.  The row statistics are not recomputed: the launch that last wrote x
+// PRO_LN: the input is LayerNorm(x) of the residual stream (fragment order, f32),
+// normalized as the fragments arrive.  The row statistics are not recomputed: the launch that last wrote x
 // (EPI_RESID) left the f64 sums of x and x^2 of every 16 columns beside it, and the
 // prologue adds those P = K / 16 partials per row in a fixed order.
 //
-// Epilogues: EPI_STORE y = x W^T + bias (ReLU), f32 or split into hi and lo planes; EPI_RESID x += x_in W^T + bias in place,
+// Epilogues: EPI_STORE y = x W^T + bias (ReLU), f32 rows or split fragments; EPI_RESID x += x_in W^T + bias in place,
 // plus the statistics of the new x; EPI_QKV q (f32) and K/V (f16, cache slot *step).
 #include "kernels.hpp"
 #include "mfma_core.hpp"
@@ -44,9 +45,9 @@ struct DArgs {
     const float *gamma, *beta;
     float eps;
     const float *bias;
-    float *y;  // EPI_STORE [M][ldy] f32 (split rows if split_out)
-    int ldy, relu, split_out;
-    float *xres;        // EPI_RESID: the residual stream [M][N]
+    float *y;  // EPI_STORE [M][ldy] f32 rows, or split fragments (frag_out)
+    int ldy, relu, frag_out;
+    float *xres;        // EPI_RESID: the residual stream [M][N], fragment order
     double *stats_out;  // EPI_RESID: [N / 16][M][2]
     float *q;           // EPI_QKV: q [M][d], caches [M][H][slots][hd]
     __half *kc, *vc;
@@ -108,7 +109,7 @@ __global__ __launch_bounds__(kDgMaxNW * 64) void k_dgemm(DArgs a) {
         const int o = t + 256 * u, omc = min(m0 + o / TN, a.M - 1), onc = min(n0 + o % TN, a.w.N - 1);
         bias_v[u] = a.bias ? a.bias[onc] : 0.f;
         xold[u] = 0.f;
-        if constexpr (EPI == EPI_RESID) xold[u] = a.xres[size_t(omc) * a.w.N + onc];
+        if constexpr (EPI == EPI_RESID) xold[u] = a.xres[frag_index(omc, onc & ~3, a.w.N) * 4 + (onc & 3)];
     }
 
     using WR = typename W::Regs;
@@ -122,15 +123,21 @@ __global__ __launch_bounds__(kDgMaxNW * 64) void k_dgemm(DArgs a) {
     }
 
     // X fragment of (block kb, slice s): row m0 + ln, columns kb 256 + s SK + kq SK / 4
-    // (PRO_SPLIT: the same bytes hold [hi0..hi3 | lo0..lo3] per 4 columns)
+    // (fragment order: the tile's padding rows are stored)
     const float *xrow = a.x + size_t(min(m0 + ln, a.M - 1)) * a.ldx;
+    const float4 *xfr = reinterpret_cast<const float4 *>(a.x);
     struct Frag {
         float4 x[XQ];
     };
     auto load_x = [&](int kb, int s, Frag &f) {
-        const float4 *src = reinterpret_cast<const float4 *>(xrow + kb * kStep + s * SK + kq * (SK / 4));
+        if constexpr (PRO != PRO_RAW) {
 #pragma unroll
-        for (int i = 0; i < XQ; ++i) f.x[i] = src[i];
+            for (int i = 0; i < XQ; ++i) f.x[i] = xfr[frag_index(m0 + ln, kb * kStep + s * SK + kq * (SK / 4) + 4 * i, K)];
+        } else {
+            const float4 *src = reinterpret_cast<const float4 *>(xrow + kb * kStep + s * SK + kq * (SK / 4));
+#pragma unroll
+            for (int i = 0; i < XQ; ++i) f.x[i] = src[i];
+        }
     };
     // The (block, slice) items of this wave in order, D fragments in flight: item i uses
     // slot i % D, refilled with item i + D as soon as it is used.
@@ -290,9 +297,9 @@ __global__ __launch_bounds__(kDgMaxNW * 64) void k_dgemm(DArgs a) {
         v += bias_v[u];
         if constexpr (EPI == EPI_STORE) {
             const float r = a.relu ? fmaxf(v, 0.f) : v;
-            if (a.split_out) {  // kernel argument: every lane takes this branch
+            if (a.frag_out) {  // kernel argument: every lane takes this branch
                 // lanes 4g .. 4g + 3 hold 4 consecutive columns of one row; the first
-                // writes their [hi0..hi3 | lo0..lo3] as one 16-byte store
+                // writes their [hi0..hi3 | lo0..lo3] fragment with one 16-byte store
                 h4_t hv, lv;
 #pragma unroll
                 for (int j = 0; j < 4; ++j) {
@@ -302,7 +309,7 @@ __global__ __launch_bounds__(kDgMaxNW * 64) void k_dgemm(DArgs a) {
                 }
                 if (own && (c & 3) == 0) {
                     const uint2 hb = __builtin_bit_cast(uint2, hv), lb = __builtin_bit_cast(uint2, lv);
-                    *reinterpret_cast<uint4 *>(a.y + size_t(om) * a.ldy + on) = make_uint4(hb.x, hb.y, lb.x, lb.y);
+                    reinterpret_cast<uint4 *>(a.y)[frag_index(om, on, a.w.N)] = make_uint4(hb.x, hb.y, lb.x, lb.y);
                 }
             } else if (own) {
                 a.y[size_t(om) * a.ldy + on] = r;
@@ -325,7 +332,7 @@ __global__ __launch_bounds__(kDgMaxNW * 64) void k_dgemm(DArgs a) {
             }
         } else {  // EPI_RESID: x += y, and the new x's sums per row and 16 columns (16 lanes)
             const float xn = own ? xold[u] + v : 0.f;
-            if (own) a.xres[size_t(om) * a.w.N + on] = xn;
+            if (own) a.xres[frag_index(om, on & ~3, a.w.N) * 4 + (on & 3)] = xn;
             const double s1 = group_sum_f64<16>(double(xn)), s2 = group_sum_f64<16>(double(xn) * double(xn));
             if (own && (c & 15) == 0) {
                 double *sp_out = a.stats_out + (size_t(on >> 4) * a.M + om) * 2;
@@ -421,11 +428,11 @@ bool dgemm_supported(const DevMatrix &w, int M) {
 hipError_t dgemm_store(const DevMatrix &w, const float *x, int ldx, int M, const DgemmLn *ln, const float *bias,
                        bool relu, float *y, int ldy, hipStream_t st, bool y_split) {
     if (!dgemm_args_ok(w, x, ldx, M, ln) || !y || ldy < w.N) return hipErrorInvalidValue;
-    // split rows are written 4 columns (16 bytes) at a time
-    if (y_split && (w.N % 4 || ldy % 4 || reinterpret_cast<uintptr_t>(y) % 16)) return hipErrorInvalidValue;
+    // split fragments: 16-byte aligned, whole slices of 16 columns
+    if (y_split && (w.N % 16 || reinterpret_cast<uintptr_t>(y) % 16)) return hipErrorInvalidValue;
     DArgs a = dargs(w, x, ldx, M, ln, bias);
     a.y = y;
-    a.split_out = y_split ? 1 : 0;
+    a.frag_out = y_split ? 1 : 0;
     a.ldy = ldy;
     a.relu = relu ? 1 : 0;
     return ln ? launch_dgemm_t<PRO_LN, EPI_STORE>(w, a, st) : launch_dgemm_t<PRO_RAW, EPI_STORE>(w, a, st);

@@ -15,7 +15,8 @@ namespace {
 // ---- rows: one wave per row, four rows per workgroup ----------------------------
 
 // LayerNorm of rows (RESID: x += y first, stored back; the normalized row goes to h).
-template <int NJ, bool RESID>
+// FRAG: x in fragment order (frag_index), h row-major.
+template <int NJ, bool RESID, bool FRAG = false>
 __global__ __launch_bounds__(256) void k_rows_ln(float *x, const float *y, int rows, int d, const float *g,
                                                  const float *b, float eps, float *h) {
     const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
@@ -23,6 +24,7 @@ __global__ __launch_bounds__(256) void k_rows_ln(float *x, const float *y, int r
     float4 *xr = reinterpret_cast<float4 *>(x + size_t(row) * d);
     const float4 *yr = reinterpret_cast<const float4 *>(y + size_t(row) * d);
     auto form = [&](int f) {
+        if constexpr (FRAG) return reinterpret_cast<const float4 *>(x)[frag_index(row, 4 * f, d)];
         float4 v = xr[f];
         if constexpr (RESID) add4(v, yr[f]);
         return v;
@@ -53,7 +55,7 @@ __global__ __launch_bounds__(256) void k_embed_pos_ln(const uint8_t *q, const ui
                                                       const uint32_t *ids, int rows, const float *pos,
                                                       const uint32_t *step, uint32_t base, float scale, int d,
                                                       uint32_t last, const float *g, const float *b, float eps,
-                                                      float *x, float *h, SrcEmb src) {
+                                                      float *x, float *h, SrcEmb src, int x_frag) {
     const int row = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
     if (row >= rows) return;  // wave-uniform
     const uint32_t sr = src.row ? src.row[row] : kNoRow;  // wave-uniform
@@ -91,7 +93,10 @@ __global__ __launch_bounds__(256) void k_embed_pos_ln(const uint8_t *q, const ui
             const float4 p = ld4(pr, 4 * c + u);
             v[j][u] = make_float4(w[j][4 * u] * scale + p.x, w[j][4 * u + 1] * scale + p.y,
                                   w[j][4 * u + 2] * scale + p.z, w[j][4 * u + 3] * scale + p.w);
-            xr[4 * c + u] = v[j][u];
+            if (x_frag)  // kernel argument
+                reinterpret_cast<float4 *>(x)[frag_index(row, 4 * (4 * c + u), d)] = v[j][u];
+            else
+                xr[4 * c + u] = v[j][u];
             ln_acc(v[j][u], s1, s2);
         }
     }
@@ -455,8 +460,7 @@ __global__ __launch_bounds__(256) void k_attn_waves(const float *q, const __half
     __builtin_amdgcn_s_waitcnt(0xc07f);
     __builtin_amdgcn_wave_barrier();
     if (out_split) {
-        // per 4 values f16 hi0..hi3, lo0..lo3 in the 16 bytes of their f32 values: one
-        // lane per 4 values, one whole store each
+        // split fragments [hi0..hi3 | lo0..lo3]: one lane per 4 values, one whole store each
         for (int e4 = lane; e4 < HD / 4; e4 += 64) {
             h4_t hv, lv;
 #pragma unroll
@@ -470,7 +474,7 @@ __global__ __launch_bounds__(256) void k_attn_waves(const float *q, const __half
                 lv[j] = _Float16(o - float(hv[j]));
             }
             const uint2 hb = __builtin_bit_cast(uint2, hv), lb = __builtin_bit_cast(uint2, lv);
-            reinterpret_cast<uint4 *>(out + size_t(bi) * d + hh * HD)[e4] = make_uint4(hb.x, hb.y, lb.x, lb.y);
+            reinterpret_cast<uint4 *>(out)[frag_index(bi, hh * HD + 4 * e4, d)] = make_uint4(hb.x, hb.y, lb.x, lb.y);
         }
         return;
     }
@@ -639,21 +643,22 @@ inline int embed_nc(int d) { return d <= 1024 ? 1 : d <= 2048 ? 2 : 4; }
 template <int T>
 hipError_t launch_embed_pos_ln(const DevMatrix &E, const uint32_t *ids, int rows, const float *pos,
                                const uint32_t *step, uint32_t base, float scale, const float *g, const float *b,
-                               float eps, float *x, float *h, hipStream_t st, const SrcEmb &src) {
+                               float eps, float *x, float *h, hipStream_t st, const SrcEmb &src, bool x_frag) {
     const dim3 grid(unsigned((rows + 3) / 4));
     const uint32_t last = uint32_t(E.N - 1);
+    const int xf = x_frag ? 1 : 0;
     switch (embed_nc(E.K)) {
     case 1:
         hipLaunchKernelGGL((k_embed_pos_ln<T, 1>), grid, dim3(256), 0, st, E.q, E.s, E.d, ids, rows, pos, step, base,
-                           scale, E.K, last, g, b, eps, x, h, src);
+                           scale, E.K, last, g, b, eps, x, h, src, xf);
         break;
     case 2:
         hipLaunchKernelGGL((k_embed_pos_ln<T, 2>), grid, dim3(256), 0, st, E.q, E.s, E.d, ids, rows, pos, step, base,
-                           scale, E.K, last, g, b, eps, x, h, src);
+                           scale, E.K, last, g, b, eps, x, h, src, xf);
         break;
     default:
         hipLaunchKernelGGL((k_embed_pos_ln<T, 4>), grid, dim3(256), 0, st, E.q, E.s, E.d, ids, rows, pos, step, base,
-                           scale, E.K, last, g, b, eps, x, h, src);
+                           scale, E.K, last, g, b, eps, x, h, src, xf);
     }
     return hipGetLastError();
 }
@@ -678,22 +683,27 @@ hipError_t launch_embed_pos_rows(const DevMatrix &E, const uint32_t *ids, const 
     return hipGetLastError();
 }
 
-template <bool RESID>
+template <bool RESID, bool FRAG = false>
 hipError_t launch_rows_ln(float *x, const float *y, int rows, int d, const float *g, const float *b, float eps,
                           float *h, hipStream_t st) {
-    if (d % 4 || d > kWaveLnMaxD) return hipErrorInvalidValue;
+    if (d % 4 || d > kWaveLnMaxD || (FRAG && d % 16)) return hipErrorInvalidValue;
     if (rows <= 0) return hipSuccess;
     const dim3 grid(unsigned((rows + 3) / 4));
     const int nj = (d + 255) / 256;
-    if (nj <= 1) hipLaunchKernelGGL((k_rows_ln<1, RESID>), grid, dim3(256), 0, st, x, y, rows, d, g, b, eps, h);
-    else if (nj <= 2) hipLaunchKernelGGL((k_rows_ln<2, RESID>), grid, dim3(256), 0, st, x, y, rows, d, g, b, eps, h);
-    else if (nj <= 4) hipLaunchKernelGGL((k_rows_ln<4, RESID>), grid, dim3(256), 0, st, x, y, rows, d, g, b, eps, h);
-    else if (nj <= 8) hipLaunchKernelGGL((k_rows_ln<8, RESID>), grid, dim3(256), 0, st, x, y, rows, d, g, b, eps, h);
-    else hipLaunchKernelGGL((k_rows_ln<16, RESID>), grid, dim3(256), 0, st, x, y, rows, d, g, b, eps, h);
+    if (nj <= 1) hipLaunchKernelGGL((k_rows_ln<1, RESID, FRAG>), grid, dim3(256), 0, st, x, y, rows, d, g, b, eps, h);
+    else if (nj <= 2) hipLaunchKernelGGL((k_rows_ln<2, RESID, FRAG>), grid, dim3(256), 0, st, x, y, rows, d, g, b, eps, h);
+    else if (nj <= 4) hipLaunchKernelGGL((k_rows_ln<4, RESID, FRAG>), grid, dim3(256), 0, st, x, y, rows, d, g, b, eps, h);
+    else if (nj <= 8) hipLaunchKernelGGL((k_rows_ln<8, RESID, FRAG>), grid, dim3(256), 0, st, x, y, rows, d, g, b, eps, h);
+    else hipLaunchKernelGGL((k_rows_ln<16, RESID, FRAG>), grid, dim3(256), 0, st, x, y, rows, d, g, b, eps, h);
     return hipGetLastError();
 }
 
 }  // namespace
+
+hipError_t layernorm_frag(const float *x, int rows, int d, const float *g, const float *b, float eps, float *out,
+                          hipStream_t st) {
+    return launch_rows_ln<false, true>(const_cast<float *>(x), nullptr, rows, d, g, b, eps, out, st);
+}
 
 hipError_t layernorm(const float *x, int rows, int d, const float *g, const float *b, float eps, float *out,
                      hipStream_t st) {
@@ -707,10 +717,11 @@ hipError_t residual_ln(float *x, const float *y, int rows, int d, const float *g
 
 hipError_t embed_pos_ln(const DevMatrix &E, const uint32_t *ids, int rows, const float *pos, const uint32_t *step,
                         uint32_t base, float scale, const float *g, const float *b, float eps, float *x, float *h,
-                        hipStream_t st, const SrcEmb &src) {
+                        hipStream_t st, const SrcEmb &src, bool x_frag) {
     if (E.K > kWaveLnMaxD || E.K % 16 || (src.row && (!src.emb || src.S < 1))) return hipErrorInvalidValue;
     if (rows <= 0) return hipSuccess;
-    MLG_DISPATCH_TYPE(E.type, launch_embed_pos_ln, E, ids, rows, pos, step, base, scale, g, b, eps, x, h, st, src)
+    MLG_DISPATCH_TYPE(E.type, launch_embed_pos_ln, E, ids, rows, pos, step, base, scale, g, b, eps, x, h, st, src,
+                      x_frag)
 }
 
 hipError_t embed_rows(const DevMatrix &E, const uint32_t *ids, int rows, float *out, hipStream_t st) {
@@ -751,6 +762,7 @@ hipError_t attn_decode(const float *q, const __half *K, const __half *V, int b, 
                        const uint32_t *lens, const uint32_t *step, float *out, hipStream_t st, const uint32_t *rows,
                        bool out_split) {
     if (b * H <= 0) return hipSuccess;
+    if (out_split && ((H * hd) % 16 || reinterpret_cast<uintptr_t>(out) % 16)) return hipErrorInvalidValue;
     const dim3 wgrid(unsigned((b * H + 3) / 4));
     switch (hd) {
 #define MLG_ATTN_WAVES(HD)                                                                                          \

@@ -83,7 +83,8 @@ hipError_t gemm_qkv(const DevMatrix &w, const float *X, int ldx, int M, const fl
 // ---- decode projections for batches of up to 64 rows, one launch each (k_dgemm.hip) ----
 constexpr int kDgemmMaxRows = 64;
 // Input LayerNorm from the statistics the residual stream's last writer left:
-// stats [K / 16][M][2] (f64 sums of x and x^2 per 16 columns), gamma/beta [K].
+// stats [K / 16][M][2] (f64 sums of x and x^2 per 16 columns), gamma/beta [K].  With a
+// DgemmLn, x is the residual stream in fragment order (frag_index, device.hpp).
 struct DgemmLn {
     const double *stats;
     const float *g, *b;
@@ -91,12 +92,13 @@ struct DgemmLn {
 };
 bool dgemm_supported(const DevMatrix &w, int M);
 // y[m][n] = (LN(x) or x)[m] . W[n] + bias[n], ReLU optional.  y_split: y is written as
-// split rows in the same bytes: per 4 columns f16 hi0..hi3 = f16(y) then lo0..lo3 =
-// f16(y - hi), the A-operand form of the decode GEMMs.
+// split fragments (frag_index, device.hpp), the A-operand form of the decode GEMMs; it
+// then holds (M padded to 16) x N floats.
 hipError_t dgemm_store(const DevMatrix &w, const float *x, int ldx, int M, const DgemmLn *ln, const float *bias,
                        bool relu, float *y, int ldy, hipStream_t st, bool y_split = false);
-// xres[m][n] += x[m] . W[n] + bias[n] in place (xres [M][N]), and stats_out [N / 16][M][2]
-// of the new rows.  x_split: x holds split rows (as y_split above).
+// xres[m][n] += x[m] . W[n] + bias[n] in place (xres: the residual stream, (M padded to
+// 16) x N floats in fragment order), and stats_out [N / 16][M][2] of the new rows.
+// x_split: x holds split fragments (else row-major f32 rows of ldx).
 hipError_t dgemm_resid(const DevMatrix &w, const float *x, int ldx, int M, const float *bias, float *xres,
                        double *stats_out, hipStream_t st, bool x_split = false);
 // The fused QKV projection: q [M][d] f32, K/V f16 into the caches [M][H][slots][hd] at *step.
@@ -114,6 +116,9 @@ hipError_t gemm_argmax(const DevMatrix &w, const float *X, int ldx, int M, int m
 // Row LayerNorm (biased variance): out = (x - mean) * rsqrt(var + eps) * g + b.
 hipError_t layernorm(const float *x, int rows, int d, const float *g, const float *b, float eps, float *out,
                      hipStream_t st);
+// The same with x in fragment order (frag_index, device.hpp; d % 16 == 0), out row-major.
+hipError_t layernorm_frag(const float *x, int rows, int d, const float *g, const float *b, float eps, float *out,
+                          hipStream_t st);
 // x = x + y ; h = LayerNorm(x).  (bias already added to y by the producer)
 hipError_t residual_ln(float *x, const float *y, int rows, int d, const float *g, const float *b, float eps, float *h,
                        hipStream_t st);
@@ -147,10 +152,11 @@ hipError_t source_logits(const float *h, const float *emb, const uint32_t *src_i
 hipError_t embed_rows(const DevMatrix &E, const uint32_t *ids, int rows, float *out, hipStream_t st);
 
 // Decoder input: x = dequant(E[ids[r]]) * scale + pos[*step + base]; h = LayerNorm(x).
-// src: rows whose input is a source-token embedding.
+// src: rows whose input is a source-token embedding.  x_frag: x in fragment order
+// (frag_index, device.hpp), h row-major.
 hipError_t embed_pos_ln(const DevMatrix &E, const uint32_t *ids, int rows, const float *pos, const uint32_t *step,
                         uint32_t base, float scale, const float *g, const float *b, float eps, float *x, float *h,
-                        hipStream_t st, const SrcEmb &src = SrcEmb{});
+                        hipStream_t st, const SrcEmb &src = SrcEmb{}, bool x_frag = false);
 // Encoder input rows: x[r] = dequant(E[ids[r]]) * scale + pos[pidx[r]].
 hipError_t embed_pos_rows(const DevMatrix &E, const uint32_t *ids, const uint32_t *pidx, int rows, const float *pos,
                           float scale, float *x, hipStream_t st);
@@ -165,8 +171,8 @@ hipError_t attn_decode(const float *q, const __half *K, const __half *V, int b, 
                        const uint32_t *lens, const uint32_t *step, float *out, hipStream_t st, const uint32_t *rows = nullptr,
                        bool out_split = false);
 // rows (optional, [b][L]): cache row holding slot j of row b (beam reordering without copies).
-// out_split: out is written as split rows (per 4 values f16 hi0..hi3, then lo0..lo3 =
-// f16(out - hi), in the bytes of the f32 row): the input form of the decode GEMMs' x_split.
+// out_split: out is written as split fragments (frag_index, device.hpp), the input form
+// of the decode GEMMs; out then holds (b padded to 16) x H*hd floats.
 // Encoder self-attention over f32 qkv [b*s][3d] (rows of sentence i are i*s..),
 // key j of row i valid iff j < lens[i].  out [b*s][d].
 hipError_t attn_prefill(const float *qkv, int b, int s, int H, int hd, const uint32_t *lens, float *out,

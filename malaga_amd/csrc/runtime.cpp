@@ -659,7 +659,10 @@ std::unique_ptr<StaticState> Model::new_state(int b, int s, int m, bool logits, 
         st->ck.push_back(cross_kv + 2 * i * cross_pair);
         st->cv.push_back(cross_kv + (2 * i + 1) * cross_pair);
     }
-    st->x = static_cast<float *>(get(size_t(b) * d * 4, "x"));
+    // rows padded to 16: the decode-GEMM step keeps x in fragment order (whole row tiles)
+    const size_t bp = size_t(b + 15) / 16 * 16;
+    st->x = static_cast<float *>(get(bp * d * 4, "x"));
+    check_hip(hipMemsetAsync(st->x, 0, bp * d * 4, ctx->stream), "memset");
     st->xb = static_cast<float *>(get(size_t(b) * d * 4, "x (second buffer)"));
     st->qc = static_cast<float *>(get(size_t(b) * d * 4, "cross q"));
     st->fused = fusable(b, m, s) && (!sl || step_embed_supported(dec[0].qkv.w.type, sl->head.type));
@@ -671,10 +674,14 @@ std::unique_ptr<StaticState> Model::new_state(int b, int s, int m, bool logits, 
         st->lnstat = static_cast<double *>(get(size_t(d / 16) * b * 2 * sizeof(double), "LayerNorm statistics"));
     st->h = static_cast<float *>(get(size_t(b) * d * 4, "h"));
     st->y = static_cast<float *>(get(size_t(b) * d * 4, "y"));
-    st->att = static_cast<float *>(get(size_t(b) * d * 4, "att"));
+    // att and u: rows padded to 16, zero-filled (the decode-GEMM step keeps them as split
+    // fragments, whose row tiles are stored whole)
+    st->att = static_cast<float *>(get(bp * d * 4, "att"));
     st->q = static_cast<float *>(get(size_t(b) * d * 4, "q"));
     st->qkv = static_cast<float *>(get(size_t(b) * 3 * d * 4, "qkv"));
-    st->u = static_cast<float *>(get(size_t(b) * cfg.decoder_ffn * 4, "ffn"));
+    st->u = static_cast<float *>(get(bp * cfg.decoder_ffn * 4, "ffn"));
+    check_hip(hipMemsetAsync(st->att, 0, bp * d * 4, ctx->stream), "memset");
+    check_hip(hipMemsetAsync(st->u, 0, bp * cfg.decoder_ffn * 4, ctx->stream), "memset");
     if (logits || b > gemv_max_batch(head))
         st->logits = static_cast<float *>(get(size_t(b) * (sl ? head.N : V) * 4, "logits"));
     if (sl) {  // src/graph.rs:76-79
@@ -940,10 +947,10 @@ void Model::step_dgemm(StaticState &st, bool greedy_mode, int mask_id) {
     hipStream_t s = ctx->stream;
     const int B = st.b, d = cfg.d_model, H = cfg.decoder_heads, hd = d / H, f = cfg.decoder_ffn;
     const SrcEmb src = st.sl ? SrcEmb{st.src_emb, st.src_row, st.s} : SrcEmb{};
-    // x = embedding + position, h = LayerNorm(x) with layer 0's attn_norm
+    // x = embedding + position (fragment order), h = LayerNorm(x) with layer 0's attn_norm
     check_hip(embed_pos_ln(st.sl ? st.sl->head : embed, st.sl ? st.sl_row : st.ids, B, pos, st.step,
                            uint32_t(cfg.pad_token_id + 1), embed_scale, dec[0].attn_norm.g, dec[0].attn_norm.b,
-                           kLnEps, st.x, st.h, s, src),
+                           kLnEps, st.x, st.h, s, src, true),
               "embed_pos_ln");
     auto ln = [&](const LNorm &n) { return DgemmLn{st.lnstat, n.g, n.b, kLnEps}; };
     for (size_t i = 0; i < dec.size(); ++i) {
@@ -952,7 +959,8 @@ void Model::step_dgemm(StaticState &st, bool greedy_mode, int mask_id) {
         check_hip(dgemm_qkv(l.qkv.w, i == 0 ? st.h : st.x, d, B, i == 0 ? nullptr : &ln_attn, l.qkv.b, H, hd, st.m,
                             st.step, st.q, st.kc[i], st.vc[i], s),
                   "dgemm_qkv");
-        // att and u travel as split f16 hi / lo planes (the A-operand form of the GEMMs)
+        // x in fragment order, att and u as split f16 hi / lo fragments: the A-operand
+        // order of the decode GEMMs (frag_index, device.hpp)
         check_hip(attn_decode(st.q, st.kc[i], st.vc[i], B, H, hd, st.m, nullptr, st.step, st.att, s, st.rows, true),
                   "attn");
         check_hip(dgemm_resid(l.out.w, st.att, d, B, l.out.b, st.x, st.lnstat, s, true), "dgemm_out");
@@ -964,7 +972,7 @@ void Model::step_dgemm(StaticState &st, bool greedy_mode, int mask_id) {
         check_hip(dgemm_resid(l.down.w, st.u, f, B, l.down.b, st.x, st.lnstat, s, true), "dgemm_down");
     }
     // st.h = dec_norm(x): tied LM head
-    check_hip(layernorm(st.x, B, d, dec_norm.g, dec_norm.b, kLnEps, st.h, s), "layernorm");
+    check_hip(layernorm_frag(st.x, B, d, dec_norm.g, dec_norm.b, kLnEps, st.h, s), "layernorm");
     lm_head(st, greedy_mode, mask_id);
 }
 
