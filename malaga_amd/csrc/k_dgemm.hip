@@ -40,7 +40,7 @@ struct DArgs {
     WPtr w;
     const float *x;  // [M][ldx] input rows (PRO_LN: the residual stream; PRO_SPLIT: split rows)
     int ldx, M;
-    const double *stats;  // PRO_LN: [P][M][2] sums of x and x^2 per 16 columns
+    const double *stats;  // PRO_LN: [M][P][2] sums of x and x^2 per 16 columns
     int P;
     const float *gamma, *beta;
     float eps;
@@ -48,7 +48,7 @@ struct DArgs {
     float *y;  // EPI_STORE [M][ldy] f32 rows, or split fragments (frag_out)
     int ldy, relu, frag_out;
     float *xres;        // EPI_RESID: the residual stream [M][N], fragment order
-    double *stats_out;  // EPI_RESID: [N / 16][M][2]
+    double *stats_out;  // EPI_RESID: [M][N / 16][2]
     float *q;           // EPI_QKV: q [M][d], caches [M][H][slots][hd]
     __half *kc, *vc;
     int H, hd, slots;
@@ -85,7 +85,8 @@ __global__ __launch_bounds__(kDgMaxNW * 64) void k_dgemm(DArgs a) {
     auto blk = [&](int j) { return min(wv + j * NW, nblk - 1); };
 
     // PRO_LN operands: this thread's float4 of gamma and beta, and its share of the
-    // statistics of row m0 + t / 16 (partials p = t % 16 + 16 q)
+    // statistics of row m0 + t / 16 (partials p = t % 16 + 16 q: a row's partials are
+    // contiguous, so 16 lanes read 256 bytes)
     float4 gv = make_float4(0.f, 0.f, 0.f, 0.f), bv = gv;
     double2 sp[PRO == PRO_LN ? kLnQ : 1];
     if constexpr (PRO == PRO_LN) {
@@ -98,7 +99,7 @@ __global__ __launch_bounds__(kDgMaxNW * 64) void k_dgemm(DArgs a) {
 #pragma unroll
         for (int q = 0; q < kLnQ; ++q) {
             const int p = wv < 4 ? min((t & 15) + q * kLnTPR, a.P - 1) : 0;
-            sp[q] = *reinterpret_cast<const double2 *>(a.stats + (size_t(p) * a.M + m) * 2);
+            sp[q] = *reinterpret_cast<const double2 *>(a.stats + (size_t(m) * a.P + p) * 2);
         }
     }
     // epilogue operands of this thread's outputs o = t + 256 u: row m0 + o / TN, column
@@ -335,7 +336,7 @@ __global__ __launch_bounds__(kDgMaxNW * 64) void k_dgemm(DArgs a) {
             if (own) a.xres[frag_index(om, on & ~3, a.w.N) * 4 + (on & 3)] = xn;
             const double s1 = group_sum_f64<16>(double(xn)), s2 = group_sum_f64<16>(double(xn) * double(xn));
             if (own && (c & 15) == 0) {
-                double *sp_out = a.stats_out + (size_t(on >> 4) * a.M + om) * 2;
+                double *sp_out = a.stats_out + (size_t(om) * (a.w.N >> 4) + (on >> 4)) * 2;
                 sp_out[0] = s1;
                 sp_out[1] = s2;
             }

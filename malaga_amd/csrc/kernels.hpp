@@ -83,7 +83,7 @@ hipError_t gemm_qkv(const DevMatrix &w, const float *X, int ldx, int M, const fl
 // ---- decode projections for batches of up to 64 rows, one launch each (k_dgemm.hip) ----
 constexpr int kDgemmMaxRows = 64;
 // Input LayerNorm from the statistics the residual stream's last writer left:
-// stats [K / 16][M][2] (f64 sums of x and x^2 per 16 columns), gamma/beta [K].  With a
+// stats [M][K / 16][2] (f64 sums of x and x^2 per 16 columns), gamma/beta [K].  With a
 // DgemmLn, x is the residual stream in fragment order (frag_index, device.hpp).
 struct DgemmLn {
     const double *stats;
@@ -97,7 +97,7 @@ bool dgemm_supported(const DevMatrix &w, int M);
 hipError_t dgemm_store(const DevMatrix &w, const float *x, int ldx, int M, const DgemmLn *ln, const float *bias,
                        bool relu, float *y, int ldy, hipStream_t st, bool y_split = false);
 // xres[m][n] += x[m] . W[n] + bias[n] in place (xres: the residual stream, (M padded to
-// 16) x N floats in fragment order), and stats_out [N / 16][M][2] of the new rows.
+// 16) x N floats in fragment order), and stats_out [M][N / 16][2] of the new rows.
 // x_split: x holds split fragments (else row-major f32 rows of ldx).
 hipError_t dgemm_resid(const DevMatrix &w, const float *x, int ldx, int M, const float *bias, float *xres,
                        double *stats_out, hipStream_t st, bool x_split = false);

@@ -131,7 +131,7 @@ struct StaticState {
     float *logits = nullptr, *pv = nullptr;
     uint32_t *pi = nullptr;
     int parts = 0;
-    // decode-GEMM step (batches of 5..64 rows): [d / 16][b][2] f64 sums of the residual
+    // decode-GEMM step (batches of 5..64 rows): [b][d / 16][2] f64 sums of the residual
     // stream and its squares per 16 columns, written with x by every projection that adds
     // to it and read by the next LayerNorm (null: the split-K step)
     double *lnstat = nullptr;
