@@ -244,13 +244,13 @@ GemvArgs make_args(const DevMatrix &w, const GemvGeom &g, const float *x, int ld
 
 constexpr int kGemvSmallRows = 65536;
 
-// The LM head streams its first kLmHeadCachedBytes of rows with cached loads and the
-// rest non-temporally: with the layer weights (112 MB for 600M q4_k_m) that part
-// stays in the 256 MB MALL from step to step, while an all-cached 215 MB head would
-// evict the layers.  Measured on 600M q4_k_m batch-1 decode with one resident round
-// of workgroups: 0, 16 and 32 MB within noise of each other, 64 MB 0.15 ms per
-// sentence slower, 128 MB 0.6 ms slower.  A smaller head (a 37k-row shortlist is
-// 31 MB) is cached whole.
+// An LM head of at most kLmHeadCachedBytes (a 37k-row shortlist is 31 MB) is read with
+// cached loads, so that it stays in the 256 MB MALL from step to step; a larger one is
+// streamed non-temporally, so that its pass evicts less of the layer weights (112 MB
+// for 600M q4_k_m) between steps.  Measured on the 600M head (215 MB): an all
+// non-temporal stream 38.1 us against 38.7 us with its first 32 MB cached, and on
+// batch-1 decode a cached prefix of 0, 16 or 32 MB within noise (64 MB 0.15 ms per
+// sentence slower, 128 MB 0.6 ms).
 constexpr size_t kLmHeadCachedBytes = 32000000;
 
 }  // namespace
@@ -332,8 +332,7 @@ hipError_t gemv_argmax(const DevMatrix &w, const float *x, int ldx, int b, int m
         a.ln_h = ln->h;
     }
     int grid = gemv_grid(w, 1);
-    const size_t row_bytes = w.bytes / size_t(w.N);
-    a.nt_from = row_bytes ? int(std::min<size_t>(size_t(w.N), kLmHeadCachedBytes / row_bytes)) : w.N;
+    a.nt_from = w.bytes <= kLmHeadCachedBytes ? w.N : 0;  // first row streamed non-temporally
     const hipError_t e = dispatch<1>(w.type, a, gemv_round_b(b), cpl, grid, st, w.lm);
     *parts = grid;  // the workgroups launched, = gemv_argmax_parts(w, b)
     return e;
