@@ -607,20 +607,6 @@ __device__ __forceinline__ void gemv_rows(const WPtr &w, const GemvGeom &g, XR (
 #pragma unroll
     for (int t = 0; t < CPL; ++t) cidx[t] = (cl + t * lpr < g.nchunks) ? cl + t * lpr : 0;
 
-    auto load_step = [&](int rg, Raw<T> (&r)[G][CPL], float (&bv)[G]) {
-#pragma unroll
-        for (int u = 0; u < G; ++u) {
-            const int row = min((rg + u * nwaves) * rpw + grp, w.N - 1);
-            if (NT && (rg + u * nwaves) * rpw >= nt_from) {  // wave-uniform
-#pragma unroll
-                for (int t = 0; t < CPL; ++t) load_chunk<T, true, LM>(w, row, cidx[t], r[u][t]);
-            } else {
-#pragma unroll
-                for (int t = 0; t < CPL; ++t) load_chunk<T, false, LM>(w, row, cidx[t], r[u][t]);
-            }
-            bv[u] = bias ? bias[row] : 0.f;
-        }
-    };
     auto compute_step = [&](int rg, const Raw<T> (&r)[G][CPL], const float (&bv)[G]) {
 #pragma unroll
         for (int u = 0; u < G; ++u) {
@@ -703,39 +689,62 @@ __device__ __forceinline__ void gemv_rows(const WPtr &w, const GemvGeom &g, XR (
             bias ? ring(no{}, yes{}) : ring(no{}, no{});
         return;
     }
-    int rg = gwave;
-    const bool any = rg * rpw < w.N;  // wave-uniform
-    Raw<T> A[G][CPL], Bf[G][CPL];
-    float ba[G], bb[G];
+    // The choice of a bias is made once, outside the loop, and the first step is requested
+    // by every wave (one past the last row group reads the last one and returns after
+    // the prologue): a load behind a branch would leave the compiler unsure of the order
+    // of the loads after it, and the prologue and each step would wait for all of them.
+    auto run = [&](auto biasc) {
+        constexpr bool BIAS = decltype(biasc)::value;
+        auto load = [&](int rg, Raw<T>(&r)[G][CPL], float(&b)[G]) {
 #pragma unroll
-    for (int u = 0; u < G; ++u) ba[u] = bb[u] = 0.f;
-    pre();
-    __builtin_amdgcn_sched_barrier(0);
-    if (any) load_step(rg, A, ba);
-    __builtin_amdgcn_sched_barrier(0);
-    prologue();
-    if (!any) return;
-    // The last step is peeled off, so that every compute in the main loop follows
-    // an issued prefetch: a conditional prefetch would merge two load states and
-    // the compiler would wait for all loads (the prefetch included) before computing.
-    for (;;) {
-        const int rb = rg + stride;
-        if (rb * rpw >= w.N) {  // wave-uniform
+            for (int u = 0; u < G; ++u) {
+                const int row = min((rg + u * nwaves) * rpw + grp, w.N - 1);
+                if (NT && (rg + u * nwaves) * rpw >= nt_from) {  // wave-uniform
+#pragma unroll
+                    for (int t = 0; t < CPL; ++t) load_chunk<T, true, LM>(w, row, cidx[t], r[u][t]);
+                } else {
+#pragma unroll
+                    for (int t = 0; t < CPL; ++t) load_chunk<T, false, LM>(w, row, cidx[t], r[u][t]);
+                }
+                b[u] = BIAS ? bias[row] : 0.f;
+            }
+        };
+        int rg = gwave;
+        const bool any = rg * rpw < w.N;  // wave-uniform
+        Raw<T> A[G][CPL], Bf[G][CPL];
+        float ba[G], bb[G];
+        pre();
+        __builtin_amdgcn_sched_barrier(0);
+        load(min(rg, (w.N - 1) / rpw), A, ba);
+        __builtin_amdgcn_sched_barrier(0);
+        prologue();
+        if (!any) return;
+        // The last step is peeled off, so that every compute in the main loop follows
+        // an issued prefetch: a conditional prefetch would merge two load states and
+        // the compiler would wait for all loads (the prefetch included) before computing.
+        for (;;) {
+            const int rb = rg + stride;
+            if (rb * rpw >= w.N) {  // wave-uniform
+                compute_step(rg, A, ba);
+                break;
+            }
+            load(rb, Bf, bb);
             compute_step(rg, A, ba);
-            break;
-        }
-        load_step(rb, Bf, bb);
-        compute_step(rg, A, ba);
-        rg = rb;
-        const int ra = rg + stride;
-        if (ra * rpw >= w.N) {
+            rg = rb;
+            const int ra = rg + stride;
+            if (ra * rpw >= w.N) {
+                compute_step(rg, Bf, bb);
+                break;
+            }
+            load(ra, A, ba);
             compute_step(rg, Bf, bb);
-            break;
+            rg = ra;
         }
-        load_step(ra, A, ba);
-        compute_step(rg, Bf, bb);
-        rg = ra;
-    }
+    };
+    if (bias)
+        run(std::integral_constant<bool, true>{});
+    else
+        run(std::integral_constant<bool, false>{});
 }
 
 // ---- host-side geometry shared by the launchers ----

@@ -75,16 +75,18 @@ using PreLoads = PreLoadsR<2>;
 
 template <int R = 2>
 __device__ __forceinline__ void preload(const StepArgs &a, PreLoadsR<R> &L) {
+    // every load unconditional (partials past a.P and rows past nb read a valid one,
+    // never used): a skipped load would leave the compiler unsure of the order of the
+    // loads issued after these, and the prologue would wait for them too
     const int f = min(int(threadIdx.x), (a.d >> 2) - 1);
 #pragma unroll
     for (int bi = 0; bi < R; ++bi) {
-        if (bi >= a.nb) break;
+        const int bc = min(bi, a.nb - 1);
 #pragma unroll
-        for (int p = 0; p < kPreParts; ++p)
-            if (p < a.P) L.part[bi][p] = ld4(a.part + (size_t(p) * a.nb + bi) * a.d, f);
-        L.x[bi] = ld4(a.x_in + size_t(bi) * a.d, f);
+        for (int p = 0; p < kPreParts; ++p) L.part[bi][p] = ld4(a.part + (size_t(min(p, a.P - 1)) * a.nb + bc) * a.d, f);
+        L.x[bi] = ld4(a.x_in + size_t(bc) * a.d, f);
     }
-    L.pb = a.pbias ? ld4(a.pbias, f) : make_float4(0.f, 0.f, 0.f, 0.f);
+    L.pb = ld4(a.pbias ? a.pbias : a.gamma, f);  // used only with a.pbias
     L.gr = ld4(a.gamma, f);
     L.br = ld4(a.beta, f);
 }
@@ -163,7 +165,7 @@ __device__ __forceinline__ void resid_ln_prologue(const StepArgs &a, const PreLo
 #pragma unroll
             for (int p = 1; p < kPreParts; ++p)
                 if (p < a.P) add4(acc, L.part[bi][p]);
-            add4(acc, L.pb);
+            if (a.pbias) add4(acc, L.pb);
             v[bi][0] = make_float4(L.x[bi].x + acc.x, L.x[bi].y + acc.y, L.x[bi].z + acc.z, L.x[bi].w + acc.w);
         }
     } else {
@@ -236,7 +238,8 @@ __global__ __launch_bounds__(256) void k_step(StepArgs a) {
     __shared__ double red[32];
     const int lane = threadIdx.x & 63;
     const int cl = lane & ((1 << a.g.lpr_log2) - 1);
-    const int gwave = blockIdx.x * 4 + (threadIdx.x >> 6), nwaves = gridDim.x * 4;
+    // a scalar: the per-step branches on it stay uniform (no divergent load paths)
+    const int gwave = __builtin_amdgcn_readfirstlane(blockIdx.x * 4 + (threadIdx.x >> 6)), nwaves = gridDim.x * 4;
     // f32 x: these kernels are latency-bound, and staging integer limbs of x would
     // add a conversion and a barrier to the critical path (measured slower)
     XF<T, B> xr[CPL];
@@ -314,7 +317,8 @@ __global__ __launch_bounds__(256) void k_attn_head(HeadArgs a) {
     constexpr int SPL = 64 / TPK;   // keys per pass of a wave
     constexpr int U = 8;            // passes per chunk (loads in flight)
     extern __shared__ float lds[];
-    const int t = threadIdx.x, lane = t & 63, w = t >> 6;
+    // w a scalar: branches on it stay uniform (no divergent load paths)
+    const int t = threadIdx.x, lane = t & 63, w = __builtin_amdgcn_readfirstlane(t >> 6);
     const int nb = a.nb, d = a.d, H = a.H, L = a.L, HG = a.HG, hg_log2 = __builtin_ctz(a.HG);
     const int C = HG * HD, g = blockIdx.x, h0 = g * HG, col0 = g * C;
     const int pairs = nb * HG;
@@ -330,11 +334,20 @@ __global__ __launch_bounds__(256) void k_attn_head(HeadArgs a) {
     float4 qa, qb;
     auto load_chunk_kv = [&](int p, int j0) {
         const int bi = p >> hg_log2, hh = h0 + (p & (HG - 1));
+        // the cache rows first (beam search's row map; greedy: the row itself), then every
+        // K/V load back to back (a row lookup per key would make each pair wait for the last)
+        uint32_t r[U];
+        if (a.rows) {  // kernel argument
+#pragma unroll
+            for (int u = 0; u < U; ++u) r[u] = a.rows[size_t(bi) * L + min(j0 + u * SPL + split, L - 1)];
+        } else {
+#pragma unroll
+            for (int u = 0; u < U; ++u) r[u] = uint32_t(bi);
+        }
 #pragma unroll
         for (int u = 0; u < U; ++u) {
             const int j = min(j0 + u * SPL + split, L - 1);
-            const size_t r = a.rows ? a.rows[size_t(bi) * L + j] : size_t(bi);
-            const size_t o = ((r * H + hh) * L + j) * HD + sub * 8;
+            const size_t o = ((size_t(r[u]) * H + hh) * L + j) * HD + sub * 8;
             kr[u] = *reinterpret_cast<const uint4 *>(a.K + o);
             vr[u] = *reinterpret_cast<const uint4 *>(a.V + o);
         }
@@ -557,7 +570,8 @@ __global__ __launch_bounds__(kXThreads) void k_xattn(XAttnArgs a) {
     constexpr int TPK = HD / 8, SPL = 64 / TPK, U = 8, NW = kXThreads / 64;
     extern __shared__ float lds[];
     __shared__ double red[2 * 4 * NW];
-    const int t = threadIdx.x, lane = t & 63, w = t >> 6;
+    // w a scalar: branches on it stay uniform (no divergent load paths)
+    const int t = threadIdx.x, lane = t & 63, w = __builtin_amdgcn_readfirstlane(t >> 6);
     const int nb = a.s.nb, d = a.s.d, H = a.H, L = a.L, HG = a.HG, hg_log2 = __builtin_ctz(a.HG);
     const int C = HG * HD, g = blockIdx.x, h0 = g * HG, col0 = g * C;
     const int pairs = nb * HG;
@@ -571,7 +585,7 @@ __global__ __launch_bounds__(kXThreads) void k_xattn(XAttnArgs a) {
     // rows, the out-projection chunk, the first K/V chunk.  Loads complete in order,
     // so each phase waits only for what it uses.
     PreLoadsR<PR> PL;
-    if (t < 256) {  // wave-uniform: the threads that own the float4 slots
+    if (w < 4) {  // scalar: the threads that own the float4 slots
         preload<PR>(a.s, PL);
     } else {
 #pragma unroll
