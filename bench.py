@@ -422,6 +422,42 @@ def bench_kernels(T, lm_blocks: np.ndarray):
     return rows, dict(residual_ln_1x1024_us=ln_us, argmax_partial_256206_us=argmax_us)
 
 
+def stream_ceiling(nbytes: int = 215223280, grids=(1024, 2048, 4096, 8192), launches: int = 60):
+    """The read ceiling the LM head's roofline sits under: mlg_bench_stream_read over
+    rotating buffers of the head's bytes (> 1.1 GB in all, as the roofline leg, so that the
+    256 MB MALL cannot serve repeats), per load kind and grid; GB/s from HIP events on the
+    launch stream."""
+    import ctypes as C
+    import torch
+    from malaga_amd import _lib
+
+    lib = _lib.load()
+    copies = max(2, int(np.ceil(1.1e9 / nbytes)))
+    bufs = [torch.ones(nbytes // 4 + 4, dtype=torch.int32, device="cuda") for _ in range(copies)]
+    out = torch.zeros(1, dtype=torch.int32, device="cuda")
+    stream = torch.cuda.Stream()
+    sp, op = C.c_void_p(stream.cuda_stream), C.c_void_p(out.data_ptr())
+    bps = [C.c_void_p(b.data_ptr()) for b in bufs]
+    rows = []
+    torch.cuda.synchronize()
+    with torch.cuda.stream(stream):
+        for mode, kind in ((0, "ordinary"), (1, "non-temporal"), (2, "direct-to-LDS")):
+            for grid in grids:
+                for i in range(2 * copies):
+                    _lib.check(lib.mlg_bench_stream_read(bps[i % copies], nbytes, mode, grid, op, sp))
+                start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                start.record(stream)
+                for i in range(launches):
+                    _lib.check(lib.mlg_bench_stream_read(bps[i % copies], nbytes, mode, grid, op, sp))
+                end.record(stream)
+                end.synchronize()
+                us = start.elapsed_time(end) * 1e3 / launches
+                rows.append(dict(loads=kind, grid=grid, us=round(us, 2), GBps=round(nbytes / us / 1e3, 1)))
+    del bufs
+    best = max(rows, key=lambda r: r["GBps"])
+    return dict(bytes=nbytes, copies=copies, best_GBps=best["GBps"], best=best, runs=rows)
+
+
 def measured_traffic():
     """HBM bytes per LM-head launch from the committed rocprofv3 counter summary
     (FETCH_SIZE + WRITE_SIZE, calibrated on a copy kernel), or None."""
@@ -479,6 +515,7 @@ def main():
                          "'config5' alone runs only the 3.3B batch-64 leg, 'mfma' alone the short "
                          "MFMA-GEMM runs used for counter collection")
     ap.add_argument("--roofline-only", action="store_true", help="only the LM-head roofline leg (for rocprof)")
+    ap.add_argument("--stream-ceiling", action="store_true", help="only the streaming-read ceiling (for rocprof)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this build targets one GPU: the decode path has no multi-GPU mode "
@@ -494,6 +531,10 @@ def main():
     lm_blocks, info = tensor_bytes(q4, "token_embd.weight")
     assert info["type"] == 14
     lm_blocks = np.ascontiguousarray(lm_blocks)
+    if args.stream_ceiling:
+        M._Ctx(0)
+        print(json.dumps({"stream_ceiling": stream_ceiling()}))
+        return
     if args.roofline_only:
         ctx = M._Ctx(0)
         r = GemvBench(ctx).run(14, lm_blocks, 256206, 1024, launches=200, argmax=True)
@@ -559,6 +600,11 @@ def main():
                                    "(rocprofv3 --pmc FETCH_SIZE, WRITE_SIZE; copy-kernel calibrated)",
                     kernel="k_gemv<q6_K,B=1,argmax> (LM head 256206x1024 + fused argmax partials)",
                     bytes_per_launch=lm["bytes"], us_per_launch=round(lm["us"], 3))
+    ceiling = stream_ceiling()
+    log(f"read ceiling: {ceiling['best_GBps']:.0f} GB/s ({ceiling['best']['loads']} loads, grid "
+        f"{ceiling['best']['grid']}); LM head at {lm['GBps'] / ceiling['best_GBps']:.3f} of it")
+    roofline["read_ceiling_GBps"] = ceiling["best_GBps"]
+    roofline["frac_of_read_ceiling"] = round(lm["GBps"] / ceiling["best_GBps"], 4)
     q4_lm = next(r for r in gemv_rows if r["type"] == "q4_K" and r["name"] == "lm_head")
     cpu = None
     if "cpu" in legs:

@@ -205,6 +205,12 @@ int mlg_graph_stats(const mlg_model *m, int *entries, int *graphs, int *capture_
 int mlg_graph_cache_keys(const mlg_model *m, int *keys, int cap);
 /* Test hook: the n-th following device allocation fails with MLG_ERR_OOM (n < 0: off). */
 void mlg_debug_fail_alloc_after(long n);
+/* Streaming-read ceiling, the reference point of the LM head's roofline (measurement only;
+   no counterpart in the reference): `grid` workgroups of 256 threads read every 16-byte word
+   of p[0, bytes) once, 8 loads of 16 bytes in flight per thread; mode 0 ordinary loads,
+   1 non-temporal loads, 2 direct-to-LDS loads (global_load_lds_dwordx4).  bytes % 16 == 0,
+   p 16-byte aligned; out: 4 bytes the kernel may write (so that the loads are kept). */
+int mlg_bench_stream_read(const void *p, size_t bytes, int mode, int grid, uint32_t *out, void *stream);
 
 /* ---- kernel-level entry points (microbenchmarks and tests; device pointers) ---- */
 /* A GGUF matrix [N][K] of `type` (raw GGUF row bytes from the host) uploaded in the device layout. */

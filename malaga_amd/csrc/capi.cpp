@@ -506,6 +506,10 @@ int mlg_graph_cache_keys(const mlg_model *m, int *keys, int cap) {
 
 void mlg_debug_fail_alloc_after(long n) { mlg::set_fail_alloc_after(n); }
 
+int mlg_bench_stream_read(const void *p, size_t bytes, int mode, int grid, uint32_t *out, void *stream) {
+    return hip_status(mlg::stream_read(p, bytes, mode, grid, out, static_cast<hipStream_t>(stream)), "stream_read");
+}
+
 int mlg_matrix_upload(mlg_ctx *ctx, uint32_t type, int N, int K, const void *gguf_rows, mlg_matrix **out) {
     return guarded([&]() -> int {
         if (!ctx || !gguf_rows || N <= 0 || K <= 0 || !out) return set_err(MLG_ERR_INVALID, "bad argument");

@@ -113,6 +113,9 @@ int gemm_argmax_parts(const DevMatrix &w, int M);
 hipError_t gemm_argmax(const DevMatrix &w, const float *X, int ldx, int M, int mask_id, float *pv, uint32_t *pi,
                        int *parts, hipStream_t st);
 
+// Streaming read of p[0, bytes) (measurement: the read ceiling), mode 0 / 1 / 2 =
+// ordinary / non-temporal / direct-to-LDS 16-byte loads.
+hipError_t stream_read(const void *p, size_t bytes, int mode, int grid, uint32_t *out, hipStream_t st);
 // Row LayerNorm (biased variance): out = (x - mean) * rsqrt(var + eps) * g + b.
 hipError_t layernorm(const float *x, int rows, int d, const float *g, const float *b, float eps, float *out,
                      hipStream_t st);
