@@ -107,6 +107,7 @@ SIGNATURES = {
     "mlg_graph_stats": (C.c_int, [_P, _intp, _intp, _intp]),
     "mlg_graph_cache_keys": (C.c_int, [_P, _P, C.c_int]),
     "mlg_debug_fail_alloc_after": (None, [C.c_long]),
+    "mlg_debug_tile_major": (C.c_int64, [C.c_uint32, C.c_int, C.c_int, C.c_void_p, C.c_void_p, C.c_int64]),
     "mlg_bench_stream_read": (C.c_int, [C.c_void_p, C.c_size_t, C.c_int, C.c_int, C.c_void_p, C.c_void_p]),
     "mlg_matrix_upload": (C.c_int, [_P, C.c_uint32, C.c_int, C.c_int, _P, C.POINTER(_P)]),
     "mlg_matrix_free": (None, [_P]),

@@ -506,6 +506,17 @@ int mlg_graph_cache_keys(const mlg_model *m, int *keys, int cap) {
 
 void mlg_debug_fail_alloc_after(long n) { mlg::set_fail_alloc_after(n); }
 
+int64_t mlg_debug_tile_major(uint32_t type, int N, int K, const void *gguf_rows, void *out, int64_t cap) {
+    if (!gguf_rows || N <= 0 || K <= 0 || cap < 0) return -set_err(MLG_ERR_INVALID, "bad argument");
+    const size_t tb = mlg::tile_major_bytes(type, N, K);
+    if (!tb || !out || cap < int64_t(tb)) return int64_t(tb);
+    std::vector<uint8_t> host(mlg::planes_bytes(type, N, K));
+    size_t off_s, off_d, total;
+    mlg::layout_planes(type, N, K, static_cast<const uint8_t *>(gguf_rows), host.data(), &off_s, &off_d, &total);
+    mlg::layout_tile_major(N, K, host.data(), off_s, off_d, static_cast<uint8_t *>(out));
+    return int64_t(tb);
+}
+
 int mlg_bench_stream_read(const void *p, size_t bytes, int mode, int grid, uint32_t *out, void *stream) {
     return hip_status(mlg::stream_read(p, bytes, mode, grid, out, static_cast<hipStream_t>(stream)), "stream_read");
 }

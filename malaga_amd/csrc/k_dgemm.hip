@@ -38,6 +38,7 @@ namespace {
 
 struct DArgs {
     WPtr w;
+    const uint8_t *tw;  // the tile-major copy of a q6_K W (DevMatrix::tm), or null
     const float *x;  // [M][ldx] input rows (PRO_LN: the residual stream; PRO_SPLIT: split rows)
     int ldx, M;
     const double *stats;  // PRO_LN: [M][P][2] sums of x and x^2 per 16 columns
@@ -63,12 +64,12 @@ constexpr int kDgMaxBPW = 4;     // K blocks per wave at most: K <= 8192
 constexpr int kDgMaxLnK = 2048;  // LayerNorm projections: K = d_model <= 2048 (gamma, beta in LDS)
 constexpr int kLnTPR = 16;                          // threads per row adding the statistics
 constexpr int kLnQ = kDgMaxLnK / 16 / kLnTPR;       // partials per thread at most
-constexpr int kRS = 17;                             // LDS row stride of the partial tiles
 
 // BPW: K blocks per wave (compile time, it sizes the fragment ring); NT: 16-column tiles
 // per workgroup (1 or 2; with 2, each X fragment, once normalized and split, feeds two
-// tiles); the wave count NW (4 or 8) is blockDim.x / 64.
-template <int T, int BPW, int NT, int PRO, int EPI>
+// tiles); TL: W from the tile-major copy a.tw (q6_K); the wave count NW (4 or 8) is
+// blockDim.x / 64.
+template <int T, int BPW, int NT, int PRO, int EPI, bool TL>
 __global__ __launch_bounds__(kDgMaxNW * 64) void k_dgemm(DArgs a) {
     using W = MW<T>;
     constexpr int SK = W::SK, XQ = SK / 16;  // float4s of X per lane and slice
@@ -117,10 +118,14 @@ __global__ __launch_bounds__(kDgMaxNW * 64) void k_dgemm(DArgs a) {
     // W of the first K block, then the next block's when a block starts
     WR wr[2][NT];
     int wrow[NT];
+    auto load_w = [&](int nt, int kb, WR &r) {
+        if constexpr (TL) W::load_tile(a.tw, a.w.nb, min((n0 >> 4) + nt, (a.w.N >> 4) - 1), kb, kq, ln, r);
+        else W::load(a.w, wrow[nt], kb, kq, r);
+    };
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt) {
         wrow[nt] = min(n0 + nt * 16 + ln, a.w.N - 1);
-        W::load(a.w, wrow[nt], blk(0), kq, wr[0][nt]);
+        load_w(nt, blk(0), wr[0][nt]);
     }
 
     // X fragment of (block kb, slice s): row m0 + ln, columns kb 256 + s SK + kq SK / 4
@@ -267,7 +272,7 @@ __global__ __launch_bounds__(kDgMaxNW * 64) void k_dgemm(DArgs a) {
         const bool live = wv + j * NW < nblk;  // scalar
         if constexpr (j + 1 < BPW)
 #pragma unroll
-            for (int nt = 0; nt < NT; ++nt) W::load(a.w, wrow[nt], blk(j + 1), kq, wr[(j + 1) & 1][nt]);
+            for (int nt = 0; nt < NT; ++nt) load_w(nt, blk(j + 1), wr[(j + 1) & 1][nt]);
         static_for<0, W::SLICES>([&](auto sc) {
             constexpr int s = decltype(sc)::value, i = j * W::SLICES + s, r = i + D;
             compute(kb, s, wr[j & 1], buf[i % D], live);
@@ -356,18 +361,27 @@ inline int dg_bpw(int nblk) {
 // FFN-up 7.4 instead of 9.3).
 constexpr int kDgWideGrid = 384;
 
-template <int T, int BPW, int PRO, int EPI>
-hipError_t launch_dgemm(const DArgs &a, hipStream_t st) {
+template <int T, int BPW, int PRO, int EPI, bool TL>
+hipError_t launch_dgemm_l(const DArgs &a, hipStream_t st) {
     const unsigned gy = unsigned((a.M + 15) / 16), block = unsigned(dg_waves(a.w.K / kStep) * 64);
     const unsigned tiles1 = unsigned((a.w.N + 15) / 16);
     if constexpr (EPI != EPI_RESID) {  // the residual projections are N = d_model wide
         if (tiles1 * gy >= unsigned(kDgWideGrid)) {
-            hipLaunchKernelGGL((k_dgemm<T, BPW, 2, PRO, EPI>), dim3((a.w.N + 31) / 32, gy), dim3(block), 0, st, a);
+            hipLaunchKernelGGL((k_dgemm<T, BPW, 2, PRO, EPI, TL>), dim3((a.w.N + 31) / 32, gy), dim3(block), 0, st, a);
             return hipGetLastError();
         }
     }
-    hipLaunchKernelGGL((k_dgemm<T, BPW, 1, PRO, EPI>), dim3(tiles1, gy), dim3(block), 0, st, a);
+    hipLaunchKernelGGL((k_dgemm<T, BPW, 1, PRO, EPI, TL>), dim3(tiles1, gy), dim3(block), 0, st, a);
     return hipGetLastError();
+}
+
+// q6_K with its tile-major copy (N % 16 == 0) reads that copy
+template <int T, int BPW, int PRO, int EPI>
+hipError_t launch_dgemm(const DArgs &a, hipStream_t st) {
+    if constexpr (T == GGML_Q6_K) {
+        if (a.tw) return launch_dgemm_l<T, BPW, PRO, EPI, true>(a, st);
+    }
+    return launch_dgemm_l<T, BPW, PRO, EPI, false>(a, st);
 }
 
 // only the residual projections (ffn_down: K = the FFN width) take more than one K
@@ -399,6 +413,7 @@ hipError_t launch_dgemm_t(const DevMatrix &w, const DArgs &a, hipStream_t st) {
 DArgs dargs(const DevMatrix &w, const float *x, int ldx, int M, const DgemmLn *ln, const float *bias) {
     DArgs a{};
     a.w = wptr_of(w);
+    a.tw = w.type == GGML_Q6_K && w.N % 16 == 0 ? w.tm : nullptr;
     a.x = x;
     a.ldx = ldx;
     a.M = M;

@@ -118,6 +118,20 @@ struct MW<GGML_Q6_K> {
         r.sc = *reinterpret_cast<const uint4 *>(w.s + blk * 16);
         r.d = *reinterpret_cast<const unsigned short *>(w.d + blk * 2);
     }
+    // the same registers from the tile-major copy (kQ6TileBytes per tile and block):
+    // five loads, each of whole cache lines, instead of fourteen of 16 scattered rows
+    __device__ static void load_tile(const uint8_t *tw, int nb, int tile, int kb, int kq, int ln, Regs &r) {
+        const uint8_t *tb = tw + (size_t(tile) * nb + kb) * kQ6TileBytes;
+        const int li = 16 * kq + ln;
+        const uint4 a = *reinterpret_cast<const uint4 *>(tb + 16 * li);
+        const uint4 b = *reinterpret_cast<const uint4 *>(tb + 1024 + 16 * li);
+        const uint4 h = *reinterpret_cast<const uint4 *>(tb + 2048 + 16 * li);
+        r.qa[0] = a.x, r.qa[1] = a.y, r.qa[2] = a.z, r.qa[3] = a.w;
+        r.qb[0] = b.x, r.qb[1] = b.y, r.qb[2] = b.z, r.qb[3] = b.w;
+        r.qh[0] = h.x, r.qh[1] = h.y, r.qh[2] = h.z, r.qh[3] = h.w;
+        r.sc = *reinterpret_cast<const uint4 *>(tb + 3072 + 16 * ln);
+        r.d = *reinterpret_cast<const unsigned short *>(tb + 3328 + 2 * ln);
+    }
     __device__ static h4_t b(const Regs &r, int G) {
         const int n = G >> 3, t = (G >> 1) & 3, h = G & 1, nh = 2 * n + h;
         const uint32_t ql = (t & 1) ? r.qb[nh] : r.qa[nh];

@@ -177,6 +177,34 @@ void layout_lane_major(int N, int K, const uint8_t *q_plane, uint8_t *out) {
         }
 }
 
+size_t tile_major_bytes(uint32_t type, int N, int K) {
+    return type == GGML_Q6_K && N % 16 == 0 && K % 256 == 0 ? size_t(N / 16) * (K / 256) * kQ6TileBytes : 0;
+}
+
+void layout_tile_major(int N, int K, const uint8_t *planes, size_t off_s, size_t off_d, uint8_t *out) {
+    const int nb = K / 256;
+    std::memset(out, 0, tile_major_bytes(GGML_Q6_K, N, K));
+    for (int t = 0; t < N / 16; ++t)
+        for (int kb = 0; kb < nb; ++kb) {
+            uint8_t *tb = out + (size_t(t) * nb + kb) * kQ6TileBytes;
+            for (int r = 0; r < 16; ++r) {
+                const size_t blk = size_t(16 * t + r) * nb + kb;
+                const uint8_t *qp = planes + blk * 192;  // ql[128] | qh[64]
+                for (int kq = 0; kq < 4; ++kq) {
+                    const int l = 16 * kq + r;
+                    for (int nh = 0; nh < 4; ++nh) {  // the dwords MW<GGML_Q6_K>::load reads
+                        const int n = nh >> 1, h = nh & 1;
+                        std::memcpy(tb + 16 * l + 4 * nh, qp + 64 * n + 16 * h + 4 * kq, 4);
+                        std::memcpy(tb + 1024 + 16 * l + 4 * nh, qp + 64 * n + 32 + 16 * h + 4 * kq, 4);
+                        std::memcpy(tb + 2048 + 16 * l + 4 * nh, qp + 128 + 32 * n + 16 * h + 4 * kq, 4);
+                    }
+                }
+                std::memcpy(tb + 3072 + 16 * r, planes + off_s + blk * 16, 16);
+                std::memcpy(tb + 3328 + 2 * r, planes + off_d + blk * 2, 2);
+            }
+        }
+}
+
 float *Context::gemm_workspace() {
     if (!gemm_ws) gemm_ws = static_cast<float *>(dev_alloc(kGemmWorkspaceBytes, "GEMM workspace"));
     return gemm_ws;
@@ -226,7 +254,7 @@ const GgufTensorInfo *matrix_info(GgufFile &g, const std::string &name, int n, i
 }
 }  // namespace
 
-DevMatrix Model::upload_matrix(GgufFile &g, const std::string &name, int n, int k, bool head) {
+DevMatrix Model::upload_matrix(GgufFile &g, const std::string &name, int n, int k, bool head, bool tile) {
     const GgufTensorInfo *t = matrix_info(g, name, n, k);
     DevMatrix m;
     m.type = t->type;
@@ -245,6 +273,14 @@ DevMatrix Model::upload_matrix(GgufFile &g, const std::string &name, int n, int 
     m.bytes = total;
     weight_bytes += total;
     if (head) upload_lane_major(m, host.data());
+    if (const size_t tb = tile ? tile_major_bytes(m.type, n, k) : 0) {
+        std::vector<uint8_t> tmh(tb);
+        layout_tile_major(n, k, host.data(), off_s, off_d, tmh.data());
+        m.tm = static_cast<uint8_t *>(dev_alloc(tb, (name + " (tile-major)").c_str()));
+        owned_.push_back(m.tm);
+        check_hip(hipMemcpy(m.tm, tmh.data(), tb, hipMemcpyHostToDevice), "upload");
+        weight_bytes += tb;
+    }
     return m;
 }
 
@@ -259,9 +295,9 @@ void Model::upload_lane_major(DevMatrix &m, const uint8_t *q_plane) {
     weight_bytes += lb;
 }
 
-Linear Model::load_linear(GgufFile &g, const std::string &name, int n, int k) {
+Linear Model::load_linear(GgufFile &g, const std::string &name, int n, int k, bool tile) {
     Linear l;
-    l.w = upload_matrix(g, name + ".weight", n, k);
+    l.w = upload_matrix(g, name + ".weight", n, k, false, tile);
     l.b = upload_f32(g, name + ".bias", n);
     return l;
 }
@@ -426,14 +462,15 @@ void Model::load(const std::string &path) {
         const std::string p = "dec.blk." + std::to_string(i);
         DecLayer l;
         l.attn_norm = load_ln(g, p + ".attn_norm", d);
-        l.qkv = load_linear(g, p + ".attn_qkv", 3 * d, d);
-        l.out = load_linear(g, p + ".attn_out", d, d);
+        // the decode GEMMs' q6_K matrices also get their tile-major copy
+        l.qkv = load_linear(g, p + ".attn_qkv", 3 * d, d, true);
+        l.out = load_linear(g, p + ".attn_out", d, d, true);
         l.cross_norm = load_ln(g, p + ".cross_attn_norm", d);
-        l.cross_q = load_linear(g, p + ".cross_attn_q", d, d);
-        l.cross_out = load_linear(g, p + ".cross_attn_out", d, d);
+        l.cross_q = load_linear(g, p + ".cross_attn_q", d, d, true);
+        l.cross_out = load_linear(g, p + ".cross_attn_out", d, d, true);
         l.ffn_norm = load_ln(g, p + ".ffn_norm", d);
-        l.up = load_linear(g, p + ".ffn_up", cfg.decoder_ffn, d);
-        l.down = load_linear(g, p + ".ffn_down", d, cfg.decoder_ffn);
+        l.up = load_linear(g, p + ".ffn_up", cfg.decoder_ffn, d, true);
+        l.down = load_linear(g, p + ".ffn_down", d, cfg.decoder_ffn, true);
         dec.push_back(l);
     }
     cross_kv = load_stacked(g, ".cross_attn_kv", cfg.decoder_layers, 2 * d, d);

@@ -42,3 +42,46 @@ def test_unknown_preset_is_an_error():
     n = ctypes.c_int()
     assert _lib.load().mlg_preset_from_name(b"q4_0", ctypes.byref(n)) == _lib.ERR_INVALID
     assert b"q4_k_m" in _lib.load().mlg_last_error()
+
+
+def test_q6k_tile_major_copy_holds_what_each_lane_reads():
+    """The decode GEMMs' tile-major q6_K copy, checked against the GGUF q6_K block format
+    (ql[128] | qh[64] | int8 scales[16] | f16 d per 256 values): lane 16 kq + r of tile t
+    finds, for K block kb, ql[64 n + 16 h + 4 kq .. +4] (piece 0), ql[64 n + 32 + 16 h + 4 kq
+    .. +4] (piece 1) and qh[32 n + 16 h + 4 kq .. +4] (piece 2) as dword 2 n + h of its
+    16-byte piece, then row 16 t + r's scales and d.  Every quant byte is read exactly once."""
+    import numpy as np
+
+    lib = _lib.load()
+    N, K = 48, 768
+    nb = K // 256
+    rng = np.random.default_rng(7)
+    rows = rng.integers(0, 256, size=(N, nb, 210), dtype=np.uint8)
+    src = np.ascontiguousarray(rows)
+    size = lib.mlg_debug_tile_major(14, N, K, src.ctypes.data, None, 0)
+    assert size == (N // 16) * nb * 3456
+    out = np.zeros(size, dtype=np.uint8)
+    assert lib.mlg_debug_tile_major(14, N, K, src.ctypes.data, out.ctypes.data, size) == size
+    # no tile-major form: other types, N not a multiple of 16
+    assert lib.mlg_debug_tile_major(12, N, K, src.ctypes.data, None, 0) == 0
+    assert lib.mlg_debug_tile_major(14, N - 8, K, src.ctypes.data, None, 0) == 0
+    seen = np.zeros((N, nb, 192), dtype=np.int32)
+    for t in range(N // 16):
+        for kb in range(nb):
+            tb = out[(t * nb + kb) * 3456:(t * nb + kb + 1) * 3456]
+            for r in range(16):
+                blk = rows[16 * t + r, kb]
+                for kq in range(4):
+                    lane = 16 * kq + r
+                    for n in range(2):
+                        for h in range(2):
+                            dw = 4 * (2 * n + h)
+                            for piece, off in ((0, 64 * n + 16 * h + 4 * kq), (1, 64 * n + 32 + 16 * h + 4 * kq),
+                                               (2, 128 + 32 * n + 16 * h + 4 * kq)):
+                                got = tb[1024 * piece + 16 * lane + dw:1024 * piece + 16 * lane + dw + 4]
+                                assert (got == blk[off:off + 4]).all()
+                                seen[16 * t + r, kb, off:off + 4] += 1
+                assert (tb[3072 + 16 * r:3088 + 16 * r] == blk[192:208]).all()
+                assert (tb[3328 + 2 * r:3330 + 2 * r] == blk[208:210]).all()
+            assert not tb[3360:].any()
+    assert (seen == 1).all()
