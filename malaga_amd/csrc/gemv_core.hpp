@@ -48,6 +48,7 @@ struct GTraits<GGML_F32> { static constexpr int XW = 4, NS = 1; };
 struct WPtr {
     const uint8_t *q, *s, *d;
     int N, K, nb;  // nb: blocks per row
+    const uint8_t *t = nullptr;  // the tile-major copy (DevMatrix::tm), or null
 };
 
 // x position of element e (0..XW-1) of chunk c
@@ -764,7 +765,7 @@ inline int gemv_xw(uint32_t t) {
 inline WPtr wptr_of(const DevMatrix &w) {
     TypeInfo ti;
     type_info(w.type, &ti);
-    return WPtr{w.q, w.s, w.d, w.N, w.K, w.K / ti.block_elems};
+    return WPtr{w.q, w.s, w.d, w.N, w.K, w.K / ti.block_elems, w.tm};
 }
 
 // lanes per row group and chunks per lane for matrix w

@@ -38,7 +38,6 @@ namespace {
 
 struct DArgs {
     WPtr w;
-    const uint8_t *tw;  // the tile-major copy of a q6_K W (DevMatrix::tm), or null
     const float *x;  // [M][ldx] input rows (PRO_LN: the residual stream; PRO_SPLIT: split rows)
     int ldx, M;
     const double *stats;  // PRO_LN: [M][P][2] sums of x and x^2 per 16 columns
@@ -67,7 +66,7 @@ constexpr int kLnQ = kDgMaxLnK / 16 / kLnTPR;       // partials per thread at mo
 
 // BPW: K blocks per wave (compile time, it sizes the fragment ring); NT: 16-column tiles
 // per workgroup (1 or 2; with 2, each X fragment, once normalized and split, feeds two
-// tiles); TL: W from the tile-major copy a.tw (q6_K); the wave count NW (4 or 8) is
+// tiles); TL: W from the tile-major copy a.w.t (q6_K); the wave count NW (4 or 8) is
 // blockDim.x / 64.
 template <int T, int BPW, int NT, int PRO, int EPI, bool TL>
 __global__ __launch_bounds__(kDgMaxNW * 64) void k_dgemm(DArgs a) {
@@ -117,16 +116,8 @@ __global__ __launch_bounds__(kDgMaxNW * 64) void k_dgemm(DArgs a) {
     using WR = typename W::Regs;
     // W of the first K block, then the next block's when a block starts
     WR wr[2][NT];
-    int wrow[NT];
-    auto load_w = [&](int nt, int kb, WR &r) {
-        if constexpr (TL) W::load_tile(a.tw, a.w.nb, min((n0 >> 4) + nt, (a.w.N >> 4) - 1), kb, kq, ln, r);
-        else W::load(a.w, wrow[nt], kb, kq, r);
-    };
 #pragma unroll
-    for (int nt = 0; nt < NT; ++nt) {
-        wrow[nt] = min(n0 + nt * 16 + ln, a.w.N - 1);
-        load_w(nt, blk(0), wr[0][nt]);
-    }
+    for (int nt = 0; nt < NT; ++nt) load_w<T, TL>(a.w, (n0 >> 4) + nt, ln, blk(0), kq, wr[0][nt]);
 
     // X fragment of (block kb, slice s): row m0 + ln, columns kb 256 + s SK + kq SK / 4
     // (fragment order: the tile's padding rows are stored)
@@ -272,7 +263,8 @@ __global__ __launch_bounds__(kDgMaxNW * 64) void k_dgemm(DArgs a) {
         const bool live = wv + j * NW < nblk;  // scalar
         if constexpr (j + 1 < BPW)
 #pragma unroll
-            for (int nt = 0; nt < NT; ++nt) load_w(nt, blk(j + 1), wr[(j + 1) & 1][nt]);
+            for (int nt = 0; nt < NT; ++nt)
+                load_w<T, TL>(a.w, (n0 >> 4) + nt, ln, blk(j + 1), kq, wr[(j + 1) & 1][nt]);
         static_for<0, W::SLICES>([&](auto sc) {
             constexpr int s = decltype(sc)::value, i = j * W::SLICES + s, r = i + D;
             compute(kb, s, wr[j & 1], buf[i % D], live);
@@ -375,11 +367,11 @@ hipError_t launch_dgemm_l(const DArgs &a, hipStream_t st) {
     return hipGetLastError();
 }
 
-// q6_K with its tile-major copy (N % 16 == 0) reads that copy
+// q6_K with its tile-major copy reads that copy
 template <int T, int BPW, int PRO, int EPI>
 hipError_t launch_dgemm(const DArgs &a, hipStream_t st) {
     if constexpr (T == GGML_Q6_K) {
-        if (a.tw) return launch_dgemm_l<T, BPW, PRO, EPI, true>(a, st);
+        if (a.w.t) return launch_dgemm_l<T, BPW, PRO, EPI, true>(a, st);
     }
     return launch_dgemm_l<T, BPW, PRO, EPI, false>(a, st);
 }
@@ -413,7 +405,6 @@ hipError_t launch_dgemm_t(const DevMatrix &w, const DArgs &a, hipStream_t st) {
 DArgs dargs(const DevMatrix &w, const float *x, int ldx, int M, const DgemmLn *ln, const float *bias) {
     DArgs a{};
     a.w = wptr_of(w);
-    a.tw = w.type == GGML_Q6_K && w.N % 16 == 0 ? w.tm : nullptr;
     a.x = x;
     a.ldx = ldx;
     a.M = M;

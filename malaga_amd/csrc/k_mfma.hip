@@ -39,7 +39,8 @@ struct MfmaArgs {
 };
 
 
-template <int T, int BM>
+// TL (all three GEMM kernels): W from the tile-major copy a.w.t (q6_K)
+template <int T, int BM, bool TL>
 __global__ __launch_bounds__(256) void k_mfma(MfmaArgs a) {
     using W = MW<T>;
     constexpr int MT = BM / 16;     // 16-row tiles of X
@@ -50,7 +51,6 @@ __global__ __launch_bounds__(256) void k_mfma(MfmaArgs a) {
     const int t = threadIdx.x, lane = t & 63, w = t >> 6;
     const int kq = lane >> 4, ln = lane & 15;
     const int n0 = blockIdx.x * kTileN + 16 * w;
-    const int row = min(n0 + ln, a.w.N - 1);
     const int m0 = blockIdx.y * BM;
     // K steps [kb0, kb1) of this split
     const int nsteps = a.w.K / kStep, ks = gridDim.z;
@@ -94,14 +94,14 @@ __global__ __launch_bounds__(256) void k_mfma(MfmaArgs a) {
     for (int mt = 0; mt < MT; ++mt) acc[mt] = f4_t{0.f, 0.f, 0.f, 0.f};
 
     typename W::Regs cur, nxt;
-    W::load(a.w, row, kb0, kq, cur);
+    load_w<T, TL>(a.w, n0 >> 4, ln, kb0, kq, cur);
     load_x(kb0);
     for (int kb = kb0; kb < kb1; ++kb) {
         if (kb != kb0) lds_barrier();  // the previous step's reads of xh / xl / xsum are done
         stage_x();
         lds_barrier();
         if (kb + 1 < kb1) {
-            W::load(a.w, row, kb + 1, kq, nxt);
+            load_w<T, TL>(a.w, n0 >> 4, ln, kb + 1, kq, nxt);
             load_x(kb + 1);
         }
 #pragma unroll
@@ -204,7 +204,7 @@ constexpr size_t mfma_w_lds() {
     return size_t(2) * BM * kXS * sizeof(_Float16) + size_t(16) * BM * sizeof(float);
 }
 
-template <int T, int BM, int WT>
+template <int T, int BM, int WT, bool TL>
 __global__ __launch_bounds__(512) void k_mfma_w(MfmaArgs a) {
     using W = MW<T>;
     constexpr int MT = BM / 16;
@@ -262,7 +262,7 @@ __global__ __launch_bounds__(512) void k_mfma_w(MfmaArgs a) {
 
     typename W::Regs cur[WT], nxt[WT];
 #pragma unroll
-    for (int j = 0; j < WT; ++j) W::load(a.w, min(n0 + 16 * j + ln, a.w.N - 1), kb0, kq, cur[j]);
+    for (int j = 0; j < WT; ++j) load_w<T, TL>(a.w, (n0 >> 4) + j, ln, kb0, kq, cur[j]);
     load_x(kb0);
     for (int kb = kb0; kb < kb1; ++kb) {
         if (kb != kb0) lds_barrier();  // the previous step's reads of xh / xl / xsum are done
@@ -270,7 +270,7 @@ __global__ __launch_bounds__(512) void k_mfma_w(MfmaArgs a) {
         lds_barrier();
         if (kb + 1 < kb1) {
 #pragma unroll
-            for (int j = 0; j < WT; ++j) W::load(a.w, min(n0 + 16 * j + ln, a.w.N - 1), kb + 1, kq, nxt[j]);
+            for (int j = 0; j < WT; ++j) load_w<T, TL>(a.w, (n0 >> 4) + j, ln, kb + 1, kq, nxt[j]);
             load_x(kb + 1);
         }
 #pragma unroll
@@ -370,30 +370,39 @@ int wide_wt(int N, int M) {
     return size_t((N + 255) / 256) * gy >= 192 ? 2 : 0;
 }
 
-template <int T, int BM, int WT>
+template <int T, int BM, int WT, bool TL>
 hipError_t launch_w_t(const MfmaArgs &a, int M, int ks, hipStream_t st) {
-    static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void *>(&k_mfma_w<T, BM, WT>),
+    static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void *>(&k_mfma_w<T, BM, WT, TL>),
                                                        hipFuncAttributeMaxDynamicSharedMemorySize,
                                                        int(mfma_w_lds<BM>()));
     if (attr != hipSuccess) return attr;
     const int gx = (a.w.N + 128 * WT - 1) / (128 * WT);
-    hipLaunchKernelGGL((k_mfma_w<T, BM, WT>), dim3(gx, (M + BM - 1) / BM, ks), dim3(kWWaves * 64), mfma_w_lds<BM>(),
-                       st, a);
+    hipLaunchKernelGGL((k_mfma_w<T, BM, WT, TL>), dim3(gx, (M + BM - 1) / BM, ks), dim3(kWWaves * 64),
+                       mfma_w_lds<BM>(), st, a);
     return hipGetLastError();
 }
 
-template <int T>
-hipError_t launch(const MfmaArgs &a, int M, int ks, hipStream_t st) {
-    if (wide_wt(a.w.N, M) == 2) return launch_w_t<T, 64, 2>(a, M, ks, st);
+template <int T, bool TL>
+hipError_t launch_tl(const MfmaArgs &a, int M, int ks, hipStream_t st) {
+    if (wide_wt(a.w.N, M) == 2) return launch_w_t<T, 64, 2, TL>(a, M, ks, st);
     const int gx = (a.w.N + kTileN - 1) / kTileN;
     if (M <= 16) {
-        hipLaunchKernelGGL((k_mfma<T, 16>), dim3(gx, (M + 15) / 16, ks), dim3(256), 0, st, a);
+        hipLaunchKernelGGL((k_mfma<T, 16, TL>), dim3(gx, (M + 15) / 16, ks), dim3(256), 0, st, a);
     } else if (M <= 32) {
-        hipLaunchKernelGGL((k_mfma<T, 32>), dim3(gx, 1, ks), dim3(256), 0, st, a);
+        hipLaunchKernelGGL((k_mfma<T, 32, TL>), dim3(gx, 1, ks), dim3(256), 0, st, a);
     } else {
-        hipLaunchKernelGGL((k_mfma<T, 64>), dim3(gx, (M + 63) / 64, ks), dim3(256), 0, st, a);
+        hipLaunchKernelGGL((k_mfma<T, 64, TL>), dim3(gx, (M + 63) / 64, ks), dim3(256), 0, st, a);
     }
     return hipGetLastError();
+}
+
+// q6_K with its tile-major copy reads that copy
+template <int T>
+hipError_t launch(const MfmaArgs &a, int M, int ks, hipStream_t st) {
+    if constexpr (T == GGML_Q6_K) {
+        if (a.w.t) return launch_tl<T, true>(a, M, ks, st);
+    }
+    return launch_tl<T, false>(a, M, ks, st);
 }
 
 // Split-K reduction fused with the decoder's residual add and the next LayerNorm
@@ -508,7 +517,7 @@ size_t rx_lds_bytes(int BM, int K) {
     return size_t(BM) * rx_stride(K) * 2 * sizeof(_Float16) + size_t(K / 16) * BM * sizeof(float);
 }
 
-template <int T, int BM, int MODE>
+template <int T, int BM, int MODE, bool TL>
 __global__ __launch_bounds__(kRxWaves * 64) void k_mfma_rx(RxArgs a) {
     using W = MW<T>;
     constexpr int MT = BM / 16;
@@ -530,8 +539,7 @@ __global__ __launch_bounds__(kRxWaves * 64) void k_mfma_rx(RxArgs a) {
     auto job_base = [&](int j) { return (gw + (j / nsteps) * nw) * 16 * kRxNT; };
     auto load_job = [&](int j, typename W::Regs (&r)[kRxNT]) {
 #pragma unroll
-        for (int nt = 0; nt < kRxNT; ++nt)
-            W::load(a.w, min(job_base(j) + nt * 16 + ln, a.w.N - 1), j % nsteps, kq, r[nt]);
+        for (int nt = 0; nt < kRxNT; ++nt) load_w<T, TL>(a.w, (job_base(j) >> 4) + nt, ln, j % nsteps, kq, r[nt]);
     };
 
     // stage X: chunks of 16 values, up to 4 per thread in flight
@@ -729,18 +737,27 @@ __global__ __launch_bounds__(kRxWaves * 64) void k_mfma_rx(RxArgs a) {
 }
 
 // Dynamic LDS beyond 64 KB needs the kernel attribute raised once.
-template <int T, int BM, int MODE>
+template <int T, int BM, int MODE, bool TL>
 hipError_t launch_rx_bm(const RxArgs &a, int grid, hipStream_t st) {
-    static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void *>(&k_mfma_rx<T, BM, MODE>),
+    static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void *>(&k_mfma_rx<T, BM, MODE, TL>),
                                                        hipFuncAttributeMaxDynamicSharedMemorySize, int(kRxMaxLds));
     if (attr != hipSuccess) return attr;
-    hipLaunchKernelGGL((k_mfma_rx<T, BM, MODE>), dim3(grid), dim3(kRxWaves * 64), rx_lds_bytes(BM, a.w.K), st, a);
+    hipLaunchKernelGGL((k_mfma_rx<T, BM, MODE, TL>), dim3(grid), dim3(kRxWaves * 64), rx_lds_bytes(BM, a.w.K), st,
+                       a);
     return hipGetLastError();
+}
+
+template <int T, int MODE, bool TL>
+hipError_t launch_rx_tl(const RxArgs &a, int M, int grid, hipStream_t st) {
+    return M <= 16 ? launch_rx_bm<T, 16, MODE, TL>(a, grid, st) : launch_rx_bm<T, 32, MODE, TL>(a, grid, st);
 }
 
 template <int T, int MODE>
 hipError_t launch_rx(const RxArgs &a, int M, int grid, hipStream_t st) {
-    return M <= 16 ? launch_rx_bm<T, 16, MODE>(a, grid, st) : launch_rx_bm<T, 32, MODE>(a, grid, st);
+    if constexpr (T == GGML_Q6_K) {
+        if (a.w.t) return launch_rx_tl<T, MODE, true>(a, M, grid, st);
+    }
+    return launch_rx_tl<T, MODE, false>(a, M, grid, st);
 }
 
 int rx_nt_of(uint32_t t) {

@@ -20,13 +20,14 @@ struct DevMatrix {
     // q6_K LM heads: a second copy of the quant plane in lane-major order, read by the
     // large-matrix GEMVs (layout_lane_major); null elsewhere
     uint8_t *lm = nullptr;
-    // q6_K decoder matrices (N % 16 == 0): quants, scales and d in tile-major order, read
-    // by the decode GEMMs (layout_tile_major); null elsewhere
+    // q6_K matrices of the MFMA GEMMs: quants, scales and d in tile-major order
+    // (layout_tile_major); null elsewhere
     uint8_t *tm = nullptr;
 };
 
-// Tile-major q6_K (the decode GEMMs' W operand): per 16-row tile t and 256-wide K block
-// kb, kQ6TileBytes at (t * K/256 + kb) * kQ6TileBytes.  Lane l = 16 kq + r of a wave
+// Tile-major q6_K (the MFMA GEMMs' W operand): per 16-row tile t < ceil(N / 16) and
+// 256-wide K block kb, kQ6TileBytes at (t * K/256 + kb) * kQ6TileBytes (rows past N are
+// zero).  Lane l = 16 kq + r of a wave
 // (row 16 t + r, k-group kq) finds the 12 quant dwords it multiplies as three 16-byte
 // pieces at 1024 j + 16 l (j = 0: ql[64 n + 16 h + 4 kq], 1: ql[64 n + 32 + 16 h + 4 kq],
 // 2: qh[32 n + 16 h + 4 kq], dword 2 n + h of each piece), the row's 16 scales at

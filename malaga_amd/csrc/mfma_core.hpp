@@ -193,4 +193,12 @@ struct MW<GGML_F16> {
     }
 };
 
+// W registers of row 16 tile + ln, K block kb: from the tile-major copy (TL, q6_K; a
+// tile past the last reads the last) or from the planes (the row clamped to N - 1)
+template <int T, bool TL>
+__device__ __forceinline__ void load_w(const WPtr &w, int tile, int ln, int kb, int kq, typename MW<T>::Regs &r) {
+    if constexpr (TL) MW<T>::load_tile(w.t, w.nb, min(tile, (w.N + 15) / 16 - 1), kb, kq, ln, r);
+    else MW<T>::load(w, min(16 * tile + ln, w.N - 1), kb, kq, r);
+}
+
 }  // namespace mlg

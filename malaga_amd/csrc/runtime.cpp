@@ -178,16 +178,16 @@ void layout_lane_major(int N, int K, const uint8_t *q_plane, uint8_t *out) {
 }
 
 size_t tile_major_bytes(uint32_t type, int N, int K) {
-    return type == GGML_Q6_K && N % 16 == 0 && K % 256 == 0 ? size_t(N / 16) * (K / 256) * kQ6TileBytes : 0;
+    return type == GGML_Q6_K && K % 256 == 0 ? size_t((N + 15) / 16) * (K / 256) * kQ6TileBytes : 0;
 }
 
 void layout_tile_major(int N, int K, const uint8_t *planes, size_t off_s, size_t off_d, uint8_t *out) {
     const int nb = K / 256;
     std::memset(out, 0, tile_major_bytes(GGML_Q6_K, N, K));
-    for (int t = 0; t < N / 16; ++t)
+    for (int t = 0; t < (N + 15) / 16; ++t)
         for (int kb = 0; kb < nb; ++kb) {
             uint8_t *tb = out + (size_t(t) * nb + kb) * kQ6TileBytes;
-            for (int r = 0; r < 16; ++r) {
+            for (int r = 0; r < 16 && 16 * t + r < N; ++r) {  // rows past N stay zero
                 const size_t blk = size_t(16 * t + r) * nb + kb;
                 const uint8_t *qp = planes + blk * 192;  // ql[128] | qh[64]
                 for (int kq = 0; kq < 4; ++kq) {
@@ -254,7 +254,7 @@ const GgufTensorInfo *matrix_info(GgufFile &g, const std::string &name, int n, i
 }
 }  // namespace
 
-DevMatrix Model::upload_matrix(GgufFile &g, const std::string &name, int n, int k, bool head, bool tile) {
+DevMatrix Model::upload_matrix(GgufFile &g, const std::string &name, int n, int k, bool head) {
     const GgufTensorInfo *t = matrix_info(g, name, n, k);
     DevMatrix m;
     m.type = t->type;
@@ -273,15 +273,19 @@ DevMatrix Model::upload_matrix(GgufFile &g, const std::string &name, int n, int 
     m.bytes = total;
     weight_bytes += total;
     if (head) upload_lane_major(m, host.data());
-    if (const size_t tb = tile ? tile_major_bytes(m.type, n, k) : 0) {
-        std::vector<uint8_t> tmh(tb);
-        layout_tile_major(n, k, host.data(), off_s, off_d, tmh.data());
-        m.tm = static_cast<uint8_t *>(dev_alloc(tb, (name + " (tile-major)").c_str()));
-        owned_.push_back(m.tm);
-        check_hip(hipMemcpy(m.tm, tmh.data(), tb, hipMemcpyHostToDevice), "upload");
-        weight_bytes += tb;
-    }
+    upload_tile_major(m, host.data(), off_s, off_d);
     return m;
+}
+
+void Model::upload_tile_major(DevMatrix &m, const uint8_t *planes, size_t off_s, size_t off_d) {
+    const size_t tb = tile_major_bytes(m.type, m.N, m.K);
+    if (!tb) return;
+    std::vector<uint8_t> tmh(tb);
+    layout_tile_major(m.N, m.K, planes, off_s, off_d, tmh.data());
+    m.tm = static_cast<uint8_t *>(dev_alloc(tb, "q6_K matrix (tile-major)"));
+    owned_.push_back(m.tm);
+    check_hip(hipMemcpy(m.tm, tmh.data(), tb, hipMemcpyHostToDevice), "upload");
+    weight_bytes += tb;
 }
 
 void Model::upload_lane_major(DevMatrix &m, const uint8_t *q_plane) {
@@ -295,9 +299,9 @@ void Model::upload_lane_major(DevMatrix &m, const uint8_t *q_plane) {
     weight_bytes += lb;
 }
 
-Linear Model::load_linear(GgufFile &g, const std::string &name, int n, int k, bool tile) {
+Linear Model::load_linear(GgufFile &g, const std::string &name, int n, int k) {
     Linear l;
-    l.w = upload_matrix(g, name + ".weight", n, k, false, tile);
+    l.w = upload_matrix(g, name + ".weight", n, k);
     l.b = upload_f32(g, name + ".bias", n);
     return l;
 }
@@ -336,6 +340,7 @@ Linear Model::load_stacked(GgufFile &g, const std::string &suffix, int layers, i
     l.w.s = d + off_s;
     l.w.d = d + off_d;
     l.w.bytes = total;
+    upload_tile_major(l.w, host.data(), off_s, off_d);
     l.b = static_cast<float *>(dev_alloc(bias.size() * 4, ("dec.blk.*" + suffix + " bias").c_str()));
     owned_.push_back(l.b);
     check_hip(hipMemcpy(l.b, bias.data(), bias.size() * 4, hipMemcpyHostToDevice), "upload");
@@ -462,15 +467,14 @@ void Model::load(const std::string &path) {
         const std::string p = "dec.blk." + std::to_string(i);
         DecLayer l;
         l.attn_norm = load_ln(g, p + ".attn_norm", d);
-        // the decode GEMMs' q6_K matrices also get their tile-major copy
-        l.qkv = load_linear(g, p + ".attn_qkv", 3 * d, d, true);
-        l.out = load_linear(g, p + ".attn_out", d, d, true);
+        l.qkv = load_linear(g, p + ".attn_qkv", 3 * d, d);
+        l.out = load_linear(g, p + ".attn_out", d, d);
         l.cross_norm = load_ln(g, p + ".cross_attn_norm", d);
-        l.cross_q = load_linear(g, p + ".cross_attn_q", d, d, true);
-        l.cross_out = load_linear(g, p + ".cross_attn_out", d, d, true);
+        l.cross_q = load_linear(g, p + ".cross_attn_q", d, d);
+        l.cross_out = load_linear(g, p + ".cross_attn_out", d, d);
         l.ffn_norm = load_ln(g, p + ".ffn_norm", d);
-        l.up = load_linear(g, p + ".ffn_up", cfg.decoder_ffn, d, true);
-        l.down = load_linear(g, p + ".ffn_down", d, cfg.decoder_ffn, true);
+        l.up = load_linear(g, p + ".ffn_up", cfg.decoder_ffn, d);
+        l.down = load_linear(g, p + ".ffn_down", d, cfg.decoder_ffn);
         dec.push_back(l);
     }
     cross_kv = load_stacked(g, ".cross_attn_kv", cfg.decoder_layers, 2 * d, d);
@@ -519,6 +523,7 @@ void Model::ensure_embed() {
     embed.d = d + off_d;
     weight_bytes += total;
     upload_lane_major(embed, host.data());
+    upload_tile_major(embed, host.data(), off_s, off_d);
     embed_host_.clear();
     embed_host_.shrink_to_fit();
 }

@@ -245,15 +245,14 @@ class Model {
     // call allocates only the cross K/V it returns.
     void *enc_ws_ = nullptr;
     size_t enc_ws_bytes_ = 0;
-    // tile: also the tile-major copy a q6_K decoder matrix carries for the decode GEMMs
-    Linear load_linear(class GgufFile &g, const std::string &name, int n, int k, bool tile = false);
+    Linear load_linear(class GgufFile &g, const std::string &name, int n, int k);
     LNorm load_ln(class GgufFile &g, const std::string &name, int d);
     float *upload_f32(class GgufFile &g, const std::string &name, int64_t n);
-    // head: also the lane-major quant copy of a q6_K LM head (DevMatrix::lm); tile: the
-    // tile-major copy of a q6_K decoder matrix (DevMatrix::tm)
-    DevMatrix upload_matrix(class GgufFile &g, const std::string &name, int n, int k, bool head = false,
-                            bool tile = false);
+    // q6_K: also the tile-major copy (DevMatrix::tm); head: the lane-major quant copy of a
+    // q6_K LM head (DevMatrix::lm)
+    DevMatrix upload_matrix(class GgufFile &g, const std::string &name, int n, int k, bool head = false);
     void upload_lane_major(DevMatrix &m, const uint8_t *q_plane);
+    void upload_tile_major(DevMatrix &m, const uint8_t *planes, size_t off_s, size_t off_d);
     Linear load_stacked(class GgufFile &g, const std::string &suffix, int layers, int n, int k);
     void matmul(const Linear &l, const float *x, int rows, float *y, bool relu, const float *resid);
     // final_ln: end with h = dec_norm(x + y); otherwise return x for the LM head to

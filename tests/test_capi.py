@@ -49,27 +49,35 @@ def test_q6k_tile_major_copy_holds_what_each_lane_reads():
     (ql[128] | qh[64] | int8 scales[16] | f16 d per 256 values): lane 16 kq + r of tile t
     finds, for K block kb, ql[64 n + 16 h + 4 kq .. +4] (piece 0), ql[64 n + 32 + 16 h + 4 kq
     .. +4] (piece 1) and qh[32 n + 16 h + 4 kq .. +4] (piece 2) as dword 2 n + h of its
-    16-byte piece, then row 16 t + r's scales and d.  Every quant byte is read exactly once."""
+    16-byte piece, then row 16 t + r's scales and d.  Every quant byte is read exactly once;
+    the rows that pad N to a multiple of 16 are zero."""
     import numpy as np
 
     lib = _lib.load()
-    N, K = 48, 768
+    N, K = 40, 768
     nb = K // 256
     rng = np.random.default_rng(7)
     rows = rng.integers(0, 256, size=(N, nb, 210), dtype=np.uint8)
     src = np.ascontiguousarray(rows)
     size = lib.mlg_debug_tile_major(14, N, K, src.ctypes.data, None, 0)
-    assert size == (N // 16) * nb * 3456
+    assert size == 3 * nb * 3456
     out = np.zeros(size, dtype=np.uint8)
     assert lib.mlg_debug_tile_major(14, N, K, src.ctypes.data, out.ctypes.data, size) == size
-    # no tile-major form: other types, N not a multiple of 16
+    # no tile-major form: other types, K not a whole number of q6_K blocks
     assert lib.mlg_debug_tile_major(12, N, K, src.ctypes.data, None, 0) == 0
-    assert lib.mlg_debug_tile_major(14, N - 8, K, src.ctypes.data, None, 0) == 0
+    assert lib.mlg_debug_tile_major(14, N, 128, src.ctypes.data, None, 0) == 0
     seen = np.zeros((N, nb, 192), dtype=np.int32)
-    for t in range(N // 16):
+    for t in range(3):
         for kb in range(nb):
             tb = out[(t * nb + kb) * 3456:(t * nb + kb + 1) * 3456]
             for r in range(16):
+                if 16 * t + r >= N:
+                    for piece in range(3):
+                        for kq in range(4):
+                            lane = 16 * kq + r
+                            assert not tb[1024 * piece + 16 * lane:1024 * piece + 16 * lane + 16].any()
+                    assert not tb[3072 + 16 * r:3088 + 16 * r].any() and not tb[3328 + 2 * r:3330 + 2 * r].any()
+                    continue
                 blk = rows[16 * t + r, kb]
                 for kq in range(4):
                     lane = 16 * kq + r
