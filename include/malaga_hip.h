@@ -205,7 +205,7 @@ int mlg_graph_stats(const mlg_model *m, int *entries, int *graphs, int *capture_
 int mlg_graph_cache_keys(const mlg_model *m, int *keys, int cap);
 /* Test hook: the n-th following device allocation fails with MLG_ERR_OOM (n < 0: off). */
 void mlg_debug_fail_alloc_after(long n);
-/* Test hook: the tile-major copy the MFMA GEMMs read for q6_K GGUF rows [N][K] (K % 256
+/* Test hook: the tile-major copy the MFMA GEMMs read for q6_K / q4_K GGUF rows [N][K] (K % 256
    == 0; rows past N padded to a multiple of 16 with zeros): returns its size in bytes
    (0: the type or shape has none) and
    writes it to out when cap holds it.  No counterpart in the reference (the layout is this

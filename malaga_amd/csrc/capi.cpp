@@ -513,7 +513,7 @@ int64_t mlg_debug_tile_major(uint32_t type, int N, int K, const void *gguf_rows,
     std::vector<uint8_t> host(mlg::planes_bytes(type, N, K));
     size_t off_s, off_d, total;
     mlg::layout_planes(type, N, K, static_cast<const uint8_t *>(gguf_rows), host.data(), &off_s, &off_d, &total);
-    mlg::layout_tile_major(N, K, host.data(), off_s, off_d, static_cast<uint8_t *>(out));
+    mlg::layout_tile_major(type, N, K, host.data(), off_s, off_d, static_cast<uint8_t *>(out));
     return int64_t(tb);
 }
 

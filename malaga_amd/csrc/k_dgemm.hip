@@ -66,7 +66,7 @@ constexpr int kLnQ = kDgMaxLnK / 16 / kLnTPR;       // partials per thread at mo
 
 // BPW: K blocks per wave (compile time, it sizes the fragment ring); NT: 16-column tiles
 // per workgroup (1 or 2; with 2, each X fragment, once normalized and split, feeds two
-// tiles); TL: W from the tile-major copy a.w.t (q6_K); the wave count NW (4 or 8) is
+// tiles); TL: W from the tile-major copy a.w.t (q6_K / q4_K); the wave count NW (4 or 8) is
 // blockDim.x / 64.
 template <int T, int BPW, int NT, int PRO, int EPI, bool TL>
 __global__ __launch_bounds__(kDgMaxNW * 64) void k_dgemm(DArgs a) {
@@ -367,10 +367,10 @@ hipError_t launch_dgemm_l(const DArgs &a, hipStream_t st) {
     return hipGetLastError();
 }
 
-// q6_K with its tile-major copy reads that copy
+// q6_K / q4_K with its tile-major copy reads that copy
 template <int T, int BPW, int PRO, int EPI>
 hipError_t launch_dgemm(const DArgs &a, hipStream_t st) {
-    if constexpr (T == GGML_Q6_K) {
+    if constexpr (T == GGML_Q6_K || T == GGML_Q4_K) {
         if (a.w.t) return launch_dgemm_l<T, BPW, PRO, EPI, true>(a, st);
     }
     return launch_dgemm_l<T, BPW, PRO, EPI, false>(a, st);

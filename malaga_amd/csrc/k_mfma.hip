@@ -39,7 +39,7 @@ struct MfmaArgs {
 };
 
 
-// TL (all three GEMM kernels): W from the tile-major copy a.w.t (q6_K)
+// TL (all three GEMM kernels): W from the tile-major copy a.w.t (q6_K / q4_K)
 template <int T, int BM, bool TL>
 __global__ __launch_bounds__(256) void k_mfma(MfmaArgs a) {
     using W = MW<T>;
@@ -396,10 +396,10 @@ hipError_t launch_tl(const MfmaArgs &a, int M, int ks, hipStream_t st) {
     return hipGetLastError();
 }
 
-// q6_K with its tile-major copy reads that copy
+// q6_K / q4_K with its tile-major copy reads that copy
 template <int T>
 hipError_t launch(const MfmaArgs &a, int M, int ks, hipStream_t st) {
-    if constexpr (T == GGML_Q6_K) {
+    if constexpr (T == GGML_Q6_K || T == GGML_Q4_K) {
         if (a.w.t) return launch_tl<T, true>(a, M, ks, st);
     }
     return launch_tl<T, false>(a, M, ks, st);
@@ -754,7 +754,7 @@ hipError_t launch_rx_tl(const RxArgs &a, int M, int grid, hipStream_t st) {
 
 template <int T, int MODE>
 hipError_t launch_rx(const RxArgs &a, int M, int grid, hipStream_t st) {
-    if constexpr (T == GGML_Q6_K) {
+    if constexpr (T == GGML_Q6_K || T == GGML_Q4_K) {
         if (a.w.t) return launch_rx_tl<T, MODE, true>(a, M, grid, st);
     }
     return launch_rx_tl<T, MODE, false>(a, M, grid, st);

@@ -20,22 +20,26 @@ struct DevMatrix {
     // q6_K LM heads: a second copy of the quant plane in lane-major order, read by the
     // large-matrix GEMVs (layout_lane_major); null elsewhere
     uint8_t *lm = nullptr;
-    // q6_K matrices of the MFMA GEMMs: quants, scales and d in tile-major order
-    // (layout_tile_major); null elsewhere
+    // q6_K / q4_K matrices: the MFMA GEMMs' copy in tile-major order (layout_tile_major);
+    // null elsewhere
     uint8_t *tm = nullptr;
 };
 
-// Tile-major q6_K (the MFMA GEMMs' W operand): per 16-row tile t < ceil(N / 16) and
-// 256-wide K block kb, kQ6TileBytes at (t * K/256 + kb) * kQ6TileBytes (rows past N are
-// zero).  Lane l = 16 kq + r of a wave
-// (row 16 t + r, k-group kq) finds the 12 quant dwords it multiplies as three 16-byte
-// pieces at 1024 j + 16 l (j = 0: ql[64 n + 16 h + 4 kq], 1: ql[64 n + 32 + 16 h + 4 kq],
-// 2: qh[32 n + 16 h + 4 kq], dword 2 n + h of each piece), the row's 16 scales at
-// 3072 + 16 r and its d at 3328 + 2 r.  Every load of a wave then reads whole cache lines.
+// Tile-major q6_K / q4_K (the MFMA GEMMs' W operand): per 16-row tile t < ceil(N / 16)
+// and 256-wide K block kb, B bytes at (t * K/256 + kb) * B (rows past N are zero).  Lane
+// l = 16 kq + r of a wave (row 16 t + r, k-group kq) finds what it multiplies in 16-byte
+// pieces at 1024 j + 16 l, so every load of a wave reads whole cache lines:
+//   q6_K (B = kQ6TileBytes): pieces j = 0: ql[64 n + 16 h + 4 kq], 1: ql[64 n + 32 + 16 h
+//     + 4 kq], 2: qh[32 n + 16 h + 4 kq] (4 bytes each, dword 2 n + h of the piece); the
+//     row's 16 scales at 3072 + 16 r and its f16 d at 3328 + 2 r;
+//   q4_K (B = kQ4TileBytes): the row's 16-byte header (d, dmin, packed scales) at 16 r;
+//     pieces at 256 + 1024 j + 16 l: qs[32 g + 8 kq .. + 8] for g = 2 j, 2 j + 1.
 constexpr int kQ6TileBytes = 3456;
+constexpr int kQ4TileBytes = 2304;
 size_t tile_major_bytes(uint32_t type, int N, int K);  // 0: no tile-major form
 // planes: q | s | d as layout_planes writes them (off_s, off_d: the plane offsets)
-void layout_tile_major(int N, int K, const uint8_t *planes, size_t off_s, size_t off_d, uint8_t *out);
+void layout_tile_major(uint32_t type, int N, int K, const uint8_t *planes, size_t off_s, size_t off_d,
+                       uint8_t *out);
 
 // Splits/copies GGUF rows [N][K] of `type` into the device layout (host side).
 // Fills `host_planes` with q | s | d concatenated and the plane offsets.

@@ -45,6 +45,16 @@ struct MW<GGML_Q4_K> {
 #pragma unroll
         for (int g = 0; g < 4; ++g) r.q[g] = *reinterpret_cast<const uint2 *>(blk + 16 + 32 * g + 8 * kq);
     }
+    // the same registers from the tile-major copy (kQ4TileBytes per tile and block)
+    __device__ static void load_tile(const uint8_t *tw, int nb, int tile, int kb, int kq, int ln, Regs &r) {
+        const uint8_t *tb = tw + (size_t(tile) * nb + kb) * kQ4TileBytes;
+        const int li = 16 * kq + ln;
+        r.hdr = *reinterpret_cast<const uint4 *>(tb + 16 * ln);
+        const uint4 a = *reinterpret_cast<const uint4 *>(tb + 256 + 16 * li);
+        const uint4 b = *reinterpret_cast<const uint4 *>(tb + 1280 + 16 * li);
+        r.q[0] = make_uint2(a.x, a.y), r.q[1] = make_uint2(a.z, a.w);
+        r.q[2] = make_uint2(b.x, b.y), r.q[3] = make_uint2(b.z, b.w);
+    }
     __device__ static h8_t b(const Regs &r, int s) {
         const uint2 q = r.q[s >> 1];
         const int sh = 4 * (s & 1);
@@ -193,7 +203,7 @@ struct MW<GGML_F16> {
     }
 };
 
-// W registers of row 16 tile + ln, K block kb: from the tile-major copy (TL, q6_K; a
+// W registers of row 16 tile + ln, K block kb: from the tile-major copy (TL, q6_K / q4_K; a
 // tile past the last reads the last) or from the planes (the row clamped to N - 1)
 template <int T, bool TL>
 __device__ __forceinline__ void load_w(const WPtr &w, int tile, int ln, int kb, int kq, typename MW<T>::Regs &r) {

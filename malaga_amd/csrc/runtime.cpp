@@ -178,12 +178,29 @@ void layout_lane_major(int N, int K, const uint8_t *q_plane, uint8_t *out) {
 }
 
 size_t tile_major_bytes(uint32_t type, int N, int K) {
-    return type == GGML_Q6_K && K % 256 == 0 ? size_t((N + 15) / 16) * (K / 256) * kQ6TileBytes : 0;
+    const int B = type == GGML_Q6_K ? kQ6TileBytes : type == GGML_Q4_K ? kQ4TileBytes : 0;
+    return B && K % 256 == 0 ? size_t((N + 15) / 16) * (K / 256) * B : 0;
 }
 
-void layout_tile_major(int N, int K, const uint8_t *planes, size_t off_s, size_t off_d, uint8_t *out) {
+void layout_tile_major(uint32_t type, int N, int K, const uint8_t *planes, size_t off_s, size_t off_d,
+                       uint8_t *out) {
     const int nb = K / 256;
-    std::memset(out, 0, tile_major_bytes(GGML_Q6_K, N, K));
+    std::memset(out, 0, tile_major_bytes(type, N, K));
+    if (type == GGML_Q4_K) {  // GGUF blocks as they are: header[16] | qs[128]
+        for (int t = 0; t < (N + 15) / 16; ++t)
+            for (int kb = 0; kb < nb; ++kb) {
+                uint8_t *tb = out + (size_t(t) * nb + kb) * kQ4TileBytes;
+                for (int r = 0; r < 16 && 16 * t + r < N; ++r) {  // rows past N stay zero
+                    const uint8_t *blk = planes + (size_t(16 * t + r) * nb + kb) * 144;
+                    std::memcpy(tb + 16 * r, blk, 16);
+                    for (int kq = 0; kq < 4; ++kq)
+                        for (int g = 0; g < 4; ++g)  // the 8-byte groups MW<GGML_Q4_K>::load reads
+                            std::memcpy(tb + 256 + 1024 * (g >> 1) + 16 * (16 * kq + r) + 8 * (g & 1),
+                                        blk + 16 + 32 * g + 8 * kq, 8);
+                }
+            }
+        return;
+    }
     for (int t = 0; t < (N + 15) / 16; ++t)
         for (int kb = 0; kb < nb; ++kb) {
             uint8_t *tb = out + (size_t(t) * nb + kb) * kQ6TileBytes;
@@ -281,8 +298,8 @@ void Model::upload_tile_major(DevMatrix &m, const uint8_t *planes, size_t off_s,
     const size_t tb = tile_major_bytes(m.type, m.N, m.K);
     if (!tb) return;
     std::vector<uint8_t> tmh(tb);
-    layout_tile_major(m.N, m.K, planes, off_s, off_d, tmh.data());
-    m.tm = static_cast<uint8_t *>(dev_alloc(tb, "q6_K matrix (tile-major)"));
+    layout_tile_major(m.type, m.N, m.K, planes, off_s, off_d, tmh.data());
+    m.tm = static_cast<uint8_t *>(dev_alloc(tb, "matrix (tile-major)"));
     owned_.push_back(m.tm);
     check_hip(hipMemcpy(m.tm, tmh.data(), tb, hipMemcpyHostToDevice), "upload");
     weight_bytes += tb;

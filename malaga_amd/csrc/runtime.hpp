@@ -248,7 +248,7 @@ class Model {
     Linear load_linear(class GgufFile &g, const std::string &name, int n, int k);
     LNorm load_ln(class GgufFile &g, const std::string &name, int d);
     float *upload_f32(class GgufFile &g, const std::string &name, int64_t n);
-    // q6_K: also the tile-major copy (DevMatrix::tm); head: the lane-major quant copy of a
+    // q6_K / q4_K: also the tile-major copy (DevMatrix::tm); head: the lane-major quant copy of a
     // q6_K LM head (DevMatrix::lm)
     DevMatrix upload_matrix(class GgufFile &g, const std::string &name, int n, int k, bool head = false);
     void upload_lane_major(DevMatrix &m, const uint8_t *q_plane);

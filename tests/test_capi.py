@@ -64,7 +64,7 @@ def test_q6k_tile_major_copy_holds_what_each_lane_reads():
     out = np.zeros(size, dtype=np.uint8)
     assert lib.mlg_debug_tile_major(14, N, K, src.ctypes.data, out.ctypes.data, size) == size
     # no tile-major form: other types, K not a whole number of q6_K blocks
-    assert lib.mlg_debug_tile_major(12, N, K, src.ctypes.data, None, 0) == 0
+    assert lib.mlg_debug_tile_major(8, N, K, src.ctypes.data, None, 0) == 0  # q8_0
     assert lib.mlg_debug_tile_major(14, N, 128, src.ctypes.data, None, 0) == 0
     seen = np.zeros((N, nb, 192), dtype=np.int32)
     for t in range(3):
@@ -92,4 +92,39 @@ def test_q6k_tile_major_copy_holds_what_each_lane_reads():
                 assert (tb[3072 + 16 * r:3088 + 16 * r] == blk[192:208]).all()
                 assert (tb[3328 + 2 * r:3330 + 2 * r] == blk[208:210]).all()
             assert not tb[3360:].any()
+    assert (seen == 1).all()
+
+
+def test_q4k_tile_major_copy_holds_what_each_lane_reads():
+    """The q4_K tile-major copy against the GGUF q4_K block (f16 d | f16 dmin | 12 bytes of
+    packed scales | qs[128] per 256 values): row 16 t + r's 16-byte header at 16 r, and lane
+    16 kq + r's 8-byte groups qs[32 g + 8 kq .. + 8] at 256 + 1024 (g / 2) + 16 lane + 8 (g % 2).
+    Every qs byte is read exactly once; padding rows are zero."""
+    import numpy as np
+
+    lib = _lib.load()
+    N, K = 24, 512
+    nb = K // 256
+    rows = np.random.default_rng(8).integers(0, 256, size=(N, nb, 144), dtype=np.uint8)
+    size = lib.mlg_debug_tile_major(12, N, K, rows.ctypes.data, None, 0)
+    assert size == 2 * nb * 2304
+    out = np.zeros(size, dtype=np.uint8)
+    assert lib.mlg_debug_tile_major(12, N, K, rows.ctypes.data, out.ctypes.data, size) == size
+    seen = np.zeros((N, nb, 128), dtype=np.int32)
+    for t in range(2):
+        for kb in range(nb):
+            tb = out[(t * nb + kb) * 2304:(t * nb + kb + 1) * 2304]
+            for r in range(16):
+                n = 16 * t + r
+                for kq in range(4):
+                    lane = 16 * kq + r
+                    for g in range(4):
+                        o = 256 + 1024 * (g // 2) + 16 * lane + 8 * (g % 2)
+                        if n >= N:
+                            assert not tb[o:o + 8].any()
+                            continue
+                        assert (tb[o:o + 8] == rows[n, kb, 16 + 32 * g + 8 * kq:24 + 32 * g + 8 * kq]).all()
+                        seen[n, kb, 32 * g + 8 * kq:32 * g + 8 * kq + 8] += 1
+                want = rows[n, kb, :16] if n < N else np.zeros(16, np.uint8)
+                assert (tb[16 * r:16 * r + 16] == want).all()
     assert (seen == 1).all()

@@ -111,11 +111,14 @@ def test_lazy_embeddings(sl_models, model_dir, monkeypatch):
     monkeypatch.delenv("MALAGA_LAZY_EMBEDDINGS")
     raw, info = tensor_bytes(p, "token_embd.weight")
     # the resident table, plus the lane-major quant copy a q6_K LM head carries (192 B per
-    # block) and its tile-major copy (3456 B per 16-row tile and 256-wide block)
+    # block) and the tile-major copy of a q6_K / q4_K one (3456 / 2304 B per 16-row tile and
+    # 256-wide block)
     emb_bytes = raw.size
+    K, V = info["ne"][0], info["ne"][1]
     if info["type"] == 14:
-        K, V = info["ne"][0], info["ne"][1]
         emb_bytes += raw.size // 210 * 192 + (V + 15) // 16 * (K // 256) * 3456
+    elif info["type"] == 12:
+        emb_bytes += (V + 15) // 16 * (K // 256) * 2304
     assert lazy.weight_bytes == eager.weight_bytes - emb_bytes
     for nb in (4, 7):
         src = _sources(nb, 70 + nb)
