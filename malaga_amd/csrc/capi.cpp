@@ -33,9 +33,11 @@ struct mlg_matrix {
     mlg::DevMatrix w;
     void *mem = nullptr;
     void *mem_lm = nullptr;
+    void *mem_tm = nullptr;
     ~mlg_matrix() {
         mlg::dev_free(mem);
         mlg::dev_free(mem_lm);
+        mlg::dev_free(mem_tm);
     }
     mlg_ctx *ctx = nullptr;
 };
@@ -549,6 +551,13 @@ int mlg_matrix_upload(mlg_ctx *ctx, uint32_t type, int N, int K, const void *ggu
             w->mem_lm = mlg::dev_alloc(lb, "matrix (lane-major quants)");
             w->w.lm = static_cast<uint8_t *>(w->mem_lm);
             mlg::check_hip(hipMemcpy(w->mem_lm, lm.data(), lb, hipMemcpyHostToDevice), "upload");
+        }
+        if (const size_t tb = mlg::tile_major_bytes(type, N, K)) {  // as the model's q6_K / q4_K ones
+            std::vector<uint8_t> tm(tb);
+            mlg::layout_tile_major(type, N, K, host.data(), off_s, off_d, tm.data());
+            w->mem_tm = mlg::dev_alloc(tb, "matrix (tile-major)");
+            w->w.tm = static_cast<uint8_t *>(w->mem_tm);
+            mlg::check_hip(hipMemcpy(w->mem_tm, tm.data(), tb, hipMemcpyHostToDevice), "upload");
         }
         *out = w.release();
         return MLG_OK;

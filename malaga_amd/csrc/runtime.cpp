@@ -373,6 +373,9 @@ DevMatrix rows_view(const DevMatrix &w, int r0, int n) {
     v.N = n;
     v.lm = nullptr;
     v.bytes = size_t(n) * nb * ti.block_bytes;
+    // the tile-major copy from tile r0 / 16 on (a view starting inside a tile has none)
+    const size_t tb = tile_major_bytes(w.type, 16, w.K);
+    v.tm = w.tm && r0 % 16 == 0 ? w.tm + size_t(r0 / 16) * tb : nullptr;
     if (w.type == GGML_Q6_K) {  // planes: quants 192, scales 16, d 2 bytes per block
         v.q = w.q + b0 * 192;
         v.s = w.s + b0 * 16;
@@ -608,8 +611,12 @@ std::unique_ptr<Batch> Model::encode(const std::vector<std::vector<uint32_t>> &s
     const size_t n_act = (size_t(M) * d * 4 + 255) & ~size_t(255);
     const size_t n_qkv = (size_t(M) * std::max(3 * d, f) * 4 + 255) & ~size_t(255);
     // cross K/V of all decoder layers per GEMM while the f32 staging stays <= 128 MB
+    // (MALAGA_CROSS_KV_STAGING_MB, a test hook, sets another budget; 0: one layer per GEMM)
+    size_t staging = size_t(128) << 20;
+    if (const char *e = std::getenv("MALAGA_CROSS_KV_STAGING_MB"))
+        staging = size_t(std::strtoull(e, nullptr, 10)) << 20;
     const int L = int(dec.size()), per_layer = int(std::min<size_t>(std::max<size_t>(size_t(L), 1),
-                                                    std::max<size_t>(1, (size_t(128) << 20) / (size_t(M) * 2 * d * 4))));
+                                                    std::max<size_t>(1, staging / (size_t(M) * 2 * d * 4))));
     const size_t n_kv = (size_t(M) * 2 * d * 4 * per_layer + 255) & ~size_t(255);
     // lazy embeddings: the batch's token_embd rows, gathered on the host (src/model.rs:269-273)
     const size_t n_rows = embed.q ? 0 : (planes_bytes(embed.type, M, d) + 255) & ~size_t(255);

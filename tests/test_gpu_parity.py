@@ -259,6 +259,30 @@ def test_batched_decode_mfma_path(kq_gguf, models, preset, nb):
     assert np.abs(lg - orc.teacher_forced_logits(src, tgt, kv_f16=True)).max() < 2e-3
 
 
+@pytest.mark.parametrize("preset", ["q4_k_m", "q6_k"])
+def test_cross_kv_in_layer_chunks(kq_gguf, models, preset, monkeypatch):
+    """The encoder computes the stacked cross K/V of several decoder layers per GEMM while
+    its f32 staging fits a budget; past it, later chunks read row views of the stacked
+    matrix (their planes and tile-major copies from the chunk's first row on).  With the
+    budget at 0 every layer is a chunk of its own: same tokens and logits as the oracle."""
+    gpu, orc = models(kq_gguf(preset))
+    rng = np.random.default_rng(450)
+    src = [[997] + rng.integers(4, 990, int(n)).tolist() + [2] for n in rng.integers(2, 40, 16)]
+    want, gap = orc.translate_batch(src, 998, max_batch=64, kv_f16=True, max_new_tokens=10)
+    T = 8
+    tgt = np.zeros((len(src), T), np.uint32)
+    tgt[:, 0], tgt[:, 1] = 2, 998
+    tgt[:, 2:] = rng.integers(4, 990, (len(src), T - 2))
+    monkeypatch.setenv("MALAGA_CROSS_KV_STAGING_MB", "0")
+    got = gpu.generate(src, 998, M.GenOptions(max_new_tokens=10, max_batch=64))
+    one = gpu.generate(src[:1], 998, M.GenOptions(max_new_tokens=10))
+    lg = gpu.teacher_forced_logits(src, tgt)
+    monkeypatch.delenv("MALAGA_CROSS_KV_STAGING_MB")
+    assert got == want, f"min top-2 gap {gap}"
+    assert one == want[:1]
+    assert np.abs(lg - orc.teacher_forced_logits(src, tgt, kv_f16=True)).max() < 2e-3
+
+
 def test_config5_shapes_batch64(model_dir, models):
     """BASELINE config 5 shapes (NLLB-3.3B: d_model 2048, 16 heads of 128, FFN 8192,
     q4_k_m) at two layers and a 4096-token vocabulary so that the oracle finishes in
