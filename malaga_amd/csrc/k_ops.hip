@@ -398,27 +398,44 @@ __global__ __launch_bounds__(256) void k_attn_waves(const float *q, const __half
                                                     const uint32_t *rows, int out_split) {
     constexpr int TPK = HD / 8, SPL = 64 / TPK, U = 8;
     __shared__ float wsc_all[4 * 512];
-    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    // w a scalar: the pair, its row and the key count stay in scalar registers
+    const int lane = threadIdx.x & 63, w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int p = blockIdx.x * 4 + w;
     if (p >= b * H) return;  // wave-uniform; no workgroup barrier below
     float *wsc = wsc_all + w * 512;
     const int bi = p / H, hh = p % H, d = H * HD;
     const int sub = lane % TPK, split = lane / TPK;
-    const int n = lens ? int(lens[bi]) : int(*step) + 1;
-    const float *qp = q + size_t(bi) * d + hh * HD + sub * 8;
-    const float4 qa = *reinterpret_cast<const float4 *>(qp), qb = *reinterpret_cast<const float4 *>(qp + 4);
-    float m = -INFINITY, l = 0.f;
-    float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-    for (int j0 = 0; j0 < n; j0 += U * SPL) {
-        uint4 kr[U], vr[U];
+    // Order of issue: the first chunk's cache rows (beam's row map) and keys/values, q,
+    // then the key count.  The addresses do not depend on the count (keys past it are
+    // masked when used), so the chunk is not held back by that scalar read; the loads
+    // complete in order.
+    uint4 kr[U], vr[U];
+    auto load_chunk = [&](int j0) {
+        size_t r[U];
+        if (rows) {  // kernel argument: wave-uniform
+#pragma unroll
+            for (int u = 0; u < U; ++u) r[u] = rows[size_t(bi) * L + min(j0 + u * SPL + split, L - 1)];
+        } else {
+#pragma unroll
+            for (int u = 0; u < U; ++u) r[u] = size_t(bi);
+        }
 #pragma unroll
         for (int u = 0; u < U; ++u) {
             const int j = min(j0 + u * SPL + split, L - 1);
-            const size_t r = rows ? rows[size_t(bi) * L + j] : size_t(bi);
-            const size_t o = ((r * H + hh) * L + j) * HD + sub * 8;
+            const size_t o = ((r[u] * H + hh) * L + j) * HD + sub * 8;
             kr[u] = *reinterpret_cast<const uint4 *>(K + o);
             vr[u] = *reinterpret_cast<const uint4 *>(V + o);
         }
+    };
+    load_chunk(0);
+    const float *qp = q + size_t(bi) * d + hh * HD + sub * 8;
+    const float4 qa = *reinterpret_cast<const float4 *>(qp), qb = *reinterpret_cast<const float4 *>(qp + 4);
+    __builtin_amdgcn_sched_barrier(0);
+    const int n = lens ? int(lens[bi]) : int(*step) + 1;
+    float m = -INFINITY, l = 0.f;
+    float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    for (int j0 = 0; j0 < n; j0 += U * SPL) {
+        if (j0) load_chunk(j0);
         float sc[U];
         float cmax = -INFINITY;
 #pragma unroll
