@@ -299,6 +299,88 @@ struct HeadArgs {
 constexpr int kHeadCols = 256;  // max columns (HG * HD) per workgroup
 constexpr int kHeadParts = 8;   // head groups are sized so that P = H / HG <= this when possible
 
+// ---- one (row, head) pair shared by two waves (batch 1, head groups of <= 2 heads) ----
+// Wave q of the pair takes the SPL-key groups 2 i + q: pass u of its chunk c covers keys
+// SPL (2 (c U2 + u) + q) + split.  Each wave keeps an online softmax over its keys and
+// leaves its partial in LDS: po[HD] = sum_j p_j v_j (unnormalized), pml = (max, sum_j p_j)
+// with p_j = exp(s_j - max).  attn_combine2 then rescales the two partials to their common
+// max and divides: the same keys and the same order of sums whichever kernel runs it.
+constexpr int kHalfU = 4;                  // passes per chunk of a half
+constexpr int kHalfSlot = 128 + 2;         // floats of one wave's partial (HD <= 128)
+__host__ __device__ constexpr int half_key(int spl, int c, int u, int q) { return spl * (2 * (c * kHalfU + u) + q); }
+
+template <int HD, class LoadF>
+__device__ __forceinline__ void attn_half(int n, int q, const float4 &qa, const float4 &qb, const uint4 (&kr)[kHalfU],
+                                          const uint4 (&vr)[kHalfU], LoadF &&load, float *wsc, float *slot) {
+    constexpr int TPK = HD / 8, SPL = 64 / TPK;
+    const int lane = threadIdx.x & 63, sub = lane % TPK, split = lane / TPK;
+    float m = -INFINITY, l = 0.f;
+    float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    for (int c = 0; half_key(SPL, c, 0, q) < n; ++c) {  // wave-uniform; chunk 0 is in flight
+        if (c) load(c);
+        float sc[kHalfU];
+        float cmax = -INFINITY;
+#pragma unroll
+        for (int u = 0; u < kHalfU; ++u) {
+            float s = h2f(kr[u].x) * qa.x;
+            s = fmaf(h2f(kr[u].x >> 16), qa.y, s);
+            s = fmaf(h2f(kr[u].y), qa.z, s);
+            s = fmaf(h2f(kr[u].y >> 16), qa.w, s);
+            s = fmaf(h2f(kr[u].z), qb.x, s);
+            s = fmaf(h2f(kr[u].z >> 16), qb.y, s);
+            s = fmaf(h2f(kr[u].w), qb.z, s);
+            s = fmaf(h2f(kr[u].w >> 16), qb.w, s);
+            s = group_sum<TPK>(s);
+            sc[u] = half_key(SPL, c, u, q) + split < n ? s : -INFINITY;
+            cmax = fmaxf(cmax, sc[u]);
+        }
+        const float mnew = fmaxf(m, wave_max(cmax));  // finite: the chunk's first key is valid
+        const float r = expf(m - mnew);
+        l *= r;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) acc[e] *= r;
+#pragma unroll
+        for (int u = 0; u < kHalfU; ++u) {
+            const bool in = half_key(SPL, c, u, q) + split < n;
+            const float pj = in ? expf(sc[u] - mnew) : 0.f;
+            l += pj;
+            const uint32_t wv[4] = {in ? vr[u].x : 0u, in ? vr[u].y : 0u, in ? vr[u].z : 0u, in ? vr[u].w : 0u};
+#pragma unroll
+            for (int q2 = 0; q2 < 4; ++q2) {
+                acc[2 * q2] = fmaf(pj, h2f(wv[q2]), acc[2 * q2]);
+                acc[2 * q2 + 1] = fmaf(pj, h2f(wv[q2] >> 16), acc[2 * q2 + 1]);
+            }
+        }
+        m = mnew;
+    }
+    // every lane of a split holds that split's sum; count each split once
+    const float lsum = wave_sum(sub == 0 ? l : 0.f);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) wsc[lane * 8 + e] = acc[e];
+    __builtin_amdgcn_s_waitcnt(0xc07f);  // this wave's LDS writes are done
+    __builtin_amdgcn_wave_barrier();
+    for (int e = lane; e < HD; e += 64) {
+        float o = 0.f;
+#pragma unroll
+        for (int s2 = 0; s2 < SPL; ++s2) o += wsc[(s2 * TPK + e / 8) * 8 + e % 8];
+        slot[e] = o;
+    }
+    if (lane == 0) {
+        slot[HD] = m;  // -inf when this wave had no key
+        slot[HD + 1] = lsum;
+    }
+}
+
+// out[e] of the pair from the partials of its two waves (after a workgroup barrier)
+template <int HD>
+__device__ __forceinline__ void attn_combine2(const float *s0, const float *s1, float *out) {
+    const int lane = threadIdx.x & 63;
+    const float m0 = s0[HD], m1 = s1[HD], M = fmaxf(m0, m1);  // m0 finite: wave 0 has key 0
+    const float e0 = expf(m0 - M), e1 = expf(m1 - M);
+    const float inv = 1.f / (e0 * s0[HD + 1] + e1 * s1[HD + 1]);
+    for (int e = lane; e < HD; e += 64) out[e] = (e0 * s0[e] + e1 * s1[e]) * inv;
+}
+
 // Workgroup (g, r): attention of heads [g HG, (g + 1) HG) for all nb rows, then
 // part[g][bi][row] = sum_{c < C} W[row][g C + c] * att[bi][g C + c] for the RW
 // rows [r RW, (r + 1) RW), one (row, chunk) item per thread.  Workgroups with the
@@ -310,7 +392,8 @@ constexpr int kHeadParts = 8;   // head groups are sized so that P = H / HG <= t
 // so the score a lane computes (summed over the TPK lanes of its split) is the
 // weight it applies to its own values.  Keys are consumed in chunks of U SPL with
 // an online softmax (running max and sum), so any length fits in registers.
-template <int T, int HD>
+// S2 (batch 1, head groups of <= 2 heads): two waves per pair (attn_half).
+template <int T, int HD, bool S2>
 __global__ __launch_bounds__(256) void k_attn_head(HeadArgs a) {
     constexpr int XW = GTraits<T>::XW, NS = GTraits<T>::NS;
     constexpr int TPK = HD / 8;     // lanes per key: 8-wide dimension groups
@@ -324,6 +407,7 @@ __global__ __launch_bounds__(256) void k_attn_head(HeadArgs a) {
     const int pairs = nb * HG;
     float *outv = lds;                           // [pairs][HD] = [nb][C]
     float *wsc = lds + 4 * kHeadCols + w * 512;  // this wave's [64][8] scratch
+    float *slots = lds + 4 * kHeadCols + 4 * 512;  // S2: [4 waves][kHalfSlot]
     const int sub = lane % TPK, split = lane / TPK;
 
     // Order of issue: the first chunk of this wave's first pair (addresses do not
@@ -355,7 +439,36 @@ __global__ __launch_bounds__(256) void k_attn_head(HeadArgs a) {
         qa = *reinterpret_cast<const float4 *>(qp);
         qb = *reinterpret_cast<const float4 *>(qp + 4);
     };
-    if (w < pairs) load_chunk_kv(w, 0);
+    // S2: chunk c of wave q of pair p (rows first, as above)
+    uint4 kr2[kHalfU], vr2[kHalfU];
+    auto load_half = [&](int p, int q, int c) {
+        const int hh = h0 + p;
+        uint32_t r[kHalfU];
+        if (a.rows) {  // kernel argument
+#pragma unroll
+            for (int u = 0; u < kHalfU; ++u) r[u] = a.rows[min(half_key(SPL, c, u, q) + split, L - 1)];
+        } else {
+#pragma unroll
+            for (int u = 0; u < kHalfU; ++u) r[u] = 0u;
+        }
+#pragma unroll
+        for (int u = 0; u < kHalfU; ++u) {
+            const int j = min(half_key(SPL, c, u, q) + split, L - 1);
+            const size_t o = ((size_t(r[u]) * H + hh) * L + j) * HD + sub * 8;
+            kr2[u] = *reinterpret_cast<const uint4 *>(a.K + o);
+            vr2[u] = *reinterpret_cast<const uint4 *>(a.V + o);
+        }
+        if (c == 0) {
+            const float *qp = a.q + hh * HD + sub * 8;
+            qa = *reinterpret_cast<const float4 *>(qp);
+            qb = *reinterpret_cast<const float4 *>(qp + 4);
+        }
+    };
+    if constexpr (S2) {
+        if (w < 2 * pairs) load_half(w >> 1, w & 1, 0);
+    } else {
+        if (w < pairs) load_chunk_kv(w, 0);
+    }
     __builtin_amdgcn_sched_barrier(0);
 
     const int CPR = C / XW, cpr_log2 = __builtin_ctz(CPR), c0 = col0 / XW;
@@ -372,62 +485,70 @@ __global__ __launch_bounds__(256) void k_attn_head(HeadArgs a) {
 #pragma unroll
     for (int bi = 0; bi < 4; ++bi) nk[bi] = bi < nb ? (a.lens ? int(a.lens[bi]) : n_self) : 0;
 
-    for (int p = w; p < pairs; p += 4) {  // wave-uniform
-        const int bi = p >> hg_log2;
-        const int n = bi == 0 ? nk[0] : bi == 1 ? nk[1] : bi == 2 ? nk[2] : nk[3];
-        float m = -INFINITY, l = 0.f;
-        float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-        for (int j0 = 0; j0 < n; j0 += U * SPL) {
-            if (p != w || j0 != 0) load_chunk_kv(p, j0);
-            float sc[U];
-            float cmax = -INFINITY;
-#pragma unroll
-            for (int u = 0; u < U; ++u) {
-                float s = h2f(kr[u].x) * qa.x;
-                s = fmaf(h2f(kr[u].x >> 16), qa.y, s);
-                s = fmaf(h2f(kr[u].y), qa.z, s);
-                s = fmaf(h2f(kr[u].y >> 16), qa.w, s);
-                s = fmaf(h2f(kr[u].z), qb.x, s);
-                s = fmaf(h2f(kr[u].z >> 16), qb.y, s);
-                s = fmaf(h2f(kr[u].w), qb.z, s);
-                s = fmaf(h2f(kr[u].w >> 16), qb.w, s);
-                s = group_sum<TPK>(s);
-                sc[u] = j0 + u * SPL + split < n ? s : -INFINITY;
-                cmax = fmaxf(cmax, sc[u]);
-            }
-            const float mnew = fmaxf(m, wave_max(cmax));  // finite: key j0 is valid
-            const float r = expf(m - mnew);
-            l *= r;
-#pragma unroll
-            for (int e = 0; e < 8; ++e) acc[e] *= r;
-#pragma unroll
-            for (int u = 0; u < U; ++u) {
-                const bool in = j0 + u * SPL + split < n;
-                const float pj = in ? expf(sc[u] - mnew) : 0.f;
-                l += pj;
-                const uint32_t wv[4] = {in ? vr[u].x : 0u, in ? vr[u].y : 0u, in ? vr[u].z : 0u, in ? vr[u].w : 0u};
-#pragma unroll
-                for (int q2 = 0; q2 < 4; ++q2) {
-                    acc[2 * q2] = fmaf(pj, h2f(wv[q2]), acc[2 * q2]);
-                    acc[2 * q2 + 1] = fmaf(pj, h2f(wv[q2] >> 16), acc[2 * q2 + 1]);
+    if constexpr (S2) {
+        if (w < 2 * pairs)
+            attn_half<HD>(nk[0], w & 1, qa, qb, kr2, vr2, [&](int c) { load_half(w >> 1, w & 1, c); }, wsc,
+                          slots + w * kHalfSlot);
+        lds_barrier();
+        if (w < pairs) attn_combine2<HD>(slots + 2 * w * kHalfSlot, slots + (2 * w + 1) * kHalfSlot, outv + w * HD);
+    } else {
+        for (int p = w; p < pairs; p += 4) {  // wave-uniform
+            const int bi = p >> hg_log2;
+            const int n = bi == 0 ? nk[0] : bi == 1 ? nk[1] : bi == 2 ? nk[2] : nk[3];
+            float m = -INFINITY, l = 0.f;
+            float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+            for (int j0 = 0; j0 < n; j0 += U * SPL) {
+                if (p != w || j0 != 0) load_chunk_kv(p, j0);
+                float sc[U];
+                float cmax = -INFINITY;
+    #pragma unroll
+                for (int u = 0; u < U; ++u) {
+                    float s = h2f(kr[u].x) * qa.x;
+                    s = fmaf(h2f(kr[u].x >> 16), qa.y, s);
+                    s = fmaf(h2f(kr[u].y), qa.z, s);
+                    s = fmaf(h2f(kr[u].y >> 16), qa.w, s);
+                    s = fmaf(h2f(kr[u].z), qb.x, s);
+                    s = fmaf(h2f(kr[u].z >> 16), qb.y, s);
+                    s = fmaf(h2f(kr[u].w), qb.z, s);
+                    s = fmaf(h2f(kr[u].w >> 16), qb.w, s);
+                    s = group_sum<TPK>(s);
+                    sc[u] = j0 + u * SPL + split < n ? s : -INFINITY;
+                    cmax = fmaxf(cmax, sc[u]);
                 }
+                const float mnew = fmaxf(m, wave_max(cmax));  // finite: key j0 is valid
+                const float r = expf(m - mnew);
+                l *= r;
+    #pragma unroll
+                for (int e = 0; e < 8; ++e) acc[e] *= r;
+    #pragma unroll
+                for (int u = 0; u < U; ++u) {
+                    const bool in = j0 + u * SPL + split < n;
+                    const float pj = in ? expf(sc[u] - mnew) : 0.f;
+                    l += pj;
+                    const uint32_t wv[4] = {in ? vr[u].x : 0u, in ? vr[u].y : 0u, in ? vr[u].z : 0u, in ? vr[u].w : 0u};
+    #pragma unroll
+                    for (int q2 = 0; q2 < 4; ++q2) {
+                        acc[2 * q2] = fmaf(pj, h2f(wv[q2]), acc[2 * q2]);
+                        acc[2 * q2 + 1] = fmaf(pj, h2f(wv[q2] >> 16), acc[2 * q2 + 1]);
+                    }
+                }
+                m = mnew;
             }
-            m = mnew;
+            // every lane of a split holds that split's sum; count each split once
+            const float inv = 1.f / wave_sum(sub == 0 ? l : 0.f);
+    #pragma unroll
+            for (int e = 0; e < 8; ++e) wsc[lane * 8 + e] = acc[e];
+            __builtin_amdgcn_s_waitcnt(0xc07f);  // this wave's LDS writes are done
+            __builtin_amdgcn_wave_barrier();
+            for (int e = lane; e < HD; e += 64) {
+                float o = 0.f;
+    #pragma unroll
+                for (int s2 = 0; s2 < SPL; ++s2) o += wsc[(s2 * TPK + e / 8) * 8 + e % 8];
+                outv[p * HD + e] = o * inv;
+            }
+            __builtin_amdgcn_s_waitcnt(0xc07f);
+            __builtin_amdgcn_wave_barrier();
         }
-        // every lane of a split holds that split's sum; count each split once
-        const float inv = 1.f / wave_sum(sub == 0 ? l : 0.f);
-#pragma unroll
-        for (int e = 0; e < 8; ++e) wsc[lane * 8 + e] = acc[e];
-        __builtin_amdgcn_s_waitcnt(0xc07f);  // this wave's LDS writes are done
-        __builtin_amdgcn_wave_barrier();
-        for (int e = lane; e < HD; e += 64) {
-            float o = 0.f;
-#pragma unroll
-            for (int s2 = 0; s2 < SPL; ++s2) o += wsc[(s2 * TPK + e / 8) * 8 + e % 8];
-            outv[p * HD + e] = o * inv;
-        }
-        __builtin_amdgcn_s_waitcnt(0xc07f);
-        __builtin_amdgcn_wave_barrier();
     }
     lds_barrier();
 
@@ -564,7 +685,8 @@ struct XAttnArgs {
 // repeat those C rows (72 KB at 600M, from L2) instead of waiting for a separate
 // launch.  Every sum is in the order of the separate kernels, so the partials equal
 // theirs bit for bit.
-template <int T, int HD, int PR>
+// S2 (batch 1, head groups of <= 2 heads): two waves per pair (attn_half), as k_attn_head.
+template <int T, int HD, int PR, bool S2>
 __global__ __launch_bounds__(kXThreads) void k_xattn(XAttnArgs a) {
     constexpr int XW = GTraits<T>::XW, NS = GTraits<T>::NS;
     constexpr int TPK = HD / 8, SPL = 64 / TPK, U = 8, NW = kXThreads / 64;
@@ -580,6 +702,7 @@ __global__ __launch_bounds__(kXThreads) void k_xattn(XAttnArgs a) {
     float *qs = xs + nb * ldx;      // [nb][C]
     float *outv = qs + nb * C;      // [nb][C] = [pairs][HD]
     float *wsc = outv + nb * C + w * 512;  // attention waves: [64][8] scratch
+    float *slots = outv + nb * C + 4 * 512;  // S2: [4 waves][kHalfSlot]
 
     // Order of issue: residual operands (the prologue waits for them first), the q
     // rows, the out-projection chunk, the first K/V chunk.  Loads complete in order,
@@ -627,8 +750,24 @@ __global__ __launch_bounds__(kXThreads) void k_xattn(XAttnArgs a) {
             vr[u] = *reinterpret_cast<const uint4 *>(a.V + o);
         }
     };
+    // S2: chunk c of wave q of head p (batch 1)
+    uint4 kr2[kHalfU], vr2[kHalfU];
+    auto load_half = [&](int p, int q, int c) {
+        const int hh = h0 + p;
+#pragma unroll
+        for (int u = 0; u < kHalfU; ++u) {
+            const int j = min(half_key(SPL, c, u, q) + split, L - 1);
+            const size_t o = (size_t(hh) * L + j) * HD + sub * 8;
+            kr2[u] = *reinterpret_cast<const uint4 *>(a.K + o);
+            vr2[u] = *reinterpret_cast<const uint4 *>(a.V + o);
+        }
+    };
     constexpr bool kEarlyKV = PR == 1;  // two rows' q would not fit the registers beside them
-    if (kEarlyKV && w < pairs) load_kv(w, 0);
+    if constexpr (S2) {
+        if (w < 2 * pairs) load_half(w >> 1, w & 1, 0);
+    } else {
+        if (kEarlyKV && w < pairs) load_kv(w, 0);
+    }
     __builtin_amdgcn_sched_barrier(0);
     int nk[PR];
 #pragma unroll
@@ -661,64 +800,75 @@ __global__ __launch_bounds__(kXThreads) void k_xattn(XAttnArgs a) {
     }
     lds_barrier();
 
-    // attention: one (row, head) pair per wave, as in k_attn_head
-    for (int p = w; p < pairs; p += NW) {  // wave-uniform
-        const int bi = p >> hg_log2, hl = p & (HG - 1);
-        const int n = PR == 1 || bi == 0 ? nk[0] : nk[PR - 1];
-        const float4 qa = *reinterpret_cast<const float4 *>(qs + bi * C + hl * HD + sub * 8);
-        const float4 qb = *reinterpret_cast<const float4 *>(qs + bi * C + hl * HD + sub * 8 + 4);
-        float m = -INFINITY, l = 0.f;
-        float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-        for (int j0 = 0; j0 < n; j0 += U * SPL) {
-            if (!kEarlyKV || p != w || j0 != 0) load_kv(p, j0);
-            float sc[U];
-            float cmax = -INFINITY;
-#pragma unroll
-            for (int u = 0; u < U; ++u) {
-                float s = h2f(kr[u].x) * qa.x;
-                s = fmaf(h2f(kr[u].x >> 16), qa.y, s);
-                s = fmaf(h2f(kr[u].y), qa.z, s);
-                s = fmaf(h2f(kr[u].y >> 16), qa.w, s);
-                s = fmaf(h2f(kr[u].z), qb.x, s);
-                s = fmaf(h2f(kr[u].z >> 16), qb.y, s);
-                s = fmaf(h2f(kr[u].w), qb.z, s);
-                s = fmaf(h2f(kr[u].w >> 16), qb.w, s);
-                s = group_sum<TPK>(s);
-                sc[u] = j0 + u * SPL + split < n ? s : -INFINITY;
-                cmax = fmaxf(cmax, sc[u]);
-            }
-            const float mnew = fmaxf(m, wave_max(cmax));
-            const float r = expf(m - mnew);
-            l *= r;
-#pragma unroll
-            for (int e = 0; e < 8; ++e) acc[e] *= r;
-#pragma unroll
-            for (int u = 0; u < U; ++u) {
-                const bool in = j0 + u * SPL + split < n;
-                const float pj = in ? expf(sc[u] - mnew) : 0.f;
-                l += pj;
-                const uint32_t wv[4] = {in ? vr[u].x : 0u, in ? vr[u].y : 0u, in ? vr[u].z : 0u, in ? vr[u].w : 0u};
-#pragma unroll
-                for (int q2 = 0; q2 < 4; ++q2) {
-                    acc[2 * q2] = fmaf(pj, h2f(wv[q2]), acc[2 * q2]);
-                    acc[2 * q2 + 1] = fmaf(pj, h2f(wv[q2] >> 16), acc[2 * q2 + 1]);
+    if constexpr (S2) {
+        if (w < 2 * pairs) {
+            const float4 qa = *reinterpret_cast<const float4 *>(qs + (w >> 1) * HD + sub * 8);
+            const float4 qb = *reinterpret_cast<const float4 *>(qs + (w >> 1) * HD + sub * 8 + 4);
+            attn_half<HD>(nk[0], w & 1, qa, qb, kr2, vr2, [&](int c) { load_half(w >> 1, w & 1, c); }, wsc,
+                          slots + w * kHalfSlot);
+        }
+        lds_barrier();
+        if (w < pairs) attn_combine2<HD>(slots + 2 * w * kHalfSlot, slots + (2 * w + 1) * kHalfSlot, outv + w * HD);
+    } else {
+        // attention: one (row, head) pair per wave, as in k_attn_head
+        for (int p = w; p < pairs; p += NW) {  // wave-uniform
+            const int bi = p >> hg_log2, hl = p & (HG - 1);
+            const int n = PR == 1 || bi == 0 ? nk[0] : nk[PR - 1];
+            const float4 qa = *reinterpret_cast<const float4 *>(qs + bi * C + hl * HD + sub * 8);
+            const float4 qb = *reinterpret_cast<const float4 *>(qs + bi * C + hl * HD + sub * 8 + 4);
+            float m = -INFINITY, l = 0.f;
+            float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+            for (int j0 = 0; j0 < n; j0 += U * SPL) {
+                if (!kEarlyKV || p != w || j0 != 0) load_kv(p, j0);
+                float sc[U];
+                float cmax = -INFINITY;
+    #pragma unroll
+                for (int u = 0; u < U; ++u) {
+                    float s = h2f(kr[u].x) * qa.x;
+                    s = fmaf(h2f(kr[u].x >> 16), qa.y, s);
+                    s = fmaf(h2f(kr[u].y), qa.z, s);
+                    s = fmaf(h2f(kr[u].y >> 16), qa.w, s);
+                    s = fmaf(h2f(kr[u].z), qb.x, s);
+                    s = fmaf(h2f(kr[u].z >> 16), qb.y, s);
+                    s = fmaf(h2f(kr[u].w), qb.z, s);
+                    s = fmaf(h2f(kr[u].w >> 16), qb.w, s);
+                    s = group_sum<TPK>(s);
+                    sc[u] = j0 + u * SPL + split < n ? s : -INFINITY;
+                    cmax = fmaxf(cmax, sc[u]);
                 }
+                const float mnew = fmaxf(m, wave_max(cmax));
+                const float r = expf(m - mnew);
+                l *= r;
+    #pragma unroll
+                for (int e = 0; e < 8; ++e) acc[e] *= r;
+    #pragma unroll
+                for (int u = 0; u < U; ++u) {
+                    const bool in = j0 + u * SPL + split < n;
+                    const float pj = in ? expf(sc[u] - mnew) : 0.f;
+                    l += pj;
+                    const uint32_t wv[4] = {in ? vr[u].x : 0u, in ? vr[u].y : 0u, in ? vr[u].z : 0u, in ? vr[u].w : 0u};
+    #pragma unroll
+                    for (int q2 = 0; q2 < 4; ++q2) {
+                        acc[2 * q2] = fmaf(pj, h2f(wv[q2]), acc[2 * q2]);
+                        acc[2 * q2 + 1] = fmaf(pj, h2f(wv[q2] >> 16), acc[2 * q2 + 1]);
+                    }
+                }
+                m = mnew;
             }
-            m = mnew;
+            const float inv = 1.f / wave_sum(sub == 0 ? l : 0.f);
+    #pragma unroll
+            for (int e = 0; e < 8; ++e) wsc[lane * 8 + e] = acc[e];
+            __builtin_amdgcn_s_waitcnt(0xc07f);
+            __builtin_amdgcn_wave_barrier();
+            for (int e = lane; e < HD; e += 64) {
+                float o = 0.f;
+    #pragma unroll
+                for (int s2 = 0; s2 < SPL; ++s2) o += wsc[(s2 * TPK + e / 8) * 8 + e % 8];
+                outv[p * HD + e] = o * inv;
+            }
+            __builtin_amdgcn_s_waitcnt(0xc07f);
+            __builtin_amdgcn_wave_barrier();
         }
-        const float inv = 1.f / wave_sum(sub == 0 ? l : 0.f);
-#pragma unroll
-        for (int e = 0; e < 8; ++e) wsc[lane * 8 + e] = acc[e];
-        __builtin_amdgcn_s_waitcnt(0xc07f);
-        __builtin_amdgcn_wave_barrier();
-        for (int e = lane; e < HD; e += 64) {
-            float o = 0.f;
-#pragma unroll
-            for (int s2 = 0; s2 < SPL; ++s2) o += wsc[(s2 * TPK + e / 8) * 8 + e % 8];
-            outv[p * HD + e] = o * inv;
-        }
-        __builtin_amdgcn_s_waitcnt(0xc07f);
-        __builtin_amdgcn_wave_barrier();
     }
     lds_barrier();
 
@@ -822,13 +972,19 @@ bool head_geometry(const DevMatrix &w, int nb, int d, int H, int hd, int L, Head
     hg->P = H / HG;
     hg->RW = RW;
     hg->R = (d + RW - 1) / RW;
-    hg->lds = sizeof(float) * (size_t(4) * kHeadCols + 4 * 512);
+    hg->lds = sizeof(float) * (size_t(4) * kHeadCols + 4 * 512 + 4 * kHalfSlot);
     return true;
 }
 
+// two waves per (row, head) pair where the batch is one row and a group at most 2 heads
+inline bool head_split2(int nb, int HG) { return nb == 1 && HG <= 2; }
+
 template <int T, int HD>
 hipError_t launch_head(const HeadArgs &a, int R, size_t lds, hipStream_t st) {
-    hipLaunchKernelGGL((k_attn_head<T, HD>), dim3(a.H / a.HG, R), dim3(256), lds, st, a);
+    if (head_split2(a.nb, a.HG))
+        hipLaunchKernelGGL((k_attn_head<T, HD, true>), dim3(a.H / a.HG, R), dim3(256), lds, st, a);
+    else
+        hipLaunchKernelGGL((k_attn_head<T, HD, false>), dim3(a.H / a.HG, R), dim3(256), lds, st, a);
     return hipGetLastError();
 }
 
@@ -952,10 +1108,12 @@ namespace {
 
 template <int T, int HD>
 hipError_t launch_xattn(const XAttnArgs &a, int R, size_t lds, hipStream_t st) {
-    if (a.s.nb == 1)
-        hipLaunchKernelGGL((k_xattn<T, HD, 1>), dim3(a.H / a.HG, R), dim3(kXThreads), lds, st, a);
+    if (head_split2(a.s.nb, a.HG))
+        hipLaunchKernelGGL((k_xattn<T, HD, 1, true>), dim3(a.H / a.HG, R), dim3(kXThreads), lds, st, a);
+    else if (a.s.nb == 1)
+        hipLaunchKernelGGL((k_xattn<T, HD, 1, false>), dim3(a.H / a.HG, R), dim3(kXThreads), lds, st, a);
     else
-        hipLaunchKernelGGL((k_xattn<T, HD, 2>), dim3(a.H / a.HG, R), dim3(kXThreads), lds, st, a);
+        hipLaunchKernelGGL((k_xattn<T, HD, 2, false>), dim3(a.H / a.HG, R), dim3(kXThreads), lds, st, a);
     return hipGetLastError();
 }
 
@@ -1015,8 +1173,10 @@ hipError_t step_cross_attn(const DevMatrix &wq, const float *bq, const DevMatrix
     a.lens = lens;
     a.part = part_out;
     const int pairs = nb * hg.HG;
-    const size_t lds = sizeof(float) * (size_t(nb) * lds_pad(d) + 2 * size_t(nb) * C +
-                                        size_t(pairs < kXThreads / 64 ? pairs : kXThreads / 64) * 512);
+    // the attention waves' scratch (S2: 4 waves' and their partials)
+    const size_t att = head_split2(nb, hg.HG) ? size_t(4) * 512 + 4 * kHalfSlot
+                                              : size_t(pairs < kXThreads / 64 ? pairs : kXThreads / 64) * 512;
+    const size_t lds = sizeof(float) * (size_t(nb) * lds_pad(d) + 2 * size_t(nb) * C + att);
     switch (wq.type) {
     case GGML_Q4_K: return launch_xattn_hd<GGML_Q4_K>(a, hd, R, lds, st);
     case GGML_Q5_K: return launch_xattn_hd<GGML_Q5_K>(a, hd, R, lds, st);
