@@ -604,6 +604,73 @@ __device__ __forceinline__ float dot4u8_chain(uint32_t v, const float (&x)[4], f
     return acc;
 }
 
+// dot4u8_chain of four items' words against the same four x values, as one asm block:
+// byte b of every word is converted, then the four products are added, so the four
+// items' dependent chains interleave (one chain per block left each product waiting for
+// the previous one); per item the operations and their order are dot4u8_chain's
+__device__ __forceinline__ void dot4u8_chain4(const uint32_t (&v)[4], const float (&x)[4], float (&acc)[4]) {
+    float t0, t1, t2, t3;
+    asm("v_cvt_f32_ubyte0 %4, %8\n\t"
+        "v_cvt_f32_ubyte0 %5, %9\n\t"
+        "v_cvt_f32_ubyte0 %6, %10\n\t"
+        "v_cvt_f32_ubyte0 %7, %11\n\t"
+        "v_fmac_f32 %0, %4, %12\n\t"
+        "v_fmac_f32 %1, %5, %12\n\t"
+        "v_fmac_f32 %2, %6, %12\n\t"
+        "v_fmac_f32 %3, %7, %12\n\t"
+        "v_cvt_f32_ubyte1 %4, %8\n\t"
+        "v_cvt_f32_ubyte1 %5, %9\n\t"
+        "v_cvt_f32_ubyte1 %6, %10\n\t"
+        "v_cvt_f32_ubyte1 %7, %11\n\t"
+        "v_fmac_f32 %0, %4, %13\n\t"
+        "v_fmac_f32 %1, %5, %13\n\t"
+        "v_fmac_f32 %2, %6, %13\n\t"
+        "v_fmac_f32 %3, %7, %13\n\t"
+        "v_cvt_f32_ubyte2 %4, %8\n\t"
+        "v_cvt_f32_ubyte2 %5, %9\n\t"
+        "v_cvt_f32_ubyte2 %6, %10\n\t"
+        "v_cvt_f32_ubyte2 %7, %11\n\t"
+        "v_fmac_f32 %0, %4, %14\n\t"
+        "v_fmac_f32 %1, %5, %14\n\t"
+        "v_fmac_f32 %2, %6, %14\n\t"
+        "v_fmac_f32 %3, %7, %14\n\t"
+        "v_cvt_f32_ubyte3 %4, %8\n\t"
+        "v_cvt_f32_ubyte3 %5, %9\n\t"
+        "v_cvt_f32_ubyte3 %6, %10\n\t"
+        "v_cvt_f32_ubyte3 %7, %11\n\t"
+        "v_fmac_f32 %0, %4, %15\n\t"
+        "v_fmac_f32 %1, %5, %15\n\t"
+        "v_fmac_f32 %2, %6, %15\n\t"
+        "v_fmac_f32 %3, %7, %15"
+        : "+v"(acc[0]), "+v"(acc[1]), "+v"(acc[2]), "+v"(acc[3]), "=&v"(t0), "=&v"(t1), "=&v"(t2), "=&v"(t3)
+        : "v"(v[0]), "v"(v[1]), "v"(v[2]), "v"(v[3]), "v"(x[0]), "v"(x[1]), "v"(x[2]), "v"(x[3]));
+}
+
+// group_sum_dyn of N values at once, step by step, so that their DPP chains interleave
+// (per value the same operations in the same order)
+template <int N>
+__device__ __forceinline__ void group_sum_dyn_n(float (&v)[N], int log2w) {
+    if (log2w >= 1)
+#pragma unroll
+        for (int i = 0; i < N; ++i) v[i] = v[i] + dpp_mov<kDppXor1>(v[i]);
+    if (log2w >= 2)
+#pragma unroll
+        for (int i = 0; i < N; ++i) v[i] = v[i] + dpp_mov<kDppXor2>(v[i]);
+    if (log2w >= 3)
+#pragma unroll
+        for (int i = 0; i < N; ++i) v[i] = v[i] + dpp_mov<kDppHalfMirror>(v[i]);
+    if (log2w >= 4)
+#pragma unroll
+        for (int i = 0; i < N; ++i) v[i] = v[i] + dpp_mov<kDppMirror>(v[i]);
+    if (log2w >= 5)
+#pragma unroll
+        for (int i = 0; i < N; ++i) {
+            const float r0 = lane_value(v[i], 0), r1 = lane_value(v[i], 16), r2 = lane_value(v[i], 32),
+                        r3 = lane_value(v[i], 48);
+            v[i] = log2w == 5 ? ((threadIdx.x & 32) ? r2 + r3 : r0 + r1) : (r0 + r1) + (r2 + r3);
+        }
+}
+
 // dot_chunk of KI q4_K / q5_K items that share chunk c, with x read from LDS (xc:
 // the chunk's 64 contiguous values) one float4 at a time and applied to every item,
 // so no item's values are expanded all at once.  Per item the operations and their
@@ -621,20 +688,28 @@ __device__ __forceinline__ void dot_items(int c, const Raw<T> (&r)[KI], const fl
         const float4 xl = *reinterpret_cast<const float4 *>(xc + 4 * u);
         const float4 xh = *reinterpret_cast<const float4 *>(xc + 32 + 4 * u);
         const float vl[4] = {xl.x, xl.y, xl.z, xl.w}, vh[4] = {xh.x, xh.y, xh.z, xh.w};
+        uint32_t lo[KI], hi[KI];
 #pragma unroll
         for (int k = 0; k < KI; ++k) {
             const uint32_t wu = u < 4 ? (&r[k].a.x)[u] : (&r[k].b.x)[u - 4];
-            uint32_t lo, hi;
             if constexpr (T == GGML_Q5_K) {
                 const uint32_t hb = u < 4 ? (&r[k].c.x)[u] : (&r[k].e.x)[u - 4];
-                lo = (wu & 0x0F0F0F0Fu) | (((hb >> (2 * g)) & 0x01010101u) << 4);
-                hi = ((wu >> 4) & 0x0F0F0F0Fu) | (((hb >> (2 * g + 1)) & 0x01010101u) << 4);
+                lo[k] = (wu & 0x0F0F0F0Fu) | (((hb >> (2 * g)) & 0x01010101u) << 4);
+                hi[k] = ((wu >> 4) & 0x0F0F0F0Fu) | (((hb >> (2 * g + 1)) & 0x01010101u) << 4);
             } else {
-                lo = wu & 0x0F0F0F0Fu;
-                hi = wu & 0xF0F0F0F0u;  // 16 * nibble; scaled back below
+                lo[k] = wu & 0x0F0F0F0Fu;
+                hi[k] = wu & 0xF0F0F0F0u;  // 16 * nibble; scaled back below
             }
-            al[k] = dot4u8_chain(lo, vl, al[k]);
-            ah[k] = dot4u8_chain(hi, vh, ah[k]);
+        }
+        if constexpr (KI == 4) {
+            dot4u8_chain4(lo, vl, al);
+            dot4u8_chain4(hi, vh, ah);
+        } else {
+#pragma unroll
+            for (int k = 0; k < KI; ++k) {
+                al[k] = dot4u8_chain(lo[k], vl, al[k]);
+                ah[k] = dot4u8_chain(hi[k], vh, ah[k]);
+            }
         }
     }
     // the sums of gemv_load_x (xslot: values 0..31 -> 0, 32..63 -> 1), in its order
@@ -788,14 +863,18 @@ __global__ __launch_bounds__(kXThreads) void k_xattn(XAttnArgs a) {
 #pragma unroll
             for (int k = 0; k < kXItems; ++k) acc[k][bi] = o[k];
         }
+        float sums[kXItems * PR];
+#pragma unroll
+        for (int k = 0; k < kXItems; ++k)
+#pragma unroll
+            for (int bi = 0; bi < PR; ++bi) sums[k * PR + bi] = acc[k][bi];
+        group_sum_dyn_n(sums, cq_log2);
 #pragma unroll
         for (int k = 0; k < kXItems; ++k) {
             const int row = (t + k * kXThreads) >> cq_log2;
 #pragma unroll
-            for (int bi = 0; bi < PR; ++bi) {
-                const float v = group_sum_dyn(acc[k][bi], cq_log2);
-                if (qc == 0 && row < C && bi < nb) qs[bi * C + row] = v + qbias[k];
-            }
+            for (int bi = 0; bi < PR; ++bi)
+                if (qc == 0 && row < C && bi < nb) qs[bi * C + row] = sums[k * PR + bi] + qbias[k];
         }
     }
     lds_barrier();
