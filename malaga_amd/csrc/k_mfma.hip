@@ -485,7 +485,7 @@ int split_k(const DevMatrix &w, int M, size_t ws_bytes) {
 // with the next (tile, K-step) in flight in registers.  No split K, no reduction
 // kernel, and X is read from HBM/L2 once per workgroup instead of once per tile.
 // MODE 0 stores Y (bias, residual, ReLU); MODE 1 keeps a running argmax per X row
-// (the greedy LM head) and writes one partial per wave.
+// (the greedy LM head) and writes one partial per workgroup (its waves' merged in LDS).
 
 constexpr int kRxWaves = 8;
 constexpr int kRxDepth = 2;  // (group, K-step) jobs of W in flight per wave
@@ -716,7 +716,13 @@ __global__ __launch_bounds__(kRxWaves * 64) void k_mfma_rx(RxArgs a) {
         }
     }
     if constexpr (MODE == 1) {
-        // lanes 16 kq .. 16 kq + 15 hold the same X rows: reduce within each 16-lane row
+        // lanes 16 kq .. 16 kq + 15 hold the same X rows: reduce within each 16-lane row,
+        // then over the workgroup's waves (LDS; the staged X is no longer read), so the
+        // finalize merges one partial per workgroup and row
+        __syncthreads();  // every wave's last reads of the staged X are done
+        float *mv = reinterpret_cast<float *>(rx_lds);                  // [kRxWaves][BM]
+        uint32_t *mi = reinterpret_cast<uint32_t *>(mv + kRxWaves * BM);  // [kRxWaves][BM]
+        const int wv = t >> 6;
 #pragma unroll
         for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
@@ -728,11 +734,20 @@ __global__ __launch_bounds__(kRxWaves * 64) void k_mfma_rx(RxArgs a) {
                 argmax_merge(v, i, dpp_mov<kDppHalfMirror>(v), dpp_mov<kDppHalfMirror>(i));
                 argmax_merge(v, i, dpp_mov<kDppMirror>(v), dpp_mov<kDppMirror>(i));
                 const int m = mt * 16 + 4 * kq + r;
-                if (ln == 0 && m < a.M) {
-                    a.pv[size_t(m) * a.parts + gw] = v;
-                    a.pi[size_t(m) * a.parts + gw] = i;
+                if (ln == 0) {
+                    mv[wv * BM + m] = v;
+                    mi[wv * BM + m] = i;
                 }
             }
+        __syncthreads();
+        if (t < BM && t < a.M) {  // ties -> the lowest index, so the order of the merge is free
+            float v = mv[t];
+            uint32_t i = mi[t];
+#pragma unroll
+            for (int w2 = 1; w2 < kRxWaves; ++w2) argmax_merge(v, i, mv[w2 * BM + t], mi[w2 * BM + t]);
+            a.pv[size_t(t) * a.parts + blockIdx.x] = v;
+            a.pi[size_t(t) * a.parts + blockIdx.x] = i;
+        }
     }
 }
 
@@ -820,7 +835,7 @@ RxArgs rx_args(const DevMatrix &w, const float *X, int ldx, int M) {
 }
 }  // namespace
 
-int gemm_argmax_parts(const DevMatrix &w, int M) { return rx_grid(w, M) * kRxWaves; }
+int gemm_argmax_parts(const DevMatrix &w, int M) { return rx_grid(w, M); }  // one per workgroup
 
 hipError_t gemm_argmax(const DevMatrix &w, const float *X, int ldx, int M, int mask_id, float *pv, uint32_t *pi,
                        int *parts, hipStream_t st) {
@@ -830,7 +845,7 @@ hipError_t gemm_argmax(const DevMatrix &w, const float *X, int ldx, int M, int m
     a.pv = pv;
     a.pi = pi;
     const int grid = rx_grid(w, M);
-    a.parts = grid * kRxWaves;
+    a.parts = grid;
     *parts = a.parts;
     return run_rx<1>(w, a, M, grid, st);
 }

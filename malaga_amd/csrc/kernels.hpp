@@ -126,7 +126,7 @@ hipError_t dgemm_qkv(const DevMatrix &w, const float *x, int ldx, int M, const D
 
 // M <= 32 rows with X resident in LDS (K <= 1024 at M > 16, K <= 2048 at M <= 16).
 bool gemm_rx_supported(const DevMatrix &w, int M);
-// Greedy LM head for 4 < M <= 32: per-wave argmax partials pv/pi [M][parts] of
+// Greedy LM head for 4 < M <= 32: per-workgroup argmax partials pv/pi [M][parts] of
 // X W^T (mask_id skipped), without storing the logits.
 int gemm_argmax_parts(const DevMatrix &w, int M);
 hipError_t gemm_argmax(const DevMatrix &w, const float *X, int ldx, int M, int mask_id, float *pv, uint32_t *pi,
