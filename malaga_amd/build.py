@@ -9,10 +9,10 @@ PKG = Path(__file__).resolve().parent
 CSRC = PKG / "csrc"
 
 
-def build_library(jobs: int | None = None, verbose: bool = False) -> Path:
-    """Compiles malaga_amd/_build/libmalaga_hip.so (always runs make)."""
+def build_library(jobs: int | None = None, verbose: bool = False, force: bool = False) -> Path:
+    """Compiles malaga_amd/_build/libmalaga_hip.so (make; force: every source again)."""
     jobs = jobs or min(16, os.cpu_count() or 8)
-    cmd = ["make", "-C", str(CSRC), f"-j{jobs}"]
+    cmd = ["make", "-C", str(CSRC), f"-j{jobs}"] + (["-B"] if force else [])
     res = subprocess.run(cmd, capture_output=not verbose, text=True)
     if res.returncode != 0:
         raise RuntimeError(f"building libmalaga_hip.so failed:\n{res.stdout}\n{res.stderr}")

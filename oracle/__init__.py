@@ -38,8 +38,8 @@ class OrcGenOptions(C.Structure):
 _lib = None
 
 
-def build() -> Path:
-    res = subprocess.run(["make", "-C", str(HERE)], capture_output=True, text=True)
+def build(force: bool = False) -> Path:
+    res = subprocess.run(["make", "-C", str(HERE)] + (["-B"] if force else []), capture_output=True, text=True)
     if res.returncode != 0:
         raise RuntimeError(f"building the oracle failed:\n{res.stdout}\n{res.stderr}")
     return LIB
