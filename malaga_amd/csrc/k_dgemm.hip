@@ -53,6 +53,7 @@ struct DArgs {
     __half *kc, *vc;
     int H, hd, slots;
     const uint32_t *step;
+    const uint32_t *lens;  // k_dxattn: the rows' key counts (kc / vc: the cross caches [M][H][slots][hd])
 };
 
 enum DPro : int { PRO_RAW = 0, PRO_LN = 1, PRO_SPLIT = 2 };
@@ -63,6 +64,102 @@ constexpr int kDgMaxBPW = 4;     // K blocks per wave at most: K <= 8192
 constexpr int kDgMaxLnK = 2048;  // LayerNorm projections: K = d_model <= 2048 (gamma, beta in LDS)
 constexpr int kLnTPR = 16;                          // threads per row adding the statistics
 constexpr int kLnQ = kDgMaxLnK / 16 / kLnTPR;       // partials per thread at most
+
+// X fragment of one lane: XQ float4s of one (K block, slice)
+template <int XQ>
+struct DFrag {
+    float4 x[XQ];
+};
+
+// Slice s of K block kb: acc[nt] += sc (W[nt] . X) over the slice's SK values (and - mn
+// sum(X) for the k-quants with mins), for the W registers wrb[nt] of tile nt and the X
+// fragment f of this lane (A row ln, k-group kq).  PRO_LN normalizes X with the row's mean
+// mrow and 1 / std rrow and gamma | beta in gb (LDS, K each); PRO_SPLIT takes X already
+// split into f16 hi | lo.  live false: the block is past the end and weighs 0.
+template <int T, int NT, int PRO>
+__device__ __forceinline__ void dg_slice(int kb, int s, int kq, const typename MW<T>::Regs (&wrb)[NT],
+                                         const DFrag<MW<T>::SK / 16> &f, bool live, const float *gb, int K,
+                                         float mrow, float rrow, f4_t (&acc)[NT]) {
+    using W = MW<T>;
+    constexpr int SK = W::SK, XQ = SK / 16;
+    float sc[NT], mn[NT];
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) {
+        W::scale(wrb[nt], s, sc[nt], mn[nt]);
+        sc[nt] = live ? sc[nt] : 0.f;
+        mn[nt] = live ? mn[nt] : 0.f;
+    }
+    float v[SK / 4];
+#pragma unroll
+    for (int i = 0; i < (PRO == PRO_SPLIT ? 0 : XQ); ++i) {
+        float4 e = f.x[i];
+        if constexpr (PRO == PRO_LN) {
+            const int k = kb * kStep + s * SK + kq * (SK / 4) + 4 * i;
+            const float4 g = *reinterpret_cast<const float4 *>(gb + k), b = *reinterpret_cast<const float4 *>(gb + K + k);
+            e = make_float4((e.x - mrow) * rrow * g.x + b.x, (e.y - mrow) * rrow * g.y + b.y,
+                            (e.z - mrow) * rrow * g.z + b.z, (e.w - mrow) * rrow * g.w + b.w);
+        }
+        v[4 * i] = e.x;
+        v[4 * i + 1] = e.y;
+        v[4 * i + 2] = e.z;
+        v[4 * i + 3] = e.w;
+    }
+    if constexpr (SK == 32) {
+        h8_t ah, al;
+        if constexpr (PRO == PRO_SPLIT) {
+            // whole-vector shuffles (component access would keep the ring in memory)
+            const h8_t p0 = __builtin_bit_cast(h8_t, f.x[0]), p1 = __builtin_bit_cast(h8_t, f.x[1]);
+            ah = __builtin_shufflevector(p0, p1, 0, 1, 2, 3, 8, 9, 10, 11);
+            al = __builtin_shufflevector(p0, p1, 4, 5, 6, 7, 12, 13, 14, 15);
+        } else {
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                ah[i] = _Float16(v[i]);
+                al[i] = _Float16(v[i] - float(ah[i]));
+            }
+        }
+        f4_t xs = f4_t{0.f, 0.f, 0.f, 0.f};
+        if constexpr (W::MIN) {  // per-row sums of the 32 X values: B = ones
+            const h8_t ones = {_Float16(1), _Float16(1), _Float16(1), _Float16(1),
+                               _Float16(1), _Float16(1), _Float16(1), _Float16(1)};
+            xs = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, ones, xs, 0, 0, 0);
+            xs = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, ones, xs, 0, 0, 0);
+        }
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt) {
+            const h8_t bop = W::b(wrb[nt], s);
+            f4_t tmp = f4_t{0.f, 0.f, 0.f, 0.f};
+            tmp = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bop, tmp, 0, 0, 0);
+            tmp = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, bop, tmp, 0, 0, 0);
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+                acc[nt][r] = W::MIN ? fmaf(sc[nt], tmp[r], fmaf(-mn[nt], xs[r], acc[nt][r]))
+                                    : fmaf(sc[nt], tmp[r], acc[nt][r]);
+        }
+    } else {
+        h4_t ah, al;
+        if constexpr (PRO == PRO_SPLIT) {
+            const h8_t p0 = __builtin_bit_cast(h8_t, f.x[0]);
+            ah = __builtin_shufflevector(p0, p0, 0, 1, 2, 3);
+            al = __builtin_shufflevector(p0, p0, 4, 5, 6, 7);
+        } else {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                ah[i] = _Float16(v[i]);
+                al[i] = _Float16(v[i] - float(ah[i]));
+            }
+        }
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt) {
+            const h4_t bop = W::b(wrb[nt], s);
+            f4_t tmp = f4_t{0.f, 0.f, 0.f, 0.f};
+            tmp = __builtin_amdgcn_mfma_f32_16x16x16f16(ah, bop, tmp, 0, 0, 0);
+            tmp = __builtin_amdgcn_mfma_f32_16x16x16f16(al, bop, tmp, 0, 0, 0);
+#pragma unroll
+            for (int r = 0; r < 4; ++r) acc[nt][r] = fmaf(sc[nt], tmp[r], acc[nt][r]);
+        }
+    }
+}
 
 // BPW: K blocks per wave (compile time, it sizes the fragment ring); NT: 16-column tiles
 // per workgroup (1 or 2; with 2, each X fragment, once normalized and split, feeds two
@@ -123,9 +220,7 @@ __global__ __launch_bounds__(kDgMaxNW * 64) void k_dgemm(DArgs a) {
     // (fragment order: the tile's padding rows are stored)
     const float *xrow = a.x + size_t(min(m0 + ln, a.M - 1)) * a.ldx;
     const float4 *xfr = reinterpret_cast<const float4 *>(a.x);
-    struct Frag {
-        float4 x[XQ];
-    };
+    using Frag = DFrag<XQ>;
     auto load_x = [&](int kb, int s, Frag &f) {
         if constexpr (PRO != PRO_RAW) {
 #pragma unroll
@@ -179,83 +274,7 @@ __global__ __launch_bounds__(kDgMaxNW * 64) void k_dgemm(DArgs a) {
     for (int nt = 0; nt < NT; ++nt) acc[nt] = f4_t{0.f, 0.f, 0.f, 0.f};
     // slice s of block kb with the W registers wrb and the fragment f
     auto compute = [&](int kb, int s, const WR (&wrb)[NT], const Frag &f, bool live) {
-        float sc[NT], mn[NT];
-#pragma unroll
-        for (int nt = 0; nt < NT; ++nt) {
-            W::scale(wrb[nt], s, sc[nt], mn[nt]);
-            sc[nt] = live ? sc[nt] : 0.f;
-            mn[nt] = live ? mn[nt] : 0.f;
-        }
-        float v[SK / 4];
-#pragma unroll
-        for (int i = 0; i < (PRO == PRO_SPLIT ? 0 : XQ); ++i) {
-            float4 e = f.x[i];
-            if constexpr (PRO == PRO_LN) {
-                const int k = kb * kStep + s * SK + kq * (SK / 4) + 4 * i;
-                const float4 g = *reinterpret_cast<const float4 *>(gb + k), b = *reinterpret_cast<const float4 *>(gb + K + k);
-                e = make_float4((e.x - mrow) * rrow * g.x + b.x, (e.y - mrow) * rrow * g.y + b.y,
-                                (e.z - mrow) * rrow * g.z + b.z, (e.w - mrow) * rrow * g.w + b.w);
-            }
-            v[4 * i] = e.x;
-            v[4 * i + 1] = e.y;
-            v[4 * i + 2] = e.z;
-            v[4 * i + 3] = e.w;
-        }
-        if constexpr (SK == 32) {
-            h8_t ah, al;
-            if constexpr (PRO == PRO_SPLIT) {
-                // whole-vector shuffles (component access would keep the ring in memory)
-                const h8_t p0 = __builtin_bit_cast(h8_t, f.x[0]), p1 = __builtin_bit_cast(h8_t, f.x[1]);
-                ah = __builtin_shufflevector(p0, p1, 0, 1, 2, 3, 8, 9, 10, 11);
-                al = __builtin_shufflevector(p0, p1, 4, 5, 6, 7, 12, 13, 14, 15);
-            } else {
-#pragma unroll
-                for (int i = 0; i < 8; ++i) {
-                    ah[i] = _Float16(v[i]);
-                    al[i] = _Float16(v[i] - float(ah[i]));
-                }
-            }
-            f4_t xs = f4_t{0.f, 0.f, 0.f, 0.f};
-            if constexpr (W::MIN) {  // per-row sums of the 32 X values: B = ones
-                const h8_t ones = {_Float16(1), _Float16(1), _Float16(1), _Float16(1),
-                                   _Float16(1), _Float16(1), _Float16(1), _Float16(1)};
-                xs = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, ones, xs, 0, 0, 0);
-                xs = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, ones, xs, 0, 0, 0);
-            }
-#pragma unroll
-            for (int nt = 0; nt < NT; ++nt) {
-                const h8_t bop = W::b(wrb[nt], s);
-                f4_t tmp = f4_t{0.f, 0.f, 0.f, 0.f};
-                tmp = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bop, tmp, 0, 0, 0);
-                tmp = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, bop, tmp, 0, 0, 0);
-#pragma unroll
-                for (int r = 0; r < 4; ++r)
-                    acc[nt][r] = W::MIN ? fmaf(sc[nt], tmp[r], fmaf(-mn[nt], xs[r], acc[nt][r]))
-                                        : fmaf(sc[nt], tmp[r], acc[nt][r]);
-            }
-        } else {
-            h4_t ah, al;
-            if constexpr (PRO == PRO_SPLIT) {
-                const h8_t p0 = __builtin_bit_cast(h8_t, f.x[0]);
-                ah = __builtin_shufflevector(p0, p0, 0, 1, 2, 3);
-                al = __builtin_shufflevector(p0, p0, 4, 5, 6, 7);
-            } else {
-#pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    ah[i] = _Float16(v[i]);
-                    al[i] = _Float16(v[i] - float(ah[i]));
-                }
-            }
-#pragma unroll
-            for (int nt = 0; nt < NT; ++nt) {
-                const h4_t bop = W::b(wrb[nt], s);
-                f4_t tmp = f4_t{0.f, 0.f, 0.f, 0.f};
-                tmp = __builtin_amdgcn_mfma_f32_16x16x16f16(ah, bop, tmp, 0, 0, 0);
-                tmp = __builtin_amdgcn_mfma_f32_16x16x16f16(al, bop, tmp, 0, 0, 0);
-#pragma unroll
-                for (int r = 0; r < 4; ++r) acc[nt][r] = fmaf(sc[nt], tmp[r], acc[nt][r]);
-            }
-        }
+        dg_slice<T, NT, PRO>(kb, s, kq, wrb, f, live, gb, K, mrow, rrow, acc);
     };
     static_for<0, BPW>([&](auto jc) {
         constexpr int j = decltype(jc)::value;
@@ -339,6 +358,296 @@ __global__ __launch_bounds__(kDgMaxNW * 64) void k_dgemm(DArgs a) {
             }
         }
     }
+}
+
+// ---- the cross attention of a decode step in one launch ----
+// crates/malaga-core/src/model.rs:573-578: q = cross_q(cross_norm(x)), then the cross
+// attention of q over the source keys.  Workgroup (h, g), 8 waves, owns the RG = 8 / S
+// rows [g RG, (g + 1) RG) and head h:
+//   1. LN(x) of those rows, normalized once (k_dgemm's PRO_LN arithmetic: the statistics
+//      partials added in the same order, the same expression) and split into f16 hi | lo
+//      quads in LDS, [K / 4][RG];
+//   2. q = LN(x) Wq^T + bq for the HD columns of the head on the MFMA units: wave w takes
+//      the column tiles 2 (w % TG), + 1 of the head and K block w / TG (K <= 1024: one
+//      block per wave), its A fragments from LDS (A-tile rows past RG repeat row RG - 1
+//      and are dropped); the KG partial tiles are added in K-block order, then the bias:
+//      k_dgemm's sums at its KG waves, so q is k_dgemm's bit for bit;
+//   3. the attention of those rows and that head, S waves per (row, head) pair: wave
+//      (pair p, split q) takes the keys SPL (S (c U + u) + q) + split of its lane splits
+//      (k_attn_waves' loop, k_ops.hip, at S = 1, same keys and order), with an online
+//      softmax; at S > 1 the S partials meet in LDS and are rescaled to their common max.
+// Every global operand is requested at the start: the W tiles, the X quads with gamma and
+// beta, the first chunk of keys and values (it depends neither on q nor on the key count,
+// so it arrives while the projection runs), then the statistics.  att goes out as split
+// fragments (frag_index), the A operand of the cross out-projection.
+constexpr int kDxHD = 64, kDxMaxBlocks = 256 / kDxHD, kDxMaxK = kDxMaxBlocks * kStep;
+
+template <int T, int HD, int S, bool TL>
+__global__ __launch_bounds__(512) void k_dxattn(DArgs a) {
+    using W = MW<T>;
+    using WR = typename W::Regs;
+    constexpr int SK = W::SK, XQ = SK / 16;
+    constexpr int NT = 2, TG = HD / 32, KG = 8 / TG, RG = 8 / S;
+    constexpr int TPK = HD / 8, SPL = 64 / TPK, U = 8 / S, RS = HD + 1, SLOT = HD + 2;
+    constexpr int QN = kDxMaxK / 16 / kLnTPR;   // statistics partials per thread
+    constexpr int SW = (16 * RG + 63) / 64;     // waves adding the statistics (16 lanes a row)
+    __shared__ uint4 xs[kDxMaxK / 4 * RG];      // LN(x) quads [hi0..hi3 | lo0..lo3], [K / 4][RG]
+    __shared__ float red[KG * RG * RS];
+    __shared__ float qs[RG * HD];
+    __shared__ float lnm[RG], lnr[RG];
+    __shared__ float scr[8 * 512];                  // the waves' [64][8] attention sums
+    __shared__ float slots[S > 1 ? 8 * SLOT : 1];   // S > 1: the waves' partials
+    const int t = threadIdx.x, lane = t & 63, ln = lane & 15, kq = lane >> 4;
+    const int wv = __builtin_amdgcn_readfirstlane(t >> 6);
+    const int K = a.w.K, hh = blockIdx.x, m0 = blockIdx.y * RG;
+    const int tile0 = hh * (HD / 16) + 2 * (wv % TG), kw = wv / TG;
+    const int kb = min(kw, K / kStep - 1);
+    const bool live = kw < K / kStep;  // scalar; a block past the end weighs 0
+
+    WR wr[NT];
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) load_w<T, TL>(a.w, tile0 + nt, ln, kb, kq, wr[nt]);
+    // quad f = t of the RG rows with its gamma and beta (threads t < K / 4: whole waves)
+    const int f = min(t, K / 4 - 1);
+    const float4 *xfr = reinterpret_cast<const float4 *>(a.x);
+    float4 xv[RG], gv, bv;
+    if (wv < K / 256) {  // scalar
+#pragma unroll
+        for (int r = 0; r < RG; ++r) xv[r] = xfr[frag_index(min(m0 + r, a.M - 1), 4 * f, K)];
+        gv = ld4(a.gamma, f);
+        bv = ld4(a.beta, f);
+    }
+
+    // this wave's (row, head) pair and the first chunk of its keys and values (keys past
+    // the row's count are read at slot L - 1 and masked when used)
+    const int pr = wv / S, ks = wv % S, bi = min(m0 + pr, a.M - 1);
+    const int sub = lane % TPK, split = lane / TPK, L = a.slots, d = a.H * HD;
+    const size_t kv0 = (size_t(bi) * a.H + hh) * size_t(L) * HD + sub * 8;
+    uint4 kr[U], vr[U];
+    auto key = [&](int c, int u) { return SPL * (S * (c * U + u) + ks) + split; };
+    auto load_kv = [&](int c) {
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const size_t o = kv0 + size_t(min(key(c, u), L - 1)) * HD;
+            kr[u] = *reinterpret_cast<const uint4 *>(a.kc + o);
+            vr[u] = *reinterpret_cast<const uint4 *>(a.vc + o);
+        }
+    };
+    load_kv(0);
+    const int n = int(a.lens[bi]);
+    // all of the above is requested before any of it is used
+    __builtin_amdgcn_sched_barrier(0);
+
+    // the row statistics: partials p = t % 16 + 16 q of row t / 16 (rows past RG repeat
+    // RG - 1), requested last by the waves that add them (a branch around loads whose
+    // values outlive it would wait for them before the loads after it)
+    if (wv < SW) {  // scalar
+        const int j = t & 15, ml = t >> 4;
+        const int m = min(m0 + min(ml, RG - 1), a.M - 1);
+        double2 sp[QN];
+#pragma unroll
+        for (int q = 0; q < QN; ++q) {
+            const int p = min(j + q * kLnTPR, a.P - 1);
+            sp[q] = *reinterpret_cast<const double2 *>(a.stats + (size_t(m) * a.P + p) * 2);
+        }
+        double s1 = 0.0, s2 = 0.0;
+#pragma unroll
+        for (int q = 0; q < QN; ++q)
+            if (j + q * kLnTPR < a.P) {
+                s1 += sp[q].x;
+                s2 += sp[q].y;
+            }
+        s1 = group_sum_f64<kLnTPR>(s1);
+        s2 = group_sum_f64<kLnTPR>(s2);
+        if (j == 0 && ml < RG) {
+            const double mu = s1 / K, var = fmax(s2 / K - mu * mu, 0.0);
+            lnm[ml] = m0 + ml < a.M ? float(mu) : 0.f;
+            lnr[ml] = m0 + ml < a.M ? float(1.0 / sqrt(var + double(a.eps))) : 0.f;
+        }
+    }
+    __syncthreads();
+    if (wv < K / 256) {
+#pragma unroll
+        for (int r = 0; r < RG; ++r) {
+            const float mr = lnm[r], rr = lnr[r];
+            const float4 e = xv[r];
+            const float v[4] = {(e.x - mr) * rr * gv.x + bv.x, (e.y - mr) * rr * gv.y + bv.y,
+                                (e.z - mr) * rr * gv.z + bv.z, (e.w - mr) * rr * gv.w + bv.w};
+            h4_t hv, lv;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                hv[j] = _Float16(v[j]);
+                lv[j] = _Float16(v[j] - float(hv[j]));
+            }
+            const uint2 hb = __builtin_bit_cast(uint2, hv), lb = __builtin_bit_cast(uint2, lv);
+            xs[f * RG + r] = make_uint4(hb.x, hb.y, lb.x, lb.y);
+        }
+    }
+    __syncthreads();
+
+    f4_t acc[NT];
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) acc[nt] = f4_t{0.f, 0.f, 0.f, 0.f};
+    const int ar = min(ln, RG - 1);
+    static_for<0, W::SLICES>([&](auto sc) {
+        constexpr int s = decltype(sc)::value;
+        DFrag<XQ> fr;
+#pragma unroll
+        for (int i = 0; i < XQ; ++i)
+            fr.x[i] = __builtin_bit_cast(float4, xs[(kb * (kStep / 4) + s * (SK / 4) + kq * (SK / 16) + i) * RG + ar]);
+        dg_slice<T, NT, PRO_SPLIT>(kb, s, kq, wr, fr, live, nullptr, K, 0.f, 0.f, acc);
+    });
+    // the K blocks' partial tiles (lane: column nt 16 + ln, A rows 4 kq .. 4 kq + 3), then
+    // q = their sum in K-block order + bias, in LDS
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt)
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+            if (4 * kq + r < RG) red[(kw * RG + 4 * kq + r) * RS + (wv % TG) * 32 + nt * 16 + ln] = acc[nt][r];
+    __syncthreads();
+    for (int o = t; o < RG * HD; o += 512) {
+        const int r = o / HD, c = o % HD;
+        float v = red[r * RS + c];
+        for (int w = 1; w < KG; ++w) v += red[(w * RG + r) * RS + c];
+        v += a.bias ? a.bias[hh * HD + c] : 0.f;
+        qs[o] = v;
+    }
+    __syncthreads();
+
+    const float *qp = qs + pr * HD + sub * 8;
+    const float4 qa = *reinterpret_cast<const float4 *>(qp), qb = *reinterpret_cast<const float4 *>(qp + 4);
+    float m = -INFINITY, l = 0.f;
+    float o8[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    for (int c = 0; SPL * (S * c * U + ks) < n; ++c) {  // wave-uniform; chunk 0 is in flight
+        if (c) load_kv(c);
+        float sc[U];
+        float cmax = -INFINITY;
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            float sdot = h2f(kr[u].x) * qa.x;
+            sdot = fmaf(h2f(kr[u].x >> 16), qa.y, sdot);
+            sdot = fmaf(h2f(kr[u].y), qa.z, sdot);
+            sdot = fmaf(h2f(kr[u].y >> 16), qa.w, sdot);
+            sdot = fmaf(h2f(kr[u].z), qb.x, sdot);
+            sdot = fmaf(h2f(kr[u].z >> 16), qb.y, sdot);
+            sdot = fmaf(h2f(kr[u].w), qb.z, sdot);
+            sdot = fmaf(h2f(kr[u].w >> 16), qb.w, sdot);
+            sdot = group_sum<TPK>(sdot);
+            sc[u] = key(c, u) < n ? sdot : -INFINITY;
+            cmax = fmaxf(cmax, sc[u]);
+        }
+        const float mnew = fmaxf(m, wave_max(cmax));  // finite: the chunk's first key is valid
+        const float rs = expf(m - mnew);
+        l *= rs;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) o8[e] *= rs;
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const bool in = key(c, u) < n;
+            const float pj = in ? expf(sc[u] - mnew) : 0.f;
+            l += pj;
+            const uint32_t wv4[4] = {in ? vr[u].x : 0u, in ? vr[u].y : 0u, in ? vr[u].z : 0u, in ? vr[u].w : 0u};
+#pragma unroll
+            for (int q2 = 0; q2 < 4; ++q2) {
+                o8[2 * q2] = fmaf(pj, h2f(wv4[q2]), o8[2 * q2]);
+                o8[2 * q2 + 1] = fmaf(pj, h2f(wv4[q2] >> 16), o8[2 * q2 + 1]);
+            }
+        }
+        m = mnew;
+    }
+    // every lane of a split holds that split's sum: count each split once
+    const float lsum = wave_sum(sub == 0 ? l : 0.f);
+    float *wsc = scr + wv * 512;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) wsc[lane * 8 + e] = o8[e];
+    __builtin_amdgcn_s_waitcnt(0xc07f);  // this wave's LDS writes are done
+    __builtin_amdgcn_wave_barrier();
+    // split fragments [hi0..hi3 | lo0..lo3] of att[bi][h HD + 4 e4 ..], one lane per 4 values
+    auto store4 = [&](int e4, const float (&v)[4]) {
+        h4_t hv, lv;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            hv[j] = _Float16(v[j]);
+            lv[j] = _Float16(v[j] - float(hv[j]));
+        }
+        const uint2 hb = __builtin_bit_cast(uint2, hv), lb = __builtin_bit_cast(uint2, lv);
+        reinterpret_cast<uint4 *>(a.y)[frag_index(bi, hh * HD + 4 * e4, d)] = make_uint4(hb.x, hb.y, lb.x, lb.y);
+    };
+    const bool own = m0 + pr < a.M;  // scalar
+    if constexpr (S == 1) {
+        const float inv = 1.f / lsum;
+        if (own)
+            for (int e4 = lane; e4 < HD / 4; e4 += 64) {
+                float v[4];
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const int e = 4 * e4 + j;
+                    float o = 0.f;
+#pragma unroll
+                    for (int s2 = 0; s2 < SPL; ++s2) o += wsc[(s2 * TPK + e / 8) * 8 + e % 8];
+                    v[j] = o * inv;
+                }
+                store4(e4, v);
+            }
+    } else {
+        // this wave's partial: sum_j p_j v_j over its keys, its max (-inf without keys) and sum p_j
+        float *slot = slots + wv * SLOT;
+        for (int e = lane; e < HD; e += 64) {
+            float o = 0.f;
+#pragma unroll
+            for (int s2 = 0; s2 < SPL; ++s2) o += wsc[(s2 * TPK + e / 8) * 8 + e % 8];
+            slot[e] = o;
+        }
+        if (lane == 0) {
+            slot[HD] = m;
+            slot[HD + 1] = lsum;
+        }
+        __syncthreads();
+        if (ks == 0 && own) {  // scalar; the pair's wave 0 has key 0, so its max is finite
+            const float *ps = slots + wv * SLOT;
+            float mx = ps[HD];
+#pragma unroll
+            for (int q = 1; q < S; ++q) mx = fmaxf(mx, ps[q * SLOT + HD]);
+            float ew[S], den = 0.f;
+#pragma unroll
+            for (int q = 0; q < S; ++q) {
+                ew[q] = expf(ps[q * SLOT + HD] - mx);
+                den += ew[q] * ps[q * SLOT + HD + 1];
+            }
+            const float inv = 1.f / den;
+            for (int e4 = lane; e4 < HD / 4; e4 += 64) {
+                float v[4];
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    float o = 0.f;
+#pragma unroll
+                    for (int q = 0; q < S; ++q) o += ew[q] * ps[q * SLOT + 4 * e4 + j];
+                    v[j] = o * inv;
+                }
+                store4(e4, v);
+            }
+        }
+    }
+}
+
+
+// Waves of S per (row, head) pair: 4 (2 rows per workgroup)
+constexpr int kDxSplit = 4;
+inline int dx_rows() { return 8 / kDxSplit; }
+// Heads of 64 and K <= 1024 (d_model of the 600M and 1.3B checkpoints): one K block per
+// wave; other shapes keep the two launches.
+
+template <int T>
+hipError_t launch_dxattn_t(const DArgs &a, hipStream_t st) {
+    const dim3 grid(unsigned(a.H), unsigned((a.M + dx_rows() - 1) / dx_rows()));
+    if constexpr (T == GGML_Q6_K || T == GGML_Q4_K) {
+        if (a.w.t) {
+            hipLaunchKernelGGL((k_dxattn<T, kDxHD, kDxSplit, true>), grid, dim3(512), 0, st, a);
+            return hipGetLastError();
+        }
+    }
+    hipLaunchKernelGGL((k_dxattn<T, kDxHD, kDxSplit, false>), grid, dim3(512), 0, st, a);
+    return hipGetLastError();
 }
 
 // The K split: 4 waves up to four K blocks (K <= 1024), else 8 waves of 1, 2 or 4 blocks.
@@ -469,6 +778,35 @@ hipError_t dgemm_qkv(const DevMatrix &w, const float *x, int ldx, int M, const D
     a.slots = slots;
     a.step = step;
     return ln ? launch_dgemm_t<PRO_LN, EPI_QKV>(w, a, st) : launch_dgemm_t<PRO_RAW, EPI_QKV>(w, a, st);
+}
+
+bool dgemm_cross_attn_supported(const DevMatrix &w, int M, int H, int hd) {
+    return dgemm_supported(w, M) && hd == kDxHD && H >= 1 && w.N == H * hd && w.K / kStep <= kDxMaxBlocks;
+}
+
+hipError_t dgemm_cross_attn(const DevMatrix &w, const float *x, int M, const DgemmLn &ln, const float *bias,
+                            const __half *K, const __half *V, int H, int hd, int L, const uint32_t *lens, float *att,
+                            hipStream_t st) {
+    if (!dgemm_cross_attn_supported(w, M, H, hd) || !dgemm_args_ok(w, x, w.K, M, &ln) || !K || !V || !lens || !att ||
+        L < 1 || reinterpret_cast<uintptr_t>(K) % 16 || reinterpret_cast<uintptr_t>(V) % 16 ||
+        reinterpret_cast<uintptr_t>(att) % 16)
+        return hipErrorInvalidValue;
+    DArgs a = dargs(w, x, w.K, M, &ln, bias);
+    a.kc = const_cast<__half *>(K);
+    a.vc = const_cast<__half *>(V);
+    a.H = H;
+    a.hd = hd;
+    a.slots = L;
+    a.lens = lens;
+    a.y = att;
+    switch (w.type) {
+    case GGML_Q4_K: return launch_dxattn_t<GGML_Q4_K>(a, st);
+    case GGML_Q5_K: return launch_dxattn_t<GGML_Q5_K>(a, st);
+    case GGML_Q6_K: return launch_dxattn_t<GGML_Q6_K>(a, st);
+    case GGML_Q8_0: return launch_dxattn_t<GGML_Q8_0>(a, st);
+    case GGML_F16: return launch_dxattn_t<GGML_F16>(a, st);
+    default: return hipErrorInvalidValue;
+    }
 }
 
 }  // namespace mlg

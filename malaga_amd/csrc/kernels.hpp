@@ -123,6 +123,13 @@ hipError_t dgemm_resid(const DevMatrix &w, const float *x, int ldx, int M, const
 // The fused QKV projection: q [M][d] f32, K/V f16 into the caches [M][H][slots][hd] at *step.
 hipError_t dgemm_qkv(const DevMatrix &w, const float *x, int ldx, int M, const DgemmLn *ln, const float *bias, int H,
                      int hd, int slots, const uint32_t *step, float *q, __half *kc, __half *vc, hipStream_t st);
+// The cross attention of a decode step in one launch: q = LN(x) W^T + bias (x the residual
+// stream, fragment order) and its attention over K/V [M][H][L][hd] (f16, lens[m] keys
+// each); att [M][H hd] as split fragments, the cross out-projection's A operand.
+bool dgemm_cross_attn_supported(const DevMatrix &w, int M, int H, int hd);
+hipError_t dgemm_cross_attn(const DevMatrix &w, const float *x, int M, const DgemmLn &ln, const float *bias,
+                            const __half *K, const __half *V, int H, int hd, int L, const uint32_t *lens, float *att,
+                            hipStream_t st);
 
 // M <= 32 rows with X resident in LDS (K <= 1024 at M > 16, K <= 2048 at M <= 16).
 bool gemm_rx_supported(const DevMatrix &w, int M);

@@ -1030,9 +1030,16 @@ void Model::step_dgemm(StaticState &st, bool greedy_mode, int mask_id) {
         check_hip(attn_decode(st.q, st.kc[i], st.vc[i], B, H, hd, st.m, nullptr, st.step, st.att, s, st.rows, true),
                   "attn");
         check_hip(dgemm_resid(l.out.w, st.att, d, B, l.out.b, st.x, st.lnstat, s, true), "dgemm_out");
-        check_hip(dgemm_store(l.cross_q.w, st.x, d, B, &ln_cross, l.cross_q.b, false, st.q, d, s), "dgemm_cross_q");
-        check_hip(attn_decode(st.q, st.ck[i], st.cv[i], B, H, hd, st.s, st.lens, nullptr, st.att, s, nullptr, true),
-                  "attn");
+        if (!split_cross_ && dgemm_cross_attn_supported(l.cross_q.w, B, H, hd)) {
+            check_hip(dgemm_cross_attn(l.cross_q.w, st.x, B, ln_cross, l.cross_q.b, st.ck[i], st.cv[i], H, hd, st.s,
+                                       st.lens, st.att, s),
+                      "dgemm_cross_attn");
+        } else {
+            check_hip(dgemm_store(l.cross_q.w, st.x, d, B, &ln_cross, l.cross_q.b, false, st.q, d, s),
+                      "dgemm_cross_q");
+            check_hip(attn_decode(st.q, st.ck[i], st.cv[i], B, H, hd, st.s, st.lens, nullptr, st.att, s, nullptr, true),
+                      "attn");
+        }
         check_hip(dgemm_resid(l.cross_out.w, st.att, d, B, l.cross_out.b, st.x, st.lnstat, s, true), "dgemm_cross_out");
         check_hip(dgemm_store(l.up.w, st.x, d, B, &ln_ffn, l.up.b, true, st.u, f, s, true), "dgemm_up");
         check_hip(dgemm_resid(l.down.w, st.u, f, B, l.down.b, st.x, st.lnstat, s, true), "dgemm_down");

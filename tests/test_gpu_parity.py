@@ -239,6 +239,42 @@ def test_fused_cross_attention_equals_split_kernels(kq_gguf, models, preset, nb)
         split.close()
 
 
+@pytest.mark.parametrize("preset", ["q4_k_m", "q6_k", "q8_0"])
+@pytest.mark.parametrize("nb", [7, 33])
+def test_batched_fused_cross_attention(kq_gguf, models, preset, nb):
+    """k_dxattn (batches of 5..64 rows: cross_q with the cross LayerNorm and the cross
+    attention in one launch, 4 rows x 1 head per workgroup) against the same steps with the
+    two launches (MALAGA_SPLIT_CROSS_STEP=1).  q is the same sum in the same order; the
+    attention splits each pair's keys over two waves and rescales their partials, so the
+    logits agree to f32 rounding, not bit for bit (measured 1.1e-4 at logits of ~5; the bar
+    is 5e-4, four times below the oracle's).  7 rows leave a partial row group;
+    33 pad to 64 rows, the last 31 idle."""
+    import os
+
+    gpu, orc = models(kq_gguf(preset))
+    os.environ["MALAGA_SPLIT_CROSS_STEP"] = "1"
+    try:
+        split = M.Translator.load(kq_gguf(preset))
+    finally:
+        del os.environ["MALAGA_SPLIT_CROSS_STEP"]
+    rng = np.random.default_rng(400 + nb)
+    src = [[997] + rng.integers(4, 990, int(n)).tolist() + [2] for n in rng.integers(2, 60, nb)]
+    T = 8
+    tgt = np.zeros((nb, T), np.uint32)
+    tgt[:, 0], tgt[:, 1] = 2, 998
+    tgt[:, 2:] = rng.integers(4, 990, (nb, T - 2))
+    try:
+        lg = gpu.teacher_forced_logits(src, tgt)
+        assert np.abs(lg - split.teacher_forced_logits(src, tgt)).max() < 5e-4
+        assert np.abs(lg - orc.teacher_forced_logits(src, tgt, kv_f16=True)).max() < 2e-3
+        want, gap = orc.translate_batch(src, 998, max_batch=64, kv_f16=True, max_new_tokens=10)
+        got = gpu.generate(src, 998, M.GenOptions(max_new_tokens=10, max_batch=64))
+        assert got == want, f"min top-2 gap {gap}"
+        assert split.generate(src, 998, M.GenOptions(max_new_tokens=10, max_batch=64)) == want
+    finally:
+        split.close()
+
+
 @pytest.mark.parametrize("preset", ["q4_k_m", "q5_k_m", "q6_k", "q8_0", "f16"])
 @pytest.mark.parametrize("nb", [7, 16, 33])
 def test_batched_decode_mfma_path(kq_gguf, models, preset, nb):
