@@ -325,6 +325,8 @@ void mlg_gen_options_default(mlg_gen_options *o) {
     o->shortlist = nullptr;
 }
 
+}  // extern "C"
+
 namespace {
 mlg::GenOptions gen_options(const mlg_gen_options *o) {
     mlg::GenOptions g;
@@ -339,6 +341,8 @@ mlg::GenOptions gen_options(const mlg_gen_options *o) {
     return g;
 }
 }  // namespace
+
+extern "C" {
 
 int mlg_generate(mlg_model *m, const uint32_t *ids, const uint32_t *lens, int n, uint32_t tgt_lang,
                  const mlg_gen_options *o, uint32_t *out, int out_cap, int *out_len) {

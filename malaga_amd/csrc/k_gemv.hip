@@ -305,7 +305,7 @@ int gemv_argmax_parts(const DevMatrix &w, int b) {
     if (b < 1 || b > gemv_max_batch(w) || !gemv_geometry(w, &g, &cpl)) return gemv_grid(w, 1);
     GemvArgs a = make_args(w, g, nullptr, 0, b);
     int grid = gemv_grid(w, 1);
-    dispatch<1>(w.type, a, gemv_round_b(b), cpl, grid, nullptr, w.lm, false);
+    (void)dispatch<1>(w.type, a, gemv_round_b(b), cpl, grid, nullptr, w.lm, false);  // the grid only: no launch
     return grid;
 }
 

@@ -589,7 +589,7 @@ constexpr int kXItems = 4;      // (row, chunk) items of the q projection per th
 // dot4u8 as one asm block: each byte is converted where it is used, so a schedule
 // cannot convert every item's bytes ahead of their products (which overflows the
 // registers of a multi-item dot); same operations, same order
-__device__ __forceinline__ float dot4u8_chain(uint32_t v, const float (&x)[4], float acc) {
+[[maybe_unused]] __device__ __forceinline__ float dot4u8_chain(uint32_t v, const float (&x)[4], float acc) {
     float t0, t1, t2, t3;
     asm("v_cvt_f32_ubyte0 %1, %5\n\t"
         "v_cvt_f32_ubyte1 %2, %5\n\t"

@@ -243,11 +243,11 @@ def test_fused_cross_attention_equals_split_kernels(kq_gguf, models, preset, nb)
 @pytest.mark.parametrize("nb", [7, 33])
 def test_batched_fused_cross_attention(kq_gguf, models, preset, nb):
     """k_dxattn (batches of 5..64 rows: cross_q with the cross LayerNorm and the cross
-    attention in one launch, 4 rows x 1 head per workgroup) against the same steps with the
+    attention in one launch, 2 rows x 1 head per workgroup) against the same steps with the
     two launches (MALAGA_SPLIT_CROSS_STEP=1).  q is the same sum in the same order; the
-    attention splits each pair's keys over two waves and rescales their partials, so the
-    logits agree to f32 rounding, not bit for bit (measured 1.1e-4 at logits of ~5; the bar
-    is 5e-4, four times below the oracle's).  7 rows leave a partial row group;
+    attention splits each pair's keys over four waves and rescales their partials, so the
+    logits agree to f32 rounding, not bit for bit (1.1e-4 measured with two waves at logits
+    of ~5; the bar is 5e-4, four times below the oracle's).  7 rows leave a partial row group;
     33 pad to 64 rows, the last 31 idle."""
     import os
 
