@@ -374,7 +374,7 @@ __global__ __launch_bounds__(kDgMaxNW * 64) void k_dgemm(DArgs a) {
 //      k_dgemm's sums at its KG waves, so q is k_dgemm's bit for bit;
 //   3. the attention of those rows and that head, S waves per (row, head) pair: wave
 //      (pair p, split q) takes the keys SPL (S (c U + u) + q) + split of its lane splits
-//      (k_attn_waves' loop, k_ops.hip, at S = 1, same keys and order), with an online
+//      (k_attn_waves' loop, k_ops.hip: the same keys and order at the same S), with an online
 //      softmax; at S > 1 the S partials meet in LDS and are rescaled to their common max.
 // Every global operand is requested at the start: the W tiles, the X quads with gamma and
 // beta, the first chunk of keys and values (it depends neither on q nor on the key count,

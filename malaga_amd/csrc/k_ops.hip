@@ -388,41 +388,46 @@ __global__ __launch_bounds__(1024) void k_greedy_finalize(const float *pv, const
     if (threadIdx.x == 0) *step = s + 1;
 }
 
-// Batched decode attention, one wave per (row, head) pair, no workgroup barrier:
-// lane (split, sub) owns dimensions [8 sub, 8 sub + 8) of keys j = k SPL + split; the
-// scores of a chunk of U SPL keys feed an online softmax (running max and sum), and
-// the splits are combined through the wave's LDS scratch at the end.
-template <int HD>
+// Batched decode attention, S waves per (row, head) pair (4 / S pairs per workgroup of 4
+// waves): lane (split, sub) of wave q of the pair owns dimensions [8 sub, 8 sub + 8) of
+// the keys SPL (S (c U + u) + q) + split, pass u < U = 8 / S of chunk c; the scores of a
+// chunk feed an online softmax (running max and sum), and the wave's splits are combined
+// through its LDS scratch at the end.  S = 1: no workgroup barrier; S > 1: the S partials
+// (sum p_j v_j unnormalized, max, sum p_j) meet in LDS and the pair's first wave rescales
+// them to their common max.
+template <int HD, int S>
 __global__ __launch_bounds__(256) void k_attn_waves(const float *q, const __half *K, const __half *V, int b, int H,
                                                     int L, const uint32_t *lens, const uint32_t *step, float *out,
                                                     const uint32_t *rows, int out_split) {
-    constexpr int TPK = HD / 8, SPL = 64 / TPK, U = 8;
+    constexpr int TPK = HD / 8, SPL = 64 / TPK, U = 8 / S, SLOT = HD + 2;
     __shared__ float wsc_all[4 * 512];
+    __shared__ float slots[S > 1 ? 4 * SLOT : 1];
     // w a scalar: the pair, its row and the key count stay in scalar registers
     const int lane = threadIdx.x & 63, w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int p = blockIdx.x * 4 + w;
-    if (p >= b * H) return;  // wave-uniform; no workgroup barrier below
+    const int ks = w % S, p0 = blockIdx.x * (4 / S) + w / S;
+    if (S == 1 && p0 >= b * H) return;  // wave-uniform; no workgroup barrier below
+    const int p = min(p0, b * H - 1);  // S > 1: a pair past the end runs on the last and is not stored
     float *wsc = wsc_all + w * 512;
     const int bi = p / H, hh = p % H, d = H * HD;
     const int sub = lane % TPK, split = lane / TPK;
+    auto key = [&](int c, int u) { return SPL * (S * (c * U + u) + ks) + split; };
     // Order of issue: the first chunk's cache rows (beam's row map) and keys/values, q,
     // then the key count.  The addresses do not depend on the count (keys past it are
     // masked when used), so the chunk is not held back by that scalar read; the loads
     // complete in order.
     uint4 kr[U], vr[U];
-    auto load_chunk = [&](int j0) {
+    auto load_chunk = [&](int c) {
         size_t r[U];
         if (rows) {  // kernel argument: wave-uniform
 #pragma unroll
-            for (int u = 0; u < U; ++u) r[u] = rows[size_t(bi) * L + min(j0 + u * SPL + split, L - 1)];
+            for (int u = 0; u < U; ++u) r[u] = rows[size_t(bi) * L + min(key(c, u), L - 1)];
         } else {
 #pragma unroll
             for (int u = 0; u < U; ++u) r[u] = size_t(bi);
         }
 #pragma unroll
         for (int u = 0; u < U; ++u) {
-            const int j = min(j0 + u * SPL + split, L - 1);
-            const size_t o = ((r[u] * H + hh) * L + j) * HD + sub * 8;
+            const size_t o = ((r[u] * H + hh) * L + min(key(c, u), L - 1)) * HD + sub * 8;
             kr[u] = *reinterpret_cast<const uint4 *>(K + o);
             vr[u] = *reinterpret_cast<const uint4 *>(V + o);
         }
@@ -434,8 +439,8 @@ __global__ __launch_bounds__(256) void k_attn_waves(const float *q, const __half
     const int n = lens ? int(lens[bi]) : int(*step) + 1;
     float m = -INFINITY, l = 0.f;
     float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-    for (int j0 = 0; j0 < n; j0 += U * SPL) {
-        if (j0) load_chunk(j0);
+    for (int c = 0; SPL * (S * c * U + ks) < n; ++c) {  // wave-uniform; chunk 0 is in flight
+        if (c) load_chunk(c);
         float sc[U];
         float cmax = -INFINITY;
 #pragma unroll
@@ -449,17 +454,17 @@ __global__ __launch_bounds__(256) void k_attn_waves(const float *q, const __half
             sdot = fmaf(h2f(kr[u].w), qb.z, sdot);
             sdot = fmaf(h2f(kr[u].w >> 16), qb.w, sdot);
             sdot = group_sum<TPK>(sdot);
-            sc[u] = j0 + u * SPL + split < n ? sdot : -INFINITY;
+            sc[u] = key(c, u) < n ? sdot : -INFINITY;
             cmax = fmaxf(cmax, sc[u]);
         }
-        const float mnew = fmaxf(m, wave_max(cmax));  // finite: key j0 is valid
+        const float mnew = fmaxf(m, wave_max(cmax));  // finite: the chunk's first key is valid
         const float rs = expf(m - mnew);
         l *= rs;
 #pragma unroll
         for (int e = 0; e < 8; ++e) acc[e] *= rs;
 #pragma unroll
         for (int u = 0; u < U; ++u) {
-            const bool in = j0 + u * SPL + split < n;
+            const bool in = key(c, u) < n;
             const float pj = in ? expf(sc[u] - mnew) : 0.f;
             l += pj;
             const uint32_t wv[4] = {in ? vr[u].x : 0u, in ? vr[u].y : 0u, in ? vr[u].z : 0u, in ? vr[u].w : 0u};
@@ -471,22 +476,61 @@ __global__ __launch_bounds__(256) void k_attn_waves(const float *q, const __half
         }
         m = mnew;
     }
-    const float inv = 1.f / wave_sum(sub == 0 ? l : 0.f);
+    // every lane of a split holds that split's sum: count each split once
+    const float lsum = wave_sum(sub == 0 ? l : 0.f);
 #pragma unroll
     for (int e = 0; e < 8; ++e) wsc[lane * 8 + e] = acc[e];
     __builtin_amdgcn_s_waitcnt(0xc07f);
     __builtin_amdgcn_wave_barrier();
+    // output e of the pair: sum over the splits of wave q's scratch, rescaled by ew[q]
+    const float *ps = S > 1 ? slots + (w - ks) * SLOT : slots;  // S > 1: the pair's partials
+    float ew[S], inv;
+    if constexpr (S == 1) {
+        ew[0] = 1.f;
+        inv = 1.f / lsum;
+    } else {
+        float *slot = slots + w * SLOT;
+        for (int e = lane; e < HD; e += 64) {
+            float o = 0.f;
+#pragma unroll
+            for (int s2 = 0; s2 < SPL; ++s2) o += wsc[(s2 * TPK + e / 8) * 8 + e % 8];
+            slot[e] = o;
+        }
+        if (lane == 0) {
+            slot[HD] = m;  // -inf when this wave had no key
+            slot[HD + 1] = lsum;
+        }
+        __syncthreads();
+        if (ks != 0 || p0 >= b * H) return;  // scalar; no barrier below
+        float mx = ps[HD];  // finite: the pair's first wave has key 0
+#pragma unroll
+        for (int qq = 1; qq < S; ++qq) mx = fmaxf(mx, ps[qq * SLOT + HD]);
+        float den = 0.f;
+#pragma unroll
+        for (int qq = 0; qq < S; ++qq) {
+            ew[qq] = expf(ps[qq * SLOT + HD] - mx);
+            den += ew[qq] * ps[qq * SLOT + HD + 1];
+        }
+        inv = 1.f / den;
+    }
+    auto value = [&](int e) {
+        float o = 0.f;
+        if constexpr (S == 1) {
+#pragma unroll
+            for (int s2 = 0; s2 < SPL; ++s2) o += wsc[(s2 * TPK + e / 8) * 8 + e % 8];
+        } else {
+#pragma unroll
+            for (int qq = 0; qq < S; ++qq) o += ew[qq] * ps[qq * SLOT + e];
+        }
+        return o * inv;
+    };
     if (out_split) {
         // split fragments [hi0..hi3 | lo0..lo3]: one lane per 4 values, one whole store each
         for (int e4 = lane; e4 < HD / 4; e4 += 64) {
             h4_t hv, lv;
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
-                const int e = 4 * e4 + j;
-                float o = 0.f;
-#pragma unroll
-                for (int s2 = 0; s2 < SPL; ++s2) o += wsc[(s2 * TPK + e / 8) * 8 + e % 8];
-                o *= inv;
+                const float o = value(4 * e4 + j);
                 hv[j] = _Float16(o);
                 lv[j] = _Float16(o - float(hv[j]));
             }
@@ -495,12 +539,7 @@ __global__ __launch_bounds__(256) void k_attn_waves(const float *q, const __half
         }
         return;
     }
-    for (int e = lane; e < HD; e += 64) {
-        float o = 0.f;
-#pragma unroll
-        for (int s2 = 0; s2 < SPL; ++s2) o += wsc[(s2 * TPK + e / 8) * 8 + e % 8];
-        out[size_t(bi) * d + hh * HD + e] = o * inv;
-    }
+    for (int e = lane; e < HD; e += 64) out[size_t(bi) * d + hh * HD + e] = value(e);
 }
 
 // ---- log-softmax + top-k (beam search) ------------------------------------
@@ -829,6 +868,8 @@ hipError_t qkv_split(const float *qkv, int b, int H, int hd, int m, const uint32
     return hipGetLastError();
 }
 
+constexpr int kAttnSplit = 4;  // waves per (row, head) pair in k_attn_waves
+
 bool attn_head_size_supported(int hd) {
     return hd == 8 || hd == 16 || hd == 32 || hd == 64 || hd == 128 || hd == 256;
 }
@@ -838,12 +879,13 @@ hipError_t attn_decode(const float *q, const __half *K, const __half *V, int b, 
                        bool out_split) {
     if (b * H <= 0) return hipSuccess;
     if (out_split && ((H * hd) % 16 || reinterpret_cast<uintptr_t>(out) % 16)) return hipErrorInvalidValue;
-    const dim3 wgrid(unsigned((b * H + 3) / 4));
+    constexpr int ppw = 4 / kAttnSplit;  // pairs per workgroup of 4 waves
+    const dim3 wgrid(unsigned((b * H + ppw - 1) / ppw));
     switch (hd) {
 #define MLG_ATTN_WAVES(HD)                                                                                          \
     case HD:                                                                                                        \
-        hipLaunchKernelGGL(k_attn_waves<HD>, wgrid, dim3(256), 0, st, q, K, V, b, H, L, lens, step, out, rows,      \
-                           out_split ? 1 : 0);                                                                      \
+        hipLaunchKernelGGL((k_attn_waves<HD, kAttnSplit>), wgrid, dim3(256), 0, st, q, K, V, b, H, L, lens, step,   \
+                           out, rows, out_split ? 1 : 0);                                                           \
         return hipGetLastError();
         MLG_ATTN_WAVES(8)
         MLG_ATTN_WAVES(16)
