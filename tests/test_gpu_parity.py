@@ -242,13 +242,12 @@ def test_fused_cross_attention_equals_split_kernels(kq_gguf, models, preset, nb)
 @pytest.mark.parametrize("preset", ["q4_k_m", "q6_k", "q8_0"])
 @pytest.mark.parametrize("nb", [7, 33])
 def test_batched_fused_cross_attention(kq_gguf, models, preset, nb):
-    """k_dxattn (batches of 5..64 rows: cross_q with the cross LayerNorm and the cross
-    attention in one launch, 2 rows x 1 head per workgroup) against the same steps with the
-    two launches (MALAGA_SPLIT_CROSS_STEP=1).  q is the same sum in the same order; the
-    attention splits each pair's keys over four waves and rescales their partials, so the
-    logits agree to f32 rounding, not bit for bit (1.1e-4 measured with two waves at logits
-    of ~5; the bar is 5e-4, four times below the oracle's).  7 rows leave a partial row group;
-    33 pad to 64 rows, the last 31 idle."""
+    """k_dxattn (batches of 5..64 rows, heads of 64: cross_q with the cross LayerNorm and
+    the cross attention in one launch, 2 rows x 1 head per workgroup, 4 waves per (row,
+    head) pair) against the same steps with the two launches (MALAGA_SPLIT_CROSS_STEP=1):
+    q adds the same partials in the same order as k_dgemm and the attention takes the same
+    keys in the same order as k_attn_waves, so the logits are equal bit for bit.  7 rows
+    leave a partial row pair; 33 pad to 64 rows; beam 4 over two sentences gives 8 rows."""
     import os
 
     gpu, orc = models(kq_gguf(preset))
@@ -265,12 +264,14 @@ def test_batched_fused_cross_attention(kq_gguf, models, preset, nb):
     tgt[:, 2:] = rng.integers(4, 990, (nb, T - 2))
     try:
         lg = gpu.teacher_forced_logits(src, tgt)
-        assert np.abs(lg - split.teacher_forced_logits(src, tgt)).max() < 5e-4
+        assert np.array_equal(lg, split.teacher_forced_logits(src, tgt))
         assert np.abs(lg - orc.teacher_forced_logits(src, tgt, kv_f16=True)).max() < 2e-3
         want, gap = orc.translate_batch(src, 998, max_batch=64, kv_f16=True, max_new_tokens=10)
         got = gpu.generate(src, 998, M.GenOptions(max_new_tokens=10, max_batch=64))
         assert got == want, f"min top-2 gap {gap}"
         assert split.generate(src, 998, M.GenOptions(max_new_tokens=10, max_batch=64)) == want
+        opts = M.GenOptions(beam_size=4, max_new_tokens=8, max_batch=8)
+        assert gpu.generate(src[:2], 998, opts) == split.generate(src[:2], 998, opts)
     finally:
         split.close()
 
