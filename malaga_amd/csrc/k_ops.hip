@@ -607,33 +607,50 @@ __global__ __launch_bounds__(256) void k_lsm_topk_partial(const float *logits, i
         if (i != mask_id && mx > -INFINITY) s += expf(r[i] - mx);
     __syncthreads();
     s = block_sum(s, red);
+    // the workgroup's best 8: the 256 sorted lists in LDS, then wave 0 takes the best head
+    // of all lists 8 times (lane l holds the heads of lists 4 l .. 4 l + 3); the order is
+    // total (value, then lower index), so the result is the 8 best whatever the merge order
 #pragma unroll
     for (int j = 0; j < kTopMax; ++j) {
         lv[threadIdx.x * kTopMax + j] = t.v[j];
         li[threadIdx.x * kTopMax + j] = t.i[j];
     }
     __syncthreads();
-    for (int stride = 128; stride > 0; stride >>= 1) {
-        if (int(threadIdx.x) < stride) {
-            const int o = threadIdx.x + stride;
+    if (threadIdx.x >= 64) return;  // wave-uniform; no barrier below
+    const int lane = threadIdx.x;
+    int head[4] = {0, 0, 0, 0};
+    float ov[kTopMax];
+    uint32_t oi[kTopMax];
 #pragma unroll
-            for (int j = 0; j < kTopMax; ++j) top8_insert(t, lv[o * kTopMax + j], li[o * kTopMax + j]);
+    for (int r = 0; r < kTopMax; ++r) {
+        float bv = -INFINITY;
+        uint32_t bx = 0xffffffffu;
 #pragma unroll
-            for (int j = 0; j < kTopMax; ++j) {
-                lv[threadIdx.x * kTopMax + j] = t.v[j];
-                li[threadIdx.x * kTopMax + j] = t.i[j];
+        for (int q = 0; q < 4; ++q) {
+            const int e = (4 * lane + q) * kTopMax + min(head[q], kTopMax - 1);
+            const float v = head[q] < kTopMax ? lv[e] : -INFINITY;
+            const uint32_t i = head[q] < kTopMax ? li[e] : 0xffffffffu;
+            if (better(v, i, bv, bx)) {
+                bv = v;
+                bx = i;
             }
         }
-        __syncthreads();
+        wave_argmax(bv, bx);
+        ov[r] = bv;
+        oi[r] = bx;
+        // the list whose head won moves on (indices are unique; padding entries are -inf)
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+            if (head[q] < kTopMax && li[(4 * lane + q) * kTopMax + head[q]] == bx) ++head[q];
     }
-    if (threadIdx.x == 0) {
+    if (lane == 0) {
         float *o = work + (size_t(row) * P + p) * (2 + 2 * kTopMax);
         o[0] = mx;
         o[1] = s;
 #pragma unroll
         for (int j = 0; j < kTopMax; ++j) {
-            o[2 + j] = t.v[j];
-            o[2 + kTopMax + j] = __uint_as_float(t.i[j]);
+            o[2 + j] = ov[j];
+            o[2 + kTopMax + j] = __uint_as_float(oi[j]);
         }
     }
 }

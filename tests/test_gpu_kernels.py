@@ -352,6 +352,7 @@ def test_logsoftmax_topk(ctx):
     rows, V, k = 6, 256206, 4
     x = rng.normal(0, 1, (rows, V)).astype(np.float32)
     x[2, 100] = x[2, 50] = x[2, 7000] = 9.0  # ties -> lowest index first
+    x[3, 10:60] = 8.5  # 50 equal values inside one workgroup's chunk, over many threads' lists
     xd = dev(x)
     scratch = torch.zeros(ctx.lib.mlg_logsoftmax_topk_scratch(rows, k) // 4 + 1, device="cuda")
     vals = torch.zeros((rows, k), device="cuda")
@@ -367,6 +368,7 @@ def test_logsoftmax_topk(ctx):
         np.testing.assert_array_equal(idx.cpu().numpy(), order)
         np.testing.assert_allclose(vals.cpu().numpy(), np.take_along_axis(xx, order, 1) - lse[:, None], atol=2e-5)
     assert idx.cpu().numpy()[2, :3].tolist() == [50, 100, 7000]
+    assert idx.cpu().numpy()[3].tolist() == [10, 11, 12, 13]
 
 
 def test_attention_rejects_unsupported_head_size(ctx):
