@@ -163,14 +163,14 @@ __device__ __forceinline__ void dg_slice(int kb, int s, int kq, const typename M
 
 // BPW: K blocks per wave (compile time, it sizes the fragment ring); NT: 16-column tiles
 // per workgroup (1 or 2; with 2, each X fragment, once normalized and split, feeds two
-// tiles); TL: W from the tile-major copy a.w.t (q6_K / q4_K); the wave count NW (4 or 8) is
-// blockDim.x / 64.
-template <int T, int BPW, int NT, int PRO, int EPI, bool TL>
-__global__ __launch_bounds__(kDgMaxNW * 64) void k_dgemm(DArgs a) {
+// tiles); TL: W from the tile-major copy a.w.t (q6_K / q4_K); the wave count NW (4, 8, or
+// up to NWL) is blockDim.x / 64.
+template <int T, int BPW, int NT, int PRO, int EPI, bool TL, int NWL = kDgMaxNW>
+__global__ __launch_bounds__(NWL * 64) void k_dgemm(DArgs a) {
     using W = MW<T>;
     constexpr int SK = W::SK, XQ = SK / 16;  // float4s of X per lane and slice
     constexpr int TN = 16 * NT, RS = TN + 1;  // columns of the tile; LDS row stride
-    __shared__ float red[kDgMaxNW * 16 * RS];
+    __shared__ float red[NWL * 16 * RS];
     __shared__ float lnm[16], lnr[16];
     __shared__ float gb[PRO == PRO_LN ? 2 * kDgMaxLnK : 1];  // PRO_LN: gamma | beta
     const int NW = int(blockDim.x) >> 6;
@@ -685,11 +685,31 @@ hipError_t launch_dgemm(const DArgs &a, hipStream_t st) {
     return launch_dgemm_l<T, BPW, PRO, EPI, false>(a, st);
 }
 
+// A residual projection of 9..16 K blocks (ffn_down at FFN width 4096): 16 waves of one
+// block each (1024 threads; the one-block variants fit the 128 VGPRs that allows) rather
+// than 8 waves of two
+constexpr int kDgWaves16 = 16;
+template <int T, int PRO, int EPI>
+hipError_t launch_dgemm16(const DArgs &a, hipStream_t st) {
+    const dim3 grid(unsigned((a.w.N + 15) / 16), unsigned((a.M + 15) / 16)), block(kDgWaves16 * 64);
+    if constexpr (T == GGML_Q6_K || T == GGML_Q4_K) {
+        if (a.w.t) {
+            hipLaunchKernelGGL((k_dgemm<T, 1, 1, PRO, EPI, true, kDgWaves16>), grid, block, 0, st, a);
+            return hipGetLastError();
+        }
+    }
+    hipLaunchKernelGGL((k_dgemm<T, 1, 1, PRO, EPI, false, kDgWaves16>), grid, block, 0, st, a);
+    return hipGetLastError();
+}
+
 // only the residual projections (ffn_down: K = the FFN width) take more than one K
 // block per wave
 template <int T, int PRO, int EPI>
 hipError_t launch_dgemm_m(const DArgs &a, hipStream_t st) {
     const int bpw = dg_bpw(a.w.K / kStep);
+    if constexpr (EPI == EPI_RESID && PRO == PRO_SPLIT) {
+        if (a.w.K / kStep > kDgMaxNW && a.w.K / kStep <= kDgWaves16) return launch_dgemm16<T, PRO, EPI>(a, st);
+    }
     if constexpr (EPI == EPI_RESID) {
         if (bpw == 4) return launch_dgemm<T, 4, PRO, EPI>(a, st);
         if (bpw == 2) return launch_dgemm<T, 2, PRO, EPI>(a, st);
