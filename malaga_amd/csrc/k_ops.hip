@@ -565,21 +565,20 @@ __device__ __forceinline__ void top8_init(Top8 &t) {
     }
 }
 
+// Without branches: c[j] = (v, i) ranks above entry j (c[j] implies c[j + 1], the list
+// being sorted), so entry j becomes entry j - 1 where c[j - 1], (v, i) where c[j] alone,
+// and stays otherwise; nothing changes when (v, i) does not beat the last entry.
 __device__ __forceinline__ void top8_insert(Top8 &t, float v, uint32_t i) {
-    if (!better(v, i, t.v[kTopMax - 1], t.i[kTopMax - 1])) return;
-    t.v[kTopMax - 1] = v;
-    t.i[kTopMax - 1] = i;
+    bool c[kTopMax];
+#pragma unroll
+    for (int j = 0; j < kTopMax; ++j) c[j] = better(v, i, t.v[j], t.i[j]);
 #pragma unroll
     for (int j = kTopMax - 1; j > 0; --j) {
-        if (better(t.v[j], t.i[j], t.v[j - 1], t.i[j - 1])) {
-            const float tv = t.v[j];
-            const uint32_t ti = t.i[j];
-            t.v[j] = t.v[j - 1];
-            t.i[j] = t.i[j - 1];
-            t.v[j - 1] = tv;
-            t.i[j - 1] = ti;
-        }
+        t.v[j] = c[j - 1] ? t.v[j - 1] : (c[j] ? v : t.v[j]);
+        t.i[j] = c[j - 1] ? t.i[j - 1] : (c[j] ? i : t.i[j]);
     }
+    t.v[0] = c[0] ? v : t.v[0];
+    t.i[0] = c[0] ? i : t.i[0];
 }
 
 // Pass 1: per (part, row): chunk max M, sum exp(x - M), chunk top-8.
@@ -607,41 +606,51 @@ __global__ __launch_bounds__(256) void k_lsm_topk_partial(const float *logits, i
         if (i != mask_id && mx > -INFINITY) s += expf(r[i] - mx);
     __syncthreads();
     s = block_sum(s, red);
-    // the workgroup's best 8: the 256 sorted lists in LDS, then wave 0 takes the best head
-    // of all lists 8 times (lane l holds the heads of lists 4 l .. 4 l + 3); the order is
-    // total (value, then lower index), so the result is the 8 best whatever the merge order
+    // the workgroup's best 8: the 256 sorted lists in LDS, entry e of list L at e 256 + L
+    // (consecutive lanes, consecutive banks), then wave 0 takes the best head of all lists
+    // 8 times: lane l keeps the heads of lists l + 64 q in registers and reads a list's next
+    // entry only when its head wins.  The order is total (value, then lower index), so the
+    // result is the 8 best whatever the merge order.
 #pragma unroll
     for (int j = 0; j < kTopMax; ++j) {
-        lv[threadIdx.x * kTopMax + j] = t.v[j];
-        li[threadIdx.x * kTopMax + j] = t.i[j];
+        lv[j * 256 + threadIdx.x] = t.v[j];
+        li[j * 256 + threadIdx.x] = t.i[j];
     }
     __syncthreads();
     if (threadIdx.x >= 64) return;  // wave-uniform; no barrier below
     const int lane = threadIdx.x;
-    int head[4] = {0, 0, 0, 0};
+    int head[4];
+    float hv[4];
+    uint32_t hx[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        head[q] = 0;
+        hv[q] = lv[64 * q + lane];
+        hx[q] = li[64 * q + lane];
+    }
     float ov[kTopMax];
     uint32_t oi[kTopMax];
 #pragma unroll
     for (int r = 0; r < kTopMax; ++r) {
-        float bv = -INFINITY;
-        uint32_t bx = 0xffffffffu;
+        float bv = hv[0];
+        uint32_t bx = hx[0];
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {
-            const int e = (4 * lane + q) * kTopMax + min(head[q], kTopMax - 1);
-            const float v = head[q] < kTopMax ? lv[e] : -INFINITY;
-            const uint32_t i = head[q] < kTopMax ? li[e] : 0xffffffffu;
-            if (better(v, i, bv, bx)) {
-                bv = v;
-                bx = i;
+        for (int q = 1; q < 4; ++q)
+            if (better(hv[q], hx[q], bv, bx)) {
+                bv = hv[q];
+                bx = hx[q];
             }
-        }
         wave_argmax(bv, bx);
         ov[r] = bv;
         oi[r] = bx;
         // the list whose head won moves on (indices are unique; padding entries are -inf)
 #pragma unroll
         for (int q = 0; q < 4; ++q)
-            if (head[q] < kTopMax && li[(4 * lane + q) * kTopMax + head[q]] == bx) ++head[q];
+            if (hx[q] == bx && head[q] < kTopMax) {
+                const int e = ++head[q];
+                hv[q] = e < kTopMax ? lv[e * 256 + 64 * q + lane] : -INFINITY;
+                hx[q] = e < kTopMax ? li[e * 256 + 64 * q + lane] : 0xffffffffu;
+            }
     }
     if (lane == 0) {
         float *o = work + (size_t(row) * P + p) * (2 + 2 * kTopMax);
