@@ -591,20 +591,72 @@ __global__ __launch_bounds__(256) void k_lsm_topk_partial(const float *logits, i
     const int row = blockIdx.y, p = blockIdx.x, P = gridDim.x;
     const int chunk = (V + P - 1) / P, start = p * chunk, end = min(start + chunk, V);
     const float *r = logits + size_t(row) * V;
-    Top8 t;
-    top8_init(t);
-    float mx = -INFINITY;
+    __shared__ float thv;
+    __shared__ uint32_t thx;
+    // pass 1: the thread's own best (value, index) and the chunk's max
+    float bv = -INFINITY;
+    uint32_t bx = 0xffffffffu;
     for (int i = start + threadIdx.x; i < end; i += blockDim.x) {
         if (i == mask_id) continue;
         const float v = r[i];
-        mx = fmaxf(mx, v);
-        top8_insert(t, v, uint32_t(i));
+        if (better(v, uint32_t(i), bv, bx)) {
+            bv = v;
+            bx = uint32_t(i);
+        }
     }
-    mx = block_max(mx, red);
-    float s = 0.f;
-    for (int i = start + threadIdx.x; i < end; i += blockDim.x)
-        if (i != mask_id && mx > -INFINITY) s += expf(r[i] - mx);
+    lv[threadIdx.x] = bv;
+    li[threadIdx.x] = bx;
+    const float mx = block_max(bv, red);  // its barrier also orders lv / li
+    // the chunk's 8 best are all at least as good as the 8th best of the 256 threads' bests
+    // (8 distinct elements): wave 0 finds that threshold ((-inf, ~0) below 8 elements)
+    if (threadIdx.x < 64) {  // wave-uniform
+        const int lane = threadIdx.x;
+        float hv[4];
+        uint32_t hx[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            hv[q] = lv[64 * q + lane];
+            hx[q] = li[64 * q + lane];
+        }
+        float wv = -INFINITY;
+        uint32_t wx = 0xffffffffu;
+#pragma unroll
+        for (int rr = 0; rr < kTopMax; ++rr) {
+            wv = hv[0];
+            wx = hx[0];
+#pragma unroll
+            for (int q = 1; q < 4; ++q)
+                if (better(hv[q], hx[q], wv, wx)) {
+                    wv = hv[q];
+                    wx = hx[q];
+                }
+            wave_argmax(wv, wx);
+#pragma unroll
+            for (int q = 0; q < 4; ++q)
+                if (hx[q] == wx) {
+                    hv[q] = -INFINITY;
+                    hx[q] = 0xffffffffu;
+                }
+        }
+        if (lane == 0) {
+            thv = wv;
+            thx = wx;
+        }
+    }
     __syncthreads();
+    const float tv = thv;
+    const uint32_t tx = thx;
+    // pass 2: sum exp(x - max), and a sorted top-8 of the thread's elements that reach the
+    // threshold (a handful per workgroup)
+    Top8 t;
+    top8_init(t);
+    float s = 0.f;
+    for (int i = start + threadIdx.x; i < end; i += blockDim.x) {
+        if (i == mask_id) continue;
+        const float v = r[i];
+        if (mx > -INFINITY) s += expf(v - mx);
+        if (!better(tv, tx, v, uint32_t(i))) top8_insert(t, v, uint32_t(i));
+    }
     s = block_sum(s, red);
     // the workgroup's best 8: the 256 sorted lists in LDS, entry e of list L at e 256 + L
     // (consecutive lanes, consecutive banks), then wave 0 takes the best head of all lists
