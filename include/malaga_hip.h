@@ -73,7 +73,11 @@ typedef struct {
     float length_penalty;
     int sync_every;
     int max_batch;
-    int fused;            /* 1 = static step replayed as a hipGraph; 0 = same step, eager */
+    int fused;            /* GenOptions::fused (src/translator.rs:184-201).  1: greedy runs the graph
+                             cache's static step (f16 K/V, replayed as a hipGraph).  0: greedy runs the
+                             generic decoder (Nllb::decode semantics: f32 K/V caches and cross K/V,
+                             eager launches).  Beam search always runs the generic decoder (f32 K/V);
+                             fused = 1 replays its captured step, 0 launches it eagerly. */
     uint32_t flags;       /* MLG_FLAG_* */
     const char *shortlist; /* GenOptions::shortlist (--fast-vocab): the target-language code whose
                               shortlist greedy decoding uses when the model has one that holds
@@ -144,14 +148,20 @@ void mlg_batch_free(mlg_batch *b);
 /* GraphCache::greedy (src/graph.rs:204-223); rows stripped at EOS. */
 int mlg_greedy(mlg_model *m, const mlg_batch *b, uint32_t tgt_lang, int max_new, int sync_every, uint32_t flags,
                uint32_t *out, int out_cap, int *out_len);
+/* mlg_greedy, plus top [n][out_cap]: the logit of each returned token as the step's
+   argmax saw it (the LM head's winning value, before the finished / pad rule).  Parity
+   hook for tests of the fused argmax head; no counterpart in the reference. */
+int mlg_greedy_top(mlg_model *m, const mlg_batch *b, uint32_t tgt_lang, int max_new, int sync_every, uint32_t flags,
+                   uint32_t *out, float *top, int out_cap, int *out_len);
 /* GraphCache::greedy with Some(shortlist) (src/graph.rs:204-298, src/model.rs:597-606): the
    candidates of each step are the shortlist rows of language `code` and the batch's source
    tokens.  MLG_ERR_INVALID if the model has no such shortlist or it lacks decoder_start or
    tgt_lang ("token missing from the shortlist", src/graph.rs:125). */
 int mlg_greedy_sl(mlg_model *m, const mlg_batch *b, uint32_t tgt_lang, const char *code, int max_new, int sync_every,
                   uint32_t flags, uint32_t *out, int out_cap, int *out_len);
-/* Translator::beam_search (src/translator.rs:250-335).  One decoder step + top-k is captured
-   once and replayed per step (MLG_FLAG_NO_GRAPH: eager); MLG_FLAG_EOS_MASK as for mlg_greedy. */
+/* Translator::beam_search (src/translator.rs:250-335) on the generic decoder's f32 K/V caches
+   (src/model.rs:195-227).  One decoder step + top-k is captured once and replayed per step
+   (MLG_FLAG_NO_GRAPH: eager); MLG_FLAG_EOS_MASK as for mlg_greedy. */
 int mlg_beam(mlg_model *m, const mlg_batch *b, uint32_t tgt_lang, int max_new, int beam_size, float length_penalty,
              uint32_t flags, uint32_t *out, int out_cap, int *out_len);
 /* The host half of Translator::beam_search (src/translator.rs:250-335: candidate merge,
@@ -269,9 +279,11 @@ int mlg_logsoftmax_topk(const float *logits, int rows, int V, int k, int mask_id
 int mlg_logsoftmax_topk_noalloc(const float *logits, int rows, int V, int k, int mask_id, float *vals, uint32_t *idx,
                                 void *stream);
 /* Logits after feeding tgt[i][t] at decoder position t (t < T), eagerly: out is [n][T][vocab].
- * Parity hook for Nllb::decode (src/model.rs:514-540); no counterpart in the reference. */
+ * kv_f32 = 0: K/V caches in f16, as the graph step stores them (kernels/malaga.cu:142-154);
+ * kv_f32 = 1: in f32, as Nllb::decode keeps them (src/model.rs:195-227, 514-540).
+ * Parity hook; no counterpart in the reference. */
 int mlg_teacher_forced_logits(mlg_model *m, const uint32_t *ids, const uint32_t *lens, int n, const uint32_t *tgt, int T,
-                              float *logits);
+                              int kv_f32, float *logits);
 /* src/graph.rs:138-140 */
 int mlg_bucket(int n, int min, int max);
 /* per-sentence output budget, src/translator.rs:181-182 */

@@ -89,10 +89,13 @@ class EncodedBatch:
     def __init__(self, lib, h, n: int):
         self.lib, self.h, self.n = lib, h, n
 
-    def __del__(self):
+    def close(self):
         if getattr(self, "h", None):
             self.lib.mlg_batch_free(self.h)
             self.h = None
+
+    def __del__(self):
+        self.close()
 
 
 class Translator:
@@ -211,6 +214,18 @@ class Translator:
                                       max_new + 1, out_len.ctypes.data))
         return _rows(out, out_len)
 
+    def greedy_top(self, batch: EncodedBatch, tgt_lang: int, max_new: int, sync_every: int = 4,
+                   eos_mask: bool = False, graph: bool = True) -> tuple[list[list[int]], list[list[float]]]:
+        """greedy, plus the winning logit of every returned token (parity hook of the
+        fused argmax head)."""
+        out = np.zeros((batch.n, max_new + 1), dtype=np.uint32)
+        top = np.zeros((batch.n, max_new + 1), dtype=np.float32)
+        out_len = np.zeros(batch.n, dtype=np.int32)
+        flags = (FLAG_EOS_MASK if eos_mask else 0) | (0 if graph else FLAG_NO_GRAPH)
+        check(self.lib.mlg_greedy_top(self.h, batch.h, tgt_lang, max_new, sync_every, flags, out.ctypes.data,
+                                      top.ctypes.data, max_new + 1, out_len.ctypes.data))
+        return _rows(out, out_len), [top[i, : out_len[i]].tolist() for i in range(batch.n)]
+
     def shortlists(self) -> dict[str, int]:
         """Languages with a vocabulary shortlist and their row counts (src/model.rs:439-447)."""
         res = {}
@@ -229,14 +244,15 @@ class Translator:
                                 FLAG_EOS_MASK if eos_mask else 0, out.ctypes.data, max_new + 1, out_len.ctypes.data))
         return _rows(out, out_len)
 
-    def teacher_forced_logits(self, src: Sequence[Sequence[int]], tgt: np.ndarray) -> np.ndarray:
-        """Logits [n, T, vocab] after feeding tgt[:, t] at decoder position t."""
+    def teacher_forced_logits(self, src: Sequence[Sequence[int]], tgt: np.ndarray, kv_f32: bool = False) -> np.ndarray:
+        """Logits [n, T, vocab] after feeding tgt[:, t] at decoder position t; K/V in f16 (the
+        graph step) or, with kv_f32, in f32 (the generic decoder, src/model.rs:514-540)."""
         ids, lens = _flat(src)
         tgt = np.ascontiguousarray(tgt, dtype=np.uint32)
         n, T = tgt.shape
         out = np.zeros((n, T, self.cfg["vocab_size"]), dtype=np.float32)
         check(self.lib.mlg_teacher_forced_logits(self.h, ids.ctypes.data, lens.ctypes.data, n, tgt.ctypes.data, T,
-                                                 out.ctypes.data))
+                                                 int(kv_f32), out.ctypes.data))
         return out
 
     def clear_graphs(self):

@@ -90,6 +90,7 @@ SIGNATURES = {
     "mlg_encode": (C.c_int, [_P, _P, _P, C.c_int, C.POINTER(_P)]),
     "mlg_batch_free": (None, [_P]),
     "mlg_greedy": (C.c_int, [_P, _P, C.c_uint32, C.c_int, C.c_int, C.c_uint32, _P, C.c_int, _P]),
+    "mlg_greedy_top": (C.c_int, [_P, _P, C.c_uint32, C.c_int, C.c_int, C.c_uint32, _P, _P, C.c_int, _P]),
     "mlg_greedy_sl": (C.c_int, [_P, _P, C.c_uint32, C.c_char_p, C.c_int, C.c_int, C.c_uint32, _P, C.c_int, _P]),
     "mlg_beam": (C.c_int, [_P, _P, C.c_uint32, C.c_int, C.c_int, C.c_float, C.c_uint32, _P, C.c_int, _P]),
     "mlg_beam_search_host": (C.c_int, [C.c_int, C.c_int, C.c_int, C.c_float, C.c_uint32, BEAM_DECODE_FN, _P, _P,
@@ -129,7 +130,7 @@ SIGNATURES = {
     "mlg_logsoftmax_topk_scratch": (C.c_size_t, [C.c_int, C.c_int]),
     "mlg_logsoftmax_topk": (C.c_int, [_P, C.c_int, C.c_int, C.c_int, C.c_int, _P, _P, _P, _P]),
     "mlg_logsoftmax_topk_noalloc": (C.c_int, [_P, C.c_int, C.c_int, C.c_int, C.c_int, _P, _P, _P]),
-    "mlg_teacher_forced_logits": (C.c_int, [_P, _P, _P, C.c_int, _P, C.c_int, _P]),
+    "mlg_teacher_forced_logits": (C.c_int, [_P, _P, _P, C.c_int, _P, C.c_int, C.c_int, _P]),
     "mlg_bucket": (C.c_int, [C.c_int, C.c_int, C.c_int]),
     "mlg_budget": (C.c_int, [_P, C.c_int, C.c_int]),
     "mlg_synchronize": (C.c_int, []),

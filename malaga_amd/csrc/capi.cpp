@@ -386,6 +386,23 @@ int mlg_greedy(mlg_model *m, const mlg_batch *b, uint32_t tgt_lang, int max_new,
     });
 }
 
+int mlg_greedy_top(mlg_model *m, const mlg_batch *b, uint32_t tgt_lang, int max_new, int sync_every, uint32_t flags,
+                   uint32_t *out, float *top, int out_cap, int *out_len) {
+    return guarded([&]() -> int {
+        if (!m || !b || max_new < 1 || !out || !top || !out_len) return set_err(MLG_ERR_INVALID, "bad argument");
+        std::lock_guard<std::mutex> lk(m->m->ctx->mu);
+        mlg::check_hip(hipSetDevice(m->m->ctx->device), "hipSetDevice");
+        std::vector<std::vector<float>> tv;
+        auto rows = m->m->graphs.greedy(*b->b, tgt_lang, max_new, sync_every > 0 ? sync_every : 1,
+                                        (flags & MLG_FLAG_EOS_MASK) != 0, !(flags & MLG_FLAG_NO_GRAPH), nullptr, &tv);
+        const int st = write_rows(rows, out, out_cap, out_len);
+        if (st == MLG_OK)
+            for (size_t r = 0; r < tv.size(); ++r)
+                std::copy(tv[r].begin(), tv[r].end(), top + r * size_t(out_cap));
+        return st;
+    });
+}
+
 int mlg_greedy_sl(mlg_model *m, const mlg_batch *b, uint32_t tgt_lang, const char *code, int max_new, int sync_every,
                   uint32_t flags, uint32_t *out, int out_cap, int *out_len) {
     return guarded([&]() -> int {
@@ -683,14 +700,14 @@ int mlg_logsoftmax_topk_noalloc(const float *logits, int rows, int V, int k, int
 }
 
 int mlg_teacher_forced_logits(mlg_model *m, const uint32_t *ids, const uint32_t *lens, int n, const uint32_t *tgt, int T,
-                              float *logits) {
+                              int kv_f32, float *logits) {
     return guarded([&]() -> int {
         if (!m || !ids || !lens || n <= 0 || !tgt || T < 1 || !logits) return set_err(MLG_ERR_INVALID, "bad argument");
         std::lock_guard<std::mutex> lk(m->m->ctx->mu);
         mlg::check_hip(hipSetDevice(m->m->ctx->device), "hipSetDevice");
         auto batch = m->m->encode(rows_of(ids, lens, n));
         std::vector<uint32_t> t(tgt, tgt + size_t(n) * T);
-        auto out = m->m->teacher_forced(*batch, t, T);
+        auto out = m->m->teacher_forced(*batch, t, T, kv_f32 != 0);
         std::memcpy(logits, out.data(), out.size() * sizeof(float));
         return MLG_OK;
     });

@@ -51,6 +51,7 @@ struct DArgs {
     double *stats_out;  // EPI_RESID: [M][N / 16][2]
     float *q;           // EPI_QKV: q [M][d], caches [M][H][slots][hd]
     __half *kc, *vc;
+    float *kc32, *vc32;  // EPI_QKV with f32 caches (the generic path; kc / vc unused)
     int H, hd, slots;
     const uint32_t *step;
     const uint32_t *lens;  // k_dxattn: the rows' key counts (kc / vc: the cross caches [M][H][slots][hd])
@@ -339,11 +340,13 @@ __global__ __launch_bounds__(NWL * 64) void k_dgemm(DArgs a) {
 #pragma unroll
             for (int j = 0; j < 8; ++j) hv[j] = _Float16(__shfl(v, j, 8));
             if (own) {
+                const int cc = on < 2 * d ? on - d : on - 2 * d;
+                const size_t off = ((size_t(om) * a.H + cc / a.hd) * a.slots + slot) * a.hd + cc % a.hd;
                 if (on < d) {
                     a.q[size_t(om) * d + on] = v;
+                } else if (a.kc32) {  // kernel argument: the same branch in every lane
+                    (on < 2 * d ? a.kc32 : a.vc32)[off] = v;
                 } else if ((c & 7) == 0) {
-                    const int cc = on < 2 * d ? on - d : on - 2 * d;
-                    const size_t off = ((size_t(om) * a.H + cc / a.hd) * a.slots + slot) * a.hd + cc % a.hd;
                     *reinterpret_cast<h8_t *>((on < 2 * d ? a.kc : a.vc) + off) = hv;
                 }
             }
@@ -784,20 +787,36 @@ hipError_t dgemm_resid(const DevMatrix &w, const float *x, int ldx, int M, const
     return launch_dgemm_t<PRO_RAW, EPI_RESID>(w, a, st);
 }
 
-hipError_t dgemm_qkv(const DevMatrix &w, const float *x, int ldx, int M, const DgemmLn *ln, const float *bias, int H,
-                     int hd, int slots, const uint32_t *step, float *q, __half *kc, __half *vc, hipStream_t st) {
-    if (!dgemm_args_ok(w, x, ldx, M, ln) || w.N != 3 * H * hd || hd % 8 || !q || !kc || !vc || !step ||
-        reinterpret_cast<uintptr_t>(kc) % 16 || reinterpret_cast<uintptr_t>(vc) % 16)
+namespace {
+hipError_t dgemm_qkv_any(const DevMatrix &w, const float *x, int ldx, int M, const DgemmLn *ln, const float *bias,
+                         int H, int hd, int slots, const uint32_t *step, float *q, __half *kc, __half *vc, float *kc32,
+                         float *vc32, hipStream_t st) {
+    const void *k = kc ? static_cast<const void *>(kc) : kc32, *v = vc ? static_cast<const void *>(vc) : vc32;
+    if (!dgemm_args_ok(w, x, ldx, M, ln) || w.N != 3 * H * hd || hd % 8 || !q || !k || !v || !step ||
+        reinterpret_cast<uintptr_t>(k) % 16 || reinterpret_cast<uintptr_t>(v) % 16)
         return hipErrorInvalidValue;
     DArgs a = dargs(w, x, ldx, M, ln, bias);
     a.q = q;
     a.kc = kc;
     a.vc = vc;
+    a.kc32 = kc32;
+    a.vc32 = vc32;
     a.H = H;
     a.hd = hd;
     a.slots = slots;
     a.step = step;
     return ln ? launch_dgemm_t<PRO_LN, EPI_QKV>(w, a, st) : launch_dgemm_t<PRO_RAW, EPI_QKV>(w, a, st);
+}
+}  // namespace
+
+hipError_t dgemm_qkv(const DevMatrix &w, const float *x, int ldx, int M, const DgemmLn *ln, const float *bias, int H,
+                     int hd, int slots, const uint32_t *step, float *q, __half *kc, __half *vc, hipStream_t st) {
+    return dgemm_qkv_any(w, x, ldx, M, ln, bias, H, hd, slots, step, q, kc, vc, nullptr, nullptr, st);
+}
+
+hipError_t dgemm_qkv(const DevMatrix &w, const float *x, int ldx, int M, const DgemmLn *ln, const float *bias, int H,
+                     int hd, int slots, const uint32_t *step, float *q, float *kc, float *vc, hipStream_t st) {
+    return dgemm_qkv_any(w, x, ldx, M, ln, bias, H, hd, slots, step, q, nullptr, nullptr, kc, vc, st);
 }
 
 bool dgemm_cross_attn_supported(const DevMatrix &w, int M, int H, int hd) {

@@ -440,10 +440,15 @@ __global__ __launch_bounds__(256) void k_splitk_residual_ln(const float *part, i
 }
 
 // Split-K reduction of the fused QKV projection written straight into q [M][d] and
-// the f16 caches at slot *step (kernels/malaga.cu:142-154).
+// the caches at slot *step (kernels/malaga.cu:142-154): f16 (rounded to nearest even) or
+// f32 (the generic path's caches).
+__device__ __forceinline__ void store_kv(__half *p, float v) { *p = __float2half(v); }
+__device__ __forceinline__ void store_kv(float *p, float v) { *p = v; }
+
+template <typename KT>
 __global__ __launch_bounds__(256) void k_splitk_qkv(const float *part, int ks, int M, int d, const float *bias, int H,
-                                                     int hd, int slots, const uint32_t *step, float *q, __half *kc,
-                                                     __half *vc) {
+                                                     int hd, int slots, const uint32_t *step, float *q, KT *kc,
+                                                     KT *vc) {
     const size_t i = size_t(blockIdx.x) * 256 + threadIdx.x, N = size_t(3) * d, mn = size_t(M) * N;
     if (i >= mn) return;
     const int m = int(i / N), c = int(i % N);
@@ -462,7 +467,7 @@ __global__ __launch_bounds__(256) void k_splitk_qkv(const float *part, int ks, i
     } else {
         const int cc = c < 2 * d ? c - d : c - 2 * d;
         const size_t o = ((size_t(m) * H + cc / hd) * slots + *step) * hd + cc % hd;
-        (c < 2 * d ? kc : vc)[o] = __float2half(v);
+        store_kv((c < 2 * d ? kc : vc) + o, v);
     }
 }
 
@@ -940,9 +945,11 @@ hipError_t gemm_residual_ln(const DevMatrix &w, const float *X, int ldx, int M, 
     return layernorm(x, M, w.N, g, b, eps, h, st);
 }
 
-hipError_t gemm_qkv(const DevMatrix &w, const float *X, int ldx, int M, const float *bias, int H, int hd, int slots,
-                    const uint32_t *step, float *q, __half *kc, __half *vc, float *qkv_tmp, hipStream_t st, float *ws,
-                    size_t ws_bytes) {
+namespace {
+template <typename KT>
+hipError_t gemm_qkv_t(const DevMatrix &w, const float *X, int ldx, int M, const float *bias, int H, int hd, int slots,
+                      const uint32_t *step, float *q, KT *kc, KT *vc, float *qkv_tmp, hipStream_t st, float *ws,
+                      size_t ws_bytes) {
     if (M <= 0) return hipSuccess;
     const int d = H * hd;
     if (w.N != 3 * d) return hipErrorInvalidValue;
@@ -951,13 +958,26 @@ hipError_t gemm_qkv(const DevMatrix &w, const float *X, int ldx, int M, const fl
     if (e != hipSuccess) return e;
     if (ks > 1) {
         const size_t n = size_t(M) * w.N;
-        hipLaunchKernelGGL(k_splitk_qkv, dim3(unsigned((n + 255) / 256)), dim3(256), 0, st, ws, ks, M, d, bias, H, hd,
-                           slots, step, q, kc, vc);
+        hipLaunchKernelGGL(k_splitk_qkv<KT>, dim3(unsigned((n + 255) / 256)), dim3(256), 0, st, ws, ks, M, d, bias, H,
+                           hd, slots, step, q, kc, vc);
         return hipGetLastError();
     }
     e = gemm(w, X, ldx, M, qkv_tmp, w.N, bias, false, nullptr, 0, st, ws, ws_bytes);
     if (e != hipSuccess) return e;
     return qkv_split(qkv_tmp, M, H, hd, slots, step, q, kc, vc, st);
+}
+}  // namespace
+
+hipError_t gemm_qkv(const DevMatrix &w, const float *X, int ldx, int M, const float *bias, int H, int hd, int slots,
+                    const uint32_t *step, float *q, __half *kc, __half *vc, float *qkv_tmp, hipStream_t st, float *ws,
+                    size_t ws_bytes) {
+    return gemm_qkv_t(w, X, ldx, M, bias, H, hd, slots, step, q, kc, vc, qkv_tmp, st, ws, ws_bytes);
+}
+
+hipError_t gemm_qkv(const DevMatrix &w, const float *X, int ldx, int M, const float *bias, int H, int hd, int slots,
+                    const uint32_t *step, float *q, float *kc, float *vc, float *qkv_tmp, hipStream_t st, float *ws,
+                    size_t ws_bytes) {
+    return gemm_qkv_t(w, X, ldx, M, bias, H, hd, slots, step, q, kc, vc, qkv_tmp, st, ws, ws_bytes);
 }
 
 }  // namespace mlg

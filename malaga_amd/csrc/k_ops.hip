@@ -161,11 +161,28 @@ __global__ __launch_bounds__(256) void k_source_logits(const float *h, const flo
     }
 }
 
+// Eight cache values from f32: f16 caches round to nearest even (one 16-byte store), f32
+// caches keep the values (two 16-byte stores).
+__device__ __forceinline__ void store_kv8(__half *dst, const float *p) {
+    const float4 a = ld4(p, 0), z = ld4(p, 1);
+    uint4 o;
+    o.x = uint32_t(__half_as_ushort(__float2half(a.x))) | uint32_t(__half_as_ushort(__float2half(a.y))) << 16;
+    o.y = uint32_t(__half_as_ushort(__float2half(a.z))) | uint32_t(__half_as_ushort(__float2half(a.w))) << 16;
+    o.z = uint32_t(__half_as_ushort(__float2half(z.x))) | uint32_t(__half_as_ushort(__float2half(z.y))) << 16;
+    o.w = uint32_t(__half_as_ushort(__float2half(z.z))) | uint32_t(__half_as_ushort(__float2half(z.w))) << 16;
+    *reinterpret_cast<uint4 *>(dst) = o;
+}
+__device__ __forceinline__ void store_kv8(float *dst, const float *p) {
+    reinterpret_cast<float4 *>(dst)[0] = ld4(p, 0);
+    reinterpret_cast<float4 *>(dst)[1] = ld4(p, 1);
+}
+
 // The fused projection's rows [b][3d] (bias included) split into q (f32 [b][d]) and
-// the f16 K/V caches at slot *step ([b][H][m][hd]): one thread per 8 consecutive values
-// of the row's d columns, two 16-byte loads per part, one 16-byte store per f16 part.
+// the K/V caches at slot *step ([b][H][m][hd], f16 or f32): one thread per 8 consecutive
+// values of the row's d columns, two 16-byte loads per part.
+template <typename KT>
 __global__ __launch_bounds__(256) void k_split_qkv8(const float *qkv, int b, int H, int hd, int m,
-                                                    const uint32_t *step, float *q, __half *kc, __half *vc) {
+                                                    const uint32_t *step, float *q, KT *kc, KT *vc) {
     const int d = H * hd, per_row = d / 8;
     const int t = blockIdx.x * 256 + threadIdx.x;
     if (t >= b * per_row) return;
@@ -175,17 +192,8 @@ __global__ __launch_bounds__(256) void k_split_qkv8(const float *qkv, int b, int
     qd[0] = ld4(r, 0);
     qd[1] = ld4(r, 1);
     const size_t slot = ((size_t(bi) * H + hh) * m + *step) * hd + e;
-    auto f16x8 = [](const float *p) {
-        const float4 a = ld4(p, 0), z = ld4(p, 1);
-        uint4 o;
-        o.x = uint32_t(__half_as_ushort(__float2half(a.x))) | uint32_t(__half_as_ushort(__float2half(a.y))) << 16;
-        o.y = uint32_t(__half_as_ushort(__float2half(a.z))) | uint32_t(__half_as_ushort(__float2half(a.w))) << 16;
-        o.z = uint32_t(__half_as_ushort(__float2half(z.x))) | uint32_t(__half_as_ushort(__float2half(z.y))) << 16;
-        o.w = uint32_t(__half_as_ushort(__float2half(z.z))) | uint32_t(__half_as_ushort(__float2half(z.w))) << 16;
-        return o;
-    };
-    *reinterpret_cast<uint4 *>(kc + slot) = f16x8(r + d);
-    *reinterpret_cast<uint4 *>(vc + slot) = f16x8(r + 2 * d);
+    store_kv8(kc + slot, r + d);
+    store_kv8(vc + slot, r + 2 * d);
 }
 
 // Encoder attention: one wave per (sentence i, query t, head h).
@@ -226,7 +234,7 @@ __global__ __launch_bounds__(64) void k_attn_prefill(const float *qkv, int s, in
     }
 }
 
-__global__ void k_split_cross_kv(const float *kv, int b, int s, int H, int hd, int L, __half *K0, size_t kv_elems) {
+__global__ void k_split_cross_kv(const float *kv, int b, int s, int H, int hd, int L, float *K0, size_t kv_elems) {
     const int d = H * hd;
     const size_t total = size_t(b) * s * L * d;
     for (size_t idx = blockIdx.x * size_t(blockDim.x) + threadIdx.x; idx < total; idx += size_t(gridDim.x) * blockDim.x) {
@@ -235,19 +243,21 @@ __global__ void k_split_cross_kv(const float *kv, int b, int s, int H, int hd, i
         const int l = int(rest % L);
         const int j = int(tok % s), i = int(tok / s), hh = c / hd, e = c % hd;
         const size_t dst = ((size_t(i) * H + hh) * s + j) * hd + e;
-        __half *K = K0 + 2 * size_t(l) * kv_elems;
+        float *K = K0 + 2 * size_t(l) * kv_elems;
         const float *src = kv + (tok * L + l) * 2 * d;
-        K[dst] = __float2half(src[c]);
-        K[kv_elems + dst] = __float2half(src[d + c]);
+        K[dst] = src[c];
+        K[kv_elems + dst] = src[d + c];
     }
 }
 
 // dst row r (< n_dst) <- src row map[r] (or r when map is null)
-// Every layer's cross K and V in one launch, 16 bytes per thread: pair p of the source
-// [b][H][s][hd] at src0 + p * src_pair -> pair p of the state [n][H][S][hd] at
-// dst0 + p * dst_pair; state row r takes source row map[r] (or r).
-__global__ void k_copy_cross(const __half *src0, size_t src_pair, const uint32_t *map, int n_dst, int H, int s, int hd,
-                             __half *dst0, size_t dst_pair, int S, int pairs) {
+// Every layer's cross K and V in one launch, 8 values per thread: pair p of the source
+// [b][H][s][hd] (f32, as the encoder computed them) at src0 + p * src_pair -> pair p of the
+// state [n][H][S][hd] (f16 for the graph step, src/graph.rs:94-97; f32 for the generic
+// path) at dst0 + p * dst_pair; state row r takes source row map[r] (or r).
+template <typename KT>
+__global__ void k_copy_cross(const float *src0, size_t src_pair, const uint32_t *map, int n_dst, int H, int s, int hd,
+                             KT *dst0, size_t dst_pair, int S, int pairs) {
     const int hv = hd / 8;
     const size_t per_row = size_t(H) * s * hv, per_pair = size_t(n_dst) * per_row, total = per_pair * pairs;
     for (size_t idx = blockIdx.x * size_t(blockDim.x) + threadIdx.x; idx < total; idx += size_t(gridDim.x) * blockDim.x) {
@@ -257,9 +267,9 @@ __global__ void k_copy_cross(const __half *src0, size_t src_pair, const uint32_t
         const size_t hj = rem / hv;
         const int j = int(hj % s), hh = int(hj / s);
         const size_t sr = map ? map[r] : r;
-        const uint4 *sp = reinterpret_cast<const uint4 *>(src0 + p * src_pair) + sr * per_row + rem;
-        uint4 *dp = reinterpret_cast<uint4 *>(dst0 + p * dst_pair) + ((r * H + hh) * S + j) * hv + ev;
-        *dp = *sp;
+        const float *sp = src0 + p * src_pair + (sr * per_row + rem) * 8;
+        KT *dp = dst0 + p * dst_pair + (((r * H + hh) * S + j) * hv + ev) * 8;
+        store_kv8(dp, sp);
     }
 }
 
@@ -306,7 +316,7 @@ __device__ __forceinline__ uint32_t sl_token(const SlFinalize &sl, int row, uint
 __global__ __launch_bounds__(256) void k_greedy_finalize_wg(const float *pv, const uint32_t *pi, int P, int b,
                                                             uint8_t *finished, uint32_t *ids, uint32_t *out, int m,
                                                             uint32_t *step, uint32_t eos, uint32_t pad,
-                                                            SlFinalize sl) {
+                                                            SlFinalize sl, float *outv) {
     __shared__ float sv[4];
     __shared__ uint32_t si[4];
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
@@ -344,6 +354,7 @@ __global__ __launch_bounds__(256) void k_greedy_finalize_wg(const float *pv, con
             if (tok == eos) finished[row] = 1;
             ids[row] = tok;
             out[size_t(row) * m + s] = tok;
+            if (outv) outv[size_t(row) * m + s] = best;  // the winning logit (parity hook)
         }
         __syncthreads();
     }
@@ -354,7 +365,8 @@ __global__ __launch_bounds__(256) void k_greedy_finalize_wg(const float *pv, con
 // lane in flight; the step counter is advanced after every wave has read it.
 __global__ __launch_bounds__(1024) void k_greedy_finalize(const float *pv, const uint32_t *pi, int P, int b,
                                                           uint8_t *finished, uint32_t *ids, uint32_t *out, int m,
-                                                          uint32_t *step, uint32_t eos, uint32_t pad, SlFinalize sl) {
+                                                          uint32_t *step, uint32_t eos, uint32_t pad, SlFinalize sl,
+                                                          float *outv) {
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, nw = blockDim.x >> 6;
     const uint32_t s = *step;
     for (int row = w; row < b; row += nw) {  // wave-uniform
@@ -382,6 +394,7 @@ __global__ __launch_bounds__(1024) void k_greedy_finalize(const float *pv, const
             if (tok == eos) finished[row] = 1;
             ids[row] = tok;
             out[size_t(row) * m + s] = tok;
+            if (outv) outv[size_t(row) * m + s] = best;
         }
     }
     __syncthreads();
@@ -395,8 +408,40 @@ __global__ __launch_bounds__(1024) void k_greedy_finalize(const float *pv, const
 // through its LDS scratch at the end.  S = 1: no workgroup barrier; S > 1: the S partials
 // (sum p_j v_j unnormalized, max, sum p_j) meet in LDS and the pair's first wave rescales
 // them to their common max.
-template <int HD, int S>
-__global__ __launch_bounds__(256) void k_attn_waves(const float *q, const __half *K, const __half *V, int b, int H,
+// Eight consecutive values of a K or V cache row: f16 (one 16-byte load) or f32 (two).
+// unpack yields them as f32, zeros where keep is false (a masked key's value must not
+// reach the sum even as 0 * NaN).
+template <typename KT>
+struct Kv8;
+template <>
+struct Kv8<__half> {
+    uint4 w;
+    __device__ __forceinline__ void load(const __half *p) { w = *reinterpret_cast<const uint4 *>(p); }
+    __device__ __forceinline__ void unpack(float (&o)[8], bool keep = true) const {
+        const uint32_t a[4] = {keep ? w.x : 0u, keep ? w.y : 0u, keep ? w.z : 0u, keep ? w.w : 0u};
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            o[2 * j] = h2f(a[j]);
+            o[2 * j + 1] = h2f(a[j] >> 16);
+        }
+    }
+};
+template <>
+struct Kv8<float> {
+    float4 a, b;
+    __device__ __forceinline__ void load(const float *p) {
+        a = ld4(p, 0);
+        b = ld4(p, 1);
+    }
+    __device__ __forceinline__ void unpack(float (&o)[8], bool keep = true) const {
+        const float v[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+#pragma unroll
+        for (int j = 0; j < 8; ++j) o[j] = keep ? v[j] : 0.f;
+    }
+};
+
+template <int HD, int S, typename KT>
+__global__ __launch_bounds__(256) void k_attn_waves(const float *q, const KT *K, const KT *V, int b, int H,
                                                     int L, const uint32_t *lens, const uint32_t *step, float *out,
                                                     const uint32_t *rows, int out_split) {
     constexpr int TPK = HD / 8, SPL = 64 / TPK, U = 8 / S, SLOT = HD + 2;
@@ -415,7 +460,7 @@ __global__ __launch_bounds__(256) void k_attn_waves(const float *q, const __half
     // then the key count.  The addresses do not depend on the count (keys past it are
     // masked when used), so the chunk is not held back by that scalar read; the loads
     // complete in order.
-    uint4 kr[U], vr[U];
+    Kv8<KT> kr[U], vr[U];
     auto load_chunk = [&](int c) {
         size_t r[U];
         if (rows) {  // kernel argument: wave-uniform
@@ -428,8 +473,8 @@ __global__ __launch_bounds__(256) void k_attn_waves(const float *q, const __half
 #pragma unroll
         for (int u = 0; u < U; ++u) {
             const size_t o = ((r[u] * H + hh) * L + min(key(c, u), L - 1)) * HD + sub * 8;
-            kr[u] = *reinterpret_cast<const uint4 *>(K + o);
-            vr[u] = *reinterpret_cast<const uint4 *>(V + o);
+            kr[u].load(K + o);
+            vr[u].load(V + o);
         }
     };
     load_chunk(0);
@@ -445,14 +490,16 @@ __global__ __launch_bounds__(256) void k_attn_waves(const float *q, const __half
         float cmax = -INFINITY;
 #pragma unroll
         for (int u = 0; u < U; ++u) {
-            float sdot = h2f(kr[u].x) * qa.x;
-            sdot = fmaf(h2f(kr[u].x >> 16), qa.y, sdot);
-            sdot = fmaf(h2f(kr[u].y), qa.z, sdot);
-            sdot = fmaf(h2f(kr[u].y >> 16), qa.w, sdot);
-            sdot = fmaf(h2f(kr[u].z), qb.x, sdot);
-            sdot = fmaf(h2f(kr[u].z >> 16), qb.y, sdot);
-            sdot = fmaf(h2f(kr[u].w), qb.z, sdot);
-            sdot = fmaf(h2f(kr[u].w >> 16), qb.w, sdot);
+            float kv[8];
+            kr[u].unpack(kv);
+            float sdot = kv[0] * qa.x;
+            sdot = fmaf(kv[1], qa.y, sdot);
+            sdot = fmaf(kv[2], qa.z, sdot);
+            sdot = fmaf(kv[3], qa.w, sdot);
+            sdot = fmaf(kv[4], qb.x, sdot);
+            sdot = fmaf(kv[5], qb.y, sdot);
+            sdot = fmaf(kv[6], qb.z, sdot);
+            sdot = fmaf(kv[7], qb.w, sdot);
             sdot = group_sum<TPK>(sdot);
             sc[u] = key(c, u) < n ? sdot : -INFINITY;
             cmax = fmaxf(cmax, sc[u]);
@@ -467,12 +514,10 @@ __global__ __launch_bounds__(256) void k_attn_waves(const float *q, const __half
             const bool in = key(c, u) < n;
             const float pj = in ? expf(sc[u] - mnew) : 0.f;
             l += pj;
-            const uint32_t wv[4] = {in ? vr[u].x : 0u, in ? vr[u].y : 0u, in ? vr[u].z : 0u, in ? vr[u].w : 0u};
+            float vv[8];
+            vr[u].unpack(vv, in);
 #pragma unroll
-            for (int q2 = 0; q2 < 4; ++q2) {
-                acc[2 * q2] = fmaf(pj, h2f(wv[q2]), acc[2 * q2]);
-                acc[2 * q2 + 1] = fmaf(pj, h2f(wv[q2] >> 16), acc[2 * q2 + 1]);
-            }
+            for (int e = 0; e < 8; ++e) acc[e] = fmaf(pj, vv[e], acc[e]);
         }
         m = mnew;
     }
@@ -937,13 +982,26 @@ hipError_t embed_pos_rows(const DevMatrix &E, const uint32_t *ids, const uint32_
     MLG_DISPATCH_TYPE(E.type, launch_embed_pos_rows, E, ids, pidx, rows, pos, scale, x, st)
 }
 
-hipError_t qkv_split(const float *qkv, int b, int H, int hd, int m, const uint32_t *step, float *q, __half *kc,
-                     __half *vc, hipStream_t st) {
+namespace {
+template <typename KT>
+hipError_t qkv_split_t(const float *qkv, int b, int H, int hd, int m, const uint32_t *step, float *q, KT *kc, KT *vc,
+                       hipStream_t st) {
     if (hd % 8 || b <= 0) return b <= 0 ? hipSuccess : hipErrorInvalidValue;
     const int n = b * H * hd / 8;
-    hipLaunchKernelGGL(k_split_qkv8, dim3(unsigned((n + 255) / 256)), dim3(256), 0, st, qkv, b, H, hd, m, step, q, kc,
-                       vc);
+    hipLaunchKernelGGL(k_split_qkv8<KT>, dim3(unsigned((n + 255) / 256)), dim3(256), 0, st, qkv, b, H, hd, m, step, q,
+                       kc, vc);
     return hipGetLastError();
+}
+}  // namespace
+
+hipError_t qkv_split(const float *qkv, int b, int H, int hd, int m, const uint32_t *step, float *q, __half *kc,
+                     __half *vc, hipStream_t st) {
+    return qkv_split_t(qkv, b, H, hd, m, step, q, kc, vc, st);
+}
+
+hipError_t qkv_split(const float *qkv, int b, int H, int hd, int m, const uint32_t *step, float *q, float *kc,
+                     float *vc, hipStream_t st) {
+    return qkv_split_t(qkv, b, H, hd, m, step, q, kc, vc, st);
 }
 
 constexpr int kAttnSplit = 4;  // waves per (row, head) pair in k_attn_waves
@@ -952,9 +1010,10 @@ bool attn_head_size_supported(int hd) {
     return hd == 8 || hd == 16 || hd == 32 || hd == 64 || hd == 128 || hd == 256;
 }
 
-hipError_t attn_decode(const float *q, const __half *K, const __half *V, int b, int H, int hd, int L,
-                       const uint32_t *lens, const uint32_t *step, float *out, hipStream_t st, const uint32_t *rows,
-                       bool out_split) {
+namespace {
+template <typename KT>
+hipError_t attn_decode_t(const float *q, const KT *K, const KT *V, int b, int H, int hd, int L, const uint32_t *lens,
+                         const uint32_t *step, float *out, hipStream_t st, const uint32_t *rows, bool out_split) {
     if (b * H <= 0) return hipSuccess;
     if (out_split && ((H * hd) % 16 || reinterpret_cast<uintptr_t>(out) % 16)) return hipErrorInvalidValue;
     constexpr int ppw = 4 / kAttnSplit;  // pairs per workgroup of 4 waves
@@ -962,8 +1021,8 @@ hipError_t attn_decode(const float *q, const __half *K, const __half *V, int b, 
     switch (hd) {
 #define MLG_ATTN_WAVES(HD)                                                                                          \
     case HD:                                                                                                        \
-        hipLaunchKernelGGL((k_attn_waves<HD, kAttnSplit>), wgrid, dim3(256), 0, st, q, K, V, b, H, L, lens, step,   \
-                           out, rows, out_split ? 1 : 0);                                                           \
+        hipLaunchKernelGGL((k_attn_waves<HD, kAttnSplit, KT>), wgrid, dim3(256), 0, st, q, K, V, b, H, L, lens,     \
+                           step, out, rows, out_split ? 1 : 0);                                                     \
         return hipGetLastError();
         MLG_ATTN_WAVES(8)
         MLG_ATTN_WAVES(16)
@@ -975,6 +1034,19 @@ hipError_t attn_decode(const float *q, const __half *K, const __half *V, int b, 
     default: return hipErrorInvalidValue;  // attn_head_size_supported is checked at model load
     }
 }
+}  // namespace
+
+hipError_t attn_decode(const float *q, const __half *K, const __half *V, int b, int H, int hd, int L,
+                       const uint32_t *lens, const uint32_t *step, float *out, hipStream_t st, const uint32_t *rows,
+                       bool out_split) {
+    return attn_decode_t(q, K, V, b, H, hd, L, lens, step, out, st, rows, out_split);
+}
+
+hipError_t attn_decode(const float *q, const float *K, const float *V, int b, int H, int hd, int L,
+                       const uint32_t *lens, const uint32_t *step, float *out, hipStream_t st, const uint32_t *rows,
+                       bool out_split) {
+    return attn_decode_t(q, K, V, b, H, hd, L, lens, step, out, st, rows, out_split);
+}
 
 hipError_t attn_prefill(const float *qkv, int b, int s, int H, int hd, const uint32_t *lens, float *out,
                         hipStream_t st) {
@@ -983,7 +1055,7 @@ hipError_t attn_prefill(const float *qkv, int b, int s, int H, int hd, const uin
     return hipGetLastError();
 }
 
-hipError_t split_cross_kv(const float *kv, int b, int s, int H, int hd, int L, __half *K0, size_t kv_elems,
+hipError_t split_cross_kv(const float *kv, int b, int s, int H, int hd, int L, float *K0, size_t kv_elems,
                           hipStream_t st) {
     const size_t n = size_t(b) * s * H * hd * L;
     if (!n) return hipSuccess;
@@ -991,16 +1063,29 @@ hipError_t split_cross_kv(const float *kv, int b, int s, int H, int hd, int L, _
     return hipGetLastError();
 }
 
-hipError_t copy_cross(const __half *src0, size_t src_pair, const uint32_t *map, int n_dst, int H, int s, int hd,
-                      __half *dst0, size_t dst_pair, int S, int pairs, hipStream_t st) {
+namespace {
+template <typename KT>
+hipError_t copy_cross_t(const float *src0, size_t src_pair, const uint32_t *map, int n_dst, int H, int s, int hd,
+                        KT *dst0, size_t dst_pair, int S, int pairs, hipStream_t st) {
     if (hd % 8 || src_pair % 8 || dst_pair % 8 || reinterpret_cast<uintptr_t>(src0) % 16 ||
         reinterpret_cast<uintptr_t>(dst0) % 16 || s > S)
         return hipErrorInvalidValue;
     const size_t total = size_t(pairs) * n_dst * H * s * (hd / 8);
     if (!total) return hipSuccess;
-    hipLaunchKernelGGL(k_copy_cross, dim3(grid_1d(total, 256)), dim3(256), 0, st, src0, src_pair, map, n_dst, H, s, hd,
-                       dst0, dst_pair, S, pairs);
+    hipLaunchKernelGGL(k_copy_cross<KT>, dim3(grid_1d(total, 256)), dim3(256), 0, st, src0, src_pair, map, n_dst, H, s,
+                       hd, dst0, dst_pair, S, pairs);
     return hipGetLastError();
+}
+}  // namespace
+
+hipError_t copy_cross(const float *src0, size_t src_pair, const uint32_t *map, int n_dst, int H, int s, int hd,
+                      __half *dst0, size_t dst_pair, int S, int pairs, hipStream_t st) {
+    return copy_cross_t(src0, src_pair, map, n_dst, H, s, hd, dst0, dst_pair, S, pairs, st);
+}
+
+hipError_t copy_cross(const float *src0, size_t src_pair, const uint32_t *map, int n_dst, int H, int s, int hd,
+                      float *dst0, size_t dst_pair, int S, int pairs, hipStream_t st) {
+    return copy_cross_t(src0, src_pair, map, n_dst, H, s, hd, dst0, dst_pair, S, pairs, st);
 }
 
 hipError_t argmax_partial(const float *logits, int b, int V, int ldl, int mask_id, float *pv, uint32_t *pi, int parts,
@@ -1012,15 +1097,15 @@ hipError_t argmax_partial(const float *logits, int b, int V, int ldl, int mask_i
 
 hipError_t greedy_finalize(const float *pv, const uint32_t *pi, int parts, int b, uint8_t *finished, uint32_t *ids,
                            uint32_t *out, int m, uint32_t *step, uint32_t eos, uint32_t pad, hipStream_t st,
-                           const SlFinalize &sl) {
+                           const SlFinalize &sl, float *outv) {
     if (sl.vocab_map && (!sl.spv || !sl.spi || !sl.src_ids || !sl.sl_row || !sl.src_row || sl.S < 1))
         return hipErrorInvalidValue;
     if (b <= 4)
         hipLaunchKernelGGL(k_greedy_finalize_wg, dim3(1), dim3(256), 0, st, pv, pi, parts, b, finished, ids, out, m,
-                           step, eos, pad, sl);
+                           step, eos, pad, sl, outv);
     else
         hipLaunchKernelGGL(k_greedy_finalize, dim3(1), dim3(1024), 0, st, pv, pi, parts, b, finished, ids, out, m,
-                           step, eos, pad, sl);
+                           step, eos, pad, sl, outv);
     return hipGetLastError();
 }
 

@@ -99,6 +99,9 @@ hipError_t gemm_residual_ln(const DevMatrix &w, const float *X, int ldx, int M, 
 hipError_t gemm_qkv(const DevMatrix &w, const float *X, int ldx, int M, const float *bias, int H, int hd, int slots,
                     const uint32_t *step, float *q, __half *kc, __half *vc, float *qkv_tmp, hipStream_t st, float *ws,
                     size_t ws_bytes);
+hipError_t gemm_qkv(const DevMatrix &w, const float *X, int ldx, int M, const float *bias, int H, int hd, int slots,
+                    const uint32_t *step, float *q, float *kc, float *vc, float *qkv_tmp, hipStream_t st, float *ws,
+                    size_t ws_bytes);
 // ---- decode projections for batches of up to 64 rows, one launch each (k_dgemm.hip) ----
 constexpr int kDgemmMaxRows = 64;
 // Input LayerNorm from the statistics the residual stream's last writer left:
@@ -123,6 +126,9 @@ hipError_t dgemm_resid(const DevMatrix &w, const float *x, int ldx, int M, const
 // The fused QKV projection: q [M][d] f32, K/V f16 into the caches [M][H][slots][hd] at *step.
 hipError_t dgemm_qkv(const DevMatrix &w, const float *x, int ldx, int M, const DgemmLn *ln, const float *bias, int H,
                      int hd, int slots, const uint32_t *step, float *q, __half *kc, __half *vc, hipStream_t st);
+// The same with f32 caches (the generic decode path).
+hipError_t dgemm_qkv(const DevMatrix &w, const float *x, int ldx, int M, const DgemmLn *ln, const float *bias, int H,
+                     int hd, int slots, const uint32_t *step, float *q, float *kc, float *vc, hipStream_t st);
 // The cross attention of a decode step in one launch: q = LN(x) W^T + bias (x the residual
 // stream, fragment order) and its attention over K/V [M][H][L][hd] (f16, lens[m] keys
 // each); att [M][H hd] as split fragments, the cross out-projection's A operand.
@@ -193,10 +199,17 @@ hipError_t embed_pos_rows(const DevMatrix &E, const uint32_t *ids, const uint32_
 // [b][H][m][hd] at slot *step.
 hipError_t qkv_split(const float *qkv, int b, int H, int hd, int m, const uint32_t *step, float *q, __half *kc,
                      __half *vc, hipStream_t st);
+// The same into f32 caches (the generic decode path's K/V, src/model.rs:195-227).
+hipError_t qkv_split(const float *qkv, int b, int H, int hd, int m, const uint32_t *step, float *q, float *kc,
+                     float *vc, hipStream_t st);
 // Single-query attention per (row, head) over f16 K/V [b][H][L][hd]: n = lens[row]
 // if lens, else *step + 1.  out [b][H*hd].  Head sizes: attn_head_size_supported.
 bool attn_head_size_supported(int hd);
 hipError_t attn_decode(const float *q, const __half *K, const __half *V, int b, int H, int hd, int L,
+                       const uint32_t *lens, const uint32_t *step, float *out, hipStream_t st, const uint32_t *rows = nullptr,
+                       bool out_split = false);
+// The same over f32 K/V (the generic decode path: candle KvCache and cross K/V in f32).
+hipError_t attn_decode(const float *q, const float *K, const float *V, int b, int H, int hd, int L,
                        const uint32_t *lens, const uint32_t *step, float *out, hipStream_t st, const uint32_t *rows = nullptr,
                        bool out_split = false);
 // rows (optional, [b][L]): cache row holding slot j of row b (beam reordering without copies).
@@ -206,28 +219,31 @@ hipError_t attn_decode(const float *q, const __half *K, const __half *V, int b, 
 // key j of row i valid iff j < lens[i].  out [b*s][d].
 hipError_t attn_prefill(const float *qkv, int b, int s, int H, int hd, const uint32_t *lens, float *out,
                         hipStream_t st);
-// kv [b*s][2d] f32 (k | v) -> f16 K, V [b][H][s][hd]
-// kv [b*s][L][2d] f32 (the stacked cross K/V projection of L layers) -> f16 [b][H][s][hd]:
+// kv [b*s][L][2d] f32 (the stacked cross K/V projection of L layers) -> f32 [b][H][s][hd]:
 // layer l's K at K0 + 2 l kv_elems, its V at K + kv_elems (kv_elems = b*s*d)
-hipError_t split_cross_kv(const float *kv, int b, int s, int H, int hd, int L, __half *K0, size_t kv_elems,
+hipError_t split_cross_kv(const float *kv, int b, int s, int H, int hd, int L, float *K0, size_t kv_elems,
                           hipStream_t st);
 // rows [r0, r0 + n) of w as a matrix of their own (block-major planes; no lane-major copy)
 DevMatrix rows_view(const DevMatrix &w, int r0, int n);
 // For each of `pairs` arrays (every layer's cross K and V): dst0 + p * dst_pair
 // [.][H][S][hd] row r (< n_dst) <- src0 + p * src_pair [.][H][s][hd] row map[r] (row r if
-// map is null), S >= s.  map is a device array; hd, the pair strides and the bases are
-// 16-byte multiples.
-hipError_t copy_cross(const __half *src0, size_t src_pair, const uint32_t *map, int n_dst, int H, int s, int hd,
+// map is null), S >= s.  map is a device array; hd, the pair strides are multiples of 8
+// values and the bases 16-byte aligned.  The source is f32 (the encoder's output); an f16
+// destination receives it rounded to nearest even.
+hipError_t copy_cross(const float *src0, size_t src_pair, const uint32_t *map, int n_dst, int H, int s, int hd,
                       __half *dst0, size_t dst_pair, int S, int pairs, hipStream_t st);
+hipError_t copy_cross(const float *src0, size_t src_pair, const uint32_t *map, int n_dst, int H, int s, int hd,
+                      float *dst0, size_t dst_pair, int S, int pairs, hipStream_t st);
 // Argmax over logits [b][V] (row stride ldl) into pv/pi [b][parts].
 hipError_t argmax_partial(const float *logits, int b, int V, int ldl, int mask_id, float *pv, uint32_t *pi,
                           int parts, hipStream_t st);
 // Second argmax pass + greedy bookkeeping (kernels/malaga.cu:290-326 semantics):
 // tok = finished ? pad : argmax ; finished |= tok == eos ; ids = tok ;
-// out[row][*step] = tok ; ++*step.
+// out[row][*step] = tok ; ++*step.  outv (optional, [b][m]): outv[row][*step] = the
+// winning logit (before the finished / pad rule).
 hipError_t greedy_finalize(const float *pv, const uint32_t *pi, int parts, int b, uint8_t *finished, uint32_t *ids,
                            uint32_t *out, int m, uint32_t *step, uint32_t eos, uint32_t pad, hipStream_t st,
-                           const SlFinalize &sl = SlFinalize{});
+                           const SlFinalize &sl = SlFinalize{}, float *outv = nullptr);
 // Beam: per row log-softmax of logits [rows][V] and its top-k (k <= 8, ties -> lowest
 // index): vals/idx [rows][k].  mask_id (>= 0) is treated as -inf.
 hipError_t logsoftmax_topk(const float *logits, int rows, int V, int k, int mask_id, float *work, float *vals,

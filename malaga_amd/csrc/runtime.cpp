@@ -6,6 +6,7 @@
 #include <cstdlib>
 #include <cstring>
 #include <numeric>
+#include <type_traits>
 
 #include "beam.hpp"
 #include "gguf.hpp"
@@ -674,8 +675,8 @@ std::unique_ptr<Batch> Model::encode(const std::vector<std::vector<uint32_t>> &s
     }
     const int Hd = cfg.decoder_heads, hdd = d / Hd;
     const size_t kv_elems = size_t(M) * d;
-    out->block = dev_alloc(std::max<size_t>(dec.size(), 1) * 2 * kv_elems * 2, "cross K/V");
-    __half *K0 = static_cast<__half *>(out->block);
+    out->block = dev_alloc(std::max<size_t>(dec.size(), 1) * 2 * kv_elems * 4, "cross K/V");
+    float *K0 = static_cast<float *>(out->block);
     for (int i = 0; i < L; ++i) {
         out->ck.push_back(K0 + 2 * size_t(i) * kv_elems);
         out->cv.push_back(K0 + (2 * size_t(i) + 1) * kv_elems);
@@ -692,12 +693,14 @@ std::unique_ptr<Batch> Model::encode(const std::vector<std::vector<uint32_t>> &s
     return out;
 }
 
-std::unique_ptr<StaticState> Model::new_state(int b, int s, int m, bool logits, bool row_map, const Shortlist *sl) {
+std::unique_ptr<StaticState> Model::new_state(int b, int s, int m, bool logits, bool row_map, const Shortlist *sl,
+                                              bool kv32) {
     auto st = std::make_unique<StaticState>();
     st->b = b;
     st->s = s;
     st->m = m;
     st->sl = sl;
+    st->kv32 = kv32;
     const DevMatrix &head = sl ? sl->head : embed;
     const int d = cfg.d_model, H = cfg.decoder_heads, hd = d / H, L = cfg.decoder_layers, V = cfg.vocab_size;
     auto get = [&](size_t bytes, const char *what) {
@@ -710,20 +713,28 @@ std::unique_ptr<StaticState> Model::new_state(int b, int s, int m, bool logits, 
     st->step = static_cast<uint32_t *>(get(4, "step"));
     st->lens = static_cast<uint32_t *>(get(size_t(b) * 4, "lens"));
     st->out = static_cast<uint32_t *>(get(size_t(b) * m * 4, "out"));
+    st->outv = static_cast<float *>(get(size_t(b) * m * 4, "winning logits"));
     st->finished = static_cast<uint8_t *>(get(size_t(b), "finished"));
     st->row_src = static_cast<uint32_t *>(get(size_t(b) * 4, "source rows"));
     // one block each for the self and the cross K/V of every layer (layer l: K, then V);
     // slots past the step are read (and masked) by the fused attention: keep them finite
-    const size_t self_pair = size_t(b) * H * m * hd, cross_pair = size_t(b) * H * s * hd;
-    __half *self_kv = static_cast<__half *>(get(std::max<size_t>(2 * L * self_pair, 1) * 2, "self K/V"));
-    __half *cross_kv = static_cast<__half *>(get(std::max<size_t>(2 * L * cross_pair, 1) * 2, "cross K/V"));
-    check_hip(hipMemsetAsync(self_kv, 0, 2 * L * self_pair * 2, ctx->stream), "memset");
-    check_hip(hipMemsetAsync(cross_kv, 0, 2 * L * cross_pair * 2, ctx->stream), "memset");
+    const size_t self_pair = size_t(b) * H * m * hd, cross_pair = size_t(b) * H * s * hd, es = kv32 ? 4 : 2;
+    void *self_kv = get(std::max<size_t>(2 * L * self_pair, 1) * es, "self K/V");
+    void *cross_kv = get(std::max<size_t>(2 * L * cross_pair, 1) * es, "cross K/V");
+    check_hip(hipMemsetAsync(self_kv, 0, 2 * L * self_pair * es, ctx->stream), "memset");
+    check_hip(hipMemsetAsync(cross_kv, 0, 2 * L * cross_pair * es, ctx->stream), "memset");
     for (int i = 0; i < L; ++i) {
-        st->kc.push_back(self_kv + 2 * i * self_pair);
-        st->vc.push_back(self_kv + (2 * i + 1) * self_pair);
-        st->ck.push_back(cross_kv + 2 * i * cross_pair);
-        st->cv.push_back(cross_kv + (2 * i + 1) * cross_pair);
+        if (kv32) {
+            st->kc32.push_back(static_cast<float *>(self_kv) + 2 * i * self_pair);
+            st->vc32.push_back(static_cast<float *>(self_kv) + (2 * i + 1) * self_pair);
+            st->ck32.push_back(static_cast<float *>(cross_kv) + 2 * i * cross_pair);
+            st->cv32.push_back(static_cast<float *>(cross_kv) + (2 * i + 1) * cross_pair);
+        } else {
+            st->kc.push_back(static_cast<__half *>(self_kv) + 2 * i * self_pair);
+            st->vc.push_back(static_cast<__half *>(self_kv) + (2 * i + 1) * self_pair);
+            st->ck.push_back(static_cast<__half *>(cross_kv) + 2 * i * cross_pair);
+            st->cv.push_back(static_cast<__half *>(cross_kv) + (2 * i + 1) * cross_pair);
+        }
     }
     // rows padded to 16: the decode-GEMM step keeps x in fragment order (whole row tiles)
     const size_t bp = size_t(b + 15) / 16 * 16;
@@ -731,7 +742,7 @@ std::unique_ptr<StaticState> Model::new_state(int b, int s, int m, bool logits, 
     check_hip(hipMemsetAsync(st->x, 0, bp * d * 4, ctx->stream), "memset");
     st->xb = static_cast<float *>(get(size_t(b) * d * 4, "x (second buffer)"));
     st->qc = static_cast<float *>(get(size_t(b) * d * 4, "cross q"));
-    st->fused = fusable(b, m, s) && (!sl || step_embed_supported(dec[0].qkv.w.type, sl->head.type));
+    st->fused = !kv32 && fusable(b, m, s) && (!sl || step_embed_supported(dec[0].qkv.w.type, sl->head.type));
     if (st->fused) {
         st->part = static_cast<float *>(get(size_t(H) * b * d * 4, "attention partial sums"));
         st->part2 = static_cast<float *>(get(size_t(H) * b * d * 4, "cross attention partial sums"));
@@ -790,9 +801,15 @@ void Model::reset_state(StaticState &st, const Batch &src, const std::vector<uin
     Staging &up = ctx->staging;
     up.upload(d_map, row_of.data(), row_of.size() * 4, s);
     // every layer's K and V in one launch: both blocks hold layer l's K, then its V
+    // (src/graph.rs:94-97 stores them as f16; the generic path keeps f32)
+    const size_t src_pair = size_t(src.b) * src.s * cfg.d_model, dst_pair = size_t(st.b) * H * st.s * hd;
     if (!st.ck.empty())
-        check_hip(copy_cross(src.ck[0], size_t(src.b) * src.s * cfg.d_model, d_map, n, H, src.s, hd, st.ck[0],
-                             size_t(st.b) * H * st.s * hd, st.s, 2 * int(st.ck.size()), s),
+        check_hip(copy_cross(src.ck[0], src_pair, d_map, n, H, src.s, hd, st.ck[0], dst_pair, st.s,
+                             2 * int(st.ck.size()), s),
+                  "copy_cross");
+    if (!st.ck32.empty())
+        check_hip(copy_cross(src.ck[0], src_pair, d_map, n, H, src.s, hd, st.ck32[0], dst_pair, st.s,
+                             2 * int(st.ck32.size()), s),
                   "copy_cross");
     std::vector<uint32_t> lens(static_cast<size_t>(st.b), 1u);
     for (int r = 0; r < n; ++r) lens[r] = src.lens[row_of[r]];
@@ -842,6 +859,16 @@ bool Model::fusable(int b, int m, int s) const {
     }
     return true;
 }
+
+namespace {
+// Layer i's self and cross caches in the state's precision: f(kc, vc, ck, cv) with __half
+// pointers (the graph step) or float pointers (the generic path).
+template <typename F>
+void with_kv(const StaticState &st, size_t i, F &&f) {
+    if (st.kv32) f(st.kc32[i], st.vc32[i], st.ck32[i], st.cv32[i]);
+    else f(st.kc[i], st.vc[i], st.ck[i], st.cv[i]);
+}
+}  // namespace
 
 // src/model.rs:552-612 as six fused launches per layer (k_step.hip).
 float *Model::step_fused(StaticState &st, bool final_ln) {
@@ -924,7 +951,7 @@ void Model::lm_head(StaticState &st, bool greedy_mode, int mask_id, const float 
             sl = SlFinalize{st.sl->d_ids, V, st.spv, st.spi, st.src_ids, st.s, st.sl_row, st.src_row};
         }
         check_hip(greedy_finalize(st.pv, st.pi, parts, B, st.finished, st.ids, st.out, st.m, st.step,
-                                  uint32_t(cfg.eos_token_id), uint32_t(cfg.pad_token_id), s, sl),
+                                  uint32_t(cfg.eos_token_id), uint32_t(cfg.pad_token_id), s, sl, st.outv),
                   "greedy_finalize");
     } else {
         const int V = cfg.vocab_size;
@@ -974,18 +1001,20 @@ void Model::step(StaticState &st, bool greedy_mode, int mask_id) {
     };
     for (size_t i = 0; i < dec.size(); ++i) {
         const DecLayer &l = dec[i];
-        if (B <= gemv_max_batch(l.qkv.w)) {
-            matmul(l.qkv, st.h, B, st.qkv, false, nullptr);
-            check_hip(qkv_split(st.qkv, B, H, hd, st.m, st.step, st.q, st.kc[i], st.vc[i], s), "qkv_split");
-        } else {
-            check_hip(gemm_qkv(l.qkv.w, st.h, d, B, l.qkv.b, H, hd, st.m, st.step, st.q, st.kc[i], st.vc[i], st.qkv, s,
-                               ctx->gemm_workspace(), kGemmWorkspaceBytes),
-                      "gemm_qkv");
-        }
-        check_hip(attn_decode(st.q, st.kc[i], st.vc[i], B, H, hd, st.m, nullptr, st.step, st.att, s, st.rows), "attn");
-        project_residual_ln(l.out, st.att, l.cross_norm);
-        matmul(l.cross_q, st.h, B, st.q, false, nullptr);
-        check_hip(attn_decode(st.q, st.ck[i], st.cv[i], B, H, hd, st.s, st.lens, nullptr, st.att, s), "attn");
+        with_kv(st, i, [&](auto *kc, auto *vc, auto *ck, auto *cv) {
+            if (B <= gemv_max_batch(l.qkv.w)) {
+                matmul(l.qkv, st.h, B, st.qkv, false, nullptr);
+                check_hip(qkv_split(st.qkv, B, H, hd, st.m, st.step, st.q, kc, vc, s), "qkv_split");
+            } else {
+                check_hip(gemm_qkv(l.qkv.w, st.h, d, B, l.qkv.b, H, hd, st.m, st.step, st.q, kc, vc, st.qkv, s,
+                                   ctx->gemm_workspace(), kGemmWorkspaceBytes),
+                          "gemm_qkv");
+            }
+            check_hip(attn_decode(st.q, kc, vc, B, H, hd, st.m, nullptr, st.step, st.att, s, st.rows), "attn");
+            project_residual_ln(l.out, st.att, l.cross_norm);
+            matmul(l.cross_q, st.h, B, st.q, false, nullptr);
+            check_hip(attn_decode(st.q, ck, cv, B, H, hd, st.s, st.lens, nullptr, st.att, s), "attn");
+        });
         project_residual_ln(l.cross_out, st.att, l.ffn_norm);
         matmul(l.up, st.h, B, st.u, true, nullptr);
         project_residual_ln(l.down, st.u, i + 1 < dec.size() ? dec[i + 1].attn_norm : dec_norm);
@@ -1022,24 +1051,30 @@ void Model::step_dgemm(StaticState &st, bool greedy_mode, int mask_id) {
     for (size_t i = 0; i < dec.size(); ++i) {
         const DecLayer &l = dec[i];
         const DgemmLn ln_attn = ln(l.attn_norm), ln_cross = ln(l.cross_norm), ln_ffn = ln(l.ffn_norm);
-        check_hip(dgemm_qkv(l.qkv.w, i == 0 ? st.h : st.x, d, B, i == 0 ? nullptr : &ln_attn, l.qkv.b, H, hd, st.m,
-                            st.step, st.q, st.kc[i], st.vc[i], s),
-                  "dgemm_qkv");
-        // x in fragment order, att and u as split f16 hi / lo fragments: the A-operand
-        // order of the decode GEMMs (frag_index, device.hpp)
-        check_hip(attn_decode(st.q, st.kc[i], st.vc[i], B, H, hd, st.m, nullptr, st.step, st.att, s, st.rows, true),
-                  "attn");
-        check_hip(dgemm_resid(l.out.w, st.att, d, B, l.out.b, st.x, st.lnstat, s, true), "dgemm_out");
-        if (!split_cross_ && dgemm_cross_attn_supported(l.cross_q.w, B, H, hd)) {
-            check_hip(dgemm_cross_attn(l.cross_q.w, st.x, B, ln_cross, l.cross_q.b, st.ck[i], st.cv[i], H, hd, st.s,
-                                       st.lens, st.att, s),
-                      "dgemm_cross_attn");
-        } else {
-            check_hip(dgemm_store(l.cross_q.w, st.x, d, B, &ln_cross, l.cross_q.b, false, st.q, d, s),
-                      "dgemm_cross_q");
-            check_hip(attn_decode(st.q, st.ck[i], st.cv[i], B, H, hd, st.s, st.lens, nullptr, st.att, s, nullptr, true),
-                      "attn");
-        }
+        with_kv(st, i, [&](auto *kc, auto *vc, auto *ck, auto *cv) {
+            check_hip(dgemm_qkv(l.qkv.w, i == 0 ? st.h : st.x, d, B, i == 0 ? nullptr : &ln_attn, l.qkv.b, H, hd,
+                                st.m, st.step, st.q, kc, vc, s),
+                      "dgemm_qkv");
+            // x in fragment order, att and u as split f16 hi / lo fragments: the A-operand
+            // order of the decode GEMMs (frag_index, device.hpp)
+            check_hip(attn_decode(st.q, kc, vc, B, H, hd, st.m, nullptr, st.step, st.att, s, st.rows, true), "attn");
+            check_hip(dgemm_resid(l.out.w, st.att, d, B, l.out.b, st.x, st.lnstat, s, true), "dgemm_out");
+            bool fused_cross = false;
+            if constexpr (std::is_same_v<std::remove_const_t<std::remove_pointer_t<decltype(ck)>>, __half>) {
+                if (!split_cross_ && dgemm_cross_attn_supported(l.cross_q.w, B, H, hd)) {
+                    check_hip(dgemm_cross_attn(l.cross_q.w, st.x, B, ln_cross, l.cross_q.b, ck, cv, H, hd, st.s,
+                                               st.lens, st.att, s),
+                              "dgemm_cross_attn");
+                    fused_cross = true;
+                }
+            }
+            if (!fused_cross) {
+                check_hip(dgemm_store(l.cross_q.w, st.x, d, B, &ln_cross, l.cross_q.b, false, st.q, d, s),
+                          "dgemm_cross_q");
+                check_hip(attn_decode(st.q, ck, cv, B, H, hd, st.s, st.lens, nullptr, st.att, s, nullptr, true),
+                          "attn");
+            }
+        });
         check_hip(dgemm_resid(l.cross_out.w, st.att, d, B, l.cross_out.b, st.x, st.lnstat, s, true), "dgemm_cross_out");
         check_hip(dgemm_store(l.up.w, st.x, d, B, &ln_ffn, l.up.b, true, st.u, f, s, true), "dgemm_up");
         check_hip(dgemm_resid(l.down.w, st.u, f, B, l.down.b, st.x, st.lnstat, s, true), "dgemm_down");
@@ -1147,20 +1182,21 @@ std::vector<GraphCache::Key> GraphCache::keys() const {
 
 std::vector<std::vector<uint32_t>> GraphCache::greedy(const Batch &src, uint32_t tgt_lang, int max_new,
                                                       int sync_every, bool eos_mask, bool use_graph,
-                                                      const Shortlist *sl) {
+                                                      const Shortlist *sl, std::vector<std::vector<float>> *top) {
     try {
-        return run(src, tgt_lang, max_new, sync_every, eos_mask, use_graph, sl);
+        return run(src, tgt_lang, max_new, sync_every, eos_mask, use_graph, sl, top);
     } catch (const Failure &f) {
         // src/graph.rs:214-222: out of memory -> drop graphs for good, decode eagerly
         if (f.code != ERR_OOM || !capture_) throw;
         capture_ = false;
         clear();
-        return run(src, tgt_lang, max_new, sync_every, eos_mask, use_graph, sl);
+        return run(src, tgt_lang, max_new, sync_every, eos_mask, use_graph, sl, top);
     }
 }
 
 std::vector<std::vector<uint32_t>> GraphCache::run(const Batch &src, uint32_t tgt_lang, int max_new, int sync_every,
-                                                   bool eos_mask, bool use_graph, const Shortlist *sl) {
+                                                   bool eos_mask, bool use_graph, const Shortlist *sl,
+                                                   std::vector<std::vector<float>> *top) {
     Model &m = *model_;
     if (!sl) m.ensure_embed();  // the full LM head and input embeddings
     hipStream_t s = m.ctx->stream;
@@ -1257,14 +1293,18 @@ std::vector<std::vector<uint32_t>> GraphCache::run(const Batch &src, uint32_t tg
         ++steps;
     }
     std::vector<uint32_t> out(static_cast<size_t>(st.b) * st.m);
+    std::vector<float> outv(top ? out.size() : 0);
     check_hip(hipMemcpyAsync(out.data(), st.out, out.size() * 4, hipMemcpyDeviceToHost, s), "D2H");
+    if (top) check_hip(hipMemcpyAsync(outv.data(), st.outv, outv.size() * 4, hipMemcpyDeviceToHost, s), "D2H");
     check_hip(hipStreamSynchronize(s), "sync");
     std::vector<std::vector<uint32_t>> res(static_cast<size_t>(n));
+    if (top) top->assign(static_cast<size_t>(n), {});
     for (int r = 0; r < n; ++r)
         for (int j = 1; j < steps; ++j) {
             const uint32_t t = out[size_t(r) * st.m + j];
             if (t == uint32_t(c.eos_token_id)) break;
             res[r].push_back(t);
+            if (top) (*top)[r].push_back(outv[size_t(r) * st.m + j]);
         }
     return res;
 }
@@ -1283,7 +1323,9 @@ std::vector<std::vector<uint32_t>> Model::beam(const Batch &src, uint32_t tgt_la
     const int b = src.b, bk = b * k, V = cfg.vocab_size;
     const uint32_t eos = uint32_t(cfg.eos_token_id);
     const int mask_id = eos_mask ? cfg.eos_token_id : -1;
-    auto st = new_state(bk, src.s, max_new + 2, true, true);
+    // src/translator.rs:195-201: beam search runs Nllb::encode/decode, whose K/V caches
+    // (candle KvCache) and cross K/V are f32
+    auto st = new_state(bk, src.s, max_new + 2, true, true, nullptr, true);
     std::vector<uint32_t> expand(static_cast<size_t>(bk));
     for (int i = 0; i < bk; ++i) expand[i] = uint32_t(i / k);
     reset_state(*st, src, expand, uint32_t(cfg.decoder_start_token_id));
@@ -1390,7 +1432,50 @@ std::vector<std::vector<uint32_t>> Model::beam(const Batch &src, uint32_t tgt_la
     return merge.result();
 }
 
-std::vector<float> Model::teacher_forced(const Batch &src, const std::vector<uint32_t> &tgt, int T) {
+std::vector<std::vector<uint32_t>> Model::greedy_generic(const Batch &src, uint32_t tgt_lang, int max_new,
+                                                         int sync_every, bool eos_mask) {
+    if (max_new < 1 || max_new > cfg.max_position_embeddings - 2)
+        fail(ERR_INVALID, "greedy: max_new " + std::to_string(max_new) + " outside 1.." +
+                              std::to_string(cfg.max_position_embeddings - 2));
+    ensure_embed();
+    hipStream_t s = ctx->stream;
+    const int b = src.b, mask_id = eos_mask ? cfg.eos_token_id : -1;
+    auto st = new_state(b, src.s, max_new + 2, false, false, nullptr, true);
+    std::vector<uint32_t> rows(static_cast<size_t>(b));
+    std::iota(rows.begin(), rows.end(), 0u);
+    reset_state(*st, src, rows, uint32_t(cfg.decoder_start_token_id));
+    // [start, tgt_lang] fed one position at a time (the t = 2 causal pass of
+    // src/translator.rs:228 computes the same); the first position's token is not kept
+    step(*st, true, mask_id);
+    check_hip(fill_u32(st->ids, tgt_lang, size_t(b), s), "fill");
+    std::vector<uint8_t> fin(static_cast<size_t>(b), 0);
+    ctx->staging.upload(st->finished, fin.data(), fin.size(), s);
+    // step k (1 .. max_new) writes token k into out[:, k]; translator.rs:230-238 stops
+    // after max_new tokens or when every row has finished at a multiple of sync_every
+    int k = 1;
+    for (;; ++k) {
+        step(*st, true, mask_id);
+        if (k == max_new) break;
+        if (k % sync_every == 0) {
+            check_hip(hipMemcpyAsync(fin.data(), st->finished, fin.size(), hipMemcpyDeviceToHost, s), "D2H");
+            check_hip(hipStreamSynchronize(s), "sync");
+            if (std::all_of(fin.begin(), fin.end(), [](uint8_t v) { return v != 0; })) break;
+        }
+    }
+    std::vector<uint32_t> out(size_t(b) * st->m);
+    check_hip(hipMemcpyAsync(out.data(), st->out, out.size() * 4, hipMemcpyDeviceToHost, s), "D2H");
+    check_hip(hipStreamSynchronize(s), "sync");
+    std::vector<std::vector<uint32_t>> res(static_cast<size_t>(b));
+    for (int r = 0; r < b; ++r)
+        for (int j = 1; j <= k; ++j) {  // strip (translator.rs:243-246): up to the first EOS
+            const uint32_t t = out[size_t(r) * st->m + j];
+            if (t == uint32_t(cfg.eos_token_id)) break;
+            res[r].push_back(t);
+        }
+    return res;
+}
+
+std::vector<float> Model::teacher_forced(const Batch &src, const std::vector<uint32_t> &tgt, int T, bool kv32) {
     ensure_embed();
     hipStream_t s = ctx->stream;
     const int b = src.b, V = cfg.vocab_size;
@@ -1398,7 +1483,7 @@ std::vector<float> Model::teacher_forced(const Batch &src, const std::vector<uin
     if (T + cfg.pad_token_id + 1 >= n_pos) fail(ERR_INVALID, "teacher_forced: sequence longer than the position table");
     for (uint32_t t : tgt)
         if (t >= uint32_t(V)) fail(ERR_INVALID, "token id out of range");
-    auto st = new_state(b, src.s, T, true);
+    auto st = new_state(b, src.s, T, true, false, nullptr, kv32);
     std::vector<uint32_t> rows(static_cast<size_t>(b));
     std::iota(rows.begin(), rows.end(), 0u);
     reset_state(*st, src, rows, tgt[0]);
@@ -1430,8 +1515,12 @@ std::vector<std::vector<uint32_t>> generate_to(Model &m, const std::vector<std::
     if (sl && !(sl->contains(uint32_t(m.cfg.decoder_start_token_id)) && sl->contains(tgt_lang))) sl = nullptr;
     auto batch = m.encode(src);
     std::vector<std::vector<uint32_t>> out;
-    if (o.beam_size <= 1)
-        out = m.graphs.greedy(*batch, tgt_lang, max_new, std::max(1, o.sync_every), o.eos_mask, o.fused, sl);
+    // src/translator.rs:184-201: greedy with `fused` runs the graph cache (f16 K/V), greedy
+    // without it and beam search the generic decoder (f32 K/V)
+    if (o.beam_size <= 1 && o.fused)
+        out = m.graphs.greedy(*batch, tgt_lang, max_new, std::max(1, o.sync_every), o.eos_mask, true, sl);
+    else if (o.beam_size <= 1)
+        out = m.greedy_generic(*batch, tgt_lang, max_new, std::max(1, o.sync_every), o.eos_mask);
     else
         out = m.beam(*batch, tgt_lang, max_new, o.beam_size, o.length_penalty, o.eos_mask, o.fused);
     for (size_t i = 0; i < src.size(); ++i) {

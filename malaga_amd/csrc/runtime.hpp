@@ -93,13 +93,15 @@ struct Shortlist {
     bool contains(uint32_t id) const { return row(id) >= 0; }
 };
 
-// Encoded sources: per decoder layer cross K/V [b][H][s][hd] f16 (src/model.rs:463-477).
+// Encoded sources: per decoder layer cross K/V [b][H][s][hd] in f32, as
+// Nllb::encode_cross returns them (src/model.rs:463-477); a decode state keeps them in f16
+// (the graph step, src/graph.rs:94-97) or f32 (the generic path).
 struct Batch {
     int b = 0, s = 0;
     std::vector<uint32_t> lens;
-    std::vector<uint32_t> ids;     // [b][s] source ids, right-padded with pad
-    std::vector<__half *> ck, cv;  // per decoder layer, inside `block`
-    void *block = nullptr;         // one allocation for every layer's cross K/V
+    std::vector<uint32_t> ids;    // [b][s] source ids, right-padded with pad
+    std::vector<float *> ck, cv;  // per decoder layer, inside `block`
+    void *block = nullptr;        // one allocation for every layer's cross K/V
     ~Batch();
 };
 
@@ -107,8 +109,14 @@ struct Batch {
 struct StaticState {
     int b = 0, s = 0, m = 0;
     uint32_t *ids = nullptr, *step = nullptr, *lens = nullptr, *out = nullptr;
+    float *outv = nullptr;  // [b][m]: the winning logit of each greedy token (parity hook)
     uint8_t *finished = nullptr;
+    // self and cross K/V per layer: f16 (kc ..; the fused graph step, kernels/malaga.cu:
+    // 142-154) or, with kv32, f32 (kc32 ..; the generic decode path's candle KvCache and
+    // cross K/V, src/model.rs:195-227, 504-540)
+    bool kv32 = false;
     std::vector<__half *> kc, vc, ck, cv;
+    std::vector<float *> kc32, vc32, ck32, cv32;
     // workspace (nothing is allocated inside a step)
     float *x = nullptr, *h = nullptr, *y = nullptr, *att = nullptr, *q = nullptr, *qkv = nullptr, *u = nullptr;
     float *xb = nullptr, *qc = nullptr;  // second residual buffer and cross queries (fused step)
@@ -151,8 +159,10 @@ class GraphCache {
     void clear();
     // Greedy decoding of an encoded batch; rows stripped at EOS (src/graph.rs:204-298).
     // sl: decode over the shortlist + source tokens (src/graph.rs:204-298 with a shortlist).
+    // top (optional): receives each row's winning logits, one per returned token.
     std::vector<std::vector<uint32_t>> greedy(const Batch &src, uint32_t tgt_lang, int max_new, int sync_every,
-                                              bool eos_mask, bool use_graph, const Shortlist *sl = nullptr);
+                                              bool eos_mask, bool use_graph, const Shortlist *sl = nullptr,
+                                              std::vector<std::vector<float>> *top = nullptr);
     size_t entries() const { return entries_.size(); }
     size_t graphs() const;
     // Bucket keys (b, s, m) of the cached states, least recently used first, and
@@ -173,7 +183,8 @@ class GraphCache {
         size_t bytes() const;
     };
     std::vector<std::vector<uint32_t>> run(const Batch &src, uint32_t tgt_lang, int max_new, int sync_every,
-                                           bool eos_mask, bool use_graph, const Shortlist *sl);
+                                           bool eos_mask, bool use_graph, const Shortlist *sl,
+                                           std::vector<std::vector<float>> *top);
     void evict(const Entry *keep);
     static void trim_graph_memory();
     Model *model_;
@@ -219,8 +230,9 @@ class Model {
     bool embed_resident() const { return embed.q != nullptr; }
     // logits: keep a [b][V] logits buffer; row_map: beam-search cache-row map (rows);
     // sl: buffers of shortlist decoding (greedy only).
+    // kv32: f32 K/V caches (the generic path; never the fused step kernels)
     std::unique_ptr<StaticState> new_state(int b, int s, int m, bool logits, bool row_map = false,
-                                           const Shortlist *sl = nullptr);
+                                           const Shortlist *sl = nullptr, bool kv32 = false);
     // src/model.rs:552-612: one decoder step on fixed buffers.  greedy: argmax +
     // bookkeeping, else logits into st.logits and ++step.
     void step(StaticState &st, bool greedy, int mask_id);
@@ -231,10 +243,17 @@ class Model {
     void set_shortlist_input(StaticState &st, uint32_t id);
     // src/translator.rs:250-335.  use_graph: replay one captured step + top-k per
     // beam step (off when capture is disabled for the cache).
+    // Decodes on f32 K/V like the reference's Nllb::encode/decode path.
     std::vector<std::vector<uint32_t>> beam(const Batch &src, uint32_t tgt_lang, int max_new, int k, float lp,
                                             bool eos_mask, bool use_graph = true);
-    // Logits after feeding tgt[:, t] at position t, for t < T: [b][T][V] (parity tests).
-    std::vector<float> teacher_forced(const Batch &src, const std::vector<uint32_t> &tgt, int T);
+    // src/translator.rs:195-199, 214-241: greedy decoding on the generic path (GenOptions::
+    // fused = false): f32 K/V, every step launched eagerly, the finished flags read every
+    // sync_every steps.
+    std::vector<std::vector<uint32_t>> greedy_generic(const Batch &src, uint32_t tgt_lang, int max_new,
+                                                      int sync_every, bool eos_mask);
+    // Logits after feeding tgt[:, t] at position t, for t < T: [b][T][V] (parity tests);
+    // kv32: on f32 K/V (the generic path), else f16 (the graph step).
+    std::vector<float> teacher_forced(const Batch &src, const std::vector<uint32_t> &tgt, int T, bool kv32 = false);
 
   private:
     std::vector<void *> owned_;

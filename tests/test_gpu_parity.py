@@ -34,8 +34,11 @@ def test_fused_greedy_matches_oracle_tiny(tiny_gguf, models, preset):
     # the second run replays the cached graphs (pipeline.rs:121-122)
     assert gpu.generate(src, PLT) == got
     assert gpu.graph_stats()["graphs"] >= 1
-    # the same static step run eagerly (fused = false here)
-    assert gpu.generate(src, PLT, M.GenOptions(fused=False)) == got
+    # fused = false: the generic decoder (f32 K/V, src/translator.rs:195-199), against the
+    # oracle's f32-K/V decode; on this fixture it also equals the fused decode
+    # (pipeline.rs:105-124)
+    want32, _ = orc.translate_batch(src, PLT, kv_f16=False)
+    assert gpu.generate(src, PLT, M.GenOptions(fused=False)) == want32 == got
 
 
 @pytest.mark.parametrize("preset", ["f32", "q8_0"])
@@ -78,7 +81,8 @@ def test_beam_matches_oracle(tiny_gguf, kq_gguf, models, k):
     for path, tgt in ((tiny_gguf("f32"), PLT), (kq_gguf("q4_k_m"), 998)):
         gpu, orc = models(path)
         src = pipeline_sentences()[:4] if tgt == PLT else [[997, 5, 6, 7, 8, 2], [997, 40, 2]]
-        want, _ = orc.translate_batch(src, tgt, beam_size=k, kv_f16=True)
+        # beam search decodes on f32 K/V, as the reference's Nllb::decode (src/model.rs:195-227)
+        want, _ = orc.translate_batch(src, tgt, beam_size=k, kv_f16=False)
         got = gpu.generate(src, tgt, M.GenOptions(beam_size=k))
         assert got == want
     if k == 1:
@@ -99,7 +103,7 @@ def test_wide_beam_is_exhaustive_search(model_dir, models, preset):
             opts.fused = graph
             got = gpu.generate(WIDE_SOURCES, WIDE_TGT, opts)
             for src, row in zip(WIDE_SOURCES, got):
-                want, gap = exhaustive(orc, src, WIDE_TGT, p)
+                want, gap = exhaustive(orc, src, WIDE_TGT, p, kv_f16=False)  # beam runs on f32 K/V
                 assert gap > 1e-3
                 assert row == want, (src, p, graph)
 
@@ -180,7 +184,8 @@ def test_fused_step_small_batches_tiny(tiny_gguf, models, unfused_models, preset
     src = pipeline_sentences()[:nb]
     want, gap = orc.translate_batch(src, PLT, kv_f16=True)
     assert gpu.generate(src, PLT) == want, f"min gap {gap}"
-    assert gpu.generate(src, PLT, M.GenOptions(fused=False)) == want
+    want32, _ = orc.translate_batch(src, PLT, kv_f16=False)
+    assert gpu.generate(src, PLT, M.GenOptions(fused=False)) == want32  # the generic decoder
     assert unfused_models(tiny_gguf(preset)).generate(src, PLT) == want
     T = 9
     rng = np.random.default_rng(nb)

@@ -45,11 +45,13 @@ def _log_softmax(x: np.ndarray) -> np.ndarray:
     return ((x - m) - np.float32(np.log(s))).astype(np.float32)
 
 
-def exhaustive(orc, src: list[int], tgt: int, p: float):
-    """All hypotheses of at most two steps, scored as translator.rs:284-292.
+def exhaustive(orc, src: list[int], tgt: int, p: float, kv_f16: bool = True):
+    """All hypotheses of at most two steps, scored as translator.rs:284-292, on the
+    oracle's logits with f16 (or, kv_f16=False, f32) K/V.
     Returns (best tokens, score gap between the best and the runner-up)."""
     V, eos, start = WIDE_CONFIG["vocab_size"], WIDE_CONFIG["eos_token_id"], WIDE_CONFIG["decoder_start_token_id"]
-    tf = orc.teacher_forced_logits([src] * V, np.array([[start, tgt, t1] for t1 in range(V)], dtype=np.uint32))
+    tf = orc.teacher_forced_logits([src] * V, np.array([[start, tgt, t1] for t1 in range(V)], dtype=np.uint32),
+                                   kv_f16=kv_f16)
     pen = lambda n: np.float32(max(n, 1)) ** np.float32(p)  # noqa: E731
     lp1 = _log_softmax(tf[0, 1])
     hyps = [(float(np.float32(lp1[eos]) / pen(1)), [])]
