@@ -1157,6 +1157,16 @@ hipError_t logsoftmax_topk_static(const float *logits, int rows, int V, int k, i
                                   hipStream_t st) {
     if (rows < 1 || rows > kStaticTopkRows || logsoftmax_topk_scratch(rows, k) > sizeof(scratch))
         return hipErrorInvalidValue;
+    // the array's address is the current device's: a stream of another device is refused
+    // (the null stream belongs to the current device)
+    if (st) {
+        int cur = 0;
+        hipDevice_t sdev = 0;
+        hipError_t e = hipGetDevice(&cur);
+        if (e == hipSuccess) e = hipStreamGetDevice(st, &sdev);
+        if (e != hipSuccess) return e;
+        if (int(sdev) != cur) return hipErrorInvalidValue;
+    }
     float *work = nullptr;
     const hipError_t e = static_scratch(&work);
     if (e != hipSuccess) return e;

@@ -1096,7 +1096,9 @@ bool parse_usize(const char *s, size_t *out) {
     size_t v = 0;
     for (; *s; ++s) {
         if (*s < '0' || *s > '9') return false;
-        v = v * 10 + size_t(*s - '0');
+        const size_t digit = size_t(*s - '0');
+        if (v > (SIZE_MAX - digit) / 10) return false;  // overflows usize: a parse error
+        v = v * 10 + digit;
     }
     *out = v;
     return true;
@@ -1114,7 +1116,7 @@ bool graph_switch_on(const char *name) {
 GraphCache::GraphCache(Model *m) : model_(m) {
     size_t mb = 512;
     if (!parse_usize(std::getenv("MALAGA_GRAPH_CACHE_MB"), &mb)) mb = 512;
-    max_bytes_ = mb << 20;
+    max_bytes_ = mb << 20;  // graph.rs:185 (the shift drops high bits, as Rust's << does)
     capture_ = graph_switch_on("MALAGA_NO_CUDA_GRAPH") && graph_switch_on("MALAGA_NO_HIP_GRAPH");
 }
 

@@ -53,6 +53,7 @@ def lib() -> C.CDLL:
         L = C.CDLL(str(LIB))
         P = C.c_void_p
         L.orc_last_error.restype = C.c_char_p
+        L.orc_threads.restype, L.orc_threads.argtypes = C.c_int, []
         L.orc_h2f.restype, L.orc_h2f.argtypes = C.c_float, [C.c_uint16]
         L.orc_f2h.restype, L.orc_f2h.argtypes = C.c_uint16, [C.c_float]
         L.orc_dequant.restype, L.orc_dequant.argtypes = C.c_int, [C.c_uint32, P, C.c_int64, P]
@@ -79,6 +80,11 @@ def lib() -> C.CDLL:
 def _err(msg: str):
     e = lib().orc_last_error()
     raise RuntimeError(f"{msg}: {e.decode() if e else ''}")
+
+
+def threads() -> int:
+    """OpenMP threads of the oracle's parallel regions."""
+    return int(lib().orc_threads())
 
 
 def h2f(bits: int) -> float:

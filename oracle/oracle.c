@@ -35,6 +35,7 @@
 #include <sys/mman.h>
 #include <sys/stat.h>
 #include <unistd.h>
+#include <omp.h>
 
 #include "oracle.h"
 
@@ -372,6 +373,8 @@ struct orc_model {
 
 static char g_err[256];
 const char *orc_last_error(void) { return g_err; }
+
+int orc_threads(void) { return omp_get_max_threads(); }
 
 static float *load_tensor(const gguf *g, const char *name, int64_t expect_n, int64_t expect_k) {
     const gg_tensor *t = gguf_tensor(g, name);

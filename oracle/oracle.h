@@ -27,6 +27,8 @@ typedef struct orc_model orc_model;
 typedef struct orc_state orc_state;
 
 const char *orc_last_error(void);
+/* OpenMP threads a parallel region of the oracle uses (omp_get_max_threads). */
+int orc_threads(void);
 float orc_h2f(uint16_t h);
 uint16_t orc_f2h(float f);
 int orc_type_block(uint32_t type, int *block_elems, int *block_bytes);

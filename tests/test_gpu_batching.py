@@ -84,6 +84,22 @@ def test_budget_below_two_graphs_keeps_only_the_current_entry(tiny, mb):
         gpu.close()
 
 
+@pytest.mark.parametrize("value", ["99999999999999999999999", "18446744073709551616", "12x", "-5", ""])
+def test_budget_parse_error_means_512_mb(tiny, value):
+    """src/graph.rs:183: a value Rust's str::parse::<usize> rejects (more than 64 bits, a
+    sign, other characters, empty) falls back to 512 MB, which keeps all three tiny
+    states here; an overflowing number must not wrap to a small budget."""
+    path, orc = tiny
+    gpu = load_with_env(path, MALAGA_GRAPH_CACHE_MB=value)
+    src = pipeline_sentences()
+    try:
+        for batch in (src[:1], src[1:3], src[3:6]):
+            assert gpu.generate(batch, PLT, opts()) == oracle_rows(orc, batch)
+        assert sorted(k[0] for k in gpu.graph_keys()) == [1, 2, 4]
+    finally:
+        gpu.close()
+
+
 @pytest.mark.parametrize("name", ["MALAGA_NO_CUDA_GRAPH", "MALAGA_NO_HIP_GRAPH"])
 def test_graph_switch_names(tiny, name):
     """The reference's MALAGA_NO_CUDA_GRAPH (src/graph.rs:184) and this backend's
