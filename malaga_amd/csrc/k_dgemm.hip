@@ -363,6 +363,295 @@ __global__ __launch_bounds__(NWL * 64) void k_dgemm(DArgs a) {
     }
 }
 
+// ---- decode projections with X resident in LDS (K <= 2048) ----
+// The same products as k_dgemm for K = d_model, laid out the other way round: a workgroup
+// of 8 waves owns one 16-row tile of X and stages it once, normalized (PRO_LN: k_dgemm's
+// statistics order and expression) and split into f16 hi | lo, in LDS (128 KB at K =
+// 2048).  Its NTW = 8 / KS column tiles of W go to the waves, KS waves per tile splitting
+// the K blocks (wave kp takes blocks kp, kp + KS, ...), each wave streaming its W through
+// a two-deep register ring with A fragments read from LDS.  So each X value is read from
+// L2 and converted once per NTW column tiles (k_dgemm: once per 1, 2 or 4), and the first
+// W jobs are requested before the staging, so that their HBM latency overlaps it.  The KS
+// partial tiles of a column tile are added in K-part order through LDS; the sum then goes
+// through the wave's LDS scratch to the row-major lane layout of the epilogues (4 columns
+// of one row per lane: one 16-byte store per split fragment, float4 or f16 x 4 otherwise).
+constexpr int kDrxWaves = 8;
+constexpr int kDrxDepth = 2;               // (tile, K block) jobs of W in flight per wave
+constexpr int kDrxMaxKB = 8;               // K <= 2048
+constexpr int kDrxScr = 16 * 17;           // a wave's 16 x 16 tile, row stride 17
+__host__ __device__ constexpr int drx_xs(int K) { return K + 8; }  // halves per staged row
+
+size_t drx_lds_bytes(int K, bool mins) {
+    return size_t(16) * drx_xs(K) * 2 * sizeof(_Float16) + (mins ? size_t(K / 16) * 16 * sizeof(float) : 0) +
+           size_t(kDrxWaves) * kDrxScr * sizeof(float) + 2 * 16 * sizeof(float);
+}
+
+template <int T, int KB, int KS, int PRO, int EPI, bool TL>
+__global__ __launch_bounds__(kDrxWaves * 64) void k_drx(DArgs a) {
+    using W = MW<T>;
+    using WR = typename W::Regs;
+    constexpr int SK = W::SK, NTW = kDrxWaves / KS, JPW = KB / KS;  // tiles per workgroup, jobs per wave
+    constexpr int K = KB * kStep, XS = drx_xs(K);
+    constexpr int NU = K / 128;  // staged 4-column units per thread (16 rows x K / 4 over 512 threads)
+    static_assert(KB % KS == 0 && KB <= kDrxMaxKB, "K blocks split evenly over the waves of a tile");
+    extern __shared__ __align__(16) unsigned char drx_lds[];
+    _Float16 *xh = reinterpret_cast<_Float16 *>(drx_lds), *xl = xh + 16 * XS;
+    float *xsum = reinterpret_cast<float *>(xl + 16 * XS);  // W::MIN: [K / 16][16] sums of the staged X
+    float *scr = xsum + (W::MIN ? (K / 16) * 16 : 0);       // [waves][kDrxScr]
+    float *lnm = scr + kDrxWaves * kDrxScr, *lnr = lnm + 16;
+    const int t = threadIdx.x, lane = t & 63, ln = lane & 15, kq = lane >> 4;
+    const int wv = __builtin_amdgcn_readfirstlane(t >> 6);
+    const int m0 = blockIdx.y * 16, ntiles = (a.w.N + 15) / 16;
+    const int tile = blockIdx.x * NTW + wv / KS, kp = wv % KS;
+    const bool has_tile = tile < ntiles;  // scalar
+    const int tl = min(tile, ntiles - 1), n0 = tl * 16;
+
+    // 1. the first jobs' W (HBM), requested first
+    WR ring[kDrxDepth];
+#pragma unroll
+    for (int u = 0; u < kDrxDepth; ++u) load_w<T, TL>(a.w, tl, ln, kp + min(u, JPW - 1) * KS, kq, ring[u]);
+    __builtin_amdgcn_sched_barrier(0);
+
+    // 2. epilogue operands of this lane's outputs: row m0 + er, columns n0 + 4 eq .. + 3
+    const int er = lane >> 2, eq = lane & 3, em = min(m0 + er, a.M - 1), en = n0 + 4 * eq;
+    float4 ebias = make_float4(0.f, 0.f, 0.f, 0.f), exold = ebias;
+    uint32_t slot = 0;
+    if (a.bias) ebias = ld4(a.bias, en >> 2);  // kernel argument: uniform
+    if constexpr (EPI == EPI_RESID) exold = reinterpret_cast<const float4 *>(a.xres)[frag_index(em, en, a.w.N)];
+    if constexpr (EPI == EPI_QKV) slot = *a.step;
+
+    // 3. the X tile: unit i of this thread is row m0 + (t & 15), columns 4 cg .. 4 cg + 3 with
+    // cg = t / 16 + 32 i (a wave reads 1 KB of whole lines per load).  PRO_LN: gamma and beta
+    // pass through LDS (the start of the xh area, written only after they are read), so that
+    // only X is held in registers across the load latency.
+    const int xm = t & 15, xmc = min(m0 + xm, a.M - 1);
+    const float4 *xfr = reinterpret_cast<const float4 *>(a.x);
+    float4 xu[NU];
+    double2 sp[KB];
+    float4 gq = make_float4(0.f, 0.f, 0.f, 0.f), bq = gq;
+#pragma unroll
+    for (int i = 0; i < NU; ++i) {
+        const int cg = (t >> 4) + 32 * i;
+        if constexpr (PRO == PRO_RAW) xu[i] = ld4(a.x + size_t(xmc) * a.ldx, cg);
+        else xu[i] = xfr[frag_index(xmc, 4 * cg, K)];
+    }
+    float *gbs = reinterpret_cast<float *>(xh);  // PRO_LN: gamma [K] | beta [K]
+    if constexpr (PRO == PRO_LN) {
+        if (t < K / 4) {  // scalar per wave (K / 4 is a multiple of 64)
+            gq = ld4(a.gamma, t);
+            bq = ld4(a.beta, t);
+        }
+        // statistics partials p = t % 16 + 16 q of row t / 16 (k_dgemm's order); waves 4..7
+        // read row 0's and drop them
+        const int m = wv < 4 ? min(m0 + (t >> 4), a.M - 1) : 0;
+#pragma unroll
+        for (int q = 0; q < KB; ++q)
+            sp[q] = *reinterpret_cast<const double2 *>(a.stats + (size_t(m) * a.P + (t & 15) + q * kLnTPR) * 2);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    if constexpr (PRO == PRO_LN) {
+        if (t < K / 4) {
+            reinterpret_cast<float4 *>(gbs)[t] = gq;
+            reinterpret_cast<float4 *>(gbs + K)[t] = bq;
+        }
+        if (wv < 4) {
+            double s1 = 0.0, s2 = 0.0;
+#pragma unroll
+            for (int q = 0; q < KB; ++q) {
+                s1 += sp[q].x;
+                s2 += sp[q].y;
+            }
+            s1 = group_sum_f64<kLnTPR>(s1);
+            s2 = group_sum_f64<kLnTPR>(s2);
+            if ((t & 15) == 0) {
+                const int ml = t >> 4;
+                const double mu = s1 / K, var = fmax(s2 / K - mu * mu, 0.0);
+                lnm[ml] = m0 + ml < a.M ? float(mu) : 0.f;
+                lnr[ml] = m0 + ml < a.M ? float(1.0 / sqrt(var + double(a.eps))) : 0.f;
+            }
+        }
+        __syncthreads();
+    }
+    {
+        const float mr = PRO == PRO_LN ? lnm[xm] : 0.f, rr = PRO == PRO_LN ? lnr[xm] : 0.f;
+        uint4 hl[NU];  // [hi0..hi3 | lo0..lo3] of each unit
+        float sums[NU];
+#pragma unroll
+        for (int i = 0; i < NU; ++i) {
+            const int cg = (t >> 4) + 32 * i;
+            h4_t hv, lv;
+            float sum = 0.f;
+            if constexpr (PRO == PRO_SPLIT) {
+                const uint4 u = __builtin_bit_cast(uint4, xu[i]);
+                hv = __builtin_bit_cast(h4_t, make_uint2(u.x, u.y));
+                lv = __builtin_bit_cast(h4_t, make_uint2(u.z, u.w));
+#pragma unroll
+                for (int j = 0; j < 4; ++j) sum += float(hv[j]) + float(lv[j]);
+            } else {
+                float v[4] = {xu[i].x, xu[i].y, xu[i].z, xu[i].w};
+                if constexpr (PRO == PRO_LN) {
+                    const float4 g = reinterpret_cast<const float4 *>(gbs)[cg], b = reinterpret_cast<const float4 *>(gbs + K)[cg];
+                    v[0] = (v[0] - mr) * rr * g.x + b.x;
+                    v[1] = (v[1] - mr) * rr * g.y + b.y;
+                    v[2] = (v[2] - mr) * rr * g.z + b.z;
+                    v[3] = (v[3] - mr) * rr * g.w + b.w;
+                }
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    hv[j] = _Float16(v[j]);
+                    lv[j] = _Float16(v[j] - float(hv[j]));
+                }
+                sum = (v[0] + v[1]) + (v[2] + v[3]);
+            }
+            const uint2 hb = __builtin_bit_cast(uint2, hv), lb = __builtin_bit_cast(uint2, lv);
+            hl[i] = make_uint4(hb.x, hb.y, lb.x, lb.y);
+            sums[i] = sum;
+        }
+        if constexpr (PRO == PRO_LN) __syncthreads();  // every read of gamma / beta is done
+#pragma unroll
+        for (int i = 0; i < NU; ++i) {
+            const int cg = (t >> 4) + 32 * i;
+            *reinterpret_cast<uint2 *>(xh + xm * XS + 4 * cg) = make_uint2(hl[i].x, hl[i].y);
+            *reinterpret_cast<uint2 *>(xl + xm * XS + 4 * cg) = make_uint2(hl[i].z, hl[i].w);
+            if constexpr (W::MIN) {
+                // the 16 columns of chunk cg / 4 are in lanes xm, xm + 16, xm + 32, xm + 48
+                float sum = sums[i];
+                sum += __shfl_xor(sum, 16);
+                sum += __shfl_xor(sum, 32);
+                if (lane < 16) xsum[(cg >> 2) * 16 + xm] = sum;
+            }
+        }
+    }
+    __syncthreads();
+
+    // 4. the jobs: K blocks kp + j KS of this wave's tile
+    f4_t acc = f4_t{0.f, 0.f, 0.f, 0.f};
+    auto job = [&](int kb, const WR &cur) {
+#pragma unroll
+        for (int s = 0; s < W::SLICES; ++s) {
+            float sc, mn;
+            W::scale(cur, s, sc, mn);
+            const auto bop = W::b(cur, s);
+            const int kx = kb * kStep + s * SK, xo = ln * XS + kx + kq * (SK / 4);
+            f4_t tmp = f4_t{0.f, 0.f, 0.f, 0.f};
+            if constexpr (SK == 32) {
+                const h8_t ah = *reinterpret_cast<const h8_t *>(xh + xo), al = *reinterpret_cast<const h8_t *>(xl + xo);
+                tmp = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bop, tmp, 0, 0, 0);
+                tmp = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, bop, tmp, 0, 0, 0);
+            } else {
+                const h4_t ah = *reinterpret_cast<const h4_t *>(xh + xo), al = *reinterpret_cast<const h4_t *>(xl + xo);
+                tmp = __builtin_amdgcn_mfma_f32_16x16x16f16(ah, bop, tmp, 0, 0, 0);
+                tmp = __builtin_amdgcn_mfma_f32_16x16x16f16(al, bop, tmp, 0, 0, 0);
+            }
+            if constexpr (W::MIN) {
+                const float *xsp = xsum + (kx >> 4) * 16 + 4 * kq;
+                const float4 x0 = *reinterpret_cast<const float4 *>(xsp), x1 = *reinterpret_cast<const float4 *>(xsp + 16);
+                const float xs[4] = {x0.x + x1.x, x0.y + x1.y, x0.z + x1.z, x0.w + x1.w};
+#pragma unroll
+                for (int r = 0; r < 4; ++r) acc[r] = fmaf(sc, tmp[r], fmaf(-mn, xs[r], acc[r]));
+            } else {
+#pragma unroll
+                for (int r = 0; r < 4; ++r) acc[r] = fmaf(sc, tmp[r], acc[r]);
+            }
+        }
+    };
+    if (has_tile) {  // scalar
+        static_for<0, JPW>([&](auto jc) {
+            constexpr int j = decltype(jc)::value;
+            job(kp + j * KS, ring[j % kDrxDepth]);
+            if constexpr (j + kDrxDepth < JPW) {
+                __builtin_amdgcn_sched_barrier(0);
+                load_w<T, TL>(a.w, tl, ln, kp + (j + kDrxDepth) * KS, kq, ring[j % kDrxDepth]);
+                __builtin_amdgcn_sched_barrier(0);
+            }
+        });
+    }
+
+    // 5. the tile's sum (K parts in order), moved to 4 columns of one row per lane
+    float *my = scr + wv * kDrxScr;
+    if constexpr (KS > 1) {
+        *reinterpret_cast<f4_t *>(my + 4 * lane) = acc;
+        __syncthreads();
+        if (kp != 0 || !has_tile) return;  // scalar; no barrier below
+#pragma unroll
+        for (int k = 1; k < KS; ++k) {
+            const f4_t o = *reinterpret_cast<const f4_t *>(scr + (wv + k) * kDrxScr + 4 * lane);
+#pragma unroll
+            for (int r = 0; r < 4; ++r) acc[r] += o[r];
+        }
+        __builtin_amdgcn_s_waitcnt(0xc07f);  // this wave's reads of its own slot are done
+    } else {
+        if (!has_tile) return;
+    }
+#pragma unroll
+    for (int r = 0; r < 4; ++r) my[(4 * kq + r) * 17 + ln] = acc[r];
+    __builtin_amdgcn_s_waitcnt(0xc07f);
+    __builtin_amdgcn_wave_barrier();
+    float v[4];
+#pragma unroll
+    for (int c = 0; c < 4; ++c) v[c] = my[er * 17 + 4 * eq + c];
+    const int om = m0 + er;
+    if (om >= a.M || en >= a.w.N) return;
+    const float bv[4] = {ebias.x, ebias.y, ebias.z, ebias.w};
+#pragma unroll
+    for (int c = 0; c < 4; ++c) v[c] += bv[c];
+
+    // 6. epilogues
+    if constexpr (EPI == EPI_STORE) {
+        if (a.relu) {  // kernel argument
+#pragma unroll
+            for (int c = 0; c < 4; ++c) v[c] = fmaxf(v[c], 0.f);
+        }
+        if (a.frag_out) {
+            h4_t hv, lv;
+#pragma unroll
+            for (int c = 0; c < 4; ++c) {
+                hv[c] = _Float16(v[c]);
+                lv[c] = _Float16(v[c] - float(hv[c]));
+            }
+            const uint2 hb = __builtin_bit_cast(uint2, hv), lb = __builtin_bit_cast(uint2, lv);
+            reinterpret_cast<uint4 *>(a.y)[frag_index(om, en, a.w.N)] = make_uint4(hb.x, hb.y, lb.x, lb.y);
+        } else {
+            *reinterpret_cast<float4 *>(a.y + size_t(om) * a.ldy + en) = make_float4(v[0], v[1], v[2], v[3]);
+        }
+    } else if constexpr (EPI == EPI_RESID) {
+        const float xo[4] = {exold.x, exold.y, exold.z, exold.w};
+        float xn[4];
+        double s1 = 0.0, s2 = 0.0;
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+            xn[c] = xo[c] + v[c];
+            s1 += double(xn[c]);
+            s2 += double(xn[c]) * double(xn[c]);
+        }
+        reinterpret_cast<float4 *>(a.xres)[frag_index(om, en, a.w.N)] = make_float4(xn[0], xn[1], xn[2], xn[3]);
+        // the row's 16 columns are in lanes 4 er .. 4 er + 3
+        s1 = group_sum_f64<4>(s1);
+        s2 = group_sum_f64<4>(s2);
+        if (eq == 0) {
+            double *sp_out = a.stats_out + (size_t(om) * (a.w.N >> 4) + (en >> 4)) * 2;
+            sp_out[0] = s1;
+            sp_out[1] = s2;
+        }
+    } else {  // EPI_QKV: q f32; K / V into the caches at the step's slot (f16, or f32 with kc32)
+        const int d = a.H * a.hd;
+        if (en < d) {
+            *reinterpret_cast<float4 *>(a.q + size_t(om) * d + en) = make_float4(v[0], v[1], v[2], v[3]);
+        } else {
+            const int cc = en < 2 * d ? en - d : en - 2 * d;
+            const size_t off = ((size_t(om) * a.H + cc / a.hd) * a.slots + slot) * a.hd + cc % a.hd;
+            if (a.kc32) {  // kernel argument
+                *reinterpret_cast<float4 *>((en < 2 * d ? a.kc32 : a.vc32) + off) = make_float4(v[0], v[1], v[2], v[3]);
+            } else {
+                h4_t hv;
+#pragma unroll
+                for (int c = 0; c < 4; ++c) hv[c] = _Float16(v[c]);
+                *reinterpret_cast<h4_t *>((en < 2 * d ? a.kc : a.vc) + off) = hv;
+            }
+        }
+    }
+}
+
 // ---- the cross attention of a decode step in one launch ----
 // crates/malaga-core/src/model.rs:573-578: q = cross_q(cross_norm(x)), then the cross
 // attention of q over the source keys.  Workgroup (h, g), 8 waves, owns the RG = 8 / S
@@ -662,18 +951,25 @@ inline int dg_bpw(int nblk) {
 
 // Two column tiles per workgroup where one tile each would take 1.5 workgroups per CU or
 // more: the normalized, split X then feeds both (at 32 rows: QKV 7.7 us instead of 9.3,
-// FFN-up 7.4 instead of 9.3).
+// FFN-up 7.4 instead of 9.3).  Four where one each would take six per CU (the 3.3B
+// model's QKV and FFN-up at 64 rows): every workgroup reads its 16 rows of X once for
+// 64 columns.
 constexpr int kDgWideGrid = 384;
+constexpr int kDgWiderGrid = 1536;
 
 template <int T, int BPW, int PRO, int EPI, bool TL>
 hipError_t launch_dgemm_l(const DArgs &a, hipStream_t st) {
     const unsigned gy = unsigned((a.M + 15) / 16), block = unsigned(dg_waves(a.w.K / kStep) * 64);
     const unsigned tiles1 = unsigned((a.w.N + 15) / 16);
-    if constexpr (EPI != EPI_RESID) {  // the residual projections are N = d_model wide
-        if (tiles1 * gy >= unsigned(kDgWideGrid)) {
-            hipLaunchKernelGGL((k_dgemm<T, BPW, 2, PRO, EPI, TL>), dim3((a.w.N + 31) / 32, gy), dim3(block), 0, st, a);
+    if constexpr (EPI != EPI_RESID && BPW == 1) {
+        if (tiles1 * gy >= unsigned(kDgWiderGrid)) {
+            hipLaunchKernelGGL((k_dgemm<T, BPW, 4, PRO, EPI, TL>), dim3((a.w.N + 63) / 64, gy), dim3(block), 0, st, a);
             return hipGetLastError();
         }
+    }
+    if (tiles1 * gy >= unsigned(kDgWideGrid)) {
+        hipLaunchKernelGGL((k_dgemm<T, BPW, 2, PRO, EPI, TL>), dim3((a.w.N + 31) / 32, gy), dim3(block), 0, st, a);
+        return hipGetLastError();
     }
     hipLaunchKernelGGL((k_dgemm<T, BPW, 1, PRO, EPI, TL>), dim3(tiles1, gy), dim3(block), 0, st, a);
     return hipGetLastError();
@@ -722,6 +1018,39 @@ hipError_t launch_dgemm_m(const DArgs &a, hipStream_t st) {
     return launch_dgemm<T, 1, PRO, EPI>(a, st);
 }
 
+// Resident-X launches (k_drx): q4_K / q6_K with their tile-major copies, K = 2048 (the 3.3B
+// model's d_model), N a multiple of 16, and enough column tiles for 128 workgroups of 8
+// tiles (QKV and FFN-up at 64 rows).  Measured against k_dgemm (rocprofv3, same box):
+// at K = 2048 and 64 rows QKV 24.1 -> 16.9 us and FFN-up 24.3 -> 17.4 us, but the d-wide
+// projections (N = 2048, two waves per tile) 6.7 -> 11.0 us and 9.4 -> 12.7 us; at K = 1024
+// and 32 rows no projection gained (FFN-up 7.4 -> 8.6 us): staging 16 rows of X costs
+// more than it saves when a workgroup feeds it to few columns.
+constexpr int kDrxMinGrid = 128;
+
+bool drx_ok(const DevMatrix &w, int M) {
+    const int gx = (w.N / 16 + kDrxWaves - 1) / kDrxWaves, gy = (M + 15) / 16;
+    return (w.type == GGML_Q4_K || w.type == GGML_Q6_K) && w.tm && w.K == 2048 && w.N % 16 == 0 && M >= 1 &&
+           M <= kDgemmMaxRows && gx * gy >= kDrxMinGrid;
+}
+
+template <int T, int KB, int KS, int PRO, int EPI>
+hipError_t launch_drx_k(const DArgs &a, hipStream_t st) {
+    const size_t lds = drx_lds_bytes(KB * kStep, MW<T>::MIN);
+    static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void *>(&k_drx<T, KB, KS, PRO, EPI, true>),
+                                                       hipFuncAttributeMaxDynamicSharedMemorySize, int(lds));
+    if (attr != hipSuccess) return attr;
+    constexpr int ntw = kDrxWaves / KS;
+    const dim3 grid(unsigned((a.w.N / 16 + ntw - 1) / ntw), unsigned((a.M + 15) / 16));
+    hipLaunchKernelGGL((k_drx<T, KB, KS, PRO, EPI, true>), grid, dim3(kDrxWaves * 64), lds, st, a);
+    return hipGetLastError();
+}
+
+template <int PRO, int EPI>
+hipError_t launch_drx(const DevMatrix &w, const DArgs &a, hipStream_t st) {
+    if (w.type == GGML_Q4_K) return launch_drx_k<GGML_Q4_K, 8, 1, PRO, EPI>(a, st);
+    return launch_drx_k<GGML_Q6_K, 8, 1, PRO, EPI>(a, st);
+}
+
 template <int PRO, int EPI>
 hipError_t launch_dgemm_t(const DevMatrix &w, const DArgs &a, hipStream_t st) {
     switch (w.type) {
@@ -765,7 +1094,7 @@ bool dgemm_supported(const DevMatrix &w, int M) {
 }
 
 hipError_t dgemm_store(const DevMatrix &w, const float *x, int ldx, int M, const DgemmLn *ln, const float *bias,
-                       bool relu, float *y, int ldy, hipStream_t st, bool y_split) {
+                       bool relu, float *y, int ldy, hipStream_t st, bool y_split, bool resident) {
     if (!dgemm_args_ok(w, x, ldx, M, ln) || !y || ldy < w.N) return hipErrorInvalidValue;
     // split fragments: 16-byte aligned, whole slices of 16 columns
     if (y_split && (w.N % 16 || reinterpret_cast<uintptr_t>(y) % 16)) return hipErrorInvalidValue;
@@ -774,6 +1103,9 @@ hipError_t dgemm_store(const DevMatrix &w, const float *x, int ldx, int M, const
     a.frag_out = y_split ? 1 : 0;
     a.ldy = ldy;
     a.relu = relu ? 1 : 0;
+    // row-major stores of 4 columns need 16-byte rows
+    if (resident && ln && drx_ok(w, M) && (y_split || (ldy % 4 == 0 && reinterpret_cast<uintptr_t>(y) % 16 == 0)))
+        return launch_drx<PRO_LN, EPI_STORE>(w, a, st);
     return ln ? launch_dgemm_t<PRO_LN, EPI_STORE>(w, a, st) : launch_dgemm_t<PRO_RAW, EPI_STORE>(w, a, st);
 }
 
@@ -783,6 +1115,7 @@ hipError_t dgemm_resid(const DevMatrix &w, const float *x, int ldx, int M, const
     DArgs a = dargs(w, x, ldx, M, nullptr, bias);
     a.xres = xres;
     a.stats_out = stats_out;
+    if (x_split && drx_ok(w, M)) return launch_drx<PRO_SPLIT, EPI_RESID>(w, a, st);
     if (x_split) return launch_dgemm_t<PRO_SPLIT, EPI_RESID>(w, a, st);
     return launch_dgemm_t<PRO_RAW, EPI_RESID>(w, a, st);
 }
@@ -805,6 +1138,9 @@ hipError_t dgemm_qkv_any(const DevMatrix &w, const float *x, int ldx, int M, con
     a.hd = hd;
     a.slots = slots;
     a.step = step;
+    // the resident-X kernel stores 4 columns per lane: heads of 4 k, rows of 16 bytes
+    if (drx_ok(w, M) && hd % 4 == 0 && (ln || (ldx % 4 == 0 && reinterpret_cast<uintptr_t>(x) % 16 == 0)))
+        return ln ? launch_drx<PRO_LN, EPI_QKV>(w, a, st) : launch_drx<PRO_RAW, EPI_QKV>(w, a, st);
     return ln ? launch_dgemm_t<PRO_LN, EPI_QKV>(w, a, st) : launch_dgemm_t<PRO_RAW, EPI_QKV>(w, a, st);
 }
 }  // namespace

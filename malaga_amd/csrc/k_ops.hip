@@ -196,16 +196,19 @@ __global__ __launch_bounds__(256) void k_split_qkv8(const float *qkv, int b, int
     store_kv8(vc + slot, r + 2 * d);
 }
 
-// Encoder attention: one wave per (sentence i, query t, head h).
-__global__ __launch_bounds__(64) void k_attn_prefill(const float *qkv, int s, int H, int hd, const uint32_t *lens,
-                                                     float *out) {
+// Encoder attention over the packed rows (padding positions have no row): one wave per
+// (row p, head h); row p is a position of sentence i = rsent[p], whose keys and values are
+// the rows soff[i] .. soff[i] + lens[i] - 1 (src/model.rs:101-109 with the padding mask).
+__global__ __launch_bounds__(64) void k_attn_prefill(const float *qkv, int H, int hd, const uint32_t *soff,
+                                                     const uint32_t *rsent, const uint32_t *lens, float *out) {
     extern __shared__ float sc[];
-    const int id = blockIdx.x, hh = id % H, t = (id / H) % s, i = id / (H * s);
-    const int d = H * hd, n = int(lens[i]);
-    const float *qr = qkv + (size_t(i) * s + t) * 3 * d + hh * hd;
+    const int id = blockIdx.x, hh = id % H, p = id / H;
+    const int i = int(rsent[p]), r0 = int(soff[i]), n = int(lens[i]);
+    const int d = H * hd;
+    const float *qr = qkv + size_t(p) * 3 * d + hh * hd;
     float mx = -INFINITY;
     for (int j = threadIdx.x; j < n; j += 64) {
-        const float *kr = qkv + (size_t(i) * s + j) * 3 * d + d + hh * hd;
+        const float *kr = qkv + size_t(r0 + j) * 3 * d + d + hh * hd;
         float acc = 0.f;
         for (int e = 0; e < hd; e += 4) {
             const float4 a = *reinterpret_cast<const float4 *>(qr + e), b = *reinterpret_cast<const float4 *>(kr + e);
@@ -229,22 +232,27 @@ __global__ __launch_bounds__(64) void k_attn_prefill(const float *qkv, int s, in
     const float inv = 1.f / sum;
     for (int e = threadIdx.x; e < hd; e += 64) {
         float a = 0.f;
-        for (int j = 0; j < n; ++j) a = fmaf(sc[j], qkv[(size_t(i) * s + j) * 3 * d + 2 * d + hh * hd + e], a);
-        out[(size_t(i) * s + t) * d + hh * hd + e] = a * inv;
+        for (int j = 0; j < n; ++j) a = fmaf(sc[j], qkv[size_t(r0 + j) * 3 * d + 2 * d + hh * hd + e], a);
+        out[size_t(p) * d + hh * hd + e] = a * inv;
     }
 }
 
-__global__ void k_split_cross_kv(const float *kv, int b, int s, int H, int hd, int L, float *K0, size_t kv_elems) {
+// The stacked cross K/V projection of the packed rows, kv [Mp][L][2d] (k | v per layer), to
+// the batch's per-layer [b][H][s][hd] blocks: packed row p is position prow[p] % s of
+// sentence prow[p] / s.
+__global__ void k_split_cross_kv(const float *kv, int Mp, const uint32_t *prow, int s, int H, int hd, int L,
+                                 float *K0, size_t kv_elems) {
     const int d = H * hd;
-    const size_t total = size_t(b) * s * L * d;
+    const size_t total = size_t(Mp) * L * d;
     for (size_t idx = blockIdx.x * size_t(blockDim.x) + threadIdx.x; idx < total; idx += size_t(gridDim.x) * blockDim.x) {
         const int c = int(idx % d);
-        const size_t rest = idx / d, tok = rest / L;
+        const size_t rest = idx / d, p = rest / L;
         const int l = int(rest % L);
-        const int j = int(tok % s), i = int(tok / s), hh = c / hd, e = c % hd;
+        const uint32_t pr = prow[p];
+        const int j = int(pr % uint32_t(s)), i = int(pr / uint32_t(s)), hh = c / hd, e = c % hd;
         const size_t dst = ((size_t(i) * H + hh) * s + j) * hd + e;
         float *K = K0 + 2 * size_t(l) * kv_elems;
-        const float *src = kv + (tok * L + l) * 2 * d;
+        const float *src = kv + (p * L + l) * 2 * d;
         K[dst] = src[c];
         K[kv_elems + dst] = src[d + c];
     }
@@ -1048,18 +1056,21 @@ hipError_t attn_decode(const float *q, const float *K, const float *V, int b, in
     return attn_decode_t(q, K, V, b, H, hd, L, lens, step, out, st, rows, out_split);
 }
 
-hipError_t attn_prefill(const float *qkv, int b, int s, int H, int hd, const uint32_t *lens, float *out,
-                        hipStream_t st) {
+hipError_t attn_prefill(const float *qkv, int Mp, int H, int hd, const uint32_t *soff, const uint32_t *rsent,
+                        const uint32_t *lens, int max_len, float *out, hipStream_t st) {
     if (hd % 4) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(k_attn_prefill, dim3(b * s * H), dim3(64), sizeof(float) * s, st, qkv, s, H, hd, lens, out);
+    if (Mp <= 0) return hipSuccess;
+    hipLaunchKernelGGL(k_attn_prefill, dim3(unsigned(Mp) * unsigned(H)), dim3(64), sizeof(float) * max_len, st, qkv, H,
+                       hd, soff, rsent, lens, out);
     return hipGetLastError();
 }
 
-hipError_t split_cross_kv(const float *kv, int b, int s, int H, int hd, int L, float *K0, size_t kv_elems,
-                          hipStream_t st) {
-    const size_t n = size_t(b) * s * H * hd * L;
+hipError_t split_cross_kv(const float *kv, int Mp, const uint32_t *prow, int s, int H, int hd, int L, float *K0,
+                          size_t kv_elems, hipStream_t st) {
+    const size_t n = size_t(Mp) * H * hd * L;
     if (!n) return hipSuccess;
-    hipLaunchKernelGGL(k_split_cross_kv, dim3(grid_1d(n, 256)), dim3(256), 0, st, kv, b, s, H, hd, L, K0, kv_elems);
+    hipLaunchKernelGGL(k_split_cross_kv, dim3(grid_1d(n, 256)), dim3(256), 0, st, kv, Mp, prow, s, H, hd, L, K0,
+                       kv_elems);
     return hipGetLastError();
 }
 

@@ -116,8 +116,10 @@ bool dgemm_supported(const DevMatrix &w, int M);
 // y[m][n] = (LN(x) or x)[m] . W[n] + bias[n], ReLU optional.  y_split: y is written as
 // split fragments (frag_index, device.hpp), the A-operand form of the decode GEMMs; it
 // then holds (M padded to 16) x N floats.
+// resident: the LayerNorm projections of K = 1024 / 2048 may run the resident-X kernel
+// (k_drx); false keeps k_dgemm's sums (the cross q whose fused launch k_dxattn must equal).
 hipError_t dgemm_store(const DevMatrix &w, const float *x, int ldx, int M, const DgemmLn *ln, const float *bias,
-                       bool relu, float *y, int ldy, hipStream_t st, bool y_split = false);
+                       bool relu, float *y, int ldy, hipStream_t st, bool y_split = false, bool resident = true);
 // xres[m][n] += x[m] . W[n] + bias[n] in place (xres: the residual stream, (M padded to
 // 16) x N floats in fragment order), and stats_out [M][N / 16][2] of the new rows.
 // x_split: x holds split fragments (else row-major f32 rows of ldx).
@@ -215,14 +217,16 @@ hipError_t attn_decode(const float *q, const float *K, const float *V, int b, in
 // rows (optional, [b][L]): cache row holding slot j of row b (beam reordering without copies).
 // out_split: out is written as split fragments (frag_index, device.hpp), the input form
 // of the decode GEMMs; out then holds (b padded to 16) x H*hd floats.
-// Encoder self-attention over f32 qkv [b*s][3d] (rows of sentence i are i*s..),
-// key j of row i valid iff j < lens[i].  out [b*s][d].
-hipError_t attn_prefill(const float *qkv, int b, int s, int H, int hd, const uint32_t *lens, float *out,
-                        hipStream_t st);
-// kv [b*s][L][2d] f32 (the stacked cross K/V projection of L layers) -> f32 [b][H][s][hd]:
-// layer l's K at K0 + 2 l kv_elems, its V at K + kv_elems (kv_elems = b*s*d)
-hipError_t split_cross_kv(const float *kv, int b, int s, int H, int hd, int L, float *K0, size_t kv_elems,
-                          hipStream_t st);
+// Encoder self-attention over the packed rows (no padding rows): qkv [Mp][3d], row p a
+// position of sentence rsent[p], whose keys are rows soff[i] .. soff[i] + lens[i] - 1;
+// max_len >= every lens[i].  out [Mp][d].
+hipError_t attn_prefill(const float *qkv, int Mp, int H, int hd, const uint32_t *soff, const uint32_t *rsent,
+                        const uint32_t *lens, int max_len, float *out, hipStream_t st);
+// kv [Mp][L][2d] f32 (the stacked cross K/V projection of L layers over the packed rows) ->
+// f32 [b][H][s][hd]: packed row p is position prow[p] % s of sentence prow[p] / s; layer
+// l's K at K0 + 2 l kv_elems, its V at K + kv_elems (kv_elems = b*s*d)
+hipError_t split_cross_kv(const float *kv, int Mp, const uint32_t *prow, int s, int H, int hd, int L, float *K0,
+                          size_t kv_elems, hipStream_t st);
 // rows [r0, r0 + n) of w as a matrix of their own (block-major planes; no lane-major copy)
 DevMatrix rows_view(const DevMatrix &w, int r0, int n);
 // For each of `pairs` arrays (every layer's cross K and V): dst0 + p * dst_pair

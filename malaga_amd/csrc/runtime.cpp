@@ -594,19 +594,32 @@ std::unique_ptr<Batch> Model::encode(const std::vector<std::vector<uint32_t>> &s
     for (auto &r : src) s = std::max(s, int(r.size()));
     if (b == 0 || s == 0) fail(ERR_INVALID, "empty batch");
     if (s > cfg.max_position_embeddings) fail(ERR_INVALID, "source longer than the position table");
-    const int d = cfg.d_model, M = b * s, H = cfg.encoder_heads, hd = d / H, f = cfg.encoder_ffn;
+    const int d = cfg.d_model, H = cfg.encoder_heads, hd = d / H, f = cfg.encoder_ffn;
     const uint32_t pad = uint32_t(cfg.pad_token_id);
-    std::vector<uint32_t> ids(static_cast<size_t>(M), pad), pidx(size_t(M), pad);
+    // Every encoder operation but the attention is row-wise, so the encoder runs on the
+    // packed tokens only (M rows, sentence i at rows soff[i] ..): src/model.rs:480-500 pads
+    // the batch to [b, s] and masks the padding in the attention, which computes the same
+    // rows.  The batch keeps the [b][s] ids and the [b][H][s][hd] cross K/V of the padded
+    // layout (padding positions zero), which the decode state reads.
+    std::vector<uint32_t> ids(size_t(b) * s, pad), pids, pidx, soff, rsent, prow;
     out->b = b;
     out->s = s;
     for (int i = 0; i < b; ++i) {
+        // a row without tokens would attend over nothing (NaN in src/model.rs:101-109)
+        if (src[i].empty()) fail(ERR_INVALID, "empty source row");
         out->lens.push_back(uint32_t(src[i].size()));
+        soff.push_back(uint32_t(pids.size()));
         for (int j = 0; j < int(src[i].size()); ++j) {
             if (src[i][j] >= uint32_t(cfg.vocab_size)) fail(ERR_INVALID, "token id out of range");
             ids[size_t(i) * s + j] = src[i][j];
-            pidx[size_t(i) * s + j] = uint32_t(j) + pad + 1;
+            pids.push_back(src[i][j]);
+            pidx.push_back(uint32_t(j) + pad + 1);
+            rsent.push_back(uint32_t(i));
+            prow.push_back(uint32_t(i * s + j));
         }
     }
+    const int M = int(pids.size());
+    if (M == 0) fail(ERR_INVALID, "empty batch");
     // scratch: carved from the model's grow-only encoder workspace (256-byte aligned)
     const size_t n_ids = (size_t(M) * 4 + 255) & ~size_t(255), n_lens = (size_t(b) * 4 + 255) & ~size_t(255);
     const size_t n_act = (size_t(M) * d * 4 + 255) & ~size_t(255);
@@ -621,7 +634,7 @@ std::unique_ptr<Batch> Model::encode(const std::vector<std::vector<uint32_t>> &s
     const size_t n_kv = (size_t(M) * 2 * d * 4 * per_layer + 255) & ~size_t(255);
     // lazy embeddings: the batch's token_embd rows, gathered on the host (src/model.rs:269-273)
     const size_t n_rows = embed.q ? 0 : (planes_bytes(embed.type, M, d) + 255) & ~size_t(255);
-    const size_t need = 2 * n_ids + n_lens + 3 * n_act + n_qkv + n_kv + n_rows;
+    const size_t need = 4 * n_ids + 2 * n_lens + 3 * n_act + n_qkv + n_kv + n_rows;
     if (enc_ws_bytes_ < need) {
         check_hip(hipStreamSynchronize(st), "encode");  // a previous call may still use it
         dev_free(enc_ws_);
@@ -637,20 +650,24 @@ std::unique_ptr<Batch> Model::encode(const std::vector<std::vector<uint32_t>> &s
         return p;
     };
     uint32_t *d_ids = static_cast<uint32_t *>(carve(n_ids)), *d_pidx = static_cast<uint32_t *>(carve(n_ids));
-    uint32_t *d_lens = static_cast<uint32_t *>(carve(n_lens));
+    uint32_t *d_rsent = static_cast<uint32_t *>(carve(n_ids)), *d_prow = static_cast<uint32_t *>(carve(n_ids));
+    uint32_t *d_lens = static_cast<uint32_t *>(carve(n_lens)), *d_soff = static_cast<uint32_t *>(carve(n_lens));
     float *x = static_cast<float *>(carve(n_act)), *h = static_cast<float *>(carve(n_act));
     float *att = static_cast<float *>(carve(n_act));
     float *qkv = static_cast<float *>(carve(n_qkv));
     float *kv = static_cast<float *>(carve(n_kv));
     Staging &up = ctx->staging;
     up.upload(d_pidx, pidx.data(), pidx.size() * 4, st);
+    up.upload(d_rsent, rsent.data(), rsent.size() * 4, st);
+    up.upload(d_prow, prow.data(), prow.size() * 4, st);
+    up.upload(d_soff, soff.data(), soff.size() * 4, st);
     out->ids = ids;
     up.upload(d_lens, out->lens.data(), out->lens.size() * 4, st);
     if (embed.q) {
-        up.upload(d_ids, ids.data(), ids.size() * 4, st);
+        up.upload(d_ids, pids.data(), pids.size() * 4, st);
         check_hip(embed_pos_rows(embed, d_ids, d_pidx, M, pos, embed_scale, x, st), "embed");
     } else {
-        const DevMatrix rows = gather_embed(ids.data(), M, static_cast<uint8_t *>(carve(n_rows)));
+        const DevMatrix rows = gather_embed(pids.data(), M, static_cast<uint8_t *>(carve(n_rows)));
         std::vector<uint32_t> iota(static_cast<size_t>(M));
         std::iota(iota.begin(), iota.end(), 0u);
         up.upload(d_ids, iota.data(), iota.size() * 4, st);
@@ -664,7 +681,7 @@ std::unique_ptr<Batch> Model::encode(const std::vector<std::vector<uint32_t>> &s
         const EncLayer &l = enc[li];
         const LNorm &next = li + 1 < enc.size() ? enc[li + 1].attn_norm : enc_norm;
         matmul(l.qkv, h, M, qkv, false, nullptr);
-        check_hip(attn_prefill(qkv, b, s, H, hd, d_lens, att, st), "attn_prefill");
+        check_hip(attn_prefill(qkv, M, H, hd, d_soff, d_rsent, d_lens, s, att, st), "attn_prefill");
         check_hip(gemm_residual_ln(l.out.w, att, d, M, l.out.b, x, l.ffn_norm.g, l.ffn_norm.b, kLnEps, h, st,
                                    ctx->gemm_workspace(), kGemmWorkspaceBytes),
                   "gemm_residual_ln");
@@ -674,9 +691,11 @@ std::unique_ptr<Batch> Model::encode(const std::vector<std::vector<uint32_t>> &s
                   "gemm_residual_ln");
     }
     const int Hd = cfg.decoder_heads, hdd = d / Hd;
-    const size_t kv_elems = size_t(M) * d;
+    const size_t kv_elems = size_t(b) * s * d;
     out->block = dev_alloc(std::max<size_t>(dec.size(), 1) * 2 * kv_elems * 4, "cross K/V");
     float *K0 = static_cast<float *>(out->block);
+    if (M < b * s)  // padding positions: zero (never attended, but copied into decode states)
+        check_hip(hipMemsetAsync(K0, 0, std::max<size_t>(dec.size(), 1) * 2 * kv_elems * 4, st), "memset");
     for (int i = 0; i < L; ++i) {
         out->ck.push_back(K0 + 2 * size_t(i) * kv_elems);
         out->cv.push_back(K0 + (2 * size_t(i) + 1) * kv_elems);
@@ -685,7 +704,7 @@ std::unique_ptr<Batch> Model::encode(const std::vector<std::vector<uint32_t>> &s
         const int nl = std::min(per_layer, L - l0);
         const Linear part{rows_view(cross_kv.w, l0 * 2 * d, nl * 2 * d), cross_kv.b + size_t(l0) * 2 * d};
         matmul(part, h, M, kv, false, nullptr);
-        check_hip(split_cross_kv(kv, b, s, Hd, hdd, nl, K0 + 2 * size_t(l0) * kv_elems, kv_elems, st),
+        check_hip(split_cross_kv(kv, M, d_prow, s, Hd, hdd, nl, K0 + 2 * size_t(l0) * kv_elems, kv_elems, st),
                   "split_cross_kv");
     }
     // no wait: the batch's users run on the same stream
@@ -1069,7 +1088,10 @@ void Model::step_dgemm(StaticState &st, bool greedy_mode, int mask_id) {
                 }
             }
             if (!fused_cross) {
-                check_hip(dgemm_store(l.cross_q.w, st.x, d, B, &ln_cross, l.cross_q.b, false, st.q, d, s),
+                // where the one-launch cross attention exists, its q is k_dgemm's bit for bit:
+                // the two-launch form keeps k_dgemm too, so that both give the same logits
+                check_hip(dgemm_store(l.cross_q.w, st.x, d, B, &ln_cross, l.cross_q.b, false, st.q, d, s, false,
+                                      !dgemm_cross_attn_supported(l.cross_q.w, B, H, hd)),
                           "dgemm_cross_q");
                 check_hip(attn_decode(st.q, ck, cv, B, H, hd, st.s, st.lens, nullptr, st.att, s, nullptr, true),
                           "attn");
