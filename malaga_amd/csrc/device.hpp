@@ -327,6 +327,20 @@ __device__ __forceinline__ float block_max(float v, float *sh) {
     return t;
 }
 
+// 6-bit (scale, min) pair j of a Q4_K / Q5_K block as integers; s0..s2 are the 12 scale bytes.
+__device__ __forceinline__ void k4_scale_min_u(int j, uint32_t s0, uint32_t s1, uint32_t s2, uint32_t &a,
+                                               uint32_t &b) {
+    const uint32_t w[3] = {s0, s1, s2};
+    auto byte = [&](int k) { return (w[k >> 2] >> (8 * (k & 3))) & 0xffu; };
+    if (j < 4) {
+        a = byte(j) & 63;
+        b = byte(j + 4) & 63;
+    } else {
+        a = (byte(j + 4) & 0xf) | ((byte(j - 4) >> 6) << 4);
+        b = (byte(j + 4) >> 4) | ((byte(j) >> 6) << 4);
+    }
+}
+
 // 6-bit (scale, min) pair j of a Q4_K / Q5_K block; s0..s2 are the 12 scale bytes.
 __device__ __forceinline__ void k4_scale_min(int j, uint32_t s0, uint32_t s1, uint32_t s2, float &sc, float &m) {
     const uint32_t w[3] = {s0, s1, s2};

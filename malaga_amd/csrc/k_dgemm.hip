@@ -162,6 +162,40 @@ __device__ __forceinline__ void dg_slice(int kb, int s, int kq, const typename M
     }
 }
 
+// The A operand (f16 hi | lo) of slice s of block kb for a 32-value slice: dg_slice's X
+// arithmetic (PRO_LN: normalized with the row's statistics and gamma | beta; PRO_SPLIT:
+// taken as it is).
+template <int PRO>
+__device__ __forceinline__ void dg_x32(int kb, int s, int kq, const DFrag<2> &f, const float *gb, int K, float mrow,
+                                       float rrow, h8_t &ah, h8_t &al) {
+    if constexpr (PRO == PRO_SPLIT) {
+        const h8_t p0 = __builtin_bit_cast(h8_t, f.x[0]), p1 = __builtin_bit_cast(h8_t, f.x[1]);
+        ah = __builtin_shufflevector(p0, p1, 0, 1, 2, 3, 8, 9, 10, 11);
+        al = __builtin_shufflevector(p0, p1, 4, 5, 6, 7, 12, 13, 14, 15);
+    } else {
+        float v[8];
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            float4 e = f.x[i];
+            if constexpr (PRO == PRO_LN) {
+                const int k = kb * kStep + s * 32 + kq * 8 + 4 * i;
+                const float4 g = *reinterpret_cast<const float4 *>(gb + k), b = *reinterpret_cast<const float4 *>(gb + K + k);
+                e = make_float4((e.x - mrow) * rrow * g.x + b.x, (e.y - mrow) * rrow * g.y + b.y,
+                                (e.z - mrow) * rrow * g.z + b.z, (e.w - mrow) * rrow * g.w + b.w);
+            }
+            v[4 * i] = e.x;
+            v[4 * i + 1] = e.y;
+            v[4 * i + 2] = e.z;
+            v[4 * i + 3] = e.w;
+        }
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            ah[i] = _Float16(v[i]);
+            al[i] = _Float16(v[i] - float(ah[i]));
+        }
+    }
+}
+
 // BPW: K blocks per wave (compile time, it sizes the fragment ring); NT: 16-column tiles
 // per workgroup (1 or 2; with 2, each X fragment, once normalized and split, feeds two
 // tiles); TL: W from the tile-major copy a.w.t (q6_K / q4_K); the wave count NW (4, 8, or
@@ -285,16 +319,36 @@ __global__ __launch_bounds__(NWL * 64) void k_dgemm(DArgs a) {
 #pragma unroll
             for (int nt = 0; nt < NT; ++nt)
                 load_w<T, TL>(a.w, (n0 >> 4) + nt, ln, blk(j + 1), kq, wr[(j + 1) & 1][nt]);
-        static_for<0, W::SLICES>([&](auto sc) {
-            constexpr int s = decltype(sc)::value, i = j * W::SLICES + s, r = i + D;
-            compute(kb, s, wr[j & 1], buf[i % D], live);
-            if constexpr (r < NI) {
-                // the refill stays behind the compute that frees its slot (hoisted,
-                // it would hold a second set of fragments in registers)
-                __builtin_amdgcn_sched_barrier(0);
-                load_x(blk(r / W::SLICES), r % W::SLICES, buf[i % D]);
-            }
-        });
+        if constexpr (W::FOLD) {
+            // scales folded into B (mfma_core.hpp): the block's slices accumulate on the MFMA
+            f4_t cb[NT], mb[NT];
+#pragma unroll
+            for (int nt = 0; nt < NT; ++nt) cb[nt] = mb[nt] = f4_t{0.f, 0.f, 0.f, 0.f};
+            static_for<0, W::SLICES>([&](auto sc) {
+                constexpr int s = decltype(sc)::value, i = j * W::SLICES + s, r = i + D;
+                h8_t ah, al;
+                dg_x32<PRO>(kb, s, kq, buf[i % D], gb, K, mrow, rrow, ah, al);
+#pragma unroll
+                for (int nt = 0; nt < NT; ++nt) fold_slice<W>(wr[j & 1][nt], s, ah, al, cb[nt], mb[nt]);
+                if constexpr (r < NI) {
+                    __builtin_amdgcn_sched_barrier(0);
+                    load_x(blk(r / W::SLICES), r % W::SLICES, buf[i % D]);
+                }
+            });
+#pragma unroll
+            for (int nt = 0; nt < NT; ++nt) fold_flush<W>(wr[j & 1][nt], live, cb[nt], mb[nt], acc[nt]);
+        } else {
+            static_for<0, W::SLICES>([&](auto sc) {
+                constexpr int s = decltype(sc)::value, i = j * W::SLICES + s, r = i + D;
+                compute(kb, s, wr[j & 1], buf[i % D], live);
+                if constexpr (r < NI) {
+                    // the refill stays behind the compute that frees its slot (hoisted,
+                    // it would hold a second set of fragments in registers)
+                    __builtin_amdgcn_sched_barrier(0);
+                    load_x(blk(r / W::SLICES), r % W::SLICES, buf[i % D]);
+                }
+            });
+        }
     });
 
     // the waves' partial tiles (lane: column nt 16 + ln, rows 4 kq .. 4 kq + 3), added in
@@ -376,7 +430,7 @@ __global__ __launch_bounds__(NWL * 64) void k_dgemm(DArgs a) {
 // through the wave's LDS scratch to the row-major lane layout of the epilogues (4 columns
 // of one row per lane: one 16-byte store per split fragment, float4 or f16 x 4 otherwise).
 constexpr int kDrxWaves = 8;
-constexpr int kDrxDepth = 2;               // (tile, K block) jobs of W in flight per wave
+constexpr int kDrxMaxDepth = 2;            // (tile, K block) jobs of W in flight per wave
 constexpr int kDrxMaxKB = 8;               // K <= 2048
 constexpr int kDrxScr = 16 * 17;           // a wave's 16 x 16 tile, row stride 17
 __host__ __device__ constexpr int drx_xs(int K) { return K + 8; }  // halves per staged row
@@ -394,10 +448,14 @@ __global__ __launch_bounds__(kDrxWaves * 64) void k_drx(DArgs a) {
     constexpr int K = KB * kStep, XS = drx_xs(K);
     constexpr int NU = K / 128;  // staged 4-column units per thread (16 rows x K / 4 over 512 threads)
     static_assert(KB % KS == 0 && KB <= kDrxMaxKB, "K blocks split evenly over the waves of a tile");
+    // two jobs of W in flight: every job requested at entry measured slower (config 5, 64
+    // rows: 2.49 -> 2.57 ms per step, 214-254 VGPRs instead of 144-176)
+    constexpr int kDrxDepth = JPW < kDrxMaxDepth ? JPW : kDrxMaxDepth;
     extern __shared__ __align__(16) unsigned char drx_lds[];
     _Float16 *xh = reinterpret_cast<_Float16 *>(drx_lds), *xl = xh + 16 * XS;
-    float *xsum = reinterpret_cast<float *>(xl + 16 * XS);  // W::MIN: [K / 16][16] sums of the staged X
-    float *scr = xsum + (W::MIN ? (K / 16) * 16 : 0);       // [waves][kDrxScr]
+    constexpr bool XSUM = W::MIN && !W::FOLD;               // the min term from staged X sums
+    float *xsum = reinterpret_cast<float *>(xl + 16 * XS);  // XSUM: [K / 16][16] sums of the staged X
+    float *scr = xsum + (XSUM ? (K / 16) * 16 : 0);         // [waves][kDrxScr]
     float *lnm = scr + kDrxWaves * kDrxScr, *lnr = lnm + 16;
     const int t = threadIdx.x, lane = t & 63, ln = lane & 15, kq = lane >> 4;
     const int wv = __builtin_amdgcn_readfirstlane(t >> 6);
@@ -513,7 +571,7 @@ __global__ __launch_bounds__(kDrxWaves * 64) void k_drx(DArgs a) {
             const int cg = (t >> 4) + 32 * i;
             *reinterpret_cast<uint2 *>(xh + xm * XS + 4 * cg) = make_uint2(hl[i].x, hl[i].y);
             *reinterpret_cast<uint2 *>(xl + xm * XS + 4 * cg) = make_uint2(hl[i].z, hl[i].w);
-            if constexpr (W::MIN) {
+            if constexpr (XSUM) {
                 // the 16 columns of chunk cg / 4 are in lanes xm, xm + 16, xm + 32, xm + 48
                 float sum = sums[i];
                 sum += __shfl_xor(sum, 16);
@@ -527,6 +585,17 @@ __global__ __launch_bounds__(kDrxWaves * 64) void k_drx(DArgs a) {
     // 4. the jobs: K blocks kp + j KS of this wave's tile
     f4_t acc = f4_t{0.f, 0.f, 0.f, 0.f};
     auto job = [&](int kb, const WR &cur) {
+        if constexpr (W::FOLD) {
+            f4_t cb = f4_t{0.f, 0.f, 0.f, 0.f}, mb = cb;
+#pragma unroll
+            for (int s = 0; s < W::SLICES; ++s) {
+                const int xo = ln * XS + kb * kStep + s * SK + kq * (SK / 4);
+                const h8_t ah = *reinterpret_cast<const h8_t *>(xh + xo), al = *reinterpret_cast<const h8_t *>(xl + xo);
+                fold_slice<W>(cur, s, ah, al, cb, mb);
+            }
+            fold_flush<W>(cur, true, cb, mb, acc);
+            return;
+        }
 #pragma unroll
         for (int s = 0; s < W::SLICES; ++s) {
             float sc, mn;
@@ -781,14 +850,28 @@ __global__ __launch_bounds__(512) void k_dxattn(DArgs a) {
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt) acc[nt] = f4_t{0.f, 0.f, 0.f, 0.f};
     const int ar = min(ln, RG - 1);
+    // k_dgemm's arithmetic for the same slices (folded for q4_K / q5_K), so q equals its q
+    f4_t cb[NT], mb[NT];
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) cb[nt] = mb[nt] = f4_t{0.f, 0.f, 0.f, 0.f};
     static_for<0, W::SLICES>([&](auto sc) {
         constexpr int s = decltype(sc)::value;
         DFrag<XQ> fr;
 #pragma unroll
         for (int i = 0; i < XQ; ++i)
             fr.x[i] = __builtin_bit_cast(float4, xs[(kb * (kStep / 4) + s * (SK / 4) + kq * (SK / 16) + i) * RG + ar]);
-        dg_slice<T, NT, PRO_SPLIT>(kb, s, kq, wr, fr, live, nullptr, K, 0.f, 0.f, acc);
+        if constexpr (W::FOLD) {
+            h8_t ah, al;
+            dg_x32<PRO_SPLIT>(kb, s, kq, fr, nullptr, K, 0.f, 0.f, ah, al);
+#pragma unroll
+            for (int nt = 0; nt < NT; ++nt) fold_slice<W>(wr[nt], s, ah, al, cb[nt], mb[nt]);
+        } else {
+            dg_slice<T, NT, PRO_SPLIT>(kb, s, kq, wr, fr, live, nullptr, K, 0.f, 0.f, acc);
+        }
     });
+    if constexpr (W::FOLD)
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt) fold_flush<W>(wr[nt], live, cb[nt], mb[nt], acc[nt]);
     // the K blocks' partial tiles (lane: column nt 16 + ln, A rows 4 kq .. 4 kq + 3), then
     // q = their sum in K-block order + bias, in LDS
 #pragma unroll
@@ -1035,7 +1118,7 @@ bool drx_ok(const DevMatrix &w, int M) {
 
 template <int T, int KB, int KS, int PRO, int EPI>
 hipError_t launch_drx_k(const DArgs &a, hipStream_t st) {
-    const size_t lds = drx_lds_bytes(KB * kStep, MW<T>::MIN);
+    const size_t lds = drx_lds_bytes(KB * kStep, MW<T>::MIN && !MW<T>::FOLD);
     static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void *>(&k_drx<T, KB, KS, PRO, EPI, true>),
                                                        hipFuncAttributeMaxDynamicSharedMemorySize, int(lds));
     if (attr != hipSuccess) return attr;

@@ -324,7 +324,7 @@ __device__ __forceinline__ uint32_t sl_token(const SlFinalize &sl, int row, uint
 __global__ __launch_bounds__(256) void k_greedy_finalize_wg(const float *pv, const uint32_t *pi, int P, int b,
                                                             uint8_t *finished, uint32_t *ids, uint32_t *out, int m,
                                                             uint32_t *step, uint32_t eos, uint32_t pad,
-                                                            SlFinalize sl, float *outv) {
+                                                            SlFinalize sl, float *outv, uint32_t *err) {
     __shared__ float sv[4];
     __shared__ uint32_t si[4];
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
@@ -358,6 +358,9 @@ __global__ __launch_bounds__(256) void k_greedy_finalize_wg(const float *pv, con
             bi = si[0];
             for (int k = 1; k < 4; ++k) argmax_merge(best, bi, sv[k], si[k]);
             uint32_t tok = sl.vocab_map ? sl_token(sl, row, bi, finished[row] != 0, pad) : bi;
+            // no finite logit in a live row (NaN from an activation past the f16 range of the
+            // MFMA operands, say): reported to the host instead of decoding an arbitrary token
+            if (err && !finished[row] && !(best > -INFINITY)) *err = 1u;
             if (finished[row]) tok = pad;
             if (tok == eos) finished[row] = 1;
             ids[row] = tok;
@@ -374,7 +377,7 @@ __global__ __launch_bounds__(256) void k_greedy_finalize_wg(const float *pv, con
 __global__ __launch_bounds__(1024) void k_greedy_finalize(const float *pv, const uint32_t *pi, int P, int b,
                                                           uint8_t *finished, uint32_t *ids, uint32_t *out, int m,
                                                           uint32_t *step, uint32_t eos, uint32_t pad, SlFinalize sl,
-                                                          float *outv) {
+                                                          float *outv, uint32_t *err) {
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, nw = blockDim.x >> 6;
     const uint32_t s = *step;
     for (int row = w; row < b; row += nw) {  // wave-uniform
@@ -398,6 +401,7 @@ __global__ __launch_bounds__(1024) void k_greedy_finalize(const float *pv, const
         wave_argmax(best, bi);
         if (lane == 0) {
             uint32_t tok = sl.vocab_map ? sl_token(sl, row, bi, finished[row] != 0, pad) : bi;
+            if (err && !finished[row] && !(best > -INFINITY)) *err = 1u;
             if (finished[row]) tok = pad;
             if (tok == eos) finished[row] = 1;
             ids[row] = tok;
@@ -1108,15 +1112,15 @@ hipError_t argmax_partial(const float *logits, int b, int V, int ldl, int mask_i
 
 hipError_t greedy_finalize(const float *pv, const uint32_t *pi, int parts, int b, uint8_t *finished, uint32_t *ids,
                            uint32_t *out, int m, uint32_t *step, uint32_t eos, uint32_t pad, hipStream_t st,
-                           const SlFinalize &sl, float *outv) {
+                           const SlFinalize &sl, float *outv, uint32_t *err) {
     if (sl.vocab_map && (!sl.spv || !sl.spi || !sl.src_ids || !sl.sl_row || !sl.src_row || sl.S < 1))
         return hipErrorInvalidValue;
     if (b <= 4)
         hipLaunchKernelGGL(k_greedy_finalize_wg, dim3(1), dim3(256), 0, st, pv, pi, parts, b, finished, ids, out, m,
-                           step, eos, pad, sl, outv);
+                           step, eos, pad, sl, outv, err);
     else
         hipLaunchKernelGGL(k_greedy_finalize, dim3(1), dim3(1024), 0, st, pv, pi, parts, b, finished, ids, out, m,
-                           step, eos, pad, sl, outv);
+                           step, eos, pad, sl, outv, err);
     return hipGetLastError();
 }
 

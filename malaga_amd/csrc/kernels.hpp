@@ -244,10 +244,11 @@ hipError_t argmax_partial(const float *logits, int b, int V, int ldl, int mask_i
 // Second argmax pass + greedy bookkeeping (kernels/malaga.cu:290-326 semantics):
 // tok = finished ? pad : argmax ; finished |= tok == eos ; ids = tok ;
 // out[row][*step] = tok ; ++*step.  outv (optional, [b][m]): outv[row][*step] = the
-// winning logit (before the finished / pad rule).
+// winning logit (before the finished / pad rule).  err (optional): set to 1 when a row
+// not yet finished has no finite logit.
 hipError_t greedy_finalize(const float *pv, const uint32_t *pi, int parts, int b, uint8_t *finished, uint32_t *ids,
                            uint32_t *out, int m, uint32_t *step, uint32_t eos, uint32_t pad, hipStream_t st,
-                           const SlFinalize &sl = SlFinalize{}, float *outv = nullptr);
+                           const SlFinalize &sl = SlFinalize{}, float *outv = nullptr, uint32_t *err = nullptr);
 // Beam: per row log-softmax of logits [rows][V] and its top-k (k <= 8, ties -> lowest
 // index): vals/idx [rows][k].  mask_id (>= 0) is treated as -inf.
 hipError_t logsoftmax_topk(const float *logits, int rows, int V, int k, int mask_id, float *work, float *vals,

@@ -29,6 +29,33 @@ __device__ __forceinline__ uint2 bytes_to_h4(uint32_t v, h2_t off) {
 template <int T>
 struct MW;  // per-type W fetch for one 256-wide K step
 
+// Scale folding (FOLD types, q4_K / q5_K): the 6-bit sub-block scale a_s times a quant
+// (q <= 15, or 31 for q5_K) is at most 1953, an exact f16 integer, so B = a_s q is the MFMA
+// operand and the 8 slices of a block accumulate in the MFMA's own C operand; the min term
+// sum_k m_s x_k also runs on the MFMA (B = m_s in every element).  Per block then
+//   sum_k w_k x_k = d C - dmin M,   C = sum_s X_s (a_s q_s),   M = sum_s X_s m_s,
+// instead of two f32 FMAs per output and slice.
+template <class W>
+__device__ __forceinline__ void fold_slice(const typename W::Regs &r, int s, const h8_t &ah, const h8_t &al, f4_t &cb,
+                                           f4_t &mb) {
+    _Float16 a, m;
+    W::scale_min_h(r, s, a, m);
+    const h8_t bq = W::b(r, s) * a;
+    const h8_t bm = {m, m, m, m, m, m, m, m};
+    cb = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bq, cb, 0, 0, 0);
+    cb = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, bq, cb, 0, 0, 0);
+    mb = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bm, mb, 0, 0, 0);
+    mb = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, bm, mb, 0, 0, 0);
+}
+// acc += d C - dmin M at the end of a block (live false: a block past the end weighs 0)
+template <class W>
+__device__ __forceinline__ void fold_flush(const typename W::Regs &r, bool live, const f4_t &cb, const f4_t &mb,
+                                           f4_t &acc) {
+    const float d = live ? h2f(r.hdr.x) : 0.f, dmin = live ? h2f(r.hdr.x >> 16) : 0.f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) acc[i] = fmaf(d, cb[i], fmaf(-dmin, mb[i], acc[i]));
+}
+
 // q4_K: 8 sub-blocks of 32; lane k-group kq reads bytes qs[32 g + 8 kq, +8) of the
 // 4 byte groups g (low nibbles: sub-block 2g, high nibbles: 2g + 1).
 template <>
@@ -68,6 +95,13 @@ struct MW<GGML_Q4_K> {
         sc = h2f(r.hdr.x) * a;
         mn = h2f(r.hdr.x >> 16) * m;
     }
+    static constexpr bool FOLD = true;
+    __device__ static void scale_min_h(const Regs &r, int s, _Float16 &a, _Float16 &m) {
+        uint32_t ai, mi;
+        k4_scale_min_u(s, r.hdr.y, r.hdr.z, r.hdr.w, ai, mi);
+        a = _Float16(float(ai));
+        m = _Float16(float(mi));
+    }
 };
 
 // q5_K: as q4_K plus the fifth bit of sub-block s in bit s of qh[l] (l < 32).
@@ -100,6 +134,11 @@ struct MW<GGML_Q5_K> {
         MW<GGML_Q4_K>::Regs t{r.hdr, {}};
         MW<GGML_Q4_K>::scale(t, s, sc, mn);
     }
+    static constexpr bool FOLD = true;
+    __device__ static void scale_min_h(const Regs &r, int s, _Float16 &a, _Float16 &m) {
+        MW<GGML_Q4_K>::Regs t{r.hdr, {}};
+        MW<GGML_Q4_K>::scale_min_h(t, s, a, m);
+    }
 };
 
 // q6_K: 16 groups of 16 with an int8 scale each (one 16x16x16 MFMA per group).
@@ -110,6 +149,7 @@ template <>
 struct MW<GGML_Q6_K> {
     static constexpr int SLICES = 16, SK = 16;
     static constexpr bool MIN = false;
+    static constexpr bool FOLD = false;
     struct Regs {
         uint32_t qa[4], qb[4], qh[4];  // [2 n + h]
         uint4 sc;
@@ -161,6 +201,7 @@ template <>
 struct MW<GGML_Q8_0> {
     static constexpr int SLICES = 8, SK = 32;
     static constexpr bool MIN = false;
+    static constexpr bool FOLD = false;
     struct Regs {
         uint2 q[8];
         uint4 d;  // 8 f16 scales
@@ -188,6 +229,7 @@ template <>
 struct MW<GGML_F16> {
     static constexpr int SLICES = 8, SK = 32;
     static constexpr bool MIN = false;
+    static constexpr bool FOLD = false;
     struct Regs {
         uint4 q[8];
     };

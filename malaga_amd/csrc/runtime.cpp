@@ -733,6 +733,7 @@ std::unique_ptr<StaticState> Model::new_state(int b, int s, int m, bool logits, 
     st->lens = static_cast<uint32_t *>(get(size_t(b) * 4, "lens"));
     st->out = static_cast<uint32_t *>(get(size_t(b) * m * 4, "out"));
     st->outv = static_cast<float *>(get(size_t(b) * m * 4, "winning logits"));
+    st->err = static_cast<uint32_t *>(get(4, "non-finite flag"));
     st->finished = static_cast<uint8_t *>(get(size_t(b), "finished"));
     st->row_src = static_cast<uint32_t *>(get(size_t(b) * 4, "source rows"));
     // one block each for the self and the cross K/V of every layer (layer l: K, then V);
@@ -835,6 +836,7 @@ void Model::reset_state(StaticState &st, const Batch &src, const std::vector<uin
     up.upload(st.lens, lens.data(), lens.size() * 4, s);
     check_hip(fill_u32(st.ids, start, size_t(st.b), s), "fill");
     check_hip(fill_u32(st.step, 0, 1, s), "fill");
+    check_hip(fill_u32(st.err, 0, 1, s), "fill");
     if (st.sl) {
         // src/graph.rs:98-108: source ids of every row (pad past the row's length, idle
         // rows all pad) and their token_embd rows
@@ -880,6 +882,11 @@ bool Model::fusable(int b, int m, int s) const {
 }
 
 namespace {
+// The f16 hi / lo split of the MFMA operands holds |x| < 65520; an activation beyond it
+// becomes NaN, and every logit of its row with it.
+constexpr const char *kNonFiniteLogits =
+    "decoder produced no finite logit for a row (an activation beyond the f16 range of the MFMA operands?)";
+
 // Layer i's self and cross caches in the state's precision: f(kc, vc, ck, cv) with __half
 // pointers (the graph step) or float pointers (the generic path).
 template <typename F>
@@ -970,7 +977,7 @@ void Model::lm_head(StaticState &st, bool greedy_mode, int mask_id, const float 
             sl = SlFinalize{st.sl->d_ids, V, st.spv, st.spi, st.src_ids, st.s, st.sl_row, st.src_row};
         }
         check_hip(greedy_finalize(st.pv, st.pi, parts, B, st.finished, st.ids, st.out, st.m, st.step,
-                                  uint32_t(cfg.eos_token_id), uint32_t(cfg.pad_token_id), s, sl, st.outv),
+                                  uint32_t(cfg.eos_token_id), uint32_t(cfg.pad_token_id), s, sl, st.outv, st.err),
                   "greedy_finalize");
     } else {
         const int V = cfg.vocab_size;
@@ -1318,9 +1325,12 @@ std::vector<std::vector<uint32_t>> GraphCache::run(const Batch &src, uint32_t tg
     }
     std::vector<uint32_t> out(static_cast<size_t>(st.b) * st.m);
     std::vector<float> outv(top ? out.size() : 0);
+    uint32_t err = 0;
     check_hip(hipMemcpyAsync(out.data(), st.out, out.size() * 4, hipMemcpyDeviceToHost, s), "D2H");
     if (top) check_hip(hipMemcpyAsync(outv.data(), st.outv, outv.size() * 4, hipMemcpyDeviceToHost, s), "D2H");
+    check_hip(hipMemcpyAsync(&err, st.err, 4, hipMemcpyDeviceToHost, s), "D2H");
     check_hip(hipStreamSynchronize(s), "sync");
+    if (err) fail(ERR_INVALID, kNonFiniteLogits);
     std::vector<std::vector<uint32_t>> res(static_cast<size_t>(n));
     if (top) top->assign(static_cast<size_t>(n), {});
     for (int r = 0; r < n; ++r)
@@ -1434,6 +1444,8 @@ std::vector<std::vector<uint32_t>> Model::beam(const Batch &src, uint32_t tgt_la
         check_hip(hipMemcpyAsync(h_vals, d_vals, size_t(bk) * k * 4, hipMemcpyDeviceToHost, s), "D2H");
         check_hip(hipMemcpyAsync(h_idx, d_idx, size_t(bk) * k * 4, hipMemcpyDeviceToHost, s), "D2H");
         check_hip(hipStreamSynchronize(s), "sync");
+        for (int r = 0; r < bk; ++r)  // a row's best log-probability is finite unless its logits are not
+            if (!(vals[size_t(r) * k] > -INFINITY)) fail(ERR_INVALID, kNonFiniteLogits);
         if (merge.merge(stp, vals, idx)) break;
         const std::vector<uint32_t> &reorder = merge.reorder(), &next = merge.next();
         // src/model.rs:209-226 gathers the self-attention caches by beam; here only the
@@ -1487,8 +1499,11 @@ std::vector<std::vector<uint32_t>> Model::greedy_generic(const Batch &src, uint3
         }
     }
     std::vector<uint32_t> out(size_t(b) * st->m);
+    uint32_t err = 0;
     check_hip(hipMemcpyAsync(out.data(), st->out, out.size() * 4, hipMemcpyDeviceToHost, s), "D2H");
+    check_hip(hipMemcpyAsync(&err, st->err, 4, hipMemcpyDeviceToHost, s), "D2H");
     check_hip(hipStreamSynchronize(s), "sync");
+    if (err) fail(ERR_INVALID, kNonFiniteLogits);
     std::vector<std::vector<uint32_t>> res(static_cast<size_t>(b));
     for (int r = 0; r < b; ++r)
         for (int j = 1; j <= k; ++j) {  // strip (translator.rs:243-246): up to the first EOS

@@ -110,6 +110,7 @@ struct StaticState {
     int b = 0, s = 0, m = 0;
     uint32_t *ids = nullptr, *step = nullptr, *lens = nullptr, *out = nullptr;
     float *outv = nullptr;  // [b][m]: the winning logit of each greedy token (parity hook)
+    uint32_t *err = nullptr;  // set by the greedy finalize when a live row has no finite logit
     uint8_t *finished = nullptr;
     // self and cross K/V per layer: f16 (kc ..; the fused graph step, kernels/malaga.cu:
     // 142-154) or, with kv32, f32 (kc32 ..; the generic decode path's candle KvCache and

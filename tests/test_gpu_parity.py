@@ -375,3 +375,25 @@ def test_decode_gemm_step_equals_split_k_step(kq_gguf, models, preset):
             assert np.abs(a - orc.teacher_forced_logits(src, tgt, kv_f16=True)).max() < 2e-3
     finally:
         split.close()
+
+
+def test_activation_beyond_f16_range_is_an_error(model_dir):
+    """The MFMA products take their activations as f16 hi + lo, which holds |x| < 65520.
+    A checkpoint whose activations go past that (N(0, 2000) weights: attention outputs and
+    FFN activations ~1e5) must end in an error that says so, for greedy and beam alike,
+    never in tokens decoded from NaN logits.  (The reference keeps f32 activations; this is
+    the documented range of this backend.)"""
+    from tests.conftest import KQ_CONFIG
+
+    p = model_dir / "huge-q8_0.gguf"
+    if not p.exists():
+        M.write_synthetic(p, KQ_CONFIG, "q8_0", M.INIT_NORMAL, seed=3, std=2000.0, name="huge")
+    gpu = M.Translator.load(p)
+    try:
+        src = [[997, 5 + i, 6, 2] for i in range(8)]
+        for opts in (M.GenOptions(max_new_tokens=4, max_batch=8),
+                     M.GenOptions(max_new_tokens=4, max_batch=8, beam_size=2)):
+            with pytest.raises(M.MalagaError, match="finite logit"):
+                gpu.generate(src, 998, opts)
+    finally:
+        gpu.close()
