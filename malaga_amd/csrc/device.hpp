@@ -209,6 +209,38 @@ __host__ __device__ __forceinline__ size_t frag_index(int m, int k, int K) {
     return (size_t(m >> 4) * size_t(K >> 4) + size_t(k >> 4)) * 64 + size_t((k >> 2) & 3) * 16 + size_t(m & 15);
 }
 
+// Eight consecutive values of a K or V cache row: f16 (one 16-byte load) or f32 (two).
+// unpack yields them as f32, zeros where keep is false (a masked key's value must not
+// reach the sum even as 0 * NaN).
+template <typename KT>
+struct Kv8;
+template <>
+struct Kv8<__half> {
+    uint4 w;
+    __device__ __forceinline__ void load(const __half *p) { w = *reinterpret_cast<const uint4 *>(p); }
+    __device__ __forceinline__ void unpack(float (&o)[8], bool keep = true) const {
+        const uint32_t a[4] = {keep ? w.x : 0u, keep ? w.y : 0u, keep ? w.z : 0u, keep ? w.w : 0u};
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            o[2 * j] = h2f(a[j]);
+            o[2 * j + 1] = h2f(a[j] >> 16);
+        }
+    }
+};
+template <>
+struct Kv8<float> {
+    float4 a, b;
+    __device__ __forceinline__ void load(const float *p) {
+        a = ld4(p, 0);
+        b = ld4(p, 1);
+    }
+    __device__ __forceinline__ void unpack(float (&o)[8], bool keep = true) const {
+        const float v[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+#pragma unroll
+        for (int j = 0; j < 8; ++j) o[j] = keep ? v[j] : 0.f;
+    }
+};
+
 // f(std::integral_constant<int, I>) for I = 0 .. N - 1: loop indices that are constants
 // from the start (register arrays indexed by them stay in registers)
 template <int I, int N, class F>

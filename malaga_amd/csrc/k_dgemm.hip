@@ -29,6 +29,8 @@
 //
 // Epilogues: EPI_STORE y = x W^T + bias (ReLU), f32 rows or split fragments; EPI_RESID x += x_in W^T + bias in place,
 // plus the statistics of the new x; EPI_QKV q (f32) and K/V (f16, cache slot *step).
+#include <type_traits>
+
 #include "kernels.hpp"
 #include "mfma_core.hpp"
 
@@ -743,7 +745,7 @@ __global__ __launch_bounds__(kDrxWaves * 64) void k_drx(DArgs a) {
 // fragments (frag_index), the A operand of the cross out-projection.
 constexpr int kDxHD = 64, kDxMaxBlocks = 256 / kDxHD, kDxMaxK = kDxMaxBlocks * kStep;
 
-template <int T, int HD, int S, bool TL>
+template <int T, int HD, int S, bool TL, typename KT>
 __global__ __launch_bounds__(512) void k_dxattn(DArgs a) {
     using W = MW<T>;
     using WR = typename W::Regs;
@@ -784,14 +786,23 @@ __global__ __launch_bounds__(512) void k_dxattn(DArgs a) {
     const int pr = wv / S, ks = wv % S, bi = min(m0 + pr, a.M - 1);
     const int sub = lane % TPK, split = lane / TPK, L = a.slots, d = a.H * HD;
     const size_t kv0 = (size_t(bi) * a.H + hh) * size_t(L) * HD + sub * 8;
-    uint4 kr[U], vr[U];
+    // the caches in their precision: f16 (the graph step) or f32 (the generic decoder)
+    const KT *kc, *vc;
+    if constexpr (std::is_same_v<KT, float>) {
+        kc = a.kc32;
+        vc = a.vc32;
+    } else {
+        kc = a.kc;
+        vc = a.vc;
+    }
+    Kv8<KT> kr[U], vr[U];
     auto key = [&](int c, int u) { return SPL * (S * (c * U + u) + ks) + split; };
     auto load_kv = [&](int c) {
 #pragma unroll
         for (int u = 0; u < U; ++u) {
             const size_t o = kv0 + size_t(min(key(c, u), L - 1)) * HD;
-            kr[u] = *reinterpret_cast<const uint4 *>(a.kc + o);
-            vr[u] = *reinterpret_cast<const uint4 *>(a.vc + o);
+            kr[u].load(kc + o);
+            vr[u].load(vc + o);
         }
     };
     load_kv(0);
@@ -899,14 +910,16 @@ __global__ __launch_bounds__(512) void k_dxattn(DArgs a) {
         float cmax = -INFINITY;
 #pragma unroll
         for (int u = 0; u < U; ++u) {
-            float sdot = h2f(kr[u].x) * qa.x;
-            sdot = fmaf(h2f(kr[u].x >> 16), qa.y, sdot);
-            sdot = fmaf(h2f(kr[u].y), qa.z, sdot);
-            sdot = fmaf(h2f(kr[u].y >> 16), qa.w, sdot);
-            sdot = fmaf(h2f(kr[u].z), qb.x, sdot);
-            sdot = fmaf(h2f(kr[u].z >> 16), qb.y, sdot);
-            sdot = fmaf(h2f(kr[u].w), qb.z, sdot);
-            sdot = fmaf(h2f(kr[u].w >> 16), qb.w, sdot);
+            float kv[8];
+            kr[u].unpack(kv);
+            float sdot = kv[0] * qa.x;
+            sdot = fmaf(kv[1], qa.y, sdot);
+            sdot = fmaf(kv[2], qa.z, sdot);
+            sdot = fmaf(kv[3], qa.w, sdot);
+            sdot = fmaf(kv[4], qb.x, sdot);
+            sdot = fmaf(kv[5], qb.y, sdot);
+            sdot = fmaf(kv[6], qb.z, sdot);
+            sdot = fmaf(kv[7], qb.w, sdot);
             sdot = group_sum<TPK>(sdot);
             sc[u] = key(c, u) < n ? sdot : -INFINITY;
             cmax = fmaxf(cmax, sc[u]);
@@ -921,12 +934,10 @@ __global__ __launch_bounds__(512) void k_dxattn(DArgs a) {
             const bool in = key(c, u) < n;
             const float pj = in ? expf(sc[u] - mnew) : 0.f;
             l += pj;
-            const uint32_t wv4[4] = {in ? vr[u].x : 0u, in ? vr[u].y : 0u, in ? vr[u].z : 0u, in ? vr[u].w : 0u};
+            float vv[8];
+            vr[u].unpack(vv, in);
 #pragma unroll
-            for (int q2 = 0; q2 < 4; ++q2) {
-                o8[2 * q2] = fmaf(pj, h2f(wv4[q2]), o8[2 * q2]);
-                o8[2 * q2 + 1] = fmaf(pj, h2f(wv4[q2] >> 16), o8[2 * q2 + 1]);
-            }
+            for (int e = 0; e < 8; ++e) o8[e] = fmaf(pj, vv[e], o8[e]);
         }
         m = mnew;
     }
@@ -1012,17 +1023,22 @@ inline int dx_rows() { return 8 / kDxSplit; }
 // Heads of 64 and K <= 1024 (d_model of the 600M and 1.3B checkpoints): one K block per
 // wave; other shapes keep the two launches.
 
-template <int T>
-hipError_t launch_dxattn_t(const DArgs &a, hipStream_t st) {
+template <int T, typename KT>
+hipError_t launch_dxattn_k(const DArgs &a, hipStream_t st) {
     const dim3 grid(unsigned(a.H), unsigned((a.M + dx_rows() - 1) / dx_rows()));
     if constexpr (T == GGML_Q6_K || T == GGML_Q4_K) {
         if (a.w.t) {
-            hipLaunchKernelGGL((k_dxattn<T, kDxHD, kDxSplit, true>), grid, dim3(512), 0, st, a);
+            hipLaunchKernelGGL((k_dxattn<T, kDxHD, kDxSplit, true, KT>), grid, dim3(512), 0, st, a);
             return hipGetLastError();
         }
     }
-    hipLaunchKernelGGL((k_dxattn<T, kDxHD, kDxSplit, false>), grid, dim3(512), 0, st, a);
+    hipLaunchKernelGGL((k_dxattn<T, kDxHD, kDxSplit, false, KT>), grid, dim3(512), 0, st, a);
     return hipGetLastError();
+}
+
+template <int T>
+hipError_t launch_dxattn_t(const DArgs &a, hipStream_t st) {
+    return a.kc32 ? launch_dxattn_k<T, float>(a, st) : launch_dxattn_k<T, __half>(a, st);
 }
 
 // The K split: 4 waves up to four K blocks (K <= 1024), else 8 waves of 1, 2 or 4 blocks.
@@ -1242,16 +1258,20 @@ bool dgemm_cross_attn_supported(const DevMatrix &w, int M, int H, int hd) {
     return dgemm_supported(w, M) && hd == kDxHD && H >= 1 && w.N == H * hd && w.K / kStep <= kDxMaxBlocks;
 }
 
-hipError_t dgemm_cross_attn(const DevMatrix &w, const float *x, int M, const DgemmLn &ln, const float *bias,
-                            const __half *K, const __half *V, int H, int hd, int L, const uint32_t *lens, float *att,
-                            hipStream_t st) {
-    if (!dgemm_cross_attn_supported(w, M, H, hd) || !dgemm_args_ok(w, x, w.K, M, &ln) || !K || !V || !lens || !att ||
-        L < 1 || reinterpret_cast<uintptr_t>(K) % 16 || reinterpret_cast<uintptr_t>(V) % 16 ||
+namespace {
+hipError_t dgemm_cross_attn_any(const DevMatrix &w, const float *x, int M, const DgemmLn &ln, const float *bias,
+                                const __half *K, const __half *V, const float *K32, const float *V32, int H, int hd,
+                                int L, const uint32_t *lens, float *att, hipStream_t st) {
+    const void *k = K ? static_cast<const void *>(K) : K32, *v = V ? static_cast<const void *>(V) : V32;
+    if (!dgemm_cross_attn_supported(w, M, H, hd) || !dgemm_args_ok(w, x, w.K, M, &ln) || !k || !v || !lens || !att ||
+        L < 1 || reinterpret_cast<uintptr_t>(k) % 16 || reinterpret_cast<uintptr_t>(v) % 16 ||
         reinterpret_cast<uintptr_t>(att) % 16)
         return hipErrorInvalidValue;
     DArgs a = dargs(w, x, w.K, M, &ln, bias);
     a.kc = const_cast<__half *>(K);
     a.vc = const_cast<__half *>(V);
+    a.kc32 = const_cast<float *>(K32);
+    a.vc32 = const_cast<float *>(V32);
     a.H = H;
     a.hd = hd;
     a.slots = L;
@@ -1265,6 +1285,19 @@ hipError_t dgemm_cross_attn(const DevMatrix &w, const float *x, int M, const Dge
     case GGML_F16: return launch_dxattn_t<GGML_F16>(a, st);
     default: return hipErrorInvalidValue;
     }
+}
+}  // namespace
+
+hipError_t dgemm_cross_attn(const DevMatrix &w, const float *x, int M, const DgemmLn &ln, const float *bias,
+                            const __half *K, const __half *V, int H, int hd, int L, const uint32_t *lens, float *att,
+                            hipStream_t st) {
+    return dgemm_cross_attn_any(w, x, M, ln, bias, K, V, nullptr, nullptr, H, hd, L, lens, att, st);
+}
+
+hipError_t dgemm_cross_attn(const DevMatrix &w, const float *x, int M, const DgemmLn &ln, const float *bias,
+                            const float *K, const float *V, int H, int hd, int L, const uint32_t *lens, float *att,
+                            hipStream_t st) {
+    return dgemm_cross_attn_any(w, x, M, ln, bias, nullptr, nullptr, K, V, H, hd, L, lens, att, st);
 }
 
 }  // namespace mlg

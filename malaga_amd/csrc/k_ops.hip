@@ -420,38 +420,6 @@ __global__ __launch_bounds__(1024) void k_greedy_finalize(const float *pv, const
 // through its LDS scratch at the end.  S = 1: no workgroup barrier; S > 1: the S partials
 // (sum p_j v_j unnormalized, max, sum p_j) meet in LDS and the pair's first wave rescales
 // them to their common max.
-// Eight consecutive values of a K or V cache row: f16 (one 16-byte load) or f32 (two).
-// unpack yields them as f32, zeros where keep is false (a masked key's value must not
-// reach the sum even as 0 * NaN).
-template <typename KT>
-struct Kv8;
-template <>
-struct Kv8<__half> {
-    uint4 w;
-    __device__ __forceinline__ void load(const __half *p) { w = *reinterpret_cast<const uint4 *>(p); }
-    __device__ __forceinline__ void unpack(float (&o)[8], bool keep = true) const {
-        const uint32_t a[4] = {keep ? w.x : 0u, keep ? w.y : 0u, keep ? w.z : 0u, keep ? w.w : 0u};
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            o[2 * j] = h2f(a[j]);
-            o[2 * j + 1] = h2f(a[j] >> 16);
-        }
-    }
-};
-template <>
-struct Kv8<float> {
-    float4 a, b;
-    __device__ __forceinline__ void load(const float *p) {
-        a = ld4(p, 0);
-        b = ld4(p, 1);
-    }
-    __device__ __forceinline__ void unpack(float (&o)[8], bool keep = true) const {
-        const float v[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
-#pragma unroll
-        for (int j = 0; j < 8; ++j) o[j] = keep ? v[j] : 0.f;
-    }
-};
-
 template <int HD, int S, typename KT>
 __global__ __launch_bounds__(256) void k_attn_waves(const float *q, const KT *K, const KT *V, int b, int H,
                                                     int L, const uint32_t *lens, const uint32_t *step, float *out,

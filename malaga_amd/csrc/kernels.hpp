@@ -138,6 +138,10 @@ bool dgemm_cross_attn_supported(const DevMatrix &w, int M, int H, int hd);
 hipError_t dgemm_cross_attn(const DevMatrix &w, const float *x, int M, const DgemmLn &ln, const float *bias,
                             const __half *K, const __half *V, int H, int hd, int L, const uint32_t *lens, float *att,
                             hipStream_t st);
+// The same over f32 K/V (the generic decoder).
+hipError_t dgemm_cross_attn(const DevMatrix &w, const float *x, int M, const DgemmLn &ln, const float *bias,
+                            const float *K, const float *V, int H, int hd, int L, const uint32_t *lens, float *att,
+                            hipStream_t st);
 
 // M <= 32 rows with X resident in LDS (K <= 1024 at M > 16, K <= 2048 at M <= 16).
 bool gemm_rx_supported(const DevMatrix &w, int M);

@@ -1085,16 +1085,12 @@ void Model::step_dgemm(StaticState &st, bool greedy_mode, int mask_id) {
             // order of the decode GEMMs (frag_index, device.hpp)
             check_hip(attn_decode(st.q, kc, vc, B, H, hd, st.m, nullptr, st.step, st.att, s, st.rows, true), "attn");
             check_hip(dgemm_resid(l.out.w, st.att, d, B, l.out.b, st.x, st.lnstat, s, true), "dgemm_out");
-            bool fused_cross = false;
-            if constexpr (std::is_same_v<std::remove_const_t<std::remove_pointer_t<decltype(ck)>>, __half>) {
-                if (!split_cross_ && dgemm_cross_attn_supported(l.cross_q.w, B, H, hd)) {
-                    check_hip(dgemm_cross_attn(l.cross_q.w, st.x, B, ln_cross, l.cross_q.b, ck, cv, H, hd, st.s,
-                                               st.lens, st.att, s),
-                              "dgemm_cross_attn");
-                    fused_cross = true;
-                }
-            }
-            if (!fused_cross) {
+            const bool fused_cross = !split_cross_ && dgemm_cross_attn_supported(l.cross_q.w, B, H, hd);
+            if (fused_cross) {
+                check_hip(dgemm_cross_attn(l.cross_q.w, st.x, B, ln_cross, l.cross_q.b, ck, cv, H, hd, st.s, st.lens,
+                                           st.att, s),
+                          "dgemm_cross_attn");
+            } else {
                 // where the one-launch cross attention exists, its q is k_dgemm's bit for bit:
                 // the two-launch form keeps k_dgemm too, so that both give the same logits
                 check_hip(dgemm_store(l.cross_q.w, st.x, d, B, &ln_cross, l.cross_q.b, false, st.q, d, s, false,

@@ -271,6 +271,10 @@ def test_batched_fused_cross_attention(kq_gguf, models, preset, nb):
         lg = gpu.teacher_forced_logits(src, tgt)
         assert np.array_equal(lg, split.teacher_forced_logits(src, tgt))
         assert np.abs(lg - orc.teacher_forced_logits(src, tgt, kv_f16=True)).max() < 2e-3
+        # the generic decoder's f32 K/V through the same two forms (beam search runs it)
+        lg32 = gpu.teacher_forced_logits(src, tgt, kv_f32=True)
+        assert np.array_equal(lg32, split.teacher_forced_logits(src, tgt, kv_f32=True))
+        assert np.abs(lg32 - orc.teacher_forced_logits(src, tgt, kv_f16=False)).max() < 2e-3
         want, gap = orc.translate_batch(src, 998, max_batch=64, kv_f16=True, max_new_tokens=10)
         got = gpu.generate(src, 998, M.GenOptions(max_new_tokens=10, max_batch=64))
         assert got == want, f"min top-2 gap {gap}"
