@@ -6,7 +6,10 @@
 // q8_0 int8) are exact in f16, so the MFMA multiplies them by X, which is split
 // into two f16 terms x = hi + lo (|x - hi - lo| <= 2^-22 |x|), with f32
 // accumulation; block scales and k-quant mins are applied per sub-block in f32:
-//   sum_k w_k x_k = d sc * sum_k q_k x_k - dmin m * sum_k x_k.
+//   sum_k w_k x_k = d sc * sum_k q_k x_k - dmin m * sum_k x_k,
+// except for q6_K, whose int8 group scales are folded into B as the exact pair
+// bh + bl = q sc (MW<q6_K>::b_split): a super-block's 8 slices of 32 chain in the
+// 16x16x32 MFMA's C operand and d is applied once per block.
 //
 // Tiling: a workgroup (4 waves) owns 64 rows of W (16 per wave) and BM rows of X.
 // K is consumed in steps of 256 (one k-quant super-block): the X step is staged
@@ -25,7 +28,80 @@ namespace mlg {
 namespace {
 
 constexpr int kXS = kStep + 8;    // LDS row stride of the staged X (halves)
+
+// where the staged X keeps x[k] (k a multiple of 4): split-B types permute the
+// 4-value groups inside each 32-slice (split_pos), the others keep k
+template <bool SPLIT>
+__device__ __forceinline__ int staged_k(int k) {
+    if constexpr (SPLIT) return (k & ~31) | (split_pos((k & 31) >> 2) << 2);
+    else return k;
+}
 constexpr int kTileN = 64;        // W rows per workgroup
+
+// X staging of one 256-wide K step into LDS as f16 hi / lo (+ per-16 sums for the
+// formats with mins).  Each thread converts chunks of 8 values and writes them as one
+// 16-byte store; 16 consecutive lanes take 16 consecutive chunks of one row, so each
+// store of 16 lanes covers 256 contiguous bytes of LDS (no bank conflicts).  Thread t:
+// rows t / 16 + (NTH / 16) u, chunks t % 16 + 16 h (32 chunks per row and step).
+// Chunk c holds x[8 c .. 8 c + 7], or for split-B types the two 4-value groups that
+// split_pos puts there: x[32 (c / 4) + 4 (c % 4) + e] and x[32 (c / 4) + 16 + 4 (c % 4) + e].
+template <int BM, int NTH, bool SPLIT>
+struct XStage {
+    static constexpr int R = NTH / 16, RP = BM / R;  // rows per pass, row passes
+    static_assert(RP >= 1 && BM % R == 0, "X tile / thread count");
+    float4 v[RP][2][2];  // [row pass][chunk h][half]
+    const float *src[RP];
+    bool ok[RP];
+    int cl, rg;
+    __device__ void init(const float *x, int ldx, int m0, int M, int t) {
+        cl = t & 15, rg = t >> 4;
+#pragma unroll
+        for (int u = 0; u < RP; ++u) {
+            const int m = m0 + rg + R * u;
+            ok[u] = m < M;
+            src[u] = x + size_t(ok[u] ? m : 0) * ldx;
+        }
+    }
+    __device__ static int koff(int c, int half) {
+        if constexpr (SPLIT) return 32 * (c >> 2) + 16 * half + 4 * (c & 3);
+        else return 8 * c + 4 * half;
+    }
+    __device__ void load(int kb) {
+#pragma unroll
+        for (int u = 0; u < RP; ++u)
+#pragma unroll
+            for (int h = 0; h < 2; ++h)
+#pragma unroll
+                for (int f = 0; f < 2; ++f)
+                    v[u][h][f] = ok[u] ? *reinterpret_cast<const float4 *>(src[u] + size_t(kb) * kStep +
+                                                                         koff(cl + 16 * h, f))
+                                       : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+    template <bool SUMS>
+    __device__ void store(_Float16 *xh, _Float16 *xl, float *xsum) const {
+#pragma unroll
+        for (int u = 0; u < RP; ++u)
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                const int m = rg + R * u, c = cl + 16 * h;
+                const float e[8] = {v[u][h][0].x, v[u][h][0].y, v[u][h][0].z, v[u][h][0].w,
+                                    v[u][h][1].x, v[u][h][1].y, v[u][h][1].z, v[u][h][1].w};
+                h8_t hv, lv;
+#pragma unroll
+                for (int i = 0; i < 8; ++i) {
+                    hv[i] = _Float16(e[i]);
+                    lv[i] = _Float16(e[i] - float(hv[i]));
+                }
+                *reinterpret_cast<h8_t *>(xh + m * kXS + 8 * c) = hv;
+                *reinterpret_cast<h8_t *>(xl + m * kXS + 8 * c) = lv;
+                if constexpr (SUMS) {  // 16-value sums: this chunk and the next (lane cl ^ 1)
+                    float sm = ((e[0] + e[1]) + (e[2] + e[3])) + ((e[4] + e[5]) + (e[6] + e[7]));
+                    sm += dpp_mov<kDppXor1>(sm);
+                    if (!(cl & 1)) xsum[(c >> 1) * BM + m] = sm;
+                }
+            }
+    }
+};
 
 struct MfmaArgs {
     WPtr w;
@@ -44,8 +120,6 @@ template <int T, int BM, bool TL>
 __global__ __launch_bounds__(256) void k_mfma(MfmaArgs a) {
     using W = MW<T>;
     constexpr int MT = BM / 16;     // 16-row tiles of X
-    constexpr int FPT = BM;         // X values staged per thread and step (BM * 256 / 256)
-    constexpr int TPR = 256 / BM;   // threads per X row
     __shared__ _Float16 xh[BM * kXS], xl[BM * kXS];
     __shared__ float xsum[16 * BM];  // [16-slice][m]
     const int t = threadIdx.x, lane = t & 63, w = t >> 6;
@@ -56,38 +130,10 @@ __global__ __launch_bounds__(256) void k_mfma(MfmaArgs a) {
     const int nsteps = a.w.K / kStep, ks = gridDim.z;
     const int kb0 = int(blockIdx.z) * nsteps / ks, kb1 = (int(blockIdx.z) + 1) * nsteps / ks;
 
-    // X staging: thread t owns row m0 + t / TPR, values [(t % TPR) FPT, +FPT) of the step
-    const int xm = t / TPR, xk = (t % TPR) * FPT;
-    const bool xrow_ok = m0 + xm < a.M;
-    const float *xsrc = a.x + size_t(xrow_ok ? m0 + xm : 0) * a.ldx + xk;
-    float4 xr[FPT / 4];
-    auto load_x = [&](int kb) {
-#pragma unroll
-        for (int i = 0; i < FPT / 4; ++i)
-            xr[i] = xrow_ok ? *reinterpret_cast<const float4 *>(xsrc + size_t(kb) * kStep + 4 * i)
-                            : make_float4(0.f, 0.f, 0.f, 0.f);
-    };
-    auto stage_x = [&] {
-#pragma unroll
-        for (int i = 0; i < FPT / 4; ++i) {
-            const float v[4] = {xr[i].x, xr[i].y, xr[i].z, xr[i].w};
-            _Float16 hv[4], lv[4];
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                hv[e] = _Float16(v[e]);
-                lv[e] = _Float16(v[e] - float(hv[e]));
-            }
-            *reinterpret_cast<h4_t *>(xh + xm * kXS + xk + 4 * i) = h4_t{hv[0], hv[1], hv[2], hv[3]};
-            *reinterpret_cast<h4_t *>(xl + xm * kXS + xk + 4 * i) = h4_t{lv[0], lv[1], lv[2], lv[3]};
-        }
-#pragma unroll
-        for (int j = 0; j < FPT / 16; ++j) {
-            float s = 0.f;
-#pragma unroll
-            for (int i = 0; i < 4; ++i) s += (xr[4 * j + i].x + xr[4 * j + i].y) + (xr[4 * j + i].z + xr[4 * j + i].w);
-            xsum[((xk >> 4) + j) * BM + xm] = s;
-        }
-    };
+    XStage<BM, 256, W::SPLIT> xs;
+    xs.init(a.x, a.ldx, m0, a.M, t);
+    auto load_x = [&](int kb) { xs.load(kb); };
+    auto stage_x = [&] { xs.template store<W::MIN>(xh, xl, xsum); };
 
     f4_t acc[MT];
 #pragma unroll
@@ -104,39 +150,62 @@ __global__ __launch_bounds__(256) void k_mfma(MfmaArgs a) {
             load_w<T, TL>(a.w, n0 >> 4, ln, kb + 1, kq, nxt);
             load_x(kb + 1);
         }
+        if constexpr (W::SPLIT) {
+            // the block's 8 split-B slices chain in the MFMA's C operand; d once per block
+            f4_t cb[MT];
 #pragma unroll
-        for (int s = 0; s < W::SLICES; ++s) {
-            float sc, mn;
-            W::scale(cur, s, sc, mn);
-            const auto bop = W::b(cur, s);
+            for (int s = 0; s < W::SLICES32; ++s) {
+                h8_t bh, bl;
+                W::b_split(cur, s, bh, bl);
 #pragma unroll
-            for (int mt = 0; mt < MT; ++mt) {
-                const int xo = (mt * 16 + ln) * kXS + s * W::SK + kq * (W::SK / 4);
-                f4_t tmp = f4_t{0.f, 0.f, 0.f, 0.f};
-                if constexpr (W::SK == 32) {
+                for (int mt = 0; mt < MT; ++mt) {
+                    const int xo = (mt * 16 + ln) * kXS + 32 * s + 8 * kq;
                     const h8_t ah = *reinterpret_cast<const h8_t *>(xh + xo), al = *reinterpret_cast<const h8_t *>(xl + xo);
-                    tmp = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bop, tmp, 0, 0, 0);
-                    tmp = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, bop, tmp, 0, 0, 0);
-                } else {
-                    const h4_t ah = *reinterpret_cast<const h4_t *>(xh + xo), al = *reinterpret_cast<const h4_t *>(xl + xo);
-                    tmp = __builtin_amdgcn_mfma_f32_16x16x16f16(ah, bop, tmp, 0, 0, 0);
-                    tmp = __builtin_amdgcn_mfma_f32_16x16x16f16(al, bop, tmp, 0, 0, 0);
+                    cb[mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bh, s ? cb[mt] : f4_t{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+                    cb[mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, bh, cb[mt], 0, 0, 0);
+                    cb[mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bl, cb[mt], 0, 0, 0);
                 }
-                // output rows m = mt 16 + 4 kq + r of this lane; x sums of the slice
-                if constexpr (W::MIN) {
-                    const float *xsp = xsum + (s * W::SK / 16) * BM + mt * 16 + 4 * kq;
-                    float4 xsv = *reinterpret_cast<const float4 *>(xsp);
-                    if constexpr (W::SK == 32) {
-                        const float4 x2 = *reinterpret_cast<const float4 *>(xsp + BM);
-                        xsv = make_float4(xsv.x + x2.x, xsv.y + x2.y, xsv.z + x2.z, xsv.w + x2.w);
-                    }
-                    acc[mt][0] = fmaf(sc, tmp[0], fmaf(-mn, xsv.x, acc[mt][0]));
-                    acc[mt][1] = fmaf(sc, tmp[1], fmaf(-mn, xsv.y, acc[mt][1]));
-                    acc[mt][2] = fmaf(sc, tmp[2], fmaf(-mn, xsv.z, acc[mt][2]));
-                    acc[mt][3] = fmaf(sc, tmp[3], fmaf(-mn, xsv.w, acc[mt][3]));
-                } else {
+            }
+            const float d = W::d_of(cur);
 #pragma unroll
-                    for (int r = 0; r < 4; ++r) acc[mt][r] = fmaf(sc, tmp[r], acc[mt][r]);
+            for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) acc[mt][r] = fmaf(d, cb[mt][r], acc[mt][r]);
+        } else {
+#pragma unroll
+            for (int s = 0; s < W::SLICES; ++s) {
+                float sc, mn;
+                W::scale(cur, s, sc, mn);
+                const auto bop = W::b(cur, s);
+#pragma unroll
+                for (int mt = 0; mt < MT; ++mt) {
+                    const int xo = (mt * 16 + ln) * kXS + s * W::SK + kq * (W::SK / 4);
+                    f4_t tmp = f4_t{0.f, 0.f, 0.f, 0.f};
+                    if constexpr (W::SK == 32) {
+                        const h8_t ah = *reinterpret_cast<const h8_t *>(xh + xo), al = *reinterpret_cast<const h8_t *>(xl + xo);
+                        tmp = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bop, tmp, 0, 0, 0);
+                        tmp = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, bop, tmp, 0, 0, 0);
+                    } else {
+                        const h4_t ah = *reinterpret_cast<const h4_t *>(xh + xo), al = *reinterpret_cast<const h4_t *>(xl + xo);
+                        tmp = __builtin_amdgcn_mfma_f32_16x16x16f16(ah, bop, tmp, 0, 0, 0);
+                        tmp = __builtin_amdgcn_mfma_f32_16x16x16f16(al, bop, tmp, 0, 0, 0);
+                    }
+                    // output rows m = mt 16 + 4 kq + r of this lane; x sums of the slice
+                    if constexpr (W::MIN) {
+                        const float *xsp = xsum + (s * W::SK / 16) * BM + mt * 16 + 4 * kq;
+                        float4 xsv = *reinterpret_cast<const float4 *>(xsp);
+                        if constexpr (W::SK == 32) {
+                            const float4 x2 = *reinterpret_cast<const float4 *>(xsp + BM);
+                            xsv = make_float4(xsv.x + x2.x, xsv.y + x2.y, xsv.z + x2.z, xsv.w + x2.w);
+                        }
+                        acc[mt][0] = fmaf(sc, tmp[0], fmaf(-mn, xsv.x, acc[mt][0]));
+                        acc[mt][1] = fmaf(sc, tmp[1], fmaf(-mn, xsv.y, acc[mt][1]));
+                        acc[mt][2] = fmaf(sc, tmp[2], fmaf(-mn, xsv.z, acc[mt][2]));
+                        acc[mt][3] = fmaf(sc, tmp[3], fmaf(-mn, xsv.w, acc[mt][3]));
+                    } else {
+#pragma unroll
+                        for (int r = 0; r < 4; ++r) acc[mt][r] = fmaf(sc, tmp[r], acc[mt][r]);
+                    }
                 }
             }
         }
@@ -209,8 +278,6 @@ __global__ __launch_bounds__(512) void k_mfma_w(MfmaArgs a) {
     using W = MW<T>;
     constexpr int MT = BM / 16;
     constexpr int NTH = kWWaves * 64;
-    constexpr int FPT = BM * kStep / NTH;  // X values staged per thread and step
-    constexpr int TPR = NTH / BM;          // threads per X row
     extern __shared__ __align__(16) unsigned char wlds[];
     _Float16 *xh = reinterpret_cast<_Float16 *>(wlds);
     _Float16 *xl = xh + BM * kXS;
@@ -222,37 +289,10 @@ __global__ __launch_bounds__(512) void k_mfma_w(MfmaArgs a) {
     const int nsteps = a.w.K / kStep, ks = gridDim.z;
     const int kb0 = int(blockIdx.z) * nsteps / ks, kb1 = (int(blockIdx.z) + 1) * nsteps / ks;
 
-    const int xm = t / TPR, xk = (t % TPR) * FPT;
-    const bool xrow_ok = m0 + xm < a.M;
-    const float *xsrc = a.x + size_t(xrow_ok ? m0 + xm : 0) * a.ldx + xk;
-    float4 xr[FPT / 4];
-    auto load_x = [&](int kb) {
-#pragma unroll
-        for (int i = 0; i < FPT / 4; ++i)
-            xr[i] = xrow_ok ? *reinterpret_cast<const float4 *>(xsrc + size_t(kb) * kStep + 4 * i)
-                            : make_float4(0.f, 0.f, 0.f, 0.f);
-    };
-    auto stage_x = [&] {
-#pragma unroll
-        for (int i = 0; i < FPT / 4; ++i) {
-            const float v[4] = {xr[i].x, xr[i].y, xr[i].z, xr[i].w};
-            _Float16 hv[4], lv[4];
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                hv[e] = _Float16(v[e]);
-                lv[e] = _Float16(v[e] - float(hv[e]));
-            }
-            *reinterpret_cast<h4_t *>(xh + xm * kXS + xk + 4 * i) = h4_t{hv[0], hv[1], hv[2], hv[3]};
-            *reinterpret_cast<h4_t *>(xl + xm * kXS + xk + 4 * i) = h4_t{lv[0], lv[1], lv[2], lv[3]};
-        }
-#pragma unroll
-        for (int j = 0; j < FPT / 16; ++j) {
-            float s = 0.f;
-#pragma unroll
-            for (int i = 0; i < 4; ++i) s += (xr[4 * j + i].x + xr[4 * j + i].y) + (xr[4 * j + i].z + xr[4 * j + i].w);
-            xsum[((xk >> 4) + j) * BM + xm] = s;
-        }
-    };
+    XStage<BM, NTH, W::SPLIT> xs;
+    xs.init(a.x, a.ldx, m0, a.M, t);
+    auto load_x = [&](int kb) { xs.load(kb); };
+    auto stage_x = [&] { xs.template store<W::MIN>(xh, xl, xsum); };
 
     f4_t acc[WT][MT];
 #pragma unroll
@@ -273,56 +313,99 @@ __global__ __launch_bounds__(512) void k_mfma_w(MfmaArgs a) {
             for (int j = 0; j < WT; ++j) load_w<T, TL>(a.w, (n0 >> 4) + j, ln, kb + 1, kq, nxt[j]);
             load_x(kb + 1);
         }
+        if constexpr (W::SPLIT) {
+            // the block's 8 split-B slices chain in the MFMA's C operand; d once per block
+            f4_t cb[WT][MT];
+            // A fragments of slice s + 1 are read from LDS while slice s runs on the MFMA
+            h8_t ahs[2][MT], als[2][MT];
+            auto read_a = [&](int s, h8_t (&ah)[MT], h8_t (&al)[MT]) {
 #pragma unroll
-        for (int s = 0; s < W::SLICES; ++s) {
-            float sc[WT], mn[WT];
-            decltype(W::b(cur[0], 0)) bop[WT];
+                for (int mt = 0; mt < MT; ++mt) {
+                    const int xo = (mt * 16 + ln) * kXS + 32 * s + 8 * kq;
+                    ah[mt] = *reinterpret_cast<const h8_t *>(xh + xo);
+                    al[mt] = *reinterpret_cast<const h8_t *>(xl + xo);
+                }
+            };
+            read_a(0, ahs[0], als[0]);
 #pragma unroll
-            for (int j = 0; j < WT; ++j) {
-                W::scale(cur[j], s, sc[j], mn[j]);
-                bop[j] = W::b(cur[j], s);
+            for (int s = 0; s < W::SLICES32; ++s) {
+                if (s + 1 < W::SLICES32) read_a(s + 1, ahs[(s + 1) & 1], als[(s + 1) & 1]);
+                h8_t bh[WT], bl[WT];
+#pragma unroll
+                for (int j = 0; j < WT; ++j) W::b_split(cur[j], s, bh[j], bl[j]);
+#pragma unroll
+                for (int mt = 0; mt < MT; ++mt) {
+                    const h8_t ah = ahs[s & 1][mt], al = als[s & 1][mt];
+#pragma unroll
+                    for (int j = 0; j < WT; ++j)
+                        cb[j][mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bh[j], s ? cb[j][mt] : f4_t{0.f, 0.f, 0.f, 0.f},
+                                                                          0, 0, 0);
+#pragma unroll
+                    for (int j = 0; j < WT; ++j) cb[j][mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, bh[j], cb[j][mt], 0, 0, 0);
+#pragma unroll
+                    for (int j = 0; j < WT; ++j) cb[j][mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bl[j], cb[j][mt], 0, 0, 0);
+                }
             }
 #pragma unroll
-            for (int mt = 0; mt < MT; ++mt) {
-                const int xo = (mt * 16 + ln) * kXS + s * W::SK + kq * (W::SK / 4);
-                float4 xsv = make_float4(0.f, 0.f, 0.f, 0.f);
-                if constexpr (W::MIN) {
-                    const float *xsp = xsum + (s * W::SK / 16) * BM + mt * 16 + 4 * kq;
-                    xsv = *reinterpret_cast<const float4 *>(xsp);
-                    if constexpr (W::SK == 32) {
-                        const float4 x2 = *reinterpret_cast<const float4 *>(xsp + BM);
-                        xsv = make_float4(xsv.x + x2.x, xsv.y + x2.y, xsv.z + x2.z, xsv.w + x2.w);
-                    }
+            for (int j = 0; j < WT; ++j) {
+                const float d = W::d_of(cur[j]);
+#pragma unroll
+                for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) acc[j][mt][r] = fmaf(d, cb[j][mt][r], acc[j][mt][r]);
+            }
+        } else {
+#pragma unroll
+            for (int s = 0; s < W::SLICES; ++s) {
+                float sc[WT], mn[WT];
+                decltype(W::b(cur[0], 0)) bop[WT];
+#pragma unroll
+                for (int j = 0; j < WT; ++j) {
+                    W::scale(cur[j], s, sc[j], mn[j]);
+                    bop[j] = W::b(cur[j], s);
                 }
-                // acc += sc tmp (- mn xsum for the formats with mins)
-                auto scale_add = [&](f4_t &a4, const f4_t &tmp, float scj, float mnj) {
+#pragma unroll
+                for (int mt = 0; mt < MT; ++mt) {
+                    const int xo = (mt * 16 + ln) * kXS + s * W::SK + kq * (W::SK / 4);
+                    float4 xsv = make_float4(0.f, 0.f, 0.f, 0.f);
                     if constexpr (W::MIN) {
-                        a4[0] = fmaf(scj, tmp[0], fmaf(-mnj, xsv.x, a4[0]));
-                        a4[1] = fmaf(scj, tmp[1], fmaf(-mnj, xsv.y, a4[1]));
-                        a4[2] = fmaf(scj, tmp[2], fmaf(-mnj, xsv.z, a4[2]));
-                        a4[3] = fmaf(scj, tmp[3], fmaf(-mnj, xsv.w, a4[3]));
+                        const float *xsp = xsum + (s * W::SK / 16) * BM + mt * 16 + 4 * kq;
+                        xsv = *reinterpret_cast<const float4 *>(xsp);
+                        if constexpr (W::SK == 32) {
+                            const float4 x2 = *reinterpret_cast<const float4 *>(xsp + BM);
+                            xsv = make_float4(xsv.x + x2.x, xsv.y + x2.y, xsv.z + x2.z, xsv.w + x2.w);
+                        }
+                    }
+                    // acc += sc tmp (- mn xsum for the formats with mins)
+                    auto scale_add = [&](f4_t &a4, const f4_t &tmp, float scj, float mnj) {
+                        if constexpr (W::MIN) {
+                            a4[0] = fmaf(scj, tmp[0], fmaf(-mnj, xsv.x, a4[0]));
+                            a4[1] = fmaf(scj, tmp[1], fmaf(-mnj, xsv.y, a4[1]));
+                            a4[2] = fmaf(scj, tmp[2], fmaf(-mnj, xsv.z, a4[2]));
+                            a4[3] = fmaf(scj, tmp[3], fmaf(-mnj, xsv.w, a4[3]));
+                        } else {
+#pragma unroll
+                            for (int r = 0; r < 4; ++r) a4[r] = fmaf(scj, tmp[r], a4[r]);
+                        }
+                    };
+                    if constexpr (W::SK == 32) {
+                        const h8_t ah = *reinterpret_cast<const h8_t *>(xh + xo), al = *reinterpret_cast<const h8_t *>(xl + xo);
+#pragma unroll
+                        for (int j = 0; j < WT; ++j) {
+                            f4_t tmp = f4_t{0.f, 0.f, 0.f, 0.f};
+                            tmp = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bop[j], tmp, 0, 0, 0);
+                            tmp = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, bop[j], tmp, 0, 0, 0);
+                            scale_add(acc[j][mt], tmp, sc[j], mn[j]);
+                        }
                     } else {
+                        const h4_t ah = *reinterpret_cast<const h4_t *>(xh + xo), al = *reinterpret_cast<const h4_t *>(xl + xo);
 #pragma unroll
-                        for (int r = 0; r < 4; ++r) a4[r] = fmaf(scj, tmp[r], a4[r]);
-                    }
-                };
-                if constexpr (W::SK == 32) {
-                    const h8_t ah = *reinterpret_cast<const h8_t *>(xh + xo), al = *reinterpret_cast<const h8_t *>(xl + xo);
-#pragma unroll
-                    for (int j = 0; j < WT; ++j) {
-                        f4_t tmp = f4_t{0.f, 0.f, 0.f, 0.f};
-                        tmp = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bop[j], tmp, 0, 0, 0);
-                        tmp = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, bop[j], tmp, 0, 0, 0);
-                        scale_add(acc[j][mt], tmp, sc[j], mn[j]);
-                    }
-                } else {
-                    const h4_t ah = *reinterpret_cast<const h4_t *>(xh + xo), al = *reinterpret_cast<const h4_t *>(xl + xo);
-#pragma unroll
-                    for (int j = 0; j < WT; ++j) {
-                        f4_t tmp = f4_t{0.f, 0.f, 0.f, 0.f};
-                        tmp = __builtin_amdgcn_mfma_f32_16x16x16f16(ah, bop[j], tmp, 0, 0, 0);
-                        tmp = __builtin_amdgcn_mfma_f32_16x16x16f16(al, bop[j], tmp, 0, 0, 0);
-                        scale_add(acc[j][mt], tmp, sc[j], mn[j]);
+                        for (int j = 0; j < WT; ++j) {
+                            f4_t tmp = f4_t{0.f, 0.f, 0.f, 0.f};
+                            tmp = __builtin_amdgcn_mfma_f32_16x16x16f16(ah, bop[j], tmp, 0, 0, 0);
+                            tmp = __builtin_amdgcn_mfma_f32_16x16x16f16(al, bop[j], tmp, 0, 0, 0);
+                            scale_add(acc[j][mt], tmp, sc[j], mn[j]);
+                        }
                     }
                 }
             }
@@ -577,8 +660,9 @@ __global__ __launch_bounds__(kRxWaves * 64) void k_mfma_rx(RxArgs a) {
                         hv[q] = _Float16(e[q]);
                         lv[q] = _Float16(e[q] - float(hv[q]));
                     }
-                    *reinterpret_cast<h4_t *>(xh + m * XS + k0 + 4 * i) = h4_t{hv[0], hv[1], hv[2], hv[3]};
-                    *reinterpret_cast<h4_t *>(xl + m * XS + k0 + 4 * i) = h4_t{lv[0], lv[1], lv[2], lv[3]};
+                    const int kp = staged_k<W::SPLIT>(k0 + 4 * i);
+                    *reinterpret_cast<h4_t *>(xh + m * XS + kp) = h4_t{hv[0], hv[1], hv[2], hv[3]};
+                    *reinterpret_cast<h4_t *>(xl + m * XS + kp) = h4_t{lv[0], lv[1], lv[2], lv[3]};
                     sum += (e[0] + e[1]) + (e[2] + e[3]);
                 }
                 xsum[(k0 >> 4) * BM + m] = sum;
@@ -617,51 +701,96 @@ __global__ __launch_bounds__(kRxWaves * 64) void k_mfma_rx(RxArgs a) {
     // each X fragment read from LDS feeds kRxNT tiles of W
     auto job = [&](int j, const typename W::Regs (&cur)[kRxNT]) {
         const int kb = j % nsteps;
+        if constexpr (W::SPLIT) {
+            // the block's 8 split-B slices chain in the MFMA's C operand; d once per block
+            f4_t cb[MT][kRxNT];
+            // A fragments of slice s + 1 are read from LDS while slice s runs on the MFMA
+            h8_t ahs[2][MT], als[2][MT];
+            auto read_a = [&](int s, h8_t (&ah)[MT], h8_t (&al)[MT]) {
 #pragma unroll
-        for (int s = 0; s < W::SLICES; ++s) {
-            float sc[kRxNT], mn[kRxNT];
-            decltype(W::b(cur[0], s)) bop[kRxNT];
+                for (int mt = 0; mt < MT; ++mt) {
+                    const int xo = (mt * 16 + ln) * XS + kb * kStep + 32 * s + 8 * kq;
+                    ah[mt] = *reinterpret_cast<const h8_t *>(xh + xo);
+                    al[mt] = *reinterpret_cast<const h8_t *>(xl + xo);
+                }
+            };
+            read_a(0, ahs[0], als[0]);
+#pragma unroll
+            for (int s = 0; s < W::SLICES32; ++s) {
+                if (s + 1 < W::SLICES32) read_a(s + 1, ahs[(s + 1) & 1], als[(s + 1) & 1]);
+                h8_t bh[kRxNT], bl[kRxNT];
+#pragma unroll
+                for (int nt = 0; nt < kRxNT; ++nt) W::b_split(cur[nt], s, bh[nt], bl[nt]);
+#pragma unroll
+                for (int mt = 0; mt < MT; ++mt) {
+                    const h8_t ah = ahs[s & 1][mt], al = als[s & 1][mt];
+#pragma unroll
+                    for (int nt = 0; nt < kRxNT; ++nt)
+                        cb[mt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+                            ah, bh[nt], s ? cb[mt][nt] : f4_t{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+#pragma unroll
+                    for (int nt = 0; nt < kRxNT; ++nt)
+                        cb[mt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, bh[nt], cb[mt][nt], 0, 0, 0);
+#pragma unroll
+                    for (int nt = 0; nt < kRxNT; ++nt)
+                        cb[mt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bl[nt], cb[mt][nt], 0, 0, 0);
+                }
+            }
 #pragma unroll
             for (int nt = 0; nt < kRxNT; ++nt) {
-                W::scale(cur[nt], s, sc[nt], mn[nt]);
-                bop[nt] = W::b(cur[nt], s);
+                const float d = W::d_of(cur[nt]);
+#pragma unroll
+                for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) acc[mt][nt][r] = fmaf(d, cb[mt][nt][r], acc[mt][nt][r]);
             }
-            const int kx = kb * kStep + s * W::SK;
+        } else {
 #pragma unroll
-            for (int mt = 0; mt < MT; ++mt) {
-                const int xo = (mt * 16 + ln) * XS + kx + kq * (W::SK / 4);
-                const float *xsp = xsum + (kx >> 4) * BM + mt * 16 + 4 * kq;
-                float4 xsv = make_float4(0.f, 0.f, 0.f, 0.f);
-                if constexpr (W::MIN) {
-                    xsv = *reinterpret_cast<const float4 *>(xsp);
-                    if constexpr (W::SK == 32) {
-                        const float4 x2 = *reinterpret_cast<const float4 *>(xsp + BM);
-                        xsv = make_float4(xsv.x + x2.x, xsv.y + x2.y, xsv.z + x2.z, xsv.w + x2.w);
-                    }
+            for (int s = 0; s < W::SLICES; ++s) {
+                float sc[kRxNT], mn[kRxNT];
+                decltype(W::b(cur[0], s)) bop[kRxNT];
+#pragma unroll
+                for (int nt = 0; nt < kRxNT; ++nt) {
+                    W::scale(cur[nt], s, sc[nt], mn[nt]);
+                    bop[nt] = W::b(cur[nt], s);
                 }
-                if constexpr (W::SK == 32) {
-                    const h8_t ah = *reinterpret_cast<const h8_t *>(xh + xo), al = *reinterpret_cast<const h8_t *>(xl + xo);
+                const int kx = kb * kStep + s * W::SK;
 #pragma unroll
-                    for (int nt = 0; nt < kRxNT; ++nt) {
-                        f4_t tmp = f4_t{0.f, 0.f, 0.f, 0.f};
-                        tmp = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bop[nt], tmp, 0, 0, 0);
-                        tmp = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, bop[nt], tmp, 0, 0, 0);
-#pragma unroll
-                        for (int r = 0; r < 4; ++r)
-                            acc[mt][nt][r] = W::MIN ? fmaf(sc[nt], tmp[r], fmaf(-mn[nt], (&xsv.x)[r], acc[mt][nt][r]))
-                                                    : fmaf(sc[nt], tmp[r], acc[mt][nt][r]);
+                for (int mt = 0; mt < MT; ++mt) {
+                    const int xo = (mt * 16 + ln) * XS + kx + kq * (W::SK / 4);
+                    const float *xsp = xsum + (kx >> 4) * BM + mt * 16 + 4 * kq;
+                    float4 xsv = make_float4(0.f, 0.f, 0.f, 0.f);
+                    if constexpr (W::MIN) {
+                        xsv = *reinterpret_cast<const float4 *>(xsp);
+                        if constexpr (W::SK == 32) {
+                            const float4 x2 = *reinterpret_cast<const float4 *>(xsp + BM);
+                            xsv = make_float4(xsv.x + x2.x, xsv.y + x2.y, xsv.z + x2.z, xsv.w + x2.w);
+                        }
                     }
-                } else {
-                    const h4_t ah = *reinterpret_cast<const h4_t *>(xh + xo), al = *reinterpret_cast<const h4_t *>(xl + xo);
+                    if constexpr (W::SK == 32) {
+                        const h8_t ah = *reinterpret_cast<const h8_t *>(xh + xo), al = *reinterpret_cast<const h8_t *>(xl + xo);
 #pragma unroll
-                    for (int nt = 0; nt < kRxNT; ++nt) {
-                        f4_t tmp = f4_t{0.f, 0.f, 0.f, 0.f};
-                        tmp = __builtin_amdgcn_mfma_f32_16x16x16f16(ah, bop[nt], tmp, 0, 0, 0);
-                        tmp = __builtin_amdgcn_mfma_f32_16x16x16f16(al, bop[nt], tmp, 0, 0, 0);
+                        for (int nt = 0; nt < kRxNT; ++nt) {
+                            f4_t tmp = f4_t{0.f, 0.f, 0.f, 0.f};
+                            tmp = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bop[nt], tmp, 0, 0, 0);
+                            tmp = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, bop[nt], tmp, 0, 0, 0);
 #pragma unroll
-                        for (int r = 0; r < 4; ++r)
-                            acc[mt][nt][r] = W::MIN ? fmaf(sc[nt], tmp[r], fmaf(-mn[nt], (&xsv.x)[r], acc[mt][nt][r]))
-                                                    : fmaf(sc[nt], tmp[r], acc[mt][nt][r]);
+                            for (int r = 0; r < 4; ++r)
+                                acc[mt][nt][r] = W::MIN ? fmaf(sc[nt], tmp[r], fmaf(-mn[nt], (&xsv.x)[r], acc[mt][nt][r]))
+                                                        : fmaf(sc[nt], tmp[r], acc[mt][nt][r]);
+                        }
+                    } else {
+                        const h4_t ah = *reinterpret_cast<const h4_t *>(xh + xo), al = *reinterpret_cast<const h4_t *>(xl + xo);
+#pragma unroll
+                        for (int nt = 0; nt < kRxNT; ++nt) {
+                            f4_t tmp = f4_t{0.f, 0.f, 0.f, 0.f};
+                            tmp = __builtin_amdgcn_mfma_f32_16x16x16f16(ah, bop[nt], tmp, 0, 0, 0);
+                            tmp = __builtin_amdgcn_mfma_f32_16x16x16f16(al, bop[nt], tmp, 0, 0, 0);
+#pragma unroll
+                            for (int r = 0; r < 4; ++r)
+                                acc[mt][nt][r] = W::MIN ? fmaf(sc[nt], tmp[r], fmaf(-mn[nt], (&xsv.x)[r], acc[mt][nt][r]))
+                                                        : fmaf(sc[nt], tmp[r], acc[mt][nt][r]);
+                        }
                     }
                 }
             }

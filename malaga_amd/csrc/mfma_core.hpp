@@ -2,7 +2,9 @@
 // the integer quants (q4_K / q5_K nibbles, q6_K 6-bit values - 32, q8_0 int8) are exact
 // in f16, so they are the B operand as they are; block scales and k-quant mins are
 // applied per sub-block in f32 by the caller:
-//   sum_k w_k x_k = d sc * sum_k q_k x_k - dmin m * sum_k x_k.
+//   sum_k w_k x_k = d sc * sum_k q_k x_k - dmin m * sum_k x_k,
+// or folded into B where that stays exact (FOLD: q4_K / q5_K in the decode GEMMs;
+// SPLIT: q6_K as an exact f16 pair in the prefill / LM-head GEMMs).
 // B-operand layout (16x16x32 / 16x16x16 f16 MFMA): lane l holds W row l % 16 and the
 // k-group l / 16 of the sub-block.  Quant bytes become f16 with v_perm
 // (byte -> 0x64xx = 1024 + byte) and one packed f16 subtraction.
@@ -96,6 +98,7 @@ struct MW<GGML_Q4_K> {
         mn = h2f(r.hdr.x >> 16) * m;
     }
     static constexpr bool FOLD = true;
+    static constexpr bool SPLIT = false;
     __device__ static void scale_min_h(const Regs &r, int s, _Float16 &a, _Float16 &m) {
         uint32_t ai, mi;
         k4_scale_min_u(s, r.hdr.y, r.hdr.z, r.hdr.w, ai, mi);
@@ -135,6 +138,7 @@ struct MW<GGML_Q5_K> {
         MW<GGML_Q4_K>::scale(t, s, sc, mn);
     }
     static constexpr bool FOLD = true;
+    static constexpr bool SPLIT = false;
     __device__ static void scale_min_h(const Regs &r, int s, _Float16 &a, _Float16 &m) {
         MW<GGML_Q4_K>::Regs t{r.hdr, {}};
         MW<GGML_Q4_K>::scale_min_h(t, s, a, m);
@@ -153,7 +157,9 @@ struct MW<GGML_Q6_K> {
     struct Regs {
         uint32_t qa[4], qb[4], qh[4];  // [2 n + h]
         uint4 sc;
-        uint32_t d;
+        // 16 bits as loaded: a 32-bit field would be zero-extended right after the load,
+        // which makes the wave wait for its prefetched block before computing this one
+        unsigned short d;
     };
     __device__ static void load(const WPtr &w, int row, int kb, int kq, Regs &r) {
         const size_t blk = size_t(row) * w.nb + kb;
@@ -194,7 +200,34 @@ struct MW<GGML_Q6_K> {
         sc = h2f(r.d) * float(int8_t(wv >> (8 * (G & 3))));
         mn = 0.f;
     }
+    // Split-B slices (SPLIT): the 16x16x32 MFMA over the two groups 2 s and 2 s + 1 of
+    // 32-slice s, with the int8 group scale folded into B.  |q sc| <= 32 * 128 = 4096 is
+    // an integer, so bh = f16(q sc) (one rounding) and bl = q sc - bh (in {-1, 0, 1}) are
+    // exact and sum to q sc; with x = xh + xl the product is xh bh + xl bh + xh bl up to
+    // xl bl (<= 2^-22 |x q sc|).  The lane keeps its registers: elements 0..3 are
+    // j = 4 kq .. 4 kq + 3 of group 2 s, elements 4..7 the same j of group 2 s + 1, so the
+    // A fragment of lane k-group kq is x[32 s + 4 kq + e] then x[32 s + 16 + 4 kq + e]
+    // (split_pos gives where the staged X keeps them).  Per block then
+    //   sum_k w_k x_k = d C,   C = sum_s (xh bh_s + xl bh_s + xh bl_s)   (MFMA C operand).
+    static constexpr bool SPLIT = true;
+    static constexpr int SLICES32 = 8;
+    __device__ static void b_split(const Regs &r, int s, h8_t &bh, h8_t &bl) {
+        const h4_t q0 = b(r, 2 * s), q1 = b(r, 2 * s + 1);
+        const uint32_t wv = s < 4 ? (s < 2 ? r.sc.x : r.sc.y) : (s < 6 ? r.sc.z : r.sc.w);
+        const int sh = 16 * (s & 1);
+        const _Float16 f0 = _Float16(float(int8_t(wv >> sh))), f1 = _Float16(float(int8_t(wv >> (sh + 8))));
+        const h8_t q = {q0[0], q0[1], q0[2], q0[3], q1[0], q1[1], q1[2], q1[3]};
+        const h8_t sc = {f0, f0, f0, f0, f1, f1, f1, f1};
+        bh = q * sc;
+        bl = __builtin_elementwise_fma(q, sc, -bh);
+    }
+    __device__ static float d_of(const Regs &r) { return h2f(r.d); }
 };
+
+// Position in the staged X of the 4-value group g4 (0..7) of a 32-slice for split-B
+// slices: group g4 < 4 sits at 2 g4, group 4 + g at 2 g + 1, so lane k-group kq reads
+// its A fragment (groups kq and 4 + kq) as the 8 halves at 8 kq.
+__host__ __device__ constexpr int split_pos(int g4) { return g4 < 4 ? 2 * g4 : 2 * (g4 - 4) + 1; }
 
 // q8_0: 8 blocks of 32 per step, int8 values (q ^ 0x80 = q + 128 as a byte).
 template <>
@@ -202,6 +235,7 @@ struct MW<GGML_Q8_0> {
     static constexpr int SLICES = 8, SK = 32;
     static constexpr bool MIN = false;
     static constexpr bool FOLD = false;
+    static constexpr bool SPLIT = false;
     struct Regs {
         uint2 q[8];
         uint4 d;  // 8 f16 scales
@@ -230,6 +264,7 @@ struct MW<GGML_F16> {
     static constexpr int SLICES = 8, SK = 32;
     static constexpr bool MIN = false;
     static constexpr bool FOLD = false;
+    static constexpr bool SPLIT = false;
     struct Regs {
         uint4 q[8];
     };
