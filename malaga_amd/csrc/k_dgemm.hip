@@ -324,14 +324,18 @@ __global__ __launch_bounds__(NWL * 64) void k_dgemm(DArgs a) {
         if constexpr (W::FOLD) {
             // scales folded into B (mfma_core.hpp): the block's slices accumulate on the MFMA
             f4_t cb[NT], mb[NT];
+            FoldPrep fp[NT];
 #pragma unroll
-            for (int nt = 0; nt < NT; ++nt) cb[nt] = mb[nt] = f4_t{0.f, 0.f, 0.f, 0.f};
+            for (int nt = 0; nt < NT; ++nt) {
+                cb[nt] = mb[nt] = f4_t{0.f, 0.f, 0.f, 0.f};
+                fp[nt] = fold_prep<W>(wr[j & 1][nt]);
+            }
             static_for<0, W::SLICES>([&](auto sc) {
                 constexpr int s = decltype(sc)::value, i = j * W::SLICES + s, r = i + D;
                 h8_t ah, al;
                 dg_x32<PRO>(kb, s, kq, buf[i % D], gb, K, mrow, rrow, ah, al);
 #pragma unroll
-                for (int nt = 0; nt < NT; ++nt) fold_slice<W>(wr[j & 1][nt], s, ah, al, cb[nt], mb[nt]);
+                for (int nt = 0; nt < NT; ++nt) fold_slice<W>(wr[j & 1][nt], fp[nt], s, ah, al, cb[nt], mb[nt]);
                 if constexpr (r < NI) {
                     __builtin_amdgcn_sched_barrier(0);
                     load_x(blk(r / W::SLICES), r % W::SLICES, buf[i % D]);
@@ -589,11 +593,12 @@ __global__ __launch_bounds__(kDrxWaves * 64) void k_drx(DArgs a) {
     auto job = [&](int kb, const WR &cur) {
         if constexpr (W::FOLD) {
             f4_t cb = f4_t{0.f, 0.f, 0.f, 0.f}, mb = cb;
+            const FoldPrep fp = fold_prep<W>(cur);
 #pragma unroll
             for (int s = 0; s < W::SLICES; ++s) {
                 const int xo = ln * XS + kb * kStep + s * SK + kq * (SK / 4);
                 const h8_t ah = *reinterpret_cast<const h8_t *>(xh + xo), al = *reinterpret_cast<const h8_t *>(xl + xo);
-                fold_slice<W>(cur, s, ah, al, cb, mb);
+                fold_slice<W>(cur, fp, s, ah, al, cb, mb);
             }
             fold_flush<W>(cur, true, cb, mb, acc);
             return;
@@ -863,8 +868,12 @@ __global__ __launch_bounds__(512) void k_dxattn(DArgs a) {
     const int ar = min(ln, RG - 1);
     // k_dgemm's arithmetic for the same slices (folded for q4_K / q5_K), so q equals its q
     f4_t cb[NT], mb[NT];
+    FoldPrep fp[NT];
 #pragma unroll
-    for (int nt = 0; nt < NT; ++nt) cb[nt] = mb[nt] = f4_t{0.f, 0.f, 0.f, 0.f};
+    for (int nt = 0; nt < NT; ++nt) {
+        cb[nt] = mb[nt] = f4_t{0.f, 0.f, 0.f, 0.f};
+        if constexpr (W::FOLD) fp[nt] = fold_prep<W>(wr[nt]);
+    }
     static_for<0, W::SLICES>([&](auto sc) {
         constexpr int s = decltype(sc)::value;
         DFrag<XQ> fr;
@@ -875,7 +884,7 @@ __global__ __launch_bounds__(512) void k_dxattn(DArgs a) {
             h8_t ah, al;
             dg_x32<PRO_SPLIT>(kb, s, kq, fr, nullptr, K, 0.f, 0.f, ah, al);
 #pragma unroll
-            for (int nt = 0; nt < NT; ++nt) fold_slice<W>(wr[nt], s, ah, al, cb[nt], mb[nt]);
+            for (int nt = 0; nt < NT; ++nt) fold_slice<W>(wr[nt], fp[nt], s, ah, al, cb[nt], mb[nt]);
         } else {
             dg_slice<T, NT, PRO_SPLIT>(kb, s, kq, wr, fr, live, nullptr, K, 0.f, 0.f, acc);
         }

@@ -37,13 +37,49 @@ struct MW;  // per-type W fetch for one 256-wide K step
 // sum_k m_s x_k also runs on the MFMA (B = m_s in every element).  Per block then
 //   sum_k w_k x_k = d C - dmin M,   C = sum_s X_s (a_s q_s),   M = sum_s X_s m_s,
 // instead of two f32 FMAs per output and slice.
+//
+// The 8 sub-block scales and mins of a block are decoded once per block (fold_prep) as f16
+// pairs: pair i holds sub-blocks 2 i and 2 i + 1, and na = -1024 a.  q4_K then builds B with
+// one packed FMA per pair of values, fma(1024 + q, a, -1024 a) = q a: v_perm gives 1024 + q
+// exactly, (1024 + 15) * 63 <= 65504 stays finite, and the result q a <= 945 is exact.
+// q5_K (q <= 31 would overflow that product) subtracts 1024 first and then multiplies.
+struct FoldPrep {
+    uint32_t a[4], na[4], m[4];
+};
+// the k-quant header's 6-bit scales a_j and mins m_j (j < 8, get_scale_min_k4 in ggml's
+// k-quants) for all 8 sub-blocks at once, bytewise: j < 4 from the low 6 bits of bytes j,
+// j + 4; j >= 4 from the nibbles of byte j + 4 and the top 2 bits of bytes j - 4, j
+__device__ __forceinline__ FoldPrep k4_fold_prep(const uint4 &hdr) {
+    const uint32_t a03 = hdr.y & 0x3F3F3F3Fu, m03 = hdr.z & 0x3F3F3F3Fu;
+    const uint32_t a47 = (hdr.w & 0x0F0F0F0Fu) | ((hdr.y >> 2) & 0x30303030u);
+    const uint32_t m47 = ((hdr.w >> 4) & 0x0F0F0F0Fu) | ((hdr.z >> 2) & 0x30303030u);
+    const h2_t off = {_Float16(1024), _Float16(1024)}, neg = {_Float16(-1024), _Float16(-1024)};
+    const uint2 a0 = bytes_to_h4(a03, off), a1 = bytes_to_h4(a47, off);
+    const uint2 m0 = bytes_to_h4(m03, off), m1 = bytes_to_h4(m47, off);
+    FoldPrep p;
+    p.a[0] = a0.x, p.a[1] = a0.y, p.a[2] = a1.x, p.a[3] = a1.y;
+    p.m[0] = m0.x, p.m[1] = m0.y, p.m[2] = m1.x, p.m[3] = m1.y;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) p.na[i] = __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2_t, p.a[i]) * neg);
+    return p;
+}
+// half h of the f16 pair u in both halves
+__device__ __forceinline__ h2_t splat_half(uint32_t u, int h) {
+    const h2_t v = __builtin_bit_cast(h2_t, u);
+    return h ? __builtin_shufflevector(v, v, 1, 1) : __builtin_shufflevector(v, v, 0, 0);
+}
+
 template <class W>
-__device__ __forceinline__ void fold_slice(const typename W::Regs &r, int s, const h8_t &ah, const h8_t &al, f4_t &cb,
-                                           f4_t &mb) {
-    _Float16 a, m;
-    W::scale_min_h(r, s, a, m);
-    const h8_t bq = W::b(r, s) * a;
-    const h8_t bm = {m, m, m, m, m, m, m, m};
+__device__ __forceinline__ FoldPrep fold_prep(const typename W::Regs &r) {
+    return k4_fold_prep(r.hdr);
+}
+
+template <class W>
+__device__ __forceinline__ void fold_slice(const typename W::Regs &r, const FoldPrep &p, int s, const h8_t &ah,
+                                           const h8_t &al, f4_t &cb, f4_t &mb) {
+    const h8_t bq = W::b_fold(r, p, s);
+    const h2_t m2 = splat_half(p.m[s >> 1], s & 1);
+    const h8_t bm = __builtin_shufflevector(m2, m2, 0, 1, 0, 1, 0, 1, 0, 1);
     cb = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bq, cb, 0, 0, 0);
     cb = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, bq, cb, 0, 0, 0);
     mb = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bm, mb, 0, 0, 0);
@@ -99,11 +135,18 @@ struct MW<GGML_Q4_K> {
     }
     static constexpr bool FOLD = true;
     static constexpr bool SPLIT = false;
-    __device__ static void scale_min_h(const Regs &r, int s, _Float16 &a, _Float16 &m) {
-        uint32_t ai, mi;
-        k4_scale_min_u(s, r.hdr.y, r.hdr.z, r.hdr.w, ai, mi);
-        a = _Float16(float(ai));
-        m = _Float16(float(mi));
+    // B = a_s q of slice s (FoldPrep): v_perm's 1024 + q times a_s, minus 1024 a_s, in one FMA
+    __device__ static h8_t b_fold(const Regs &r, const FoldPrep &p, int s) {
+        const uint2 q = r.q[s >> 1];
+        const int sh = 4 * (s & 1);
+        const uint32_t v0 = (q.x >> sh) & 0x0F0F0F0Fu, v1 = (q.y >> sh) & 0x0F0F0F0Fu;
+        const h2_t a = splat_half(p.a[s >> 1], s & 1), na = splat_half(p.na[s >> 1], s & 1);
+        auto pair = [&](uint32_t v, uint32_t sel) {
+            const h2_t raw = __builtin_bit_cast(h2_t, __builtin_amdgcn_perm(0x64646464u, v, sel));
+            return __builtin_bit_cast(uint32_t, __builtin_elementwise_fma(raw, a, na));
+        };
+        return __builtin_bit_cast(h8_t, make_uint4(pair(v0, 0x04010400u), pair(v0, 0x04030402u), pair(v1, 0x04010400u),
+                                                   pair(v1, 0x04030402u)));
     }
 };
 
@@ -139,9 +182,11 @@ struct MW<GGML_Q5_K> {
     }
     static constexpr bool FOLD = true;
     static constexpr bool SPLIT = false;
-    __device__ static void scale_min_h(const Regs &r, int s, _Float16 &a, _Float16 &m) {
-        MW<GGML_Q4_K>::Regs t{r.hdr, {}};
-        MW<GGML_Q4_K>::scale_min_h(t, s, a, m);
+    // B = a_s q (q <= 31: (1024 + q) a_s could exceed the f16 range, so q first)
+    __device__ static h8_t b_fold(const Regs &r, const FoldPrep &p, int s) {
+        const h2_t a = splat_half(p.a[s >> 1], s & 1);
+        const h8_t av = __builtin_shufflevector(a, a, 0, 1, 0, 1, 0, 1, 0, 1);
+        return b(r, s) * av;
     }
 };
 
