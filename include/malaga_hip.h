@@ -242,8 +242,9 @@ int mlg_gemm(const mlg_matrix *w, const float *x, int M, float *y, const float *
  * projections that precede them. */
 int mlg_gemm_resid(const mlg_matrix *w, const float *x, int M, float *y, const float *bias, int relu, const float *r,
                    void *stream);
-/* The same for decode batches of up to 32 rows on the MFMA units (X resident in LDS):
- * partials [M][mlg_gemm_argmax_parts(w, M)]. */
+/* The same for decode batches of up to 64 rows on the MFMA units (X resident in LDS up
+ * to 32 rows, staged per K step above): partials [M][mlg_gemm_argmax_parts(w, M)];
+ * mlg_gemm_argmax_parts returns 0 where this form does not apply. */
 int mlg_gemm_argmax_parts(const mlg_matrix *w, int M);
 int mlg_gemm_argmax(const mlg_matrix *w, const float *x, int M, int mask_id, float *pv, uint32_t *pi, void *stream);
 /* LM head + first argmax pass (kernels/malaga.cu:247-280 fused into the GEMV):

@@ -619,11 +619,11 @@ int mlg_gemm_resid(const mlg_matrix *w, const float *x, int M, float *y, const f
 }
 
 int mlg_gemm_argmax_parts(const mlg_matrix *w, int M) {
-    return w && mlg::gemm_rx_supported(w->w, M) ? mlg::gemm_argmax_parts(w->w, M) : 0;
+    return w && mlg::gemm_argmax_supported(w->w, M) ? mlg::gemm_argmax_parts(w->w, M) : 0;
 }
 
 int mlg_gemm_argmax(const mlg_matrix *w, const float *x, int M, int mask_id, float *pv, uint32_t *pi, void *stream) {
-    if (!w || !x || !pv || !pi || !mlg::gemm_rx_supported(w->w, M)) return set_err(MLG_ERR_INVALID, "bad argument");
+    if (!w || !x || !pv || !pi || !mlg::gemm_argmax_supported(w->w, M)) return set_err(MLG_ERR_INVALID, "bad argument");
     int parts = 0;
     return hip_status(mlg::gemm_argmax(w->w, x, w->w.K, M, mask_id, pv, pi, &parts, as_stream(stream)),
                       "gemm_argmax");

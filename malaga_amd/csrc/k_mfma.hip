@@ -112,6 +112,10 @@ struct MfmaArgs {
     const float *bias, *R;
     int ldr, relu;
     float *part;  // split K: raw sums [gridDim.z][M][N], epilogue in k_splitk_reduce
+    int mask_id;  // k_mfma_w MODE 1: row index never selected (-1: none)
+    float *pv;    // k_mfma_w MODE 1: argmax partials [M][parts], one per workgroup
+    uint32_t *pi;
+    int parts;
 };
 
 
@@ -273,7 +277,9 @@ constexpr size_t mfma_w_lds() {
     return size_t(2) * BM * kXS * sizeof(_Float16) + size_t(16) * BM * sizeof(float);
 }
 
-template <int T, int BM, int WT, bool TL>
+// MODE 0 stores Y (or split-K partials); MODE 1 (the greedy LM head of 33..64 rows) keeps
+// a (value, lowest index) argmax per X row and workgroup instead (gridDim.y = z = 1).
+template <int T, int BM, int WT, bool TL, int MODE = 0>
 __global__ __launch_bounds__(512) void k_mfma_w(MfmaArgs a) {
     using W = MW<T>;
     constexpr int MT = BM / 16;
@@ -413,6 +419,57 @@ __global__ __launch_bounds__(512) void k_mfma_w(MfmaArgs a) {
 #pragma unroll
         for (int j = 0; j < WT; ++j) cur[j] = nxt[j];
     }
+    if constexpr (MODE == 1) {
+        // lane (kq, ln) holds rows mt 16 + 4 kq + r of columns n0 + 16 j + ln: its best over
+        // its WT columns, then over the 16 lanes of the row group (DPP), then over the
+        // waves (LDS; every wave's reads of the staged X are done first)
+        float best[MT][4];
+        uint32_t bidx[MT][4];
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                best[mt][r] = -INFINITY;
+                bidx[mt][r] = 0xffffffffu;
+            }
+#pragma unroll
+        for (int j = 0; j < WT; ++j) {
+            const int n = n0 + 16 * j + ln;
+            if (n >= a.w.N || n == a.mask_id) continue;
+#pragma unroll
+            for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) argmax_merge(best[mt][r], bidx[mt][r], acc[j][mt][r], uint32_t(n));
+        }
+        __syncthreads();
+        float *mv = reinterpret_cast<float *>(wlds);                     // [waves][BM]
+        uint32_t *mi = reinterpret_cast<uint32_t *>(mv + kWWaves * BM);  // [waves][BM]
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                float v = best[mt][r];
+                uint32_t i = bidx[mt][r];
+                argmax_merge(v, i, dpp_mov<kDppXor1>(v), dpp_mov<kDppXor1>(i));
+                argmax_merge(v, i, dpp_mov<kDppXor2>(v), dpp_mov<kDppXor2>(i));
+                argmax_merge(v, i, dpp_mov<kDppHalfMirror>(v), dpp_mov<kDppHalfMirror>(i));
+                argmax_merge(v, i, dpp_mov<kDppMirror>(v), dpp_mov<kDppMirror>(i));
+                if (ln == 0) {
+                    mv[w * BM + mt * 16 + 4 * kq + r] = v;
+                    mi[w * BM + mt * 16 + 4 * kq + r] = i;
+                }
+            }
+        __syncthreads();
+        if (t < BM && m0 + t < a.M) {  // ties -> the lowest index, so the merge order is free
+            float v = mv[t];
+            uint32_t i = mi[t];
+#pragma unroll
+            for (int w2 = 1; w2 < kWWaves; ++w2) argmax_merge(v, i, mv[w2 * BM + t], mi[w2 * BM + t]);
+            a.pv[size_t(m0 + t) * a.parts + blockIdx.x] = v;
+            a.pi[size_t(m0 + t) * a.parts + blockIdx.x] = i;
+        }
+        return;
+    }
 #pragma unroll
     for (int j = 0; j < WT; ++j) {
         const int n = n0 + 16 * j + ln;
@@ -453,14 +510,14 @@ int wide_wt(int N, int M) {
     return size_t((N + 255) / 256) * gy >= 192 ? 2 : 0;
 }
 
-template <int T, int BM, int WT, bool TL>
+template <int T, int BM, int WT, bool TL, int MODE = 0>
 hipError_t launch_w_t(const MfmaArgs &a, int M, int ks, hipStream_t st) {
-    static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void *>(&k_mfma_w<T, BM, WT, TL>),
+    static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void *>(&k_mfma_w<T, BM, WT, TL, MODE>),
                                                        hipFuncAttributeMaxDynamicSharedMemorySize,
                                                        int(mfma_w_lds<BM>()));
     if (attr != hipSuccess) return attr;
     const int gx = (a.w.N + 128 * WT - 1) / (128 * WT);
-    hipLaunchKernelGGL((k_mfma_w<T, BM, WT, TL>), dim3(gx, (M + BM - 1) / BM, ks), dim3(kWWaves * 64),
+    hipLaunchKernelGGL((k_mfma_w<T, BM, WT, TL, MODE>), dim3(gx, (M + BM - 1) / BM, ks), dim3(kWWaves * 64),
                        mfma_w_lds<BM>(), st, a);
     return hipGetLastError();
 }
@@ -969,11 +1026,51 @@ RxArgs rx_args(const DevMatrix &w, const float *X, int ldx, int M) {
 }
 }  // namespace
 
-int gemm_argmax_parts(const DevMatrix &w, int M) { return rx_grid(w, M); }  // one per workgroup
+// 33..64 rows: the wide-tile kernel with the argmax epilogue (X staged per K step)
+namespace {
+constexpr int kWArgmaxMaxRows = 64;
+bool w_argmax_rows(const DevMatrix &w, int M) {
+    return !gemm_rx_supported(w, M) && gemm_mfma_supported(w) && M > 32 && M <= kWArgmaxMaxRows;
+}
+int w_argmax_grid(const DevMatrix &w) { return (w.N + 256 - 1) / 256; }  // WT = 2: 256 rows of W per workgroup
+
+template <int T>
+hipError_t launch_w_argmax(const MfmaArgs &a, int M, hipStream_t st) {
+    if constexpr (T == GGML_Q6_K || T == GGML_Q4_K) {
+        if (a.w.t) return launch_w_t<T, 64, 2, true, 1>(a, M, 1, st);
+    }
+    return launch_w_t<T, 64, 2, false, 1>(a, M, 1, st);
+}
+}  // namespace
+
+bool gemm_argmax_supported(const DevMatrix &w, int M) { return gemm_rx_supported(w, M) || w_argmax_rows(w, M); }
+
+// one partial per workgroup
+int gemm_argmax_parts(const DevMatrix &w, int M) { return w_argmax_rows(w, M) ? w_argmax_grid(w) : rx_grid(w, M); }
 
 hipError_t gemm_argmax(const DevMatrix &w, const float *X, int ldx, int M, int mask_id, float *pv, uint32_t *pi,
                        int *parts, hipStream_t st) {
-    if (!gemm_rx_supported(w, M) || ldx % 4 || reinterpret_cast<uintptr_t>(X) % 16) return hipErrorInvalidValue;
+    if (!gemm_argmax_supported(w, M) || ldx % 4 || reinterpret_cast<uintptr_t>(X) % 16) return hipErrorInvalidValue;
+    if (w_argmax_rows(w, M)) {
+        MfmaArgs a{};
+        a.w = wptr_of(w);
+        a.x = X;
+        a.ldx = ldx;
+        a.M = M;
+        a.mask_id = mask_id;
+        a.pv = pv;
+        a.pi = pi;
+        a.parts = w_argmax_grid(w);
+        *parts = a.parts;
+        switch (w.type) {
+        case GGML_Q4_K: return launch_w_argmax<GGML_Q4_K>(a, M, st);
+        case GGML_Q5_K: return launch_w_argmax<GGML_Q5_K>(a, M, st);
+        case GGML_Q6_K: return launch_w_argmax<GGML_Q6_K>(a, M, st);
+        case GGML_Q8_0: return launch_w_argmax<GGML_Q8_0>(a, M, st);
+        case GGML_F16: return launch_w_argmax<GGML_F16>(a, M, st);
+        default: return hipErrorInvalidValue;
+        }
+    }
     RxArgs a = rx_args(w, X, ldx, M);
     a.mask_id = mask_id;
     a.pv = pv;

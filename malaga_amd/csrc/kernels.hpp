@@ -145,8 +145,10 @@ hipError_t dgemm_cross_attn(const DevMatrix &w, const float *x, int M, const Dge
 
 // M <= 32 rows with X resident in LDS (K <= 1024 at M > 16, K <= 2048 at M <= 16).
 bool gemm_rx_supported(const DevMatrix &w, int M);
-// Greedy LM head for 4 < M <= 32: per-workgroup argmax partials pv/pi [M][parts] of
-// X W^T (mask_id skipped), without storing the logits.
+// Greedy LM head for 4 < M <= 64: per-workgroup argmax partials pv/pi [M][parts] of
+// X W^T (mask_id skipped), without storing the logits (M <= 32: X resident in LDS;
+// 33..64: the wide-tile GEMM with an argmax epilogue).
+bool gemm_argmax_supported(const DevMatrix &w, int M);
 int gemm_argmax_parts(const DevMatrix &w, int M);
 hipError_t gemm_argmax(const DevMatrix &w, const float *X, int ldx, int M, int mask_id, float *pv, uint32_t *pi,
                        int *parts, hipStream_t st);

@@ -804,7 +804,8 @@ std::unique_ptr<StaticState> Model::new_state(int b, int s, int m, bool logits, 
         h2d(st->rows, id, ctx->stream);
     }
     st->parts = std::max(gemv_argmax_parts(head, b), 64);
-    if (b > gemv_max_batch(head) && gemm_rx_supported(head, b)) st->parts = std::max(st->parts, gemm_argmax_parts(head, b));
+    if (b > gemv_max_batch(head) && gemm_argmax_supported(head, b))
+        st->parts = std::max(st->parts, gemm_argmax_parts(head, b));
     st->pv = static_cast<float *>(get(size_t(b) * st->parts * 4, "argmax partials"));
     st->pi = static_cast<uint32_t *>(get(size_t(b) * st->parts * 4, "argmax partials"));
     check_hip(hipStreamSynchronize(ctx->stream), "state");
@@ -962,7 +963,7 @@ void Model::lm_head(StaticState &st, bool greedy_mode, int mask_id, const float 
         if (B <= gemv_max_batch(head)) {
             const GemvLn ln{ln_x, st.y, dec_norm.g, dec_norm.b, kLnEps, st.h};
             check_hip(gemv_argmax(head, st.h, d, B, hmask, st.pv, st.pi, &parts, s, ln_x ? &ln : nullptr), "lm_head");
-        } else if (gemm_rx_supported(head, B)) {
+        } else if (gemm_argmax_supported(head, B)) {
             check_hip(gemm_argmax(head, st.h, d, B, hmask, st.pv, st.pi, &parts, s), "lm_head");
         } else {
             check_hip(gemm(head, st.h, d, B, st.logits, V, nullptr, false, nullptr, 0, s, ctx->gemm_workspace(),

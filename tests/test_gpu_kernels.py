@@ -147,10 +147,12 @@ def test_gemm_wide_tiles(ctx, t, N, K):
         ctx.lib.mlg_matrix_free(w)
 
 
-@pytest.mark.parametrize("t,K", [(Q6_K, 1024), (Q4_K, 1024), (Q8_0, 512), (Q5_K, 2048)])
+@pytest.mark.parametrize("t,K", [(Q6_K, 1024), (Q4_K, 1024), (Q8_0, 512), (Q5_K, 2048), (Q6_K, 2048)])
 def test_gemm_argmax_batched_lm_head(ctx, t, K):
-    """Batched LM head (5..32 rows): per-wave argmax partials merged on the host equal
-    the argmax of the oracle's logits; ties -> lowest index; mask_id is skipped."""
+    """Batched LM head (5..64 rows): per-workgroup argmax partials merged on the host equal
+    the argmax of the oracle's logits; ties -> lowest index; mask_id is skipped.  Up to 32
+    rows X is resident in LDS (17..32 rows need K <= 1024, else the form is refused: 0
+    partials); 33..64 rows run the wide-tile GEMM with the argmax epilogue, any K."""
     rng = np.random.default_rng(5 + t)
     N = 20000
     wf = rng.normal(0, 0.02, (N, K)).astype(np.float32)
@@ -158,13 +160,14 @@ def test_gemm_argmax_batched_lm_head(ctx, t, K):
     blocks = M.quantize(t, wf)
     w = upload(ctx, t, blocks, N, K)
     try:
-        for M_ in (5, 16, 17, 32):
-            if K > 1024 and M_ > 16:
+        for M_ in (5, 16, 17, 32, 33, 64):
+            parts = ctx.lib.mlg_gemm_argmax_parts(w, M_)
+            if K > 1024 and 16 < M_ <= 32:
+                assert parts == 0
                 continue
+            assert parts > 0
             x = rng.normal(0, 1, (M_, K)).astype(np.float32)
             x[0] = np.abs(x[0]) * np.sign(wf[4321])
-            parts = ctx.lib.mlg_gemm_argmax_parts(w, M_)
-            assert parts > 0
             ref = O.gemv(t, blocks, N, K, x)
             for mask in (-1, 4321):
                 pv = torch.zeros((M_, parts), device="cuda")
