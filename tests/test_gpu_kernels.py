@@ -193,6 +193,61 @@ def test_gemm_argmax_batched_lm_head(ctx, t, K):
         ctx.lib.mlg_matrix_free(w)
 
 
+def test_lm_head_3b3_batch64(ctx):
+    """The 3.3B model's batched LM head at its real size: the q6_K token embedding (256206 x
+    2048) of the GGUF file bench.py times, 64 rows.  The logits of mlg_gemm (the wide-tile GEMM,
+    split-B q6_K slices) on 2048 sampled rows against the oracle's f64 dot (2e-6 of
+    sum |x||w|); mlg_gemm_argmax (the same GEMM with the argmax epilogue, row 7 masked)
+    against the argmax of those logits, with planted rows that make the winners known: row
+    1000 m + 1007 (x[m]'s signs) wins row m once row 7 (the signs of all 64 rows, so it would
+    win every row) is masked."""
+    from bench import model_path_3b
+    from malaga_amd.gguf import tensor_bytes
+
+    N, K, Mr = 256206, 2048, 64
+    raw, info = tensor_bytes(model_path_3b("q4_k_m"), "token_embd.weight")
+    assert info["type"] == Q6_K and list(info["ne"]) == [K, N]
+    blocks = np.array(raw)  # a writable copy
+    row_bytes = len(blocks) // N
+    rng = np.random.default_rng(77)
+    x = rng.normal(0, 1, (Mr, K)).astype(np.float32)
+    planted = {1000 * m + 1007: 0.05 * np.sign(x[m]) for m in range(Mr)}
+    planted[7] = 0.5 * np.sign(x).sum(0)
+    for r, v in planted.items():
+        blocks[r * row_bytes:(r + 1) * row_bytes] = M.quantize(Q6_K, v.astype(np.float32)[None])
+    w = upload(ctx, Q6_K, blocks, N, K)
+    try:
+        xd = dev(x)
+        y = torch.empty((Mr, N), device="cuda")
+        _lib.check(ctx.lib.mlg_gemm(w, ptr(xd), Mr, ptr(y), None, 0, None))
+        torch.cuda.synchronize()
+        rows = np.sort(rng.choice(N, 2048, replace=False))
+        rows[:2] = (7, 63007)
+        rows = np.unique(rows)
+        sub = np.ascontiguousarray(blocks.reshape(N, row_bytes)[rows]).reshape(-1)
+        ref = O.gemv(Q6_K, sub, len(rows), K, x)
+        wd = O.dequant(Q6_K, sub, len(rows) * K).reshape(len(rows), K)
+        yl = y.cpu().numpy()
+        assert (np.abs(yl[:, rows] - ref) <= 2e-6 * bound(x, wd) + 1e-6).all()
+        win = 1000 * np.arange(Mr) + 1007
+        assert (yl[:, 7] > yl[np.arange(Mr), win]).all()  # row 7 would win: the mask matters
+        parts = ctx.lib.mlg_gemm_argmax_parts(w, Mr)
+        assert parts > 0
+        pv = torch.zeros((Mr, parts), device="cuda")
+        pi = torch.zeros((Mr, parts), dtype=torch.int32, device="cuda")
+        _lib.check(ctx.lib.mlg_gemm_argmax(w, ptr(xd), Mr, 7, ptr(pv), ptr(pi), None))
+        torch.cuda.synchronize()
+        v, i = pv.cpu().numpy(), pi.cpu().numpy().view(np.uint32)
+        yl[:, 7] = -np.inf
+        for m in range(Mr):
+            best = v[m].max()
+            got = int(i[m][v[m] == best].min())
+            assert got == win[m] == int(np.argmax(yl[m])), (m, got)
+            assert best == yl[m, got]  # the same GEMM arithmetic: the same value bit for bit
+    finally:
+        ctx.lib.mlg_matrix_free(w)
+
+
 @pytest.mark.parametrize("t,K,N", [(Q4_K, 1024, 70001), (Q5_K, 512, 70001), (Q6_K, 1024, 70001), (Q6_K, 2048, 70001),
                                    (Q6_K, 256, 70001), (Q8_0, 1024, 70001), (Q8_0, 96, 70001),
                                    # the LM head at BASELINE config 2's full size: 256206 x 1024
