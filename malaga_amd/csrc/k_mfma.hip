@@ -27,7 +27,11 @@ namespace mlg {
 
 namespace {
 
-constexpr int kXS = kStep + 8;    // LDS row stride of the staged X (halves)
+// LDS row stride of the staged X (halves).  272 (136 dwords): the A-fragment reads and the
+// 16-byte staging stores have no bank conflicts (rocprofv3: 264 and 280 left 49-65 K conflict
+// cycles per CU in each encoder GEMM launch, 272 none for q6_K); the resident-X kernels keep
+// K + 8 (K + 16 measured no faster there, k_drx 5% slower)
+constexpr int kXS = kStep + 16;
 
 // where the staged X keeps x[k] (k a multiple of 4): split-B types permute the
 // 4-value groups inside each 32-slice (split_pos), the others keep k
