@@ -380,33 +380,47 @@ __global__ __launch_bounds__(1024) void k_greedy_finalize(const float *pv, const
                                                           float *outv, uint32_t *err) {
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, nw = blockDim.x >> 6;
     const uint32_t s = *step;
-    for (int row = w; row < b; row += nw) {  // wave-uniform
-        float best = -INFINITY;
-        uint32_t bi = 0xffffffffu;
-        for (int p0 = lane; p0 < P; p0 += 64 * 8) {
-            float v[8];
-            uint32_t ix[8];
+    // two rows per pass (row0 and row0 + nw), up to 1024 partials of each requested before
+    // any is merged: a wave waits for one round of loads per pass, not per 512 partials and row
+    constexpr int U = 16;
+    for (int row0 = w; row0 < b; row0 += 2 * nw) {  // wave-uniform
+        float best[2] = {-INFINITY, -INFINITY};
+        uint32_t bi[2] = {0xffffffffu, 0xffffffffu};
+        for (int p0 = lane; p0 < P; p0 += 64 * U) {
+            float v[2][U];
+            uint32_t ix[2][U];
 #pragma unroll
-            for (int u = 0; u < 8; ++u) {
-                const int p = p0 + u * 64;
-                v[u] = p < P ? pv[size_t(row) * P + p] : -INFINITY;
-                ix[u] = p < P ? pi[size_t(row) * P + p] : 0xffffffffu;
+            for (int r = 0; r < 2; ++r) {
+                const int row = min(row0 + r * nw, b - 1);  // a row past b reads row b - 1, unused
+#pragma unroll
+                for (int u = 0; u < U; ++u) {
+                    const int p = p0 + u * 64;
+                    v[r][u] = p < P ? pv[size_t(row) * P + p] : -INFINITY;
+                    ix[r][u] = p < P ? pi[size_t(row) * P + p] : 0xffffffffu;
+                }
             }
 #pragma unroll
-            for (int u = 0; u < 8; ++u) argmax_merge(best, bi, v[u], ix[u]);
+            for (int r = 0; r < 2; ++r)
+#pragma unroll
+                for (int u = 0; u < U; ++u) argmax_merge(best[r], bi[r], v[r][u], ix[r][u]);
         }
-        if (sl.vocab_map)  // the source-token candidates
-            for (int p = lane; p < sl.S; p += 64)
-                argmax_merge(best, bi, sl.spv[size_t(row) * sl.S + p], sl.spi[size_t(row) * sl.S + p]);
-        wave_argmax(best, bi);
-        if (lane == 0) {
-            uint32_t tok = sl.vocab_map ? sl_token(sl, row, bi, finished[row] != 0, pad) : bi;
-            if (err && !finished[row] && !(best > -INFINITY)) *err = 1u;
-            if (finished[row]) tok = pad;
-            if (tok == eos) finished[row] = 1;
-            ids[row] = tok;
-            out[size_t(row) * m + s] = tok;
-            if (outv) outv[size_t(row) * m + s] = best;
+#pragma unroll
+        for (int r = 0; r < 2; ++r) {
+            const int row = row0 + r * nw;
+            if (row >= b) break;  // wave-uniform
+            if (sl.vocab_map)  // the source-token candidates
+                for (int p = lane; p < sl.S; p += 64)
+                    argmax_merge(best[r], bi[r], sl.spv[size_t(row) * sl.S + p], sl.spi[size_t(row) * sl.S + p]);
+            wave_argmax(best[r], bi[r]);
+            if (lane == 0) {
+                uint32_t tok = sl.vocab_map ? sl_token(sl, row, bi[r], finished[row] != 0, pad) : bi[r];
+                if (err && !finished[row] && !(best[r] > -INFINITY)) *err = 1u;
+                if (finished[row]) tok = pad;
+                if (tok == eos) finished[row] = 1;
+                ids[row] = tok;
+                out[size_t(row) * m + s] = tok;
+                if (outv) outv[size_t(row) * m + s] = best[r];
+            }
         }
     }
     __syncthreads();
