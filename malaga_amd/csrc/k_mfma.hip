@@ -505,13 +505,15 @@ __global__ __launch_bounds__(512) void k_mfma_w(MfmaArgs a) {
 }
 
 // W tiles per wave of the wide kernel for (N, M), 0: use k_mfma.  Wide tiles pay
-// off once X (M > 32 rows) is re-staged by many tiles and enough workgroups remain.
+// off once X (M > 32 rows) is re-staged by many tiles and enough workgroups remain:
+// from 96 wide workgroups (config 4's encoder QKV, N = 3072 at 13 row tiles: 105.9 us on
+// k_mfma -> 35 us; at 48 the K = 4096 FFN-down switches too and slows, 37.4 -> 43.6 us).
 int wide_wt(int N, int M) {
     if (M <= 32) return 0;
     const int gy = (M + 63) / 64;
     // WT = 4 (512 rows) would need more than the 256 registers a wave of a
     // 512-thread workgroup can hold (spills), so 2 (256 rows)
-    return size_t((N + 255) / 256) * gy >= 192 ? 2 : 0;
+    return size_t((N + 255) / 256) * gy >= 96 ? 2 : 0;
 }
 
 template <int T, int BM, int WT, bool TL, int MODE = 0>

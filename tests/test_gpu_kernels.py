@@ -124,7 +124,7 @@ def test_gemm_mfma_tiles_bias_relu_residual(ctx, t, N, K):
                                    (F16, 12290, 256)])
 def test_gemm_wide_tiles(ctx, t, N, K):
     """M > 32 with many W rows runs the wide-tile kernel (8 waves x 32 rows of W per
-    workgroup) once ceil(N / 256) * ceil(M / 64) >= 192: partial tiles in M and N,
+    workgroup) once ceil(N / 256) * ceil(M / 64) >= 96: partial tiles in M and N,
     bias, ReLU, residual; q4_K at M = 200 also splits K (gemm + reduction)."""
     rng = np.random.default_rng(43 + t)
     wf = rng.normal(0, 0.02, (N, K)).astype(np.float32)
