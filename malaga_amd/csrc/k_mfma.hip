@@ -33,13 +33,6 @@ namespace {
 // K + 8 (K + 16 measured no faster there, k_drx 5% slower)
 constexpr int kXS = kStep + 16;
 
-// where the staged X keeps x[k] (k a multiple of 4): split-B types permute the
-// 4-value groups inside each 32-slice (split_pos), the others keep k
-template <bool SPLIT>
-__device__ __forceinline__ int staged_k(int k) {
-    if constexpr (SPLIT) return (k & ~31) | (split_pos((k & 31) >> 2) << 2);
-    else return k;
-}
 constexpr int kTileN = 64;        // W rows per workgroup
 
 // X staging of one 256-wide K step into LDS as f16 hi / lo (+ per-16 sums for the
@@ -662,7 +655,9 @@ struct RxArgs {
     int parts;
 };
 
-__host__ __device__ constexpr int rx_stride(int K) { return K + 8; }  // halves per staged X row
+// halves per staged X row: 8 mod 64 dwords, where the A reads (16 rows x 4 k-groups of
+// 16 bytes) meet no bank conflict (K + 8: 5.4 M conflict cycles per LM-head launch)
+__host__ __device__ constexpr int rx_stride(int K) { return K + 16; }
 
 size_t rx_lds_bytes(int BM, int K) {
     return size_t(BM) * rx_stride(K) * 2 * sizeof(_Float16) + size_t(K / 16) * BM * sizeof(float);
@@ -693,42 +688,49 @@ __global__ __launch_bounds__(kRxWaves * 64) void k_mfma_rx(RxArgs a) {
         for (int nt = 0; nt < kRxNT; ++nt) load_w<T, TL>(a.w, (job_base(j) >> 4) + nt, ln, j % nsteps, kq, r[nt]);
     };
 
-    // stage X: chunks of 16 values, up to 4 per thread in flight
+    // stage X: chunks of 8 values, one 16-byte store each (consecutive lanes: consecutive
+    // chunks of a row, so a store of 16 lanes covers 256 contiguous bytes of LDS: no bank
+    // conflicts), up to 4 per thread in flight.  Chunk c of a row holds x[8 c .. 8 c + 7], or
+    // for split-B types the two 4-value groups split_pos puts there.  BM K / 8 is a multiple
+    // of the 512 threads, so every lane runs the same trips (the DPP sums below need them all).
     {
-        const int cpr = K / 16, nch = BM * cpr;
+        const int cpr = K / 8, nch = BM * cpr;
+        auto koff = [](int c, int half) {
+            if constexpr (W::SPLIT) return 32 * (c >> 2) + 16 * half + 4 * (c & 3);
+            else return 8 * c + 4 * half;
+        };
         for (int c0 = t; c0 < nch; c0 += kRxWaves * 64 * 4) {
-            float4 v[4][4];
+            float4 v[4][2];
 #pragma unroll
             for (int u = 0; u < 4; ++u) {
                 const int c = c0 + u * kRxWaves * 64;
-                const int m = c / cpr, k0 = (c % cpr) * 16;
+                const int m = c / cpr, cc = c % cpr;
                 const bool ok = c < nch && m < a.M;
-                const float *src = a.x + size_t(ok ? m : 0) * a.ldx + (ok ? k0 : 0);
+                const float *src = a.x + size_t(ok ? m : 0) * a.ldx;
 #pragma unroll
-                for (int i = 0; i < 4; ++i)
-                    v[u][i] = ok ? reinterpret_cast<const float4 *>(src)[i] : make_float4(0.f, 0.f, 0.f, 0.f);
+                for (int f = 0; f < 2; ++f)
+                    v[u][f] = ok ? *reinterpret_cast<const float4 *>(src + koff(cc, f)) : make_float4(0.f, 0.f, 0.f, 0.f);
             }
 #pragma unroll
             for (int u = 0; u < 4; ++u) {
                 const int c = c0 + u * kRxWaves * 64;
-                if (c >= nch) break;
-                const int m = c / cpr, k0 = (c % cpr) * 16;
-                float sum = 0.f;
+                if (c >= nch) break;  // the same trips in every lane
+                const int m = c / cpr, cc = c % cpr;
+                const float e[8] = {v[u][0].x, v[u][0].y, v[u][0].z, v[u][0].w,
+                                    v[u][1].x, v[u][1].y, v[u][1].z, v[u][1].w};
+                h8_t hv, lv;
 #pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    const float e[4] = {v[u][i].x, v[u][i].y, v[u][i].z, v[u][i].w};
-                    _Float16 hv[4], lv[4];
-#pragma unroll
-                    for (int q = 0; q < 4; ++q) {
-                        hv[q] = _Float16(e[q]);
-                        lv[q] = _Float16(e[q] - float(hv[q]));
-                    }
-                    const int kp = staged_k<W::SPLIT>(k0 + 4 * i);
-                    *reinterpret_cast<h4_t *>(xh + m * XS + kp) = h4_t{hv[0], hv[1], hv[2], hv[3]};
-                    *reinterpret_cast<h4_t *>(xl + m * XS + kp) = h4_t{lv[0], lv[1], lv[2], lv[3]};
-                    sum += (e[0] + e[1]) + (e[2] + e[3]);
+                for (int i = 0; i < 8; ++i) {
+                    hv[i] = _Float16(e[i]);
+                    lv[i] = _Float16(e[i] - float(hv[i]));
                 }
-                xsum[(k0 >> 4) * BM + m] = sum;
+                *reinterpret_cast<h8_t *>(xh + m * XS + 8 * cc) = hv;
+                *reinterpret_cast<h8_t *>(xl + m * XS + 8 * cc) = lv;
+                if constexpr (W::MIN) {  // 16-value sums: this chunk and the next (lane t ^ 1)
+                    float sm = ((e[0] + e[1]) + (e[2] + e[3])) + ((e[4] + e[5]) + (e[6] + e[7]));
+                    sm += dpp_mov<kDppXor1>(sm);
+                    if (!(cc & 1)) xsum[(cc >> 1) * BM + m] = sm;
+                }
             }
         }
     }
