@@ -531,7 +531,7 @@ def main():
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this build targets one GPU: the decode path has no multi-GPU mode "
-                                   "(sentences shard across GPUs with zero exchange; see DESIGN.md)",
+                                   "(sentences shard across GPUs with zero exchange, one process per GPU)",
                           "n_gpus": args.gpus}))
         sys.exit(2)
 

@@ -1,7 +1,7 @@
 """Block codecs: the oracle's dequantizers and the converter's quantizers.
 
 No golden vectors for these formats exist in the reference (k-quants are never
-exercised by its tests, SURVEY §4).  What pins them here:
+exercised by its tests).  What pins them here:
   * f16: exhaustive over all 65536 bit patterns against numpy's IEEE binary16.
   * Q8_0: closed form on hand-built blocks.
   * Q4_K / Q5_K / Q6_K: hand-built blocks where a single sub-block scale is
