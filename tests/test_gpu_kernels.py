@@ -156,7 +156,9 @@ def test_gemm_argmax_batched_lm_head(ctx, t, K):
     rng = np.random.default_rng(5 + t)
     N = 20000
     wf = rng.normal(0, 0.02, (N, K)).astype(np.float32)
-    wf[4321] = wf[15000] = rng.normal(0, 0.5, K).astype(np.float32)  # tied dominant rows
+    # tied dominant rows: 4300 / 4321 / 4325 share a 256-row workgroup of the wide-tile
+    # kernel (two waves; 4321 and 4325 one wave's lanes), 15000 is in another
+    wf[4300] = wf[4321] = wf[4325] = wf[15000] = rng.normal(0, 0.5, K).astype(np.float32)
     blocks = M.quantize(t, wf)
     w = upload(ctx, t, blocks, N, K)
     try:
@@ -169,7 +171,7 @@ def test_gemm_argmax_batched_lm_head(ctx, t, K):
             x = rng.normal(0, 1, (M_, K)).astype(np.float32)
             x[0] = np.abs(x[0]) * np.sign(wf[4321])
             ref = O.gemv(t, blocks, N, K, x)
-            for mask in (-1, 4321):
+            for mask in (-1, 4300):
                 pv = torch.zeros((M_, parts), device="cuda")
                 pi = torch.zeros((M_, parts), dtype=torch.int32, device="cuda")
                 _lib.check(ctx.lib.mlg_gemm_argmax(w, ptr(dev(x)), M_, mask, ptr(pv), ptr(pi), None))
@@ -185,10 +187,8 @@ def test_gemm_argmax_batched_lm_head(ctx, t, K):
                     # near-ties within f32 rounding may legitimately resolve either way
                     assert got == want or abs(r[m][got] - r[m][want]) <= 2e-6 * bound(x[m:m + 1], O.dequant(
                         t, blocks, N * K).reshape(N, K)[[got, want]]).max() + 1e-6, (M_, m, got, want)
-                if mask < 0:
-                    assert int(i[0][v[0] == v[0].max()].min()) == 4321  # tie between 4321 and 15000
-                else:
-                    assert int(i[0][v[0] == v[0].max()].min()) == 15000
+                # the lowest index of the tied rows, the masked one skipped
+                assert int(i[0][v[0] == v[0].max()].min()) == (4300 if mask < 0 else 4321)
     finally:
         ctx.lib.mlg_matrix_free(w)
 
@@ -460,3 +460,38 @@ def test_greedy_finalize_bookkeeping(ctx):
     assert out.cpu().numpy()[:, 3].tolist() == [42, 2, 8, 1]
     assert find.cpu().tolist() == [0, 1, 0, 1]
     assert step.cpu().tolist() == [4]
+
+
+@pytest.mark.parametrize("b,P", [(5, 7), (17, 1001), (33, 1100), (47, 2100), (64, 1001)])
+def test_greedy_finalize_batched(ctx, b, P):
+    """The batched finalize (b > 4: two rows per pass, 1024 partials per pass and row):
+    lowest index among equal maxima, also across passes, EOS and finished rows, against a
+    numpy restatement of kernels/malaga.cu:290-326."""
+    rng = np.random.default_rng(b * 1000 + P)
+    m, eos, pad, s0 = 12, 2, 1, 5
+    pv = rng.normal(0, 1, (b, P)).astype(np.float32)
+    pi = rng.permutation(b * P).reshape(b, P).astype(np.uint32) + 10
+    for r in range(b):  # a planted maximum, tied in a later (or earlier) partial with a lower index
+        j1, j2 = rng.integers(0, P, 2)
+        pv[r, j1] = pv[r, j2] = 9.0 + (r % 3)
+        pi[r, j2] = min(pi[r, j1], pi[r, j2]) - 1 if r % 2 else pi[r, j2]
+    pv[3, -1], pi[3, -1] = 50.0, eos          # row 3 picks EOS from the very last partial
+    fin = (rng.random(b) < 0.2).astype(np.uint8)
+    fin[3] = 0
+    want = []
+    for r in range(b):
+        mx = pv[r].max()
+        tok = int(pi[r][pv[r] == mx].min())
+        want.append(pad if fin[r] else tok)
+    want_fin = [1 if (fin[r] or want[r] == eos) else 0 for r in range(b)]
+    pvd, pid, find = dev(pv), dev(pi.view(np.int32)), dev(fin)
+    ids = torch.zeros(b, dtype=torch.int32, device="cuda")
+    out = torch.zeros((b, m), dtype=torch.int32, device="cuda")
+    step = dev(np.array([s0], np.int32))
+    _lib.check(ctx.lib.mlg_greedy_finalize(ptr(pvd), ptr(pid), P, b, ptr(find), ptr(ids), ptr(out), m, ptr(step),
+                                           eos, pad, None))
+    torch.cuda.synchronize()
+    assert ids.cpu().tolist() == want
+    assert out.cpu().numpy()[:, s0].tolist() == want
+    assert find.cpu().tolist() == want_fin
+    assert step.cpu().tolist() == [s0 + 1]
