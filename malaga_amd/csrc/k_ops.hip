@@ -50,17 +50,44 @@ __device__ __forceinline__ void embed_chunks(const uint8_t *q, const uint8_t *s,
 // src/model.rs:558-568: x = token_embd[id] * scale + pos[*step + base] (or, for a copied
 // source token, its row of src.emb), stored to x, and h = LayerNorm(x) (decoder layer
 // 0's attn_norm).  The row's values stay in registers: one pass of f64 statistics.
-template <int T, int NC>
+// SRC: a source-copy row map is given (shortlist decoding); without it no branch on it.
+template <int T, int NC, bool SRC>
 __global__ __launch_bounds__(256) void k_embed_pos_ln(const uint8_t *q, const uint8_t *s, const uint8_t *dp,
                                                       const uint32_t *ids, int rows, const float *pos,
                                                       const uint32_t *step, uint32_t base, float scale, int d,
                                                       uint32_t last, const float *g, const float *b, float eps,
                                                       float *x, float *h, SrcEmb src, int x_frag) {
-    const int row = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
+    // row a scalar: the token id and the source-row flag are scalar loads, which do not
+    // make the wave wait for the vector loads below
+    const int row = __builtin_amdgcn_readfirstlane(blockIdx.x * 4 + (threadIdx.x >> 6)), lane = threadIdx.x & 63;
     if (row >= rows) return;  // wave-uniform
-    const uint32_t sr = src.row ? src.row[row] : kNoRow;  // wave-uniform
+    const uint32_t sr = SRC ? src.row[row] : kNoRow;  // wave-uniform
+    // a token the device produced: clamped to the table (an all-NaN row of logits
+    // yields 0xffffffff, malaga.cu:257-258), so a bad model cannot read past it
+    const uint32_t tok = min(ids[row], last), stp = *step;
+    // all three read here (an empty statement that uses them): the compiler would otherwise
+    // load the id only in the branch that needs it, one round trip later
+    __asm__ volatile("" ::"s"(tok), "s"(sr), "s"(stp));
+    // the operands that do not depend on the token first (positions; gamma and beta up to
+    // d = 2048), so that their loads overlap the token's round trip instead of following
+    // the embedding row one after another
+    constexpr bool kGB = NC <= 2;  // gamma | beta in registers from the start
+    const float *pr = pos + size_t(stp + base) * d;
+    float4 pq[NC][4], gq[kGB ? NC : 1][4], bq[kGB ? NC : 1][4];
+#pragma unroll
+    for (int j = 0; j < NC; ++j) {
+        const int c = min(lane + 64 * j, d / 16 - 1);  // lanes past d re-read the last chunk
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            pq[j][u] = ld4(pr, 4 * c + u);
+            if constexpr (kGB) {
+                gq[j][u] = ld4(g, 4 * c + u);
+                bq[j][u] = ld4(b, 4 * c + u);
+            }
+        }
+    }
     float w[NC][16];
-    if (sr != kNoRow) {  // the previous token was a copy of source position sr
+    if (SRC && sr != kNoRow) {  // the previous token was a copy of source position sr
         const float *er = src.emb + (size_t(row) * src.S + sr) * d;
 #pragma unroll
         for (int j = 0; j < NC; ++j) {
@@ -76,11 +103,8 @@ __global__ __launch_bounds__(256) void k_embed_pos_ln(const uint8_t *q, const ui
                 }
         }
     } else {
-        // a token the device produced: clamped to the table (an all-NaN row of logits
-        // yields 0xffffffff, malaga.cu:257-258), so a bad model cannot read past it
-        embed_chunks<T, NC>(q, s, dp, d, min(ids[row], last), w);
+        embed_chunks<T, NC>(q, s, dp, d, tok, w);
     }
-    const float *pr = pos + size_t(*step + base) * d;
     float4 *xr = reinterpret_cast<float4 *>(x + size_t(row) * d);
     float4 v[NC][4];
     double s1 = 0.0, s2 = 0.0;
@@ -90,7 +114,7 @@ __global__ __launch_bounds__(256) void k_embed_pos_ln(const uint8_t *q, const ui
         if (16 * c >= d) continue;
 #pragma unroll
         for (int u = 0; u < 4; ++u) {
-            const float4 p = ld4(pr, 4 * c + u);
+            const float4 p = pq[j][u];
             v[j][u] = make_float4(w[j][4 * u] * scale + p.x, w[j][4 * u + 1] * scale + p.y,
                                   w[j][4 * u + 2] * scale + p.z, w[j][4 * u + 3] * scale + p.w);
             if (x_frag)  // kernel argument
@@ -108,7 +132,10 @@ __global__ __launch_bounds__(256) void k_embed_pos_ln(const uint8_t *q, const ui
         const int c = lane + 64 * j;
         if (16 * c >= d) continue;
 #pragma unroll
-        for (int u = 0; u < 4; ++u) hr[4 * c + u] = ln_apply(v[j][u], mean, rstd, ld4(g, 4 * c + u), ld4(b, 4 * c + u));
+        for (int u = 0; u < 4; ++u) {
+            if constexpr (kGB) hr[4 * c + u] = ln_apply(v[j][u], mean, rstd, gq[j][u], bq[j][u]);
+            else hr[4 * c + u] = ln_apply(v[j][u], mean, rstd, ld4(g, 4 * c + u), ld4(b, 4 * c + u));
+        }
     }
 }
 
@@ -822,16 +849,28 @@ hipError_t launch_embed_pos_ln(const DevMatrix &E, const uint32_t *ids, int rows
     const int xf = x_frag ? 1 : 0;
     switch (embed_nc(E.K)) {
     case 1:
-        hipLaunchKernelGGL((k_embed_pos_ln<T, 1>), grid, dim3(256), 0, st, E.q, E.s, E.d, ids, rows, pos, step, base,
-                           scale, E.K, last, g, b, eps, x, h, src, xf);
+        if (src.row)
+            hipLaunchKernelGGL((k_embed_pos_ln<T, 1, true>), grid, dim3(256), 0, st, E.q, E.s, E.d, ids, rows, pos,
+                               step, base, scale, E.K, last, g, b, eps, x, h, src, xf);
+        else
+            hipLaunchKernelGGL((k_embed_pos_ln<T, 1, false>), grid, dim3(256), 0, st, E.q, E.s, E.d, ids, rows, pos,
+                               step, base, scale, E.K, last, g, b, eps, x, h, src, xf);
         break;
     case 2:
-        hipLaunchKernelGGL((k_embed_pos_ln<T, 2>), grid, dim3(256), 0, st, E.q, E.s, E.d, ids, rows, pos, step, base,
-                           scale, E.K, last, g, b, eps, x, h, src, xf);
+        if (src.row)
+            hipLaunchKernelGGL((k_embed_pos_ln<T, 2, true>), grid, dim3(256), 0, st, E.q, E.s, E.d, ids, rows, pos,
+                               step, base, scale, E.K, last, g, b, eps, x, h, src, xf);
+        else
+            hipLaunchKernelGGL((k_embed_pos_ln<T, 2, false>), grid, dim3(256), 0, st, E.q, E.s, E.d, ids, rows, pos,
+                               step, base, scale, E.K, last, g, b, eps, x, h, src, xf);
         break;
     default:
-        hipLaunchKernelGGL((k_embed_pos_ln<T, 4>), grid, dim3(256), 0, st, E.q, E.s, E.d, ids, rows, pos, step, base,
-                           scale, E.K, last, g, b, eps, x, h, src, xf);
+        if (src.row)
+            hipLaunchKernelGGL((k_embed_pos_ln<T, 4, true>), grid, dim3(256), 0, st, E.q, E.s, E.d, ids, rows, pos,
+                               step, base, scale, E.K, last, g, b, eps, x, h, src, xf);
+        else
+            hipLaunchKernelGGL((k_embed_pos_ln<T, 4, false>), grid, dim3(256), 0, st, E.q, E.s, E.d, ids, rows, pos,
+                               step, base, scale, E.K, last, g, b, eps, x, h, src, xf);
     }
     return hipGetLastError();
 }
