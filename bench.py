@@ -20,7 +20,8 @@ Also reported on the same JSON line:
     copies (> 2x the 256 MB Infinity Cache), LayerNorm and argmax latency;
   * ``roofline`` of the dominant kernel (the fused LM-head GEMV + argmax, q6_K
     256206 x 1024, 66% of the step's bytes), timed with HIP events on the stream
-    it runs on;
+    it runs on; the GEMVs and the read ceiling are timed as launches replayed from
+    one hipGraph (the decode step's launch mode), the eager figure beside them;
   * ``cpu_baseline``: the C restatement of the reference's generic path (oracle/,
     f32 K/V) on the host cores, on the headline workload (config 3's first sentence)
     and on config 1 (600M q8_0, 32 ids, 32 greedy steps); the GPU's config-1 tokens
@@ -362,12 +363,26 @@ class GemvBench:
                 _lib.check(launch(mats[i % copies]))
             end.record(self.stream)
         end.synchronize()
+        us_eager = start.elapsed_time(end) * 1e3 / launches
+        # the same launches replayed from one hipGraph, the way the decode step issues its
+        # kernels: eager launches add the dispatch gap between two kernels to each of them
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=self.stream):
+            for i in range(launches):
+                _lib.check(launch(mats[i % copies]))
+        with torch.cuda.stream(self.stream):
+            graph.replay()
+            start.record(self.stream)
+            graph.replay()
+            end.record(self.stream)
+        end.synchronize()
         us = start.elapsed_time(end) * 1e3 / launches
+        del graph
         for m in mats:
             self.lib.mlg_matrix_free(m)
         out_bytes = parts * 8 if argmax else N * 4
         alg = nbytes + K * 4 + out_bytes
-        return dict(us=us, bytes=alg, GBps=alg / us / 1e3, copies=copies)
+        return dict(us=us, us_eager=us_eager, bytes=alg, GBps=alg / us / 1e3, copies=copies, timing="hipGraph replay")
 
 
 def bench_kernels(T, lm_blocks: np.ndarray):
@@ -441,19 +456,27 @@ def stream_ceiling(nbytes: int = 215223280, grids=(1024, 2048, 4096, 8192), laun
     bps = [C.c_void_p(b.data_ptr()) for b in bufs]
     rows = []
     torch.cuda.synchronize()
-    with torch.cuda.stream(stream):
-        for mode, kind in ((0, "ordinary"), (1, "non-temporal"), (2, "direct-to-LDS")):
-            for grid in grids:
+    for mode, kind in ((0, "ordinary"), (1, "non-temporal"), (2, "direct-to-LDS")):
+        for grid in grids:
+            with torch.cuda.stream(stream):
                 for i in range(2 * copies):
                     _lib.check(lib.mlg_bench_stream_read(bps[i % copies], nbytes, mode, grid, op, sp))
-                start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-                start.record(stream)
+            stream.synchronize()
+            # replayed from one hipGraph, as the LM head is timed (GemvBench.run)
+            graph = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(graph, stream=stream):
                 for i in range(launches):
                     _lib.check(lib.mlg_bench_stream_read(bps[i % copies], nbytes, mode, grid, op, sp))
+            with torch.cuda.stream(stream):
+                graph.replay()
+                start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                start.record(stream)
+                graph.replay()
                 end.record(stream)
-                end.synchronize()
-                us = start.elapsed_time(end) * 1e3 / launches
-                rows.append(dict(loads=kind, grid=grid, us=round(us, 2), GBps=round(nbytes / us / 1e3, 1)))
+            end.synchronize()
+            del graph
+            us = start.elapsed_time(end) * 1e3 / launches
+            rows.append(dict(loads=kind, grid=grid, us=round(us, 2), GBps=round(nbytes / us / 1e3, 1)))
     del bufs
     best = max(rows, key=lambda r: r["GBps"])
     return dict(bytes=nbytes, copies=copies, best_GBps=best["GBps"], best=best, runs=rows)
@@ -611,7 +634,10 @@ def main():
                     traffic_source="profile-derived, not measured in this run: profiles/lm_head_q6k_traffic.txt "
                                    "(rocprofv3 --pmc FETCH_SIZE, WRITE_SIZE; copy-kernel calibrated)",
                     kernel="k_gemv<q6_K,B=1,argmax> (LM head 256206x1024 + fused argmax partials)",
-                    bytes_per_launch=lm["bytes"], us_per_launch=round(lm["us"], 3))
+                    bytes_per_launch=lm["bytes"], us_per_launch=round(lm["us"], 3),
+                    timing="200 launches over rotating copies, replayed from one hipGraph (HIP events); "
+                           "eager launches: us_per_launch_eager",
+                    us_per_launch_eager=round(lm["us_eager"], 3))
     ceiling = stream_ceiling()
     log(f"read ceiling: {ceiling['best_GBps']:.0f} GB/s ({ceiling['best']['loads']} loads, grid "
         f"{ceiling['best']['grid']}); LM head at {lm['GBps'] / ceiling['best_GBps']:.3f} of it")
