@@ -29,8 +29,9 @@ namespace {
 
 // LDS row stride of the staged X (halves).  272 (136 dwords): the A-fragment reads and the
 // 16-byte staging stores have no bank conflicts (rocprofv3: 264 and 280 left 49-65 K conflict
-// cycles per CU in each encoder GEMM launch, 272 none for q6_K); the resident-X kernels keep
-// K + 8 (K + 16 measured no faster there, k_drx 5% slower)
+// cycles per CU in each encoder GEMM launch, 272 none for q6_K).  The resident-X LM head
+// (k_mfma_rx) uses the same 8-mod-64-dword stride (rx_stride); k_drx keeps K + 8 (its bank
+// conflicts are off the critical path)
 constexpr int kXS = kStep + 16;
 
 constexpr int kTileN = 64;        // W rows per workgroup
